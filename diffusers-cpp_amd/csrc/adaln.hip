@@ -1,0 +1,176 @@
+// adaln.hip -- fused LayerNorm(no affine) + adaLN modulation:
+//   y = add(mul(norm_eps(x), add(scale, 1.0f)), shift)
+// the node chain LayerNorm::forward + `(1 + scale) * n + shift` emits in
+// Flux2SingleTransformerBlock.hpp:50-54 / Flux2TransformerBlock.hpp:63-72.
+//
+// Fast path: one wave64 per row.  The row is held in VGPRs (one HBM read,
+// one HBM write), the mean and the centred variance are two wave-wide DPP
+// reductions over registers, and each wave keeps (1+scale) and shift for
+// its columns in VGPRs across all the rows it processes.
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace dit {
+namespace {
+
+template <typename T, int VPL>
+__global__ __launch_bounds__(256) void adaln_wave_kernel(
+    const T* __restrict__ x, int64_t xs, const float* __restrict__ shift,
+    const float* __restrict__ scale, T* __restrict__ y, int64_t ys, int rows,
+    int nvec, float cols_f, float eps, float addend) {
+    constexpr int EPV = Io<T>::EPV;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const int nwaves = (int)((gridDim.x * blockDim.x) / kWave);
+
+    float t1[VPL][EPV], sh[VPL][EPV];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int v = lane + kWave * j;
+#pragma unroll
+        for (int e = 0; e < EPV; e += 4) {
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (v < nvec) {
+                a = *reinterpret_cast<const float4*>(scale + (int64_t)v * EPV + e);
+                b = *reinterpret_cast<const float4*>(shift + (int64_t)v * EPV + e);
+            }
+            t1[j][e + 0] = a.x + addend; t1[j][e + 1] = a.y + addend;
+            t1[j][e + 2] = a.z + addend; t1[j][e + 3] = a.w + addend;
+            sh[j][e + 0] = b.x; sh[j][e + 1] = b.y; sh[j][e + 2] = b.z; sh[j][e + 3] = b.w;
+        }
+    }
+
+    for (int r = wave; r < rows; r += nwaves) {
+        const T* xr = x + (int64_t)r * xs;
+        T* yr = y + (int64_t)r * ys;
+        float v[VPL][EPV];
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int vi = lane + kWave * j;
+            if (vi < nvec) {
+                Io<T>::load(xr + (int64_t)vi * EPV, v[j]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) v[j][e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) s += v[j][e];
+        }
+        s = wave_sum(s);
+        const float mean = s / cols_f;
+        float s2 = 0.f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            if (lane + kWave * j < nvec) {
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) {
+                    const float d = v[j][e] - mean;
+                    v[j][e] = d;
+                    s2 += d * d;
+                }
+            }
+        }
+        s2 = wave_sum(s2);
+        const float rstd = 1.0f / sqrtf(s2 / cols_f + eps);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int vi = lane + kWave * j;
+            if (vi < nvec) {
+                float o[EPV];
+#pragma unroll
+                for (int e = 0; e < EPV; ++e) o[e] = add_rn(mul_rn(mul_rn(v[j][e], rstd), t1[j][e]), sh[j][e]);
+                Io<T>::store(yr + (int64_t)vi * EPV, o);
+            }
+        }
+    }
+}
+
+// Any cols / stride / alignment: one 256-thread block per row, LDS reductions.
+template <typename T>
+__global__ __launch_bounds__(256) void adaln_generic_kernel(
+    const T* __restrict__ x, int64_t xs, const float* __restrict__ shift,
+    const float* __restrict__ scale, T* y, int64_t ys, int64_t cols, float eps, float addend) {
+    __shared__ float red[4];
+    const T* xr = x + (int64_t)blockIdx.x * xs;
+    T* yr = y + (int64_t)blockIdx.x * ys;
+    float s = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) s += Io<T>::get(xr + c);
+    const float mean = block_sum_f32(s, red) / (float)cols;
+    float s2 = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        const float d = Io<T>::get(xr + c) - mean;
+        s2 += d * d;
+    }
+    const float rstd = 1.0f / sqrtf(block_sum_f32(s2, red) / (float)cols + eps);
+    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
+        const float d = Io<T>::get(xr + c) - mean;
+        Io<T>::put(yr + c, add_rn(mul_rn(mul_rn(d, rstd), scale[c] + addend), shift[c]));
+    }
+}
+
+template <typename T, int VPL>
+void launch_wave(const void* x, int64_t xs, const float* shift, const float* scale, void* y,
+                 int64_t ys, int rows, int nvec, int64_t cols, float eps, float addend,
+                 hipStream_t st) {
+    // Enough waves to cover the chip a few times over; each wave keeps its
+    // modulation columns in registers across rows.
+    const int cap_waves = cu_count() * 16;
+    const int rpw = (rows + cap_waves - 1) / cap_waves;
+    const int nwaves = (rows + rpw - 1) / rpw;
+    const int blocks = (nwaves + 3) / 4;
+    hipLaunchKernelGGL((adaln_wave_kernel<T, VPL>), dim3(blocks), dim3(256), 0, st,
+                       (const T*)x, xs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps,
+                       addend);
+}
+
+template <typename T>
+int run(const void* x, int64_t rows, int64_t cols, int64_t xs, const float* shift,
+        const float* scale, float addend, void* y, int64_t ys, float eps, hipStream_t st) {
+    constexpr int EPV = Io<T>::EPV;
+    const int64_t nvec = cols / EPV;
+    const bool vec_ok = cols % EPV == 0 && xs % EPV == 0 && ys % EPV == 0 && aligned16(x) &&
+                        aligned16(y) && aligned16(shift) && aligned16(scale) &&
+                        nvec <= 16 * kWave && rows < (1ll << 31);
+    if (vec_ok) {
+        const int vpl = (int)((nvec + kWave - 1) / kWave);
+        const int r = (int)rows, nv = (int)nvec;
+        if (vpl <= 1) launch_wave<T, 1>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+        else if (vpl <= 2) launch_wave<T, 2>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+        else if (vpl <= 4) launch_wave<T, 4>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+        else if (vpl <= 6) launch_wave<T, 6>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+        else if (vpl <= 8) launch_wave<T, 8>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+        else if (vpl <= 12) launch_wave<T, 12>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+        else launch_wave<T, 16>(x, xs, shift, scale, y, ys, r, nv, cols, eps, addend, st);
+    } else {
+        DT_REQUIRE(rows <= 0x7FFFFFFF, "dt_adaln_mod: too many rows for the generic path");
+        hipLaunchKernelGGL((adaln_generic_kernel<T>), dim3((unsigned)rows), dim3(256), 0, st,
+                           (const T*)x, xs, shift, scale, (T*)y, ys, cols, eps, addend);
+    }
+    return check_launch("dt_adaln_mod");
+}
+
+}  // namespace
+
+int adaln_launch(const void* x, int64_t rows, int64_t cols, int64_t xs, const float* shift,
+                 const float* scale, float addend, void* y, int64_t ys, float eps, int32_t io,
+                 hipStream_t st) {
+    DT_REQUIRE(rows >= 0 && cols > 0, "dt_adaln_mod: bad shape rows=%lld cols=%lld",
+               (long long)rows, (long long)cols);
+    DT_REQUIRE(xs >= cols && ys >= cols, "dt_adaln_mod: stride smaller than cols");
+    DT_REQUIRE(is_io_type(io), "dt_adaln_mod: io_type %d unsupported", io);
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(x && y && shift && scale, "dt_adaln_mod: null pointer");
+    if (io == DT_TYPE_F32) return run<float>(x, rows, cols, xs, shift, scale, addend, y, ys, eps, st);
+    return run<bf16>(x, rows, cols, xs, shift, scale, addend, y, ys, eps, st);
+}
+
+}  // namespace dit
+
+extern "C" int dt_adaln_mod(const void* x, int64_t rows, int64_t cols, int64_t x_stride,
+                            const float* shift, const float* scale, void* y, int64_t y_stride,
+                            float eps, int32_t io_type, dt_stream_t stream) {
+    return dit::adaln_launch(x, rows, cols, x_stride, shift, scale, 1.0f, y, y_stride, eps, io_type,
+                             (hipStream_t)stream);
+}

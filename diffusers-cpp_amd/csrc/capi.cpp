@@ -1,0 +1,185 @@
+// capi.cpp -- library-level C-ABI: thread-local error text, device
+// properties, the backend handle (device + stream), device buffers and
+// host<->device tensor transfer.  Stand-ins for the reference's RAII wrappers
+// over ggml_backend_dev_t / ggml_backend_t / buffers (src/ggml/Device.hpp,
+// Backend.hpp, Buffer.hpp) and ggml_backend_tensor_set/get
+// (src/ggml/ExecutionRuntime.cpp:150-156, 302-313).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "capi_util.hpp"
+#include "dit_hip.h"
+#include "kernels.hpp"
+
+namespace dit {
+namespace {
+thread_local std::string g_last_error;
+std::mutex g_cu_mutex;
+std::vector<int> g_cu_counts;
+}  // namespace
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(DT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return DT_OK;
+}
+
+int cu_count() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(g_cu_mutex);
+    if ((int)g_cu_counts.size() <= dev) g_cu_counts.resize(dev + 1, 0);
+    if (g_cu_counts[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        g_cu_counts[dev] = n;
+    }
+    return g_cu_counts[dev];
+}
+
+}  // namespace dit
+
+struct dt_backend {
+    int device;
+    hipStream_t stream;
+    void* scratch;
+    size_t scratch_bytes;
+};
+
+extern "C" const char* dt_last_error(void) { return dit::g_last_error.c_str(); }
+
+extern "C" const char* dt_version(void) { return "dit_hip 0.1 (gfx950)"; }
+
+#define DT_HIP(call, what)                                                              \
+    do {                                                                                \
+        hipError_t e_ = (call);                                                         \
+        if (e_ != hipSuccess) return dit::fail(DT_ERR_HIP, "%s: %s", what, hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" int dt_backend_init(int32_t device_ordinal, dt_backend** out) {
+    DT_REQUIRE(out != nullptr, "dt_backend_init: null out");
+    int n = 0;
+    DT_HIP(hipGetDeviceCount(&n), "dt_backend_init");
+    DT_REQUIRE(device_ordinal >= 0 && device_ordinal < n, "dt_backend_init: device %d of %d",
+               device_ordinal, n);
+    DT_HIP(hipSetDevice(device_ordinal), "dt_backend_init");
+    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0};
+    *out = be;
+    return DT_OK;
+}
+
+extern "C" int dt_backend_free(dt_backend* be) {
+    if (!be) return DT_OK;
+    if (be->scratch) {
+        (void)hipSetDevice(be->device);
+        (void)hipStreamSynchronize(be->stream);
+        (void)hipFree(be->scratch);
+    }
+    delete be;
+    return DT_OK;
+}
+
+extern "C" int dt_backend_set_stream(dt_backend* be, dt_stream_t stream) {
+    DT_REQUIRE(be != nullptr, "dt_backend_set_stream: null backend");
+    be->stream = (hipStream_t)stream;
+    return DT_OK;
+}
+
+extern "C" int dt_backend_synchronize(dt_backend* be) {
+    DT_REQUIRE(be != nullptr, "dt_backend_synchronize: null backend");
+    DT_HIP(hipSetDevice(be->device), "dt_backend_synchronize");
+    DT_HIP(hipStreamSynchronize(be->stream), "dt_backend_synchronize");
+    return DT_OK;
+}
+
+extern "C" int dt_buffer_alloc(dt_backend* be, size_t bytes, void** out) {
+    DT_REQUIRE(be != nullptr && out != nullptr, "dt_buffer_alloc: null argument");
+    DT_HIP(hipSetDevice(be->device), "dt_buffer_alloc");
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes ? bytes : 1);
+    if (e != hipSuccess) return dit::fail(DT_ERR_OOM, "dt_buffer_alloc(%zu): %s", bytes, hipGetErrorString(e));
+    *out = p;
+    return DT_OK;
+}
+
+extern "C" int dt_buffer_free(dt_backend* be, void* ptr) {
+    DT_REQUIRE(be != nullptr, "dt_buffer_free: null backend");
+    if (!ptr) return DT_OK;
+    DT_HIP(hipSetDevice(be->device), "dt_buffer_free");
+    DT_HIP(hipFree(ptr), "dt_buffer_free");
+    return DT_OK;
+}
+
+static bool contiguous(const dt_tensor* t) {
+    const int es = dit::elem_size(t->type);
+    if (es == 0) return true;  // block types: caller addresses raw bytes
+    int64_t expect = es;
+    for (int i = 0; i < 4; ++i) {
+        if (t->ne[i] > 1 && t->nb[i] != expect) return false;
+        expect *= t->ne[i];
+    }
+    return true;
+}
+
+extern "C" int dt_tensor_set(const dt_tensor* t, const void* host, size_t offset, size_t n,
+                             dt_stream_t stream) {
+    DT_REQUIRE(t && t->data && (host || n == 0), "dt_tensor_set: null argument");
+    DT_REQUIRE(contiguous(t), "dt_tensor_set: tensor is not contiguous");
+    DT_HIP(hipMemcpyAsync((char*)t->data + offset, host, n, hipMemcpyHostToDevice, (hipStream_t)stream),
+           "dt_tensor_set");
+    DT_HIP(hipStreamSynchronize((hipStream_t)stream), "dt_tensor_set");
+    return DT_OK;
+}
+
+extern "C" int dt_tensor_get(const dt_tensor* t, void* host, size_t offset, size_t n,
+                             dt_stream_t stream) {
+    DT_REQUIRE(t && t->data && (host || n == 0), "dt_tensor_get: null argument");
+    DT_REQUIRE(contiguous(t), "dt_tensor_get: tensor is not contiguous");
+    DT_HIP(hipMemcpyAsync(host, (const char*)t->data + offset, n, hipMemcpyDeviceToHost, (hipStream_t)stream),
+           "dt_tensor_get");
+    DT_HIP(hipStreamSynchronize((hipStream_t)stream), "dt_tensor_get");
+    return DT_OK;
+}
+
+namespace dit {
+
+hipStream_t backend_stream(dt_backend* be) { return be ? be->stream : nullptr; }
+
+int backend_device(dt_backend* be) { return be ? be->device : 0; }
+
+int backend_scratch(dt_backend* be, size_t bytes, void** out) {
+    DT_REQUIRE(be != nullptr && out != nullptr, "backend_scratch: null argument");
+    if (bytes > be->scratch_bytes) {
+        if (be->scratch) {
+            // The old buffer may still be read by queued kernels.
+            DT_HIP(hipStreamSynchronize(be->stream), "backend_scratch");
+            DT_HIP(hipFree(be->scratch), "backend_scratch");
+            be->scratch = nullptr;
+            be->scratch_bytes = 0;
+        }
+        const hipError_t e = hipMalloc(&be->scratch, bytes);
+        if (e != hipSuccess) return fail(DT_ERR_OOM, "backend_scratch(%zu): %s", bytes, hipGetErrorString(e));
+        be->scratch_bytes = bytes;
+    }
+    *out = be->scratch;
+    return DT_OK;
+}
+
+}  // namespace dit

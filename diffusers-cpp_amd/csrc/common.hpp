@@ -1,0 +1,166 @@
+// common.hpp -- shared device helpers for the gfx950 kernels: bf16 bit
+// conversions, 128-bit vector I/O over fp32/bf16 rows, wave64 reductions
+// built on DPP row operations, and a 32-bit invariant-divisor helper.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dit_hip.h"
+
+namespace dit {
+
+constexpr int kWave = 64;
+
+// bf16 as a distinct type so templates can tell it apart from uint16_t data.
+struct bf16 {
+    uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 bits; NaN stays NaN (quiet bit set).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// Round-to-nearest-even fp32 -> fp16 bits.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Row I/O in 16-byte vectors.  EPV = elements per vector.
+template <typename T> struct Io;
+
+template <> struct Io<float> {
+    static constexpr int EPV = 4;
+    static constexpr int kType = DT_TYPE_F32;
+    __device__ __forceinline__ static void load(const float* p, float* v) {
+        const float4 t = *reinterpret_cast<const float4*>(p);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+    __device__ __forceinline__ static void store(float* p, const float* v) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __device__ __forceinline__ static float get(const float* p) { return *p; }
+    __device__ __forceinline__ static void put(float* p, float v) { *p = v; }
+};
+
+template <> struct Io<bf16> {
+    static constexpr int EPV = 8;
+    static constexpr int kType = DT_TYPE_BF16;
+    __device__ __forceinline__ static void load(const bf16* p, float* v) {
+        const uint4 t = *reinterpret_cast<const uint4*>(p);
+        v[0] = bf16_lo(t.x); v[1] = bf16_hi(t.x);
+        v[2] = bf16_lo(t.y); v[3] = bf16_hi(t.y);
+        v[4] = bf16_lo(t.z); v[5] = bf16_hi(t.z);
+        v[6] = bf16_lo(t.w); v[7] = bf16_hi(t.w);
+    }
+    __device__ __forceinline__ static void store(bf16* p, const float* v) {
+        uint4 t;
+        t.x = pack_bf16x2(v[0], v[1]);
+        t.y = pack_bf16x2(v[2], v[3]);
+        t.z = pack_bf16x2(v[4], v[5]);
+        t.w = pack_bf16x2(v[6], v[7]);
+        *reinterpret_cast<uint4*>(p) = t;
+    }
+    __device__ __forceinline__ static float get(const bf16* p) { return __uint_as_float((uint32_t)p->bits << 16); }
+    __device__ __forceinline__ static void put(bf16* p, float v) { p->bits = (uint16_t)f32_to_bf16_bits(v); }
+};
+
+// Explicitly rounded fp32 arithmetic: keeps the compiler from contracting
+// a*b+c into one fma where the emitted ggml graph rounds after each op.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+
+// ggml's sigmoid, 1/(1+expf(-x)), with the accurate device expf.
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ---- DPP-based reductions ---------------------------------------------------
+// dpp_ctrl encodings (GCN/CDNA): quad_perm = p0 | p1<<2 | p2<<4 | p3<<6,
+// row_mirror = 0x140, row_half_mirror = 0x141.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum across each 16-lane DPP row; every lane of the row receives the sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    v += dpp_f32<0x141>(v);  // row_half_mirror: pairs quad 0 with quad 1
+    v += dpp_f32<0x140>(v);  // row_mirror: pairs the two halves of the row
+    return v;
+}
+
+// Sum across the full wave64; every lane receives the sum.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// Block-wide sum of doubles through LDS; `red` holds >= blockDim.x/64 slots.
+// All threads receive the result.  Must be called by every thread.
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+    v = wave_sum_f64(v);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int i = 0; i < nw; ++i) s += red[i];
+    return s;
+}
+
+__device__ __forceinline__ float block_sum_f32(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; ++i) s += red[i];
+    return s;
+}
+
+// ---- invariant 32-bit division (n < 2^31) -----------------------------------
+struct FastDiv {
+    uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    f.d = d;
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    f.s = l;
+    f.m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+}  // namespace dit

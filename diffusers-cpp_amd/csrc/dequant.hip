@@ -1,0 +1,140 @@
+// dequant.hip -- ggml Q8_0 / Q4_K weight dequantisation to bf16 or fp32,
+// bit-exact with ggml's dequantize_row_q8_0 / dequantize_row_q4_K.
+//
+// Work unit: one lane produces 8 consecutive outputs (one 16-byte bf16 store,
+// two for fp32), so a wave writes 1 KB of contiguous output per instruction.
+//   Q8_0  block = {fp16 d; int8 qs[32]} (34 B): 4 lanes share a block, each
+//         reads d and 8 quant bytes (2-byte aligned -> four u16 loads).
+//         d*q is exact in fp32 (11-bit x 8-bit significands).
+//   Q4_K  super-block = {fp16 d, dmin; u8 scales[12]; u8 qs[128]} (144 B):
+//         32 lanes share a super-block; each reads the 16-byte header and 8
+//         quant bytes (one 16 B + one 8 B load), decodes its sub-block's
+//         6-bit (scale, min) and computes (d*sc)*q - (dmin*m) with each
+//         operation rounded separately.
+#include "capi_util.hpp"
+#include "common.hpp"
+
+namespace dit {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ void store_out8(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store_out8<bf16>(bf16* p, const float* v) { Io<bf16>::store(p, v); }
+template <>
+__device__ __forceinline__ void store_out8<float>(float* p, const float* v) {
+    Io<float>::store(p, v);
+    Io<float>::store(p + 4, v + 4);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t* __restrict__ src,
+                                                           int64_t row_bytes, T* __restrict__ dst,
+                                                           int64_t dst_stride, uint32_t total,
+                                                           FastDiv chunks_per_row) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t r = fdiv(idx, chunks_per_row);
+    const uint32_t k = idx - r * chunks_per_row.d;
+    const uint32_t blk = k >> 2, part = k & 3;
+    const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 34;
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+    const float d = f16_bits_to_f32(h[0]);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t two = h[1 + part * 4 + i];
+        v[2 * i] = mul_rn(d, (float)(int8_t)(two & 0xFF));
+        v[2 * i + 1] = mul_rn(d, (float)(int8_t)(two >> 8));
+    }
+    store_out8<T>(dst + (int64_t)r * dst_stride + (int64_t)k * 8, v);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q4_K_kernel(const uint8_t* __restrict__ src,
+                                                           int64_t row_bytes, T* __restrict__ dst,
+                                                           int64_t dst_stride, uint32_t total,
+                                                           FastDiv chunks_per_row) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t r = fdiv(idx, chunks_per_row);
+    const uint32_t k = idx - r * chunks_per_row.d;
+    const uint32_t blk = k >> 5, e0 = (k & 31) * 8;     // element offset in the super-block
+    const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
+    const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 144;
+    const uint4 hdr = *reinterpret_cast<const uint4*>(b);
+    const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
+    // Sub-block j = 2*c64 + hi; header bytes 4..15 are scales[0..11].
+    const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);
+    const uint32_t by = (hdr.y >> sh) & 0xFF;   // scales[j & 3]
+    const uint32_t bz = (hdr.z >> sh) & 0xFF;   // scales[(j & 3) + 4]
+    const uint32_t bw = (hdr.w >> sh) & 0xFF;   // scales[(j & 3) + 8]
+    uint32_t sc, m;
+    if (j < 4) {
+        sc = by & 63;
+        m = bz & 63;
+    } else {
+        sc = (bw & 0xF) | ((by >> 6) << 4);
+        m = (bw >> 4) | ((bz >> 6) << 4);
+    }
+    const float d1 = mul_rn(f16_bits_to_f32(hdr.x & 0xFFFF), (float)sc);
+    const float m1 = mul_rn(f16_bits_to_f32(hdr.x >> 16), (float)m);
+    const uint32_t shift = hi * 4;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = sub_rn(mul_rn(d1, (float)((q8.x >> (8 * i + shift)) & 0xF)), m1);
+        v[4 + i] = sub_rn(mul_rn(d1, (float)((q8.y >> (8 * i + shift)) & 0xF)), m1);
+    }
+    store_out8<T>(dst + (int64_t)r * dst_stride + (int64_t)k * 8, v);
+}
+
+template <typename T>
+int run(const void* src, int32_t qtype, int64_t rows, int64_t cols, int64_t row_bytes, void* dst,
+        int64_t dst_stride, hipStream_t st) {
+    const int64_t cpr = cols / 8, total = rows * cpr;
+    DT_REQUIRE(total < (1ll << 31), "dt_dequant: %lld chunks exceed the 32-bit index range",
+               (long long)total);
+    const unsigned blocks = (unsigned)((total + 255) / 256);
+    const FastDiv fd = make_fastdiv((uint32_t)cpr);
+    if (qtype == DT_TYPE_Q8_0)
+        hipLaunchKernelGGL((dequant_q8_0_kernel<T>), dim3(blocks), dim3(256), 0, st,
+                           (const uint8_t*)src, row_bytes, (T*)dst, dst_stride, (uint32_t)total, fd);
+    else
+        hipLaunchKernelGGL((dequant_q4_K_kernel<T>), dim3(blocks), dim3(256), 0, st,
+                           (const uint8_t*)src, row_bytes, (T*)dst, dst_stride, (uint32_t)total, fd);
+    return check_launch("dt_dequant");
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_dequant(const void* src, int32_t qtype, int64_t rows, int64_t cols,
+                          int64_t row_bytes, void* dst, int64_t dst_stride, int32_t dst_type,
+                          dt_stream_t stream) {
+    DT_REQUIRE(qtype == DT_TYPE_Q8_0 || qtype == DT_TYPE_Q4_K, "dt_dequant: qtype %d unsupported",
+               qtype);
+    DT_REQUIRE(dst_type == DT_TYPE_F32 || dst_type == DT_TYPE_BF16,
+               "dt_dequant: dst_type %d unsupported", dst_type);
+    DT_REQUIRE(rows >= 0 && cols > 0, "dt_dequant: bad shape");
+    const int64_t qk = qtype == DT_TYPE_Q8_0 ? 32 : 256, bsz = qtype == DT_TYPE_Q8_0 ? 34 : 144;
+    DT_REQUIRE(cols % qk == 0, "dt_dequant: cols %lld not a multiple of the block size %lld",
+               (long long)cols, (long long)qk);
+    DT_REQUIRE(row_bytes >= cols / qk * bsz, "dt_dequant: row_bytes %lld < %lld",
+               (long long)row_bytes, (long long)(cols / qk * bsz));
+    DT_REQUIRE(dst_stride >= cols, "dt_dequant: dst_stride < cols");
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(src && dst, "dt_dequant: null pointer");
+    const int epv = dst_type == DT_TYPE_BF16 ? 8 : 4;
+    DT_REQUIRE(dit::aligned16(dst) && dst_stride % epv == 0,
+               "dt_dequant: dst must be 16-byte aligned with a stride multiple of %d", epv);
+    if (qtype == DT_TYPE_Q8_0)
+        DT_REQUIRE((reinterpret_cast<uintptr_t>(src) & 1) == 0 && row_bytes % 2 == 0,
+                   "dt_dequant: Q8_0 rows must be 2-byte aligned");
+    else
+        DT_REQUIRE(dit::aligned16(src) && row_bytes % 16 == 0,
+                   "dt_dequant: Q4_K rows must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    if (dst_type == DT_TYPE_F32) return dit::run<float>(src, qtype, rows, cols, row_bytes, dst, dst_stride, st);
+    return dit::run<dit::bf16>(src, qtype, rows, cols, row_bytes, dst, dst_stride, st);
+}

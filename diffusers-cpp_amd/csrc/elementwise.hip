@@ -1,0 +1,221 @@
+// elementwise.hip -- streaming fused elementwise kernels of the Flux2 chain:
+//   SwiGLU          y = (g * sigmoid(g)) * u         Flux2SwiGLU.hpp:17-21
+//   gated residual  y = h + o * gate[col]            Flux2SingleTransformerBlock.hpp:58
+//   Euler step      y = x + v * dt                   FlowMatchEulerDiscreteScheduler.cpp:210-222
+// Each thread moves U independent 16-byte vectors per operand (all loads
+// issued before any math), consecutive threads take consecutive vectors so
+// every wave instruction touches 1 KB of contiguous HBM, and the row index
+// of a vector comes from a multiply-high invariant division.
+#include "capi_util.hpp"
+#include "common.hpp"
+
+namespace dit {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <typename T, int U>
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(const T* __restrict__ g, int64_t gs,
+                                                        const T* __restrict__ u, int64_t us,
+                                                        T* __restrict__ y, int64_t ys,
+                                                        uint32_t total, FastDiv nv) {
+    constexpr int EPV = Io<T>::EPV;
+    const uint32_t base = blockIdx.x * (kBlock * U) + threadIdx.x;
+    float gv[U][EPV], uv[U][EPV];
+    int64_t yo[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t idx = base + k * kBlock;
+        yo[k] = -1;
+        if (idx < total) {
+            const uint32_t r = fdiv(idx, nv);
+            const uint32_t c = (idx - r * nv.d) * EPV;
+            Io<T>::load(g + r * gs + c, gv[k]);
+            Io<T>::load(u + r * us + c, uv[k]);
+            yo[k] = r * ys + c;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        if (yo[k] >= 0) {
+            float o[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const float s = sigmoid_ref(gv[k][e]);
+                o[e] = mul_rn(mul_rn(gv[k][e], s), uv[k][e]);
+            }
+            Io<T>::store(y + yo[k], o);
+        }
+    }
+}
+
+template <typename T, int U>
+__global__ __launch_bounds__(kBlock) void gated_residual_kernel(
+    const T* h, int64_t hs, const T* __restrict__ o, int64_t os,
+    const float* __restrict__ gate, T* y, int64_t ys, uint32_t total, FastDiv nv) {
+    constexpr int EPV = Io<T>::EPV;
+    const uint32_t base = blockIdx.x * (kBlock * U) + threadIdx.x;
+    float hv[U][EPV], ov[U][EPV], gv[U][EPV];
+    int64_t yo[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        const uint32_t idx = base + k * kBlock;
+        yo[k] = -1;
+        if (idx < total) {
+            const uint32_t r = fdiv(idx, nv);
+            const uint32_t c = (idx - r * nv.d) * EPV;
+            Io<T>::load(h + r * hs + c, hv[k]);
+            Io<T>::load(o + r * os + c, ov[k]);
+#pragma unroll
+            for (int e = 0; e < EPV; e += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(gate + c + e);
+                gv[k][e] = a.x; gv[k][e + 1] = a.y; gv[k][e + 2] = a.z; gv[k][e + 3] = a.w;
+            }
+            yo[k] = r * ys + c;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        if (yo[k] >= 0) {
+            float out[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) out[e] = add_rn(hv[k][e], mul_rn(ov[k][e], gv[k][e]));
+            Io<T>::store(y + yo[k], out);
+        }
+    }
+}
+
+// Strided / unaligned fallbacks: one element per thread, grid-stride.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_generic_kernel(const T* g, int64_t gs, const T* u,
+                                                                int64_t us, T* y, int64_t ys,
+                                                                int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c = i % cols;
+        const float gv = Io<T>::get(g + r * gs + c);
+        const float s = sigmoid_ref(gv);
+        Io<T>::put(y + r * ys + c, mul_rn(mul_rn(gv, s), Io<T>::get(u + r * us + c)));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void gated_residual_generic_kernel(
+    const T* h, int64_t hs, const T* o, int64_t os, const float* gate, T* y, int64_t ys,
+    int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c = i % cols;
+        const float t = mul_rn(Io<T>::get(o + r * os + c), gate[c]);
+        Io<T>::put(y + r * ys + c, add_rn(Io<T>::get(h + r * hs + c), t));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void euler_kernel(const T* x, const T* v, float dt, T* y,
+                                                       int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float t = mul_rn(Io<T>::get(v + i), dt);
+        Io<T>::put(y + i, add_rn(Io<T>::get(x + i), t));
+    }
+}
+
+unsigned generic_blocks(int64_t n) {
+    int64_t b = (n + kBlock - 1) / kBlock;
+    const int64_t cap = (int64_t)cu_count() * 64;
+    return (unsigned)(b < 1 ? 1 : (b > cap ? cap : b));
+}
+
+constexpr int kUnroll = 4;
+
+template <typename T>
+int run_swiglu(const void* g, int64_t gs, const void* u, int64_t us, void* y, int64_t ys,
+               int64_t rows, int64_t cols, hipStream_t st) {
+    constexpr int EPV = Io<T>::EPV;
+    const int64_t nvec = cols / EPV, total = rows * nvec;
+    const bool vec = cols % EPV == 0 && gs % EPV == 0 && us % EPV == 0 && ys % EPV == 0 &&
+                     aligned16(g) && aligned16(u) && aligned16(y) && total < (1ll << 31);
+    if (vec) {
+        const int64_t blocks = (total + kBlock * kUnroll - 1) / (kBlock * kUnroll);
+        hipLaunchKernelGGL((swiglu_kernel<T, kUnroll>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
+                           (const T*)g, gs, (const T*)u, us, (T*)y, ys, (uint32_t)total,
+                           make_fastdiv((uint32_t)nvec));
+    } else {
+        hipLaunchKernelGGL((swiglu_generic_kernel<T>), dim3(generic_blocks(rows * cols)), dim3(kBlock),
+                           0, st, (const T*)g, gs, (const T*)u, us, (T*)y, ys, rows, cols);
+    }
+    return check_launch("dt_swiglu");
+}
+
+template <typename T>
+int run_gated(const void* h, int64_t hs, const void* o, int64_t os, const float* gate, void* y,
+              int64_t ys, int64_t rows, int64_t cols, hipStream_t st) {
+    constexpr int EPV = Io<T>::EPV;
+    const int64_t nvec = cols / EPV, total = rows * nvec;
+    const bool vec = cols % EPV == 0 && hs % EPV == 0 && os % EPV == 0 && ys % EPV == 0 &&
+                     aligned16(h) && aligned16(o) && aligned16(y) && aligned16(gate) &&
+                     total < (1ll << 31);
+    if (vec) {
+        const int64_t blocks = (total + kBlock * kUnroll - 1) / (kBlock * kUnroll);
+        hipLaunchKernelGGL((gated_residual_kernel<T, kUnroll>), dim3((unsigned)blocks), dim3(kBlock),
+                           0, st, (const T*)h, hs, (const T*)o, os, gate, (T*)y, ys,
+                           (uint32_t)total, make_fastdiv((uint32_t)nvec));
+    } else {
+        hipLaunchKernelGGL((gated_residual_generic_kernel<T>), dim3(generic_blocks(rows * cols)),
+                           dim3(kBlock), 0, st, (const T*)h, hs, (const T*)o, os, gate, (T*)y, ys,
+                           rows, cols);
+    }
+    return check_launch("dt_gated_residual");
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_swiglu(const void* gate, int64_t gate_stride, const void* up, int64_t up_stride,
+                         void* y, int64_t y_stride, int64_t rows, int64_t inner, int32_t io_type,
+                         dt_stream_t stream) {
+    DT_REQUIRE(dit::is_io_type(io_type), "dt_swiglu: io_type %d unsupported", io_type);
+    DT_REQUIRE(rows >= 0 && inner > 0, "dt_swiglu: bad shape");
+    DT_REQUIRE(gate_stride >= inner && up_stride >= inner && y_stride >= inner,
+               "dt_swiglu: stride smaller than inner");
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(gate && up && y, "dt_swiglu: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    if (io_type == DT_TYPE_F32)
+        return dit::run_swiglu<float>(gate, gate_stride, up, up_stride, y, y_stride, rows, inner, st);
+    return dit::run_swiglu<dit::bf16>(gate, gate_stride, up, up_stride, y, y_stride, rows, inner, st);
+}
+
+extern "C" int dt_gated_residual(const void* h, int64_t h_stride, const void* o, int64_t o_stride,
+                                 const float* gate, void* y, int64_t y_stride, int64_t rows,
+                                 int64_t cols, int32_t io_type, dt_stream_t stream) {
+    DT_REQUIRE(dit::is_io_type(io_type), "dt_gated_residual: io_type %d unsupported", io_type);
+    DT_REQUIRE(rows >= 0 && cols > 0, "dt_gated_residual: bad shape");
+    DT_REQUIRE(h_stride >= cols && o_stride >= cols && y_stride >= cols,
+               "dt_gated_residual: stride smaller than cols");
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(h && o && gate && y, "dt_gated_residual: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    if (io_type == DT_TYPE_F32)
+        return dit::run_gated<float>(h, h_stride, o, o_stride, gate, y, y_stride, rows, cols, st);
+    return dit::run_gated<dit::bf16>(h, h_stride, o, o_stride, gate, y, y_stride, rows, cols, st);
+}
+
+extern "C" int dt_euler_step(const void* x, const void* v, float dt, void* y, int64_t n,
+                             int32_t io_type, dt_stream_t stream) {
+    DT_REQUIRE(dit::is_io_type(io_type), "dt_euler_step: io_type %d unsupported", io_type);
+    DT_REQUIRE(n >= 0, "dt_euler_step: n < 0");
+    if (n == 0) return DT_OK;
+    DT_REQUIRE(x && v && y, "dt_euler_step: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    if (io_type == DT_TYPE_F32)
+        hipLaunchKernelGGL((dit::euler_kernel<float>), dim3(dit::generic_blocks(n)), dim3(256), 0, st,
+                           (const float*)x, (const float*)v, dt, (float*)y, n);
+    else
+        hipLaunchKernelGGL((dit::euler_kernel<dit::bf16>), dim3(dit::generic_blocks(n)), dim3(256), 0,
+                           st, (const dit::bf16*)x, (const dit::bf16*)v, dt, (dit::bf16*)y, n);
+    return dit::check_launch("dt_euler_step");
+}

@@ -1,0 +1,528 @@
+// graph.cpp -- dt_graph_compute: executes a ggml-shaped node list (the role
+// of ggml_backend_graph_compute at src/ggml/ExecutionRuntime.cpp:227, 254)
+// after a fusion pass that recognises the node chains the reference's
+// modules emit and lowers each to one fused kernel:
+//
+//   adaLN           ADD(MUL(NORM(x), t[c]), shift[c])
+//                   LayerNorm.cpp:17 + Flux2SingleTransformerBlock.hpp:53
+//   gated residual  ADD(h, MUL(o, gate[c]))          Flux2SingleTransformerBlock.hpp:58
+//   SwiGLU          MUL(MUL(g, SIGMOID(g)), u)        Flux2SwiGLU.hpp:20, SiLU.hpp:12
+//   GroupNorm+SiLU  MUL(a, SIGMOID(a)), a = ADD(MUL(VIEW(NORM(VIEW(x))), w), b)
+//                   GroupNorm.cpp:98-156 + SiLU.hpp:12 (affine / SiLU optional)
+//   QK-RMSNorm+RoPE CONCAT*(ROPE(VIEW_a(MUL(RMS_NORM(q), w))), ...) along ne0
+//                   RMSNorm.cpp:13-20 + Flux2PosEmbed.hpp:29-108, optionally
+//                   with the txt|img CONCAT of Flux2Attention.hpp:114-116
+//                   between the norm and the views.
+//
+// A chain is fused only when every interior node is consumed solely inside
+// the chain and is not flagged DT_FLAG_OUTPUT; everything else runs the
+// unfused per-op kernels of ops.hip.
+#include <algorithm>
+#include <cstring>
+#include <unordered_map>
+#include <vector>
+
+#include "capi_util.hpp"
+#include "dit_hip.h"
+#include "kernels.hpp"
+
+namespace dit {
+namespace {
+
+thread_local int g_kernels = 0;
+thread_local int g_fused = 0;
+
+float fparam(const dt_tensor* t, int i) {
+    float f;
+    std::memcpy(&f, &t->op_params[i], 4);
+    return f;
+}
+
+// Rows of ne[0] elements at a uniform row stride (in elements) covering
+// dims 1..3.
+bool row_layout(const dt_tensor* t, int64_t* rows, int64_t* stride) {
+    const int es = elem_size(t->type);
+    if (!es || t->nb[0] != es) return false;
+    int64_t rs;
+    if (t->ne[1] > 1) rs = t->nb[1];
+    else if (t->ne[2] > 1) rs = t->nb[2];
+    else if (t->ne[3] > 1) rs = t->nb[3];
+    else rs = t->ne[0] * es;
+    if (t->ne[1] > 1 && t->nb[1] != rs) return false;
+    if (t->ne[2] > 1 && t->nb[2] != rs * t->ne[1]) return false;
+    if (t->ne[3] > 1 && t->nb[3] != rs * t->ne[1] * t->ne[2]) return false;
+    if (rs % es) return false;
+    *rows = t->ne[1] * t->ne[2] * t->ne[3];
+    *stride = rs / es;
+    return true;
+}
+
+bool same_shape(const dt_tensor* a, const dt_tensor* b) {
+    for (int i = 0; i < 4; ++i)
+        if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+
+bool contiguous_f32(const dt_tensor* t) {
+    return t->type == DT_TYPE_F32 && t->nb[0] == 4 &&
+           (t->ne[1] == 1 || t->nb[1] == 4 * t->ne[0]) &&
+           (t->ne[2] == 1 || t->nb[2] == 4 * t->ne[0] * t->ne[1]) &&
+           (t->ne[3] == 1 || t->nb[3] == 4 * t->ne[0] * t->ne[1] * t->ne[2]);
+}
+
+// fp32 vector of n contiguous elements whose single non-unit dim is `dim`.
+bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
+    if (!t || !contiguous_f32(t)) return false;
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] != (i == dim ? n : 1)) return false;
+    return true;
+}
+
+enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU };
+
+struct QkSeg {
+    const dt_tensor* q;   // RMS_NORM input
+    const dt_tensor* w;   // norm weight [head_dim]
+    int64_t tok0, tokens; // token range inside the rope output
+    float eps;            // the RMS_NORM's eps
+};
+
+struct Plan {
+    Kind kind = K_NONE;
+    const dt_tensor* in[4] = {nullptr, nullptr, nullptr, nullptr};
+    float eps = 0.f;
+    int silu = 0;
+    // QK
+    std::vector<QkSeg> segs;
+    std::vector<const dt_tensor*> pos;  // per axis
+    int axis_dim = 0;
+    float base = 0.f;
+};
+
+struct Graph {
+    std::unordered_map<const dt_tensor*, int> uses;
+    std::unordered_map<const dt_tensor*, int> index;
+    std::vector<char> claimed;
+
+    bool internal(const dt_tensor* t, int n_uses = 1) const {
+        if (!t || (t->flags & DT_FLAG_OUTPUT)) return false;
+        auto i = index.find(t);
+        if (i == index.end() || claimed[i->second]) return false;
+        auto u = uses.find(t);
+        return u != uses.end() && u->second == n_uses;
+    }
+    void claim(const dt_tensor* t) { claimed[index.at(t)] = 1; }
+};
+
+bool match_adaln(Graph& g, const dt_tensor* a, Plan& p) {
+    if (a->op != DT_OP_ADD) return false;
+    const dt_tensor* m = a->src[0];
+    const dt_tensor* sh = a->src[1];
+    if (!m || m->op != DT_OP_MUL || !g.internal(m)) return false;
+    const dt_tensor* n = m->src[0];
+    const dt_tensor* t = m->src[1];
+    if (!n || n->op != DT_OP_NORM || !g.internal(n)) return false;
+    const dt_tensor* x = n->src[0];
+    const int64_t cols = x->ne[0];
+    int64_t r1, s1, r2, s2;
+    if (!is_vec(t, cols) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
+        !is_io_type(x->type) || !row_layout(x, &r1, &s1) || !row_layout(a, &r2, &s2))
+        return false;
+    g.claim(m);
+    g.claim(n);
+    p.kind = K_ADALN;
+    p.in[0] = x;
+    p.in[1] = t;
+    p.in[2] = sh;
+    p.eps = fparam(n, 0);
+    return true;
+}
+
+bool match_gated(Graph& g, const dt_tensor* a, Plan& p) {
+    if (a->op != DT_OP_ADD) return false;
+    for (int k = 1; k >= 0; --k) {
+        const dt_tensor* m = a->src[k];
+        const dt_tensor* h = a->src[1 - k];
+        if (!m || !h || m->op != DT_OP_MUL || !g.internal(m)) continue;
+        const dt_tensor* o = m->src[0];
+        const dt_tensor* gate = m->src[1];
+        int64_t r, s;
+        if (!is_vec(gate, a->ne[0]) || !same_shape(h, a) || !same_shape(o, a) ||
+            h->type != a->type || o->type != a->type || !is_io_type(a->type) ||
+            !row_layout(h, &r, &s) || !row_layout(o, &r, &s) || !row_layout(a, &r, &s))
+            continue;
+        g.claim(m);
+        p.kind = K_GATED;
+        p.in[0] = h;
+        p.in[1] = o;
+        p.in[2] = gate;
+        return true;
+    }
+    return false;
+}
+
+bool match_swiglu(Graph& g, const dt_tensor* y, Plan& p) {
+    if (y->op != DT_OP_MUL) return false;
+    for (int k = 0; k < 2; ++k) {
+        const dt_tensor* a = y->src[k];
+        const dt_tensor* u = y->src[1 - k];
+        if (!a || !u || a->op != DT_OP_MUL || !g.internal(a)) continue;
+        for (int j = 0; j < 2; ++j) {
+            const dt_tensor* gt = a->src[j];
+            const dt_tensor* s = a->src[1 - j];
+            if (!gt || !s || s->op != DT_OP_SIGMOID || s->src[0] != gt || !g.internal(s)) continue;
+            int64_t r, st;
+            if (!same_shape(gt, y) || !same_shape(u, y) || gt->type != y->type ||
+                u->type != y->type || !is_io_type(y->type) || !row_layout(gt, &r, &st) ||
+                !row_layout(u, &r, &st) || !row_layout(y, &r, &st))
+                continue;
+            g.claim(a);
+            g.claim(s);
+            p.kind = K_SWIGLU;
+            p.in[0] = gt;
+            p.in[1] = u;
+            return true;
+        }
+    }
+    return false;
+}
+
+// GroupNorm over x ne {W, H, C, N}: NORM of a VIEW with ne {C/G*H*W, G, N, 1},
+// VIEWed back to x's shape, then optional MUL(w), ADD(b), SiLU.
+bool match_groupnorm(Graph& g, const dt_tensor* root, Plan& p) {
+    std::vector<std::pair<const dt_tensor*, int>> chain;  // interior node, expected uses
+    const dt_tensor* cur = root;
+    int silu = 0;
+    if (root->op == DT_OP_MUL) {
+        for (int k = 0; k < 2; ++k) {
+            const dt_tensor* a = root->src[k];
+            const dt_tensor* s = root->src[1 - k];
+            if (a && s && s->op == DT_OP_SIGMOID && s->src[0] == a) {
+                silu = 1;
+                chain.push_back({s, 1});
+                cur = a;
+                break;
+            }
+        }
+    }
+    int cur_uses = silu ? 2 : 1;  // the SiLU input feeds both SIGMOID and the final MUL
+    auto push = [&](const dt_tensor* t) {
+        if (t != root) chain.push_back({t, cur_uses});
+        cur_uses = 1;
+    };
+    const dt_tensor *w = nullptr, *b = nullptr;
+    if (cur->op == DT_OP_ADD && cur->src[0] && cur->src[0]->op == DT_OP_MUL) {
+        b = cur->src[1];
+        push(cur);
+        cur = cur->src[0];
+    }
+    if (cur->op == DT_OP_MUL && cur->src[0] && cur->src[0]->op == DT_OP_VIEW) {
+        w = cur->src[1];
+        push(cur);
+        cur = cur->src[0];
+    }
+    if (cur->op != DT_OP_VIEW || !(silu || w || b)) return false;  // a bare norm runs unfused
+    const dt_tensor* r = cur;
+    push(r);
+    const dt_tensor* n = r->src[0];
+    if (!n || n->op != DT_OP_NORM) return false;
+    push(n);
+    const dt_tensor* v = n->src[0];
+    if (!v || v->op != DT_OP_VIEW) return false;
+    push(v);
+    const dt_tensor* x = v->src[0];
+    if (!x) return false;
+    for (const auto& c : chain)
+        if (!g.internal(c.first, c.second)) return false;
+    // Shapes: x is contiguous NCHW = ne {W, H, C, N}; v is ne {L, G, N, 1}.
+    const int64_t W_ = x->ne[0], H_ = x->ne[1], C = x->ne[2], N = x->ne[3];
+    const int64_t G = v->ne[1];
+    int64_t rows, stride;
+    if (!is_io_type(x->type) || x->type != root->type || !same_shape(x, root) || G <= 0 ||
+        C % G || v->ne[0] != C / G * H_ * W_ || v->ne[2] != N || v->ne[3] != 1 ||
+        !row_layout(x, &rows, &stride) || stride != W_ || !row_layout(root, &rows, &stride) ||
+        stride != W_ || v->data != x->data || r->data != n->data || !same_shape(r, x))
+        return false;
+    if ((w && !is_vec(w, C, 2)) || (b && !is_vec(b, C, 2))) return false;
+    for (const auto& c : chain) g.claim(c.first);
+    p.kind = K_GN;
+    p.in[0] = x;
+    p.in[1] = w;
+    p.in[2] = b;
+    p.in[3] = v;
+    p.eps = fparam(n, 0);
+    p.silu = silu;
+    return true;
+}
+
+// MUL(x, SIGMOID(x)): the SiLU module's composite (SiLU.hpp:12) as one kernel.
+bool match_silu(Graph& g, const dt_tensor* y, Plan& p) {
+    if (y->op != DT_OP_MUL) return false;
+    for (int k = 0; k < 2; ++k) {
+        const dt_tensor* x = y->src[k];
+        const dt_tensor* s = y->src[1 - k];
+        if (x && s && s->op == DT_OP_SIGMOID && s->src[0] == x && g.internal(s) &&
+            same_shape(x, y)) {
+            g.claim(s);
+            p.kind = K_SILU;
+            p.in[0] = x;
+            return true;
+        }
+    }
+    return false;
+}
+
+// Leaves of a CONCAT tree along ne0, left to right.
+bool concat_leaves(Graph& g, const dt_tensor* t, bool is_root, std::vector<const dt_tensor*>& out,
+                   std::vector<const dt_tensor*>& chain) {
+    if (t->op == DT_OP_CONCAT && t->op_params[0] == 0 && (is_root || g.internal(t))) {
+        if (!is_root) chain.push_back(t);
+        return concat_leaves(g, t->src[0], false, out, chain) &&
+               concat_leaves(g, t->src[1], false, out, chain);
+    }
+    out.push_back(t);
+    return true;
+}
+
+bool match_qk(Graph& g, const dt_tensor* y, Plan& p) {
+    if (y->op != DT_OP_CONCAT) return false;
+    std::vector<const dt_tensor*> leaves, chain;
+    if (!concat_leaves(g, y, true, leaves, chain) || leaves.size() < 2 ||
+        leaves.size() > (size_t)kMaxRopeAxes)
+        return false;
+    const int n_axes = (int)leaves.size();
+    const dt_tensor* wsrc = nullptr;
+    int axis_dim = 0;
+    float base = 0.f;
+    std::vector<const dt_tensor*> pos;
+    for (int a = 0; a < n_axes; ++a) {
+        const dt_tensor* r = leaves[a];
+        if (r->op != DT_OP_ROPE || !g.internal(r)) return false;
+        const dt_tensor* v = r->src[0];
+        const dt_tensor* ps = r->src[1];
+        if (!v || v->op != DT_OP_VIEW || !g.internal(v) || !ps || ps->type != DT_TYPE_I32) return false;
+        const int nd = r->op_params[0];
+        if (r->op_params[1] != 0 || fparam(r, 3) != 1.0f || fparam(r, 4) != 0.0f ||
+            fparam(r, 5) != 1.0f || nd != v->ne[0])
+            return false;
+        if (a == 0) {
+            wsrc = v->src[0];
+            axis_dim = nd;
+            base = fparam(r, 2);
+        }
+        if (v->src[0] != wsrc || nd != axis_dim || fparam(r, 2) != base) return false;
+        const int es = elem_size(wsrc->type);
+        if ((const char*)v->data - (const char*)wsrc->data != (int64_t)a * axis_dim * es) return false;
+        if (v->nb[0] != es) return false;
+        for (int i = 1; i < 4; ++i)
+            if (v->ne[i] != wsrc->ne[i] || v->nb[i] != wsrc->nb[i]) return false;
+        if (ps->ne[0] != wsrc->ne[2] || ps->ne[1] != 1 || ps->ne[2] != 1 || ps->ne[3] != 1 ||
+            ps->nb[0] % 4)
+            return false;
+        chain.push_back(r);
+        chain.push_back(v);
+        pos.push_back(ps);
+    }
+    if (!wsrc || !g.internal(wsrc, n_axes)) return false;
+    const int64_t head_dim = wsrc->ne[0];
+    if ((int64_t)n_axes * axis_dim != head_dim || !same_shape(wsrc, y) || y->ne[3] != 1 ||
+        y->type != wsrc->type || !is_io_type(y->type) || y->nb[0] != elem_size(y->type))
+        return false;
+    // Segments: MUL(RMS_NORM(q), w) directly, or a CONCAT of two along ne2.
+    std::vector<const dt_tensor*> muls;
+    std::vector<int64_t> tok0;
+    if (wsrc->op == DT_OP_CONCAT && wsrc->op_params[0] == 2) {
+        muls = {wsrc->src[0], wsrc->src[1]};
+        tok0 = {0, wsrc->src[0] ? wsrc->src[0]->ne[2] : 0};
+    } else {
+        muls = {wsrc};
+        tok0 = {0};
+    }
+    std::vector<QkSeg> segs;
+    for (size_t i = 0; i < muls.size(); ++i) {
+        const dt_tensor* m = muls[i];
+        if (!m || m->op != DT_OP_MUL) return false;
+        if (m != wsrc && !g.internal(m)) return false;
+        const dt_tensor* rn = m->src[0];
+        const dt_tensor* w = m->src[1];
+        if (!rn || rn->op != DT_OP_RMS_NORM || !g.internal(rn) || !is_vec(w, head_dim)) return false;
+        const dt_tensor* q = rn->src[0];
+        if (q->type != y->type || q->ne[0] != head_dim || q->ne[1] != y->ne[1] || q->ne[3] != 1 ||
+            q->nb[0] != elem_size(q->type))
+            return false;
+        if (m != wsrc) chain.push_back(m);
+        chain.push_back(rn);
+        segs.push_back({q, w, tok0[i], q->ne[2], fparam(rn, 0)});
+    }
+    if (segs.back().tok0 + segs.back().tokens != y->ne[2]) return false;
+    chain.push_back(wsrc);
+    for (const dt_tensor* t : chain) g.claim(t);
+    p.kind = K_QK;
+    p.segs = segs;
+    p.pos = pos;
+    p.axis_dim = axis_dim;
+    p.base = base;
+    return true;
+}
+
+int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
+    hipStream_t st = backend_stream(be);
+    switch (p.kind) {
+        case K_ADALN: {
+            int64_t rows, xs, ys;
+            row_layout(p.in[0], &rows, &xs);
+            row_layout(root, &rows, &ys);
+            ++g_kernels;
+            return adaln_launch(p.in[0]->data, rows, root->ne[0], xs, (const float*)p.in[2]->data,
+                                (const float*)p.in[1]->data, 0.0f, root->data, ys, p.eps,
+                                root->type, st);
+        }
+        case K_GATED: {
+            int64_t rows, hs, os, ys;
+            row_layout(p.in[0], &rows, &hs);
+            row_layout(p.in[1], &rows, &os);
+            row_layout(root, &rows, &ys);
+            ++g_kernels;
+            return dt_gated_residual(p.in[0]->data, hs, p.in[1]->data, os, (const float*)p.in[2]->data,
+                                     root->data, ys, rows, root->ne[0], root->type, st);
+        }
+        case K_SWIGLU: {
+            int64_t rows, gs, us, ys;
+            row_layout(p.in[0], &rows, &gs);
+            row_layout(p.in[1], &rows, &us);
+            row_layout(root, &rows, &ys);
+            ++g_kernels;
+            return dt_swiglu(p.in[0]->data, gs, p.in[1]->data, us, root->data, ys, rows, root->ne[0],
+                             root->type, st);
+        }
+        case K_GN: {
+            const dt_tensor* x = p.in[0];
+            const int64_t N = x->ne[3], C = x->ne[2], HW = x->ne[0] * x->ne[1], G = p.in[3]->ne[1];
+            const size_t ws_bytes = dt_groupnorm_workspace_bytes(N, C, HW, G);
+            void* ws = nullptr;
+            int rc = backend_scratch(be, ws_bytes, &ws);
+            if (rc) return rc;
+            g_kernels += 2;
+            return dt_groupnorm_silu(x->data, N, C, HW, G, p.in[1] ? (const float*)p.in[1]->data : nullptr,
+                                     p.in[2] ? (const float*)p.in[2]->data : nullptr, p.eps, p.silu,
+                                     root->data, ws, ws_bytes, root->type, st);
+        }
+        case K_QK: {
+            const int es = elem_size(root->type);
+            const int n_axes = (int)p.pos.size();
+            for (const QkSeg& s : p.segs) {
+                RopeAxisPos ap{};
+                for (int a = 0; a < n_axes; ++a) {
+                    ap.stride[a] = p.pos[a]->nb[0] / 4;
+                    ap.ptr[a] = (const int32_t*)p.pos[a]->data + s.tok0 * ap.stride[a];
+                }
+                const dt_tensor* q = s.q;
+                char* out = (char*)root->data + s.tok0 * root->nb[2];
+                ++g_kernels;
+                int rc = qk_launch(q->data, nullptr, out, nullptr, (const float*)s.w->data, nullptr,
+                                   s.tokens, q->ne[1], q->ne[0], q->nb[2] / es, q->nb[1] / es,
+                                   root->nb[2] / es, root->nb[1] / es, s.eps, ap,
+                                   n_axes, p.axis_dim, p.base, nullptr, 0, root->type, st);
+                if (rc) return rc;
+            }
+            return DT_OK;
+        }
+        case K_SILU:
+            ++g_kernels;
+            return dt_op_unary(DT_UN_SILU, p.in[0], root, 0.f, 0.f, st);
+        default:
+            return fail(DT_ERR_INVALID_ARG, "run_plan: no plan");
+    }
+}
+
+int run_unfused(dt_backend* be, dt_tensor* t) {
+    hipStream_t st = backend_stream(be);
+    switch (t->op) {
+        case DT_OP_NONE:
+        case DT_OP_VIEW:
+            return DT_OK;
+        case DT_OP_ADD:
+        case DT_OP_SUB:
+        case DT_OP_MUL:
+        case DT_OP_DIV:
+            ++g_kernels;
+            return dt_op_binary(t->op - DT_OP_ADD, t->src[0], t->src[1], t, st);
+        case DT_OP_SCALE:
+            ++g_kernels;
+            return dt_op_unary(DT_UN_SCALE, t->src[0], t, fparam(t, 0), 0.f, st);
+        case DT_OP_SIGMOID:
+            ++g_kernels;
+            return dt_op_unary(DT_UN_SIGMOID, t->src[0], t, 0.f, 0.f, st);
+        case DT_OP_FILL:
+            ++g_kernels;
+            return dt_op_unary(DT_UN_FILL, nullptr, t, fparam(t, 0), 0.f, st);
+        case DT_OP_NORM:
+            ++g_kernels;
+            return dt_op_norm(t->src[0], t, fparam(t, 0), st);
+        case DT_OP_RMS_NORM:
+            ++g_kernels;
+            return dt_op_rms_norm(t->src[0], t, fparam(t, 0), st);
+        case DT_OP_ROPE: {
+            const dt_tensor* ps = t->src[1];
+            DT_REQUIRE(ps && ps->type == DT_TYPE_I32 && ps->nb[0] == 4,
+                       "dt_graph_compute: ROPE positions must be contiguous I32");
+            ++g_kernels;
+            return dt_op_rope_ext(t->src[0], (const int32_t*)ps->data, t, t->op_params[0],
+                                  t->op_params[1], fparam(t, 2), fparam(t, 3), fparam(t, 4),
+                                  fparam(t, 5), st);
+        }
+        case DT_OP_CONCAT:
+            ++g_kernels;
+            return dt_op_concat(t->src[0], t->src[1], t->op_params[0], t, st);
+        case DT_OP_CPY:
+            ++g_kernels;
+            return dt_op_cpy(t->src[0], t, st);
+        default:
+            return fail(DT_ERR_UNSUPPORTED, "dt_graph_compute: op %d not supported", t->op);
+    }
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nodes) {
+    using namespace dit;
+    DT_REQUIRE(be != nullptr, "dt_graph_compute: null backend");
+    DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0), "dt_graph_compute: bad node list");
+    g_kernels = 0;
+    g_fused = 0;
+    Graph g;
+    g.claimed.assign(n_nodes, 0);
+    for (int i = 0; i < n_nodes; ++i) {
+        DT_REQUIRE(nodes[i] != nullptr, "dt_graph_compute: node %d is null", i);
+        g.index[nodes[i]] = i;
+        for (int s = 0; s < 4; ++s)
+            if (nodes[i]->src[s]) g.uses[nodes[i]->src[s]]++;
+    }
+    std::vector<Plan> plans(n_nodes);
+    for (int i = n_nodes - 1; i >= 0; --i) {
+        if (g.claimed[i]) continue;
+        dt_tensor* t = nodes[i];
+        Plan& p = plans[i];
+        if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_adaln(g, t, p) ||
+            match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p)) {
+            continue;
+        }
+        p = Plan();
+    }
+    for (int i = 0; i < n_nodes; ++i) {
+        if (g.claimed[i]) {
+            ++g_fused;
+            continue;
+        }
+        int rc = plans[i].kind != K_NONE ? run_plan(be, nodes[i], plans[i]) : run_unfused(be, nodes[i]);
+        if (rc) return rc;
+    }
+    return DT_OK;
+}
+
+extern "C" int dt_graph_last_stats(int32_t* kernels_launched, int32_t* nodes_fused) {
+    if (kernels_launched) *kernels_launched = dit::g_kernels;
+    if (nodes_fused) *nodes_fused = dit::g_fused;
+    return DT_OK;
+}

@@ -1,0 +1,41 @@
+// kernels.hpp -- internal launchers shared by the C-ABI entry points and the
+// graph executor (graph.cpp).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dit_hip.h"
+
+struct dt_backend;
+
+namespace dit {
+
+// y = (x - mean) * rstd * (scale + addend) + shift per row.  The public
+// dt_adaln_mod uses addend 1 (the reference's `1 + scale`); the graph
+// executor passes addend 0 with an already-computed factor tensor.
+int adaln_launch(const void* x, int64_t rows, int64_t cols, int64_t xs, const float* shift,
+                 const float* scale, float addend, void* y, int64_t ys, float eps, int32_t io,
+                 hipStream_t st);
+
+constexpr int kMaxRopeAxes = 8;
+
+// Position of token t on axis a: ptr[a][t * stride[a]].
+struct RopeAxisPos {
+    const int32_t* ptr[kMaxRopeAxes];
+    int64_t stride[kMaxRopeAxes];
+};
+
+int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const float* wq,
+              const float* wk, int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts,
+              int64_t in_hs, int64_t out_ts, int64_t out_hs, float eps, const RopeAxisPos& pos,
+              int n_axes, int axis_dim, float freq_base, const float* table, int n_pos, int32_t io,
+              hipStream_t st);
+
+// Backend accessors (capi.cpp).
+hipStream_t backend_stream(dt_backend* be);
+int backend_device(dt_backend* be);
+// Backend-owned scratch of at least `bytes` (grown on demand, freed with the backend).
+int backend_scratch(dt_backend* be, size_t bytes, void** out);
+
+}  // namespace dit

@@ -1,0 +1,295 @@
+// qk_rope.hip -- fused per-head RMSNorm(q,k) * w + multi-axis RoPE (NORMAL
+// mode, adjacent pairs), the node chain RMSNorm::forward (RMS_NORM + MUL)
+// and Flux2PosEmbed::forward (4x ROPE on 32-wide views + 3x CONCAT) emit per
+// q and per k (Flux2Attention.hpp:93-122, Flux2ParallelSelfAttention.hpp:
+// 181-194, Flux2PosEmbed.hpp:29-108).
+//
+// Fast path (head_dim 128, axis_dim % 8 == 0): a head is one 16-lane DPP row,
+// each lane owns 8 consecutive dims (one 16-byte bf16 load, two for fp32) =
+// 4 rotation pairs of a single axis.  The sum of squares is a 4-step DPP
+// row reduction.  cos/sin come from a table built on the host with ggml's
+// fp32 angle recurrence, so angles match the CPU op exactly; the table is a
+// few tens of KB and stays L2-resident.  q and k go in one launch
+// (blockIdx.y selects the tensor); the per-lane norm weights stay in VGPRs.
+#include <math.h>
+
+#include <utility>
+
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace dit {
+namespace {
+
+struct QkHalf {
+    const void* x;
+    void* y;
+    const float* w;
+};
+
+struct QkShape {
+    int64_t in_ts, in_hs, out_ts, out_hs;
+    RopeAxisPos pos;
+    int tokens, heads, head_dim, axis_dim, n_axes, n_pos;
+    float eps, theta_scale;
+};
+
+// Position pointer and token stride of one axis, chosen with an unrolled
+// select so the kernel-argument arrays are never indexed dynamically.
+__device__ __forceinline__ void axis_pos(const QkShape& sh, int axis, const int32_t*& p,
+                                         int64_t& stride) {
+    p = sh.pos.ptr[0];
+    stride = sh.pos.stride[0];
+#pragma unroll
+    for (int a = 1; a < kMaxRopeAxes; ++a) {
+        if (axis == a) {
+            p = sh.pos.ptr[a];
+            stride = sh.pos.stride[a];
+        }
+    }
+}
+
+// cos/sin of pairs [i0/2, i0/2 + NP) of an axis at position p.
+template <int NP>
+__device__ __forceinline__ void rope_angles(int p, int i0, const float* __restrict__ table,
+                                            int n_pos, int axis_dim, float theta_scale,
+                                            float* cs) {
+    if (table != nullptr && p >= 0 && p < n_pos) {
+        const float* t = table + (int64_t)p * axis_dim + i0;
+#pragma unroll
+        for (int e = 0; e < 2 * NP; e += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(t + e);
+            cs[e] = a.x; cs[e + 1] = a.y; cs[e + 2] = a.z; cs[e + 3] = a.w;
+        }
+    } else {
+        // Same fp32 recurrence as the table: theta_0 = p, theta *= scale.
+        float theta = (float)p;
+        for (int k = 0; k < i0 / 2; ++k) theta = mul_rn(theta, theta_scale);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            cs[2 * q] = cosf(theta);
+            cs[2 * q + 1] = sinf(theta);
+            theta = mul_rn(theta, theta_scale);
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* v);
+template <>
+__device__ __forceinline__ void load8<bf16>(const bf16* p, float* v) { Io<bf16>::load(p, v); }
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* v) {
+    Io<float>::load(p, v);
+    Io<float>::load(p + 4, v + 4);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* v);
+template <>
+__device__ __forceinline__ void store8<bf16>(bf16* p, const float* v) { Io<bf16>::store(p, v); }
+template <>
+__device__ __forceinline__ void store8<float>(float* p, const float* v) {
+    Io<float>::store(p, v);
+    Io<float>::store(p + 4, v + 4);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkShape sh,
+                                                         const float* __restrict__ table) {
+    const QkHalf a = blockIdx.y == 0 ? q : k;
+    if (a.x == nullptr) return;
+    const int lane16 = threadIdx.x & 15;
+    const int d0 = lane16 * 8;
+    const int axis = d0 / sh.axis_dim;
+    const int i0 = d0 - axis * sh.axis_dim;
+    const int32_t* pax;
+    int64_t pst;
+    axis_pos(sh, axis, pax, pst);
+
+    float w[8];
+    load8<float>(a.w + d0, w);
+
+    const int n_groups = sh.tokens * sh.heads;
+    const int g0 = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
+    const int gstride = (int)((gridDim.x * blockDim.x) >> 4);
+    const T* __restrict__ xb = (const T*)a.x;
+    T* __restrict__ yb = (T*)a.y;
+    const float hd_f = (float)sh.head_dim;
+
+    for (int g = g0; g < n_groups; g += gstride) {
+        const int t = g / sh.heads;
+        const int h = g - t * sh.heads;
+        float v[8];
+        load8<T>(xb + t * sh.in_ts + h * sh.in_hs + d0, v);
+        const int p = pax[t * pst];
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+        ss = row16_sum(ss);
+        const float r = 1.0f / sqrtf(ss / hd_f + sh.eps);
+        float cs[8];
+        rope_angles<4>(p, i0, table, sh.n_pos, sh.axis_dim, sh.theta_scale, cs);
+        float o[8];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const float x0 = mul_rn(mul_rn(v[2 * qd], r), w[2 * qd]);
+            const float x1 = mul_rn(mul_rn(v[2 * qd + 1], r), w[2 * qd + 1]);
+            const float c = cs[2 * qd], s = cs[2 * qd + 1];
+            o[2 * qd] = sub_rn(mul_rn(x0, c), mul_rn(x1, s));
+            o[2 * qd + 1] = add_rn(mul_rn(x0, s), mul_rn(x1, c));
+        }
+        store8<T>(yb + t * sh.out_ts + h * sh.out_hs + d0, o);
+    }
+}
+
+// Any head_dim / axis_dim (even) / stride: one thread per (token, head).
+template <typename T>
+__global__ __launch_bounds__(256) void qk_rope_generic_kernel(QkHalf q, QkHalf k, QkShape sh,
+                                                              const float* __restrict__ table) {
+    const QkHalf a = blockIdx.y == 0 ? q : k;
+    if (a.x == nullptr) return;
+    const int64_t n_groups = (int64_t)sh.tokens * sh.heads;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_groups) return;
+    const int64_t t = g / sh.heads, h = g % sh.heads;
+    const T* xr = (const T*)a.x + t * sh.in_ts + h * sh.in_hs;
+    T* yr = (T*)a.y + t * sh.out_ts + h * sh.out_hs;
+    float ss = 0.f;
+    for (int d = 0; d < sh.head_dim; ++d) {
+        const float v = Io<T>::get(xr + d);
+        ss += v * v;
+    }
+    const float r = 1.0f / sqrtf(ss / (float)sh.head_dim + sh.eps);
+    // Pairs are read before either element is written, so y may alias x.
+    for (int d = 0; d < sh.head_dim; d += 2) {
+        const int axis = d / sh.axis_dim, i0 = d - axis * sh.axis_dim;
+        const int32_t* pax;
+        int64_t pst;
+        axis_pos(sh, axis, pax, pst);
+        const int p = pax[t * pst];
+        float cs[2];
+        if (table != nullptr && p >= 0 && p < sh.n_pos) {
+            cs[0] = table[(int64_t)p * sh.axis_dim + i0];
+            cs[1] = table[(int64_t)p * sh.axis_dim + i0 + 1];
+        } else {
+            rope_angles<1>(p, i0, nullptr, 0, sh.axis_dim, sh.theta_scale, cs);
+        }
+        const float x0 = mul_rn(mul_rn(Io<T>::get(xr + d), r), a.w[d]);
+        const float x1 = mul_rn(mul_rn(Io<T>::get(xr + d + 1), r), a.w[d + 1]);
+        Io<T>::put(yr + d, sub_rn(mul_rn(x0, cs[0]), mul_rn(x1, cs[1])));
+        Io<T>::put(yr + d + 1, add_rn(mul_rn(x0, cs[1]), mul_rn(x1, cs[0])));
+    }
+}
+
+template <typename T>
+int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t st) {
+    constexpr int EPV = Io<T>::EPV;
+    bool fast = sh.head_dim == 128 && sh.axis_dim % 8 == 0 && sh.in_ts % EPV == 0 &&
+                sh.in_hs % EPV == 0 && sh.out_ts % EPV == 0 && sh.out_hs % EPV == 0 &&
+                (table == nullptr || aligned16(table));
+    const int64_t max_in = (int64_t)(sh.tokens - 1) * sh.in_ts + (int64_t)(sh.heads - 1) * sh.in_hs + sh.head_dim;
+    const int64_t max_out = (int64_t)(sh.tokens - 1) * sh.out_ts + (int64_t)(sh.heads - 1) * sh.out_hs + sh.head_dim;
+    fast = fast && max_in < (1ll << 31) && max_out < (1ll << 31) &&
+           (int64_t)sh.tokens * sh.heads < (1ll << 31);
+    for (const QkHalf* h : {&q, &k})
+        if (h->x) fast = fast && aligned16(h->x) && aligned16(h->y) && aligned16(h->w);
+    const int ny = k.x ? 2 : 1;
+    if (fast) {
+        const int64_t groups = (int64_t)sh.tokens * sh.heads;
+        int64_t blocks = (groups * 16 + 255) / 256;
+        const int64_t cap = (int64_t)cu_count() * 32;
+        if (blocks > cap) blocks = cap;
+        hipLaunchKernelGGL((qk_rope128_kernel<T>), dim3((unsigned)blocks, ny), dim3(256), 0, st,
+                           q, k, sh, table);
+    } else {
+        const int64_t groups = (int64_t)sh.tokens * sh.heads;
+        const int64_t blocks = (groups + 255) / 256;
+        DT_REQUIRE(blocks < (1ll << 31), "dt_qk_rmsnorm_rope: too many heads");
+        hipLaunchKernelGGL((qk_rope_generic_kernel<T>), dim3((unsigned)blocks, ny), dim3(256), 0,
+                           st, q, k, sh, table);
+    }
+    return check_launch("dt_qk_rmsnorm_rope");
+}
+
+}  // namespace
+
+int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const float* wq,
+              const float* wk, int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts,
+              int64_t in_hs, int64_t out_ts, int64_t out_hs, float eps, const RopeAxisPos& pos,
+              int n_axes, int axis_dim, float freq_base, const float* table, int n_pos, int32_t io,
+              hipStream_t st) {
+    DT_REQUIRE(is_io_type(io), "dt_qk_rmsnorm_rope: io_type %d unsupported", io);
+    DT_REQUIRE(tokens >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0,
+               "dt_qk_rmsnorm_rope: bad shape");
+    DT_REQUIRE(n_axes > 0 && n_axes <= kMaxRopeAxes && axis_dim > 0 && axis_dim % 2 == 0 &&
+                   (int64_t)n_axes * axis_dim == head_dim,
+               "dt_qk_rmsnorm_rope: need n_axes <= %d and n_axes*axis_dim (%d*%d) == head_dim %lld",
+               kMaxRopeAxes, n_axes, axis_dim, (long long)head_dim);
+    DT_REQUIRE(in_hs >= head_dim && out_hs >= head_dim && in_ts >= 0 && out_ts >= 0,
+               "dt_qk_rmsnorm_rope: bad strides");
+    DT_REQUIRE(tokens < (1ll << 31) && heads < (1ll << 31) && head_dim < (1ll << 31),
+               "dt_qk_rmsnorm_rope: shape too large");
+    DT_REQUIRE(n_pos >= 0, "dt_qk_rmsnorm_rope: n_pos < 0");
+    if (tokens == 0 || (!q && !k)) return DT_OK;
+    for (int a = 0; a < n_axes; ++a)
+        DT_REQUIRE(pos.ptr[a] != nullptr, "dt_qk_rmsnorm_rope: null position pointer for axis %d", a);
+    DT_REQUIRE(!q || (q_out && wq), "dt_qk_rmsnorm_rope: q given without q_out/wq");
+    DT_REQUIRE(!k || (k_out && wk), "dt_qk_rmsnorm_rope: k given without k_out/wk");
+    QkHalf hq{q, q_out, wq}, hk{k, k_out, wk};
+    if (!q) std::swap(hq, hk);  // k alone runs as the first half
+    QkShape sh;
+    sh.in_ts = in_ts; sh.in_hs = in_hs;
+    sh.out_ts = out_ts; sh.out_hs = out_hs;
+    sh.pos = pos;
+    for (int a = n_axes; a < kMaxRopeAxes; ++a) {
+        sh.pos.ptr[a] = pos.ptr[0];
+        sh.pos.stride[a] = pos.stride[0];
+    }
+    sh.tokens = (int)tokens; sh.heads = (int)heads; sh.head_dim = (int)head_dim;
+    sh.axis_dim = axis_dim; sh.n_axes = n_axes; sh.n_pos = table ? n_pos : 0;
+    sh.eps = eps;
+    sh.theta_scale = powf(freq_base, -2.0f / (float)axis_dim);
+    if (io == DT_TYPE_F32) return run<float>(hq, hk, sh, table, st);
+    return run<bf16>(hq, hk, sh, table, st);
+}
+
+}  // namespace dit
+
+extern "C" int dt_rope_table_fill(float* table, int32_t n_pos, int32_t n_dims, float freq_base,
+                                  float freq_scale, float attn_factor) {
+    DT_REQUIRE(table != nullptr && n_pos >= 0 && n_dims > 0 && n_dims % 2 == 0,
+               "dt_rope_table_fill: bad arguments");
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    for (int32_t p = 0; p < n_pos; ++p) {
+        float theta = (float)p;
+        float* row = table + (int64_t)p * n_dims;
+        for (int32_t i0 = 0; i0 < n_dims; i0 += 2) {
+            const float t = freq_scale * theta;
+            row[i0] = cosf(t) * attn_factor;
+            row[i0 + 1] = sinf(t) * attn_factor;
+            theta *= theta_scale;
+        }
+    }
+    return DT_OK;
+}
+
+extern "C" int dt_qk_rmsnorm_rope(const void* q, const void* k, void* q_out, void* k_out,
+                                  int64_t tokens, int64_t heads, int64_t head_dim,
+                                  int64_t in_tok_stride, int64_t in_head_stride,
+                                  int64_t out_tok_stride, int64_t out_head_stride,
+                                  const float* wq, const float* wk, float eps,
+                                  const int32_t* pos, int64_t pos_stride, int32_t n_axes,
+                                  int32_t axis_dim, float freq_base, const float* rope_table,
+                                  int32_t n_pos, int32_t io_type, dt_stream_t stream) {
+    DT_REQUIRE(n_axes > 0 && n_axes <= dit::kMaxRopeAxes, "dt_qk_rmsnorm_rope: n_axes %d", n_axes);
+    DT_REQUIRE(pos_stride >= n_axes, "dt_qk_rmsnorm_rope: pos_stride < n_axes");
+    dit::RopeAxisPos ap{};
+    for (int a = 0; a < n_axes; ++a) {
+        ap.ptr[a] = pos ? pos + a : nullptr;
+        ap.stride[a] = pos_stride;
+    }
+    return dit::qk_launch(q, k, q_out, k_out, wq, wk, tokens, heads, head_dim, in_tok_stride,
+                          in_head_stride, out_tok_stride, out_head_stride, eps, ap, n_axes,
+                          axis_dim, freq_base, rope_table, n_pos, io_type, (hipStream_t)stream);
+}

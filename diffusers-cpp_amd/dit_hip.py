@@ -1,0 +1,343 @@
+"""ctypes binding of libdit_hip.so (include/dit_hip.h) for Python callers.
+
+Device memory and streams come from PyTorch-ROCm tensors; every call goes
+through the C ABI of the HIP library.  There is no fallback: if the library
+is missing or a call fails, a `DtError` is raised.
+
+Shapes follow PyTorch order at this level; `desc()` converts a tensor to the
+ggml-ordered `dt_tensor` descriptor (ne[0] = last PyTorch dim).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_void_p
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libdit_hip.so")
+
+# ggml type ids
+F32, F16, Q8_0, Q4_K, I32, BF16 = 0, 1, 8, 12, 26, 30
+
+# dt_tensor.op ids
+(OP_NONE, OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_SCALE, OP_SIGMOID, OP_NORM, OP_RMS_NORM,
+ OP_ROPE, OP_CONCAT, OP_CPY, OP_VIEW, OP_FILL) = range(14)
+FLAG_OUTPUT = 1
+
+BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = range(4)
+(UN_SIGMOID, UN_EXP, UN_LOG, UN_SQRT, UN_SIN, UN_COS, UN_SCALE, UN_CLAMP, UN_SILU,
+ UN_FILL) = range(10)
+
+
+class DtError(RuntimeError):
+    pass
+
+
+class DtTensor(ctypes.Structure):
+    pass
+
+
+DtTensor._fields_ = [
+    ("type", c_int32),
+    ("op", c_int32),
+    ("ne", c_int64 * 4),
+    ("nb", c_int64 * 4),
+    ("data", c_void_p),
+    ("op_params", c_int32 * 16),
+    ("src", POINTER(DtTensor) * 4),
+    ("flags", c_int32),
+    ("id", c_int32),
+]
+
+# Every exported symbol with (restype, argtypes).
+_S = c_void_p
+_SIGS = {
+    "dt_last_error": (c_char_p, []),
+    "dt_version": (c_char_p, []),
+    "dt_adaln_mod": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                               c_int64, c_float, c_int32, _S]),
+    "dt_qk_rmsnorm_rope": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                     c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
+                                     c_void_p, c_float, c_void_p, c_int64, c_int32, c_int32,
+                                     c_float, c_void_p, c_int32, c_int32, _S]),
+    "dt_rope_table_fill": (c_int32, [c_void_p, c_int32, c_int32, c_float, c_float, c_float]),
+    "dt_swiglu": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+                            c_int64, c_int32, _S]),
+    "dt_gated_residual": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                    c_int64, c_int64, c_int64, c_int32, _S]),
+    "dt_dequant": (c_int32, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
+                             c_int32, _S]),
+    "dt_groupnorm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64]),
+    "dt_groupnorm_silu": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p,
+                                    c_void_p, c_float, c_int32, c_void_p, c_void_p, c_size_t,
+                                    c_int32, _S]),
+    "dt_euler_step": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_int64, c_int32, _S]),
+    "dt_op_binary": (c_int32, [c_int32, POINTER(DtTensor), POINTER(DtTensor), POINTER(DtTensor), _S]),
+    "dt_op_unary": (c_int32, [c_int32, POINTER(DtTensor), POINTER(DtTensor), c_float, c_float, _S]),
+    "dt_op_norm": (c_int32, [POINTER(DtTensor), POINTER(DtTensor), c_float, _S]),
+    "dt_op_rms_norm": (c_int32, [POINTER(DtTensor), POINTER(DtTensor), c_float, _S]),
+    "dt_op_rope_ext": (c_int32, [POINTER(DtTensor), c_void_p, POINTER(DtTensor), c_int32, c_int32,
+                                 c_float, c_float, c_float, c_float, _S]),
+    "dt_op_concat": (c_int32, [POINTER(DtTensor), POINTER(DtTensor), c_int32, POINTER(DtTensor), _S]),
+    "dt_op_cpy": (c_int32, [POINTER(DtTensor), POINTER(DtTensor), _S]),
+    "dt_backend_init": (c_int32, [c_int32, POINTER(c_void_p)]),
+    "dt_backend_free": (c_int32, [c_void_p]),
+    "dt_backend_set_stream": (c_int32, [c_void_p, _S]),
+    "dt_backend_synchronize": (c_int32, [c_void_p]),
+    "dt_buffer_alloc": (c_int32, [c_void_p, c_size_t, POINTER(c_void_p)]),
+    "dt_buffer_free": (c_int32, [c_void_p, c_void_p]),
+    "dt_tensor_set": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
+    "dt_tensor_get": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
+    "dt_graph_compute": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32]),
+    "dt_graph_last_stats": (c_int32, [POINTER(c_int32), POINTER(c_int32)]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load the library (once) and declare every signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise DtError(f"{path} is not built: run `make -C diffusers-cpp_amd` "
+                      "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+def check(rc: int, what: str = ""):
+    if rc != 0:
+        msg = load().dt_last_error().decode()
+        raise DtError(f"{what or 'dit_hip'} failed (status {rc}): {msg}")
+
+
+# --------------------------------------------------------------------------
+# torch helpers
+# --------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def io_type(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    if t.dtype == torch.float16:
+        return F16
+    if t.dtype == torch.int32:
+        return I32
+    raise DtError(f"unsupported dtype {t.dtype}")
+
+
+def _p(t):
+    return None if t is None else c_void_p(t.data_ptr())
+
+
+def stream():
+    return c_void_p(_torch().cuda.current_stream().cuda_stream)
+
+
+def desc(t, op=OP_NONE) -> DtTensor:
+    """ggml-ordered descriptor of a torch tensor (at most 4-D)."""
+    if t.dim() > 4:
+        raise DtError("at most 4 dims")
+    d = DtTensor()
+    d.type = io_type(t)
+    d.op = op
+    es = t.element_size()
+    shape = list(t.shape)[::-1] + [1] * (4 - t.dim())
+    strides = [s * es for s in list(t.stride())[::-1]]
+    for i in range(4):
+        d.ne[i] = shape[i]
+        if i < len(strides):
+            d.nb[i] = strides[i]
+        else:
+            d.nb[i] = (d.nb[i - 1] * d.ne[i - 1]) if i > 0 else es
+    d.data = t.data_ptr()
+    return d
+
+
+def _rows(t):
+    """(rows, cols, row_stride) of a tensor whose last dim is contiguous and
+    whose leading dims collapse to a uniform row stride."""
+    if t.stride(-1) != 1:
+        raise DtError("last dim must be contiguous")
+    cols = t.shape[-1]
+    if t.dim() == 1:
+        return 1, cols, cols
+    rows = 1
+    for s in t.shape[:-1]:
+        rows *= s
+    rs = t.stride(-2)
+    expect = rs
+    for i in range(t.dim() - 2, -1, -1):
+        if t.shape[i] > 1 and t.stride(i) != expect:
+            raise DtError("leading dims do not collapse to one row stride")
+        expect *= t.shape[i]
+    return rows, cols, rs
+
+
+# --------------------------------------------------------------------------
+# fused entry points
+# --------------------------------------------------------------------------
+
+def adaln_mod(x, shift, scale, eps=1e-6, out=None):
+    torch = _torch()
+    rows, cols, xs = _rows(x)
+    y = torch.empty_like(x) if out is None else out
+    _, _, ys = _rows(y)
+    check(load().dt_adaln_mod(_p(x), rows, cols, xs, _p(shift), _p(scale), _p(y), ys, eps,
+                              io_type(x), stream()), "dt_adaln_mod")
+    return y
+
+
+def rope_table(n_pos: int, n_dims: int, freq_base: float, device="cuda"):
+    """cos/sin table [n_pos, n_dims] (ggml fp32 recurrence), on `device`."""
+    torch = _torch()
+    host = torch.empty((n_pos, n_dims), dtype=torch.float32)
+    check(load().dt_rope_table_fill(c_void_p(host.data_ptr()), n_pos, n_dims, freq_base, 1.0, 1.0),
+          "dt_rope_table_fill")
+    return host.to(device) if device != "cpu" else host
+
+
+def qk_rmsnorm_rope(q, k, wq, wk, pos, axis_dim, freq_base, eps=1e-6, table=None,
+                    q_out=None, k_out=None):
+    """q, k: [tokens, heads, head_dim] views (strides honoured); pos: int32
+    [tokens, n_axes] (row stride honoured)."""
+    torch = _torch()
+    x = q if q is not None else k
+    tokens, heads, head_dim = x.shape
+    if q is not None and q_out is None:
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if k is not None and k_out is None:
+        k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    o = q_out if q is not None else k_out
+    for a, b in ((q, k), (q_out, k_out)):
+        if a is not None and b is not None and a.stride() != b.stride():
+            raise DtError("q and k (and their outputs) must share strides")
+    if x.stride(2) != 1 or o.stride(2) != 1 or pos.stride(1) != 1:
+        raise DtError("head_dim and axis columns must be contiguous")
+    n_axes = pos.shape[1]
+    n_pos = 0 if table is None else table.shape[0]
+    check(load().dt_qk_rmsnorm_rope(
+        _p(q), _p(k), _p(q_out), _p(k_out), tokens, heads, head_dim, x.stride(0), x.stride(1),
+        o.stride(0), o.stride(1), _p(wq), _p(wk), eps, _p(pos), pos.stride(0), n_axes, axis_dim,
+        freq_base, _p(table), n_pos, io_type(x), stream()), "dt_qk_rmsnorm_rope")
+    return q_out, k_out
+
+
+def swiglu(gate, up, out=None):
+    torch = _torch()
+    rows, cols, gs = _rows(gate)
+    _, _, us = _rows(up)
+    y = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device) if out is None else out
+    _, _, ys = _rows(y)
+    check(load().dt_swiglu(_p(gate), gs, _p(up), us, _p(y), ys, rows, cols, io_type(gate),
+                           stream()), "dt_swiglu")
+    return y
+
+
+def gated_residual(h, o, gate, out=None):
+    torch = _torch()
+    rows, cols, hs = _rows(h)
+    _, _, os_ = _rows(o)
+    y = torch.empty(h.shape, dtype=h.dtype, device=h.device) if out is None else out
+    _, _, ys = _rows(y)
+    check(load().dt_gated_residual(_p(h), hs, _p(o), os_, _p(gate), _p(y), ys, rows, cols,
+                                   io_type(h), stream()), "dt_gated_residual")
+    return y
+
+
+def block_bytes(qtype: int) -> tuple[int, int]:
+    """(elements per block, bytes per block)"""
+    return (32, 34) if qtype == Q8_0 else (256, 144)
+
+
+def dequant(src, qtype, rows, cols, out_dtype=None, out=None):
+    """src: uint8 device tensor of rows*(cols/qk)*block bytes."""
+    torch = _torch()
+    out_dtype = out_dtype or torch.bfloat16
+    qk, bs = block_bytes(qtype)
+    y = torch.empty((rows, cols), dtype=out_dtype, device=src.device) if out is None else out
+    check(load().dt_dequant(_p(src), qtype, rows, cols, cols // qk * bs, _p(y), y.stride(0),
+                            io_type(y), stream()), "dt_dequant")
+    return y
+
+
+def groupnorm_silu(x, groups, w=None, b=None, eps=1e-6, silu=True, out=None, workspace=None):
+    """x: [N, C, H, W] contiguous."""
+    torch = _torch()
+    N, C, H, W = x.shape
+    HW = H * W
+    lib = load()
+    nbytes = lib.dt_groupnorm_workspace_bytes(N, C, HW, groups)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=x.device)
+    y = torch.empty_like(x) if out is None else out
+    check(lib.dt_groupnorm_silu(_p(x), N, C, HW, groups, _p(w), _p(b), eps, 1 if silu else 0,
+                                _p(y), _p(workspace), workspace.numel(), io_type(x), stream()),
+          "dt_groupnorm_silu")
+    return y
+
+
+def euler_step(x, v, dt, out=None):
+    torch = _torch()
+    y = torch.empty_like(x) if out is None else out
+    check(load().dt_euler_step(_p(x), _p(v), dt, _p(y), x.numel(), io_type(x), stream()),
+          "dt_euler_step")
+    return y
+
+
+# --------------------------------------------------------------------------
+# unfused ops on descriptors
+# --------------------------------------------------------------------------
+
+def op_binary(op, a, b, out):
+    check(load().dt_op_binary(op, ctypes.byref(desc(a)), ctypes.byref(desc(b)),
+                              ctypes.byref(desc(out)), stream()), "dt_op_binary")
+    return out
+
+
+def op_unary(op, a, out, p0=0.0, p1=0.0):
+    da = None if a is None else ctypes.byref(desc(a))
+    check(load().dt_op_unary(op, da, ctypes.byref(desc(out)), p0, p1, stream()), "dt_op_unary")
+    return out
+
+
+def op_norm(a, out, eps, rms=False):
+    fn = load().dt_op_rms_norm if rms else load().dt_op_norm
+    check(fn(ctypes.byref(desc(a)), ctypes.byref(desc(out)), eps, stream()), "dt_op_norm")
+    return out
+
+
+def op_rope(a, pos, out, n_dims, freq_base, freq_scale=1.0, attn_factor=1.0, mode=0):
+    check(load().dt_op_rope_ext(ctypes.byref(desc(a)), _p(pos), ctypes.byref(desc(out)), n_dims,
+                                mode, freq_base, freq_scale, 0.0, attn_factor, stream()),
+          "dt_op_rope_ext")
+    return out
+
+
+def op_concat(a, b, dim_ggml, out):
+    check(load().dt_op_concat(ctypes.byref(desc(a)), ctypes.byref(desc(b)), dim_ggml,
+                              ctypes.byref(desc(out)), stream()), "dt_op_concat")
+    return out
+
+
+def op_cpy(a, out):
+    check(load().dt_op_cpy(ctypes.byref(desc(a)), ctypes.byref(desc(out)), stream()), "dt_op_cpy")
+    return out

@@ -1,0 +1,263 @@
+/*
+ * dit_hip.h -- C ABI of libdit_hip.so: MI355X (gfx950) kernels for the
+ * Flux2 DiT elementwise / reduction / broadcast chain of diffusers-cpp.
+ *
+ * The reference reaches this arithmetic through its `Runtime` op-builder
+ * (src/ggml/Runtime.hpp:7-317), which forwards 1:1 to ggml
+ * (src/ggml/ExecutionRuntime.cpp:319-766) and executes the graph with
+ * ggml_backend_graph_compute (src/ggml/ExecutionRuntime.cpp:227, 254).
+ * This library replaces the ggml backend for that op subset.  It exposes
+ * three groups of entry points:
+ *
+ *   (i)   a ggml-shaped tensor descriptor and graph executor (dt_graph_*),
+ *         which pattern-matches the op chains the reference emits and
+ *         lowers them to the fused kernels;
+ *   (ii)  the fused kernels themselves (dt_adaln_mod, dt_qk_rmsnorm_rope,
+ *         dt_swiglu, dt_gated_residual, dt_dequant, dt_groupnorm_silu);
+ *   (iii) unfused single-op kernels with ggml semantics (dt_op_*), used
+ *         where no fusion pattern applies.
+ *
+ * Conventions
+ *  - Every pointer named x/y/src/dst/... is DEVICE memory owned by the
+ *    caller; the library never allocates device memory except where a
+ *    function says so (dt_buffer_alloc).
+ *  - `stream` is a hipStream_t (NULL = the default stream).  All kernels are
+ *    stream-ordered and asynchronous; none synchronises the device.
+ *  - Strides are in ELEMENTS unless named *_bytes / nb.
+ *  - Every function returns 0 (DT_OK) or a DT_ERR_* code and never aborts;
+ *    dt_last_error() returns a thread-local message for the last failure.
+ *  - io_type selects the element type of activations: DT_TYPE_F32 or
+ *    DT_TYPE_BF16 (all arithmetic is fp32 either way).  Modulation vectors,
+ *    norm weights and rope tables are always fp32.
+ */
+#ifndef DIT_HIP_H
+#define DIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (ggml.h enum ggml_type), kept numerically identical. */
+enum {
+    DT_TYPE_F32 = 0,
+    DT_TYPE_F16 = 1,
+    DT_TYPE_Q8_0 = 8,
+    DT_TYPE_Q4_K = 12,
+    DT_TYPE_I32 = 26,
+    DT_TYPE_BF16 = 30
+};
+
+enum {
+    DT_OK = 0,
+    DT_ERR_INVALID_ARG = 1,
+    DT_ERR_UNSUPPORTED = 2,
+    DT_ERR_HIP = 3,
+    DT_ERR_OOM = 4
+};
+
+typedef void *dt_stream_t; /* hipStream_t */
+
+const char *dt_last_error(void);
+const char *dt_version(void);
+
+/* ======================================================================== */
+/* (ii) fused entry points                                                  */
+/* ======================================================================== */
+
+/* adaLN: y = (1 + scale) * LayerNorm_eps(x) + shift, per row of `cols`.
+ * Replaces the NORM -> ADD(scale,1) -> MUL -> ADD node chain emitted by
+ * LayerNorm::forward (src/nn/modules/normalization/LayerNorm.cpp:16-32,
+ * Runtime::norm at src/ggml/Runtime.hpp:273-275) followed by the modulation
+ * in Flux2SingleTransformerBlock.hpp:50-54, Flux2TransformerBlock.hpp:63-72,
+ * 91-92, 105-106 and AdaLayerNormContinuous.inl:38-40.
+ * shift/scale: fp32 [cols] (the chunk views of the Flux2Modulation output). */
+int dt_adaln_mod(const void *x, int64_t rows, int64_t cols, int64_t x_stride,
+                 const float *shift, const float *scale,
+                 void *y, int64_t y_stride, float eps, int32_t io_type,
+                 dt_stream_t stream);
+
+/* QK-RMSNorm + multi-axis RoPE for q and k in one launch:
+ *   z = RMSNorm_eps(x[t,h,:]) * w ;  y[t,h,:] = cat_a RoPE_NORMAL(z[a-th section], pos[t,a])
+ * Replaces RMSNorm::forward (src/nn/modules/normalization/RMSNorm.cpp:12-22,
+ * Runtime::rms_norm at src/ggml/Runtime.hpp:277-279) on the unflattened q/k
+ * (Flux2Attention.hpp:93-112, Flux2ParallelSelfAttention.hpp:181-189) and
+ * Flux2PosEmbed::forward (Flux2PosEmbed.hpp:18-109: four Runtime::rope_ext,
+ * src/ggml/Runtime.hpp:281-293, mode NORMAL, plus Tensor::cat).
+ * Layout: element (t, h, d) of q/k at t*tok_stride + h*head_stride + d.
+ * q or k may be NULL (that half is skipped); q_out may alias q.
+ * pos: int32, position of token t on axis a at pos[t*pos_stride + a].
+ * n_axes * axis_dim must equal head_dim.  rope_table: fp32
+ * [n_pos][axis_dim] holding (cos, sin) pairs as filled by
+ * dt_rope_table_fill for the same axis_dim/freq_base (NULL or n_pos = 0:
+ * angles are computed on the device); positions outside [0, n_pos) are
+ * computed on the device. */
+int dt_qk_rmsnorm_rope(const void *q, const void *k, void *q_out, void *k_out,
+                       int64_t tokens, int64_t heads, int64_t head_dim,
+                       int64_t in_tok_stride, int64_t in_head_stride,
+                       int64_t out_tok_stride, int64_t out_head_stride,
+                       const float *wq, const float *wk, float eps,
+                       const int32_t *pos, int64_t pos_stride,
+                       int32_t n_axes, int32_t axis_dim, float freq_base,
+                       const float *rope_table, int32_t n_pos,
+                       int32_t io_type, dt_stream_t stream);
+
+/* Host-side: fill table[p*n_dims + 2i] = cos(theta_i(p)) * attn_factor and
+ * table[p*n_dims + 2i + 1] = sin(...) for p < n_pos, i < n_dims/2, with
+ * ggml's fp32 angle recurrence theta_0 = p*freq_scale,
+ * theta_{i+1} = theta_i * powf(freq_base, -2/n_dims) (the rope cache of
+ * ggml_rope_ext with ext_factor 0).  `table` is HOST memory of
+ * n_pos*n_dims floats; upload it once per model. */
+int dt_rope_table_fill(float *table, int32_t n_pos, int32_t n_dims,
+                       float freq_base, float freq_scale, float attn_factor);
+
+/* SwiGLU: y = silu(gate) * up = (gate * sigmoid(gate)) * up.
+ * Replaces SIGMOID -> MUL -> MUL of Flux2SwiGLU::forward
+ * (Flux2SwiGLU.hpp:17-21, SiLU.hpp:9-13; Runtime::sigmoid/mul at
+ * src/ggml/Runtime.hpp:89-91, 107-110). Rows of `inner` elements. */
+int dt_swiglu(const void *gate, int64_t gate_stride, const void *up, int64_t up_stride,
+              void *y, int64_t y_stride, int64_t rows, int64_t inner,
+              int32_t io_type, dt_stream_t stream);
+
+/* Gated residual: y = h + gate * o, gate fp32 [cols] broadcast over rows.
+ * Replaces MUL -> ADD of Flux2SingleTransformerBlock.hpp:58 and
+ * Flux2TransformerBlock.hpp:86-87, 97, 100-101, 111.  y may alias h. */
+int dt_gated_residual(const void *h, int64_t h_stride, const void *o, int64_t o_stride,
+                      const float *gate, void *y, int64_t y_stride,
+                      int64_t rows, int64_t cols, int32_t io_type, dt_stream_t stream);
+
+/* Weight dequantisation to dst_type (DT_TYPE_BF16 or DT_TYPE_F32).
+ * qtype DT_TYPE_Q8_0 (cols % 32 == 0) or DT_TYPE_Q4_K (cols % 256 == 0);
+ * ggml blocks run along cols (ne0); row r starts at src + r*row_bytes.
+ * fp32 value = d*q (Q8_0) or (d*sc)*q - (dmin*m) (Q4_K), each operation
+ * rounded; bf16 output is the RNE rounding of that value.  Stands in for the
+ * implicit dequantisation inside Runtime::mul_mat (src/ggml/Runtime.hpp:136-139)
+ * of Linear::forward (src/nn/Linear.cpp:17-36) on Q8_0/Q4_K GGUF weights. */
+int dt_dequant(const void *src, int32_t qtype, int64_t rows, int64_t cols,
+               int64_t row_bytes, void *dst, int64_t dst_stride, int32_t dst_type,
+               dt_stream_t stream);
+
+/* GroupNorm(groups, eps) over x[N][C][HW] (NCHW, contiguous), optional
+ * per-channel affine (w, b may be NULL), then SiLU when apply_silu.
+ * Replaces GroupNorm::forward (src/nn/modules/normalization/GroupNorm.cpp:79-161:
+ * reshape -> NORM -> reshape -> MUL -> ADD) and SiLU::forward
+ * (SiLU.hpp:9-13) as used in ResnetBlock2D.inl:111-122, 160-171 and
+ * Decoder.hpp:147-160.  `workspace` is caller-owned device memory of at
+ * least dt_groupnorm_workspace_bytes(...) bytes.  y may alias x. */
+size_t dt_groupnorm_workspace_bytes(int64_t N, int64_t C, int64_t HW, int64_t groups);
+int dt_groupnorm_silu(const void *x, int64_t N, int64_t C, int64_t HW, int64_t groups,
+                      const float *w, const float *b, float eps, int32_t apply_silu,
+                      void *y, void *workspace, size_t workspace_bytes,
+                      int32_t io_type, dt_stream_t stream);
+
+/* Euler step of FlowMatchEulerDiscreteScheduler::integrate
+ * (src/diffusers/schedulers/FlowMatchEulerDiscreteScheduler.cpp:210-222):
+ * y = x + dt * v over n contiguous elements. */
+int dt_euler_step(const void *x, const void *v, float dt, void *y, int64_t n,
+                  int32_t io_type, dt_stream_t stream);
+
+/* ======================================================================== */
+/* (iii) unfused ggml-op kernels on ggml-shaped descriptors                 */
+/* ======================================================================== */
+
+/* A ggml_tensor-shaped descriptor: ne[] ggml order (ne[0] fastest),
+ * nb[] byte strides, device data.  op/op_params/src describe graph nodes
+ * for dt_graph_compute; single-op kernels read only type/ne/nb/data. */
+typedef struct dt_tensor {
+    int32_t type;
+    int32_t op;
+    int64_t ne[4];
+    int64_t nb[4];
+    void *data;
+    int32_t op_params[16];
+    struct dt_tensor *src[4];
+    int32_t flags;
+    int32_t id;
+} dt_tensor;
+
+/* Binary ops with ggml broadcast (src1 repeats into src0's shape, dst has
+ * src0's shape): Runtime::add/sub/mul/div (src/ggml/Runtime.hpp:97-115). */
+enum { DT_BIN_ADD = 0, DT_BIN_SUB = 1, DT_BIN_MUL = 2, DT_BIN_DIV = 3 };
+int dt_op_binary(int32_t op, const dt_tensor *src0, const dt_tensor *src1,
+                 const dt_tensor *dst, dt_stream_t stream);
+
+/* Unary ops: Runtime::sigmoid/exp/log/sqrt/sin/cos (Runtime.hpp:69-91),
+ * scale (:121-124, p0 = factor), clamp (:126-130, p0 = min, p1 = max),
+ * SILU (x * sigmoid(x), the SiLU module's composite). */
+enum {
+    DT_UN_SIGMOID = 0, DT_UN_EXP = 1, DT_UN_LOG = 2, DT_UN_SQRT = 3,
+    DT_UN_SIN = 4, DT_UN_COS = 5, DT_UN_SCALE = 6, DT_UN_CLAMP = 7,
+    DT_UN_SILU = 8, DT_UN_FILL = 9
+};
+int dt_op_unary(int32_t op, const dt_tensor *src, const dt_tensor *dst,
+                float p0, float p1, dt_stream_t stream);
+
+/* Row norms over ne[0]: Runtime::norm / rms_norm (Runtime.hpp:273-279). */
+int dt_op_norm(const dt_tensor *src, const dt_tensor *dst, float eps, dt_stream_t stream);
+int dt_op_rms_norm(const dt_tensor *src, const dt_tensor *dst, float eps, dt_stream_t stream);
+
+/* Runtime::rope_ext (Runtime.hpp:281-293), mode 0 (NORMAL) only, no
+ * frequency factors, ext_factor 0.  pos: int32 [src->ne[2]] device. */
+int dt_op_rope_ext(const dt_tensor *src, const int32_t *pos, const dt_tensor *dst,
+                   int32_t n_dims, int32_t mode, float freq_base, float freq_scale,
+                   float ext_factor, float attn_factor, dt_stream_t stream);
+
+/* Runtime::concat (Runtime.hpp:236-240) along ggml dim `dim`; same-type
+ * operands of any 2/4-byte type (I32 included) are copied bit for bit. */
+int dt_op_concat(const dt_tensor *a, const dt_tensor *b, int32_t dim,
+                 const dt_tensor *dst, dt_stream_t stream);
+
+/* Runtime::cont / cpy / cast (Runtime.hpp:47-63): strided copy with
+ * conversion between F32, F16 and BF16 (same element count); same-type
+ * copies (I32 included) move the bits unchanged. */
+int dt_op_cpy(const dt_tensor *src, const dt_tensor *dst, dt_stream_t stream);
+
+/* ======================================================================== */
+/* (i) device, buffers and graph execution                                  */
+/* ======================================================================== */
+
+typedef struct dt_backend dt_backend;
+
+/* Device / Backend / Buffer RAII stand-ins (src/ggml/Device.hpp:8-27,
+ * Backend.hpp:5-31, Buffer.hpp:8-42). */
+int dt_backend_init(int32_t device_ordinal, dt_backend **out);
+int dt_backend_free(dt_backend *be);
+int dt_backend_set_stream(dt_backend *be, dt_stream_t stream);
+int dt_backend_synchronize(dt_backend *be);
+int dt_buffer_alloc(dt_backend *be, size_t bytes, void **out);
+int dt_buffer_free(dt_backend *be, void *ptr);
+int dt_tensor_set(const dt_tensor *t, const void *host, size_t offset, size_t n, dt_stream_t stream);
+int dt_tensor_get(const dt_tensor *t, void *host, size_t offset, size_t n, dt_stream_t stream);
+
+/* Graph op ids for dt_tensor.op (the subset of ggml_op the Flux2 chain
+ * emits; numbering is this library's own). */
+enum {
+    DT_OP_NONE = 0,      /* leaf: data already set */
+    DT_OP_ADD, DT_OP_SUB, DT_OP_MUL, DT_OP_DIV,
+    DT_OP_SCALE,         /* op_params[0] = float bits */
+    DT_OP_SIGMOID, DT_OP_NORM, DT_OP_RMS_NORM, /* norms: op_params[0] = eps bits */
+    DT_OP_ROPE,          /* src[1] = pos (I32); op_params: n_dims, mode, base bits, scale bits */
+    DT_OP_CONCAT,        /* op_params[0] = dim */
+    DT_OP_CPY,           /* cont / cast into dst layout */
+    DT_OP_VIEW,          /* no-op: data aliases src[0] with own ne/nb */
+    DT_OP_FILL,          /* op_params[0] = value bits */
+    DT_OP_COUNT
+};
+
+/* Execute nodes in order.  Before dispatch a fusion pass rewrites the
+ * chains listed for the fused entry points above into single kernels when
+ * the intermediate nodes are not flagged DT_FLAG_OUTPUT; every other node
+ * runs its unfused kernel.  Intermediate node data must be allocated by
+ * the caller (ggml_gallocr's role in the reference). */
+enum { DT_FLAG_OUTPUT = 1 };
+int dt_graph_compute(dt_backend *be, dt_tensor **nodes, int32_t n_nodes);
+/* Statistics of the last dt_graph_compute on this thread: kernels launched
+ * and nodes absorbed into fused kernels. */
+int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DIT_HIP_H */

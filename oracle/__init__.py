@@ -1,0 +1,298 @@
+"""numpy-facing wrapper of the oracle (liboracle.so, a C restatement of the
+ggml CPU arithmetic the diffusers-cpp Flux2 modules emit).
+
+Test infrastructure only: the tests, the smoke check and the CPU-baseline
+leg of the benchmark may use it, as the checker (or as the timed CPU
+baseline).  The product library never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from ctypes import POINTER, c_float, c_int, c_int32, c_int64, c_uint16, c_uint64, c_void_p
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+_lib = None
+
+
+def build():
+    subprocess.check_call(["make", "-s", "-C", _HERE])
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = ctypes.CDLL(LIB_PATH)
+    P = c_void_p
+    sigs = {
+        "or_mt64_nth": (c_uint64, [c_uint64, c_uint64]),
+        "or_randn_f32": (None, [c_uint64, c_int64, c_float, c_float, P]),
+        "or_rand_int32": (None, [c_uint64, c_int64, c_int32, c_int32, P]),
+        "or_f16_to_f32": (c_float, [c_uint16]),
+        "or_f32_to_f16": (c_uint16, [c_float]),
+        "or_bf16_to_f32": (c_float, [c_uint16]),
+        "or_f32_to_bf16": (c_uint16, [c_float]),
+        "or_f32_to_bf16_n": (None, [P, c_int64, P]),
+        "or_bf16_to_f32_n": (None, [P, c_int64, P]),
+        "or_round_bf16_n": (None, [P, c_int64, P]),
+        "or_norm_f32": (None, [P, c_int64, c_int64, c_float, P, c_int]),
+        "or_rms_norm_f32": (None, [P, c_int64, c_int64, c_float, P, c_int]),
+        "or_sigmoid_f32": (None, [P, c_int64, P]),
+        "or_scale_f32": (None, [P, c_int64, c_float, P]),
+        "or_binary_f32": (None, [c_int, P, P, P, P, P, P, P]),
+        "or_concat_f32": (None, [P, P, P, P, c_int, P]),
+        "or_rope_cache": (None, [c_float, c_int, c_int64, c_float, c_float, c_float, P]),
+        "or_rope_normal_f32": (None, [P, P, P, P, c_int, c_float, c_float, c_float, P]),
+        "or_adaln_f32": (None, [P, c_int64, c_int64, P, P, c_float, P, c_int]),
+        "or_qk_rmsnorm_rope_f32": (None, [P, c_int64, c_int64, c_int64, P, c_float, P, c_int64,
+                                          c_int, c_int, c_float, P, c_int]),
+        "or_swiglu_f32": (None, [P, c_int64, P, c_int64, c_int64, c_int64, P, c_int]),
+        "or_gated_residual_f32": (None, [P, P, P, c_int64, c_int64, P, c_int]),
+        "or_groupnorm_silu_f32": (None, [P, c_int64, c_int64, c_int64, c_int64, P, P, c_float,
+                                         c_int, P, c_int]),
+        "or_euler_f32": (None, [P, P, c_float, c_int64, P]),
+        "or_quantize_q8_0": (None, [P, c_int64, P]),
+        "or_dequant_q8_0_f32": (None, [P, c_int64, P]),
+        "or_quantize_q4_K": (None, [P, c_int64, P]),
+        "or_dequant_q4_K_f32": (None, [P, c_int64, P]),
+        "or_q4_K_scale_min": (None, [c_int, P, P, P]),
+        "or_max_threads": (c_int, []),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return c_void_p(a.ctypes.data)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- generator / formats ---------------------------------------------------
+
+def mt64_nth(seed: int, n: int) -> int:
+    return int(load().or_mt64_nth(seed, n))
+
+
+def randn(seed: int, shape, mean=0.0, std=1.0) -> np.ndarray:
+    out = np.empty(int(np.prod(shape)), dtype=np.float32)
+    load().or_randn_f32(seed, out.size, mean, std, _p(out))
+    return out.reshape(shape)
+
+
+def randint(seed: int, shape, lo: int, hi: int) -> np.ndarray:
+    out = np.empty(int(np.prod(shape)), dtype=np.int32)
+    load().or_rand_int32(seed, out.size, lo, hi, _p(out))
+    return out.reshape(shape)
+
+
+def tensor_seed(index: int) -> int:
+    """Seed of the index-th generated tensor of a workload."""
+    return 0x5EED0000 + index
+
+
+def to_bf16_bits(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(x.shape, dtype=np.uint16)
+    load().or_f32_to_bf16_n(_p(x), x.size, _p(out))
+    return out
+
+
+def from_bf16_bits(b) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    load().or_bf16_to_f32_n(_p(b), b.size, _p(out))
+    return out
+
+
+def round_bf16(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    load().or_round_bf16_n(_p(x), x.size, _p(out))
+    return out
+
+
+def f16_to_f32(h: int) -> float:
+    return float(load().or_f16_to_f32(h))
+
+
+def f32_to_f16(f: float) -> int:
+    return int(load().or_f32_to_f16(f))
+
+
+# ---- single ops ------------------------------------------------------------
+
+def norm(x, eps, threads=0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    load().or_norm_f32(_p(x), x.size // x.shape[-1], x.shape[-1], eps, _p(y), threads)
+    return y
+
+
+def rms_norm(x, eps, threads=0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    load().or_rms_norm_f32(_p(x), x.size // x.shape[-1], x.shape[-1], eps, _p(y), threads)
+    return y
+
+
+def sigmoid(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    load().or_sigmoid_f32(_p(x), x.size, _p(y))
+    return y
+
+
+def _ggml_ne_nb(a: np.ndarray):
+    """ggml ne/nb (int64[4]) of an ndarray of <= 4 dims (strides honoured)."""
+    ne = list(a.shape)[::-1] + [1] * (4 - a.ndim)
+    nb = [s for s in a.strides[::-1]]
+    while len(nb) < 4:
+        nb.append(nb[-1] * ne[len(nb) - 1] if nb else a.itemsize)
+    return np.array(ne, dtype=np.int64), np.array(nb, dtype=np.int64)
+
+
+def binary(op: int, a, b):
+    """ggml binary op (0 add, 1 sub, 2 mul, 3 div): b repeats into a's shape."""
+    a = np.asarray(a, dtype=np.float32)
+    b = np.asarray(b, dtype=np.float32)
+    nea, nba = _ggml_ne_nb(a)
+    neb, nbb = _ggml_ne_nb(b)
+    out = np.empty(a.shape, dtype=np.float32)
+    load().or_binary_f32(op, c_void_p(a.ctypes.data), _p(nea), _p(nba), c_void_p(b.ctypes.data),
+                         _p(neb), _p(nbb), _p(out))
+    return out
+
+
+def concat(a, b, dim_ggml: int):
+    a, b = _f32(a), _f32(b)
+    nea, _ = _ggml_ne_nb(a)
+    neb, _ = _ggml_ne_nb(b)
+    axis = a.ndim - 1 - dim_ggml
+    out = np.empty(np.concatenate([a, b], axis=axis).shape, dtype=np.float32)
+    load().or_concat_f32(_p(a), _p(nea), _p(b), _p(neb), dim_ggml, _p(out))
+    return out
+
+
+def rope_cache(p: float, n_dims: int, ne0: int, freq_base: float, freq_scale=1.0, attn_factor=1.0):
+    out = np.empty(ne0, dtype=np.float32)
+    load().or_rope_cache(p, n_dims, ne0, freq_base, freq_scale, attn_factor, _p(out))
+    return out
+
+
+def rope_normal(x, pos, n_dims, freq_base, freq_scale=1.0, attn_factor=1.0):
+    """x: ndarray [B, S, H, D] (any strides, PyTorch order); pos: int32 [S]."""
+    x = np.asarray(x, dtype=np.float32)
+    while x.ndim < 4:
+        x = x[None]
+    ne, nb = _ggml_ne_nb(x)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    out = np.empty(x.shape, dtype=np.float32)
+    load().or_rope_normal_f32(c_void_p(x.ctypes.data), _p(ne), _p(nb), _p(pos), n_dims, freq_base,
+                              freq_scale, attn_factor, _p(out))
+    return out
+
+
+# ---- chains ----------------------------------------------------------------
+
+def adaln(x, shift, scale, eps=1e-6, threads=0):
+    x = _f32(x)
+    y = np.empty_like(x)
+    cols = x.shape[-1]
+    load().or_adaln_f32(_p(x), x.size // cols, cols, _p(_f32(shift)), _p(_f32(scale)), eps, _p(y),
+                        threads)
+    return y
+
+
+def qk_rmsnorm_rope(x, w, pos, axis_dim, freq_base, eps=1e-6, threads=0):
+    """x: [tokens, heads, head_dim]; pos: int32 [tokens, n_axes]."""
+    x = _f32(x)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    tokens, heads, head_dim = x.shape
+    y = np.empty_like(x)
+    load().or_qk_rmsnorm_rope_f32(_p(x), tokens, heads, head_dim, _p(_f32(w)), eps, _p(pos),
+                                  pos.shape[1], pos.shape[1], axis_dim, freq_base, _p(y), threads)
+    return y
+
+
+def swiglu(g, u, threads=0):
+    g, u = _f32(g), _f32(u)
+    cols = g.shape[-1]
+    y = np.empty_like(g)
+    load().or_swiglu_f32(_p(g), cols, _p(u), cols, g.size // cols, cols, _p(y), threads)
+    return y
+
+
+def gated_residual(h, o, gate, threads=0):
+    h, o = _f32(h), _f32(o)
+    cols = h.shape[-1]
+    y = np.empty_like(h)
+    load().or_gated_residual_f32(_p(h), _p(o), _p(_f32(gate)), h.size // cols, cols, _p(y), threads)
+    return y
+
+
+def groupnorm_silu(x, groups, w=None, b=None, eps=1e-6, silu=True, threads=0):
+    x = _f32(x)
+    N, C = x.shape[0], x.shape[1]
+    HW = x.size // (N * C)
+    y = np.empty_like(x)
+    wp = _p(_f32(w)) if w is not None else None
+    bp = _p(_f32(b)) if b is not None else None
+    load().or_groupnorm_silu_f32(_p(x), N, C, HW, groups, wp, bp, eps, 1 if silu else 0, _p(y),
+                                 threads)
+    return y
+
+
+def euler(x, v, dt):
+    x, v = _f32(x), _f32(v)
+    y = np.empty_like(x)
+    load().or_euler_f32(_p(x), _p(v), dt, x.size, _p(y))
+    return y
+
+
+# ---- quantisation ------------------------------------------------------------
+
+def quantize(x, qtype: int) -> np.ndarray:
+    """Row-major float32 matrix -> ggml block bytes (qtype 8 = Q8_0, 12 = Q4_K)."""
+    x = _f32(x)
+    qk, bs = (32, 34) if qtype == 8 else (256, 144)
+    assert x.shape[-1] % qk == 0
+    out = np.empty(x.size // qk * bs, dtype=np.uint8)
+    fn = load().or_quantize_q8_0 if qtype == 8 else load().or_quantize_q4_K
+    fn(_p(x), x.size, _p(out))
+    return out
+
+
+def dequantize(b, n: int, qtype: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    fn = load().or_dequant_q8_0_f32 if qtype == 8 else load().or_dequant_q4_K_f32
+    fn(_p(b), n, _p(out))
+    return out
+
+
+def q4_K_scale_min(j: int, scales12) -> tuple[int, int]:
+    s = np.ascontiguousarray(scales12, dtype=np.uint8)
+    sc = np.zeros(1, dtype=np.uint8)
+    m = np.zeros(1, dtype=np.uint8)
+    load().or_q4_K_scale_min(j, _p(s), _p(sc), _p(m))
+    return int(sc[0]), int(m[0])
+
+
+def max_threads() -> int:
+    return int(load().or_max_threads())

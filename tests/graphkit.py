@@ -1,0 +1,154 @@
+"""Test-side graph builder: emits dt_tensor nodes the way the reference's
+Runtime calls emit ggml nodes (src/ggml/Runtime.hpp), with every node's
+data allocated up front as a torch tensor (gallocr's role in the
+reference), then runs them through dt_graph_compute.
+
+Shapes are given in ggml order (ne[0] fastest) to keep the node structure
+one-to-one with the reference's graphs."""
+import ctypes
+import struct
+
+import torch
+
+import dit_hip as dh
+
+_TORCH = {dh.F32: torch.float32, dh.BF16: torch.bfloat16, dh.F16: torch.float16, dh.I32: torch.int32}
+_ES = {dh.F32: 4, dh.BF16: 2, dh.F16: 2, dh.I32: 4}
+
+
+def fbits(v: float) -> int:
+    return struct.unpack("<i", struct.pack("<f", v))[0]
+
+
+class Node:
+    def __init__(self, d: dh.DtTensor, data=None):
+        self.d = d
+        self.data = data          # torch tensor owning the memory (None for views)
+
+    @property
+    def ne(self):
+        return list(self.d.ne)
+
+    def torch(self):
+        """Contiguous node data as a torch tensor of PyTorch shape."""
+        return self.data
+
+
+class Graph:
+    def __init__(self, device="cuda"):
+        self.nodes = []
+        self.keep = []
+        self.device = device
+
+    # ---- tensors ----------------------------------------------------------
+    def leaf(self, t: torch.Tensor) -> Node:
+        t = t.contiguous() if t.dim() <= 4 else t
+        self.keep.append(t)
+        return Node(dh.desc(t), t)
+
+    def _new(self, op, ne, type_, srcs, params=()):
+        ne = list(ne) + [1] * (4 - len(ne))
+        shape = [n for n in reversed(ne)]
+        data = torch.empty(shape, dtype=_TORCH[type_], device=self.device)
+        d = dh.desc(data, op)
+        for i, s in enumerate(srcs):
+            d.src[i] = ctypes.pointer(s.d) if s is not None else None
+        for i, p in enumerate(params):
+            d.op_params[i] = p
+        n = Node(d, data)
+        self.nodes.append(n)
+        return n
+
+    def view(self, src: Node, ne, nb, offset_bytes=0) -> Node:
+        d = dh.DtTensor()
+        d.type = src.d.type
+        d.op = dh.OP_VIEW
+        ne = list(ne) + [1] * (4 - len(ne))
+        for i in range(4):
+            d.ne[i] = ne[i]
+        nb = list(nb)
+        while len(nb) < 4:
+            nb.append(nb[-1] * ne[len(nb) - 1])
+        for i in range(4):
+            d.nb[i] = nb[i]
+        d.data = src.d.data + offset_bytes
+        d.src[0] = ctypes.pointer(src.d)
+        n = Node(d)
+        self.nodes.append(n)
+        return n
+
+    def reshape(self, src: Node, ne) -> Node:
+        es = _ES[src.d.type]
+        ne = list(ne) + [1] * (4 - len(ne))
+        nb = [es]
+        for i in range(1, 4):
+            nb.append(nb[-1] * ne[i - 1])
+        return self.view(src, ne, nb, 0)
+
+    # ---- ops (Runtime method names) ----------------------------------------
+    def _binary(self, op, a, b):
+        return self._new(op, a.ne, a.d.type, [a, b])
+
+    def add(self, a, b):
+        return self._binary(dh.OP_ADD, a, b)
+
+    def sub(self, a, b):
+        return self._binary(dh.OP_SUB, a, b)
+
+    def mul(self, a, b):
+        return self._binary(dh.OP_MUL, a, b)
+
+    def div(self, a, b):
+        return self._binary(dh.OP_DIV, a, b)
+
+    def scale(self, a, s):
+        return self._new(dh.OP_SCALE, a.ne, a.d.type, [a], [fbits(s)])
+
+    def sigmoid(self, a):
+        return self._new(dh.OP_SIGMOID, a.ne, a.d.type, [a])
+
+    def fill(self, ne, type_, value):
+        return self._new(dh.OP_FILL, ne, type_, [], [fbits(value)])
+
+    def norm(self, a, eps):
+        return self._new(dh.OP_NORM, a.ne, a.d.type, [a], [fbits(eps)])
+
+    def rms_norm(self, a, eps):
+        return self._new(dh.OP_RMS_NORM, a.ne, a.d.type, [a], [fbits(eps)])
+
+    def rope_ext(self, a, pos, n_dims, mode, freq_base, freq_scale=1.0, ext_factor=0.0,
+                 attn_factor=1.0):
+        return self._new(dh.OP_ROPE, a.ne, a.d.type, [a, pos],
+                         [n_dims, mode, fbits(freq_base), fbits(freq_scale), fbits(ext_factor),
+                          fbits(attn_factor)])
+
+    def concat(self, a, b, dim):
+        ne = a.ne
+        ne[dim] += b.ne[dim]
+        return self._new(dh.OP_CONCAT, ne, a.d.type, [a, b], [dim])
+
+    def cont(self, a, type_=None):
+        return self._new(dh.OP_CPY, a.ne, type_ if type_ is not None else a.d.type, [a])
+
+    # ---- execution ---------------------------------------------------------
+    def compute(self, backend, outputs=()):
+        for o in outputs:
+            o.d.flags |= dh.FLAG_OUTPUT
+        arr = (ctypes.POINTER(dh.DtTensor) * len(self.nodes))(*[ctypes.pointer(n.d) for n in self.nodes])
+        dh.check(dh.load().dt_graph_compute(backend, arr, len(self.nodes)), "dt_graph_compute")
+        k = ctypes.c_int32()
+        f = ctypes.c_int32()
+        dh.load().dt_graph_last_stats(ctypes.byref(k), ctypes.byref(f))
+        return k.value, f.value
+
+
+class Backend:
+    def __init__(self):
+        self.h = ctypes.c_void_p()
+        dh.check(dh.load().dt_backend_init(0, ctypes.byref(self.h)), "dt_backend_init")
+        dh.check(dh.load().dt_backend_set_stream(self.h, dh.stream()), "dt_backend_set_stream")
+
+    def close(self):
+        if self.h:
+            dh.load().dt_backend_free(self.h)
+            self.h = ctypes.c_void_p()

@@ -1,0 +1,146 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function
+include/dit_hip.h declares, its descriptor layout matches the C compiler's,
+argument validation rejects bad calls before touching a device, and the
+host-side helpers (RoPE table, workspace sizing, invariant division) are
+right.  No kernel is launched here."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import dit_hip
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "dit_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = dit_hip.load()
+    names = declared_functions()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+    # and the Python binding declares a signature for each of them
+    assert sorted(dit_hip.exported_symbols()) == names
+
+
+def test_descriptor_layout_matches_c():
+    src = r"""
+    #include <stddef.h>
+    #include <stdio.h>
+    #include "dit_hip.h"
+    int main(void) {
+        printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu\n", sizeof(dt_tensor),
+               offsetof(dt_tensor, type), offsetof(dt_tensor, op), offsetof(dt_tensor, ne),
+               offsetof(dt_tensor, nb), offsetof(dt_tensor, data), offsetof(dt_tensor, op_params),
+               offsetof(dt_tensor, src), offsetof(dt_tensor, flags));
+        return 0;
+    }
+    """
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "l.c")
+        open(c, "w").write(src)
+        exe = os.path.join(d, "l")
+        subprocess.check_call(["gcc", "-I", os.path.dirname(HEADER), c, "-o", exe])
+        got = [int(v) for v in subprocess.check_output([exe]).split()]
+    T = dit_hip.DtTensor
+    want = [ctypes.sizeof(T), T.type.offset, T.op.offset, T.ne.offset, T.nb.offset, T.data.offset,
+            T.op_params.offset, T.src.offset, T.flags.offset]
+    assert got == want
+
+
+def test_type_ids_match_ggml():
+    text = open(HEADER).read()
+    for name, val in (("F32", 0), ("F16", 1), ("Q8_0", 8), ("Q4_K", 12), ("I32", 26), ("BF16", 30)):
+        assert re.search(rf"DT_TYPE_{name}\s*=\s*{val}\b", text)
+        assert getattr(dit_hip, name) == val
+
+
+def _err(rc):
+    assert rc != 0
+    return dit_hip.load().dt_last_error().decode()
+
+
+def test_validation_rejects_before_launch():
+    lib = dit_hip.load()
+    P = ctypes.c_void_p
+    dummy = P(16)
+    # unsupported io type
+    msg = _err(lib.dt_adaln_mod(dummy, 4, 64, 64, dummy, dummy, dummy, 64, 1e-6, 99, None))
+    assert "io_type" in msg
+    # stride smaller than cols
+    assert "stride" in _err(lib.dt_adaln_mod(dummy, 4, 64, 32, dummy, dummy, dummy, 64, 1e-6, 30, None))
+    # head_dim != n_axes * axis_dim
+    msg = _err(lib.dt_qk_rmsnorm_rope(dummy, None, dummy, None, 4, 2, 128, 256, 128, 256, 128,
+                                      dummy, None, 1e-6, dummy, 4, 4, 16, 1e4, None, 0, 30, None))
+    assert "head_dim" in msg
+    # Q4_K needs cols % 256 == 0; Q8_0 row_bytes too small
+    assert "multiple" in _err(lib.dt_dequant(dummy, 12, 2, 100, 1000, dummy, 100, 30, None))
+    assert "row_bytes" in _err(lib.dt_dequant(dummy, 8, 2, 64, 10, dummy, 64, 30, None))
+    # unsupported quant type / dst type
+    assert "qtype" in _err(lib.dt_dequant(dummy, 2, 2, 64, 68, dummy, 64, 30, None))
+    assert "dst_type" in _err(lib.dt_dequant(dummy, 8, 2, 64, 68, dummy, 64, 1, None))
+    # group norm: groups must divide C, workspace must be big enough
+    assert "bad shape" in _err(lib.dt_groupnorm_silu(dummy, 1, 30, 16, 32, None, None, 1e-6, 1, dummy,
+                                                     dummy, 1 << 20, 30, None))
+    assert "workspace" in _err(lib.dt_groupnorm_silu(dummy, 1, 64, 16, 32, None, None, 1e-6, 1, dummy,
+                                                     dummy, 8, 30, None))
+    # rope_ext: only NORMAL mode
+    d = dit_hip.DtTensor()
+    d.type, d.data = dit_hip.F32, 16
+    for i in range(4):
+        d.ne[i], d.nb[i] = (8 if i == 0 else 1), (4 if i == 0 else 32)
+    assert "mode" in _err(lib.dt_op_rope_ext(ctypes.byref(d), dummy, ctypes.byref(d), 8, 2, 1e4, 1.0,
+                                             0.0, 1.0, None))
+    # binary: src1 must broadcast into src0
+    e = dit_hip.DtTensor()
+    e.type, e.data = dit_hip.F32, 16
+    for i in range(4):
+        e.ne[i], e.nb[i] = (3 if i == 0 else 1), (4 if i == 0 else 12)
+    assert "broadcast" in _err(lib.dt_op_binary(0, ctypes.byref(d), ctypes.byref(e), ctypes.byref(d), None))
+    # zero rows is a no-op success
+    assert lib.dt_adaln_mod(None, 0, 64, 64, None, None, None, 64, 1e-6, 30, None) == 0
+
+
+def test_rope_table_matches_oracle_cache(orc):
+    tab = dit_hip.rope_table(512, 32, 10000.0, device="cpu").numpy()
+    for p in (0, 1, 2, 63, 64, 300, 511):
+        want = orc.rope_cache(float(p), 32, 32, 10000.0)
+        assert np.array_equal(tab[p], want), p
+    tab2 = dit_hip.rope_table(8, 2, 2000.0, device="cpu").numpy()
+    for p in range(8):
+        assert np.array_equal(tab2[p], orc.rope_cache(float(p), 2, 2, 2000.0))
+
+
+def test_groupnorm_workspace_bytes():
+    lib = dit_hip.load()
+    # one (K, sum, sumsq per chunk) record per (n, g), chunks of 2048 elements
+    assert lib.dt_groupnorm_workspace_bytes(1, 128, 1024 * 1024, 32) == 32 * (2 * 2048 + 1) * 8
+    assert lib.dt_groupnorm_workspace_bytes(2, 4, 9, 2) == 2 * 2 * (2 * 1 + 1) * 8
+    assert lib.dt_groupnorm_workspace_bytes(1, 30, 16, 32) == 0
+
+
+def test_fastdiv_arithmetic():
+    # The kernels' row index: q = (umulhi(n, m) + n) >> s with host-made (m, s).
+    def make(d):
+        s = 0
+        while (1 << s) < d:
+            s += 1
+        return ((((1 << 32) * ((1 << s) - d)) // d) + 1) & 0xFFFFFFFF, s
+
+    rng = np.random.RandomState(0)
+    for d in list(range(1, 3000)) + [int(v) for v in rng.randint(1, 1 << 30, 500)]:
+        m, s = make(d)
+        ns = [0, 1, d - 1, d, d + 1, (1 << 31) - 1] + [int(v) for v in rng.randint(0, 1 << 31, 50)]
+        for n in ns:
+            assert (((n * m) >> 32) + n) >> s == n // d

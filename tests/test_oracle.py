@@ -1,0 +1,251 @@
+"""Pins the oracle (CPU restatement of the ggml ops) before anything is
+checked against it: known-answer vectors, the golden fixtures written by
+tests/golden/make_golden.py from library routines and byte-level format
+packers, closed forms, invariants and brute force on tiny inputs.  Each
+check is chosen so that a plausible restatement mistake (dropped term, wrong
+sign, wrong index, transposed operand) fails it."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_fp32
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def fx():
+    with np.load(os.path.join(GOLD, "chain_golden.npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture(scope="module")
+def qkat():
+    with open(os.path.join(GOLD, "quant_kat.json")) as f:
+        return json.load(f)
+
+
+# ---- generator ------------------------------------------------------------
+
+def test_mt19937_64_known_answer(orc):
+    # The C++ standard fixes the 10000th output of a default-seeded mt19937_64.
+    assert orc.mt64_nth(5489, 10000) == 9981545732273789042
+
+
+def test_randn_is_standard_normal(orc):
+    from scipy import stats
+    x = orc.randn(orc.tensor_seed(0), (200_000,)).astype(np.float64)
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    assert stats.kstest(x, "norm").pvalue > 1e-3
+    y = orc.randn(orc.tensor_seed(1), (1000,), mean=1.0, std=0.02).astype(np.float64)
+    assert abs(y.mean() - 1.0) < 0.005 and abs(y.std() - 0.02) < 0.003
+    # Seeds are independent streams; the same seed is reproducible.
+    assert not np.array_equal(orc.randn(5, (8,)), orc.randn(6, (8,)))
+    assert np.array_equal(orc.randn(5, (9,)), orc.randn(5, (9,)))
+
+
+# ---- number formats -----------------------------------------------------------
+
+def test_f16_decode_exhaustive(orc):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([orc.f16_to_f32(int(b)) for b in bits], dtype=np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+
+
+def test_f16_encode_matches_numpy_rne(orc):
+    rng = np.random.RandomState(3)
+    vals = np.concatenate([
+        rng.randn(3000).astype(np.float32) * np.float32(100),
+        rng.randn(2000).astype(np.float32) * np.float32(1e-6),   # subnormal range
+        np.array([65504, 65519.99, 65520, 65536, 1e9, 2 ** -24, 2 ** -25, 3 * 2 ** -26,
+                  2 ** -25 * 1.0000001, 6.1e-5, -0.0, 0.0], dtype=np.float32),
+        # exact halfway points between neighbouring fp16 values
+        (np.arange(1, 4000, dtype=np.float32) * np.float32(2 ** -11) + np.float32(2 ** -12)),
+    ])
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([orc.f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_matches_torch_rne(orc, fx):
+    assert np.array_equal(orc.to_bf16_bits(fx["bf16_in"]), fx["bf16_bits"])
+    back = orc.from_bf16_bits(fx["bf16_bits"])
+    assert np.array_equal(back, torch.from_numpy(fx["bf16_bits"].view(np.int16)).view(
+        torch.bfloat16).float().numpy())
+
+
+# ---- norms / activations ------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["ln_small", "ln_3072"])
+def test_norm_and_adaln_vs_torch(orc, fx, name):
+    x = fx[name + "_x"]
+    assert_fp32(orc.norm(x, 1e-6), fx[name + "_norm"], what="norm")
+    assert_fp32(orc.adaln(x, fx[name + "_shift"], fx[name + "_scale"], 1e-6),
+                fx[name + "_adaln"], what="adaln")
+
+
+def test_norm_invariants(orc):
+    x = orc.randn(11, (7, 257)) * 3 + 5
+    y = orc.norm(x, 1e-6).astype(np.float64)
+    assert np.allclose(y.mean(-1), 0, atol=1e-5) and np.allclose(y.var(-1), 1, atol=1e-4)
+    # shift / scale invariance of the normalisation
+    assert_fp32(orc.norm(x * 4 - 3, 1e-6), orc.norm(x, 1e-6), tol=2e-5, what="equivariance")
+    # constant rows normalise to zero
+    assert np.all(orc.norm(np.full((2, 64), 3.25, np.float32), 1e-6) == 0)
+
+
+@pytest.mark.parametrize("name", ["rms_small", "rms_128"])
+def test_rms_norm_vs_torch(orc, fx, name):
+    x, w = fx[name + "_x"], fx[name + "_w"]
+    got = orc.binary(2, orc.rms_norm(x, 1e-6), w)
+    assert_fp32(got, fx[name + "_y"], what="rms_norm*w")
+
+
+def test_sigmoid_and_swiglu_vs_torch(orc, fx):
+    assert_fp32(orc.sigmoid(fx["act_g"]), fx["act_sigmoid"], what="sigmoid")
+    assert_fp32(orc.swiglu(fx["act_g"][None], fx["act_u"][None])[0], fx["act_swiglu"], what="swiglu")
+
+
+def test_gated_residual_and_euler_closed_form(orc):
+    h = orc.randn(1, (5, 48))
+    o = orc.randn(2, (5, 48))
+    g = orc.randn(3, (48,))
+    want = h.astype(np.float64) + o.astype(np.float64) * g.astype(np.float64)
+    assert_fp32(orc.gated_residual(h, o, g), want, what="gated")
+    assert_fp32(orc.euler(h, o, 0.125), h + o.astype(np.float64) * 0.125, what="euler")
+
+
+@pytest.mark.parametrize("name,G", [("gn_a", 2), ("gn_b", 4), ("gn_c", 32)])
+def test_groupnorm_silu_vs_torch(orc, fx, name, G):
+    x, w, b = fx[name + "_x"], fx[name + "_w"], fx[name + "_b"]
+    assert_fp32(orc.groupnorm_silu(x, G, w, b, 1e-6, silu=False), fx[name + "_gn"], what="gn")
+    assert_fp32(orc.groupnorm_silu(x, G, w, b, 1e-6, silu=True), fx[name + "_silu"], what="gn+silu")
+    # no affine == torch with unit weight / zero bias
+    ref = torch.nn.functional.group_norm(torch.from_numpy(x.astype(np.float64)), G, eps=1e-6)
+    assert_fp32(orc.groupnorm_silu(x, G, None, None, 1e-6, silu=False), ref.numpy(), what="gn noaff")
+
+
+# ---- broadcast / concat -------------------------------------------------------
+
+def test_binary_broadcast_is_modulo_repeat(orc):
+    a = orc.randn(4, (2, 3, 4, 6))
+    for bshape in [(6,), (1, 1, 1, 6), (1, 3, 1, 6), (2, 1, 4, 1), (1, 1, 2, 3), (2, 3, 4, 6)]:
+        b = orc.randn(5, bshape)
+        b4 = b.reshape((1,) * (4 - b.ndim) + b.shape)
+        reps = [a.shape[i] // b4.shape[i] for i in range(4)]
+        tiled = np.tile(b4, reps).astype(np.float64)
+        for op, f in ((0, np.add), (1, np.subtract), (2, np.multiply), (3, np.divide)):
+            assert_fp32(orc.binary(op, a, b), f(a.astype(np.float64), tiled), what=f"op{op} {bshape}")
+    # strided (transposed) src0 view
+    at = a.transpose(0, 1, 3, 2)
+    assert_fp32(orc.binary(0, at, np.float32(1.0) * np.ones(4, np.float32)), at + 1.0, what="strided")
+
+
+def test_concat_matches_numpy(orc):
+    a, b = orc.randn(6, (2, 3, 4)), orc.randn(7, (2, 3, 5))
+    assert np.array_equal(orc.concat(a, b, 0), np.concatenate([a, b], -1))
+    c = orc.randn(8, (2, 5, 4))
+    assert np.array_equal(orc.concat(a, c[:, :3] * 0 + c[:, 2:5], 1), np.concatenate([a, c[:, 2:5]], 1))
+
+
+# ---- RoPE -----------------------------------------------------------------------
+
+def test_rope_cache_recurrence(orc):
+    # theta_i = p * base^(-2i/d) up to the fp32 recurrence drift (<= 16 ulps of
+    # the angle at pair 15), and cos/sin of exactly that angle.
+    for p in (0, 1, 7, 63, 511):
+        c = orc.rope_cache(float(p), 32, 32, 10000.0).astype(np.float64)
+        th = p * 10000.0 ** (-np.arange(0, 32, 2) / 32.0)
+        assert np.allclose(c[0::2], np.cos(th), atol=4e-6 * max(p, 1) + 1e-7)
+        assert np.allclose(c[1::2], np.sin(th), atol=4e-6 * max(p, 1) + 1e-7)
+    # p = 0 is the identity rotation
+    c0 = orc.rope_cache(0.0, 32, 32, 10000.0)
+    assert np.all(c0[0::2] == 1) and np.all(c0[1::2] == 0)
+
+
+@pytest.mark.parametrize("case,axes,theta,tol", [("rope_toy", [2] * 4, 10000, 1e-5),
+                                                 ("rope_flux", [32] * 4, 2000, 1e-5),
+                                                 ("rope_far", [32] * 4, 10000, 2e-3)])
+def test_rope_vs_diffusers_complex_form(orc, fx, case, axes, theta, tol):
+    x, pos, want = fx[case + "_x"], fx[case + "_pos"], fx[case + "_y"]
+    # rope_ext per axis section + concat, as Flux2PosEmbed emits it
+    out, off = [], 0
+    for a, d in enumerate(axes):
+        out.append(orc.rope_normal(x[None, :, :, off:off + d], pos[:, a], d, float(theta))[0])
+        off += d
+    got = np.concatenate(out, -1)
+    assert_fp32(got, want, tol=tol, what=case)
+
+
+def test_qk_rmsnorm_rope_chain(orc, fx):
+    x, pos = fx["rope_flux_x"], fx["rope_flux_pos"]
+    w = orc.randn(9, (128,), mean=1.0, std=0.02)
+    xt = torch.from_numpy(x.astype(np.float64))
+    z = (torch.nn.functional.rms_norm(xt, (128,), eps=1e-6) * torch.from_numpy(w.astype(np.float64))).numpy()
+    # float64 complex rotation (diffusers' apply_rotary_emb form), theta 2000
+    from numpy import exp
+    want = np.empty_like(z)
+    for a in range(4):
+        d, off = 32, 32 * a
+        fr = 1.0 / (2000.0 ** (np.arange(0, d, 2) / d))
+        ang = pos[:, a][:, None] * fr[None]
+        zz = z[..., off:off + d:2] + 1j * z[..., off + 1:off + d:2]
+        r = zz * exp(1j * ang)[:, None, :]
+        want[..., off:off + d:2], want[..., off + 1:off + d:2] = r.real, r.imag
+    got = orc.qk_rmsnorm_rope(x, w, pos, 32, 2000.0, 1e-6)
+    assert_fp32(got, want, what="qk chain")
+    # invariant: all-zero positions leave the normalised vector unrotated
+    got0 = orc.qk_rmsnorm_rope(x, w, np.zeros_like(pos), 32, 2000.0, 1e-6)
+    assert_fp32(got0, z, what="p=0")
+    # one non-zero axis changes only that axis' 32 dims
+    p1 = np.zeros_like(pos)
+    p1[:, 2] = 5
+    g1 = orc.qk_rmsnorm_rope(x, w, p1, 32, 2000.0, 1e-6)
+    assert np.array_equal(g1[..., :64], got0[..., :64]) and np.array_equal(g1[..., 96:], got0[..., 96:])
+    assert not np.array_equal(g1[..., 64:96], got0[..., 64:96])
+
+
+# ---- quantisation ---------------------------------------------------------------
+
+def test_q8_0_known_answers(orc, qkat):
+    for case in qkat["q8_0"]:
+        blk = np.frombuffer(bytes.fromhex(case["block"]), dtype=np.uint8)
+        got = orc.dequantize(blk, 32, 8)
+        assert np.array_equal(got.view(np.uint32), np.array(case["expected_f32_bits"], np.uint32))
+
+
+def test_q4_K_known_answers(orc, qkat):
+    for case in qkat["q4_K"]:
+        blk = np.frombuffer(bytes.fromhex(case["block"]), dtype=np.uint8)
+        # 6-bit scale/min unpack of every sub-block
+        for j in range(8):
+            assert orc.q4_K_scale_min(j, blk[4:16]) == (case["sc"][j], case["m"][j])
+        got = orc.dequantize(blk, 256, 12)
+        assert np.array_equal(got.view(np.uint32), np.array(case["expected_f32_bits"], np.uint32))
+
+
+@pytest.mark.parametrize("qtype,qk", [(8, 32), (12, 256)])
+def test_quantizer_round_trip(orc, qtype, qk):
+    w = orc.randn(orc.tensor_seed(40), (8, 1024), std=0.02)
+    b = orc.quantize(w, qtype)
+    assert b.size == w.size // qk * (34 if qtype == 8 else 144)
+    y = orc.dequantize(b, w.size, qtype).reshape(w.shape)
+    blocks = np.abs(w).reshape(-1, qk).max(1)
+    err = np.abs(y - w).reshape(-1, qk).max(1)
+    # Q8_0: codes come from the fp32 step d = amax/127 but d is stored as fp16,
+    # so error <= d/2 + 127 * |d - fp16(d)| <= d * (0.5 + 127 * 2^-11).
+    # Q4_K: within ~1/15 of the block range.
+    bound = blocks / 127 * (0.5 + 127 * 2.0 ** -11) * 1.001 + 1e-9 if qtype == 8 \
+        else blocks * 2 / 15 * 0.75
+    assert np.all(err <= bound)
+    if qtype == 8:
+        # codes reach +-127 in every block (amax maps to the top code)
+        q = b.reshape(-1, 34)[:, 2:].view(np.int8)
+        assert np.all(np.abs(q).max(1) == 127)
