@@ -4,9 +4,12 @@
 // Flux2SingleTransformerBlock.hpp:50-54 / Flux2TransformerBlock.hpp:63-72.
 //
 // Fast path: one wave64 per row.  The row is held in VGPRs (one HBM read,
-// one HBM write), the mean and the centred variance are two wave-wide DPP
-// reductions over registers, and each wave keeps (1+scale) and shift for
-// its columns in VGPRs across all the rows it processes.
+// one HBM write, both non-temporal) with all of its 16-byte loads issued
+// back to back, the mean and the centred variance are two wave-wide DPP
+// reductions over registers, and while the row loads are in flight each
+// workgroup stages the fp32 (1 + scale, shift) vectors, shared by every row,
+// into LDS (24 KB at 3072 columns).  The small register footprint lets every
+// row of a Flux2 activation ([4608, 3072]) be resident at once.
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -20,69 +23,70 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
     const float* __restrict__ scale, T* __restrict__ y, int64_t ys, int rows,
     int nvec, float cols_f, float eps, float addend) {
     constexpr int EPV = Io<T>::EPV;
+    // (scale + addend, shift) interleaved per 4 columns: [nvec * EPV / 4][8].
+    extern __shared__ float4 mod_lds[];
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
-    const int nwaves = (int)((gridDim.x * blockDim.x) / kWave);
+    const int r = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const bool active = r < rows;
+    const T* xr = x + (int64_t)r * xs;
+    T* yr = y + (int64_t)r * ys;
 
-    float t1[VPL][EPV], sh[VPL][EPV];
+    // The whole row is in flight at once: VPL independent 16-byte loads.
+    float v[VPL][EPV];
+    float s = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-        const int v = lane + kWave * j;
+        const int vi = lane + kWave * j;
+        if (active && vi < nvec) {
+            Io<T>::load(xr + (int64_t)vi * EPV, v[j]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < EPV; e += 4) {
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-            if (v < nvec) {
-                a = *reinterpret_cast<const float4*>(scale + (int64_t)v * EPV + e);
-                b = *reinterpret_cast<const float4*>(shift + (int64_t)v * EPV + e);
+            for (int e = 0; e < EPV; ++e) v[j][e] = 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) s += v[j][e];
+    }
+    // Meanwhile the workgroup stages the modulation vectors (L2 hits) in LDS.
+    const int n4 = nvec * EPV / 4;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+        float4 sc = reinterpret_cast<const float4*>(scale)[i];
+        sc.x += addend; sc.y += addend; sc.z += addend; sc.w += addend;
+        mod_lds[2 * i] = sc;
+        mod_lds[2 * i + 1] = reinterpret_cast<const float4*>(shift)[i];
+    }
+    __syncthreads();
+    if (!active) return;
+    s = wave_sum(s);
+    const float mean = s / cols_f;
+    float s2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        if (lane + kWave * j < nvec) {
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const float d = v[j][e] - mean;
+                v[j][e] = d;
+                s2 += d * d;
             }
-            t1[j][e + 0] = a.x + addend; t1[j][e + 1] = a.y + addend;
-            t1[j][e + 2] = a.z + addend; t1[j][e + 3] = a.w + addend;
-            sh[j][e + 0] = b.x; sh[j][e + 1] = b.y; sh[j][e + 2] = b.z; sh[j][e + 3] = b.w;
         }
     }
-
-    for (int r = wave; r < rows; r += nwaves) {
-        const T* xr = x + (int64_t)r * xs;
-        T* yr = y + (int64_t)r * ys;
-        float v[VPL][EPV];
-        float s = 0.f;
+    s2 = wave_sum(s2);
+    const float rstd = 1.0f / sqrtf(s2 / cols_f + eps);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const int vi = lane + kWave * j;
-            if (vi < nvec) {
-                Io<T>::load(xr + (int64_t)vi * EPV, v[j]);
-            } else {
+    for (int j = 0; j < VPL; ++j) {
+        const int vi = lane + kWave * j;
+        if (vi < nvec) {
+            float o[EPV];
 #pragma unroll
-                for (int e = 0; e < EPV; ++e) v[j][e] = 0.f;
+            for (int e = 0; e < EPV; e += 4) {
+                const int i4 = (vi * EPV + e) / 4;
+                const float4 t = mod_lds[2 * i4], sh = mod_lds[2 * i4 + 1];
+                o[e + 0] = add_rn(mul_rn(mul_rn(v[j][e + 0], rstd), t.x), sh.x);
+                o[e + 1] = add_rn(mul_rn(mul_rn(v[j][e + 1], rstd), t.y), sh.y);
+                o[e + 2] = add_rn(mul_rn(mul_rn(v[j][e + 2], rstd), t.z), sh.z);
+                o[e + 3] = add_rn(mul_rn(mul_rn(v[j][e + 3], rstd), t.w), sh.w);
             }
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) s += v[j][e];
-        }
-        s = wave_sum(s);
-        const float mean = s / cols_f;
-        float s2 = 0.f;
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            if (lane + kWave * j < nvec) {
-#pragma unroll
-                for (int e = 0; e < EPV; ++e) {
-                    const float d = v[j][e] - mean;
-                    v[j][e] = d;
-                    s2 += d * d;
-                }
-            }
-        }
-        s2 = wave_sum(s2);
-        const float rstd = 1.0f / sqrtf(s2 / cols_f + eps);
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const int vi = lane + kWave * j;
-            if (vi < nvec) {
-                float o[EPV];
-#pragma unroll
-                for (int e = 0; e < EPV; ++e) o[e] = add_rn(mul_rn(mul_rn(v[j][e], rstd), t1[j][e]), sh[j][e]);
-                Io<T>::store(yr + (int64_t)vi * EPV, o);
-            }
+            Io<T>::store(yr + (int64_t)vi * EPV, o);
         }
     }
 }
@@ -114,13 +118,11 @@ template <typename T, int VPL>
 void launch_wave(const void* x, int64_t xs, const float* shift, const float* scale, void* y,
                  int64_t ys, int rows, int nvec, int64_t cols, float eps, float addend,
                  hipStream_t st) {
-    // Enough waves to cover the chip a few times over; each wave keeps its
-    // modulation columns in registers across rows.
-    const int cap_waves = cu_count() * 16;
-    const int rpw = (rows + cap_waves - 1) / cap_waves;
-    const int nwaves = (rows + rpw - 1) / rpw;
-    const int blocks = (nwaves + 3) / 4;
-    hipLaunchKernelGGL((adaln_wave_kernel<T, VPL>), dim3(blocks), dim3(256), 0, st,
+    // One wave per row, four rows per workgroup; LDS holds the block's copy
+    // of (scale + addend, shift): 8 bytes per column.
+    const int blocks = (rows + 3) / 4;
+    const size_t lds = (size_t)nvec * Io<T>::EPV * 2 * sizeof(float);
+    hipLaunchKernelGGL((adaln_wave_kernel<T, VPL>), dim3(blocks), dim3(256), lds, st,
                        (const T*)x, xs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps,
                        addend);
 }

@@ -62,7 +62,7 @@ __global__ __launch_bounds__(256) void dequant_q4_K_kernel(const uint8_t* __rest
     const uint32_t blk = k >> 5, e0 = (k & 31) * 8;     // element offset in the super-block
     const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
     const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 144;
-    const uint4 hdr = *reinterpret_cast<const uint4*>(b);
+    const uint4 hdr = *reinterpret_cast<const uint4*>(b);   // shared by 32 lanes: cached
     const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
     // Sub-block j = 2*c64 + hi; header bytes 4..15 are scales[0..11].
     const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);

@@ -3,16 +3,18 @@
 //   gated residual  y = h + o * gate[col]            Flux2SingleTransformerBlock.hpp:58
 //   Euler step      y = x + v * dt                   FlowMatchEulerDiscreteScheduler.cpp:210-222
 // Each thread moves U independent 16-byte vectors per operand (all loads
-// issued before any math), consecutive threads take consecutive vectors so
-// every wave instruction touches 1 KB of contiguous HBM, and the row index
-// of a vector comes from a multiply-high invariant division.
+// issued before any math) with non-temporal (streaming) accesses;
+// consecutive threads take consecutive vectors so every wave instruction
+// touches 1 KB of contiguous HBM, and the row index of a vector comes from a
+// multiply-high invariant division.  U = 2 with 512-thread workgroups was
+// the best of a sweep over U in {1,2,4,8} x {256,512,1024} threads.
 #include "capi_util.hpp"
 #include "common.hpp"
 
 namespace dit {
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 512;
 
 template <typename T, int U>
 __global__ __launch_bounds__(kBlock) void swiglu_kernel(const T* __restrict__ g, int64_t gs,
@@ -129,7 +131,7 @@ unsigned generic_blocks(int64_t n) {
     return (unsigned)(b < 1 ? 1 : (b > cap ? cap : b));
 }
 
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 2;
 
 template <typename T>
 int run_swiglu(const void* g, int64_t gs, const void* u, int64_t us, void* y, int64_t ys,

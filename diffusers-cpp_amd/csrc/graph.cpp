@@ -38,6 +38,11 @@ float fparam(const dt_tensor* t, int i) {
     return f;
 }
 
+// Byte offset of a VIEW into its source: op_params[0] (low) | op_params[1] (high).
+int64_t view_offset(const dt_tensor* t) {
+    return (int64_t)(uint32_t)t->op_params[0] | ((int64_t)t->op_params[1] << 32);
+}
+
 // Rows of ne[0] elements at a uniform row stride (in elements) covering
 // dims 1..3.
 bool row_layout(const dt_tensor* t, int64_t* rows, int64_t* stride) {
@@ -241,7 +246,9 @@ bool match_groupnorm(Graph& g, const dt_tensor* root, Plan& p) {
     if (!is_io_type(x->type) || x->type != root->type || !same_shape(x, root) || G <= 0 ||
         C % G || v->ne[0] != C / G * H_ * W_ || v->ne[2] != N || v->ne[3] != 1 ||
         !row_layout(x, &rows, &stride) || stride != W_ || !row_layout(root, &rows, &stride) ||
-        stride != W_ || v->data != x->data || r->data != n->data || !same_shape(r, x))
+        stride != W_ || view_offset(v) != 0 || view_offset(r) != 0 || !same_shape(r, x) ||
+        v->nb[0] != elem_size(x->type) || v->nb[1] != v->ne[0] * v->nb[0] ||
+        r->nb[0] != elem_size(x->type) || r->nb[1] != W_ * r->nb[0])
         return false;
     if ((w && !is_vec(w, C, 2)) || (b && !is_vec(b, C, 2))) return false;
     for (const auto& c : chain) g.claim(c.first);
@@ -312,7 +319,7 @@ bool match_qk(Graph& g, const dt_tensor* y, Plan& p) {
         }
         if (v->src[0] != wsrc || nd != axis_dim || fparam(r, 2) != base) return false;
         const int es = elem_size(wsrc->type);
-        if ((const char*)v->data - (const char*)wsrc->data != (int64_t)a * axis_dim * es) return false;
+        if (view_offset(v) != (int64_t)a * axis_dim * es) return false;
         if (v->nb[0] != es) return false;
         for (int i = 1; i < 4; ++i)
             if (v->ne[i] != wsrc->ne[i] || v->nb[i] != wsrc->nb[i]) return false;
@@ -439,8 +446,14 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
     hipStream_t st = backend_stream(be);
     switch (t->op) {
         case DT_OP_NONE:
-        case DT_OP_VIEW:
             return DT_OK;
+        case DT_OP_VIEW:
+            DT_REQUIRE(t->src[0] && t->src[0]->data, "dt_graph_compute: VIEW of a node without data");
+            t->data = (char*)t->src[0]->data + view_offset(t);
+            return DT_OK;
+        case DT_OP_UNARY:
+            ++g_kernels;
+            return dt_op_unary(t->op_params[0], t->src[0], t, fparam(t, 1), fparam(t, 2), st);
         case DT_OP_ADD:
         case DT_OP_SUB:
         case DT_OP_MUL:
@@ -485,6 +498,45 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
 }  // namespace
 }  // namespace dit
 
+namespace dit {
+namespace {
+
+int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& plans) {
+    g.claimed.assign(n_nodes, 0);
+    for (int i = 0; i < n_nodes; ++i) {
+        DT_REQUIRE(nodes[i] != nullptr, "dt_graph: node %d is null", i);
+        g.index[nodes[i]] = i;
+        for (int s = 0; s < 4; ++s)
+            if (nodes[i]->src[s]) g.uses[nodes[i]->src[s]]++;
+    }
+    plans.assign(n_nodes, Plan());
+    for (int i = n_nodes - 1; i >= 0; --i) {
+        if (g.claimed[i]) continue;
+        dt_tensor* t = nodes[i];
+        Plan& p = plans[i];
+        if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_adaln(g, t, p) ||
+            match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p))
+            continue;
+        p = Plan();
+    }
+    return DT_OK;
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* absorbed) {
+    using namespace dit;
+    DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0) && (absorbed || n_nodes == 0),
+               "dt_graph_plan: bad arguments");
+    Graph g;
+    std::vector<Plan> plans;
+    int rc = plan_graph(nodes, n_nodes, g, plans);
+    if (rc) return rc;
+    for (int i = 0; i < n_nodes; ++i) absorbed[i] = g.claimed[i] ? 1 : 0;
+    return DT_OK;
+}
+
 extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nodes) {
     using namespace dit;
     DT_REQUIRE(be != nullptr, "dt_graph_compute: null backend");
@@ -492,30 +544,15 @@ extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nod
     g_kernels = 0;
     g_fused = 0;
     Graph g;
-    g.claimed.assign(n_nodes, 0);
-    for (int i = 0; i < n_nodes; ++i) {
-        DT_REQUIRE(nodes[i] != nullptr, "dt_graph_compute: node %d is null", i);
-        g.index[nodes[i]] = i;
-        for (int s = 0; s < 4; ++s)
-            if (nodes[i]->src[s]) g.uses[nodes[i]->src[s]]++;
-    }
-    std::vector<Plan> plans(n_nodes);
-    for (int i = n_nodes - 1; i >= 0; --i) {
-        if (g.claimed[i]) continue;
-        dt_tensor* t = nodes[i];
-        Plan& p = plans[i];
-        if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_adaln(g, t, p) ||
-            match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p)) {
-            continue;
-        }
-        p = Plan();
-    }
+    std::vector<Plan> plans;
+    int rc = plan_graph(nodes, n_nodes, g, plans);
+    if (rc) return rc;
     for (int i = 0; i < n_nodes; ++i) {
         if (g.claimed[i]) {
             ++g_fused;
             continue;
         }
-        int rc = plans[i].kind != K_NONE ? run_plan(be, nodes[i], plans[i]) : run_unfused(be, nodes[i]);
+        rc = plans[i].kind != K_NONE ? run_plan(be, nodes[i], plans[i]) : run_unfused(be, nodes[i]);
         if (rc) return rc;
     }
     return DT_OK;

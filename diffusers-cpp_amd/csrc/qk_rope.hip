@@ -6,8 +6,8 @@
 //
 // Fast path (head_dim 128, axis_dim % 8 == 0): a head is one 16-lane DPP row,
 // each lane owns 8 consecutive dims (one 16-byte bf16 load, two for fp32) =
-// 4 rotation pairs of a single axis.  The sum of squares is a 4-step DPP
-// row reduction.  cos/sin come from a table built on the host with ggml's
+// 4 rotation pairs of a single axis, and a row walks 8 heads of one token.
+// The sum of squares is a 4-step DPP row reduction.  cos/sin come from a table built on the host with ggml's
 // fp32 angle recurrence, so angles match the CPU op exactly; the table is a
 // few tens of KB and stays L2-resident.  q and k go in one launch
 // (blockIdx.y selects the tensor); the per-lane norm weights stay in VGPRs.
@@ -94,52 +94,78 @@ __device__ __forceinline__ void store8<float>(float* p, const float* v) {
     Io<float>::store(p + 4, v + 4);
 }
 
-template <typename T>
+// A wave owns one token and up to 4*HPG of its heads: its four 16-lane DPP
+// rows take heads h0 + row + 4*i (i < HPG), so each load/store instruction
+// covers four consecutive heads = 1 KB of contiguous bf16.  The token's
+// position, its cos/sin table row and the lane's 8 norm weights are loaded
+// once per wave, and all HPG head loads are in flight before the first
+// reduction.
+template <typename T, int HPG>
 __global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkShape sh,
-                                                         const float* __restrict__ table) {
+                                                         const float* __restrict__ table,
+                                                         int chunks) {
     const QkHalf a = blockIdx.y == 0 ? q : k;
     if (a.x == nullptr) return;
+    const int wv = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    if (wv >= sh.tokens * chunks) return;  // whole waves leave together
     const int lane16 = threadIdx.x & 15;
+    const int row = (threadIdx.x & (kWave - 1)) >> 4;
     const int d0 = lane16 * 8;
     const int axis = d0 / sh.axis_dim;
     const int i0 = d0 - axis * sh.axis_dim;
+    const int t = wv / chunks;
+    const int h0 = (wv - t * chunks) * 4 * HPG + row;
+    const T* __restrict__ xb = (const T*)a.x + t * sh.in_ts + d0;
+    T* __restrict__ yb = (T*)a.y + t * sh.out_ts + d0;
+
+    // The position goes out first: loads retire in issue order, so the
+    // dependent table lookup below can start while the head loads are
+    // still in flight instead of after all of them.
     const int32_t* pax;
     int64_t pst;
     axis_pos(sh, axis, pax, pst);
-
+    const int p = pax[t * pst];
+    float v[HPG][8];
+#pragma unroll
+    for (int hh = 0; hh < HPG; ++hh) {
+        const int h = h0 + 4 * hh;
+        if (h < sh.heads) {
+            load8<T>(xb + (int64_t)h * sh.in_hs, v[hh]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[hh][e] = 0.f;
+        }
+    }
+    float cs[8];
+    rope_angles<4>(p, i0, table, sh.n_pos, sh.axis_dim, sh.theta_scale, cs);
     float w[8];
-    load8<float>(a.w + d0, w);
-
-    const int n_groups = sh.tokens * sh.heads;
-    const int g0 = (int)((blockIdx.x * blockDim.x + threadIdx.x) >> 4);
-    const int gstride = (int)((gridDim.x * blockDim.x) >> 4);
-    const T* __restrict__ xb = (const T*)a.x;
-    T* __restrict__ yb = (T*)a.y;
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {  // shared by every head: default (cached) policy
+        const float4 t4 = *reinterpret_cast<const float4*>(a.w + d0 + e);
+        w[e] = t4.x; w[e + 1] = t4.y; w[e + 2] = t4.z; w[e + 3] = t4.w;
+    }
     const float hd_f = (float)sh.head_dim;
 
-    for (int g = g0; g < n_groups; g += gstride) {
-        const int t = g / sh.heads;
-        const int h = g - t * sh.heads;
-        float v[8];
-        load8<T>(xb + t * sh.in_ts + h * sh.in_hs + d0, v);
-        const int p = pax[t * pst];
-        float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-        ss = row16_sum(ss);
-        const float r = 1.0f / sqrtf(ss / hd_f + sh.eps);
-        float cs[8];
-        rope_angles<4>(p, i0, table, sh.n_pos, sh.axis_dim, sh.theta_scale, cs);
-        float o[8];
+    for (int hh = 0; hh < HPG; ++hh) {
+        const int h = h0 + 4 * hh;
+        if (h < sh.heads) {  // uniform across the 16 lanes of a DPP row
+            float ss = 0.f;
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-            const float x0 = mul_rn(mul_rn(v[2 * qd], r), w[2 * qd]);
-            const float x1 = mul_rn(mul_rn(v[2 * qd + 1], r), w[2 * qd + 1]);
-            const float c = cs[2 * qd], s = cs[2 * qd + 1];
-            o[2 * qd] = sub_rn(mul_rn(x0, c), mul_rn(x1, s));
-            o[2 * qd + 1] = add_rn(mul_rn(x0, s), mul_rn(x1, c));
+            for (int e = 0; e < 8; ++e) ss += v[hh][e] * v[hh][e];
+            ss = row16_sum(ss);
+            const float r = 1.0f / sqrtf(ss / hd_f + sh.eps);
+            float o[8];
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const float x0 = mul_rn(mul_rn(v[hh][2 * qd], r), w[2 * qd]);
+                const float x1 = mul_rn(mul_rn(v[hh][2 * qd + 1], r), w[2 * qd + 1]);
+                const float c = cs[2 * qd], sn = cs[2 * qd + 1];
+                o[2 * qd] = sub_rn(mul_rn(x0, c), mul_rn(x1, sn));
+                o[2 * qd + 1] = add_rn(mul_rn(x0, sn), mul_rn(x1, c));
+            }
+            store8<T>(yb + (int64_t)h * sh.out_hs, o);
         }
-        store8<T>(yb + t * sh.out_ts + h * sh.out_hs + d0, o);
     }
 }
 
@@ -196,12 +222,12 @@ int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t s
         if (h->x) fast = fast && aligned16(h->x) && aligned16(h->y) && aligned16(h->w);
     const int ny = k.x ? 2 : 1;
     if (fast) {
-        const int64_t groups = (int64_t)sh.tokens * sh.heads;
-        int64_t blocks = (groups * 16 + 255) / 256;
-        const int64_t cap = (int64_t)cu_count() * 32;
-        if (blocks > cap) blocks = cap;
-        hipLaunchKernelGGL((qk_rope128_kernel<T>), dim3((unsigned)blocks, ny), dim3(256), 0, st,
-                           q, k, sh, table);
+        constexpr int HPG = 3;  // 12 heads per wave: best of HPG in {1, 2, 3, 6} on [4608, 24, 128]
+        const int chunks = (sh.heads + 4 * HPG - 1) / (4 * HPG);
+        const int64_t waves = (int64_t)sh.tokens * chunks;
+        const int64_t blocks = (waves + 3) / 4;
+        hipLaunchKernelGGL((qk_rope128_kernel<T, HPG>), dim3((unsigned)blocks, ny), dim3(256), 0, st,
+                           q, k, sh, table, chunks);
     } else {
         const int64_t groups = (int64_t)sh.tokens * sh.heads;
         const int64_t blocks = (groups + 255) / 256;

@@ -21,7 +21,7 @@ F32, F16, Q8_0, Q4_K, I32, BF16 = 0, 1, 8, 12, 26, 30
 
 # dt_tensor.op ids
 (OP_NONE, OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_SCALE, OP_SIGMOID, OP_NORM, OP_RMS_NORM,
- OP_ROPE, OP_CONCAT, OP_CPY, OP_VIEW, OP_FILL) = range(14)
+ OP_ROPE, OP_CONCAT, OP_CPY, OP_VIEW, OP_FILL, OP_UNARY) = range(15)
 FLAG_OUTPUT = 1
 
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = range(4)
@@ -89,6 +89,7 @@ _SIGS = {
     "dt_tensor_set": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
     "dt_tensor_get": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
     "dt_graph_compute": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32]),
+    "dt_graph_plan": (c_int32, [POINTER(POINTER(DtTensor)), c_int32, POINTER(c_int32)]),
     "dt_graph_last_stats": (c_int32, [POINTER(c_int32), POINTER(c_int32)]),
 }
 

@@ -241,18 +241,27 @@ enum {
     DT_OP_ROPE,          /* src[1] = pos (I32); op_params: n_dims, mode, base bits, scale bits */
     DT_OP_CONCAT,        /* op_params[0] = dim */
     DT_OP_CPY,           /* cont / cast into dst layout */
-    DT_OP_VIEW,          /* no-op: data aliases src[0] with own ne/nb */
+    DT_OP_VIEW,          /* data = src[0]->data + byte offset, own ne/nb;
+                            offset in op_params[0] (low 32 bits), [1] (high) */
     DT_OP_FILL,          /* op_params[0] = value bits */
+    DT_OP_UNARY,         /* op_params[0] = DT_UN_* kind, [1], [2] = p0, p1 bits */
     DT_OP_COUNT
 };
 
 /* Execute nodes in order.  Before dispatch a fusion pass rewrites the
  * chains listed for the fused entry points above into single kernels when
  * the intermediate nodes are not flagged DT_FLAG_OUTPUT; every other node
- * runs its unfused kernel.  Intermediate node data must be allocated by
- * the caller (ggml_gallocr's role in the reference). */
+ * runs its unfused kernel.  Node data is allocated by the caller
+ * (ggml_gallocr's role in the reference), except that a VIEW's data is set
+ * to its source's data plus its offset when the node is reached, and the
+ * nodes dt_graph_plan reports as absorbed are never read or written. */
 enum { DT_FLAG_OUTPUT = 1 };
 int dt_graph_compute(dt_backend *be, dt_tensor **nodes, int32_t n_nodes);
+
+/* Run only the fusion pass: absorbed[i] = 1 for nodes that a fused kernel
+ * replaces (their data needs no allocation), 0 otherwise.  Uses shapes,
+ * types, strides, view offsets and flags, never data pointers. */
+int dt_graph_plan(dt_tensor **nodes, int32_t n_nodes, int32_t *absorbed);
 /* Statistics of the last dt_graph_compute on this thread: kernels launched
  * and nodes absorbed into fused kernels. */
 int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);

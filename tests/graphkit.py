@@ -72,6 +72,8 @@ class Graph:
         for i in range(4):
             d.nb[i] = nb[i]
         d.data = src.d.data + offset_bytes
+        d.op_params[0] = ctypes.c_int32(offset_bytes & 0xFFFFFFFF).value
+        d.op_params[1] = offset_bytes >> 32
         d.src[0] = ctypes.pointer(src.d)
         n = Node(d)
         self.nodes.append(n)
@@ -131,11 +133,21 @@ class Graph:
         return self._new(dh.OP_CPY, a.ne, type_ if type_ is not None else a.d.type, [a])
 
     # ---- execution ---------------------------------------------------------
+    def _array(self):
+        return (ctypes.POINTER(dh.DtTensor) * len(self.nodes))(*[ctypes.pointer(n.d) for n in self.nodes])
+
+    def plan(self, outputs=()):
+        """Per-node absorbed flags from dt_graph_plan (no device work)."""
+        for o in outputs:
+            o.d.flags |= dh.FLAG_OUTPUT
+        flags = (ctypes.c_int32 * len(self.nodes))()
+        dh.check(dh.load().dt_graph_plan(self._array(), len(self.nodes), flags), "dt_graph_plan")
+        return list(flags)
+
     def compute(self, backend, outputs=()):
         for o in outputs:
             o.d.flags |= dh.FLAG_OUTPUT
-        arr = (ctypes.POINTER(dh.DtTensor) * len(self.nodes))(*[ctypes.pointer(n.d) for n in self.nodes])
-        dh.check(dh.load().dt_graph_compute(backend, arr, len(self.nodes)), "dt_graph_compute")
+        dh.check(dh.load().dt_graph_compute(backend, self._array(), len(self.nodes)), "dt_graph_compute")
         k = ctypes.c_int32()
         f = ctypes.c_int32()
         dh.load().dt_graph_last_stats(ctypes.byref(k), ctypes.byref(f))

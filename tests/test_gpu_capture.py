@@ -1,0 +1,65 @@
+"""The fused chain captured into a HIP graph (through torch.cuda.CUDAGraph,
+launches still go through the C ABI) must reproduce the eager results on
+every replay, with the program's own eager work and synchronisations in
+between.  None of the library's kernels records a memset, so replays are
+expected to be bit-identical to the eager launches."""
+import numpy as np
+import pytest
+import torch
+
+import dit_hip
+from test_gpu_fused import dev_tensor, flux_positions
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replays_match_eager(orc, dev):
+    S, D, H, I = 320, 3072, 24, 9216
+    pos = torch.from_numpy(flux_positions(64, 16)).cuda()
+    x = dev_tensor(orc.randn(1, (S, D)), torch.bfloat16)
+    sh = dev_tensor(orc.randn(2, (D,), std=0.1), torch.float32)
+    sc = dev_tensor(orc.randn(3, (D,), std=0.1), torch.float32)
+    q = dev_tensor(orc.randn(4, (S, H, 128)), torch.bfloat16)
+    k = dev_tensor(orc.randn(5, (S, H, 128)), torch.bfloat16)
+    w = dev_tensor(orc.randn(6, (128,), mean=1.0, std=0.02), torch.float32)
+    gu = dev_tensor(orc.randn(7, (S, 2 * I)), torch.bfloat16)
+    gate = dev_tensor(orc.randn(8, (D,), std=0.1), torch.float32)
+    gn_x = dev_tensor(orc.randn(9, (1, 64, 32, 32)), torch.bfloat16)
+    tab = dit_hip.rope_table(64, 32, 10000.0)
+    outs = [torch.empty((S, D), dtype=torch.bfloat16, device="cuda"),
+            torch.empty((S, H, 128), dtype=torch.bfloat16, device="cuda"),
+            torch.empty((S, H, 128), dtype=torch.bfloat16, device="cuda"),
+            torch.empty((S, I), dtype=torch.bfloat16, device="cuda"),
+            torch.empty((S, D), dtype=torch.bfloat16, device="cuda"),
+            torch.empty((1, 64, 32, 32), dtype=torch.bfloat16, device="cuda")]
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+
+    def chain():
+        dit_hip.adaln_mod(x, sh, sc, 1e-6, out=outs[0])
+        dit_hip.qk_rmsnorm_rope(q, k, w, w, pos, 32, 10000.0, 1e-6, table=tab, q_out=outs[1],
+                                k_out=outs[2])
+        dit_hip.swiglu(gu[:, :I], gu[:, I:], out=outs[3])
+        dit_hip.gated_residual(x, outs[0], gate, out=outs[4])
+        dit_hip.groupnorm_silu(gn_x, 32, None, None, 1e-6, out=outs[5], workspace=ws)
+
+    chain()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        chain()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))                      # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep} output {i}"

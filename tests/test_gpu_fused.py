@@ -36,9 +36,14 @@ def as_input(a, dtype):
     return oracle.round_bf16(a) if dtype == torch.bfloat16 else np.asarray(a, np.float32)
 
 
-def check(got, ref, dtype, what):
+def check(got, ref, dtype, what, one_rounding=True):
+    """bf16: the north-star bar (rel L2 <= 1e-2, cos >= 0.9999) and, for a
+    single fused kernel (one rounding of an fp32 result), at most one bf16
+    ulp per element; fp32: |d| <= 1e-5 * max(|ref|, 1)."""
     if dtype == torch.bfloat16:
         assert_bf16(got, ref, what)
+        if not one_rounding:
+            return
         r = np.asarray(ref, np.float64)
         err = np.abs(np.asarray(got, np.float64) - r)
         bound = np.abs(r) * 2.0 ** -8 + 1e-5 * max(1.0, float(np.abs(r).max()))
