@@ -108,6 +108,8 @@ struct Graph {
     std::unordered_map<const dt_tensor*, int> uses;
     std::unordered_map<const dt_tensor*, int> index;
     std::vector<char> claimed;
+    std::vector<int> root;   // index of the node whose fused kernel absorbs node i
+    int current_root = -1;
 
     bool internal(const dt_tensor* t, int n_uses = 1) const {
         if (!t || (t->flags & DT_FLAG_OUTPUT)) return false;
@@ -116,7 +118,11 @@ struct Graph {
         auto u = uses.find(t);
         return u != uses.end() && u->second == n_uses;
     }
-    void claim(const dt_tensor* t) { claimed[index.at(t)] = 1; }
+    void claim(const dt_tensor* t) {
+        const int i = index.at(t);
+        claimed[i] = 1;
+        root[i] = current_root;
+    }
 };
 
 bool match_adaln(Graph& g, const dt_tensor* a, Plan& p) {
@@ -503,6 +509,7 @@ namespace {
 
 int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& plans) {
     g.claimed.assign(n_nodes, 0);
+    g.root.assign(n_nodes, -1);
     for (int i = 0; i < n_nodes; ++i) {
         DT_REQUIRE(nodes[i] != nullptr, "dt_graph: node %d is null", i);
         g.index[nodes[i]] = i;
@@ -514,6 +521,7 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
         if (g.claimed[i]) continue;
         dt_tensor* t = nodes[i];
         Plan& p = plans[i];
+        g.current_root = i;
         if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_adaln(g, t, p) ||
             match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p))
             continue;
@@ -525,15 +533,15 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
 }  // namespace
 }  // namespace dit
 
-extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* absorbed) {
+extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_into) {
     using namespace dit;
-    DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0) && (absorbed || n_nodes == 0),
+    DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0) && (fused_into || n_nodes == 0),
                "dt_graph_plan: bad arguments");
     Graph g;
     std::vector<Plan> plans;
     int rc = plan_graph(nodes, n_nodes, g, plans);
     if (rc) return rc;
-    for (int i = 0; i < n_nodes; ++i) absorbed[i] = g.claimed[i] ? 1 : 0;
+    for (int i = 0; i < n_nodes; ++i) fused_into[i] = g.claimed[i] ? g.root[i] : -1;
     return DT_OK;
 }
 

@@ -1,0 +1,560 @@
+// hip_runtime.cpp -- HipRuntime: records dt_tensor nodes through the
+// Runtime interface (src/ggml/Runtime.hpp) and executes them with the C ABI.
+//
+// compute() mirrors the reference's ExecutionRuntime::run
+// (src/ggml/ExecutionRuntime.cpp:42-276) for one scope: leaves (inputs and
+// parameters) get their own buffer and are uploaded, op nodes share one
+// arena allocated with liveness reuse (ggml_gallocr's job in the reference,
+// Context.hpp:118-135), nodes a fused kernel absorbs get no memory at all
+// (dt_graph_plan tells which), and dt_graph_compute runs the graph.
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <limits>
+#include <map>
+
+namespace dit {
+namespace host {
+
+void check(int rc, const char* what) {
+    if (rc != DT_OK) throw Error(std::string(what) + ": " + dt_last_error());
+}
+
+namespace {
+
+thread_local Runtime* g_current = nullptr;
+
+int32_t fbits(float f) {
+    int32_t i;
+    std::memcpy(&i, &f, 4);
+    return i;
+}
+
+int64_t elem_size(int32_t type) {
+    switch (type) {
+        case DT_TYPE_F32:
+        case DT_TYPE_I32:
+            return 4;
+        case DT_TYPE_F16:
+        case DT_TYPE_BF16:
+            return 2;
+        default:
+            return 0;
+    }
+}
+
+// Block size (elements) and bytes per block of the quantised types.
+void block_layout(int32_t type, int64_t* qk, int64_t* bytes) {
+    if (type == DT_TYPE_Q8_0) {
+        *qk = 32;
+        *bytes = 34;
+    } else if (type == DT_TYPE_Q4_K) {
+        *qk = 256;
+        *bytes = 144;
+    } else {
+        *qk = 1;
+        *bytes = elem_size(type);
+    }
+}
+
+void contiguous_nb(int32_t type, const int64_t ne[4], int64_t nb[4]) {
+    int64_t qk, bs;
+    block_layout(type, &qk, &bs);
+    nb[0] = bs;
+    nb[1] = nb[0] * (ne[0] / qk);
+    nb[2] = nb[1] * ne[1];
+    nb[3] = nb[2] * ne[2];
+}
+
+bool is_contiguous(const Node* t) {
+    int64_t nb[4];
+    contiguous_nb(t->type, t->ne, nb);
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] > 1 && t->nb[i] != nb[i]) return false;
+    return true;
+}
+
+int64_t nelements(const Node* t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+// Best-fit free list over [0, peak) with coalescing.
+class ArenaPlanner {
+public:
+    size_t alloc(size_t n) {
+        n = align_up(n ? n : 1);
+        auto best = free_.end();
+        for (auto it = free_.begin(); it != free_.end(); ++it)
+            if (it->second >= n && (best == free_.end() || it->second < best->second)) best = it;
+        if (best != free_.end()) {
+            const size_t off = best->first, sz = best->second;
+            free_.erase(best);
+            if (sz > n) free_[off + n] = sz - n;
+            return off;
+        }
+        // Grow: reuse a free block that touches the end.
+        size_t off = peak_;
+        if (!free_.empty()) {
+            auto last = std::prev(free_.end());
+            if (last->first + last->second == peak_) {
+                off = last->first;
+                free_.erase(last);
+            }
+        }
+        peak_ = off + n;
+        return off;
+    }
+    void release(size_t off, size_t n) {
+        n = align_up(n ? n : 1);
+        auto it = free_.emplace(off, n).first;
+        auto next = std::next(it);
+        if (next != free_.end() && it->first + it->second == next->first) {
+            it->second += next->second;
+            free_.erase(next);
+        }
+        if (it != free_.begin()) {
+            auto prev = std::prev(it);
+            if (prev->first + prev->second == it->first) {
+                prev->second += it->second;
+                free_.erase(it);
+            }
+        }
+    }
+    size_t peak() const { return peak_; }
+
+private:
+    std::map<size_t, size_t> free_;
+    size_t peak_ = 0;
+};
+
+}  // namespace
+
+Runtime& current_runtime() {
+    if (!g_current) throw std::logic_error("no Runtime in scope (create a RuntimeScope)");
+    return *g_current;
+}
+
+RuntimeScope::RuntimeScope(Runtime& rt) : prev_(g_current) { g_current = &rt; }
+RuntimeScope::~RuntimeScope() { g_current = prev_; }
+
+// ---------------------------------------------------------------------------
+
+HipRuntime::HipRuntime(int device, dt_stream_t stream) {
+    check(dt_backend_init(device, &be_), "dt_backend_init");
+    check(dt_backend_set_stream(be_, stream), "dt_backend_set_stream");
+}
+
+HipRuntime::~HipRuntime() {
+    try {
+        reset();
+    } catch (...) {
+    }
+    dt_backend_free(be_);
+}
+
+size_t HipRuntime::nbytes(const Node* t) {
+    int64_t qk, bs;
+    block_layout(t->type, &qk, &bs);
+    return (size_t)(nelements(t) / qk * bs);
+}
+
+Node* HipRuntime::make(int32_t type, const int64_t ne[4], int32_t op) {
+    nodes_.emplace_back();
+    Node* t = &nodes_.back();
+    std::memset(t, 0, sizeof(Node));
+    t->type = type;
+    t->op = op;
+    for (int i = 0; i < 4; ++i) t->ne[i] = ne[i];
+    contiguous_nb(type, t->ne, t->nb);
+    t->id = (int32_t)nodes_.size() - 1;
+    if (op != DT_OP_NONE) order_.push_back(t);
+    return t;
+}
+
+Node* HipRuntime::view_of(Node* src, const int64_t ne[4], const int64_t nb[4], size_t offset) {
+    Node* t = make(src->type, ne, DT_OP_VIEW);
+    for (int i = 0; i < 4; ++i) t->nb[i] = nb[i];
+    t->src[0] = src;
+    t->op_params[0] = (int32_t)(uint32_t)(offset & 0xFFFFFFFFu);
+    t->op_params[1] = (int32_t)(offset >> 32);
+    return t;
+}
+
+Node* HipRuntime::root_of(Node* t) const {
+    for (;;) {
+        if (t->op == DT_OP_VIEW) {
+            t = t->src[0];
+            continue;
+        }
+        auto a = alias_.find(t);
+        if (a != alias_.end()) {
+            t = a->second;
+            continue;
+        }
+        return t;
+    }
+}
+
+// ---- creation ----------------------------------------------------------------
+
+Node* HipRuntime::new_tensor(int32_t type, int n_dims, const int64_t* ne) {
+    if (n_dims < 1 || n_dims > 4) throw std::invalid_argument("new_tensor: n_dims must be 1..4");
+    int64_t e[4] = {1, 1, 1, 1};
+    for (int i = 0; i < n_dims; ++i) e[i] = ne[i];
+    Node* t = make(type, e, DT_OP_NONE);
+    leaves_.push_back(t);
+    return t;
+}
+
+Node* HipRuntime::new_tensor_1d(int32_t type, int64_t ne0) { return new_tensor(type, 1, &ne0); }
+
+void HipRuntime::set_input(Node* t) { (void)t; }
+void HipRuntime::set_param(Node* t) { (void)t; }
+void HipRuntime::set_output(Node* t) { t->flags |= DT_FLAG_OUTPUT; }
+
+Node* HipRuntime::fill(Node* t, float value) {
+    Node* r = make(t->type, t->ne, DT_OP_FILL);
+    r->op_params[0] = fbits(value);
+    return r;
+}
+
+// ---- copies ------------------------------------------------------------------
+
+Node* HipRuntime::cont(Node* t) {
+    Node* r = make(t->type, t->ne, DT_OP_CPY);
+    r->src[0] = t;
+    return r;
+}
+
+Node* HipRuntime::dup(Node* t) { return cont(t); }
+
+Node* HipRuntime::cast(Node* t, int32_t type) {
+    Node* r = make(type, t->ne, DT_OP_CPY);
+    r->src[0] = t;
+    return r;
+}
+
+Node* HipRuntime::cpy(Node* src, Node* dst) {
+    if (nelements(src) != nelements(dst)) throw std::invalid_argument("cpy: element counts differ");
+    Node* r = make(dst->type, dst->ne, DT_OP_CPY);
+    for (int i = 0; i < 4; ++i) r->nb[i] = dst->nb[i];
+    r->src[0] = src;
+    r->src[1] = dst;
+    alias_[r] = dst;
+    return r;
+}
+
+// ---- elementwise ---------------------------------------------------------------
+
+Node* HipRuntime::unary(Node* a, int32_t kind, float p0, float p1) {
+    Node* r = make(a->type, a->ne, DT_OP_UNARY);
+    r->src[0] = a;
+    r->op_params[0] = kind;
+    r->op_params[1] = fbits(p0);
+    r->op_params[2] = fbits(p1);
+    return r;
+}
+
+Node* HipRuntime::sqrt(Node* t) { return unary(t, DT_UN_SQRT); }
+Node* HipRuntime::exp(Node* t) { return unary(t, DT_UN_EXP); }
+Node* HipRuntime::log(Node* t) { return unary(t, DT_UN_LOG); }
+Node* HipRuntime::sin(Node* t) { return unary(t, DT_UN_SIN); }
+Node* HipRuntime::cos(Node* t) { return unary(t, DT_UN_COS); }
+
+Node* HipRuntime::sigmoid(Node* t) {
+    Node* r = make(t->type, t->ne, DT_OP_SIGMOID);
+    r->src[0] = t;
+    return r;
+}
+
+Node* HipRuntime::binary(int32_t op, Node* a, Node* b) {
+    for (int i = 0; i < 4; ++i)
+        if (b->ne[i] == 0 || a->ne[i] % b->ne[i] != 0)
+            throw std::invalid_argument("binary op: rhs does not broadcast into lhs");
+    Node* r = make(a->type, a->ne, op);
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
+Node* HipRuntime::add(Node* a, Node* b) { return binary(DT_OP_ADD, a, b); }
+Node* HipRuntime::sub(Node* a, Node* b) { return binary(DT_OP_SUB, a, b); }
+Node* HipRuntime::mul(Node* a, Node* b) { return binary(DT_OP_MUL, a, b); }
+Node* HipRuntime::div(Node* a, Node* b) { return binary(DT_OP_DIV, a, b); }
+
+Node* HipRuntime::scale(Node* t, float value) {
+    Node* r = make(t->type, t->ne, DT_OP_SCALE);
+    r->src[0] = t;
+    r->op_params[0] = fbits(value);
+    return r;
+}
+
+Node* HipRuntime::clamp(Node* t, float mn, float mx) { return unary(t, DT_UN_CLAMP, mn, mx); }
+
+Node* HipRuntime::mul_mat(Node*, Node*) {
+    throw Unsupported("mul_mat: GEMMs run in the step harness, not in this elementwise backend");
+}
+
+// ---- views -----------------------------------------------------------------------
+
+static void reshape_check(const Node* t, const int64_t ne[4]) {
+    if (!is_contiguous(t)) throw std::invalid_argument("reshape: tensor is not contiguous");
+    if (ne[0] * ne[1] * ne[2] * ne[3] != nelements(t))
+        throw std::invalid_argument("reshape: element count changes");
+}
+
+Node* HipRuntime::reshape_4d(Node* t, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3) {
+    const int64_t ne[4] = {ne0, ne1, ne2, ne3};
+    reshape_check(t, ne);
+    int64_t nb[4];
+    contiguous_nb(t->type, ne, nb);
+    return view_of(t, ne, nb, 0);
+}
+Node* HipRuntime::reshape_1d(Node* t, int64_t ne0) { return reshape_4d(t, ne0, 1, 1, 1); }
+Node* HipRuntime::reshape_2d(Node* t, int64_t ne0, int64_t ne1) { return reshape_4d(t, ne0, ne1, 1, 1); }
+Node* HipRuntime::reshape_3d(Node* t, int64_t ne0, int64_t ne1, int64_t ne2) {
+    return reshape_4d(t, ne0, ne1, ne2, 1);
+}
+
+Node* HipRuntime::permute(Node* t, int a0, int a1, int a2, int a3) {
+    const int ax[4] = {a0, a1, a2, a3};
+    int64_t ne[4], nb[4];
+    bool seen[4] = {false, false, false, false};
+    for (int i = 0; i < 4; ++i) {
+        if (ax[i] < 0 || ax[i] > 3 || seen[ax[i]]) throw std::invalid_argument("permute: bad axes");
+        seen[ax[i]] = true;
+        ne[ax[i]] = t->ne[i];
+        nb[ax[i]] = t->nb[i];
+    }
+    return view_of(t, ne, nb, 0);
+}
+
+Node* HipRuntime::view_4d(Node* t, int64_t ne0, int64_t ne1, int64_t ne2, int64_t ne3, size_t nb1,
+                          size_t nb2, size_t nb3, size_t offset) {
+    const int64_t ne[4] = {ne0, ne1, ne2, ne3};
+    const int64_t nb[4] = {t->nb[0], (int64_t)nb1, (int64_t)nb2, (int64_t)nb3};
+    return view_of(t, ne, nb, offset);
+}
+Node* HipRuntime::view_3d(Node* t, int64_t ne0, int64_t ne1, int64_t ne2, size_t nb1, size_t nb2,
+                          size_t offset) {
+    return view_4d(t, ne0, ne1, ne2, 1, nb1, nb2, nb2 * ne2, offset);
+}
+Node* HipRuntime::view_2d(Node* t, int64_t ne0, int64_t ne1, size_t nb1, size_t offset) {
+    return view_4d(t, ne0, ne1, 1, 1, nb1, nb1 * ne1, nb1 * ne1, offset);
+}
+Node* HipRuntime::view_1d(Node* t, int64_t ne0, size_t offset) {
+    const size_t row = (size_t)(t->nb[0] * ne0);
+    return view_4d(t, ne0, 1, 1, 1, row, row, row, offset);
+}
+
+// ---- structure ---------------------------------------------------------------------
+
+Node* HipRuntime::repeat(Node* t, Node* target) {
+    // ggml_repeat tiles t into target's shape: a broadcast add onto zeros.
+    Node* zeros = make(t->type, target->ne, DT_OP_FILL);
+    zeros->op_params[0] = fbits(0.0f);
+    return binary(DT_OP_ADD, zeros, t);
+}
+
+Node* HipRuntime::concat(Node* a, Node* b, int dim) {
+    if (dim < 0 || dim > 3) throw std::invalid_argument("concat: dim must be 0..3");
+    int64_t ne[4];
+    for (int i = 0; i < 4; ++i) {
+        if (i != dim && a->ne[i] != b->ne[i]) throw std::invalid_argument("concat: shapes differ");
+        ne[i] = a->ne[i] + (i == dim ? b->ne[i] : 0);
+    }
+    Node* r = make(a->type, ne, DT_OP_CONCAT);
+    r->src[0] = a;
+    r->src[1] = b;
+    r->op_params[0] = dim;
+    return r;
+}
+
+Node* HipRuntime::sum_rows(Node*) { throw Unsupported("sum_rows: not part of the DiT elementwise chain"); }
+Node* HipRuntime::flash_attn_ext(Node*, Node*, Node*, Node*, float, float, float) {
+    throw Unsupported("flash_attn_ext: attention runs in the step harness, not in this backend");
+}
+Node* HipRuntime::conv_2d_direct(Node*, Node*, int, int, int, int, int, int) {
+    throw Unsupported("conv_2d_direct: not part of the DiT elementwise chain");
+}
+Node* HipRuntime::get_rows(Node*, Node*) { throw Unsupported("get_rows: not part of the DiT elementwise chain"); }
+Node* HipRuntime::pool_2d(Node*, PoolOp, int, int, int, int, float, float) {
+    throw Unsupported("pool_2d: not part of the DiT elementwise chain");
+}
+Node* HipRuntime::interpolate(Node*, int64_t, int64_t, int64_t, int64_t, uint32_t) {
+    throw Unsupported("interpolate: not part of the DiT elementwise chain");
+}
+Node* HipRuntime::upscale(Node*, int, ScaleMode) {
+    throw Unsupported("upscale: not part of the DiT elementwise chain");
+}
+
+// ---- norms / rope ----------------------------------------------------------------
+
+Node* HipRuntime::norm(Node* a, float eps) {
+    Node* r = make(a->type, a->ne, DT_OP_NORM);
+    r->src[0] = a;
+    r->op_params[0] = fbits(eps);
+    return r;
+}
+
+Node* HipRuntime::rms_norm(Node* a, float eps) {
+    Node* r = make(a->type, a->ne, DT_OP_RMS_NORM);
+    r->src[0] = a;
+    r->op_params[0] = fbits(eps);
+    return r;
+}
+
+Node* HipRuntime::rope_ext(Node* a, Node* b, Node* c, int n_dims, int mode, int n_ctx_orig,
+                           float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                           float beta_fast, float beta_slow) {
+    (void)n_ctx_orig;
+    (void)beta_fast;
+    (void)beta_slow;
+    if (c != nullptr) throw Unsupported("rope_ext: frequency factors are not supported");
+    if (mode != 0) throw Unsupported("rope_ext: only mode 0 (NORMAL) is supported");
+    if (ext_factor != 0.0f) throw Unsupported("rope_ext: YaRN (ext_factor != 0) is not supported");
+    if (!b || b->type != DT_TYPE_I32 || b->ne[0] != a->ne[2])
+        throw std::invalid_argument("rope_ext: positions must be I32 with ne0 == a->ne[2]");
+    Node* r = make(a->type, a->ne, DT_OP_ROPE);
+    r->src[0] = a;
+    r->src[1] = b;
+    r->op_params[0] = n_dims;
+    r->op_params[1] = mode;
+    r->op_params[2] = fbits(freq_base);
+    r->op_params[3] = fbits(freq_scale);
+    r->op_params[4] = fbits(ext_factor);
+    r->op_params[5] = fbits(attn_factor);
+    return r;
+}
+
+// ---- data and execution ----------------------------------------------------------
+
+void HipRuntime::bind(Node* leaf, const void* host, size_t bytes) {
+    if (leaf->op != DT_OP_NONE) throw std::invalid_argument("bind: only leaves carry host data");
+    if (bytes != nbytes(leaf)) throw std::invalid_argument("bind: byte count does not match the tensor");
+    auto& v = host_data_[leaf];
+    v.assign((const uint8_t*)host, (const uint8_t*)host + bytes);
+}
+
+void HipRuntime::compute() {
+    const int n = (int)order_.size();
+    // 1. fusion plan
+    std::vector<int32_t> fused_into(n, -1);
+    if (n) check(dt_graph_plan(order_.data(), n, fused_into.data()), "dt_graph_plan");
+    std::unordered_map<const Node*, int> pos;
+    for (int i = 0; i < n; ++i) pos[order_[i]] = i;
+
+    // 2. last use of every storage root, at the position where the reading
+    //    kernel runs (the fused root for absorbed nodes)
+    const int kForever = std::numeric_limits<int>::max();
+    std::unordered_map<const Node*, int> last_use;
+    for (int i = 0; i < n; ++i) {
+        Node* t = order_[i];
+        const int at = fused_into[i] >= 0 ? fused_into[i] : i;
+        for (int s = 0; s < 4; ++s) {
+            if (!t->src[s]) continue;
+            const Node* r = root_of(t->src[s]);
+            int& lu = last_use[r];
+            lu = std::max(lu, at);
+        }
+        if (t->flags & DT_FLAG_OUTPUT) last_use[root_of(t)] = kForever;
+    }
+
+    // 3. arena plan for op nodes that own storage
+    ArenaPlanner planner;
+    std::unordered_map<const Node*, size_t> offset;
+    std::vector<std::vector<const Node*>> release_at(n);
+    size_t naive = 0;
+    for (int i = 0; i < n; ++i) {
+        Node* t = order_[i];
+        const bool owns = t->op != DT_OP_VIEW && !alias_.count(t);
+        if (owns) naive += align_up(nbytes(t));
+        if (owns && fused_into[i] < 0) {
+            // The output is placed before this position's inputs are released,
+            // so a kernel never writes over what it reads.
+            offset[t] = planner.alloc(nbytes(t));
+            auto lu = last_use.find(t);
+            const int end = lu == last_use.end() ? i : lu->second;
+            if (end != kForever) release_at[std::max(end, i)].push_back(t);
+        }
+        for (const Node* r : release_at[i]) planner.release(offset.at(r), nbytes(r));
+        release_at[i].clear();
+    }
+
+    // 4. device memory: leaves in their own buffer, op nodes in the arena
+    if (leaf_buf_) {
+        check(dt_buffer_free(be_, leaf_buf_), "dt_buffer_free");
+        leaf_buf_ = nullptr;
+    }
+    size_t leaf_bytes = 0;
+    for (Node* l : leaves_) leaf_bytes += align_up(nbytes(l));
+    if (leaf_bytes) check(dt_buffer_alloc(be_, leaf_bytes, &leaf_buf_), "dt_buffer_alloc(leaves)");
+    size_t off = 0;
+    for (Node* l : leaves_) {
+        l->data = (char*)leaf_buf_ + off;
+        off += align_up(nbytes(l));
+        auto h = host_data_.find(l);
+        if (h != host_data_.end())
+            check(dt_tensor_set(l, h->second.data(), 0, h->second.size(), nullptr), "dt_tensor_set");
+    }
+    if (planner.peak() > arena_cap_) {
+        if (arena_) check(dt_buffer_free(be_, arena_), "dt_buffer_free");
+        arena_ = nullptr;
+        arena_cap_ = 0;
+        check(dt_buffer_alloc(be_, planner.peak(), &arena_), "dt_buffer_alloc(arena)");
+        arena_cap_ = planner.peak();
+    }
+    for (int i = 0; i < n; ++i) {
+        Node* t = order_[i];
+        auto o = offset.find(t);
+        t->data = o != offset.end() ? (char*)arena_ + o->second : nullptr;
+    }
+    for (int i = 0; i < n; ++i) {
+        Node* t = order_[i];
+        if (alias_.count(t)) {
+            Node* dst = t->src[1];
+            // the destination may itself be a view: resolve its address
+            Node* r = dst;
+            int64_t extra = 0;
+            while (r->op == DT_OP_VIEW) {
+                extra += (int64_t)(uint32_t)r->op_params[0] | ((int64_t)r->op_params[1] << 32);
+                r = r->src[0];
+            }
+            t->data = r->data ? (char*)r->data + extra : nullptr;
+        }
+    }
+
+    // 5. run
+    if (n) check(dt_graph_compute(be_, order_.data(), n), "dt_graph_compute");
+    check(dt_backend_synchronize(be_), "dt_backend_synchronize");
+    int32_t k = 0, f = 0;
+    dt_graph_last_stats(&k, &f);
+    stats_.nodes = n;
+    stats_.kernels = k;
+    stats_.fused_nodes = f;
+    stats_.arena_bytes = planner.peak();
+    stats_.naive_bytes = naive;
+}
+
+void HipRuntime::read(const Node* node, void* host, size_t bytes) const {
+    if (!node->data) throw std::invalid_argument("read: node has no data (was it marked as output?)");
+    check(dt_tensor_get(node, host, 0, bytes, nullptr), "dt_tensor_get");
+}
+
+void HipRuntime::reset() {
+    if (leaf_buf_) dt_buffer_free(be_, leaf_buf_);
+    if (arena_) dt_buffer_free(be_, arena_);
+    leaf_buf_ = arena_ = nullptr;
+    arena_cap_ = 0;
+    nodes_.clear();
+    order_.clear();
+    leaves_.clear();
+    host_data_.clear();
+    alias_.clear();
+    stats_ = ComputeStats();
+}
+
+}  // namespace host
+}  // namespace dit

@@ -1,0 +1,161 @@
+// modules.hpp -- the reference's nn / Flux2 module call sites for the DiT
+// elementwise chain, restated on the host Tensor layer so that they record
+// the same node graph the reference records through its Runtime:
+//   LayerNorm      src/nn/modules/normalization/LayerNorm.cpp:16-32
+//   RMSNorm        src/nn/modules/normalization/RMSNorm.cpp:12-22
+//   GroupNorm      src/nn/modules/normalization/GroupNorm.cpp:79-161
+//   SiLU           src/nn/SiLU.hpp:9-13
+//   Flux2PosEmbed  src/diffusers/models/transformers/flux2/Flux2PosEmbed.hpp:18-109
+//   Flux2SwiGLU    src/diffusers/models/transformers/flux2/Flux2SwiGLU.hpp:17-21
+//   Flux2Modulation::split  Flux2Modulation.hpp:24-41
+// plus the modulation / residual expressions of the transformer blocks
+// (Flux2SingleTransformerBlock.hpp:50-58, Flux2TransformerBlock.hpp:63-111).
+// Parameters are F32 leaves created at construction (a RuntimeScope must be
+// active); callers bind their data through HipRuntime::bind.
+#pragma once
+
+#include <array>
+#include <vector>
+
+#include "tensor.hpp"
+
+namespace dit {
+namespace host {
+
+inline Tensor parameter(const Tensor::Shape& shape) {
+    Tensor p = Tensor::empty(shape, DT_TYPE_F32);
+    current_runtime().set_param(*p);
+    return p;
+}
+
+class LayerNorm {
+public:
+    explicit LayerNorm(int64_t dim, float eps = 1e-5f, bool elementwise_affine = true, bool bias = true)
+        : eps_(eps), affine_(elementwise_affine), bias_(bias) {
+        if (affine_) {
+            weight = parameter({dim});
+            if (bias_) this->bias = parameter({dim});
+        }
+    }
+    Tensor forward(Tensor x) const {
+        x = Tensor(current_runtime().norm(*x, eps_), x.shape());
+        if (affine_) {
+            x = x * weight;
+            if (bias_) x = x + bias;
+        }
+        return x;
+    }
+    Tensor weight, bias;
+
+private:
+    float eps_;
+    bool affine_, bias_;
+};
+
+class RMSNorm {
+public:
+    explicit RMSNorm(int64_t dim, float eps = 1e-5f, bool elementwise_affine = true)
+        : eps_(eps), affine_(elementwise_affine) {
+        if (affine_) weight = parameter({dim});
+    }
+    Tensor forward(Tensor x) const {
+        x = Tensor(current_runtime().rms_norm(*x, eps_), x.shape());
+        if (affine_) x = x * weight;
+        return x;
+    }
+    Tensor weight;
+
+private:
+    float eps_;
+    bool affine_;
+};
+
+class GroupNorm {
+public:
+    GroupNorm(int64_t num_groups, int64_t num_channels, float eps = 1e-5f, bool affine = true,
+              bool bias = true)
+        : groups_(num_groups), eps_(eps), affine_(affine), bias_(bias) {
+        if (affine_) {
+            weight = parameter({num_channels});
+            if (bias_) this->bias = parameter({num_channels});
+        }
+    }
+    Tensor forward(Tensor input) const {
+        const auto s = input.shape();
+        const int64_t n = s[0], c = s[1], h = s[2], w = s[3];
+        input = input.reshape({n, groups_, -1});
+        input = Tensor(current_runtime().norm(*input, eps_), input.shape());
+        input = input.reshape({n, c, h, w});
+        if (affine_) {
+            input = input * weight.reshape({1, c, 1, 1});
+            if (bias_) input = input + bias.reshape({1, c, 1, 1});
+        }
+        return input;
+    }
+    Tensor weight, bias;
+
+private:
+    int64_t groups_;
+    float eps_;
+    bool affine_, bias_;
+};
+
+struct SiLU {
+    // x * sigmoid(x): the composite the reference emits instead of ggml_silu.
+    Tensor forward(const Tensor& x) const { return x * x.sigmoid(); }
+};
+
+class Flux2PosEmbed {
+public:
+    Flux2PosEmbed(int64_t theta, std::vector<int64_t> axes_dim) : theta_(theta), axes_(std::move(axes_dim)) {}
+
+    // x: [..., head_dim]; position_ids: I32 [sequence, n_axes].
+    Tensor forward(const Tensor& x, const Tensor& position_ids) const {
+        std::vector<Tensor> sections;
+        int64_t offset = 0;
+        for (size_t axis = 0; axis < axes_.size(); ++axis) {
+            const int64_t d = axes_[axis];
+            Tensor x_axis = x.narrow(-1, offset, d);
+            Tensor pos_axis = position_ids.select(1, (int64_t)axis);  // narrow + squeeze (-> CONT)
+            if (pos_axis.ndim() != 1) pos_axis = pos_axis.flatten(0, pos_axis.ndim() - 1);
+            Node* r = current_runtime().rope_ext(*x_axis, *pos_axis, nullptr, (int)d, 0, 0,
+                                                 (float)theta_, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f);
+            sections.emplace_back(r, x_axis.shape());
+            offset += d;
+        }
+        return Tensor::cat(sections, -1);
+    }
+
+private:
+    int64_t theta_;
+    std::vector<int64_t> axes_;
+};
+
+struct Flux2SwiGLU {
+    Tensor forward(const Tensor& gate, const Tensor& up) const { return SiLU().forward(gate) * up; }
+};
+
+struct Flux2Modulation {
+    // [1, 3*sets*D] or [1, 1, 3*sets*D] -> per set {shift, scale, gate} views.
+    static std::vector<std::array<Tensor, 3>> split(Tensor mod, int64_t sets) {
+        if (mod.ndim() == 2) mod = mod.unsqueeze(1);
+        auto parts = mod.chunk((int)(3 * sets), -1);
+        std::vector<std::array<Tensor, 3>> out;
+        for (int64_t i = 0; i < sets; ++i) out.push_back({parts[3 * i], parts[3 * i + 1], parts[3 * i + 2]});
+        return out;
+    }
+};
+
+// `(1.0f + scale) * norm(x) + shift` (Flux2SingleTransformerBlock.hpp:53).
+inline Tensor adaln_modulate(const LayerNorm& norm, const Tensor& x, const Tensor& shift,
+                             const Tensor& scale) {
+    return (1.0f + scale) * norm.forward(x) + shift;
+}
+
+// `hidden + gate * out` (Flux2SingleTransformerBlock.hpp:58).
+inline Tensor gated_residual(const Tensor& hidden, const Tensor& gate, const Tensor& out) {
+    return hidden + gate * out;
+}
+
+}  // namespace host
+}  // namespace dit

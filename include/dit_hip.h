@@ -246,6 +246,8 @@ enum {
     DT_OP_FILL,          /* op_params[0] = value bits */
     DT_OP_UNARY,         /* op_params[0] = DT_UN_* kind, [1], [2] = p0, p1 bits */
     DT_OP_COUNT
+    /* DT_OP_CPY: src[0] is copied (converted) into the node; src[1], when
+       set, is the destination tensor the node aliases (ggml_cpy). */
 };
 
 /* Execute nodes in order.  Before dispatch a fusion pass rewrites the
@@ -258,10 +260,12 @@ enum {
 enum { DT_FLAG_OUTPUT = 1 };
 int dt_graph_compute(dt_backend *be, dt_tensor **nodes, int32_t n_nodes);
 
-/* Run only the fusion pass: absorbed[i] = 1 for nodes that a fused kernel
- * replaces (their data needs no allocation), 0 otherwise.  Uses shapes,
- * types, strides, view offsets and flags, never data pointers. */
-int dt_graph_plan(dt_tensor **nodes, int32_t n_nodes, int32_t *absorbed);
+/* Run only the fusion pass: fused_into[i] = index of the node whose fused
+ * kernel absorbs node i (node i's data is then never read or written, so it
+ * needs no allocation, and the fused kernel reads node i's inputs when that
+ * root node runs), or -1 when node i runs on its own.  Uses shapes, types,
+ * strides, view offsets and flags, never data pointers. */
+int dt_graph_plan(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into);
 /* Statistics of the last dt_graph_compute on this thread: kernels launched
  * and nodes absorbed into fused kernels. */
 int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);

@@ -137,12 +137,12 @@ class Graph:
         return (ctypes.POINTER(dh.DtTensor) * len(self.nodes))(*[ctypes.pointer(n.d) for n in self.nodes])
 
     def plan(self, outputs=()):
-        """Per-node absorbed flags from dt_graph_plan (no device work)."""
+        """Per-node fused-into indices from dt_graph_plan (-1: runs alone)."""
         for o in outputs:
             o.d.flags |= dh.FLAG_OUTPUT
-        flags = (ctypes.c_int32 * len(self.nodes))()
-        dh.check(dh.load().dt_graph_plan(self._array(), len(self.nodes), flags), "dt_graph_plan")
-        return list(flags)
+        roots = (ctypes.c_int32 * len(self.nodes))()
+        dh.check(dh.load().dt_graph_plan(self._array(), len(self.nodes), roots), "dt_graph_plan")
+        return list(roots)
 
     def compute(self, backend, outputs=()):
         for o in outputs:

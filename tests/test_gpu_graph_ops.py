@@ -237,9 +237,11 @@ def oracle_single_block(orc, raw, pos, dtype, D, theta):
 @pytest.mark.parametrize("S,D,H,I", [(48, 3072, 24, 9216), (12, 256, 2, 512)])
 def test_graph_single_block_chain_fused(orc, be, dtype, S, D, H, I):
     g, raw, pos, outs, _ = build_single_block_chain(orc, dtype, S, D, H, I)
-    absorbed = g.plan(outputs=outs.values())
+    roots = g.plan(outputs=outs.values())
     kernels, fused = g.compute(be, outputs=outs.values())
-    assert sum(absorbed) == fused
+    assert sum(r >= 0 for r in roots) == fused
+    # every absorbed node is absorbed by a later node that runs a fused kernel
+    assert all(r > i and roots[r] == -1 for i, r in enumerate(roots) if r >= 0)
     torch.cuda.synchronize()
     want = oracle_single_block(orc, raw, pos, dtype, D, 2000.0)
     for name, node in outs.items():

@@ -1,0 +1,249 @@
+"""The C++ host layer end to end, the way the reference's tests exercise its
+modules: a Python test writes inputs, runs the command-line driver (here
+diffusers-cpp_amd/bin/dit_cli, in the role of test/utils/*-cli), reads the
+outputs and compares them with the oracle.  Cases follow the reference's
+unit tests (test/src/nn/modules/normalization/{LayerNorm,GroupNorm,RMSNorm}.py,
+test/src/nn/SiLU.py, test/src/diffusers/models/transformers/flux2/
+{Flux2PosEmbed,Flux2SwiGLU}.py) plus Flux2-sized chains; graph statistics
+printed by the driver confirm which node chains were fused."""
+import json
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from conftest import PKG, assert_bf16, assert_fp32
+
+pytestmark = pytest.mark.gpu
+
+CLI = os.path.join(PKG, "bin", "dit_cli")
+MAGIC = 0x31425444
+SEED = 0x5EED2000
+
+
+def write_dtb(path, a, type_):
+    a = np.ascontiguousarray(a)
+    with open(path, "wb") as f:
+        f.write(np.array([MAGIC, type_, a.ndim, 0], dtype=np.int32).tobytes())
+        f.write(np.array(a.shape, dtype=np.int64).tobytes())
+        f.write(a.tobytes())
+
+
+def read_dtb(path):
+    with open(path, "rb") as f:
+        hdr = np.frombuffer(f.read(16), dtype=np.int32)
+        assert hdr[0] == MAGIC
+        shape = tuple(np.frombuffer(f.read(8 * hdr[2]), dtype=np.int64))
+        raw = f.read()
+    if hdr[1] == 0:
+        return np.frombuffer(raw, dtype=np.float32).reshape(shape)
+    import oracle
+    return oracle.from_bf16_bits(np.frombuffer(raw, dtype=np.uint16)).reshape(shape)
+
+
+class Cli:
+    def __init__(self, tmp, bf16=False):
+        self.tmp = tmp
+        self.bf16 = bf16
+        self.n = 0
+
+    def act(self, a):
+        """An activation file; bf16 mode stores the RNE rounding and returns
+        the values the device sees."""
+        import oracle
+        self.n += 1
+        p = os.path.join(self.tmp, f"a{self.n}.dtb")
+        if self.bf16:
+            write_dtb(p, oracle.to_bf16_bits(a), 30)
+            return p, oracle.round_bf16(a)
+        write_dtb(p, np.asarray(a, np.float32), 0)
+        return p, np.asarray(a, np.float32)
+
+    def f32(self, a):
+        self.n += 1
+        p = os.path.join(self.tmp, f"p{self.n}.dtb")
+        write_dtb(p, np.asarray(a, np.float32), 0)
+        return p
+
+    def i32(self, a):
+        self.n += 1
+        p = os.path.join(self.tmp, f"i{self.n}.dtb")
+        write_dtb(p, np.asarray(a, np.int32), 26)
+        return p
+
+    def out(self, name="out"):
+        return os.path.join(self.tmp, f"{name}.dtb")
+
+    def run(self, command, *args):
+        r = subprocess.run([CLI, command, *map(str, args)], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, f"dit_cli {command} failed: {r.stderr}"
+        return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def check(got, want, bf16, what):
+    if bf16:
+        assert_bf16(got, want, what)
+    else:
+        assert_fp32(got, want, what=what)
+
+
+@pytest.fixture(params=[False, True], ids=["f32", "bf16"])
+def cli(request, dev):
+    with tempfile.TemporaryDirectory() as d:
+        yield Cli(d, bf16=request.param)
+
+
+# ---- nn modules: the reference's own toy cases --------------------------------
+
+def test_layernorm_affine_and_plain(orc, cli):
+    x = orc.randn(SEED, (2, 2, 3))
+    w = orc.randn(SEED + 1, (3,), mean=1.0, std=0.1)
+    b = orc.randn(SEED + 2, (3,), std=0.1)
+    xp, xv = cli.act(x)
+    cli.run("LayerNorm", "--dim", 3, "--eps", "1e-5", "--x", xp, "--param-weight", cli.f32(w),
+            "--param-bias", cli.f32(b), "--out", cli.out())
+    want = orc.binary(0, orc.binary(2, orc.norm(xv, 1e-5), w), b)
+    check(read_dtb(cli.out()), want, cli.bf16, "LayerNorm")
+    cli.run("LayerNorm", "--dim", 3, "--eps", "1e-5", "--elementwise_affine", "false", "--x", xp,
+            "--out", cli.out("o2"))
+    check(read_dtb(cli.out("o2")), orc.norm(xv, 1e-5), cli.bf16, "LayerNorm no affine")
+
+
+def test_rmsnorm_and_silu(orc, cli):
+    x = orc.randn(SEED + 3, (4, 5, 40))
+    w = orc.randn(SEED + 4, (40,), mean=1.0, std=0.02)
+    xp, xv = cli.act(x)
+    cli.run("RMSNorm", "--dim", 40, "--eps", "1e-6", "--x", xp, "--param-weight", cli.f32(w),
+            "--out", cli.out())
+    check(read_dtb(cli.out()), orc.binary(2, orc.rms_norm(xv, 1e-6), w), cli.bf16, "RMSNorm")
+    st = cli.run("SiLU", "--x", xp, "--out", cli.out("s"))
+    check(read_dtb(cli.out("s")), xv.astype(np.float64) / (1 + np.exp(-xv.astype(np.float64))), cli.bf16, "SiLU")
+    assert st["kernels"] == 1 and st["fused_nodes"] == 1   # MUL(x, SIGMOID(x)) -> one kernel
+
+
+@pytest.mark.parametrize("shape,G,affine,bias,silu", [
+    ((2, 4, 3, 3), 2, True, True, False), ((1, 8, 4, 4), 4, True, True, False),
+    ((2, 4, 2, 2), 2, False, False, False), ((2, 4, 2, 2), 2, True, False, False),
+    ((1, 128, 32, 32), 32, True, True, True)])
+def test_groupnorm(orc, cli, shape, G, affine, bias, silu):
+    x = orc.randn(SEED + 5, shape)
+    w = orc.randn(SEED + 6, (shape[1],), mean=1.0, std=0.02)
+    b = orc.randn(SEED + 7, (shape[1],), std=0.02)
+    xp, xv = cli.act(x)
+    args = ["--num_groups", G, "--num_channels", shape[1], "--eps", "1e-6", "--input", xp,
+            "--affine", str(affine).lower(), "--bias", str(bias).lower(), "--silu", str(silu).lower(),
+            "--out", cli.out()]
+    if affine:
+        args += ["--param-weight", cli.f32(w)]
+        if bias:
+            args += ["--param-bias", cli.f32(b)]
+    st = cli.run("GroupNorm", *args)
+    want = orc.groupnorm_silu(xv, G, w if affine else None, b if affine and bias else None, 1e-6, silu=silu)
+    check(read_dtb(cli.out()), want, cli.bf16, "GroupNorm")
+    if affine and bias:
+        assert st["kernels"] == 2, st        # stats + apply: the chain fused
+
+
+def test_flux2_posembed_reference_cases(orc, cli):
+    # Flux2PosEmbed.py test_zero / test_4d_axes: 4 axes x 2 dims, 4 heads
+    for pos in (np.zeros((3, 4), np.int32), np.array([[0, 0, 0, 0], [1, 2, 3, 4], [5, 6, 7, 8]], np.int32)):
+        x = orc.randn(SEED + 8, (1, 3, 4, 8))
+        xp, xv = cli.act(x)
+        cli.run("Flux2PosEmbed", "--theta", 10000, *sum((["--axes_dim", 2] for _ in range(4)), []),
+                "--x", xp, "--position_ids", cli.i32(pos), "--out", cli.out())
+        got = read_dtb(cli.out())
+        want = np.concatenate([orc.rope_normal(xv[..., 2 * a:2 * a + 2], pos[:, a], 2, 10000.0)
+                               for a in range(4)], -1)
+        check(got, want, cli.bf16, "posembed")
+
+
+def test_flux2_swiglu(orc, cli):
+    g, u = orc.randn(SEED + 9, (2, 5, 48)), orc.randn(SEED + 10, (2, 5, 48))
+    gp, gv = cli.act(g)
+    up, uv = cli.act(u)
+    st = cli.run("Flux2SwiGLU", "--gate", gp, "--up", up, "--out", cli.out())
+    check(read_dtb(cli.out()), orc.swiglu(gv, uv), cli.bf16, "swiglu")
+    assert st["kernels"] == 1
+
+
+def test_adaln_modulation(orc, cli):
+    x = orc.randn(SEED + 11, (1, 20, 3072))
+    mod = orc.randn(SEED + 12, (1, 3 * 3072), std=0.1)
+    xp, xv = cli.act(x)
+    st = cli.run("AdaLNModulation", "--x", xp, "--mod", cli.f32(mod), "--out", cli.out())
+    want = orc.adaln(xv[0], mod[0, :3072], mod[0, 3072:6144], 1e-6)
+    check(read_dtb(cli.out())[0], want, cli.bf16, "adaln")
+    # FILL(1) and ADD(scale, 1) run alone; NORM/MUL/ADD become one kernel
+    assert st["kernels"] == 3 and st["fused_nodes"] == 2, st
+
+
+# ---- Flux2 chains at block shape ---------------------------------------------------
+
+def seq_positions(n_txt, n_img, width):
+    txt = [[0, 0, 0, l] for l in range(n_txt)]
+    img = [[0, i // width, i % width, 0] for i in range(n_img)]
+    return np.array(txt + img, dtype=np.int32)
+
+
+def test_single_block_elementwise_chain(orc, cli):
+    S, D, H, I = 96, 3072, 24, 9216
+    pos = seq_positions(32, 64, 8)
+    x, mod = orc.randn(SEED + 13, (1, S, D)), orc.randn(SEED + 14, (1, 3 * D), std=0.1)
+    q, k = orc.randn(SEED + 15, (1, S, D)), orc.randn(SEED + 16, (1, S, D))
+    g, u = orc.randn(SEED + 17, (1, S, I)), orc.randn(SEED + 18, (1, S, I))
+    attn = orc.randn(SEED + 19, (1, S, D))
+    wq = orc.randn(SEED + 20, (128,), mean=1.0, std=0.02)
+    wk = orc.randn(SEED + 21, (128,), mean=1.0, std=0.02)
+    xp, xv = cli.act(x)
+    qp, qv = cli.act(q)
+    kp, kv = cli.act(k)
+    gp, gv = cli.act(g)
+    upp, uv = cli.act(u)
+    ap, av = cli.act(attn)
+    st = cli.run("Flux2SingleBlockElementwise", "--heads", H, "--theta", 2000,
+                 *sum((["--axes_dim", 32] for _ in range(4)), []),
+                 "--x", xp, "--mod", cli.f32(mod), "--q", qp, "--k", kp, "--mlp_gate", gp, "--mlp_up", upp,
+                 "--attn_out", ap, "--position_ids", cli.i32(pos), "--param-norm_q", cli.f32(wq),
+                 "--param-norm_k", cli.f32(wk), "--out-norm", cli.out("n"), "--out-q", cli.out("q"),
+                 "--out-k", cli.out("k"), "--out-mlp", cli.out("m"), "--out-residual", cli.out("r"))
+    m = mod[0]
+    check(read_dtb(cli.out("n"))[0], orc.adaln(xv[0], m[:D], m[D:2 * D], 1e-6), cli.bf16, "norm")
+    check(read_dtb(cli.out("q"))[0], orc.qk_rmsnorm_rope(qv[0].reshape(S, H, 128), wq, pos, 32, 2000.0),
+          cli.bf16, "q")
+    check(read_dtb(cli.out("k"))[0], orc.qk_rmsnorm_rope(kv[0].reshape(S, H, 128), wk, pos, 32, 2000.0),
+          cli.bf16, "k")
+    check(read_dtb(cli.out("m"))[0], orc.swiglu(gv[0], uv[0]), cli.bf16, "swiglu")
+    check(read_dtb(cli.out("r"))[0], orc.gated_residual(xv[0], av[0], m[2 * D:]), cli.bf16, "residual")
+    # fill + (1+scale) + adaLN + 2x4 position CONTs (Flux2PosEmbed::forward
+    # runs once for q and once for k) + q + k + SwiGLU + residual
+    assert st["kernels"] == 15, st
+    assert st["arena_bytes"] < st["naive_bytes"] / 2, st
+
+
+def test_double_stream_qk(orc, cli):
+    St, Si, H = 16, 32, 3
+    pos = seq_positions(St, Si, 8)
+    qt, qi = orc.randn(SEED + 22, (1, St, 384)), orc.randn(SEED + 23, (1, Si, 384))
+    wt = orc.randn(SEED + 24, (128,), mean=1.0, std=0.02)
+    wi = orc.randn(SEED + 25, (128,), mean=1.0, std=0.02)
+    tp, tv = cli.act(qt)
+    ip, iv = cli.act(qi)
+    st = cli.run("Flux2DoubleStreamQK", "--heads", H, "--theta", 10000, *sum((["--axes_dim", 32] for _ in range(4)), []),
+                 "--txt_q", tp, "--img_q", ip, "--position_ids", cli.i32(pos),
+                 "--param-norm_added_q", cli.f32(wt), "--param-norm_q", cli.f32(wi), "--out", cli.out())
+    got = read_dtb(cli.out())[0]
+    want = np.concatenate([orc.qk_rmsnorm_rope(tv[0].reshape(St, H, 128), wt, pos[:St], 32, 10000.0),
+                           orc.qk_rmsnorm_rope(iv[0].reshape(Si, H, 128), wi, pos[St:], 32, 10000.0)])
+    check(got, want, cli.bf16, "double-stream q")
+    assert st["kernels"] == 4 + 2, st      # 4 position CONTs + one fused launch per segment
+
+
+def test_cli_rejects_bad_input(dev):
+    with tempfile.TemporaryDirectory() as d:
+        r = subprocess.run([CLI, "NoSuchCommand"], capture_output=True, text=True, timeout=60)
+        assert r.returncode != 0
+        r = subprocess.run([CLI, "SiLU", "--x", os.path.join(d, "missing.dtb"), "--out", os.path.join(d, "o")],
+                           capture_output=True, text=True, timeout=60)
+        assert r.returncode != 0 and "cannot open" in r.stderr
