@@ -138,3 +138,72 @@ extern "C" int dt_dequant(const void* src, int32_t qtype, int64_t rows, int64_t 
     if (dst_type == DT_TYPE_F32) return dit::run<float>(src, qtype, rows, cols, row_bytes, dst, dst_stride, st);
     return dit::run<dit::bf16>(src, qtype, rows, cols, row_bytes, dst, dst_stride, st);
 }
+
+// ---------------------------------------------------------------------------
+// Q8_0 quantisation (ggml quantize_row_q8_0_ref): per block of 32,
+// d = amax / 127, id = d ? 1 / d : 0, q_j = roundf(x_j * id), d stored as the
+// RNE fp16 of d.  Four lanes share a block (8 values each); amax is combined
+// across the quad with two xor shuffles.  Used to make Q8_0 weight bytes on
+// the device (the reference reads them from GGUF files,
+// src/ggml/GGUFLoaderVisitor.cpp:214-281).
+// ---------------------------------------------------------------------------
+namespace dit {
+namespace {
+
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restrict__ src, int64_t src_stride,
+                                                            uint8_t* __restrict__ dst, int64_t row_bytes,
+                                                            uint32_t total, FastDiv quads_per_row) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = idx < total;
+    const uint32_t r = live ? fdiv(idx, quads_per_row) : 0;
+    const uint32_t k = live ? idx - r * quads_per_row.d : 0;
+    const uint32_t blk = k >> 2, part = k & 3;
+    float v[8];
+    if (live) {
+        const float4* p = reinterpret_cast<const float4*>(src + (int64_t)r * src_stride + (int64_t)k * 8);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.f;
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    // lanes 4i..4i+3 hold one block (threads of a quad are consecutive)
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    if (!live) return;
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t* b = dst + (int64_t)r * row_bytes + (int64_t)blk * 34;
+    if (part == 0) *reinterpret_cast<uint16_t*>(b) = f32_to_f16_bits(d);
+    uint16_t* qs = reinterpret_cast<uint16_t*>(b + 2 + 8 * part);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int lo = (int)roundf(v[2 * j] * id), hi = (int)roundf(v[2 * j + 1] * id);
+        qs[j] = (uint16_t)((lo & 0xFF) | ((hi & 0xFF) << 8));
+    }
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_quantize_q8_0(const float* src, int64_t rows, int64_t cols, int64_t src_stride, void* dst,
+                                int64_t row_bytes, dt_stream_t stream) {
+    DT_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "dt_quantize_q8_0: cols must be a positive multiple of 32");
+    DT_REQUIRE(src_stride >= cols && src_stride % 4 == 0, "dt_quantize_q8_0: bad src_stride");
+    DT_REQUIRE(row_bytes >= cols / 32 * 34 && row_bytes % 2 == 0, "dt_quantize_q8_0: bad row_bytes");
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(src && dst, "dt_quantize_q8_0: null pointer");
+    DT_REQUIRE(dit::aligned16(src) && (reinterpret_cast<uintptr_t>(dst) & 1) == 0,
+               "dt_quantize_q8_0: src must be 16-byte and dst 2-byte aligned");
+    const int64_t quads = cols / 8, total = rows * quads;
+    DT_REQUIRE(total < (1ll << 31), "dt_quantize_q8_0: too many elements for one launch");
+    const dit::FastDiv fd = dit::make_fastdiv((uint32_t)quads);
+    const unsigned grid = (unsigned)((total + 255) / 256);
+    hipLaunchKernelGGL(dit::quantize_q8_0_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, src_stride,
+                       (uint8_t*)dst, row_bytes, (uint32_t)total, fd);
+    return dit::check_launch("dt_quantize_q8_0");
+}

@@ -72,6 +72,12 @@ _SIGS = {
                                     c_void_p, c_float, c_int32, c_void_p, c_void_p, c_size_t,
                                     c_int32, _S]),
     "dt_euler_step": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_int64, c_int32, _S]),
+    "dt_quantize_q8_0": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, _S]),
+    "dt_gemm_bf16": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+                               c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32, _S]),
+    "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                     c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
+                                     POINTER(c_int64), POINTER(c_int64), c_float, c_int32, _S]),
     "dt_op_binary": (c_int32, [c_int32, POINTER(DtTensor), POINTER(DtTensor), POINTER(DtTensor), _S]),
     "dt_op_unary": (c_int32, [c_int32, POINTER(DtTensor), POINTER(DtTensor), c_float, c_float, _S]),
     "dt_op_norm": (c_int32, [POINTER(DtTensor), POINTER(DtTensor), c_float, _S]),
@@ -302,6 +308,48 @@ def euler_step(x, v, dt, out=None):
     check(load().dt_euler_step(_p(x), _p(v), dt, _p(y), x.numel(), io_type(x), stream()),
           "dt_euler_step")
     return y
+
+
+def quantize_q8_0(x, out=None):
+    """x: float32 [rows, cols] (row-contiguous) -> uint8 [rows, cols/32*34]."""
+    torch = _torch()
+    rows, cols = x.shape
+    rb = cols // 32 * 34
+    y = torch.empty((rows, rb), dtype=torch.uint8, device=x.device) if out is None else out
+    check(load().dt_quantize_q8_0(_p(x), rows, cols, x.stride(0), _p(y), y.stride(0), stream()),
+          "dt_quantize_q8_0")
+    return y
+
+
+def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None):
+    """a: bf16 [M, K], b: bf16 [N, K] (rows K-contiguous) -> a @ b.T (+ bias) (+ addend)."""
+    torch = _torch()
+    M, K = a.shape
+    N = b.shape[0]
+    assert b.shape[1] == K and a.stride(1) == 1 and b.stride(1) == 1
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=a.device)
+    ldd = addend.stride(0) if addend is not None else 0
+    check(load().dt_gemm_bf16(_p(a), a.stride(0), _p(b), b.stride(0), _p(out), out.stride(0), M, N,
+                              K, _p(bias), _p(addend), ldd, io_type(out), stream()),
+          "dt_gemm_bf16")
+    return out
+
+
+def flash_attn(q, k, v, scale=None, out=None, out_dtype=None):
+    """q: bf16 [B, Sq, H, 128], k, v: [B, Skv, H, 128] (any strides with d
+    contiguous) -> softmax(scale q k^T) v as [B, Sq, H, 128]."""
+    torch = _torch()
+    B, Sq, H, D = q.shape
+    Skv = k.shape[1]
+    if out is None:
+        out = torch.empty((B, Sq, H, D), dtype=out_dtype or torch.bfloat16, device=q.device)
+    st = lambda t: (c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+    scale = 1.0 / D ** 0.5 if scale is None else scale
+    check(load().dt_flash_attn_bf16(_p(q), _p(k), _p(v), _p(out), B, H, Sq, Skv, D, st(q), st(k),
+                                    st(v), st(out), scale, io_type(out), stream()),
+          "dt_flash_attn_bf16")
+    return out
 
 
 # --------------------------------------------------------------------------

@@ -158,6 +158,41 @@ int dt_groupnorm_silu(const void *x, int64_t N, int64_t C, int64_t HW, int64_t g
 int dt_euler_step(const void *x, const void *v, float dt, void *y, int64_t n,
                   int32_t io_type, dt_stream_t stream);
 
+/* Q8_0 quantisation of fp32 rows (ggml quantize_row_q8_0_ref semantics:
+ * d = amax/127, q = roundf(x / d), d stored as RNE fp16).  cols % 32 == 0;
+ * dst row r starts at dst + r*row_bytes.  Makes Q8_0 weight bytes on the
+ * device, in place of the GGUF reader of src/ggml/GGUFLoaderVisitor.cpp:214-281. */
+int dt_quantize_q8_0(const float *src, int64_t rows, int64_t cols, int64_t src_stride,
+                     void *dst, int64_t row_bytes, dt_stream_t stream);
+
+/* ---- step-time support: Linear and attention ---------------------------- */
+
+/* C[m][n] = sum_k A[m][k] * B[n][k] (+ bias[n]) (+ addend[m][n]), bf16 A and
+ * B, fp32 accumulation, C of c_type (DT_TYPE_BF16 or DT_TYPE_F32; addend has
+ * C's type and leading dimension ldd).  A is the activation [M, K] and B a
+ * Linear weight [N, K] (PyTorch [out, in]), both K-contiguous: this is
+ * Runtime::mul_mat(w, x) (src/ggml/Runtime.hpp:136-139) as called by
+ * Linear::forward (src/nn/Linear.cpp:17-36), and with `addend` the
+ * `attn(x) + mlp(y)` sum of Flux2FusedAttentionOutput::forward
+ * (src/diffusers/models/transformers/flux2/Flux2FusedAttentionOutput.hpp:31-36).
+ * K % 64 == 0; lda, ldb % 8 == 0; A, B 16-byte aligned.  C may alias addend. */
+int dt_gemm_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C, int64_t ldc,
+                 int64_t M, int64_t N, int64_t K, const float *bias, const void *addend,
+                 int64_t ldd, int32_t c_type, dt_stream_t stream);
+
+/* Unmasked attention softmax(scale * Q K^T) V per (batch, head), head_dim
+ * 128, bf16 q/k/v, fp32 softmax and accumulation, o of o_type (BF16 or F32).
+ * Element (b, s, h, d) of q is q[b*q_strides[0] + s*q_strides[1] +
+ * h*q_strides[2] + d]; likewise k, v (seq_kv tokens) and o (seq_q tokens).
+ * Replaces Runtime::flash_attn_ext (src/ggml/Runtime.hpp:250-257) as called
+ * by FlashAttentionOp::operator() (src/nn/attention/FlashAttentionOp.cpp:84-94)
+ * with no mask; strides are multiples of 8 (q, k, v) / 4 (o) elements. */
+int dt_flash_attn_bf16(const void *q, const void *k, const void *v, void *o, int64_t batch,
+                       int64_t heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                       const int64_t *q_strides, const int64_t *k_strides,
+                       const int64_t *v_strides, const int64_t *o_strides, float scale,
+                       int32_t o_type, dt_stream_t stream);
+
 /* ======================================================================== */
 /* (iii) unfused ggml-op kernels on ggml-shaped descriptors                 */
 /* ======================================================================== */

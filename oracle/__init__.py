@@ -64,6 +64,10 @@ def load():
         "or_quantize_q4_K": (None, [P, c_int64, P]),
         "or_dequant_q4_K_f32": (None, [P, c_int64, P]),
         "or_q4_K_scale_min": (None, [c_int, P, P, P]),
+        "or_linear_f32": (None, [P, c_int64, c_int64, c_int64, P, c_int64, c_int64, P, P, c_int64,
+                                 c_int]),
+        "or_attention_f32": (None, [P, P, P, P, c_int64, c_int64, c_int64, c_int64, P, P, P, P,
+                                    c_float, c_int]),
         "or_max_threads": (c_int, []),
     }
     for name, (res, args) in sigs.items():
@@ -263,6 +267,34 @@ def euler(x, v, dt):
     y = np.empty_like(x)
     load().or_euler_f32(_p(x), _p(v), dt, x.size, _p(y))
     return y
+
+
+# ---- matmul and attention ------------------------------------------------------
+
+def linear(x, w, b=None, threads=0):
+    """x: [..., K]; w: [N, K] (PyTorch Linear weight); b: [N] or None -> [..., N]."""
+    x, w = _f32(x), _f32(w)
+    K = x.shape[-1]
+    N = w.shape[0]
+    assert w.shape[1] == K
+    M = x.size // K
+    y = np.empty(x.shape[:-1] + (N,), dtype=np.float32)
+    bp = _p(_f32(b)) if b is not None else None
+    load().or_linear_f32(_p(x), M, K, K, _p(w), N, K, bp, _p(y), N, threads)
+    return y
+
+
+def attention(q, k, v, scale=None, threads=0):
+    """q: [seq_q, heads, head_dim]; k, v: [seq_kv, heads, head_dim] -> [seq_q, heads, head_dim]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    sq, heads, hd = q.shape
+    skv = k.shape[0]
+    scale = 1.0 / np.sqrt(hd) if scale is None else scale
+    o = np.empty_like(q)
+    st = lambda t: (c_int64 * 2)(t.shape[1] * t.shape[2], t.shape[2])
+    load().or_attention_f32(_p(q), _p(k), _p(v), _p(o), heads, sq, skv, hd, st(q), st(k), st(v),
+                            st(o), float(scale), threads)
+    return o
 
 
 # ---- quantisation ------------------------------------------------------------

@@ -642,3 +642,111 @@ void or_quantize_q4_K(const float *x, int64_t n, uint8_t *dst) {
                 qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
     }
 }
+
+/* ======================================================================== */
+/* matmul and attention                                                     */
+/* ======================================================================== */
+
+typedef double or_v4d __attribute__((vector_size(32)));
+
+static inline or_v4d or_load4d(const float *p) {
+    or_v4d r = {(double)p[0], (double)p[1], (double)p[2], (double)p[3]};
+    return r;
+}
+
+static inline double or_hsum4d(or_v4d a) { return ((a[0] + a[1]) + a[2]) + a[3]; }
+
+/* One dot product in the lane order documented in oracle.h. */
+static double or_dot_lanes(const float *a, const float *b, int64_t K) {
+    or_v4d acc = {0, 0, 0, 0};
+    int64_t k = 0;
+    for (; k + 4 <= K; k += 4) acc += or_load4d(a + k) * or_load4d(b + k);
+    for (; k < K; ++k) acc[k & 3] += (double)a[k] * (double)b[k];
+    return or_hsum4d(acc);
+}
+
+/* ggml_mul_mat(w, x) + ggml_add(b): src/nn/Linear.cpp:17-36.  Blocked 2x4
+ * over (x rows, w rows) so each loaded vector serves several dot products;
+ * every dot product keeps the lane order of or_dot_lanes. */
+void or_linear_f32(const float *x, int64_t M, int64_t K, int64_t x_stride,
+                   const float *w, int64_t N, int64_t w_stride, const float *b,
+                   float *y, int64_t y_stride, int nthreads) {
+    enum { MB = 32, NB = 64 };
+    const int64_t nblk = (N + NB - 1) / NB;
+#pragma omp parallel for schedule(dynamic, 1) OR_OMP_THREADS(nthreads)
+    for (int64_t jb = 0; jb < nblk; ++jb) {
+        const int64_t j0 = jb * NB, j1 = j0 + NB < N ? j0 + NB : N;
+        for (int64_t i0 = 0; i0 < M; i0 += MB) {
+            const int64_t i1 = i0 + MB < M ? i0 + MB : M;
+            for (int64_t i = i0; i < i1; i += 2) {
+                for (int64_t j = j0; j < j1; j += 4) {
+                    if (i + 2 > i1 || j + 4 > j1 || (K & 3)) {
+                        for (int64_t ii = i; ii < i1 && ii < i + 2; ++ii)
+                            for (int64_t jj = j; jj < j1 && jj < j + 4; ++jj)
+                                y[ii * y_stride + jj] =
+                                    (float)or_dot_lanes(x + ii * x_stride, w + jj * w_stride, K);
+                        continue;
+                    }
+                    const float *x0 = x + i * x_stride, *x1 = x0 + x_stride;
+                    const float *w0 = w + j * w_stride, *w1 = w0 + w_stride, *w2 = w1 + w_stride,
+                                *w3 = w2 + w_stride;
+                    or_v4d a00 = {0, 0, 0, 0}, a01 = a00, a02 = a00, a03 = a00;
+                    or_v4d a10 = a00, a11 = a00, a12 = a00, a13 = a00;
+                    for (int64_t k = 0; k < K; k += 4) {
+                        const or_v4d p0 = or_load4d(x0 + k), p1 = or_load4d(x1 + k);
+                        const or_v4d q0 = or_load4d(w0 + k), q1 = or_load4d(w1 + k),
+                                     q2 = or_load4d(w2 + k), q3 = or_load4d(w3 + k);
+                        a00 += p0 * q0; a01 += p0 * q1; a02 += p0 * q2; a03 += p0 * q3;
+                        a10 += p1 * q0; a11 += p1 * q1; a12 += p1 * q2; a13 += p1 * q3;
+                    }
+                    float *y0 = y + i * y_stride + j, *y1 = y0 + y_stride;
+                    y0[0] = (float)or_hsum4d(a00); y0[1] = (float)or_hsum4d(a01);
+                    y0[2] = (float)or_hsum4d(a02); y0[3] = (float)or_hsum4d(a03);
+                    y1[0] = (float)or_hsum4d(a10); y1[1] = (float)or_hsum4d(a11);
+                    y1[2] = (float)or_hsum4d(a12); y1[3] = (float)or_hsum4d(a13);
+                }
+            }
+        }
+        if (b)
+            for (int64_t i = 0; i < M; ++i)
+                for (int64_t j = j0; j < j1; ++j) y[i * y_stride + j] = y[i * y_stride + j] + b[j];
+    }
+}
+
+/* ggml_flash_attn_ext without mask: src/nn/attention/FlashAttentionOp.cpp:84-94. */
+void or_attention_f32(const float *q, const float *k, const float *v, float *o,
+                      int64_t heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                      const int64_t q_str[2], const int64_t k_str[2], const int64_t v_str[2],
+                      const int64_t o_str[2], float scale, int nthreads) {
+    const int64_t total = heads * seq_q;
+#pragma omp parallel OR_OMP_THREADS(nthreads)
+    {
+        double *sc = (double *)malloc(sizeof(double) * (size_t)(seq_kv > 0 ? seq_kv : 1));
+        double *acc = (double *)malloc(sizeof(double) * (size_t)(head_dim > 0 ? head_dim : 1));
+#pragma omp for schedule(static)
+        for (int64_t t = 0; t < total; ++t) {
+            const int64_t h = t / seq_q, s = t % seq_q;
+            const float *qr = q + s * q_str[0] + h * q_str[1];
+            double mx = -INFINITY;
+            for (int64_t j = 0; j < seq_kv; ++j) {
+                sc[j] = or_dot_lanes(qr, k + j * k_str[0] + h * k_str[1], head_dim) * (double)scale;
+                if (sc[j] > mx) mx = sc[j];
+            }
+            double sum = 0.0;
+            for (int64_t j = 0; j < seq_kv; ++j) {
+                sc[j] = exp(sc[j] - mx);
+                sum += sc[j];
+            }
+            for (int64_t d = 0; d < head_dim; ++d) acc[d] = 0.0;
+            for (int64_t j = 0; j < seq_kv; ++j) {
+                const float *vr = v + j * v_str[0] + h * v_str[1];
+                const double p = sc[j];
+                for (int64_t d = 0; d < head_dim; ++d) acc[d] += p * (double)vr[d];
+            }
+            float *orow = o + s * o_str[0] + h * o_str[1];
+            for (int64_t d = 0; d < head_dim; ++d) orow[d] = (float)(acc[d] / sum);
+        }
+        free(sc);
+        free(acc);
+    }
+}

@@ -115,6 +115,26 @@ void or_dequant_q4_K_f32(const uint8_t *src, int64_t n, float *y);
 void or_q4_K_scale_min(int j, const uint8_t *scales12, uint8_t *sc, uint8_t *m);
 
 /* ---- small helpers used by the timed CPU baseline ----------------------- */
+/* ---- matmul and attention (fp32) --------------------------------------- */
+/* y[m][n] = sum_k x[m][k] * w[n][k], then + b[n] when b is given: ggml_mul_mat(w, x)
+ * followed by ggml_add, as Linear::forward emits them (src/nn/Linear.cpp:17-36).
+ * Each dot product accumulates in double over 4 interleaved lanes (lane l
+ * takes k = l mod 4), the lanes are summed in order, and the sum is rounded
+ * once to fp32.  Strides are in elements. */
+void or_linear_f32(const float *x, int64_t M, int64_t K, int64_t x_stride,
+                   const float *w, int64_t N, int64_t w_stride, const float *b,
+                   float *y, int64_t y_stride, int nthreads);
+
+/* Unmasked softmax attention, ggml_flash_attn_ext as FlashAttentionOp::operator()
+ * calls it (src/nn/attention/FlashAttentionOp.cpp:84-94): for each head h and
+ * query s, o = sum_j softmax_j(scale * <q, k_j>) v_j with scores, exponentials
+ * and sums in double (max-subtracted), rounded once to fp32.  Element (s, h, d)
+ * of q is q[s*q_str[0] + h*q_str[1] + d]; likewise k, v (seq_kv tokens), o. */
+void or_attention_f32(const float *q, const float *k, const float *v, float *o,
+                      int64_t heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                      const int64_t q_str[2], const int64_t k_str[2], const int64_t v_str[2],
+                      const int64_t o_str[2], float scale, int nthreads);
+
 int or_max_threads(void);
 
 #ifdef __cplusplus

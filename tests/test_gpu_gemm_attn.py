@@ -1,0 +1,199 @@
+"""GPU parity of the step-time kernels (Linear GEMM, attention) and the Q8_0
+quantiser against the oracle, through the C ABI.
+
+Bars: the GEMM with fp32 output is held to |d| <= 1e-5 * max(|ref|, 1) (its
+products of bf16 inputs are exact in fp32 and only the accumulation order
+differs from the oracle's); bf16 outputs to the bf16 bar (rel L2 <= 1e-2,
+cos >= 0.9999) plus one bf16 ulp for a single rounding.  Attention rounds its
+softmax weights to bf16 before the PV product, so both of its output types are
+held to the bf16 bar.  The quantiser is bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import dit_hip
+from conftest import assert_bf16, assert_fp32, bf16_metrics
+from test_gpu_fused import SEED, as_input, check, dev_tensor, host
+
+pytestmark = pytest.mark.gpu
+
+
+# ---------------------------------------------------------------- quantiser --
+def _quant_rows(orc):
+    x = orc.randn(SEED + 200, (61, 3072), std=0.02)
+    x[0] = 0.0                                            # d = 0 -> id = 0
+    x[1] = orc.randn(SEED + 201, (3072,), std=1e-6)       # subnormal fp16 d
+    x[2] = orc.randn(SEED + 202, (3072,), std=300.0)
+    # exact halves: amax 127 -> d = 1, so x * id = x and roundf rounds away from 0
+    x[3] = np.tile(np.array([127.0, 0.5, 1.5, -2.5, -0.5, 2.5, 126.5, -126.5], np.float32), 384)
+    return x
+
+
+def test_quantize_q8_0_bit_exact(orc, dev):
+    print("quantize_q8_0 61x3072", flush=True)
+    x = _quant_rows(orc)
+    got = dit_hip.quantize_q8_0(dev_tensor(x, torch.float32))
+    torch.cuda.synchronize()
+    want = orc.quantize(x, 8).reshape(x.shape[0], -1)
+    g = got.cpu().numpy()
+    assert g.shape == want.shape
+    bad = np.argwhere(g != want)
+    assert bad.size == 0, f"{len(bad)} bytes differ, first at {bad[0]}"
+
+
+def test_quantize_q8_0_strided_rows(orc, dev):
+    x = orc.randn(SEED + 203, (33, 1024), std=0.02)
+    big = dev_tensor(np.concatenate([x, np.zeros((33, 64), np.float32)], axis=1), torch.float32)
+    out = torch.zeros((33, 1024 // 32 * 34 + 6), dtype=torch.uint8, device="cuda")
+    dit_hip.quantize_q8_0(big[:, :1024], out=out)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.array_equal(o[:, :1088], orc.quantize(x, 8).reshape(33, -1))
+    assert not o[:, 1088:].any(), "wrote past the row"
+
+
+# --------------------------------------------------------------------- GEMM --
+GEMM_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192)]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_gemm(orc, dev, M, N, K, out_dtype):
+    print(f"gemm M={M} N={N} K={K} {out_dtype}", flush=True)
+    a = orc.randn(SEED + 210, (M, K))
+    b = orc.randn(SEED + 211, (N, K), std=0.02)
+    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref = orc.linear(orc.round_bf16(a), orc.round_bf16(b))
+    check(host(y), ref, out_dtype, f"gemm {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_strided_bias_addend(orc, dev, out_dtype):
+    M, N, K = 300, 384, 512
+    big_a = orc.randn(SEED + 212, (M, K + 128))
+    b = orc.randn(SEED + 213, (N, K), std=0.02)
+    bias = orc.randn(SEED + 214, (N,), std=0.1)
+    add = orc.randn(SEED + 215, (M, N + 8))
+    ad = dev_tensor(big_a, torch.bfloat16)[:, 64:64 + K]           # lda = K + 128
+    addd = dev_tensor(add, out_dtype)[:, :N]                        # ldd = N + 8
+    out = torch.zeros((M, N + 16), dtype=out_dtype, device="cuda")
+    dit_hip.gemm(ad, dev_tensor(b, torch.bfloat16), bias=dev_tensor(bias, torch.float32),
+                 addend=addd, out=out[:, :N])
+    torch.cuda.synchronize()
+    lin = orc.linear(orc.round_bf16(big_a[:, 64:64 + K]), orc.round_bf16(b), bias)
+    ref = lin + as_input(add[:, :N], out_dtype)
+    got = host(out)
+    check(got[:, :N], ref, out_dtype, "gemm strided+bias+addend")
+    assert not got[:, N:].any(), "wrote past N"
+
+
+def test_gemm_in_place_addend(orc, dev):
+    """C aliasing the addend: y += x W^T, the accumulate form of the
+    attention-plus-MLP output projection."""
+    M, N, K = 200, 256, 256
+    a, b = orc.randn(SEED + 216, (M, K)), orc.randn(SEED + 217, (N, K), std=0.02)
+    c0 = orc.randn(SEED + 218, (M, N))
+    c = dev_tensor(c0, torch.float32)
+    dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), addend=c, out=c)
+    torch.cuda.synchronize()
+    assert_fp32(host(c), orc.linear(orc.round_bf16(a), orc.round_bf16(b)) + c0, what="gemm in-place")
+
+
+def test_gemm_large_sampled_rows(orc, dev):
+    """4608 x 3072 x 3072 (a Flux2 block's attention projection); 96 rows
+    spread over all 36 row tiles are checked against the oracle."""
+    M, N, K = 4608, 3072, 3072
+    a = orc.randn(SEED + 219, (M, K))
+    b = orc.randn(SEED + 220, (N, K), std=0.02)
+    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, M, 53), [M - 1]]))
+    ref = orc.linear(orc.round_bf16(a[rows]), orc.round_bf16(b))
+    assert_fp32(host(y)[rows], ref, what="gemm 4608x3072x3072")
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    a = torch.zeros((64, 48), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        dit_hip.gemm(a, a)
+    z = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
+    assert dit_hip.gemm(z, w).shape == (0, 8)
+
+
+# ---------------------------------------------------------------- attention --
+def _attn_ref(orc, q, k, v, scale=None):
+    """q [B, Sq, H, D] -> oracle attention per batch on the bf16-rounded values."""
+    return np.stack([orc.attention(orc.round_bf16(q[i]), orc.round_bf16(k[i]), orc.round_bf16(v[i]), scale)
+                     for i in range(q.shape[0])])
+
+
+ATTN_SHAPES = [(1, 300, 300, 3), (2, 128, 64, 2), (1, 77, 500, 1), (1, 64, 1, 2), (1, 1, 129, 4)]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,Sq,Skv,H", ATTN_SHAPES)
+def test_flash_attn(orc, dev, B, Sq, Skv, H, out_dtype):
+    print(f"attn B={B} Sq={Sq} Skv={Skv} H={H} {out_dtype}", flush=True)
+    q = orc.randn(SEED + 230, (B, Sq, H, 128))
+    k = orc.randn(SEED + 231, (B, Skv, H, 128))
+    v = orc.randn(SEED + 232, (B, Skv, H, 128))
+    o = dit_hip.flash_attn(dev_tensor(q, torch.bfloat16), dev_tensor(k, torch.bfloat16),
+                           dev_tensor(v, torch.bfloat16), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref = _attn_ref(orc, q, k, v)
+    rel, cos = bf16_metrics(host(o), ref)
+    print(f"  rel_l2={rel:.2e} cos={cos:.7f}", flush=True)
+    assert_bf16(host(o), ref, f"attn {B}x{Sq}x{Skv}x{H}")
+
+
+def test_flash_attn_fused_qkv_views(orc, dev):
+    """q, k, v as column views of one [S, 3*H*128] projection output (token
+    stride 3*H*128, head stride 128), output written into a wider buffer."""
+    S, H = 257, 3
+    qkv = orc.randn(SEED + 233, (S, 3 * H * 128))
+    d = dev_tensor(qkv, torch.bfloat16).view(1, S, 3, H, 128)
+    out = torch.zeros((1, S, H + 1, 128), dtype=torch.bfloat16, device="cuda")
+    dit_hip.flash_attn(d[:, :, 0], d[:, :, 1], d[:, :, 2], out=out[:, :, :H])
+    torch.cuda.synchronize()
+    r = qkv.reshape(1, S, 3, H, 128)
+    ref = _attn_ref(orc, r[:, :, 0], r[:, :, 1], r[:, :, 2])
+    got = host(out)
+    assert_bf16(got[:, :, :H], ref, "attn fused-qkv views")
+    assert not got[:, :, H].any(), "wrote outside the heads"
+
+
+def test_flash_attn_invariants(orc, dev):
+    """Constant V rows give that constant back; scale 0 gives the mean of V."""
+    S, H = 200, 2
+    q = dev_tensor(orc.randn(SEED + 234, (1, S, H, 128)), torch.bfloat16)
+    k = dev_tensor(orc.randn(SEED + 235, (1, S, H, 128)), torch.bfloat16)
+    c = np.linspace(-2, 2, 128, dtype=np.float32)
+    v_const = dev_tensor(np.broadcast_to(c, (1, S, H, 128)).copy(), torch.bfloat16)
+    o = dit_hip.flash_attn(q, k, v_const, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    cb = as_input(c, torch.bfloat16)
+    # sum_j p_j * c with sum_j p_j = 1 up to the bf16 rounding of each p_j
+    assert np.allclose(host(o), np.broadcast_to(cb, (1, S, H, 128)), rtol=4e-3, atol=4e-3)
+    v = orc.randn(SEED + 236, (1, S, H, 128))
+    o0 = dit_hip.flash_attn(q, k, dev_tensor(v, torch.bfloat16), scale=0.0, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    mean = as_input(v, torch.bfloat16).mean(axis=1, keepdims=True)
+    assert np.allclose(host(o0), np.broadcast_to(mean, o0.shape), rtol=1e-5, atol=1e-5)
+
+
+def test_flash_attn_flux2_shape_sampled(orc, dev):
+    """4608 tokens x 24 heads (a 1024^2 Flux2 step); two heads x 160 queries
+    are checked against the oracle over all 4608 keys."""
+    S, H = 4608, 24
+    q = orc.randn(SEED + 237, (1, S, H, 128))
+    k = orc.randn(SEED + 238, (1, S, H, 128))
+    v = orc.randn(SEED + 239, (1, S, H, 128))
+    o = host(dit_hip.flash_attn(dev_tensor(q, torch.bfloat16), dev_tensor(k, torch.bfloat16),
+                                dev_tensor(v, torch.bfloat16)))
+    rows = np.arange(0, S, 29)
+    for h in (0, 17):
+        ref = orc.attention(orc.round_bf16(q[0, rows, h:h + 1]), orc.round_bf16(k[0, :, h:h + 1]),
+                            orc.round_bf16(v[0, :, h:h + 1]))
+        assert_bf16(o[0, rows, h:h + 1], ref, f"attn 4608x24 head {h}")

@@ -249,3 +249,52 @@ def test_quantizer_round_trip(orc, qtype, qk):
         # codes reach +-127 in every block (amax maps to the top code)
         q = b.reshape(-1, 34)[:, 2:].view(np.int8)
         assert np.all(np.abs(q).max(1) == 127)
+
+
+# ---- matmul and attention ---------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (37, 45, 130), (64, 64, 256), (5, 9, 3)])
+def test_linear_vs_torch_float64(orc, M, N, K):
+    """Blocked 2x4 path, scalar tails and K % 4 != 0 all against float64."""
+    x = orc.randn(orc.tensor_seed(50), (M, K))
+    w = orc.randn(orc.tensor_seed(51), (N, K), std=0.02)
+    b = orc.randn(orc.tensor_seed(52), (N,))
+    ref = torch.from_numpy(x).double() @ torch.from_numpy(w).double().T
+    assert_fp32(orc.linear(x, w), ref.numpy(), tol=1e-6, what="linear")
+    assert_fp32(orc.linear(x, w, b), (ref + torch.from_numpy(b).double()).numpy(), tol=1e-6,
+                what="linear+bias")
+
+
+def test_linear_operand_roles(orc):
+    """y = x W^T, not x W or W x: a rectangular identity-like W picks columns."""
+    x = orc.randn(orc.tensor_seed(53), (6, 8))
+    w = np.zeros((3, 8), np.float32)
+    w[0, 2] = w[1, 7] = w[2, 0] = 1.0
+    assert np.array_equal(orc.linear(x, w), x[:, [2, 7, 0]])
+
+
+@pytest.mark.parametrize("Sq,Skv,H,D", [(1, 1, 1, 4), (7, 5, 2, 16), (70, 50, 3, 128)])
+def test_attention_vs_torch_sdpa(orc, Sq, Skv, H, D):
+    q = orc.randn(orc.tensor_seed(54), (Sq, H, D))
+    k = orc.randn(orc.tensor_seed(55), (Skv, H, D))
+    v = orc.randn(orc.tensor_seed(56), (Skv, H, D))
+    t = lambda a: torch.from_numpy(a).double().transpose(0, 1)
+    ref = torch.nn.functional.scaled_dot_product_attention(t(q), t(k), t(v)).transpose(0, 1).numpy()
+    assert_fp32(orc.attention(q, k, v), ref, tol=1e-6, what="attention")
+
+
+def test_attention_closed_forms(orc):
+    """One key returns its value row; scale 0 averages V; a dominant score
+    selects its key (checks which operand is softmaxed over which axis)."""
+    q = orc.randn(orc.tensor_seed(57), (9, 2, 8))
+    v1 = orc.randn(orc.tensor_seed(58), (1, 2, 8))
+    k1 = orc.randn(orc.tensor_seed(59), (1, 2, 8))
+    assert np.allclose(orc.attention(q, k1, v1), np.broadcast_to(v1, q.shape), atol=1e-7)
+    k = orc.randn(orc.tensor_seed(60), (11, 2, 8))
+    v = orc.randn(orc.tensor_seed(61), (11, 2, 8))
+    assert np.allclose(orc.attention(q, k, v, scale=0.0), np.broadcast_to(v.mean(0), q.shape), atol=1e-6)
+    kd = np.zeros((11, 2, 8), np.float32)
+    kd[4] = 1.0
+    qd = np.ones((3, 2, 8), np.float32)
+    out = orc.attention(qd, kd, v, scale=100.0)
+    assert np.allclose(out, np.broadcast_to(v[4], out.shape), atol=1e-6)
