@@ -9,17 +9,21 @@
 // data.  Parameters are passed as --param-<name>, outputs as --out[-<name>].
 // One JSON line with graph statistics is printed on success; errors print a
 // message on stderr and exit non-zero.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <iostream>
 #include <map>
+#include <random>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
-#include "modules.hpp"
+#include "flux2.hpp"
 
 using namespace dit::host;
 
@@ -50,6 +54,31 @@ Blob read_blob(const std::string& path) {
     f.read((char*)b.bytes.data(), (std::streamsize)b.bytes.size());
     if (!f) throw std::runtime_error("truncated tensor file " + path);
     return b;
+}
+
+uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Blob bytes as `type` (F32 -> BF16 by RNE; same type passes through).
+std::vector<uint8_t> convert_blob(const Blob& b, int32_t type) {
+    if (b.type == type) return b.bytes;
+    if (b.type == DT_TYPE_F32 && type == DT_TYPE_BF16) {
+        const size_t n = b.bytes.size() / 4;
+        std::vector<uint8_t> out(n * 2);
+        for (size_t i = 0; i < n; ++i) {
+            float f;
+            std::memcpy(&f, b.bytes.data() + 4 * i, 4);
+            const uint16_t h = f32_to_bf16(f);
+            std::memcpy(out.data() + 2 * i, &h, 2);
+        }
+        return out;
+    }
+    throw std::runtime_error("cannot convert tensor file type " + std::to_string(b.type) + " to " +
+                             std::to_string(type));
 }
 
 void write_blob(const std::string& path, int32_t type, const Tensor::Shape& shape,
@@ -103,7 +132,7 @@ Args parse(int argc, char** argv) {
 
 class Session {
 public:
-    explicit Session(const Args& a) : args(a), rt(0), scope(rt) {}
+    explicit Session(const Args& a) : args(a), plan_only(a.flag("plan-only", false)), rt(plan_only ? -1 : 0), scope(rt) {}
 
     Tensor input(const std::string& key) {
         Blob b = read_blob(args.str(key));
@@ -117,12 +146,46 @@ public:
         if (b.type != DT_TYPE_F32) throw std::runtime_error("parameters are F32");
         rt.bind(*p, b.bytes.data(), b.bytes.size());
     }
+    // An input converted to `type` on the host (e.g. F32 files for BF16 graphs).
+    Tensor input_as(const std::string& key, int32_t type) {
+        Blob b = read_blob(args.str(key));
+        Tensor t = Tensor::empty(b.shape, type);
+        rt.set_input(*t);
+        auto bytes = convert_blob(b, type);
+        rt.bind(*t, bytes.data(), bytes.size());
+        return t;
+    }
     void output(Tensor t, const std::string& key) {
         if (!t.is_contiguous()) t = t.contiguous();
         rt.set_output(*t);
         outs.push_back({t, args.str(key)});
     }
+    // Every parameter of `m` from DIR/<dotted name>.dtb, converted to the
+    // parameter's type.
+    void load_weights(const Module& m, const std::string& dir) {
+        std::vector<std::pair<std::string, Tensor>> ps;
+        m.named_parameters(ps);
+        for (auto& p : ps) {
+            Blob b = read_blob(dir + "/" + p.first + ".dtb");
+            if (b.shape != p.second.shape()) throw std::runtime_error("shape mismatch for " + p.first);
+            auto bytes = convert_blob(b, p.second.dtype());
+            rt.bind(*p.second, bytes.data(), bytes.size());
+        }
+    }
+    // --plan-only: record and plan the graph without a device.
+    void print_plan() {
+        const ComputeStats& s = rt.plan();
+        std::printf("{\"command\": \"%s\", \"plan_only\": true, \"nodes\": %d, \"fused_nodes\": %d, "
+                    "\"mul_mat_nodes\": %d, \"attention_nodes\": %d, \"arena_bytes\": %zu, "
+                    "\"naive_bytes\": %zu}\n",
+                    args.command.c_str(), s.nodes, s.fused_nodes, s.mul_mat_nodes, s.attention_nodes,
+                    s.arena_bytes, s.naive_bytes);
+    }
     void run() {
+        if (plan_only) {
+            print_plan();
+            return;
+        }
         rt.compute();
         for (auto& o : outs) {
             std::vector<uint8_t> host(HipRuntime::nbytes(*o.first));
@@ -136,10 +199,206 @@ public:
     }
 
     const Args& args;
+    bool plan_only;
     HipRuntime rt;
     RuntimeScope scope;
     std::vector<std::pair<Tensor, std::string>> outs;
 };
+
+// ---- Flux2Transformer2DModel: one denoising step --------------------------
+//
+// Weights come from --weights DIR (one .dtb per parameter) or, with
+// --random-weights SEED, are generated on the device: every Linear weight is
+// drawn N(0, 0.02) in fp32, quantised to Q8_0 and dequantised once to the
+// BF16 copy the GEMMs read (the Q8_0 bytes are what a GGUF file would hold);
+// RMSNorm weights are N(1, 0.02).  Inputs come from files or, with
+// --random-inputs SEED, are drawn N(0, 1) (latents, text) with the pipeline's
+// position ids (Flux2KleinPipeline.cpp:27-72): text [0, 0, 0, l], image
+// [0, y, x, 0] on a square grid.  Inputs and weights are device-resident
+// before the first step; --warmup W and --steps K run the recorded graph W + K
+// times and report the per-step wall time of the last K.
+
+struct DeviceBuffers {
+    dt_backend* be = nullptr;
+    std::vector<void*> ptrs;
+    void* alloc(size_t bytes) {
+        void* p = nullptr;
+        check(dt_buffer_alloc(be, bytes ? bytes : 1, &p), "dt_buffer_alloc");
+        ptrs.push_back(p);
+        return p;
+    }
+    ~DeviceBuffers() {
+        for (void* p : ptrs) dt_buffer_free(be, p);
+    }
+};
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffers& bufs, size_t* bf16_bytes,
+                    size_t* q8_bytes, size_t* n_params) {
+    std::vector<std::pair<std::string, Tensor>> ps;
+    m.named_parameters(ps);
+    size_t total = 0, max_n = 0;
+    for (auto& p : ps)
+        if (p.second.dtype() == DT_TYPE_BF16) {
+            total += align256((size_t)p.second.numel() * 2);
+            max_n = std::max(max_n, (size_t)p.second.numel());
+        }
+    char* big = (char*)bufs.alloc(total);
+    float* f32 = (float*)bufs.alloc(max_n * 4);
+    void* q8 = bufs.alloc(max_n / 32 * 34 + 256);
+    std::mt19937_64 gen(seed);
+    std::normal_distribution<float> nd(1.0f, 0.02f);
+    size_t off = 0, idx = 0;
+    *bf16_bytes = *q8_bytes = *n_params = 0;
+    for (auto& p : ps) {
+        const Tensor& t = p.second;
+        *n_params += (size_t)t.numel();
+        ++idx;
+        if (t.dtype() == DT_TYPE_BF16) {
+            if (t.ndim() != 2 || t.shape()[1] % 32) throw std::runtime_error("random weight layout: " + p.first);
+            const int64_t rows = t.shape()[0], cols = t.shape()[1], rb = cols / 32 * 34;
+            check(dt_fill_randn(f32, rows * cols, seed * 1000003ull + idx, 0.0f, 0.02f, nullptr), "dt_fill_randn");
+            check(dt_quantize_q8_0(f32, rows, cols, cols, q8, rb, nullptr), "dt_quantize_q8_0");
+            check(dt_dequant(q8, DT_TYPE_Q8_0, rows, cols, rb, big + off, cols, DT_TYPE_BF16, nullptr), "dt_dequant");
+            rt.bind_device(*t, big + off);
+            off += align256((size_t)t.numel() * 2);
+            *bf16_bytes += (size_t)t.numel() * 2;
+            *q8_bytes += (size_t)(rows * rb);
+        } else if (t.dtype() == DT_TYPE_F32) {
+            std::vector<float> h((size_t)t.numel());
+            for (float& v : h) v = nd(gen);  // RMSNorm weights
+            rt.bind(*t, h.data(), h.size() * 4);
+        } else {
+            throw std::runtime_error("random weights: unexpected parameter type for " + p.first);
+        }
+    }
+}
+
+// Upload host bytes once into a device buffer that `leaf` keeps.
+void resident_input(HipRuntime& rt, DeviceBuffers& bufs, const Tensor& leaf, const void* host, size_t bytes) {
+    void* d = bufs.alloc(bytes);
+    rt.bind_device(*leaf, d);
+    check(dt_tensor_set(*leaf, host, 0, bytes, nullptr), "dt_tensor_set");
+}
+
+void run_model(Session& s, const Args& a) {
+    Flux2Config cfg;
+    cfg.num_layers = a.i64("num_layers", 5);
+    cfg.num_single_layers = a.i64("num_single_layers", 20);
+    cfg.num_attention_heads = a.i64("num_attention_heads", 24);
+    cfg.attention_head_dim = a.i64("attention_head_dim", 128);
+    cfg.in_channels = cfg.out_channels = a.i64("in_channels", 128);
+    cfg.joint_attention_dim = a.i64("joint_attention_dim", 2560);
+    cfg.mlp_ratio = a.f32("mlp_ratio", 3.0f);
+    cfg.rope_theta = a.i64("rope_theta", 2000);
+    cfg.guidance_embeds = a.flag("guidance_embeds", false);
+    if (a.has("axes_dims_rope")) cfg.axes_dims_rope = a.list("axes_dims_rope");
+    const int64_t n_img = a.i64("img_tokens", 4096), n_txt = a.i64("txt_tokens", 512);
+    const int steps = (int)a.i64("steps", 1), warmup = (int)a.i64("warmup", 0);
+
+    HipRuntime& rt = s.rt;
+    DeviceBuffers bufs;
+    bufs.be = rt.backend();
+    LinearWeightType wt(DT_TYPE_BF16);
+    Flux2Transformer2DModel model(cfg);
+
+    Tensor hidden = Tensor::empty({1, n_img, cfg.in_channels}, DT_TYPE_BF16);
+    Tensor text = Tensor::empty({1, n_txt, cfg.joint_attention_dim}, DT_TYPE_BF16);
+    Tensor timestep = Tensor::empty({1}, DT_TYPE_F32);
+    Tensor img_ids = Tensor::empty({n_img, 4}, DT_TYPE_I32);
+    Tensor txt_ids = Tensor::empty({n_txt, 4}, DT_TYPE_I32);
+    for (const Tensor* t : {&hidden, &text, &timestep, &img_ids, &txt_ids}) rt.set_input(**t);
+
+    size_t bf16_bytes = 0, q8_bytes = 0, n_params = 0;
+    if (s.plan_only) {
+        std::vector<std::pair<std::string, Tensor>> ps;
+        model.named_parameters(ps);
+        for (auto& p : ps) n_params += (size_t)p.second.numel();
+        Tensor out = model.forward(hidden, text, timestep, img_ids, txt_ids);
+        rt.set_output(*out);
+        const ComputeStats& st = rt.plan();
+        std::printf("{\"command\": \"Flux2Transformer2DModel\", \"plan_only\": true, \"nodes\": %d, "
+                    "\"fused_nodes\": %d, \"mul_mat_nodes\": %d, \"attention_nodes\": %d, "
+                    "\"arena_bytes\": %zu, \"naive_bytes\": %zu, \"params\": %zu}\n",
+                    st.nodes, st.fused_nodes, st.mul_mat_nodes, st.attention_nodes, st.arena_bytes,
+                    st.naive_bytes, n_params);
+        return;
+    }
+    if (a.has("random-weights")) {
+        random_weights(rt, model, (uint64_t)a.i64("random-weights"), bufs, &bf16_bytes, &q8_bytes, &n_params);
+    } else {
+        s.load_weights(model, a.str("weights"));
+    }
+
+    if (a.has("random-inputs")) {
+        std::mt19937_64 gen((uint64_t)a.i64("random-inputs"));
+        std::normal_distribution<float> nd(0.0f, 1.0f);
+        auto bf16_normals = [&](int64_t n) {
+            std::vector<uint16_t> v((size_t)n);
+            for (auto& x : v) x = f32_to_bf16(nd(gen));
+            return v;
+        };
+        auto h = bf16_normals(hidden.numel()), e = bf16_normals(text.numel());
+        resident_input(rt, bufs, hidden, h.data(), h.size() * 2);
+        resident_input(rt, bufs, text, e.data(), e.size() * 2);
+        const float ts = a.f32("timestep", 0.5f);
+        resident_input(rt, bufs, timestep, &ts, 4);
+        const int64_t side = (int64_t)std::llround(std::sqrt((double)n_img));
+        if (side * side != n_img) throw std::runtime_error("--img_tokens must be a square for random inputs");
+        std::vector<int32_t> ii((size_t)n_img * 4, 0), ti((size_t)n_txt * 4, 0);
+        for (int64_t y = 0; y < side; ++y)
+            for (int64_t x = 0; x < side; ++x) {
+                ii[(size_t)(y * side + x) * 4 + 1] = (int32_t)y;
+                ii[(size_t)(y * side + x) * 4 + 2] = (int32_t)x;
+            }
+        for (int64_t l = 0; l < n_txt; ++l) ti[(size_t)l * 4 + 3] = (int32_t)l;
+        resident_input(rt, bufs, img_ids, ii.data(), ii.size() * 4);
+        resident_input(rt, bufs, txt_ids, ti.data(), ti.size() * 4);
+    } else {
+        auto bind_file = [&](const Tensor& t, const std::string& key) {
+            Blob b = read_blob(a.str(key));
+            auto bytes = convert_blob(b, t.dtype());
+            if (b.shape != t.shape()) throw std::runtime_error("input shape mismatch for " + key);
+            rt.bind(*t, bytes.data(), bytes.size());
+        };
+        bind_file(hidden, "hidden_states");
+        bind_file(text, "encoder_hidden_states");
+        bind_file(timestep, "timestep");
+        bind_file(img_ids, "img_ids");
+        bind_file(txt_ids, "txt_ids");
+    }
+
+    Tensor out = model.forward(hidden, text, timestep, img_ids, txt_ids);
+    if (!out.is_contiguous()) out = out.contiguous();
+    rt.set_output(*out);
+
+    std::vector<double> ms;
+    for (int i = 0; i < warmup + steps; ++i) {
+        const auto t0 = std::chrono::steady_clock::now();
+        rt.compute();
+        const auto t1 = std::chrono::steady_clock::now();
+        if (i >= warmup) ms.push_back(std::chrono::duration<double, std::milli>(t1 - t0).count());
+    }
+    if (a.has("out")) {
+        std::vector<uint8_t> host(HipRuntime::nbytes(*out));
+        rt.read(*out, host.data(), host.size());
+        write_blob(a.str("out"), out.dtype(), out.shape(), host);
+    }
+    std::vector<double> sorted = ms;
+    std::sort(sorted.begin(), sorted.end());
+    double mean = 0;
+    for (double v : ms) mean += v;
+    mean /= std::max<size_t>(ms.size(), 1);
+    const ComputeStats& st = rt.stats();
+    std::printf("{\"command\": \"Flux2Transformer2DModel\", \"steps\": %d, \"warmup\": %d, "
+                "\"ms_per_step_median\": %.4f, \"ms_per_step_mean\": %.4f, \"ms_per_step_min\": %.4f, "
+                "\"nodes\": %d, \"kernels\": %d, \"fused_nodes\": %d, \"arena_bytes\": %zu, "
+                "\"params\": %zu, \"bf16_weight_bytes\": %zu, \"q8_0_weight_bytes\": %zu}\n",
+                steps, warmup, sorted.empty() ? 0.0 : sorted[sorted.size() / 2], mean,
+                sorted.empty() ? 0.0 : sorted.front(), st.nodes, st.kernels, st.fused_nodes, st.arena_bytes,
+                n_params, bf16_bytes, q8_bytes);
+}
 
 void run(const Args& a) {
     Session s(a);
@@ -223,6 +482,34 @@ void run(const Args& a) {
         Tensor q = Tensor::cat({nt.forward(qt.unflatten(-1, {heads, -1})),
                                 ni.forward(qi.unflatten(-1, {heads, -1}))}, 1);
         s.output(pe.forward(q, pos), "out");
+    } else if (c == "Flux2SingleTransformerBlock") {
+        // Full block (Flux2SingleTransformerBlock.hpp:36-72) with weights from --weights DIR.
+        const int32_t act = a.str("dtype", "bf16") == "bf16" ? DT_TYPE_BF16 : DT_TYPE_F32;
+        LinearWeightType wt(act == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32);
+        Tensor x = s.input_as("hidden_states", act);
+        Tensor mod = s.input("temb_mod"), pos = s.input("position_ids");
+        const int64_t dim = x.shape().back(), heads = a.i64("heads");
+        Flux2SingleTransformerBlock block(dim, heads, dim / heads, a.f32("mlp_ratio", 3.0f), a.f32("eps", 1e-6f),
+                                          false);
+        s.load_weights(block, a.str("weights"));
+        Flux2PosEmbed pe(a.i64("theta"), a.list("axes_dim"));
+        s.output(block.forward(x, mod, {&pe, pos}), "out");
+    } else if (c == "Flux2TransformerBlock") {
+        // Double-stream block (Flux2TransformerBlock.hpp:47-116) with weights from --weights DIR.
+        const int32_t act = a.str("dtype", "bf16") == "bf16" ? DT_TYPE_BF16 : DT_TYPE_F32;
+        LinearWeightType wt(act == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32);
+        Tensor x = s.input_as("hidden_states", act), e = s.input_as("encoder_hidden_states", act);
+        Tensor mi = s.input("temb_mod_img"), mt = s.input("temb_mod_txt"), pos = s.input("position_ids");
+        const int64_t dim = x.shape().back(), heads = a.i64("heads");
+        Flux2TransformerBlock block(dim, heads, dim / heads, a.f32("mlp_ratio", 3.0f), a.f32("eps", 1e-6f), false);
+        s.load_weights(block, a.str("weights"));
+        Flux2PosEmbed pe(a.i64("theta"), a.list("axes_dim"));
+        auto [enc, hid] = block.forward(x, e, mi, mt, {&pe, pos});
+        s.output(enc, "out-encoder");
+        s.output(hid, "out-hidden");
+    } else if (c == "Flux2Transformer2DModel") {
+        run_model(s, a);
+        return;
     } else {
         throw std::runtime_error("unknown command " + c);
     }

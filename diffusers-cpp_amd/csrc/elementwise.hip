@@ -221,3 +221,46 @@ extern "C" int dt_euler_step(const void* x, const void* v, float dt, void* y, in
                            st, (const dit::bf16*)x, (const dit::bf16*)v, dt, (dit::bf16*)y, n);
     return dit::check_launch("dt_euler_step");
 }
+
+// ---------------------------------------------------------------------------
+// Synthetic N(mean, std^2) data for benchmark weights: pair p of outputs comes
+// from splitmix64(seed + p * 0x9E3779B97F4A7C15) through the Box-Muller
+// transform (u1 = (hi32 + 1) / 2^32 in (0, 1], u2 = lo32 / 2^32).
+// Deterministic for a seed; no statistical claims beyond that.
+// ---------------------------------------------------------------------------
+namespace dit {
+namespace {
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void randn_kernel(float* __restrict__ y, int64_t n, uint64_t seed, float mean,
+                                                    float stdv) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (2 * p >= n) return;
+    const uint64_t z = splitmix64(seed + (uint64_t)p * 0x9E3779B97F4A7C15ull);
+    const float u1 = ((float)(uint32_t)(z >> 32) + 1.0f) * 2.3283064365386963e-10f;
+    const float u2 = (float)(uint32_t)z * 2.3283064365386963e-10f;
+    const float r = sqrtf(-2.0f * logf(fminf(u1, 1.0f)));
+    float s, c;
+    sincosf(6.283185307179586f * u2, &s, &c);
+    y[2 * p] = mean + stdv * r * c;
+    if (2 * p + 1 < n) y[2 * p + 1] = mean + stdv * r * s;
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_fill_randn(float* y, int64_t n, uint64_t seed, float mean, float stdv, dt_stream_t stream) {
+    DT_REQUIRE(n >= 0, "dt_fill_randn: n < 0");
+    if (n == 0) return DT_OK;
+    DT_REQUIRE(y, "dt_fill_randn: null pointer");
+    const int64_t pairs = (n + 1) / 2, blocks = (pairs + 255) / 256;
+    DT_REQUIRE(blocks < (1ll << 31), "dt_fill_randn: n too large");
+    hipLaunchKernelGGL(dit::randn_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, y, n, seed,
+                       mean, stdv);
+    return dit::check_launch("dt_fill_randn");
+}

@@ -13,6 +13,12 @@
 //                   RMSNorm.cpp:13-20 + Flux2PosEmbed.hpp:29-108, optionally
 //                   with the txt|img CONCAT of Flux2Attention.hpp:114-116
 //                   between the norm and the views.
+//   GEMM accumulate ADD(y, MUL_MAT(w, x)): the second projection of
+//                   Flux2FusedAttentionOutput.hpp:31-36 accumulates onto the
+//                   first in the GEMM epilogue (dt_gemm_bf16 with addend).
+//
+// MUL_MAT and FLASH_ATTN_EXT (Linear.cpp:24, FlashAttentionOp.cpp:84-94) run
+// the bf16 MFMA kernels of gemm.hip and attention.hip.
 //
 // A chain is fused only when every interior node is consumed solely inside
 // the chain and is not flagged DT_FLAG_OUTPUT; everything else runs the
@@ -83,7 +89,7 @@ bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
     return true;
 }
 
-enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU };
+enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD };
 
 struct QkSeg {
     const dt_tensor* q;   // RMS_NORM input
@@ -378,6 +384,88 @@ bool match_qk(Graph& g, const dt_tensor* y, Plan& p) {
     return true;
 }
 
+// Operands of MUL_MAT node t as a dt_gemm_bf16 call: weight rows [N][K],
+// activation rows [M][K], output rows [M][N].
+struct GemmArgs {
+    const void *a, *b;
+    int64_t lda, ldb, M, N, K;
+};
+
+bool gemm_args(const dt_tensor* t, GemmArgs* g) {
+    const dt_tensor* w = t->src[0];
+    const dt_tensor* x = t->src[1];
+    if (!w || !x || w->type != DT_TYPE_BF16 || x->type != DT_TYPE_BF16) return false;
+    if (w->ne[2] != 1 || w->ne[3] != 1 || w->nb[0] != 2 || x->ne[0] != w->ne[0]) return false;
+    int64_t rows, xs;
+    if (!row_layout(x, &rows, &xs)) return false;
+    if (w->ne[1] > 1 && w->nb[1] % 2) return false;
+    g->a = x->data;
+    g->lda = xs;
+    g->b = w->data;
+    g->ldb = w->ne[1] > 1 ? w->nb[1] / 2 : w->ne[0];
+    g->M = rows;
+    g->N = w->ne[1];
+    g->K = w->ne[0];
+    return true;
+}
+
+bool out_rows(const dt_tensor* t, int64_t n_cols, int64_t* ld) {
+    int64_t rows;
+    return (t->type == DT_TYPE_BF16 || t->type == DT_TYPE_F32) && t->ne[0] == n_cols &&
+           row_layout(t, &rows, ld);
+}
+
+// ADD(y, MUL_MAT(w, x)) or ADD(MUL_MAT(w, x), y) -> one GEMM with addend y.
+bool match_gemm_add(Graph& g, const dt_tensor* a, Plan& p) {
+    if (a->op != DT_OP_ADD) return false;
+    for (int k = 1; k >= 0; --k) {
+        const dt_tensor* mm = a->src[k];
+        const dt_tensor* y = a->src[1 - k];
+        if (!mm || !y || mm->op != DT_OP_MUL_MAT || !g.internal(mm)) continue;
+        int64_t ld;
+        if (!same_shape(mm, a) || !same_shape(y, a) || y->type != a->type || mm->type != a->type ||
+            !out_rows(a, a->ne[0], &ld) || !out_rows(y, a->ne[0], &ld))
+            continue;
+        g.claim(mm);
+        p.kind = K_GEMM_ADD;
+        p.in[0] = mm;
+        p.in[1] = y;
+        return true;
+    }
+    return false;
+}
+
+int run_mul_mat(hipStream_t st, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
+    GemmArgs g;
+    int64_t ldc = 0, ldd = 0;
+    DT_REQUIRE(gemm_args(mm, &g), "dt_graph_compute: MUL_MAT needs BF16 weight rows and BF16 activation rows");
+    DT_REQUIRE(out_rows(out, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
+    if (addend) DT_REQUIRE(out_rows(addend, g.N, &ldd), "dt_graph_compute: bad GEMM addend");
+    return dt_gemm_bf16(g.a, g.lda, g.b, g.ldb, out->data, ldc, g.M, g.N, g.K, nullptr,
+                        addend ? addend->data : nullptr, ldd, out->type, st);
+}
+
+int run_flash_attn(hipStream_t st, const dt_tensor* t) {
+    const dt_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2];
+    DT_REQUIRE(q && k && v && !t->src[3], "dt_graph_compute: FLASH_ATTN_EXT needs q, k, v and no mask");
+    DT_REQUIRE(q->type == DT_TYPE_BF16 && k->type == DT_TYPE_BF16 && v->type == DT_TYPE_BF16,
+               "dt_graph_compute: FLASH_ATTN_EXT operands must be BF16");
+    DT_REQUIRE(q->nb[0] == 2 && k->nb[0] == 2 && v->nb[0] == 2 && t->nb[0] == elem_size(t->type),
+               "dt_graph_compute: FLASH_ATTN_EXT rows must be contiguous");
+    DT_REQUIRE(t->ne[0] == q->ne[0] && t->ne[1] == q->ne[2] && t->ne[2] == q->ne[1] &&
+                   t->ne[3] == q->ne[3] && k->ne[1] == v->ne[1] && k->ne[2] == q->ne[2] &&
+                   v->ne[2] == q->ne[2] && k->ne[3] == q->ne[3] && v->ne[3] == q->ne[3] &&
+                   k->ne[0] == q->ne[0] && v->ne[0] == q->ne[0],
+               "dt_graph_compute: FLASH_ATTN_EXT shapes disagree");
+    const int64_t es = elem_size(t->type);
+    const int64_t qs[3] = {q->nb[3] / 2, q->nb[1] / 2, q->nb[2] / 2};
+    const int64_t ks[3] = {k->nb[3] / 2, k->nb[1] / 2, k->nb[2] / 2};
+    const int64_t vs[3] = {v->nb[3] / 2, v->nb[1] / 2, v->nb[2] / 2};
+    const int64_t os[3] = {t->nb[3] / es, t->nb[2] / es, t->nb[1] / es};
+    return dt_flash_attn_bf16(q->data, k->data, v->data, t->data, q->ne[3], q->ne[2], q->ne[1], k->ne[1],
+                              q->ne[0], qs, ks, vs, os, fparam(t, 0), t->type, st);
+}
+
 int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
     hipStream_t st = backend_stream(be);
     switch (p.kind) {
@@ -443,6 +531,9 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
         case K_SILU:
             ++g_kernels;
             return dt_op_unary(DT_UN_SILU, p.in[0], root, 0.f, 0.f, st);
+        case K_GEMM_ADD:
+            ++g_kernels;
+            return run_mul_mat(st, p.in[0], root, p.in[1]);
         default:
             return fail(DT_ERR_INVALID_ARG, "run_plan: no plan");
     }
@@ -496,6 +587,12 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
         case DT_OP_CPY:
             ++g_kernels;
             return dt_op_cpy(t->src[0], t, st);
+        case DT_OP_MUL_MAT:
+            ++g_kernels;
+            return run_mul_mat(st, t, t, nullptr);
+        case DT_OP_FLASH_ATTN_EXT:
+            ++g_kernels;
+            return run_flash_attn(st, t);
         default:
             return fail(DT_ERR_UNSUPPORTED, "dt_graph_compute: op %d not supported", t->op);
     }
@@ -523,7 +620,8 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
         Plan& p = plans[i];
         g.current_root = i;
         if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_adaln(g, t, p) ||
-            match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p))
+            match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p) ||
+            match_gemm_add(g, t, p))
             continue;
         p = Plan();
     }

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint64, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libdit_hip.so")
@@ -72,6 +72,7 @@ _SIGS = {
                                     c_void_p, c_float, c_int32, c_void_p, c_void_p, c_size_t,
                                     c_int32, _S]),
     "dt_euler_step": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_int64, c_int32, _S]),
+    "dt_fill_randn": (c_int32, [c_void_p, c_int64, c_uint64, c_float, c_float, _S]),
     "dt_quantize_q8_0": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, _S]),
     "dt_gemm_bf16": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
                                c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32, _S]),

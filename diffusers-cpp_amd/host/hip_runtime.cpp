@@ -142,6 +142,7 @@ RuntimeScope::~RuntimeScope() { g_current = prev_; }
 // ---------------------------------------------------------------------------
 
 HipRuntime::HipRuntime(int device, dt_stream_t stream) {
+    if (device < 0) return;
     check(dt_backend_init(device, &be_), "dt_backend_init");
     check(dt_backend_set_stream(be_, stream), "dt_backend_set_stream");
 }
@@ -151,7 +152,7 @@ HipRuntime::~HipRuntime() {
         reset();
     } catch (...) {
     }
-    dt_backend_free(be_);
+    if (be_) dt_backend_free(be_);
 }
 
 size_t HipRuntime::nbytes(const Node* t) {
@@ -170,6 +171,7 @@ Node* HipRuntime::make(int32_t type, const int64_t ne[4], int32_t op) {
     contiguous_nb(type, t->ne, t->nb);
     t->id = (int32_t)nodes_.size() - 1;
     if (op != DT_OP_NONE) order_.push_back(t);
+    prepared_ = false;
     return t;
 }
 
@@ -293,8 +295,25 @@ Node* HipRuntime::scale(Node* t, float value) {
 
 Node* HipRuntime::clamp(Node* t, float mn, float mx) { return unary(t, DT_UN_CLAMP, mn, mx); }
 
-Node* HipRuntime::mul_mat(Node*, Node*) {
-    throw Unsupported("mul_mat: GEMMs run in the step harness, not in this elementwise backend");
+// ggml_mul_mat(w, x) (Runtime.hpp:136-139; Linear.cpp:24): y = x W^T over
+// ne0.  The MFMA GEMM takes BF16 operands: an F32 operand is cast to BF16 by
+// a CPY node first (ggml's CPU backend likewise converts the activation to
+// the weight's vec_dot type), and the result is F32 when the activation was
+// F32 (ggml's result type) or BF16 for BF16 activations.
+Node* HipRuntime::mul_mat(Node* w, Node* x) {
+    if (w->ne[0] != x->ne[0]) throw std::invalid_argument("mul_mat: ne0 (K) of weight and input differ");
+    if (w->ne[2] != 1 || w->ne[3] != 1) throw Unsupported("mul_mat: batched weights are not supported");
+    if (w->type == DT_TYPE_Q8_0 || w->type == DT_TYPE_Q4_K)
+        throw Unsupported("mul_mat: dequantise Q8_0/Q4_K weights to BF16 once at load (dt_dequant)");
+    const int32_t out_type = x->type == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32;
+    if (w->type != DT_TYPE_BF16) w = cast(w, DT_TYPE_BF16);
+    if (x->type != DT_TYPE_BF16) x = cast(x, DT_TYPE_BF16);
+    else if (x->nb[0] != 2) x = cont(x);
+    const int64_t ne[4] = {w->ne[1], x->ne[1], x->ne[2], x->ne[3]};
+    Node* r = make(out_type, ne, DT_OP_MUL_MAT);
+    r->src[0] = w;
+    r->src[1] = x;
+    return r;
 }
 
 // ---- views -----------------------------------------------------------------------
@@ -373,8 +392,29 @@ Node* HipRuntime::concat(Node* a, Node* b, int dim) {
 }
 
 Node* HipRuntime::sum_rows(Node*) { throw Unsupported("sum_rows: not part of the DiT elementwise chain"); }
-Node* HipRuntime::flash_attn_ext(Node*, Node*, Node*, Node*, float, float, float) {
-    throw Unsupported("flash_attn_ext: attention runs in the step harness, not in this backend");
+// ggml_flash_attn_ext (Runtime.hpp:250-257; FlashAttentionOp.cpp:84-94):
+// q ne {D, Sq, H, B}, k / v ne {D, Skv, H, B} -> ne {D, H, Sq, B}.  No mask,
+// ALiBi or softcap (Flux2 uses none); F32 operands are cast to BF16 and give
+// an F32 result, BF16 operands a BF16 result.
+Node* HipRuntime::flash_attn_ext(Node* q, Node* k, Node* v, Node* mask, float scale, float max_bias,
+                                 float logit_softcap) {
+    if (mask) throw Unsupported("flash_attn_ext: masks are not supported");
+    if (max_bias != 0.0f || logit_softcap != 0.0f)
+        throw Unsupported("flash_attn_ext: ALiBi / logit softcap are not supported");
+    if (q->ne[0] != 128 || k->ne[0] != 128 || v->ne[0] != 128)
+        throw Unsupported("flash_attn_ext: head_dim 128 only");
+    const int32_t out_type = q->type == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32;
+    auto prep = [&](Node* t) { return t->type != DT_TYPE_BF16 ? cast(t, DT_TYPE_BF16) : t->nb[0] != 2 ? cont(t) : t; };
+    q = prep(q);
+    k = prep(k);
+    v = prep(v);
+    const int64_t ne[4] = {q->ne[0], q->ne[2], q->ne[1], q->ne[3]};
+    Node* r = make(out_type, ne, DT_OP_FLASH_ATTN_EXT);
+    r->src[0] = q;
+    r->src[1] = k;
+    r->src[2] = v;
+    r->op_params[0] = fbits(scale);
+    return r;
 }
 Node* HipRuntime::conv_2d_direct(Node*, Node*, int, int, int, int, int, int) {
     throw Unsupported("conv_2d_direct: not part of the DiT elementwise chain");
@@ -436,9 +476,41 @@ void HipRuntime::bind(Node* leaf, const void* host, size_t bytes) {
     if (bytes != nbytes(leaf)) throw std::invalid_argument("bind: byte count does not match the tensor");
     auto& v = host_data_[leaf];
     v.assign((const uint8_t*)host, (const uint8_t*)host + bytes);
+    if (device_data_.erase(leaf)) prepared_ = false;
+}
+
+void HipRuntime::bind_device(Node* leaf, void* device_ptr) {
+    if (leaf->op != DT_OP_NONE) throw std::invalid_argument("bind_device: only leaves carry data");
+    if (!device_ptr) throw std::invalid_argument("bind_device: null pointer");
+    host_data_.erase(leaf);
+    device_data_[leaf] = device_ptr;
+    leaf->data = device_ptr;
+    prepared_ = false;
+}
+
+const ComputeStats& HipRuntime::plan() {
+    prepare(false);
+    return stats_;
 }
 
 void HipRuntime::compute() {
+    if (!be_) throw Error("compute: this runtime has no device");
+    if (!prepared_) prepare();
+    for (Node* l : leaves_) {
+        auto h = host_data_.find(l);
+        if (h != host_data_.end())
+            check(dt_tensor_set(l, h->second.data(), 0, h->second.size(), nullptr), "dt_tensor_set");
+    }
+    const int n = (int)order_.size();
+    if (n) check(dt_graph_compute(be_, order_.data(), n), "dt_graph_compute");
+    check(dt_backend_synchronize(be_), "dt_backend_synchronize");
+    int32_t k = 0, f = 0;
+    dt_graph_last_stats(&k, &f);
+    stats_.kernels = k;
+    stats_.fused_nodes = f;
+}
+
+void HipRuntime::prepare(bool allocate) {
     const int n = (int)order_.size();
     // 1. fusion plan
     std::vector<int32_t> fused_into(n, -1);
@@ -483,21 +555,36 @@ void HipRuntime::compute() {
         release_at[i].clear();
     }
 
+    stats_.nodes = n;
+    stats_.arena_bytes = planner.peak();
+    stats_.naive_bytes = naive;
+    stats_.fused_nodes = 0;
+    stats_.mul_mat_nodes = stats_.attention_nodes = 0;
+    for (int i = 0; i < n; ++i) {
+        stats_.fused_nodes += fused_into[i] >= 0;
+        stats_.mul_mat_nodes += order_[i]->op == DT_OP_MUL_MAT;
+        stats_.attention_nodes += order_[i]->op == DT_OP_FLASH_ATTN_EXT;
+    }
+    if (!allocate) return;
+
     // 4. device memory: leaves in their own buffer, op nodes in the arena
     if (leaf_buf_) {
         check(dt_buffer_free(be_, leaf_buf_), "dt_buffer_free");
         leaf_buf_ = nullptr;
     }
     size_t leaf_bytes = 0;
-    for (Node* l : leaves_) leaf_bytes += align_up(nbytes(l));
+    for (Node* l : leaves_)
+        if (!device_data_.count(l)) leaf_bytes += align_up(nbytes(l));
     if (leaf_bytes) check(dt_buffer_alloc(be_, leaf_bytes, &leaf_buf_), "dt_buffer_alloc(leaves)");
     size_t off = 0;
     for (Node* l : leaves_) {
+        auto d = device_data_.find(l);
+        if (d != device_data_.end()) {
+            l->data = d->second;
+            continue;
+        }
         l->data = (char*)leaf_buf_ + off;
         off += align_up(nbytes(l));
-        auto h = host_data_.find(l);
-        if (h != host_data_.end())
-            check(dt_tensor_set(l, h->second.data(), 0, h->second.size(), nullptr), "dt_tensor_set");
     }
     if (planner.peak() > arena_cap_) {
         if (arena_) check(dt_buffer_free(be_, arena_), "dt_buffer_free");
@@ -526,16 +613,7 @@ void HipRuntime::compute() {
         }
     }
 
-    // 5. run
-    if (n) check(dt_graph_compute(be_, order_.data(), n), "dt_graph_compute");
-    check(dt_backend_synchronize(be_), "dt_backend_synchronize");
-    int32_t k = 0, f = 0;
-    dt_graph_last_stats(&k, &f);
-    stats_.nodes = n;
-    stats_.kernels = k;
-    stats_.fused_nodes = f;
-    stats_.arena_bytes = planner.peak();
-    stats_.naive_bytes = naive;
+    prepared_ = true;
 }
 
 void HipRuntime::read(const Node* node, void* host, size_t bytes) const {
@@ -544,14 +622,16 @@ void HipRuntime::read(const Node* node, void* host, size_t bytes) const {
 }
 
 void HipRuntime::reset() {
-    if (leaf_buf_) dt_buffer_free(be_, leaf_buf_);
-    if (arena_) dt_buffer_free(be_, arena_);
+    if (be_ && leaf_buf_) dt_buffer_free(be_, leaf_buf_);
+    if (be_ && arena_) dt_buffer_free(be_, arena_);
     leaf_buf_ = arena_ = nullptr;
     arena_cap_ = 0;
     nodes_.clear();
     order_.clear();
     leaves_.clear();
     host_data_.clear();
+    device_data_.clear();
+    prepared_ = false;
     alias_.clear();
     stats_ = ComputeStats();
 }

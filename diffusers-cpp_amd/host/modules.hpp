@@ -15,6 +15,8 @@
 #pragma once
 
 #include <array>
+#include <string>
+#include <utility>
 #include <vector>
 
 #include "tensor.hpp"
@@ -22,19 +24,49 @@
 namespace dit {
 namespace host {
 
-inline Tensor parameter(const Tensor::Shape& shape) {
-    Tensor p = Tensor::empty(shape, DT_TYPE_F32);
+inline Tensor parameter(const Tensor::Shape& shape, int32_t type = DT_TYPE_F32) {
+    Tensor p = Tensor::empty(shape, type);
     current_runtime().set_param(*p);
     return p;
 }
 
-class LayerNorm {
+// The module tree of src/nn/Module.hpp: named children and parameters, so
+// every parameter has the dotted path the reference's loaders use
+// ("transformer_blocks.0.attn.to_q.weight").  Members are held by value and
+// registered by address, so modules are neither copied nor moved.
+class Module {
+public:
+    Module() = default;
+    Module(const Module&) = delete;
+    Module& operator=(const Module&) = delete;
+    virtual ~Module() = default;
+
+    void named_parameters(std::vector<std::pair<std::string, Tensor>>& out,
+                          const std::string& prefix = "") const {
+        for (const auto& p : params_) out.emplace_back(prefix + p.first, *p.second);
+        for (const auto& c : children_) c.second->named_parameters(out, prefix + c.first + ".");
+    }
+
+protected:
+    void register_parameter(const std::string& name, Tensor& t) { params_.emplace_back(name, &t); }
+    void register_module(const std::string& name, Module& m) { children_.emplace_back(name, &m); }
+
+private:
+    std::vector<std::pair<std::string, Tensor*>> params_;
+    std::vector<std::pair<std::string, Module*>> children_;
+};
+
+class LayerNorm : public Module {
 public:
     explicit LayerNorm(int64_t dim, float eps = 1e-5f, bool elementwise_affine = true, bool bias = true)
         : eps_(eps), affine_(elementwise_affine), bias_(bias) {
         if (affine_) {
             weight = parameter({dim});
-            if (bias_) this->bias = parameter({dim});
+            register_parameter("weight", weight);
+            if (bias_) {
+                this->bias = parameter({dim});
+                register_parameter("bias", this->bias);
+            }
         }
     }
     Tensor forward(Tensor x) const {
@@ -52,11 +84,14 @@ private:
     bool affine_, bias_;
 };
 
-class RMSNorm {
+class RMSNorm : public Module {
 public:
     explicit RMSNorm(int64_t dim, float eps = 1e-5f, bool elementwise_affine = true)
         : eps_(eps), affine_(elementwise_affine) {
-        if (affine_) weight = parameter({dim});
+        if (affine_) {
+            weight = parameter({dim});
+            register_parameter("weight", weight);
+        }
     }
     Tensor forward(Tensor x) const {
         x = Tensor(current_runtime().rms_norm(*x, eps_), x.shape());
@@ -70,14 +105,18 @@ private:
     bool affine_;
 };
 
-class GroupNorm {
+class GroupNorm : public Module {
 public:
     GroupNorm(int64_t num_groups, int64_t num_channels, float eps = 1e-5f, bool affine = true,
               bool bias = true)
         : groups_(num_groups), eps_(eps), affine_(affine), bias_(bias) {
         if (affine_) {
             weight = parameter({num_channels});
-            if (bias_) this->bias = parameter({num_channels});
+            register_parameter("weight", weight);
+            if (bias_) {
+                this->bias = parameter({num_channels});
+                register_parameter("bias", this->bias);
+            }
         }
     }
     Tensor forward(Tensor input) const {

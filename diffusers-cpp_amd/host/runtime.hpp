@@ -125,11 +125,15 @@ struct ComputeStats {
     int nodes = 0;
     int kernels = 0;
     int fused_nodes = 0;
+    int mul_mat_nodes = 0;
+    int attention_nodes = 0;
     size_t arena_bytes = 0;     // op-node memory after liveness reuse
     size_t naive_bytes = 0;     // the same nodes without reuse or fusion
 };
 
 // The Runtime that records dt_tensor nodes and runs them on one HIP device.
+// device < 0 makes a runtime without a device: graphs can be recorded and
+// planned (plan()) but not computed.
 class HipRuntime : public Runtime {
 public:
     explicit HipRuntime(int device = 0, dt_stream_t stream = nullptr);
@@ -190,10 +194,18 @@ public:
     Node* upscale(Node* a, int scale_factor, ScaleMode mode) override;
 
     // ---- data and execution ------------------------------------------------
-    // Host bytes for a leaf (input or parameter), uploaded at compute().
+    // Host bytes for a leaf (input or parameter), uploaded at every compute().
     void bind(Node* leaf, const void* host, size_t bytes);
+    // Device memory the caller owns and keeps resident for a leaf (weights
+    // loaded once, inputs already in HBM): never copied or freed here.
+    void bind_device(Node* leaf, void* device_ptr);
     // Plan, allocate and run every recorded node; output nodes keep their data.
+    // The plan and the device memory are kept while no node is added, so
+    // repeated calls on the same graph only upload host-bound leaves and run.
     void compute();
+    // Fusion and memory plan of the recorded graph without touching a device;
+    // fills stats() except `kernels`.
+    const ComputeStats& plan();
     // Copy an output (or leaf) back to the host; `bytes` = its contiguous size.
     void read(const Node* node, void* host, size_t bytes) const;
     // Drop the recorded graph and its memory.
@@ -215,6 +227,9 @@ private:
     std::vector<Node*> order_;                       // op and view nodes, creation order
     std::vector<Node*> leaves_;
     std::unordered_map<const Node*, std::vector<uint8_t>> host_data_;
+    std::unordered_map<const Node*, void*> device_data_;
+    bool prepared_ = false;
+    void prepare(bool allocate = true);
     std::unordered_map<const Node*, Node*> alias_;   // cpy node -> destination
     void* leaf_buf_ = nullptr;
     void* arena_ = nullptr;

@@ -165,6 +165,12 @@ int dt_euler_step(const void *x, const void *v, float dt, void *y, int64_t n,
 int dt_quantize_q8_0(const float *src, int64_t rows, int64_t cols, int64_t src_stride,
                      void *dst, int64_t row_bytes, dt_stream_t stream);
 
+/* Synthetic N(mean, std^2) fp32 data on the device (benchmark weights and
+ * inputs; a seeded splitmix64 + Box-Muller stream).  No counterpart in the
+ * reference, which reads weights from GGUF files. */
+int dt_fill_randn(float *y, int64_t n, uint64_t seed, float mean, float std,
+                  dt_stream_t stream);
+
 /* ---- step-time support: Linear and attention ---------------------------- */
 
 /* C[m][n] = sum_k A[m][k] * B[n][k] (+ bias[n]) (+ addend[m][n]), bf16 A and
@@ -280,6 +286,12 @@ enum {
                             offset in op_params[0] (low 32 bits), [1] (high) */
     DT_OP_FILL,          /* op_params[0] = value bits */
     DT_OP_UNARY,         /* op_params[0] = DT_UN_* kind, [1], [2] = p0, p1 bits */
+    DT_OP_MUL_MAT,       /* ggml_mul_mat(src0 = weight ne {K, N}, src1 = x ne {K, M1, M2, M3})
+                            -> ne {N, M1, M2, M3}; BF16 operands (dt_gemm_bf16),
+                            node type BF16 or F32 */
+    DT_OP_FLASH_ATTN_EXT,/* ggml_flash_attn_ext(q ne {D, Sq, H, B}, k, v ne {D, Skv, H, B},
+                            src[3] = mask, must be NULL) -> ne {D, H, Sq, B};
+                            op_params[0] = scale bits; BF16 q/k/v, D = 128 */
     DT_OP_COUNT
     /* DT_OP_CPY: src[0] is copied (converted) into the node; src[1], when
        set, is the destination tensor the node aliases (ggml_cpy). */

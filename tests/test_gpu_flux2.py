@@ -1,0 +1,161 @@
+"""Whole Flux2 blocks and a small Flux2 transformer on the GPU through the C++
+host modules (Linear -> MUL_MAT, attention -> FLASH_ATTN_EXT, the
+elementwise chain -> the fused kernels), against the oracle's fp32
+composition of the same reference forward passes (oracle/flux2.py).
+
+Weights are drawn N(0, 0.02) and rounded to bf16-representable values, and
+activations are bf16-representable, so the fp32 reference and the bf16 device
+path start from identical numbers; the device's error is then its bf16
+activation roundings and fp32 accumulation order, held to the bf16 bar
+(rel L2 <= 1e-2, cos >= 0.9999).  RMSNorm weights are N(1, 0.02) in fp32."""
+import json
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from conftest import bf16_metrics
+from test_gpu_fused import flux_positions
+from test_gpu_host_cli import CLI, read_dtb, write_dtb
+
+pytestmark = pytest.mark.gpu
+
+
+def make_params(orc, shapes, seed0):
+    P = {}
+    for i, (name, shape) in enumerate(sorted(shapes.items())):
+        if len(shape) == 2:
+            P[name] = orc.round_bf16(orc.randn(orc.tensor_seed(seed0 + i), shape, std=0.02))
+        else:
+            P[name] = orc.randn(orc.tensor_seed(seed0 + i), shape, mean=1.0, std=0.02)
+    return P
+
+
+def write_params(d, P):
+    wd = os.path.join(d, "weights")
+    os.makedirs(wd, exist_ok=True)
+    for name, a in P.items():
+        write_dtb(os.path.join(wd, name + ".dtb"), np.asarray(a, np.float32), 0)
+    return wd
+
+
+def run_cli(command, *args, timeout=300):
+    r = subprocess.run([CLI, command, *map(str, args)], capture_output=True, text=True, timeout=timeout)
+    assert r.returncode == 0, f"dit_cli {command} failed: {r.stderr}"
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def check(got, want, what):
+    rel, cos = bf16_metrics(got, want)
+    print(f"  {what}: rel_l2={rel:.3e} cos={cos:.7f}", flush=True)
+    assert rel <= 1e-2 and cos >= 0.9999, f"{what}: rel_l2={rel:.3e} cos={cos:.6f}"
+
+
+@pytest.fixture
+def tmp():
+    with tempfile.TemporaryDirectory() as d:
+        yield d
+
+
+def _single_block_case(orc, tmp, S_txt, grid, D, heads, theta, dtype, txt_zero=False):
+    import oracle.flux2 as of
+    pos = flux_positions(S_txt, grid)
+    if txt_zero:
+        pos[:S_txt] = 0
+    S = pos.shape[0]
+    P = make_params(orc, of.single_block_param_shapes(D, heads), 3000)
+    x = orc.round_bf16(orc.randn(orc.tensor_seed(2990), (S, D)))
+    cond = orc.randn(orc.tensor_seed(2991), (1, D))
+    w_mod = orc.randn(orc.tensor_seed(2992), (3 * D, D), std=0.02)
+    mod = orc.linear(of.silu(cond), w_mod)  # single_stream_modulation (SiLU + Linear)
+    wd = write_params(tmp, P)
+    xp, mp, pp, op = (os.path.join(tmp, n) for n in ("x.dtb", "mod.dtb", "pos.dtb", "out.dtb"))
+    write_dtb(xp, x.reshape(1, S, D), 0)
+    write_dtb(mp, mod.reshape(1, 3 * D), 0)
+    write_dtb(pp, pos, 26)
+    stats = run_cli("Flux2SingleTransformerBlock", "--heads", heads, "--theta", theta, *sum(
+        (["--axes_dim", 32] for _ in range(4)), []), "--weights", wd, "--hidden_states", xp,
+        "--temb_mod", mp, "--position_ids", pp, "--dtype", dtype, "--out", op)
+    want = of.single_block(x, mod, pos, P, heads, float(theta), 32)
+    return read_dtb(op).reshape(S, D), want, stats
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_single_block_small(orc, tmp, dtype):
+    print(f"single block S=16+64 D=256 {dtype}", flush=True)
+    got, want, stats = _single_block_case(orc, tmp, 16, 8, 256, 2, 2000, dtype)
+    check(got, want, f"single block {dtype}")
+    print(f"  {stats}", flush=True)
+    # adaLN, 2x QK-RMSNorm+RoPE, SwiGLU, GEMM-accumulate and gated residual fused
+    assert stats["fused_nodes"] > 0
+
+
+def test_single_block_full_size(orc, tmp):
+    """One Flux2-style single-stream block: hidden 3072, 24 x 128 heads, MLP
+    9216, 1536 tokens (512 text with zero positions, then a 32 x 32 image
+    grid), theta 2000; modulation from a N(0, 1) conditioning vector through
+    SiLU + Linear."""
+    print("single block S=512+1024 D=3072 bf16", flush=True)
+    got, want, stats = _single_block_case(orc, tmp, 512, 32, 3072, 24, 2000, "bf16", txt_zero=True)
+    check(got, want, "single block 1536x3072")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_double_block_small(orc, tmp, dtype):
+    import oracle.flux2 as of
+    print(f"double block 16+64 D=256 {dtype}", flush=True)
+    D, heads, n_txt, grid = 256, 2, 16, 8
+    pos = flux_positions(n_txt, grid)
+    n_img = grid * grid
+    P = make_params(orc, of.double_block_param_shapes(D, heads), 4000)
+    h = orc.round_bf16(orc.randn(orc.tensor_seed(3990), (n_img, D)))
+    e = orc.round_bf16(orc.randn(orc.tensor_seed(3991), (n_txt, D)))
+    mi = orc.randn(orc.tensor_seed(3992), (6 * D,), std=0.5)
+    mt = orc.randn(orc.tensor_seed(3993), (6 * D,), std=0.5)
+    wd = write_params(tmp, P)
+    f = {n: os.path.join(tmp, n + ".dtb") for n in ("h", "e", "mi", "mt", "pos", "oe", "oh")}
+    write_dtb(f["h"], h.reshape(1, n_img, D), 0)
+    write_dtb(f["e"], e.reshape(1, n_txt, D), 0)
+    write_dtb(f["mi"], mi.reshape(1, -1), 0)
+    write_dtb(f["mt"], mt.reshape(1, -1), 0)
+    write_dtb(f["pos"], pos, 26)
+    run_cli("Flux2TransformerBlock", "--heads", heads, "--theta", 2000,
+            *sum((["--axes_dim", 32] for _ in range(4)), []), "--weights", wd, "--hidden_states", f["h"],
+            "--encoder_hidden_states", f["e"], "--temb_mod_img", f["mi"], "--temb_mod_txt", f["mt"],
+            "--position_ids", f["pos"], "--dtype", dtype, "--out-encoder", f["oe"], "--out-hidden", f["oh"])
+    we, wh = of.double_block(h, e, mi, mt, pos, P, heads, 2000.0, 32)
+    check(read_dtb(f["oh"]).reshape(n_img, D), wh, f"double block hidden {dtype}")
+    check(read_dtb(f["oe"]).reshape(n_txt, D), we, f"double block encoder {dtype}")
+
+
+def test_model_small(orc, tmp):
+    """Flux2Transformer2DModel end to end at a small width: 1 double + 2
+    single blocks, 2 x 128 heads, 64 image tokens (8 x 8) and 16 text tokens,
+    timestep 0.5, no guidance embedding."""
+    import oracle.flux2 as of
+    cfg = dict(num_layers=1, num_single_layers=2, num_attention_heads=2, attention_head_dim=128,
+               in_channels=128, joint_attention_dim=128, timestep_guidance_channels=256, mlp_ratio=3.0,
+               rope_theta=2000, axes_dims_rope=[32, 32, 32, 32], eps=1e-6)
+    n_txt, grid = 16, 8
+    n_img = grid * grid
+    P = make_params(orc, of.model_param_shapes(cfg), 5000)
+    hid = orc.round_bf16(orc.randn(orc.tensor_seed(4990), (n_img, 128)))
+    txt = orc.round_bf16(orc.randn(orc.tensor_seed(4991), (n_txt, 128)))
+    pos = flux_positions(n_txt, grid)
+    wd = write_params(tmp, P)
+    f = {n: os.path.join(tmp, n + ".dtb") for n in ("h", "t", "ts", "ii", "ti", "o")}
+    write_dtb(f["h"], hid.reshape(1, n_img, 128), 0)
+    write_dtb(f["t"], txt.reshape(1, n_txt, 128), 0)
+    write_dtb(f["ts"], np.array([0.5], np.float32), 0)
+    write_dtb(f["ii"], pos[n_txt:], 26)
+    write_dtb(f["ti"], pos[:n_txt], 26)
+    stats = run_cli("Flux2Transformer2DModel", "--num_layers", 1, "--num_single_layers", 2,
+                    "--num_attention_heads", 2, "--joint_attention_dim", 128, "--img_tokens", n_img,
+                    "--txt_tokens", n_txt, "--weights", wd, "--hidden_states", f["h"],
+                    "--encoder_hidden_states", f["t"], "--timestep", f["ts"], "--img_ids", f["ii"],
+                    "--txt_ids", f["ti"], "--steps", 2, "--out", f["o"])
+    print(f"  {stats}", flush=True)
+    want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], P, cfg)
+    check(read_dtb(f["o"]).reshape(n_img, 128), want, "model 1+2 blocks")
