@@ -21,6 +21,13 @@ dominant kernel (SwiGLU) timed alone with HIP events on the stream it is
 launched on; `cpu_baseline` is the oracle's C restatement of the same chain
 (fp32, OpenMP) on a bounded sample, timed on this host's cores.
 
+`sec_per_denoise_step` is one full Flux2-klein-4B-shaped transformer step
+(5 double + 20 single blocks, hidden 3072, 24x128 heads, 4096 image tokens of
+128 features + 512 text tokens of width 2560, timestep 0.5) run by the C++
+driver (diffusers-cpp_amd/bin/dit_cli) as a child process: Q8_0 weights
+drawn N(0, 0.02) and dequantised once to bf16, bf16 activations, inputs and
+weights resident in HBM, median wall time per step of the recorded graph.
+
 Prints ONE JSON line.
 """
 import argparse
@@ -219,6 +226,51 @@ def cpu_baseline(budget_s):
     return total / t_all / 1e9, threads, sample, total / t_4 / 1e9
 
 
+def denoise_flops(n_img=4096, n_txt=512, d=3072, mlp=9216, blocks=25, txt_width=2560, ch=128):
+    """FLOP of one step: every Linear (2*M*N*K) and attention (4*S^2*d per block)."""
+    s = n_img + n_txt
+    per_token = 4 * d * d + 3 * d * mlp              # q, k, v, out + gate, up, down (both block types)
+    lin = blocks * s * per_token
+    lin += n_img * ch * d + n_txt * txt_width * d + n_img * d * ch      # x / context embedders, proj_out
+    lin += 256 * d + d * d + d * (6 * d * 2 + 3 * d) + d * 2 * d        # time embedding, modulations, norm_out
+    return 2 * lin + blocks * 4 * s * s * d
+
+
+def denoise_step(steps, warmup):
+    """Run the full-step driver as a child process; None if it is missing."""
+    import subprocess
+    cli = os.path.join(PKG, "bin", "dit_cli")
+    if not os.path.exists(cli):
+        return None
+    cmd = [cli, "Flux2Transformer2DModel", "--random-weights", "1", "--random-inputs", "2",
+           "--steps", str(steps), "--warmup", str(warmup)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError(f"dit_cli failed ({r.returncode}): {r.stderr.strip()[-500:]}")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    t = res["ms_per_step_median"] * 1e-3
+    flops = denoise_flops()
+    return {
+        "workload": "Flux2-klein-4B-shaped transformer step at 1024^2: 5 double + 20 single blocks, "
+                    "hidden 3072, 24x128 heads, MLP 9216, 4096 image + 512 text tokens (text width 2560), "
+                    "timestep 0.5, no guidance embedding",
+        "weights": "Q8_0 (N(0,0.02) quantised on device) dequantised once to bf16; RMSNorm weights N(1,0.02)",
+        "s_per_step": round(t, 5),
+        "ms_per_step_min": res["ms_per_step_min"],
+        "ms_per_step_mean": res["ms_per_step_mean"],
+        "steps": steps,
+        "warmup": warmup,
+        "params": res["params"],
+        "graph_nodes": res["nodes"],
+        "kernels_per_step": res["kernels"],
+        "fused_nodes": res["fused_nodes"],
+        "arena_bytes": res["arena_bytes"],
+        "tflop_per_step": round(flops / 1e12, 3),
+        "roofline": {"bound": "mfma", "achieved": round(flops / t / 1e12, 1), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(flops / t / 1e12 / 2500.0, 4)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -228,12 +280,18 @@ def main():
                     help="seconds of CPU-baseline sampling (0 disables)")
     ap.add_argument("--no-secondary", dest="secondary", action="store_false",
                     help="skip the dequantisation / GroupNorm measurements")
+    ap.add_argument("--denoise-steps", type=int, default=5,
+                    help="timed full denoising steps (0 skips the step measurement)")
+    ap.add_argument("--denoise-warmup", type=int, default=2)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "the chain is row-independent and would shard tokens across GPUs with no exchange",
               file=sys.stderr)
         sys.exit(2)
+
+    # The full step runs in its own process before this one touches the GPU.
+    denoise = denoise_step(args.denoise_steps, args.denoise_warmup) if args.denoise_steps > 0 else None
 
     import torch
     import dit_hip
@@ -335,7 +393,7 @@ def main():
             traffic = json.load(f).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": kernels[dom]["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(kernels[dom]["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "swiglu_kernel<bf16,4>", "alg_bytes_per_launch": ab[dom]}
+                "kernel": "swiglu_kernel<bf16,2>", "alg_bytes_per_launch": ab[dom]}
 
     cpu = None
     if args.cpu_budget > 0:
@@ -365,6 +423,8 @@ def main():
                    "alg_bytes_per_step": total, "buffer_sets": NSETS,
                    "parallelism": "none (1 GPU)"},
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "sec_per_denoise_step": denoise["s_per_step"] if denoise else None,
+        "denoise_step": denoise,
         "copy_ceiling_GBs": round(ceiling, 1),
         "kernels": kernels,
         "secondary": extra,
