@@ -234,6 +234,13 @@ struct DeviceBuffers {
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Upload host bytes once into a device buffer that `leaf` keeps.
+void resident_input(HipRuntime& rt, DeviceBuffers& bufs, const Tensor& leaf, const void* host, size_t bytes) {
+    void* d = bufs.alloc(bytes);
+    rt.bind_device(*leaf, d);
+    check(dt_tensor_set(*leaf, host, 0, bytes, nullptr), "dt_tensor_set");
+}
+
 void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffers& bufs, size_t* bf16_bytes,
                     size_t* q8_bytes, size_t* n_params) {
     std::vector<std::pair<std::string, Tensor>> ps;
@@ -268,18 +275,11 @@ void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffer
         } else if (t.dtype() == DT_TYPE_F32) {
             std::vector<float> h((size_t)t.numel());
             for (float& v : h) v = nd(gen);  // RMSNorm weights
-            rt.bind(*t, h.data(), h.size() * 4);
+            resident_input(rt, bufs, t, h.data(), h.size() * 4);
         } else {
             throw std::runtime_error("random weights: unexpected parameter type for " + p.first);
         }
     }
-}
-
-// Upload host bytes once into a device buffer that `leaf` keeps.
-void resident_input(HipRuntime& rt, DeviceBuffers& bufs, const Tensor& leaf, const void* host, size_t bytes) {
-    void* d = bufs.alloc(bytes);
-    rt.bind_device(*leaf, d);
-    check(dt_tensor_set(*leaf, host, 0, bytes, nullptr), "dt_tensor_set");
 }
 
 void run_model(Session& s, const Args& a) {

@@ -3,16 +3,36 @@
 //   C[m, n] = sum_k A[m, k] * B[n, k]  (+ bias[n]) (+ D[m, n]),  fp32 accumulation,
 // with A = activations [M, K] and B = a Linear weight [N, K] (PyTorch's
 // [out, in]), both K-contiguous, so 16-byte chunks along K are exactly the
-// 8-element bf16 operands of v_mfma_f32_32x32x16_bf16.
+// 8-element bf16 operands of v_mfma_f32_32x32x16_bf16.  One launch can run a
+// group of up to kMaxGroup independent GEMMs (the q/k/v/gate/up projections
+// of a block), whose tiles share the grid: no wave of workgroups is left
+// half-empty at the end of each small GEMM.
 //
-// Tiling (gfx950): a 256-thread workgroup owns a 128x128 C tile; each wave
-// owns 64x64 = 2x2 MFMA 32x32 tiles (64 fp32 accumulators per lane).  K
-// advances 64 at a time: the next A/B tiles are fetched into registers while
-// the MFMAs consume the current tiles from LDS (rows padded to 144 bytes so
-// 8-lane 16-byte reads hit distinct banks).  Operand layout of the 32x32x16
-// instruction: lane l supplies A[l % 32][8 (l / 32) + e] and
-// B[8 (l / 32) + e][l % 32]; accumulator element i of lane l is
-// C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
+// Two tile configurations (gfx950):
+//  * 256 x 256, 8 waves of 128 x 64: A and B travel global -> LDS by direct
+//    DMA (global_load_lds_dwordx4: lane i of an instruction writes its 16
+//    bytes to LDS base + 16 i) through four stages of K = 32, so the loads for
+//    k-tile kt + 3 are in flight while k-tile kt is multiplied and no
+//    registers are spent on staging.  A stage row is 64 bytes (4 chunks of 8
+//    bf16); chunk c of row r is stored at chunk c ^ swz(r), swz(r) =
+//    ((r >> 1) ^ (r >> 2)) & 3, which makes the 16-byte reads of 8 (32-bank)
+//    or 16 (64-bank) consecutive rows at one logical chunk hit distinct banks.
+//  * 128 x 128, 4 waves of 64 x 64, two workgroups per CU: K = 64 per step
+//    through two register-staged LDS stages (rows padded to 144 bytes), for
+//    GEMMs too small to fill the CUs with 256 x 256 tiles.
+//
+// The MFMA computes the transposed tile C^T = B A^T: the weight rows are the
+// instruction's A operand and the activation rows its B operand, so the
+// accumulator element i of lane l is C[m = 32 fm + l % 32][n = 32 fn +
+// 8 (i / 4) + 4 (l / 32) + i % 4] and every lane stores 4 consecutive n.
+// Operand layout of the 32x32x16 instruction: lane l supplies
+// A[l % 32][8 (l / 32) + e] and B[8 (l / 32) + e][l % 32].
+//
+// Workgroups are renumbered so that each XCD (8 per MI355X, one L2 each)
+// runs a contiguous range of tiles, and each GEMM's tiles are ordered in
+// groups of GROUP_M tile rows so concurrently running tiles share A rows and
+// B columns.  Rows past M or N load a clamped valid row: their products only
+// reach C entries that are never stored.
 #include "capi_util.hpp"
 #include "common.hpp"
 
@@ -22,137 +42,398 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LDSW = BK + 8;  // padded LDS row, in bf16 elements
+constexpr int GROUP_M = 4;
+constexpr int kMaxGroup = 8;
+
+struct Problem {
+    const uint16_t* A;
+    const uint16_t* B;
+    void* C;
+    const void* D;
+    const float* bias;
+    int64_t lda, ldb, ldc, ldd;
+    int M, N, K;
+};
+
+struct Group {
+    Problem p[kMaxGroup];
+    int tile_start[kMaxGroup + 1];  // prefix sums of each problem's tile count
+    int count;
+};
 
 template <typename TC>
-__device__ __forceinline__ void store_c(TC* p, float v);
+__device__ __forceinline__ void store4(TC* p, const float* v);
 template <>
-__device__ __forceinline__ void store_c<float>(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store4<float>(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
 template <>
-__device__ __forceinline__ void store_c<bf16>(bf16* p, float v) { p->bits = (uint16_t)f32_to_bf16_bits(v); }
+__device__ __forceinline__ void store4<bf16>(bf16* p, const float* v) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
 __device__ __forceinline__ float load_c(const float* p) { return *p; }
 __device__ __forceinline__ float load_c(const bf16* p) { return __uint_as_float((uint32_t)p->bits << 16); }
-
 template <typename TC>
-__global__ __launch_bounds__(256) void gemm_bf16_nt_kernel(const uint16_t* __restrict__ A, int64_t lda,
-                                                           const uint16_t* __restrict__ B, int64_t ldb,
-                                                           TC* C, int64_t ldc, int M, int N, int K,
-                                                           const float* __restrict__ bias, const TC* Dm,
-                                                           int64_t ldd) {
-    __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDSW];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * LDSW];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile_m = blockIdx.y * BM, tile_n = blockIdx.x * BN;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+__device__ __forceinline__ void store1(TC* p, float v);
+template <>
+__device__ __forceinline__ void store1<float>(float* p, float v) { *p = v; }
+template <>
+__device__ __forceinline__ void store1<bf16>(bf16* p, float v) { p->bits = (uint16_t)f32_to_bf16_bits(v); }
 
-    // Global -> register mapping: chunk c = tid + 256 r covers row c / 8,
-    // k-chunk c % 8 (8 bf16 = 16 bytes) of a 128 x 64 tile.
-    uint4 ra[4], rb[4];
-    auto load_tiles = [&](int k0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int c = tid + 256 * r, row = c >> 3, kc = c & 7;
-            const int gm = tile_m + row, gn = tile_n + row;
-            ra[r] = gm < M ? *reinterpret_cast<const uint4*>(A + (int64_t)gm * lda + k0 + kc * 8)
-                           : make_uint4(0, 0, 0, 0);
-            rb[r] = gn < N ? *reinterpret_cast<const uint4*>(B + (int64_t)gn * ldb + k0 + kc * 8)
-                           : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto store_tiles = [&]() {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int c = tid + 256 * r, row = c >> 3, kc = c & 7;
-            *reinterpret_cast<uint4*>(&As[row * LDSW + kc * 8]) = ra[r];
-            *reinterpret_cast<uint4*>(&Bs[row * LDSW + kc * 8]) = rb[r];
-        }
-    };
+// Problem and tile of this workgroup: XCD-contiguous numbering over the whole
+// group, then GROUP_M-row groups inside the problem.
+template <int BM, int BN>
+__device__ __forceinline__ const Problem& locate(const Group& g, int* tm, int* tn) {
+    uint32_t bid = blockIdx.x;
+    const uint32_t nb = gridDim.x, q = nb >> 3;
+    if (bid < (q << 3)) bid = (bid & 7u) * q + (bid >> 3);
+    int pi = 0;
+    while (pi + 1 < g.count && (int)bid >= g.tile_start[pi + 1]) ++pi;
+    const Problem& p = g.p[pi];
+    const int local = (int)bid - g.tile_start[pi];
+    const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+    const int per_group = GROUP_M * tiles_n;
+    const int group = local / per_group, first_m = group * GROUP_M;
+    const int rows = min(tiles_m - first_m, GROUP_M);
+    const int in_group = local - group * per_group;
+    *tm = first_m + in_group % rows;
+    *tn = in_group / rows;
+    return p;
+}
 
-    f32x16_t acc[2][2];
+// Bias / addend epilogue and store of one wave's FM x FN blocks of 32 x 32.
+template <int FM, int FN, typename TC>
+__device__ __forceinline__ void epilogue(const Problem& p, const f32x16_t (&acc)[FN][FM], int mw, int nw,
+                                         int lane) {
+    TC* C = reinterpret_cast<TC*>(p.C);
+    const TC* Dm = reinterpret_cast<const TC*>(p.D);
+    const int lrow = lane & 31, g = lane >> 5;
+    const bool vec = (p.N % 4) == 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i) {
+        const int m = mw + 32 * i + lrow;
+        if (m >= p.M) continue;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-
-    load_tiles(0);
-    store_tiles();
-    __syncthreads();
-    const int lrow = lane & 31, lk = (lane >> 5) * 8;
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        const bool more = k0 + BK < K;
-        if (more) load_tiles(k0 + BK);  // in flight while the MFMAs run
+            for (int q = 0; q < 4; ++q) {
+                const int n = nw + 32 * j + 8 * q + 4 * g;
+                if (n >= p.N) continue;
+                float v[4];
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            bf16x8_t af[2], bfr[2];
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = acc[j][i][4 * q + e];
+                    if (p.bias && n + e < p.N) v[e] += p.bias[n + e];
+                    if (Dm && n + e < p.N) v[e] += load_c(Dm + (int64_t)m * p.ldd + n + e);
+                }
+                TC* dst = C + (int64_t)m * p.ldc + n;
+                if (vec && n + 4 <= p.N) {
+                    store4<TC>(dst, v);
+                } else {
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *reinterpret_cast<const bf16x8_t*>(&As[(wm + 32 * i + lrow) * LDSW + kk + lk]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bfr[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[(wn + 32 * j + lrow) * LDSW + kk + lk]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-        }
-        __syncthreads();
-        if (more) {
-            store_tiles();
-            __syncthreads();
-        }
-    }
-
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = tile_n + wn + 32 * j + lrow;
-            if (col >= N) continue;
-            const float bv = bias ? bias[col] : 0.f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = tile_m + wm + 32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < M) {
-                    float v = acc[i][j][e] + bv;
-                    if (Dm) v += load_c(Dm + (int64_t)row * ldd + col);
-                    store_c<TC>(C + (int64_t)row * ldc + col, v);
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < p.N) store1<TC>(dst + e, v[e]);
                 }
             }
         }
     }
 }
 
+// ---- 256 x 256, direct global -> LDS, 4 stages ------------------------------
+constexpr int DBK = 32, DSTAGES = 4, DROWB = DBK * 2, DOPB = 256 * DROWB, DSTAGEB = 2 * DOPB;
+
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+template <int N_OUT>
+__device__ __forceinline__ void wait_vm() {
+    // s_waitcnt vmcnt(N_OUT) with expcnt / lgkmcnt left at their maxima.
+    __builtin_amdgcn_s_waitcnt((N_OUT & 15) | ((N_OUT >> 4) << 14) | 0x0F70);
+}
+
+template <typename TC>
+__global__ __launch_bounds__(512) void gemm_dma256_kernel(const Group grp) {
+    constexpr int FM = 4, FN = 2;  // wave sub-tile 128 (m) x 64 (n)
+    __shared__ __attribute__((aligned(16))) uint8_t smem[DSTAGES * DSTAGEB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    const Problem& p = locate<256, 256>(grp, &tm, &tn);
+    const int m0 = tm * 256, n0 = tn * 256;
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+
+    // DMA sources: wave w fills rows [32 w, 32 w + 32) of both operands, two
+    // instructions of 16 rows each; lane i covers row + i / 4, stored chunk i % 4.
+    const uint16_t* ga[2];
+    const uint16_t* gb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 32 * wave + 16 * j + (lane >> 2);
+        const int c = (lane & 3) ^ swz(row);
+        ga[j] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + c * 8;
+        gb[j] = p.B + (int64_t)min(n0 + row, p.N - 1) * p.ldb + c * 8;
+    }
+    auto issue = [&](int kt, int s) {
+        uint8_t* base = smem + s * DSTAGEB + 32 * wave * DROWB;
+        const int k0 = kt * DBK;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            __builtin_amdgcn_global_load_lds(ga[j] + k0, base + 16 * j * DROWB, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(gb[j] + k0, base + DOPB + 16 * j * DROWB, 16, 0, 0);
+        }
+    };
+
+    f32x16_t acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.f;
+
+    const int lrow = lane & 31, g = lane >> 5, sw = swz(lrow);
+    const int nk = p.K / DBK;
+#pragma unroll
+    for (int s = 0; s < DSTAGES - 1; ++s)
+        if (s < nk) issue(s, s);
+    for (int kt = 0; kt < nk; ++kt) {
+        const int ahead = min(nk - 1 - kt, DSTAGES - 2);
+        if (ahead >= 2) wait_vm<8>();
+        else if (ahead == 1) wait_vm<4>();
+        else wait_vm<0>();
+        // A bare barrier: the wait above already covers this wave's DMA into
+        // stage kt, and no LDS is written by ds_write in this loop, so the
+        // workgroup fence of __syncthreads (which would drain every DMA in
+        // flight, vmcnt(0)) is not needed.  Each wave's ds_reads of the stage
+        // reused next have returned (the MFMAs consumed them) before it arrives.
+        __builtin_amdgcn_s_barrier();
+        if (kt + DSTAGES - 1 < nk) issue(kt + DSTAGES - 1, (kt + DSTAGES - 1) % DSTAGES);
+        const uint8_t* As = smem + (kt % DSTAGES) * DSTAGEB;
+        const uint8_t* Bs = As + DOPB;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int pc = ((2 * kk + g) ^ sw) * 16;
+            bf16x8_t wf[FN], xf[FM];
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                wf[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn + 32 * j + lrow) * DROWB + pc);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                xf[i] = *reinterpret_cast<const bf16x8_t*>(As + (wm + 32 * i + lrow) * DROWB + pc);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+        }
+    }
+    epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
+}
+
+// ---- 128 x 128, register-staged, 2 stages --------------------------------------
+constexpr int SBK = 64;
+constexpr int SLDSW = SBK + 8;  // padded LDS row, in bf16 elements
+
+template <typename TC>
+__global__ __launch_bounds__(256) void gemm_128_kernel(const Group grp) {
+    constexpr int FM = 2, FN = 2, T = 256;
+    constexpr int CH = 128 * (SBK / 8) / T;  // 16-byte chunks per thread per operand
+    constexpr int STAGE = 256 * SLDSW;
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    const Problem& p = locate<128, 128>(grp, &tm, &tn);
+    const int m0 = tm * 128, n0 = tn * 128;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+    const uint16_t* Ap = p.A;
+    const uint16_t* Bp = p.B;
+    const int64_t lda = p.lda, ldb = p.ldb;
+    const int Mx = p.M - 1, Nx = p.N - 1;
+    // Thread chunk r covers row (tid + T r) / 8, k-chunk tid % 8 of each operand.
+    const int kc = tid & 7, row0 = tid >> 3;
+    const uint16_t* ga = Ap + (int64_t)min(m0 + row0, Mx) * lda + kc * 8;
+    const uint16_t* gb = Bp + (int64_t)min(n0 + row0, Nx) * ldb + kc * 8;
+    int64_t oa[CH], ob[CH];  // row offsets relative to ga / gb
+#pragma unroll
+    for (int r = 0; r < CH; ++r) {
+        oa[r] = ((int64_t)min(m0 + row0 + (T / 8) * r, Mx) - min(m0 + row0, Mx)) * lda;
+        ob[r] = ((int64_t)min(n0 + row0 + (T / 8) * r, Nx) - min(n0 + row0, Nx)) * ldb;
+    }
+    uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
+    static_assert(CH == 4, "four chunks per thread per operand");
+    auto fetch = [&](int k0) {
+        ra0 = *reinterpret_cast<const uint4*>(ga + oa[0] + k0);
+        ra1 = *reinterpret_cast<const uint4*>(ga + oa[1] + k0);
+        ra2 = *reinterpret_cast<const uint4*>(ga + oa[2] + k0);
+        ra3 = *reinterpret_cast<const uint4*>(ga + oa[3] + k0);
+        rb0 = *reinterpret_cast<const uint4*>(gb + ob[0] + k0);
+        rb1 = *reinterpret_cast<const uint4*>(gb + ob[1] + k0);
+        rb2 = *reinterpret_cast<const uint4*>(gb + ob[2] + k0);
+        rb3 = *reinterpret_cast<const uint4*>(gb + ob[3] + k0);
+    };
+    auto stash = [&](int s) {
+        uint16_t* As = smem + s * STAGE + row0 * SLDSW + kc * 8;
+        uint16_t* Bs = As + 128 * SLDSW;
+        constexpr int RS = (T / 8) * SLDSW;  // LDS offset between a thread's chunks
+        *reinterpret_cast<uint4*>(As) = ra0;
+        *reinterpret_cast<uint4*>(As + RS) = ra1;
+        *reinterpret_cast<uint4*>(As + 2 * RS) = ra2;
+        *reinterpret_cast<uint4*>(As + 3 * RS) = ra3;
+        *reinterpret_cast<uint4*>(Bs) = rb0;
+        *reinterpret_cast<uint4*>(Bs + RS) = rb1;
+        *reinterpret_cast<uint4*>(Bs + 2 * RS) = rb2;
+        *reinterpret_cast<uint4*>(Bs + 3 * RS) = rb3;
+    };
+
+    f32x16_t acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.f;
+
+    const int lrow = lane & 31, lk = (lane >> 5) * 8;
+    const int nk = p.K / SBK;
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int s = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) fetch((kt + 1) * SBK);
+        const uint16_t* As = smem + s * STAGE;
+        const uint16_t* Bs = As + 128 * SLDSW;
+#pragma unroll
+        for (int kk = 0; kk < SBK; kk += 16) {
+            bf16x8_t wf[FN], xf[FM];
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                wf[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[(wn + 32 * j + lrow) * SLDSW + kk + lk]);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                xf[i] = *reinterpret_cast<const bf16x8_t*>(&As[(wm + 32 * i + lrow) * SLDSW + kk + lk]);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+        }
+        if (more) stash(s ^ 1);
+        __syncthreads();
+    }
+    epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
+}
+
+// ---- launch ---------------------------------------------------------------------
+
+struct Config {
+    int bm, bn, threads, per_cu;
+    double rate;  // measured per-CU rate when the CUs are full (PFLOP/s, gfx950)
+};
+// 0: 256 x 256 pipelined (one workgroup per CU); 1: 128 x 128 (two per CU).
+constexpr Config kConfigs[2] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}};
+
+int64_t tiles_of(const Problem& p, int cfg) {
+    const Config c = kConfigs[cfg];
+    return (int64_t)((p.M + c.bm - 1) / c.bm) * ((p.N + c.bn - 1) / c.bn);
+}
+
+// Estimated time: ceil(tiles / concurrent workgroups) waves, each lasting the
+// tile area x workgroups per CU / the per-CU rate.
+int pick_config(const Problem* ps, int n, int cus) {
+    int best = 1;
+    double best_t = 1e300;
+    for (int cfg = 0; cfg < 2; ++cfg) {
+        const Config c = kConfigs[cfg];
+        int64_t tiles = 0;
+        for (int i = 0; i < n; ++i) tiles += tiles_of(ps[i], cfg);
+        const int64_t slots = (int64_t)cus * c.per_cu;
+        const int64_t waves = (tiles + slots - 1) / slots;
+        const double t = (double)waves * c.bm * c.bn * c.per_cu / c.rate;
+        if (t < best_t) {
+            best_t = t;
+            best = cfg;
+        }
+    }
+    return best;
+}
+
+template <typename TC>
+int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
+    Group g{};
+    g.count = n;
+    int64_t total = 0;
+    for (int i = 0; i < n; ++i) {
+        g.p[i] = ps[i];
+        g.tile_start[i] = (int)total;
+        total += tiles_of(ps[i], cfg);
+    }
+    DT_REQUIRE(total < (1ll << 31), "dt_gemm_bf16: too many tiles");
+    g.tile_start[n] = (int)total;
+    if (total == 0) return DT_OK;
+    const dim3 grid((unsigned)total), block((unsigned)kConfigs[cfg].threads);
+    if (cfg == 0)
+        hipLaunchKernelGGL((gemm_dma256_kernel<TC>), grid, block, 0, st, g);
+    else
+        hipLaunchKernelGGL((gemm_128_kernel<TC>), grid, block, 0, st, g);
+    return check_launch("dt_gemm_bf16");
+}
+
+int validate(const dt_gemm_problem& q, int32_t c_type, Problem* out) {
+    DT_REQUIRE(q.M >= 0 && q.N >= 0 && q.K > 0, "dt_gemm_bf16: bad shape");
+    DT_REQUIRE(q.K % 64 == 0, "dt_gemm_bf16: K (%lld) must be a multiple of 64", (long long)q.K);
+    DT_REQUIRE(q.M < (1ll << 31) && q.N < (1ll << 31) && q.K < (1ll << 31), "dt_gemm_bf16: shape too large");
+    if (q.M > 0 && q.N > 0) {  // an empty problem's leading dimensions are never used
+        DT_REQUIRE(q.lda >= q.K && q.ldb >= q.K && q.ldc >= q.N && q.lda % 8 == 0 && q.ldb % 8 == 0,
+                   "dt_gemm_bf16: leading dimensions must cover the rows and keep 16-byte alignment");
+        DT_REQUIRE(!q.addend || q.ldd >= q.N, "dt_gemm_bf16: ldd < N");
+        DT_REQUIRE(q.A && q.B && q.C, "dt_gemm_bf16: null pointer");
+        DT_REQUIRE(aligned16(q.A) && aligned16(q.B), "dt_gemm_bf16: A and B must be 16-byte aligned");
+        const int es = c_type == DT_TYPE_F32 ? 4 : 2;
+        DT_REQUIRE(q.N % 4 != 0 || ((reinterpret_cast<uintptr_t>(q.C) % (4 * es)) == 0 && q.ldc % 4 == 0),
+                   "dt_gemm_bf16: C must be %d-byte aligned with ldc %% 4 == 0", 4 * es);
+    }
+    *out = Problem{(const uint16_t*)q.A, (const uint16_t*)q.B, q.C, q.addend, q.bias, q.lda, q.ldb,
+                   q.ldc, q.ldd, (int)q.M, (int)q.N, (int)q.K};
+    return DT_OK;
+}
+
 }  // namespace
 }  // namespace dit
+
+extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t count, int32_t c_type,
+                                    int32_t config, dt_stream_t stream) {
+    using namespace dit;
+    DT_REQUIRE(c_type == DT_TYPE_BF16 || c_type == DT_TYPE_F32, "dt_gemm_bf16: c_type %d unsupported", c_type);
+    DT_REQUIRE(config >= -1 && config <= 1, "dt_gemm_bf16: config %d out of range", config);
+    DT_REQUIRE(count >= 0 && count <= kMaxGroup, "dt_gemm_bf16_grouped: count %d outside 0..%d", count,
+               kMaxGroup);
+    DT_REQUIRE(problems || count == 0, "dt_gemm_bf16_grouped: null problem list");
+    Problem ps[kMaxGroup];
+    int n = 0;
+    for (int i = 0; i < count; ++i) {
+        Problem p;
+        int rc = validate(problems[i], c_type, &p);
+        if (rc) return rc;
+        if (p.M > 0 && p.N > 0) ps[n++] = p;
+    }
+    if (n == 0) return DT_OK;
+    const int cfg = config >= 0 ? config : pick_config(ps, n, cu_count());
+    hipStream_t st = (hipStream_t)stream;
+    return c_type == DT_TYPE_F32 ? launch<float>(ps, n, cfg, st) : launch<bf16>(ps, n, cfg, st);
+}
+
+extern "C" int dt_gemm_bf16_config(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                                   int64_t M, int64_t N, int64_t K, const float* bias, const void* addend,
+                                   int64_t ldd, int32_t c_type, int32_t config, dt_stream_t stream) {
+    const dt_gemm_problem p{A, lda, B, ldb, C, ldc, addend, ldd, bias, M, N, K};
+    return dt_gemm_bf16_grouped(&p, 1, c_type, config, stream);
+}
 
 extern "C" int dt_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
                             int64_t M, int64_t N, int64_t K, const float* bias, const void* addend,
                             int64_t ldd, int32_t c_type, dt_stream_t stream) {
-    DT_REQUIRE(c_type == DT_TYPE_BF16 || c_type == DT_TYPE_F32, "dt_gemm_bf16: c_type %d unsupported",
-               c_type);
-    DT_REQUIRE(M >= 0 && N >= 0 && K > 0, "dt_gemm_bf16: bad shape");
-    DT_REQUIRE(K % dit::BK == 0, "dt_gemm_bf16: K (%lld) must be a multiple of %d", (long long)K, dit::BK);
-    DT_REQUIRE(lda >= K && ldb >= K && ldc >= N && lda % 8 == 0 && ldb % 8 == 0,
-               "dt_gemm_bf16: leading dimensions must cover the rows and keep 16-byte alignment");
-    DT_REQUIRE(!addend || ldd >= N, "dt_gemm_bf16: ldd < N");
-    DT_REQUIRE(M < (1ll << 31) && N < (1ll << 31) && K < (1ll << 31), "dt_gemm_bf16: shape too large");
-    if (M == 0 || N == 0) return DT_OK;
-    DT_REQUIRE(A && B && C, "dt_gemm_bf16: null pointer");
-    DT_REQUIRE(dit::aligned16(A) && dit::aligned16(B), "dt_gemm_bf16: A and B must be 16-byte aligned");
-    const dim3 grid((unsigned)((N + dit::BN - 1) / dit::BN), (unsigned)((M + dit::BM - 1) / dit::BM));
-    DT_REQUIRE(grid.y < 65536, "dt_gemm_bf16: M too large for one launch");
-    hipStream_t st = (hipStream_t)stream;
-    if (c_type == DT_TYPE_F32)
-        hipLaunchKernelGGL((dit::gemm_bf16_nt_kernel<float>), grid, dim3(256), 0, st, (const uint16_t*)A, lda,
-                           (const uint16_t*)B, ldb, (float*)C, ldc, (int)M, (int)N, (int)K, bias,
-                           (const float*)addend, ldd);
-    else
-        hipLaunchKernelGGL((dit::gemm_bf16_nt_kernel<dit::bf16>), grid, dim3(256), 0, st, (const uint16_t*)A,
-                           lda, (const uint16_t*)B, ldb, (dit::bf16*)C, ldc, (int)M, (int)N, (int)K,
-                           bias, (const dit::bf16*)addend, ldd);
-    return dit::check_launch("dt_gemm_bf16");
+    return dt_gemm_bf16_config(A, lda, B, ldb, C, ldc, M, N, K, bias, addend, ldd, c_type, -1, stream);
 }

@@ -17,6 +17,13 @@
 //                   Flux2FusedAttentionOutput.hpp:31-36 accumulates onto the
 //                   first in the GEMM epilogue (dt_gemm_bf16 with addend).
 //
+// After fusion, runs of independent MUL_MATs (only VIEWs between them, every
+// input computed before the first) become one grouped GEMM launch at the
+// first one's position: the q/k/v/gate/up projections Linear::forward issues
+// back to back.  Those MUL_MATs keep their own outputs; dt_graph_plan_ex
+// reports where each node's kernel runs so the caller keeps inputs alive and
+// places outputs accordingly.
+//
 // MUL_MAT and FLASH_ATTN_EXT (Linear.cpp:24, FlashAttentionOp.cpp:84-94) run
 // the bf16 MFMA kernels of gemm.hip and attention.hip.
 //
@@ -89,7 +96,7 @@ bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
     return true;
 }
 
-enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD };
+enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD, K_GEMM_GROUP, K_DEFERRED };
 
 struct QkSeg {
     const dt_tensor* q;   // RMS_NORM input
@@ -108,6 +115,8 @@ struct Plan {
     std::vector<const dt_tensor*> pos;  // per axis
     int axis_dim = 0;
     float base = 0.f;
+    // GEMM group: every member MUL_MAT, the root first
+    std::vector<const dt_tensor*> members;
 };
 
 struct Graph {
@@ -115,6 +124,7 @@ struct Graph {
     std::unordered_map<const dt_tensor*, int> index;
     std::vector<char> claimed;
     std::vector<int> root;   // index of the node whose fused kernel absorbs node i
+    std::vector<int> runs_at;  // position where node i's kernel runs
     int current_root = -1;
 
     bool internal(const dt_tensor* t, int n_uses = 1) const {
@@ -445,6 +455,74 @@ int run_mul_mat(hipStream_t st, const dt_tensor* mm, const dt_tensor* out, const
                         addend ? addend->data : nullptr, ldd, out->type, st);
 }
 
+// Data address of t, resolving VIEW chains (a VIEW's own data is set only
+// when the executor reaches it, which a grouped launch may precede).
+const void* data_of(const dt_tensor* t) {
+    int64_t off = 0;
+    while (t && t->op == DT_OP_VIEW) {
+        off += view_offset(t);
+        t = t->src[0];
+    }
+    return t && t->data ? (const char*)t->data + off : nullptr;
+}
+
+int run_gemm_group(hipStream_t st, const std::vector<const dt_tensor*>& members) {
+    dt_gemm_problem ps[8];
+    const int n = (int)members.size();
+    DT_REQUIRE(n >= 1 && n <= 8, "dt_graph_compute: GEMM group of %d", n);
+    for (int i = 0; i < n; ++i) {
+        const dt_tensor* mm = members[i];
+        GemmArgs g;
+        int64_t ldc = 0;
+        DT_REQUIRE(gemm_args(mm, &g), "dt_graph_compute: MUL_MAT needs BF16 weight rows and BF16 activation rows");
+        DT_REQUIRE(out_rows(mm, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
+        ps[i] = dt_gemm_problem{data_of(mm->src[1]), g.lda, data_of(mm->src[0]), g.ldb, mm->data, ldc, nullptr, 0,
+                                nullptr, g.M, g.N, g.K};
+    }
+    return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
+}
+
+// Forward pass over unfused MUL_MATs: node i starts a group of the MUL_MATs
+// that follow it with only VIEWs in between, whose inputs all run before i
+// and whose output type matches; the later members run in i's launch.
+void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
+    auto ready_before = [&](const dt_tensor* t, int pos) {
+        while (t && t->op == DT_OP_VIEW) t = t->src[0];
+        if (!t) return false;
+        auto it = g.index.find(t);
+        return it == g.index.end() || g.runs_at[it->second] < pos;
+    };
+    auto groupable = [&](int j) {
+        const dt_tensor* t = nodes[j];
+        GemmArgs ga;
+        return t->op == DT_OP_MUL_MAT && !g.claimed[j] && plans[j].kind == K_NONE && gemm_args(t, &ga);
+    };
+    for (int i = 0; i < n; ++i) {
+        if (!groupable(i) || !ready_before(nodes[i]->src[0], i) || !ready_before(nodes[i]->src[1], i)) continue;
+        std::vector<int> members = {i};
+        for (int j = i + 1; j < n && members.size() < 8; ++j) {
+            const dt_tensor* t = nodes[j];
+            if (t->op == DT_OP_VIEW) continue;
+            if (!groupable(j) || t->type != nodes[i]->type || !ready_before(t->src[0], i) ||
+                !ready_before(t->src[1], i))
+                break;
+            members.push_back(j);
+        }
+        if (members.size() < 2) continue;
+        Plan& p = plans[i];
+        p.kind = K_GEMM_GROUP;
+        p.members.clear();
+        for (int j : members) {
+            p.members.push_back(nodes[j]);
+            if (j != i) {
+                plans[j].kind = K_DEFERRED;
+                g.runs_at[j] = i;
+            }
+        }
+        i = members.back();
+    }
+}
+
 int run_flash_attn(hipStream_t st, const dt_tensor* t) {
     const dt_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2];
     DT_REQUIRE(q && k && v && !t->src[3], "dt_graph_compute: FLASH_ATTN_EXT needs q, k, v and no mask");
@@ -534,6 +612,11 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
         case K_GEMM_ADD:
             ++g_kernels;
             return run_mul_mat(st, p.in[0], root, p.in[1]);
+        case K_GEMM_GROUP:
+            ++g_kernels;
+            return run_gemm_group(st, p.members);
+        case K_DEFERRED:
+            return DT_OK;  // ran in its group's launch
         default:
             return fail(DT_ERR_INVALID_ARG, "run_plan: no plan");
     }
@@ -607,6 +690,8 @@ namespace {
 int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& plans) {
     g.claimed.assign(n_nodes, 0);
     g.root.assign(n_nodes, -1);
+    g.runs_at.resize(n_nodes);
+    for (int i = 0; i < n_nodes; ++i) g.runs_at[i] = i;
     for (int i = 0; i < n_nodes; ++i) {
         DT_REQUIRE(nodes[i] != nullptr, "dt_graph: node %d is null", i);
         g.index[nodes[i]] = i;
@@ -625,13 +710,16 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
             continue;
         p = Plan();
     }
+    for (int i = 0; i < n_nodes; ++i)
+        if (g.claimed[i]) g.runs_at[i] = g.root[i];
+    group_gemms(g, nodes, n_nodes, plans);
     return DT_OK;
 }
 
 }  // namespace
 }  // namespace dit
 
-extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_into) {
+extern "C" int dt_graph_plan_ex(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_into, int32_t* runs_at) {
     using namespace dit;
     DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0) && (fused_into || n_nodes == 0),
                "dt_graph_plan: bad arguments");
@@ -639,8 +727,15 @@ extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_
     std::vector<Plan> plans;
     int rc = plan_graph(nodes, n_nodes, g, plans);
     if (rc) return rc;
-    for (int i = 0; i < n_nodes; ++i) fused_into[i] = g.claimed[i] ? g.root[i] : -1;
+    for (int i = 0; i < n_nodes; ++i) {
+        fused_into[i] = g.claimed[i] ? g.root[i] : -1;
+        if (runs_at) runs_at[i] = g.runs_at[i];
+    }
     return DT_OK;
+}
+
+extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_into) {
+    return dt_graph_plan_ex(nodes, n_nodes, fused_into, nullptr);
 }
 
 extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nodes) {

@@ -76,6 +76,10 @@ _SIGS = {
     "dt_quantize_q8_0": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, _S]),
     "dt_gemm_bf16": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
                                c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32, _S]),
+    "dt_gemm_bf16_config": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                                      c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32,
+                                      c_int32, _S]),
+    "dt_gemm_bf16_grouped": (c_int32, [c_void_p, c_int32, c_int32, c_int32, _S]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                      c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
                                      POINTER(c_int64), POINTER(c_int64), c_float, c_int32, _S]),
@@ -97,6 +101,8 @@ _SIGS = {
     "dt_tensor_get": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
     "dt_graph_compute": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32]),
     "dt_graph_plan": (c_int32, [POINTER(POINTER(DtTensor)), c_int32, POINTER(c_int32)]),
+    "dt_graph_plan_ex": (c_int32, [POINTER(POINTER(DtTensor)), c_int32, POINTER(c_int32),
+                                   POINTER(c_int32)]),
     "dt_graph_last_stats": (c_int32, [POINTER(c_int32), POINTER(c_int32)]),
 }
 
@@ -322,8 +328,10 @@ def quantize_q8_0(x, out=None):
     return y
 
 
-def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None):
-    """a: bf16 [M, K], b: bf16 [N, K] (rows K-contiguous) -> a @ b.T (+ bias) (+ addend)."""
+def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None, config=-1):
+    """a: bf16 [M, K], b: bf16 [N, K] (rows K-contiguous) -> a @ b.T (+ bias) (+ addend).
+    config: tile configuration (0: 256x256 with direct global->LDS loads, 1: 128x128,
+    -1: by shape)."""
     torch = _torch()
     M, K = a.shape
     N = b.shape[0]
@@ -331,10 +339,29 @@ def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None):
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=a.device)
     ldd = addend.stride(0) if addend is not None else 0
-    check(load().dt_gemm_bf16(_p(a), a.stride(0), _p(b), b.stride(0), _p(out), out.stride(0), M, N,
-                              K, _p(bias), _p(addend), ldd, io_type(out), stream()),
+    check(load().dt_gemm_bf16_config(_p(a), a.stride(0), _p(b), b.stride(0), _p(out), out.stride(0),
+                                     M, N, K, _p(bias), _p(addend), ldd, io_type(out), config,
+                                     stream()),
           "dt_gemm_bf16")
     return out
+
+
+class GemmProblem(ctypes.Structure):
+    _fields_ = [("A", c_void_p), ("lda", c_int64), ("B", c_void_p), ("ldb", c_int64),
+                ("C", c_void_p), ("ldc", c_int64), ("addend", c_void_p), ("ldd", c_int64),
+                ("bias", c_void_p), ("M", c_int64), ("N", c_int64), ("K", c_int64)]
+
+
+def gemm_grouped(items, config=-1):
+    """items: list of (a [M,K] bf16, b [N,K] bf16, out [M,N]) -> one launch."""
+    probs = (GemmProblem * len(items))()
+    for i, (a, b, out) in enumerate(items):
+        probs[i] = GemmProblem(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(),
+                               out.stride(0), None, 0, None, a.shape[0], b.shape[0], a.shape[1])
+    ct = io_type(items[0][2])
+    check(load().dt_gemm_bf16_grouped(ctypes.cast(probs, c_void_p), len(items), ct, config, stream()),
+          "dt_gemm_bf16_grouped")
+    return [it[2] for it in items]
 
 
 def flash_attn(q, k, v, scale=None, out=None, out_dtype=None):

@@ -202,16 +202,18 @@ public:
     // -> {hidden_states, encoder_hidden_states}
     std::pair<Tensor, Tensor> forward(const Tensor& hidden_states, const Tensor& encoder_hidden_states,
                                       const RotaryEmb& rotary) const {
-        Tensor query = to_q.forward(hidden_states).unflatten(-1, {heads_, -1});
-        Tensor key = to_k.forward(hidden_states).unflatten(-1, {heads_, -1});
-        Tensor value = to_v.forward(hidden_states).unflatten(-1, {heads_, -1});
-        query = norm_q.forward(query);
-        key = norm_k.forward(key);
-        Tensor eq = add_q_proj.forward(encoder_hidden_states).unflatten(-1, {heads_, -1});
-        Tensor ek = add_k_proj.forward(encoder_hidden_states).unflatten(-1, {heads_, -1});
-        Tensor ev = add_v_proj.forward(encoder_hidden_states).unflatten(-1, {heads_, -1});
-        eq = norm_added_q.forward(eq);
-        ek = norm_added_k.forward(ek);
+        Tensor query = to_q.forward(hidden_states);
+        Tensor key = to_k.forward(hidden_states);
+        Tensor value = to_v.forward(hidden_states);
+        Tensor eq = add_q_proj.forward(encoder_hidden_states);
+        Tensor ek = add_k_proj.forward(encoder_hidden_states);
+        Tensor ev = add_v_proj.forward(encoder_hidden_states);
+        query = norm_q.forward(query.unflatten(-1, {heads_, -1}));
+        key = norm_k.forward(key.unflatten(-1, {heads_, -1}));
+        value = value.unflatten(-1, {heads_, -1});
+        eq = norm_added_q.forward(eq.unflatten(-1, {heads_, -1}));
+        ek = norm_added_k.forward(ek.unflatten(-1, {heads_, -1}));
+        ev = ev.unflatten(-1, {heads_, -1});
         query = Tensor::cat({eq, query}, 1);
         key = Tensor::cat({ek, key}, 1);
         value = Tensor::cat({ev, value}, 1);
@@ -312,13 +314,14 @@ public:
         register_module("to_out.mlp", out_mlp);
     }
     Tensor forward(const Tensor& hidden_states, const RotaryEmb& rotary) const {
-        Tensor query = q.forward(hidden_states).unflatten(-1, {heads_, -1});
-        Tensor key = k.forward(hidden_states).unflatten(-1, {heads_, -1});
-        Tensor value = v.forward(hidden_states).unflatten(-1, {heads_, -1});
+        Tensor query = q.forward(hidden_states);
+        Tensor key = k.forward(hidden_states);
+        Tensor value = v.forward(hidden_states);
         Tensor gate = mlp_in_gate.forward(hidden_states);
         Tensor up = mlp_in_up.forward(hidden_states);
-        query = norm_q.forward(query);
-        key = norm_k.forward(key);
+        query = norm_q.forward(query.unflatten(-1, {heads_, -1}));
+        key = norm_k.forward(key.unflatten(-1, {heads_, -1}));
+        value = value.unflatten(-1, {heads_, -1});
         query = rotary.first->forward(query, rotary.second);
         key = rotary.first->forward(key, rotary.second);
         Tensor h = scaled_dot_product_attention(query, key, value).flatten(2, 3);

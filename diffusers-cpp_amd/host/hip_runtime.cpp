@@ -512,19 +512,19 @@ void HipRuntime::compute() {
 
 void HipRuntime::prepare(bool allocate) {
     const int n = (int)order_.size();
-    // 1. fusion plan
-    std::vector<int32_t> fused_into(n, -1);
-    if (n) check(dt_graph_plan(order_.data(), n, fused_into.data()), "dt_graph_plan");
-    std::unordered_map<const Node*, int> pos;
-    for (int i = 0; i < n; ++i) pos[order_[i]] = i;
+    // 1. fusion plan: which nodes are absorbed (no storage) and where every
+    //    node's kernel runs (absorbed -> its root, grouped GEMMs -> the
+    //    group's first member)
+    std::vector<int32_t> fused_into(n, -1), runs_at(n, 0);
+    if (n) check(dt_graph_plan_ex(order_.data(), n, fused_into.data(), runs_at.data()), "dt_graph_plan_ex");
 
     // 2. last use of every storage root, at the position where the reading
-    //    kernel runs (the fused root for absorbed nodes)
+    //    kernel runs
     const int kForever = std::numeric_limits<int>::max();
     std::unordered_map<const Node*, int> last_use;
     for (int i = 0; i < n; ++i) {
         Node* t = order_[i];
-        const int at = fused_into[i] >= 0 ? fused_into[i] : i;
+        const int at = runs_at[i];
         for (int s = 0; s < 4; ++s) {
             if (!t->src[s]) continue;
             const Node* r = root_of(t->src[s]);
@@ -534,25 +534,29 @@ void HipRuntime::prepare(bool allocate) {
         if (t->flags & DT_FLAG_OUTPUT) last_use[root_of(t)] = kForever;
     }
 
-    // 3. arena plan for op nodes that own storage
+    // 3. arena plan for op nodes that own storage: each output is placed at
+    //    the position its kernel runs (never later than the node itself)
+    //    before that position's inputs are released, so a kernel never
+    //    writes over what it reads.
     ArenaPlanner planner;
     std::unordered_map<const Node*, size_t> offset;
-    std::vector<std::vector<const Node*>> release_at(n);
+    std::vector<std::vector<const Node*>> alloc_at(n), release_at(n);
     size_t naive = 0;
     for (int i = 0; i < n; ++i) {
         Node* t = order_[i];
         const bool owns = t->op != DT_OP_VIEW && !alias_.count(t);
         if (owns) naive += align_up(nbytes(t));
-        if (owns && fused_into[i] < 0) {
-            // The output is placed before this position's inputs are released,
-            // so a kernel never writes over what it reads.
+        if (owns && fused_into[i] < 0) alloc_at[std::min(i, (int)runs_at[i])].push_back(t);
+    }
+    for (int p = 0; p < n; ++p) {
+        for (const Node* t : alloc_at[p]) {
             offset[t] = planner.alloc(nbytes(t));
             auto lu = last_use.find(t);
-            const int end = lu == last_use.end() ? i : lu->second;
-            if (end != kForever) release_at[std::max(end, i)].push_back(t);
+            const int end = lu == last_use.end() ? p : lu->second;
+            if (end != kForever) release_at[std::max(end, p)].push_back(t);
         }
-        for (const Node* r : release_at[i]) planner.release(offset.at(r), nbytes(r));
-        release_at[i].clear();
+        for (const Node* r : release_at[p]) planner.release(offset.at(r), nbytes(r));
+        release_at[p].clear();
     }
 
     stats_.nodes = n;

@@ -148,15 +148,18 @@ class Flux2PosEmbed {
 public:
     Flux2PosEmbed(int64_t theta, std::vector<int64_t> axes_dim) : theta_(theta), axes_(std::move(axes_dim)) {}
 
-    // x: [..., head_dim]; position_ids: I32 [sequence, n_axes].
+    // x: [..., head_dim]; position_ids: I32 [sequence, n_axes].  The per-axis
+    // position columns (a narrow + squeeze, i.e. a CONT copy) are made once
+    // per position tensor and shared by every later call on it, where the
+    // reference re-derives them for q and k of every block.
     Tensor forward(const Tensor& x, const Tensor& position_ids) const {
+        const std::vector<Tensor>& pos = columns(position_ids);
         std::vector<Tensor> sections;
         int64_t offset = 0;
         for (size_t axis = 0; axis < axes_.size(); ++axis) {
             const int64_t d = axes_[axis];
             Tensor x_axis = x.narrow(-1, offset, d);
-            Tensor pos_axis = position_ids.select(1, (int64_t)axis);  // narrow + squeeze (-> CONT)
-            if (pos_axis.ndim() != 1) pos_axis = pos_axis.flatten(0, pos_axis.ndim() - 1);
+            const Tensor& pos_axis = pos[axis];
             Node* r = current_runtime().rope_ext(*x_axis, *pos_axis, nullptr, (int)d, 0, 0,
                                                  (float)theta_, 1.0f, 0.0f, 1.0f, 0.0f, 0.0f);
             sections.emplace_back(r, x_axis.shape());
@@ -166,8 +169,22 @@ public:
     }
 
 private:
+    const std::vector<Tensor>& columns(const Tensor& position_ids) const {
+        for (const auto& c : cache_)
+            if (c.first == *position_ids) return c.second;
+        std::vector<Tensor> cols;
+        for (size_t axis = 0; axis < axes_.size(); ++axis) {
+            Tensor p = position_ids.select(1, (int64_t)axis);  // narrow + squeeze (-> CONT)
+            if (p.ndim() != 1) p = p.flatten(0, p.ndim() - 1);
+            cols.push_back(p);
+        }
+        cache_.emplace_back(*position_ids, std::move(cols));
+        return cache_.back().second;
+    }
+
     int64_t theta_;
     std::vector<int64_t> axes_;
+    mutable std::vector<std::pair<Node*, std::vector<Tensor>>> cache_;
 };
 
 struct Flux2SwiGLU {

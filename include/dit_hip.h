@@ -185,6 +185,36 @@ int dt_fill_randn(float *y, int64_t n, uint64_t seed, float mean, float std,
 int dt_gemm_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C, int64_t ldc,
                  int64_t M, int64_t N, int64_t K, const float *bias, const void *addend,
                  int64_t ldd, int32_t c_type, dt_stream_t stream);
+/* dt_gemm_bf16 with an explicit tile configuration: 0 = 256x256 per
+ * workgroup with direct global->LDS loads in four stages, 1 = 128x128 with two
+ * workgroups per CU; -1 picks by shape as dt_gemm_bf16 does.  For tuning and
+ * tests; no counterpart in the reference. */
+int dt_gemm_bf16_config(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
+                        int64_t ldc, int64_t M, int64_t N, int64_t K, const float *bias,
+                        const void *addend, int64_t ldd, int32_t c_type, int32_t config,
+                        dt_stream_t stream);
+
+/* One GEMM of a group: the arguments of dt_gemm_bf16. */
+typedef struct dt_gemm_problem {
+    const void *A;
+    int64_t lda;
+    const void *B;
+    int64_t ldb;
+    void *C;
+    int64_t ldc;
+    const void *addend;
+    int64_t ldd;
+    const float *bias;
+    int64_t M, N, K;
+} dt_gemm_problem;
+
+/* Up to 8 independent GEMMs (same c_type) in one launch whose tiles share
+ * the grid, e.g. the q, k, v, gate and up projections Linear::forward issues
+ * one after another on the same input (Flux2FusedQKVProjection.hpp:61-68,
+ * Flux2Attention.hpp:64-83, Flux2FeedForward.hpp:62-72).  No outputs may
+ * overlap another problem's inputs.  config as for dt_gemm_bf16_config. */
+int dt_gemm_bf16_grouped(const dt_gemm_problem *problems, int32_t count, int32_t c_type,
+                         int32_t config, dt_stream_t stream);
 
 /* Unmasked attention softmax(scale * Q K^T) V per (batch, head), head_dim
  * 128, bf16 q/k/v, fp32 softmax and accumulation, o of o_type (BF16 or F32).
@@ -313,6 +343,13 @@ int dt_graph_compute(dt_backend *be, dt_tensor **nodes, int32_t n_nodes);
  * root node runs), or -1 when node i runs on its own.  Uses shapes, types,
  * strides, view offsets and flags, never data pointers. */
 int dt_graph_plan(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into);
+/* dt_graph_plan plus runs_at[i] = the position in the node list at which node
+ * i's kernel runs: i for most nodes, the absorbing node for absorbed ones,
+ * and the first member for MUL_MATs grouped into one GEMM launch (those keep
+ * their own outputs, which are written at that earlier position).  A caller
+ * that allocates node memory places each output at min(i, runs_at[i]) and
+ * keeps inputs alive until the runs_at of their last reader. */
+int dt_graph_plan_ex(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into, int32_t *runs_at);
 /* Statistics of the last dt_graph_compute on this thread: kernels launched
  * and nodes absorbed into fused kernels. */
 int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);

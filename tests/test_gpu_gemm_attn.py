@@ -56,20 +56,23 @@ def test_quantize_q8_0_strided_rows(orc, dev):
 GEMM_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192)]
 
 
+@pytest.mark.parametrize("config", [-1, 0, 1])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-def test_gemm(orc, dev, M, N, K, out_dtype):
-    print(f"gemm M={M} N={N} K={K} {out_dtype}", flush=True)
+def test_gemm(orc, dev, M, N, K, out_dtype, config):
+    print(f"gemm M={M} N={N} K={K} {out_dtype} config={config}", flush=True)
     a = orc.randn(SEED + 210, (M, K))
     b = orc.randn(SEED + 211, (N, K), std=0.02)
-    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), out_dtype=out_dtype)
+    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), out_dtype=out_dtype,
+                     config=config)
     torch.cuda.synchronize()
     ref = orc.linear(orc.round_bf16(a), orc.round_bf16(b))
     check(host(y), ref, out_dtype, f"gemm {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("config", [0, 1])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
-def test_gemm_strided_bias_addend(orc, dev, out_dtype):
+def test_gemm_strided_bias_addend(orc, dev, out_dtype, config):
     M, N, K = 300, 384, 512
     big_a = orc.randn(SEED + 212, (M, K + 128))
     b = orc.randn(SEED + 213, (N, K), std=0.02)
@@ -79,7 +82,7 @@ def test_gemm_strided_bias_addend(orc, dev, out_dtype):
     addd = dev_tensor(add, out_dtype)[:, :N]                        # ldd = N + 8
     out = torch.zeros((M, N + 16), dtype=out_dtype, device="cuda")
     dit_hip.gemm(ad, dev_tensor(b, torch.bfloat16), bias=dev_tensor(bias, torch.float32),
-                 addend=addd, out=out[:, :N])
+                 addend=addd, out=out[:, :N], config=config)
     torch.cuda.synchronize()
     lin = orc.linear(orc.round_bf16(big_a[:, 64:64 + K]), orc.round_bf16(b), bias)
     ref = lin + as_input(add[:, :N], out_dtype)
@@ -100,17 +103,37 @@ def test_gemm_in_place_addend(orc, dev):
     assert_fp32(host(c), orc.linear(orc.round_bf16(a), orc.round_bf16(b)) + c0, what="gemm in-place")
 
 
-def test_gemm_large_sampled_rows(orc, dev):
-    """4608 x 3072 x 3072 (a Flux2 block's attention projection); 96 rows
-    spread over all 36 row tiles are checked against the oracle."""
+@pytest.mark.parametrize("config", [0, 1])
+def test_gemm_large_sampled_rows(orc, dev, config):
+    """4608 x 3072 x 3072 (a Flux2 block's attention projection); 88 rows
+    spread over every row tile are checked against the oracle."""
     M, N, K = 4608, 3072, 3072
     a = orc.randn(SEED + 219, (M, K))
     b = orc.randn(SEED + 220, (N, K), std=0.02)
-    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), out_dtype=torch.float32)
+    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16), out_dtype=torch.float32,
+                     config=config)
     torch.cuda.synchronize()
     rows = np.unique(np.concatenate([np.arange(0, M, 53), [M - 1]]))
     ref = orc.linear(orc.round_bf16(a[rows]), orc.round_bf16(b))
     assert_fp32(host(y)[rows], ref, what="gemm 4608x3072x3072")
+
+
+@pytest.mark.parametrize("config", [-1, 0, 1])
+def test_gemm_grouped(orc, dev, config):
+    """Five GEMMs of different N and K (and an empty one) in one launch, each
+    against the oracle: the q/k/v/gate/up pattern plus ragged edges."""
+    shapes = [(300, 256, 256), (300, 384, 256), (300, 136, 320), (300, 520, 128), (0, 64, 64), (47, 72, 64)]
+    items, refs = [], []
+    for i, (M, N, K) in enumerate(shapes):
+        a = orc.randn(SEED + 240 + i, (M, K))
+        b = orc.randn(SEED + 250 + i, (N, K), std=0.02)
+        items.append((dev_tensor(a, torch.bfloat16), dev_tensor(b, torch.bfloat16),
+                      torch.zeros((M, N), dtype=torch.float32, device="cuda")))
+        refs.append(orc.linear(orc.round_bf16(a), orc.round_bf16(b)) if M else np.zeros((0, N), np.float32))
+    outs = dit_hip.gemm_grouped(items, config=config)
+    torch.cuda.synchronize()
+    for (M, N, K), o, r in zip(shapes, outs, refs):
+        assert_fp32(host(o), r, what=f"grouped gemm {M}x{N}x{K}")
 
 
 def test_gemm_rejects_bad_shapes(dev):

@@ -1,0 +1,55 @@
+"""The full Flux2 transformer recorded through the C++ host modules and
+planned without a device (dit_cli --plan-only): graph size, the GEMM and
+attention node counts, the parameter count of the 4B-shaped configuration,
+and how many nodes each block type hands to fused kernels.
+
+Per single-stream block 30 nodes are absorbed: adaLN 2 (NORM, MUL), each of
+q and k 12 (RMS_NORM, MUL, 4 x (VIEW, ROPE), 2 inner CONCATs), SwiGLU 2
+(SIGMOID, MUL), gated residual 1 (MUL), GEMM accumulate 1 (MUL_MAT).  Per
+double-stream block 46: 4 adaLNs x 2, q and k 15 each (two RMS_NORM + MUL
+segments joined by the txt|img CONCAT, plus the RoPE tree), 2 SwiGLUs x 2,
+4 gated residuals x 1."""
+import json
+import os
+import subprocess
+
+import pytest
+
+from conftest import PKG
+
+CLI = os.path.join(PKG, "bin", "dit_cli")
+
+
+def plan(**kw):
+    if not os.path.exists(CLI):
+        pytest.skip("dit_cli not built")
+    args = [CLI, "Flux2Transformer2DModel", "--plan-only", "true"]
+    for k, v in kw.items():
+        args += ["--" + k, str(v)]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_full_step_graph():
+    p = plan()
+    # 2 time-embedding + 3 modulation + 2 embedder Linears, 5 x 14 double-block
+    # and 20 x 7 single-block projections, norm_out and proj_out
+    assert p["mul_mat_nodes"] == 2 + 3 + 2 + 5 * 14 + 20 * 7 + 2 == 219
+    assert p["attention_nodes"] == 25
+    assert p["params"] == 3859815936
+    assert p["arena_bytes"] < 1 << 30 and p["arena_bytes"] * 50 < p["naive_bytes"], p
+
+
+@pytest.mark.parametrize("kind,layers,nodes,fused,mm", [
+    ("single", dict(num_layers=0), 58, 30, 7),
+    ("double", dict(num_single_layers=0), 110, 46, 14),
+])
+def test_per_block_fusion(kind, layers, nodes, fused, mm):
+    key = "num_single_layers" if kind == "single" else "num_layers"
+    a = plan(**layers, **{key: 1})
+    b = plan(**layers, **{key: 2})
+    assert b["nodes"] - a["nodes"] == nodes
+    assert b["fused_nodes"] - a["fused_nodes"] == fused
+    assert b["mul_mat_nodes"] - a["mul_mat_nodes"] == mm
+    assert b["attention_nodes"] - a["attention_nodes"] == 1
