@@ -17,7 +17,7 @@
 namespace dit {
 namespace {
 
-template <typename T, int VPL>
+template <typename T, int VPL, bool FULL>
 __global__ __launch_bounds__(256) void adaln_wave_kernel(
     const T* __restrict__ x, int64_t xs, const float* __restrict__ shift,
     const float* __restrict__ scale, T* __restrict__ y, int64_t ys, int rows,
@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
-        if (active && vi < nvec) {
+        if (active && (FULL || vi < nvec)) {
             Io<T>::load(xr + (int64_t)vi * EPV, v[j]);
         } else {
 #pragma unroll
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
     float s2 = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-        if (lane + kWave * j < nvec) {
+        if (FULL || lane + kWave * j < nvec) {
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
                 const float d = v[j][e] - mean;
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
-        if (vi < nvec) {
+        if (FULL || vi < nvec) {
             float o[EPV];
 #pragma unroll
             for (int e = 0; e < EPV; e += 4) {
@@ -119,12 +119,16 @@ void launch_wave(const void* x, int64_t xs, const float* shift, const float* sca
                  int64_t ys, int rows, int nvec, int64_t cols, float eps, float addend,
                  hipStream_t st) {
     // One wave per row, four rows per workgroup; LDS holds the block's copy
-    // of (scale + addend, shift): 8 bytes per column.
+    // of (scale + addend, shift): 8 bytes per column.  FULL rows (every lane
+    // owns exactly VPL vectors) carry no bounds branches.
     const int blocks = (rows + 3) / 4;
     const size_t lds = (size_t)nvec * Io<T>::EPV * 2 * sizeof(float);
-    hipLaunchKernelGGL((adaln_wave_kernel<T, VPL>), dim3(blocks), dim3(256), lds, st,
-                       (const T*)x, xs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps,
-                       addend);
+    if (nvec == VPL * kWave)
+        hipLaunchKernelGGL((adaln_wave_kernel<T, VPL, true>), dim3(blocks), dim3(256), lds, st, (const T*)x, xs,
+                           shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps, addend);
+    else
+        hipLaunchKernelGGL((adaln_wave_kernel<T, VPL, false>), dim3(blocks), dim3(256), lds, st, (const T*)x, xs,
+                           shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps, addend);
 }
 
 template <typename T>

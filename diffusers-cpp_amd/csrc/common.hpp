@@ -75,6 +75,10 @@ template <> struct Io<float> {
     }
     __device__ __forceinline__ static float get(const float* p) { return *p; }
     __device__ __forceinline__ static void put(float* p, float v) { *p = v; }
+    __device__ __forceinline__ static void unpack(uint4 t, float* v) {
+        v[0] = __uint_as_float(t.x); v[1] = __uint_as_float(t.y);
+        v[2] = __uint_as_float(t.z); v[3] = __uint_as_float(t.w);
+    }
 };
 
 template <> struct Io<bf16> {
@@ -97,6 +101,12 @@ template <> struct Io<bf16> {
     }
     __device__ __forceinline__ static float get(const bf16* p) { return __uint_as_float((uint32_t)p->bits << 16); }
     __device__ __forceinline__ static void put(bf16* p, float v) { p->bits = (uint16_t)f32_to_bf16_bits(v); }
+    __device__ __forceinline__ static void unpack(uint4 t, float* v) {
+        v[0] = bf16_lo(t.x); v[1] = bf16_hi(t.x);
+        v[2] = bf16_lo(t.y); v[3] = bf16_hi(t.y);
+        v[4] = bf16_lo(t.z); v[5] = bf16_hi(t.z);
+        v[6] = bf16_lo(t.w); v[7] = bf16_hi(t.w);
+    }
 };
 
 // Explicitly rounded fp32 arithmetic: keeps the compiler from contracting
