@@ -319,10 +319,11 @@ void run_model(Session& s, const Args& a) {
         rt.set_output(*out);
         const ComputeStats& st = rt.plan();
         std::printf("{\"command\": \"Flux2Transformer2DModel\", \"plan_only\": true, \"nodes\": %d, "
-                    "\"fused_nodes\": %d, \"mul_mat_nodes\": %d, \"attention_nodes\": %d, "
+                    "\"fused_nodes\": %d, \"grouped_nodes\": %d, \"deferred_nodes\": %d, "
+                    "\"mul_mat_nodes\": %d, \"attention_nodes\": %d, "
                     "\"arena_bytes\": %zu, \"naive_bytes\": %zu, \"params\": %zu}\n",
-                    st.nodes, st.fused_nodes, st.mul_mat_nodes, st.attention_nodes, st.arena_bytes,
-                    st.naive_bytes, n_params);
+                    st.nodes, st.fused_nodes, st.grouped_nodes, st.deferred_nodes, st.mul_mat_nodes,
+                    st.attention_nodes, st.arena_bytes, st.naive_bytes, n_params);
         return;
     }
     if (a.has("random-weights")) {

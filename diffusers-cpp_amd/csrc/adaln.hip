@@ -91,6 +91,103 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
     }
 }
 
+// Gated residual feeding the next adaLN, in one pass over the row:
+//   r = h + gate * o           (Flux2SingleTransformerBlock.hpp:58, Flux2TransformerBlock.hpp:86-87, 100-101)
+//   y = (1 + scale) * LayerNorm(r) + shift   (the next block's adaLN, :50-54 / :91-92)
+// r is rounded to the I/O type before it is normalised, exactly as the
+// unfused graph stores the ADD node and the NORM node reads it back.  One
+// wave per row; (gate, 1 + scale, shift) staged in LDS per workgroup.
+template <typename T, int VPL, bool FULL>
+__global__ __launch_bounds__(256) void residual_adaln_kernel(
+    const T* __restrict__ h, int64_t hs, const T* __restrict__ o, int64_t os, const float* __restrict__ gate,
+    T* __restrict__ r_out, int64_t rs, const float* __restrict__ shift, const float* __restrict__ scale,
+    T* __restrict__ y, int64_t ys, int rows, int nvec, float cols_f, float eps, float addend) {
+    constexpr int EPV = Io<T>::EPV;
+    extern __shared__ float4 mod_lds[];  // per 4 columns: (gate, scale + addend, shift)
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const bool active = row < rows;
+
+    float hv[VPL][EPV], ov[VPL][EPV];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int vi = lane + kWave * j;
+        if (active && (FULL || vi < nvec)) {
+            Io<T>::load(h + (int64_t)row * hs + (int64_t)vi * EPV, hv[j]);
+            Io<T>::load(o + (int64_t)row * os + (int64_t)vi * EPV, ov[j]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) hv[j][e] = ov[j][e] = 0.f;
+        }
+    }
+    const int n4 = nvec * EPV / 4;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+        float4 sc = reinterpret_cast<const float4*>(scale)[i];
+        sc.x += addend; sc.y += addend; sc.z += addend; sc.w += addend;
+        mod_lds[3 * i] = reinterpret_cast<const float4*>(gate)[i];
+        mod_lds[3 * i + 1] = sc;
+        mod_lds[3 * i + 2] = reinterpret_cast<const float4*>(shift)[i];
+    }
+    __syncthreads();
+    if (!active) return;
+
+    // r = h + (o * gate), stored, and kept as the rounded value for the norm.
+    T* rr = r_out + (int64_t)row * rs;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int vi = lane + kWave * j;
+        if (FULL || vi < nvec) {
+#pragma unroll
+            for (int e = 0; e < EPV; e += 4) {
+                const float4 g = mod_lds[3 * ((vi * EPV + e) / 4)];
+                hv[j][e + 0] = add_rn(hv[j][e + 0], mul_rn(ov[j][e + 0], g.x));
+                hv[j][e + 1] = add_rn(hv[j][e + 1], mul_rn(ov[j][e + 1], g.y));
+                hv[j][e + 2] = add_rn(hv[j][e + 2], mul_rn(ov[j][e + 2], g.z));
+                hv[j][e + 3] = add_rn(hv[j][e + 3], mul_rn(ov[j][e + 3], g.w));
+            }
+            Io<T>::round(hv[j]);
+            Io<T>::store(rr + (int64_t)vi * EPV, hv[j]);
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) s += hv[j][e];
+        }
+    }
+    s = wave_sum(s);
+    const float mean = s / cols_f;
+    float s2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        if (FULL || lane + kWave * j < nvec) {
+#pragma unroll
+            for (int e = 0; e < EPV; ++e) {
+                const float d = hv[j][e] - mean;
+                hv[j][e] = d;
+                s2 += d * d;
+            }
+        }
+    }
+    s2 = wave_sum(s2);
+    const float rstd = 1.0f / sqrtf(s2 / cols_f + eps);
+    T* yr = y + (int64_t)row * ys;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int vi = lane + kWave * j;
+        if (FULL || vi < nvec) {
+            float out[EPV];
+#pragma unroll
+            for (int e = 0; e < EPV; e += 4) {
+                const int i4 = (vi * EPV + e) / 4;
+                const float4 t = mod_lds[3 * i4 + 1], sh = mod_lds[3 * i4 + 2];
+                out[e + 0] = add_rn(mul_rn(mul_rn(hv[j][e + 0], rstd), t.x), sh.x);
+                out[e + 1] = add_rn(mul_rn(mul_rn(hv[j][e + 1], rstd), t.y), sh.y);
+                out[e + 2] = add_rn(mul_rn(mul_rn(hv[j][e + 2], rstd), t.z), sh.z);
+                out[e + 3] = add_rn(mul_rn(mul_rn(hv[j][e + 3], rstd), t.w), sh.w);
+            }
+            Io<T>::store(yr + (int64_t)vi * EPV, out);
+        }
+    }
+}
+
 // Any cols / stride / alignment: one 256-thread block per row, LDS reductions.
 template <typename T>
 __global__ __launch_bounds__(256) void adaln_generic_kernel(
@@ -157,7 +254,65 @@ int run(const void* x, int64_t rows, int64_t cols, int64_t xs, const float* shif
     return check_launch("dt_adaln_mod");
 }
 
+template <typename T, int VPL>
+void launch_res(const void* h, int64_t hs, const void* o, int64_t os, const float* gate, void* r, int64_t rs,
+                const float* shift, const float* scale, void* y, int64_t ys, int rows, int nvec, int64_t cols,
+                float eps, float addend, hipStream_t st) {
+    const int blocks = (rows + 3) / 4;
+    const size_t lds = (size_t)nvec * Io<T>::EPV * 3 * sizeof(float);
+    if (nvec == VPL * kWave)
+        hipLaunchKernelGGL((residual_adaln_kernel<T, VPL, true>), dim3(blocks), dim3(256), lds, st, (const T*)h, hs,
+                           (const T*)o, os, gate, (T*)r, rs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps,
+                           addend);
+    else
+        hipLaunchKernelGGL((residual_adaln_kernel<T, VPL, false>), dim3(blocks), dim3(256), lds, st, (const T*)h,
+                           hs, (const T*)o, os, gate, (T*)r, rs, shift, scale, (T*)y, ys, rows, nvec, (float)cols,
+                           eps, addend);
+}
+
+template <typename T>
+int run_res(const void* h, int64_t hs, const void* o, int64_t os, const float* gate, void* r, int64_t rs,
+            const float* shift, const float* scale, float addend, void* y, int64_t ys, int64_t rows, int64_t cols,
+            float eps, hipStream_t st) {
+    constexpr int EPV = Io<T>::EPV;
+    const int64_t nvec = cols / EPV;
+    const bool fused = cols % EPV == 0 && hs % EPV == 0 && os % EPV == 0 && rs % EPV == 0 && ys % EPV == 0 &&
+                       aligned16(h) && aligned16(o) && aligned16(r) && aligned16(y) && aligned16(gate) &&
+                       aligned16(shift) && aligned16(scale) && nvec <= 16 * kWave && rows < (1ll << 31);
+    if (!fused) {
+        // rows the one-pass kernel does not take: the two launches it replaces
+        const int rc = dt_gated_residual(h, hs, o, os, gate, r, rs, rows, cols, Io<T>::kType, st);
+        if (rc) return rc;
+        return adaln_launch(r, rows, cols, rs, shift, scale, addend, y, ys, eps, Io<T>::kType, st);
+    }
+    const int vpl = (int)((nvec + kWave - 1) / kWave);
+    const int rw = (int)rows, nv = (int)nvec;
+    if (vpl <= 2) launch_res<T, 2>(h, hs, o, os, gate, r, rs, shift, scale, y, ys, rw, nv, cols, eps, addend, st);
+    else if (vpl <= 4) launch_res<T, 4>(h, hs, o, os, gate, r, rs, shift, scale, y, ys, rw, nv, cols, eps, addend, st);
+    else if (vpl <= 6) launch_res<T, 6>(h, hs, o, os, gate, r, rs, shift, scale, y, ys, rw, nv, cols, eps, addend, st);
+    else if (vpl <= 8) launch_res<T, 8>(h, hs, o, os, gate, r, rs, shift, scale, y, ys, rw, nv, cols, eps, addend, st);
+    else if (vpl <= 12)
+        launch_res<T, 12>(h, hs, o, os, gate, r, rs, shift, scale, y, ys, rw, nv, cols, eps, addend, st);
+    else launch_res<T, 16>(h, hs, o, os, gate, r, rs, shift, scale, y, ys, rw, nv, cols, eps, addend, st);
+    return check_launch("dt_gated_residual_adaln");
+}
+
 }  // namespace
+
+int residual_adaln_launch(const void* h, int64_t hs, const void* o, int64_t os, const float* gate, void* r,
+                          int64_t rs, const float* shift, const float* scale, float addend, void* y, int64_t ys,
+                          int64_t rows, int64_t cols, float eps, int32_t io, hipStream_t st) {
+    DT_REQUIRE(rows >= 0 && cols > 0, "dt_gated_residual_adaln: bad shape rows=%lld cols=%lld", (long long)rows,
+               (long long)cols);
+    DT_REQUIRE(hs >= cols && os >= cols && rs >= cols && ys >= cols,
+               "dt_gated_residual_adaln: stride smaller than cols");
+    DT_REQUIRE(is_io_type(io), "dt_gated_residual_adaln: io_type %d unsupported", io);
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(h && o && gate && r && shift && scale && y, "dt_gated_residual_adaln: null pointer");
+    if (io == DT_TYPE_F32)
+        return run_res<float>(h, hs, o, os, gate, r, rs, shift, scale, addend, y, ys, rows, cols, eps, st);
+    return run_res<bf16>(h, hs, o, os, gate, r, rs, shift, scale, addend, y, ys, rows, cols, eps, st);
+}
 
 int adaln_launch(const void* x, int64_t rows, int64_t cols, int64_t xs, const float* shift,
                  const float* scale, float addend, void* y, int64_t ys, float eps, int32_t io,
@@ -173,6 +328,14 @@ int adaln_launch(const void* x, int64_t rows, int64_t cols, int64_t xs, const fl
 }
 
 }  // namespace dit
+
+extern "C" int dt_gated_residual_adaln(const void* h, int64_t h_stride, const void* o, int64_t o_stride,
+                                       const float* gate, void* r, int64_t r_stride, const float* shift,
+                                       const float* scale, void* y, int64_t y_stride, int64_t rows, int64_t cols,
+                                       float eps, int32_t io_type, dt_stream_t stream) {
+    return dit::residual_adaln_launch(h, h_stride, o, o_stride, gate, r, r_stride, shift, scale, 1.0f, y, y_stride,
+                                      rows, cols, eps, io_type, (hipStream_t)stream);
+}
 
 extern "C" int dt_adaln_mod(const void* x, int64_t rows, int64_t cols, int64_t x_stride,
                             const float* shift, const float* scale, void* y, int64_t y_stride,

@@ -79,6 +79,8 @@ template <> struct Io<float> {
         v[0] = __uint_as_float(t.x); v[1] = __uint_as_float(t.y);
         v[2] = __uint_as_float(t.z); v[3] = __uint_as_float(t.w);
     }
+    // The values the type stores (identity for fp32).
+    __device__ __forceinline__ static void round(float*) {}
 };
 
 template <> struct Io<bf16> {
@@ -106,6 +108,11 @@ template <> struct Io<bf16> {
         v[2] = bf16_lo(t.y); v[3] = bf16_hi(t.y);
         v[4] = bf16_lo(t.z); v[5] = bf16_hi(t.z);
         v[6] = bf16_lo(t.w); v[7] = bf16_hi(t.w);
+    }
+    // The values the type stores: RNE to bf16 and back.
+    __device__ __forceinline__ static void round(float* v) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(f32_to_bf16_bits(v[e]) << 16);
     }
 };
 

@@ -10,45 +10,16 @@
 // the best of a sweep over U in {1,2,4,8} x {256,512,1024} threads.
 #include "capi_util.hpp"
 #include "common.hpp"
+#include "swiglu_body.hpp"
 
 namespace dit {
 namespace {
 
 constexpr int kBlock = 512;
 
-template <typename T, int U>
-__global__ __launch_bounds__(kBlock) void swiglu_kernel(const T* __restrict__ g, int64_t gs,
-                                                        const T* __restrict__ u, int64_t us,
-                                                        T* __restrict__ y, int64_t ys,
-                                                        uint32_t total, FastDiv nv) {
-    constexpr int EPV = Io<T>::EPV;
-    const uint32_t base = blockIdx.x * (kBlock * U) + threadIdx.x;
-    float gv[U][EPV], uv[U][EPV];
-    int64_t yo[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-        const uint32_t idx = base + k * kBlock;
-        yo[k] = -1;
-        if (idx < total) {
-            const uint32_t r = fdiv(idx, nv);
-            const uint32_t c = (idx - r * nv.d) * EPV;
-            Io<T>::load(g + r * gs + c, gv[k]);
-            Io<T>::load(u + r * us + c, uv[k]);
-            yo[k] = r * ys + c;
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-        if (yo[k] >= 0) {
-            float o[EPV];
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                const float s = sigmoid_ref(gv[k][e]);
-                o[e] = mul_rn(mul_rn(gv[k][e], s), uv[k][e]);
-            }
-            Io<T>::store(y + yo[k], o);
-        }
-    }
+template <typename T>
+__global__ __launch_bounds__(kBlock) void swiglu_kernel(SwigluArgs a) {
+    swiglu_body<T, kBlock>(a, blockIdx.x);
 }
 
 template <typename T, int U>
@@ -141,10 +112,9 @@ int run_swiglu(const void* g, int64_t gs, const void* u, int64_t us, void* y, in
     const bool vec = cols % EPV == 0 && gs % EPV == 0 && us % EPV == 0 && ys % EPV == 0 &&
                      aligned16(g) && aligned16(u) && aligned16(y) && total < (1ll << 31);
     if (vec) {
-        const int64_t blocks = (total + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-        hipLaunchKernelGGL((swiglu_kernel<T, kUnroll>), dim3((unsigned)blocks), dim3(kBlock), 0, st,
-                           (const T*)g, gs, (const T*)u, us, (T*)y, ys, (uint32_t)total,
-                           make_fastdiv((uint32_t)nvec));
+        const SwigluArgs a{g, gs, u, us, y, ys, (uint32_t)total, make_fastdiv((uint32_t)nvec)};
+        hipLaunchKernelGGL((swiglu_kernel<T>), dim3((unsigned)swiglu_blocks<T, kBlock>((uint32_t)total)), dim3(kBlock),
+                           0, st, a);
     } else {
         hipLaunchKernelGGL((swiglu_generic_kernel<T>), dim3(generic_blocks(rows * cols)), dim3(kBlock),
                            0, st, (const T*)g, gs, (const T*)u, us, (T*)y, ys, rows, cols);

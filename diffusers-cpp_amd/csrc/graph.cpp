@@ -6,6 +6,9 @@
 //   adaLN           ADD(MUL(NORM(x), t[c]), shift[c])
 //                   LayerNorm.cpp:17 + Flux2SingleTransformerBlock.hpp:53
 //   gated residual  ADD(h, MUL(o, gate[c]))          Flux2SingleTransformerBlock.hpp:58
+//   residual+adaLN  the adaLN chain whose x is a gated residual r: block i's
+//                   residual feeding block i+1's norm, one pass writing r and
+//                   the normalised output (r runs at the adaLN's position)
 //   SwiGLU          MUL(MUL(g, SIGMOID(g)), u)        Flux2SwiGLU.hpp:20, SiLU.hpp:12
 //   GroupNorm+SiLU  MUL(a, SIGMOID(a)), a = ADD(MUL(VIEW(NORM(VIEW(x))), w), b)
 //                   GroupNorm.cpp:98-156 + SiLU.hpp:12 (affine / SiLU optional)
@@ -96,7 +99,7 @@ bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
     return true;
 }
 
-enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD, K_GEMM_GROUP, K_DEFERRED };
+enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD, K_GEMM_GROUP, K_RES_ADALN, K_QK_SWIGLU, K_DEFERRED };
 
 struct QkSeg {
     const dt_tensor* q;   // RMS_NORM input
@@ -107,7 +110,7 @@ struct QkSeg {
 
 struct Plan {
     Kind kind = K_NONE;
-    const dt_tensor* in[4] = {nullptr, nullptr, nullptr, nullptr};
+    const dt_tensor* in[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     float eps = 0.f;
     int silu = 0;
     // QK
@@ -117,6 +120,10 @@ struct Plan {
     float base = 0.f;
     // GEMM group: every member MUL_MAT, the root first
     std::vector<const dt_tensor*> members;
+    // QK + SwiGLU: the k tensor's QK segment and root, the SwiGLU's inputs and root
+    QkSeg kseg{};
+    const dt_tensor* kroot = nullptr;
+    const dt_tensor* sw[3] = {nullptr, nullptr, nullptr};  // gate, up, output
 };
 
 struct Graph {
@@ -125,6 +132,9 @@ struct Graph {
     std::vector<char> claimed;
     std::vector<int> root;   // index of the node whose fused kernel absorbs node i
     std::vector<int> runs_at;  // position where node i's kernel runs
+    std::vector<char> deferred;  // node i keeps its output but runs inside another node's kernel
+    std::unordered_map<const dt_tensor*, std::vector<int>> consumers;
+    dt_tensor** nodes = nullptr;
     int current_root = -1;
 
     bool internal(const dt_tensor* t, int n_uses = 1) const {
@@ -140,6 +150,8 @@ struct Graph {
         root[i] = current_root;
     }
 };
+
+const dt_tensor* nodes_at(const Graph& g, int i) { return g.nodes[i]; }
 
 bool match_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     if (a->op != DT_OP_ADD) return false;
@@ -161,6 +173,70 @@ bool match_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     p.in[0] = x;
     p.in[1] = t;
     p.in[2] = sh;
+    p.eps = fparam(n, 0);
+    return true;
+}
+
+// Gated-residual operands of r = ADD(h, MUL(o, gate[c])) (either operand
+// order), with the MUL used only there.
+bool gated_parts(Graph& g, const dt_tensor* a, const dt_tensor** h_out, const dt_tensor** o_out,
+                 const dt_tensor** gate_out, const dt_tensor** m_out) {
+    if (a->op != DT_OP_ADD) return false;
+    for (int k = 1; k >= 0; --k) {
+        const dt_tensor* m = a->src[k];
+        const dt_tensor* h = a->src[1 - k];
+        if (!m || !h || m->op != DT_OP_MUL || !g.internal(m)) continue;
+        const dt_tensor* o = m->src[0];
+        const dt_tensor* gate = m->src[1];
+        int64_t r, s;
+        if (!is_vec(gate, a->ne[0]) || !same_shape(h, a) || !same_shape(o, a) ||
+            h->type != a->type || o->type != a->type || !is_io_type(a->type) ||
+            !row_layout(h, &r, &s) || !row_layout(o, &r, &s) || !row_layout(a, &r, &s))
+            continue;
+        *h_out = h;
+        *o_out = o;
+        *gate_out = gate;
+        *m_out = m;
+        return true;
+    }
+    return false;
+}
+
+// The adaLN chain ADD(MUL(NORM(r), t), shift) over a gated residual r that
+// is stored (read again later): one kernel writes r and the normalised
+// output at the adaLN's position.  Every other reader of r must come later.
+bool match_res_adaln(Graph& g, const dt_tensor* a, Plan& p) {
+    if (a->op != DT_OP_ADD) return false;
+    const dt_tensor* m = a->src[0];
+    const dt_tensor* sh = a->src[1];
+    if (!m || m->op != DT_OP_MUL || !g.internal(m)) return false;
+    const dt_tensor* n = m->src[0];
+    const dt_tensor* t = m->src[1];
+    if (!n || n->op != DT_OP_NORM || !g.internal(n)) return false;
+    const dt_tensor* x = n->src[0];
+    auto xi = g.index.find(x);
+    if (xi == g.index.end() || g.claimed[xi->second] || g.deferred[xi->second]) return false;
+    const int64_t cols = x->ne[0];
+    int64_t r1, s1, r2, s2;
+    if (!is_vec(t, cols) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
+        !is_io_type(x->type) || !row_layout(x, &r1, &s1) || !row_layout(a, &r2, &s2))
+        return false;
+    const dt_tensor *h, *o, *gate, *gm;
+    if (!gated_parts(g, x, &h, &o, &gate, &gm)) return false;
+    for (int c : g.consumers[x])
+        if (nodes_at(g, c) != n && c <= g.current_root) return false;
+    g.claim(m);
+    g.claim(n);
+    g.claim(gm);
+    g.deferred[xi->second] = 1;
+    g.runs_at[xi->second] = g.current_root;
+    p.kind = K_RES_ADALN;
+    p.in[0] = h;
+    p.in[1] = o;
+    p.in[2] = gate;
+    p.in[3] = x;
+    p.in[4] = t;
+    p.in[5] = sh;
     p.eps = fparam(n, 0);
     return true;
 }
@@ -523,6 +599,60 @@ void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
     }
 }
 
+// Forward pass over SwiGLU roots: with the two single-segment QK roots that
+// precede it (q and k of the same block) and inputs computed before the
+// first of them, the three run as one launch at the first QK's position
+// (dt_qk_rmsnorm_rope_swiglu).  The other two roots keep their outputs.
+void merge_qk_swiglu(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
+    auto ready_before = [&](const dt_tensor* t, int pos) {
+        while (t && t->op == DT_OP_VIEW) t = t->src[0];
+        if (!t) return false;
+        auto it = g.index.find(t);
+        return it == g.index.end() || g.runs_at[it->second] < pos;
+    };
+    auto move_to = [&](int root, int pos) {
+        plans[root].kind = K_DEFERRED;
+        g.runs_at[root] = pos;
+        for (int i = 0; i < n; ++i)
+            if (g.claimed[i] && g.root[i] == root) g.runs_at[i] = pos;
+    };
+    for (int sidx = 0; sidx < n; ++sidx) {
+        if (plans[sidx].kind != K_SWIGLU) continue;
+        int qk[2] = {-1, -1};
+        int found = 0;
+        for (int j = sidx - 1; j >= 0 && found < 2; --j)
+            if (plans[j].kind == K_QK) qk[found++] = j;
+        if (found < 2) continue;
+        const int qa = qk[1], qb = qk[0];  // qa first in order
+        Plan& A = plans[qa];
+        Plan& B = plans[qb];
+        const Plan& S = plans[sidx];
+        const dt_tensor* ya = nodes[qa];
+        const dt_tensor* yb = nodes[qb];
+        const dt_tensor* ys = nodes[sidx];
+        if (A.segs.size() != 1 || B.segs.size() != 1 || A.pos != B.pos || A.axis_dim != B.axis_dim ||
+            A.base != B.base || A.segs[0].eps != B.segs[0].eps || ya->type != yb->type || ys->type != ya->type)
+            continue;
+        const dt_tensor* qa_in = A.segs[0].q;
+        const dt_tensor* qb_in = B.segs[0].q;
+        bool same = true;
+        for (int d = 0; d < 4; ++d)
+            same = same && qa_in->ne[d] == qb_in->ne[d] && qa_in->nb[d] == qb_in->nb[d] && ya->nb[d] == yb->nb[d] &&
+                   ya->ne[d] == yb->ne[d];
+        if (!same || !ready_before(qb_in, qa) || !ready_before(B.segs[0].w, qa) || !ready_before(S.in[0], qa) ||
+            !ready_before(S.in[1], qa))
+            continue;
+        A.kind = K_QK_SWIGLU;
+        A.kseg = B.segs[0];
+        A.kroot = yb;
+        A.sw[0] = S.in[0];
+        A.sw[1] = S.in[1];
+        A.sw[2] = ys;
+        move_to(qb, qa);
+        move_to(sidx, qa);
+    }
+}
+
 int run_flash_attn(hipStream_t st, const dt_tensor* t) {
     const dt_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2];
     DT_REQUIRE(q && k && v && !t->src[3], "dt_graph_compute: FLASH_ATTN_EXT needs q, k, v and no mask");
@@ -615,6 +745,40 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
         case K_GEMM_GROUP:
             ++g_kernels;
             return run_gemm_group(st, p.members);
+        case K_QK_SWIGLU: {
+            const int es = elem_size(root->type);
+            const int n_axes = (int)p.pos.size();
+            RopeAxisPos ap{};
+            for (int a = 0; a < n_axes; ++a) {
+                ap.stride[a] = p.pos[a]->nb[0] / 4;
+                ap.ptr[a] = (const int32_t*)data_of(p.pos[a]);
+            }
+            const QkSeg& qs = p.segs[0];
+            const dt_tensor* q = qs.q;
+            int64_t rows, gs, us, ys;
+            row_layout(p.sw[0], &rows, &gs);
+            row_layout(p.sw[1], &rows, &us);
+            row_layout(p.sw[2], &rows, &ys);
+            ++g_kernels;
+            return qk_swiglu_launch(data_of(q), data_of(p.kseg.q), root->data, p.kroot->data,
+                                    (const float*)data_of(qs.w), (const float*)data_of(p.kseg.w), qs.tokens,
+                                    q->ne[1], q->ne[0], q->nb[2] / es, q->nb[1] / es, root->nb[2] / es,
+                                    root->nb[1] / es, qs.eps, ap, n_axes, p.axis_dim, p.base, nullptr, 0,
+                                    data_of(p.sw[0]), gs, data_of(p.sw[1]), us, p.sw[2]->data, ys, rows,
+                                    p.sw[2]->ne[0], root->type, st);
+        }
+        case K_RES_ADALN: {
+            int64_t rows, hs, os, rs, ys;
+            row_layout(p.in[0], &rows, &hs);
+            row_layout(p.in[1], &rows, &os);
+            row_layout(p.in[3], &rows, &rs);
+            row_layout(root, &rows, &ys);
+            ++g_kernels;
+            return residual_adaln_launch(data_of(p.in[0]), hs, data_of(p.in[1]), os, (const float*)data_of(p.in[2]),
+                                         p.in[3]->data, rs, (const float*)data_of(p.in[5]),
+                                         (const float*)data_of(p.in[4]), 0.0f, root->data, ys, rows, root->ne[0],
+                                         p.eps, root->type, st);
+        }
         case K_DEFERRED:
             return DT_OK;  // ran in its group's launch
         default:
@@ -688,7 +852,9 @@ namespace dit {
 namespace {
 
 int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& plans) {
+    g.nodes = nodes;
     g.claimed.assign(n_nodes, 0);
+    g.deferred.assign(n_nodes, 0);
     g.root.assign(n_nodes, -1);
     g.runs_at.resize(n_nodes);
     for (int i = 0; i < n_nodes; ++i) g.runs_at[i] = i;
@@ -696,23 +862,29 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
         DT_REQUIRE(nodes[i] != nullptr, "dt_graph: node %d is null", i);
         g.index[nodes[i]] = i;
         for (int s = 0; s < 4; ++s)
-            if (nodes[i]->src[s]) g.uses[nodes[i]->src[s]]++;
+            if (nodes[i]->src[s]) {
+                g.uses[nodes[i]->src[s]]++;
+                g.consumers[nodes[i]->src[s]].push_back(i);
+            }
     }
     plans.assign(n_nodes, Plan());
     for (int i = n_nodes - 1; i >= 0; --i) {
-        if (g.claimed[i]) continue;
+        if (g.claimed[i] || g.deferred[i]) continue;
         dt_tensor* t = nodes[i];
         Plan& p = plans[i];
         g.current_root = i;
-        if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_adaln(g, t, p) ||
+        if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_res_adaln(g, t, p) || match_adaln(g, t, p) ||
             match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p) ||
             match_gemm_add(g, t, p))
             continue;
         p = Plan();
     }
-    for (int i = 0; i < n_nodes; ++i)
+    for (int i = 0; i < n_nodes; ++i) {
         if (g.claimed[i]) g.runs_at[i] = g.root[i];
+        if (g.deferred[i]) plans[i].kind = K_DEFERRED;
+    }
     group_gemms(g, nodes, n_nodes, plans);
+    merge_qk_swiglu(g, nodes, n_nodes, plans);
     return DT_OK;
 }
 

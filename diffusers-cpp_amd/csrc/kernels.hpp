@@ -18,6 +18,12 @@ int adaln_launch(const void* x, int64_t rows, int64_t cols, int64_t xs, const fl
                  const float* scale, float addend, void* y, int64_t ys, float eps, int32_t io,
                  hipStream_t st);
 
+// r = h + gate * o; y = (r - mean) * rstd * (scale + addend) + shift per row,
+// with r rounded to the I/O type before it is normalised.
+int residual_adaln_launch(const void* h, int64_t hs, const void* o, int64_t os, const float* gate, void* r,
+                          int64_t rs, const float* shift, const float* scale, float addend, void* y, int64_t ys,
+                          int64_t rows, int64_t cols, float eps, int32_t io, hipStream_t st);
+
 constexpr int kMaxRopeAxes = 8;
 
 // Position of token t on axis a: ptr[a][t * stride[a]].
@@ -31,6 +37,14 @@ int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const floa
               int64_t in_hs, int64_t out_ts, int64_t out_hs, float eps, const RopeAxisPos& pos,
               int n_axes, int axis_dim, float freq_base, const float* table, int n_pos, int32_t io,
               hipStream_t st);
+
+// QK-RMSNorm+RoPE of q and k (qk_launch's arguments) and a SwiGLU over
+// gate/up rows -> y, in one launch when both take their fast paths.
+int qk_swiglu_launch(const void* q, const void* k, void* q_out, void* k_out, const float* wq, const float* wk,
+                     int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts, int64_t in_hs, int64_t out_ts,
+                     int64_t out_hs, float eps, const RopeAxisPos& pos, int n_axes, int axis_dim, float freq_base,
+                     const float* table, int n_pos, const void* g, int64_t gs, const void* u, int64_t us, void* y,
+                     int64_t ys, int64_t rows, int64_t cols, int32_t io, hipStream_t st);
 
 // Backend accessors (capi.cpp).
 hipStream_t backend_stream(dt_backend* be);

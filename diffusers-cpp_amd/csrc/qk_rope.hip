@@ -18,6 +18,7 @@
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "swiglu_body.hpp"
 
 namespace dit {
 namespace {
@@ -101,12 +102,10 @@ __device__ __forceinline__ void store8<float>(float* p, const float* v) {
 // once per wave, and all HPG head loads are in flight before the first
 // reduction.
 template <typename T, int HPG>
-__global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkShape sh,
-                                                         const float* __restrict__ table,
-                                                         int chunks) {
-    const QkHalf a = blockIdx.y == 0 ? q : k;
+__device__ __forceinline__ void qk_rope128_body(const QkHalf& a, const QkShape& sh, const float* __restrict__ table,
+                                                int chunks, int block) {
     if (a.x == nullptr) return;
-    const int wv = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const int wv = (int)((block * 256 + threadIdx.x) / kWave);
     if (wv >= sh.tokens * chunks) return;  // whole waves leave together
     const int lane16 = threadIdx.x & 15;
     const int row = (threadIdx.x & (kWave - 1)) >> 4;
@@ -169,6 +168,27 @@ __global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkS
     }
 }
 
+template <typename T, int HPG>
+__global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkShape sh,
+                                                         const float* __restrict__ table, int chunks) {
+    qk_rope128_body<T, HPG>(blockIdx.y == 0 ? q : k, sh, table, chunks, blockIdx.x);
+}
+
+// QK-RMSNorm+RoPE of q and k and the SwiGLU of the same block in one launch
+// (Flux2ParallelSelfAttention.hpp:55-93: all three read the outputs of the
+// block's input projections): blocks [0, qk_blocks) take q, the next
+// qk_blocks k, the rest stream the SwiGLU.  The bodies are the standalone
+// kernels', so the results are bit-identical to three separate launches.
+template <typename T, int HPG>
+__global__ __launch_bounds__(256) void qk_swiglu_kernel(QkHalf q, QkHalf k, QkShape sh, const float* __restrict__ table,
+                                                        int chunks, int qk_blocks, SwigluArgs sw) {
+    const int b = blockIdx.x;
+    if (b < 2 * qk_blocks)
+        qk_rope128_body<T, HPG>(b < qk_blocks ? q : k, sh, table, chunks, b < qk_blocks ? b : b - qk_blocks);
+    else
+        swiglu_body<T, 256>(sw, b - 2 * qk_blocks);
+}
+
 // Any head_dim / axis_dim (even) / stride: one thread per (token, head).
 template <typename T>
 __global__ __launch_bounds__(256) void qk_rope_generic_kernel(QkHalf q, QkHalf k, QkShape sh,
@@ -208,8 +228,10 @@ __global__ __launch_bounds__(256) void qk_rope_generic_kernel(QkHalf q, QkHalf k
     }
 }
 
+constexpr int kHPG = 3;  // 12 heads per wave: best of HPG in {1, 2, 3, 6} on [4608, 24, 128]
+
 template <typename T>
-int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t st) {
+bool qk_fast(const QkHalf& q, const QkHalf& k, const QkShape& sh, const float* table) {
     constexpr int EPV = Io<T>::EPV;
     bool fast = sh.head_dim == 128 && sh.axis_dim % 8 == 0 && sh.in_ts % EPV == 0 &&
                 sh.in_hs % EPV == 0 && sh.out_ts % EPV == 0 && sh.out_hs % EPV == 0 &&
@@ -220,9 +242,15 @@ int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t s
            (int64_t)sh.tokens * sh.heads < (1ll << 31);
     for (const QkHalf* h : {&q, &k})
         if (h->x) fast = fast && aligned16(h->x) && aligned16(h->y) && aligned16(h->w);
+    return fast;
+}
+
+template <typename T>
+int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t st) {
+    const bool fast = qk_fast<T>(q, k, sh, table);
     const int ny = k.x ? 2 : 1;
     if (fast) {
-        constexpr int HPG = 3;  // 12 heads per wave: best of HPG in {1, 2, 3, 6} on [4608, 24, 128]
+        constexpr int HPG = kHPG;
         const int chunks = (sh.heads + 4 * HPG - 1) / (4 * HPG);
         const int64_t waves = (int64_t)sh.tokens * chunks;
         const int64_t blocks = (waves + 3) / 4;
@@ -240,11 +268,71 @@ int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t s
 
 }  // namespace
 
+int qk_prepare(const void* q, const void* k, void* q_out, void* k_out, const float* wq, const float* wk,
+               int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts, int64_t in_hs, int64_t out_ts,
+               int64_t out_hs, float eps, const RopeAxisPos& pos, int n_axes, int axis_dim, float freq_base,
+               const float* table, int n_pos, int32_t io, QkHalf* hq_out, QkHalf* hk_out, QkShape* sh_out);
+
 int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const float* wq,
               const float* wk, int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts,
               int64_t in_hs, int64_t out_ts, int64_t out_hs, float eps, const RopeAxisPos& pos,
               int n_axes, int axis_dim, float freq_base, const float* table, int n_pos, int32_t io,
               hipStream_t st) {
+    QkHalf hq, hk;
+    QkShape sh;
+    const int rc = qk_prepare(q, k, q_out, k_out, wq, wk, tokens, heads, head_dim, in_ts, in_hs, out_ts, out_hs,
+                              eps, pos, n_axes, axis_dim, freq_base, table, n_pos, io, &hq, &hk, &sh);
+    if (rc) return rc;
+    if (tokens == 0 || (!q && !k)) return DT_OK;
+    if (io == DT_TYPE_F32) return run<float>(hq, hk, sh, table, st);
+    return run<bf16>(hq, hk, sh, table, st);
+}
+
+template <typename T>
+int run_qk_swiglu(const QkHalf& hq, const QkHalf& hk, const QkShape& sh, const float* table, const void* g,
+                  int64_t gs, const void* u, int64_t us, void* y, int64_t ys, int64_t rows, int64_t cols,
+                  hipStream_t st) {
+    constexpr int EPV = Io<T>::EPV;
+    const int64_t nvec = cols / EPV, total = rows * nvec;
+    const bool sw_vec = cols % EPV == 0 && gs % EPV == 0 && us % EPV == 0 && ys % EPV == 0 && aligned16(g) &&
+                        aligned16(u) && aligned16(y) && total < (1ll << 31);
+    if (!sw_vec || !hq.x || !hk.x || sh.tokens == 0 || !qk_fast<T>(hq, hk, sh, table)) {
+        // shapes the combined kernel does not take: the two launches it replaces
+        int rc = run<T>(hq, hk, sh, table, st);
+        if (rc) return rc;
+        return dt_swiglu(g, gs, u, us, y, ys, rows, cols, Io<T>::kType, st);
+    }
+    const int chunks = (sh.heads + 4 * kHPG - 1) / (4 * kHPG);
+    const int64_t qk_blocks = ((int64_t)sh.tokens * chunks + 3) / 4;
+    const int64_t blocks = 2 * qk_blocks + swiglu_blocks<T, 256>((uint32_t)total);
+    DT_REQUIRE(blocks < (1ll << 31), "dt_qk_rmsnorm_rope_swiglu: grid too large");
+    const SwigluArgs sw{g, gs, u, us, y, ys, (uint32_t)total, make_fastdiv((uint32_t)(nvec ? nvec : 1))};
+    hipLaunchKernelGGL((qk_swiglu_kernel<T, kHPG>), dim3((unsigned)blocks), dim3(256), 0, st, hq, hk, sh, table,
+                       chunks, (int)qk_blocks, sw);
+    return check_launch("dt_qk_rmsnorm_rope_swiglu");
+}
+
+int qk_swiglu_launch(const void* q, const void* k, void* q_out, void* k_out, const float* wq, const float* wk,
+                     int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts, int64_t in_hs, int64_t out_ts,
+                     int64_t out_hs, float eps, const RopeAxisPos& pos, int n_axes, int axis_dim, float freq_base,
+                     const float* table, int n_pos, const void* g, int64_t gs, const void* u, int64_t us, void* y,
+                     int64_t ys, int64_t rows, int64_t cols, int32_t io, hipStream_t st) {
+    QkHalf hq, hk;
+    QkShape sh;
+    const int rc = qk_prepare(q, k, q_out, k_out, wq, wk, tokens, heads, head_dim, in_ts, in_hs, out_ts, out_hs,
+                              eps, pos, n_axes, axis_dim, freq_base, table, n_pos, io, &hq, &hk, &sh);
+    if (rc) return rc;
+    DT_REQUIRE(rows >= 0 && cols > 0 && gs >= cols && us >= cols && ys >= cols,
+               "dt_qk_rmsnorm_rope_swiglu: bad SwiGLU shape");
+    DT_REQUIRE(rows == 0 || (g && u && y), "dt_qk_rmsnorm_rope_swiglu: null SwiGLU pointer");
+    if (io == DT_TYPE_F32) return run_qk_swiglu<float>(hq, hk, sh, table, g, gs, u, us, y, ys, rows, cols, st);
+    return run_qk_swiglu<bf16>(hq, hk, sh, table, g, gs, u, us, y, ys, rows, cols, st);
+}
+
+int qk_prepare(const void* q, const void* k, void* q_out, void* k_out, const float* wq, const float* wk,
+               int64_t tokens, int64_t heads, int64_t head_dim, int64_t in_ts, int64_t in_hs, int64_t out_ts,
+               int64_t out_hs, float eps, const RopeAxisPos& pos, int n_axes, int axis_dim, float freq_base,
+               const float* table, int n_pos, int32_t io, QkHalf* hq_out, QkHalf* hk_out, QkShape* sh_out) {
     DT_REQUIRE(is_io_type(io), "dt_qk_rmsnorm_rope: io_type %d unsupported", io);
     DT_REQUIRE(tokens >= 0 && heads > 0 && head_dim > 0 && head_dim % 2 == 0,
                "dt_qk_rmsnorm_rope: bad shape");
@@ -257,9 +345,10 @@ int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const floa
     DT_REQUIRE(tokens < (1ll << 31) && heads < (1ll << 31) && head_dim < (1ll << 31),
                "dt_qk_rmsnorm_rope: shape too large");
     DT_REQUIRE(n_pos >= 0, "dt_qk_rmsnorm_rope: n_pos < 0");
-    if (tokens == 0 || (!q && !k)) return DT_OK;
-    for (int a = 0; a < n_axes; ++a)
-        DT_REQUIRE(pos.ptr[a] != nullptr, "dt_qk_rmsnorm_rope: null position pointer for axis %d", a);
+    if (tokens > 0 && (q || k)) {
+        for (int a = 0; a < n_axes; ++a)
+            DT_REQUIRE(pos.ptr[a] != nullptr, "dt_qk_rmsnorm_rope: null position pointer for axis %d", a);
+    }
     DT_REQUIRE(!q || (q_out && wq), "dt_qk_rmsnorm_rope: q given without q_out/wq");
     DT_REQUIRE(!k || (k_out && wk), "dt_qk_rmsnorm_rope: k given without k_out/wk");
     QkHalf hq{q, q_out, wq}, hk{k, k_out, wk};
@@ -276,8 +365,10 @@ int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const floa
     sh.axis_dim = axis_dim; sh.n_axes = n_axes; sh.n_pos = table ? n_pos : 0;
     sh.eps = eps;
     sh.theta_scale = powf(freq_base, -2.0f / (float)axis_dim);
-    if (io == DT_TYPE_F32) return run<float>(hq, hk, sh, table, st);
-    return run<bf16>(hq, hk, sh, table, st);
+    *hq_out = hq;
+    *hk_out = hk;
+    *sh_out = sh;
+    return DT_OK;
 }
 
 }  // namespace dit
@@ -318,4 +409,26 @@ extern "C" int dt_qk_rmsnorm_rope(const void* q, const void* k, void* q_out, voi
     return dit::qk_launch(q, k, q_out, k_out, wq, wk, tokens, heads, head_dim, in_tok_stride,
                           in_head_stride, out_tok_stride, out_head_stride, eps, ap, n_axes,
                           axis_dim, freq_base, rope_table, n_pos, io_type, (hipStream_t)stream);
+}
+
+extern "C" int dt_qk_rmsnorm_rope_swiglu(const void* q, const void* k, void* q_out, void* k_out, int64_t tokens,
+                                         int64_t heads, int64_t head_dim, int64_t in_tok_stride,
+                                         int64_t in_head_stride, int64_t out_tok_stride, int64_t out_head_stride,
+                                         const float* wq, const float* wk, float eps, const int32_t* pos,
+                                         int64_t pos_stride, int32_t n_axes, int32_t axis_dim, float freq_base,
+                                         const float* rope_table, int32_t n_pos, const void* gate,
+                                         int64_t gate_stride, const void* up, int64_t up_stride, void* y,
+                                         int64_t y_stride, int64_t rows, int64_t inner, int32_t io_type,
+                                         dt_stream_t stream) {
+    DT_REQUIRE(n_axes > 0 && n_axes <= dit::kMaxRopeAxes, "dt_qk_rmsnorm_rope_swiglu: n_axes %d", n_axes);
+    DT_REQUIRE(pos_stride >= n_axes, "dt_qk_rmsnorm_rope_swiglu: pos_stride < n_axes");
+    dit::RopeAxisPos ap{};
+    for (int a = 0; a < n_axes; ++a) {
+        ap.ptr[a] = pos ? pos + a : nullptr;
+        ap.stride[a] = pos_stride;
+    }
+    return dit::qk_swiglu_launch(q, k, q_out, k_out, wq, wk, tokens, heads, head_dim, in_tok_stride, in_head_stride,
+                                 out_tok_stride, out_head_stride, eps, ap, n_axes, axis_dim, freq_base, rope_table,
+                                 n_pos, gate, gate_stride, up, up_stride, y, y_stride, rows, inner, io_type,
+                                 (hipStream_t)stream);
 }

@@ -65,6 +65,14 @@ _SIGS = {
                             c_int64, c_int32, _S]),
     "dt_gated_residual": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
                                     c_int64, c_int64, c_int64, c_int32, _S]),
+    "dt_qk_rmsnorm_rope_swiglu": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                            c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
+                                            c_void_p, c_float, c_void_p, c_int64, c_int32, c_int32,
+                                            c_float, c_void_p, c_int32, c_void_p, c_int64, c_void_p,
+                                            c_int64, c_void_p, c_int64, c_int64, c_int64, c_int32, _S]),
+    "dt_gated_residual_adaln": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p,
+                                          c_int64, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+                                          c_int64, c_float, c_int32, _S]),
     "dt_dequant": (c_int32, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
                              c_int32, _S]),
     "dt_groupnorm_workspace_bytes": (c_size_t, [c_int64, c_int64, c_int64, c_int64]),
@@ -255,6 +263,27 @@ def qk_rmsnorm_rope(q, k, wq, wk, pos, axis_dim, freq_base, eps=1e-6, table=None
     return q_out, k_out
 
 
+def qk_rmsnorm_rope_swiglu(q, k, wq, wk, pos, axis_dim, freq_base, gate, up, eps=1e-6, table=None,
+                           q_out=None, k_out=None, out=None):
+    """qk_rmsnorm_rope(q, k) and swiglu(gate, up) in one launch -> (q_out, k_out, y)."""
+    torch = _torch()
+    tokens, heads, head_dim = q.shape
+    q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device) if q_out is None else q_out
+    k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device) if k_out is None else k_out
+    y = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device) if out is None else out
+    if q.stride() != k.stride() or q_out.stride() != k_out.stride():
+        raise DtError("q and k (and their outputs) must share strides")
+    rows, inner, gs = _rows(gate)
+    us, ys = _rows(up)[2], _rows(y)[2]
+    n_pos = 0 if table is None else table.shape[0]
+    check(load().dt_qk_rmsnorm_rope_swiglu(
+        _p(q), _p(k), _p(q_out), _p(k_out), tokens, heads, head_dim, q.stride(0), q.stride(1),
+        q_out.stride(0), q_out.stride(1), _p(wq), _p(wk), eps, _p(pos), pos.stride(0), pos.shape[1],
+        axis_dim, freq_base, _p(table), n_pos, _p(gate), gs, _p(up), us, _p(y), ys, rows, inner,
+        io_type(q), stream()), "dt_qk_rmsnorm_rope_swiglu")
+    return q_out, k_out, y
+
+
 def swiglu(gate, up, out=None):
     torch = _torch()
     rows, cols, gs = _rows(gate)
@@ -275,6 +304,20 @@ def gated_residual(h, o, gate, out=None):
     check(load().dt_gated_residual(_p(h), hs, _p(o), os_, _p(gate), _p(y), ys, rows, cols,
                                    io_type(h), stream()), "dt_gated_residual")
     return y
+
+
+def gated_residual_adaln(h, o, gate, shift, scale, eps=1e-6, r_out=None, out=None):
+    """r = h + gate * o; y = (1 + scale) * LayerNorm(r) + shift -> (r, y)."""
+    torch = _torch()
+    rows, cols, hs = _rows(h)
+    os_ = _rows(o)[2]
+    r = torch.empty(h.shape, dtype=h.dtype, device=h.device) if r_out is None else r_out
+    y = torch.empty(h.shape, dtype=h.dtype, device=h.device) if out is None else out
+    rs, ys = _rows(r)[2], _rows(y)[2]
+    check(load().dt_gated_residual_adaln(_p(h), hs, _p(o), os_, _p(gate), _p(r), rs, _p(shift), _p(scale),
+                                         _p(y), ys, rows, cols, eps, io_type(h), stream()),
+          "dt_gated_residual_adaln")
+    return r, y
 
 
 def block_bytes(qtype: int) -> tuple[int, int]:

@@ -563,9 +563,11 @@ void HipRuntime::prepare(bool allocate) {
     stats_.arena_bytes = planner.peak();
     stats_.naive_bytes = naive;
     stats_.fused_nodes = 0;
-    stats_.mul_mat_nodes = stats_.attention_nodes = 0;
+    stats_.mul_mat_nodes = stats_.attention_nodes = stats_.grouped_nodes = stats_.deferred_nodes = 0;
     for (int i = 0; i < n; ++i) {
         stats_.fused_nodes += fused_into[i] >= 0;
+        stats_.grouped_nodes += fused_into[i] < 0 && runs_at[i] < i;
+        stats_.deferred_nodes += fused_into[i] < 0 && runs_at[i] > i;
         stats_.mul_mat_nodes += order_[i]->op == DT_OP_MUL_MAT;
         stats_.attention_nodes += order_[i]->op == DT_OP_FLASH_ATTN_EXT;
     }

@@ -127,6 +127,8 @@ struct ComputeStats {
     int fused_nodes = 0;
     int mul_mat_nodes = 0;
     int attention_nodes = 0;
+    int grouped_nodes = 0;      // run inside an earlier node's launch (grouped GEMMs)
+    int deferred_nodes = 0;     // stored outputs computed by a later node's fused kernel
     size_t arena_bytes = 0;     // op-node memory after liveness reuse
     size_t naive_bytes = 0;     // the same nodes without reuse or fusion
 };

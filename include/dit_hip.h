@@ -128,6 +128,35 @@ int dt_gated_residual(const void *h, int64_t h_stride, const void *o, int64_t o_
                       const float *gate, void *y, int64_t y_stride,
                       int64_t rows, int64_t cols, int32_t io_type, dt_stream_t stream);
 
+/* dt_qk_rmsnorm_rope (q and k) and dt_swiglu in one launch: the three
+ * elementwise ops a Flux2 single-stream block applies to the outputs of its
+ * input projections (Flux2ParallelSelfAttention.hpp:55-93), which are all
+ * ready at once.  Arguments are those of the two functions; results are
+ * bit-identical to calling them separately (which is what happens for
+ * shapes the combined kernel does not take). */
+int dt_qk_rmsnorm_rope_swiglu(const void *q, const void *k, void *q_out, void *k_out, int64_t tokens,
+                              int64_t heads, int64_t head_dim, int64_t in_tok_stride,
+                              int64_t in_head_stride, int64_t out_tok_stride, int64_t out_head_stride,
+                              const float *wq, const float *wk, float eps, const int32_t *pos,
+                              int64_t pos_stride, int32_t n_axes, int32_t axis_dim, float freq_base,
+                              const float *rope_table, int32_t n_pos, const void *gate,
+                              int64_t gate_stride, const void *up, int64_t up_stride, void *y,
+                              int64_t y_stride, int64_t rows, int64_t inner, int32_t io_type,
+                              dt_stream_t stream);
+
+/* Gated residual and the next adaLN in one pass (fused across a block
+ * boundary): r = h + gate * o (Flux2SingleTransformerBlock.hpp:58,
+ * Flux2TransformerBlock.hpp:86-87, 100-101), then y = (1 + scale) *
+ * LayerNorm_eps(r) + shift (the next block's adaLN, Flux2SingleTransformerBlock.hpp:50-54,
+ * Flux2TransformerBlock.hpp:63-72, 91-92).  r is written, rounded to io_type,
+ * and that rounded value is what is normalised, as in the unfused graph.
+ * gate, shift, scale: fp32 [cols].  Rows 16-byte aligned, cols % 8 == 0
+ * (bf16) or % 4 (fp32), cols <= 4096 (bf16) / 2048 (fp32). */
+int dt_gated_residual_adaln(const void *h, int64_t h_stride, const void *o, int64_t o_stride,
+                            const float *gate, void *r, int64_t r_stride, const float *shift,
+                            const float *scale, void *y, int64_t y_stride, int64_t rows, int64_t cols,
+                            float eps, int32_t io_type, dt_stream_t stream);
+
 /* Weight dequantisation to dst_type (DT_TYPE_BF16 or DT_TYPE_F32).
  * qtype DT_TYPE_Q8_0 (cols % 32 == 0) or DT_TYPE_Q4_K (cols % 256 == 0);
  * ggml blocks run along cols (ne0); row r starts at src + r*row_bytes.

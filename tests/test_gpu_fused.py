@@ -175,6 +175,42 @@ def test_qk_generic_toy_shape_and_out_of_table_positions(orc, dev, dtype):
     check(host(xo2), orc.qk_rmsnorm_rope(as_input(x2, dtype), w2, pos2, 32, 10000.0, 1e-6), dtype, "off")
 
 
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("n_txt,grid,heads,head_dim,inner", [
+    (512, 64, 24, 128, 9216),   # single-stream block: q, k [4608, 24, 128], gate/up [4608, 9216]
+    (7, 3, 2, 128, 40),         # ragged: 16 tokens, SwiGLU rows not a multiple of the block
+    (3, 2, 4, 8, 6),            # head_dim 8: the generic QK path, two launches
+])
+def test_qk_rmsnorm_rope_swiglu(orc, dev, dtype, n_txt, grid, heads, head_dim, inner):
+    """q and k QK-RMSNorm+RoPE plus the block's SwiGLU in one launch: every
+    output bit-identical to the separate kernels, and within tolerance of
+    the oracle."""
+    pos = flux_positions(n_txt, grid)
+    S = pos.shape[0]
+    axis_dim = head_dim // 4
+    print(f"qk+swiglu S={S} H={heads} D={head_dim} inner={inner} {dtype}", flush=True)
+    q = orc.randn(SEED + 32, (S, heads, head_dim))
+    k = orc.randn(SEED + 33, (S, heads, head_dim))
+    wq = orc.randn(SEED + 34, (head_dim,), mean=1.0, std=0.02)
+    wk = orc.randn(SEED + 35, (head_dim,), mean=1.0, std=0.02)
+    gu = orc.randn(SEED + 36, (S, 2 * inner))
+    dq, dk, dgu = dev_tensor(q, dtype), dev_tensor(k, dtype), dev_tensor(gu, dtype)
+    dwq, dwk = dev_tensor(wq, torch.float32), dev_tensor(wk, torch.float32)
+    pt = torch.from_numpy(pos).cuda()
+    tab = dit_hip.rope_table(512, axis_dim, 10000.0)
+    qo, ko, y = dit_hip.qk_rmsnorm_rope_swiglu(dq, dk, dwq, dwk, pt, axis_dim, 10000.0,
+                                               dgu[:, :inner], dgu[:, inner:], 1e-6, table=tab)
+    qs, ks = dit_hip.qk_rmsnorm_rope(dq, dk, dwq, dwk, pt, axis_dim, 10000.0, 1e-6, table=tab)
+    ys = dit_hip.swiglu(dgu[:, :inner], dgu[:, inner:])
+    torch.cuda.synchronize()
+    assert torch.equal(qo, qs) and torch.equal(ko, ks), "fused q/k differ from the QK kernel"
+    assert torch.equal(y, ys), "fused SwiGLU differs from the SwiGLU kernel"
+    check(host(qo), orc.qk_rmsnorm_rope(as_input(q, dtype), wq, pos, axis_dim, 10000.0, 1e-6), dtype, "q")
+    check(host(ko), orc.qk_rmsnorm_rope(as_input(k, dtype), wk, pos, axis_dim, 10000.0, 1e-6), dtype, "k")
+    g, u = as_input(gu[:, :inner], dtype), as_input(gu[:, inner:], dtype)
+    check(host(y), orc.swiglu(g, u), dtype, "swiglu")
+
+
 # ------------------------------------------------------------------ SwiGLU ----
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("rows,inner", [(4608, 9216), (33, 3072), (5, 7)])
@@ -203,6 +239,34 @@ def test_gated_residual(orc, dev, dtype, rows, cols):
     dit_hip.gated_residual(hd, dev_tensor(o, dtype), dev_tensor(g, torch.float32), out=hd)  # in place
     torch.cuda.synchronize()
     check(host(hd), ref, dtype, "gated in-place")
+
+
+@pytest.mark.parametrize("dtype", DT)
+@pytest.mark.parametrize("rows,cols", [(4608, 3072), (77, 3072), (40, 1000), (9, 512), (6, 6144), (5, 8192),
+                                       (7, 1001)])
+def test_gated_residual_adaln(orc, dev, dtype, rows, cols):
+    """Block i's residual r = h + gate * o feeding block i+1's adaLN, one
+    pass.  Reference: the oracle's gated residual, rounded to the I/O type as
+    the stored ADD node is, then the oracle's adaLN of that r.  Rows of 8192
+    fp32 and 1001 columns take the two-launch path."""
+    print(f"residual+adaln rows={rows} cols={cols} {dtype}", flush=True)
+    h = orc.randn(SEED + 27, (rows, cols))
+    o = orc.randn(SEED + 28, (rows, cols))
+    g = orc.randn(SEED + 29, (cols,), std=0.1)
+    sh = orc.randn(SEED + 30, (cols,), std=0.1)
+    sc = orc.randn(SEED + 31, (cols,), std=0.1)
+    f = lambda a: dev_tensor(a, torch.float32)
+    r, y = dit_hip.gated_residual_adaln(dev_tensor(h, dtype), dev_tensor(o, dtype), f(g), f(sh), f(sc), 1e-6)
+    torch.cuda.synchronize()
+    r_ref = orc.gated_residual(as_input(h, dtype), as_input(o, dtype), g)
+    check(host(r), r_ref, dtype, "residual")
+    r_stored = as_input(r_ref, dtype)
+    # the stored r must be bit-identical to the standalone gated residual kernel
+    r_alone = dit_hip.gated_residual(dev_tensor(h, dtype), dev_tensor(o, dtype), f(g))
+    torch.cuda.synchronize()
+    assert torch.equal(r, r_alone), "fused residual differs from the standalone kernel"
+    check(host(y), orc.adaln(host(r), sh, sc, 1e-6), dtype, "adaln of r")
+    check(host(y), orc.adaln(r_stored, sh, sc, 1e-6), dtype, "adaln of oracle r", one_rounding=False)
 
 
 @pytest.mark.parametrize("dtype", DT)

@@ -41,11 +41,18 @@ def test_full_step_graph():
     assert p["arena_bytes"] < 1 << 30 and p["arena_bytes"] * 50 < p["naive_bytes"], p
 
 
-@pytest.mark.parametrize("kind,layers,nodes,fused,mm", [
-    ("single", dict(num_layers=0), 58, 30, 7),
-    ("double", dict(num_single_layers=0), 110, 46, 14),
+@pytest.mark.parametrize("kind,layers,nodes,fused,mm,grouped,deferred", [
+    ("single", dict(num_layers=0), 58, 30, 7, 6, 1),
+    ("double", dict(num_single_layers=0), 110, 46, 14, 8, 4),
 ])
-def test_per_block_fusion(kind, layers, nodes, fused, mm):
+def test_per_block_fusion(kind, layers, nodes, fused, mm, grouped, deferred):
+    """A second block adds its nodes, fusions and GEMMs; `grouped` roots run
+    in an earlier node's launch (single: k, v, gate, up with q's projection,
+    and k's QK-RMSNorm+RoPE and the SwiGLU with q's QK-RMSNorm+RoPE; double:
+    k, v and the three txt projections with q, up with gate on each stream,
+    to_out with to_add_out), and `deferred` residuals are written by the next
+    adaLN's fused kernel (one per block boundary: single 1; double 2 inside
+    the block and 2 at the boundary)."""
     key = "num_single_layers" if kind == "single" else "num_layers"
     a = plan(**layers, **{key: 1})
     b = plan(**layers, **{key: 2})
@@ -53,3 +60,5 @@ def test_per_block_fusion(kind, layers, nodes, fused, mm):
     assert b["fused_nodes"] - a["fused_nodes"] == fused
     assert b["mul_mat_nodes"] - a["mul_mat_nodes"] == mm
     assert b["attention_nodes"] - a["attention_nodes"] == 1
+    assert b["grouped_nodes"] - a["grouped_nodes"] == grouped
+    assert b["deferred_nodes"] - a["deferred_nodes"] == deferred
