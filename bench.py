@@ -1,25 +1,28 @@
 """Benchmark of the fused Flux2 DiT elementwise chain on one MI355X.
 
-Workload (one "step" = one pass of the chain over one synthetic batch, all
-inputs resident in HBM, bf16 activations, fp32 math):
-  adaLN            x[4608, 3072] -> (1 + scale) * LayerNorm(x) + shift
-  QK-RMSNorm+RoPE  q, k [4608, 24, 128], 4 axes x 32 dims, theta 1e4,
-                   positions: 512 text tokens [0,0,0,l] then a 64x64 image grid
-  SwiGLU           gate | up = [4608, 18432] -> [4608, 9216]
-  gated residual   h + gate * o, [4608, 3072]
+Workload (one "step" = the elementwise work of one Flux2 single-stream
+block between its GEMMs, over one synthetic batch, all inputs resident in
+HBM, bf16 activations, fp32 math), as two fused launches in block order:
+  gated residual + adaLN   r = h + gate * o (the previous block's residual,
+                           stored) and y = (1 + scale) * LayerNorm(r) + shift
+                           (this block's modulated norm), h, o [4608, 3072]
+  QK-RMSNorm+RoPE + SwiGLU q, k [4608, 24, 128], 4 axes x 32 dims, theta 1e4,
+                           positions: 512 text tokens [0,0,0,l] then a 64x64
+                           image grid; gate | up = [4608, 18432] -> [4608, 9216]
 Algorithmic bytes per step: every distinct input read once and every output
 written once at its I/O dtype (broadcast vectors and tables counted once).
 
 Timed steps rotate through NSETS independent buffer sets (about 1.9 GB in
 all, far above the 256 MB last-level cache), so every step reads its inputs
 from HBM.  Three schedules of the same step are timed: eager launches, a
-HIP graph of the four launches, and a HIP graph whose independent launches
-(adaLN, QK, SwiGLU) sit on parallel branches with the gated residual joined
-after adaLN; `value` = whole-step algorithmic GB/s of the fastest (all
-three are reported).  `roofline` is the
-dominant kernel (SwiGLU) timed alone with HIP events on the stream it is
-launched on; `cpu_baseline` is the oracle's C restatement of the same chain
-(fp32, OpenMP) on a bounded sample, timed on this host's cores.
+HIP graph of the two launches, and a HIP graph with the two launches on
+parallel branches; `value` = whole-step algorithmic GB/s of the fastest
+(all three are reported).  The same block order with the four standalone
+kernels (gated residual, adaLN of r, QK, SwiGLU) is timed as a graph for
+comparison.  `roofline` is the dominant launch (QK+SwiGLU) timed alone
+with HIP events on the stream it is launched on; `cpu_baseline` is the
+oracle's C restatement of the same chain (fp32, OpenMP) on a bounded
+sample, timed on this host's cores.
 
 `sec_per_denoise_step` is one full Flux2-klein-4B-shaped transformer step
 (5 double + 20 single blocks, hidden 3072, 24x128 heads, 4096 image tokens of
@@ -48,12 +51,16 @@ N_TXT, GRID = 512, 64
 
 
 def alg_bytes():
+    """Algorithmic bytes of the two fused launches of a step and of the four
+    standalone kernels they replace."""
     e = 2  # bf16
-    ad = 2 * S * D * e + 2 * D * 4                 # x in, y out, shift/scale fp32
-    qk = 4 * S * H * HD * e + 2 * HD * 4 + S * 4 * 4 + 512 * 32 * 4  # q,k in/out, w, pos, table
-    sw = 3 * S * I * e                              # gate, up in; out
-    gr = 3 * S * D * e + D * 4                      # h, o in; y out; gate
-    return {"adaln": ad, "qk_rmsnorm_rope": qk, "swiglu": sw, "gated_residual": gr}
+    qk = 4 * S * H * HD * e + 2 * HD * 4 + S * 4 * 4 + N_TXT * 32 * 4  # q,k in/out, w, pos, table
+    sw = 3 * S * I * e                                                # gate, up in; out
+    fused = {"residual_adaln": 4 * S * D * e + 3 * D * 4,              # h, o in; r, y out; 3 vectors
+             "qk_swiglu": qk + sw}
+    standalone = {"gated_residual": 3 * S * D * e + D * 4, "adaln": 2 * S * D * e + 2 * D * 4,
+                  "qk_rmsnorm_rope": qk, "swiglu": sw}
+    return fused, standalone
 
 
 def positions():
@@ -74,31 +81,44 @@ def make_inputs(torch, dev, seed=0x5EED0000):
     import dit_hip
     pos = torch.from_numpy(positions()).to(dev)
     return {
-        "x": rn((S, D)), "shift": rn((D,), 0.1, dtype=torch.float32),
-        "scale": rn((D,), 0.1, dtype=torch.float32),
+        "h": rn((S, D)), "o": rn((S, D)), "gate": rn((D,), 0.1, dtype=torch.float32),
+        "shift": rn((D,), 0.1, dtype=torch.float32), "scale": rn((D,), 0.1, dtype=torch.float32),
         "q": rn((S, H, HD)), "k": rn((S, H, HD)),
         "wq": rn((HD,), 0.02, 1.0, torch.float32), "wk": rn((HD,), 0.02, 1.0, torch.float32),
         "pos": pos, "table": dit_hip.rope_table(N_TXT, 32, 10000.0, device=dev),
-        "gu": rn((S, 2 * I)), "h": rn((S, D)), "gate": rn((D,), 0.1, dtype=torch.float32),
+        "gu": rn((S, 2 * I)),
+        "r": torch.empty((S, D), dtype=torch.bfloat16, device=dev),
         "y": torch.empty((S, D), dtype=torch.bfloat16, device=dev),
         "qo": torch.empty((S, H, HD), dtype=torch.bfloat16, device=dev),
         "ko": torch.empty((S, H, HD), dtype=torch.bfloat16, device=dev),
         "sw": torch.empty((S, I), dtype=torch.bfloat16, device=dev),
-        "r": torch.empty((S, D), dtype=torch.bfloat16, device=dev),
     }
 
 
 def chain_kernels(t):
+    """The step's two fused launches, in block order."""
     import dit_hip
     gu = t["gu"]
     return {
-        "adaln": lambda: dit_hip.adaln_mod(t["x"], t["shift"], t["scale"], 1e-6, out=t["y"]),
+        "residual_adaln": lambda: dit_hip.gated_residual_adaln(
+            t["h"], t["o"], t["gate"], t["shift"], t["scale"], 1e-6, r_out=t["r"], out=t["y"]),
+        "qk_swiglu": lambda: dit_hip.qk_rmsnorm_rope_swiglu(
+            t["q"], t["k"], t["wq"], t["wk"], t["pos"], 32, 10000.0, gu[:, :I], gu[:, I:], 1e-6,
+            table=t["table"], q_out=t["qo"], k_out=t["ko"], out=t["sw"]),
+    }
+
+
+def standalone_kernels(t):
+    """The same step as the four standalone kernels, in block order."""
+    import dit_hip
+    gu = t["gu"]
+    return {
+        "gated_residual": lambda: dit_hip.gated_residual(t["h"], t["o"], t["gate"], out=t["r"]),
+        "adaln": lambda: dit_hip.adaln_mod(t["r"], t["shift"], t["scale"], 1e-6, out=t["y"]),
         "qk_rmsnorm_rope": lambda: dit_hip.qk_rmsnorm_rope(
             t["q"], t["k"], t["wq"], t["wk"], t["pos"], 32, 10000.0, 1e-6, table=t["table"],
             q_out=t["qo"], k_out=t["ko"]),
         "swiglu": lambda: dit_hip.swiglu(gu[:, :I], gu[:, I:], out=t["sw"]),
-        # o = the adaLN output (any [S, D] bf16 activation)
-        "gated_residual": lambda: dit_hip.gated_residual(t["h"], t["y"], t["gate"], out=t["r"]),
     }
 
 
@@ -185,24 +205,24 @@ def cpu_baseline(budget_s):
 
     seed = oracle.tensor_seed
     pos = positions()
-    x = oracle.round_bf16(oracle.randn(seed(0), (S, D)))
-    sh = oracle.randn(seed(1), (D,), std=0.1)
-    sc = oracle.randn(seed(2), (D,), std=0.1)
-    q = oracle.round_bf16(oracle.randn(seed(3), (S, H, HD)))
-    k = oracle.round_bf16(oracle.randn(seed(4), (S, H, HD)))
-    w = oracle.randn(seed(5), (HD,), mean=1.0, std=0.02)
-    g = oracle.round_bf16(oracle.randn(seed(6), (S, I)))
-    u = oracle.round_bf16(oracle.randn(seed(7), (S, I)))
-    h = oracle.round_bf16(oracle.randn(seed(8), (S, D)))
-    gate = oracle.randn(seed(9), (D,), std=0.1)
-    total = sum(alg_bytes().values())
+    h = oracle.round_bf16(oracle.randn(seed(0), (S, D)))
+    o = oracle.round_bf16(oracle.randn(seed(1), (S, D)))
+    gate = oracle.randn(seed(2), (D,), std=0.1)
+    sh = oracle.randn(seed(3), (D,), std=0.1)
+    sc = oracle.randn(seed(4), (D,), std=0.1)
+    q = oracle.round_bf16(oracle.randn(seed(5), (S, H, HD)))
+    k = oracle.round_bf16(oracle.randn(seed(6), (S, H, HD)))
+    w = oracle.randn(seed(7), (HD,), mean=1.0, std=0.02)
+    g = oracle.round_bf16(oracle.randn(seed(8), (S, I)))
+    u = oracle.round_bf16(oracle.randn(seed(9), (S, I)))
+    total = sum(alg_bytes()[0].values())
 
     def chain(threads):
-        y = oracle.adaln(x, sh, sc, 1e-6, threads)
+        r = oracle.round_bf16(oracle.gated_residual(h, o, gate, threads))
+        oracle.adaln(r, sh, sc, 1e-6, threads)
         oracle.qk_rmsnorm_rope(q, w, pos, 32, 10000.0, 1e-6, threads)
         oracle.qk_rmsnorm_rope(k, w, pos, 32, 10000.0, 1e-6, threads)
         oracle.swiglu(g, u, threads)
-        oracle.gated_residual(h, y, gate, threads)
 
     def measure(threads, budget):
         times = []
@@ -221,8 +241,9 @@ def cpu_baseline(budget_s):
     threads = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
     t_all, n_all = measure(threads, budget_s)
     t_4, n_4 = measure(4, budget_s / 2)
-    sample = (f"full chain at the GPU workload's shape, median of {n_all} runs "
-              f"({threads} threads) / {n_4} runs (4 threads, ggml's default n_threads)")
+    sample = (f"full chain (gated residual, adaLN of r, QK of q and k, SwiGLU) at the GPU workload's "
+              f"shape, median of {n_all} runs ({threads} threads) / {n_4} runs (4 threads, ggml's "
+              f"default n_threads)")
     return total / t_all / 1e9, threads, sample, total / t_4 / 1e9
 
 
@@ -323,77 +344,86 @@ def main():
 
     eager_s, _ = timed(step)
 
-    # One captured graph per buffer set: the four launches of a step.
-    graphs = []
-    side = torch.cuda.Stream()
-    side.wait_stream(st)
-    with torch.cuda.stream(side):
+    def capture(fn):
+        """One HIP graph per buffer set of fn(i)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(st)
+        with torch.cuda.stream(side):
+            for i in range(NSETS):
+                fn(i)
+        st.wait_stream(side)
+        torch.cuda.synchronize()
+        out = []
         for i in range(NSETS):
-            step(i)
-    st.wait_stream(side)
-    torch.cuda.synchronize()
-    for i in range(NSETS):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(i)
-        graphs.append(g)
-    for i in range(args.warmup):
-        graphs[i % NSETS].replay()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn(i)
+            out.append(g)
+        for i in range(args.warmup):
+            out[i % NSETS].replay()
+        return out
+
+    # The step's two launches captured back to back.
+    graphs = capture(step)
     seq_s, seq_wall = timed(lambda i: graphs[i % NSETS].replay())
 
-    # The same step as a graph with parallel branches: adaLN, QK and SwiGLU
-    # are independent; the gated residual consumes the adaLN output.
+    # The same step with the two (independent) launches on parallel branches.
+    branch_stream = torch.cuda.Stream()
+
     def branched(i):
         c = chains[i % NSETS]
         main = torch.cuda.current_stream()
-        s1, s2 = branch_streams
-        s1.wait_stream(main)
-        s2.wait_stream(main)
-        with torch.cuda.stream(s1):
-            c["qk_rmsnorm_rope"]()
-        with torch.cuda.stream(s2):
-            c["swiglu"]()
-        c["adaln"]()
-        c["gated_residual"]()
-        main.wait_stream(s1)
-        main.wait_stream(s2)
+        branch_stream.wait_stream(main)
+        with torch.cuda.stream(branch_stream):
+            c["qk_swiglu"]()
+        c["residual_adaln"]()
+        main.wait_stream(branch_stream)
 
-    branch_streams = (torch.cuda.Stream(), torch.cuda.Stream())
-    bgraphs = []
-    for i in range(NSETS):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            branched(i)
-        bgraphs.append(g)
-    for i in range(args.warmup):
-        bgraphs[i % NSETS].replay()
+    bgraphs = capture(branched)
     br_s, br_wall = timed(lambda i: bgraphs[i % NSETS].replay())
     schedules = {"eager": eager_s, "graph": seq_s, "graph_branched": br_s}
     best = min(schedules, key=schedules.get)
     step_s = schedules[best]
     wall = {"eager": None, "graph": seq_wall, "graph_branched": br_wall}[best]
 
-    ab = alg_bytes()
-    total = sum(ab.values())
+    # Block order with the four standalone kernels, as a graph, for comparison.
+    singles = [standalone_kernels(t) for t in sets]
+
+    def unfused(i):
+        for f in singles[i % NSETS].values():
+            f()
+
+    ugraphs = capture(unfused)
+    unfused_s, _ = timed(lambda i: ugraphs[i % NSETS].replay())
+    del graphs, bgraphs, ugraphs
+
+    fused_ab, single_ab = alg_bytes()
+    total = sum(fused_ab.values())
     flush = Flusher(torch, dev)
-    kernels = {}
-    for name in chains[0]:
-        tk = time_cold(torch, chains[0][name], 20, flush)
-        kernels[name] = {"us": round(tk * 1e6, 2), "alg_MB": round(ab[name] / 1e6, 2),
+
+    def cold(fns, ab):
+        res = {}
+        for name, fn in fns.items():
+            tk = time_cold(torch, fn, 20, flush)
+            res[name] = {"us": round(tk * 1e6, 2), "alg_MB": round(ab[name] / 1e6, 2),
                          "GBs": round(ab[name] / tk / 1e9, 1),
                          "frac_hbm": round(ab[name] / tk / 1e9 / HBM_PEAK_GBS, 3)}
+        return res
+
+    kernels = cold(chains[0], fused_ab)
+    kernels_standalone = cold(singles[0], single_ab)
     ceiling = copy_ceiling(torch, dev, flush)
     extra = secondary(torch, dev, flush) if args.secondary else None
 
-    dom = "swiglu"
+    dom = "qk_swiglu"
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "swiglu_4608x9216_bf16_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "qk_swiglu_4608_bf16_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
     roofline = {"bound": "hbm", "achieved": kernels[dom]["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(kernels[dom]["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "swiglu_kernel<bf16,2>", "alg_bytes_per_launch": ab[dom]}
+                "kernel": "qk_swiglu_kernel<bf16,3>", "alg_bytes_per_launch": fused_ab[dom]}
 
     cpu = None
     if args.cpu_budget > 0:
@@ -417,16 +447,19 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.1) modulation vectors)",
-        "config": {"workload": "Flux2 DiT elementwise chain, bf16: adaLN x[4608,3072] + "
-                               "QK-RMSNorm+4-axis RoPE q,k[4608,24,128] + SwiGLU [4608,18432]->"
-                               "[4608,9216] + gated residual [4608,3072]",
+        "config": {"workload": "Flux2 single-stream block elementwise chain, bf16, two fused launches: "
+                               "gated residual + adaLN h,o[4608,3072] -> r,y; QK-RMSNorm+4-axis RoPE "
+                               "q,k[4608,24,128] + SwiGLU [4608,18432]->[4608,9216]",
                    "alg_bytes_per_step": total, "buffer_sets": NSETS,
                    "parallelism": "none (1 GPU)"},
+        "unfused_graph_ms_per_step": round(unfused_s * 1e3, 4),
+        "unfused_alg_bytes_per_step": sum(single_ab.values()),
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "sec_per_denoise_step": denoise["s_per_step"] if denoise else None,
         "denoise_step": denoise,
         "copy_ceiling_GBs": round(ceiling, 1),
         "kernels": kernels,
+        "kernels_standalone": kernels_standalone,
         "secondary": extra,
         "roofline": roofline,
         "cpu_baseline": cpu,

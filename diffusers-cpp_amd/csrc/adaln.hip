@@ -3,13 +3,15 @@
 // the node chain LayerNorm::forward + `(1 + scale) * n + shift` emits in
 // Flux2SingleTransformerBlock.hpp:50-54 / Flux2TransformerBlock.hpp:63-72.
 //
-// Fast path: one wave64 per row.  The row is held in VGPRs (one HBM read,
-// one HBM write, both non-temporal) with all of its 16-byte loads issued
-// back to back, the mean and the centred variance are two wave-wide DPP
-// reductions over registers, and while the row loads are in flight each
-// workgroup stages the fp32 (1 + scale, shift) vectors, shared by every row,
-// into LDS (24 KB at 3072 columns).  The small register footprint lets every
-// row of a Flux2 activation ([4608, 3072]) be resident at once.
+// Fast path: one wave64 per row.  The row is held in VGPRs as its raw
+// 16-byte vectors (bf16 stays packed: 24 VGPRs for 3072 columns) with all of
+// its loads issued back to back and each value unpacked where it is used;
+// the mean and the centred variance are two wave-wide DPP reductions, and
+// while the row loads are in flight each workgroup stages the fp32
+// (1 + scale, shift) vectors, shared by every row, into LDS (24 KB at 3072
+// columns).  Registers and LDS are sized so that every row of a Flux2
+// activation ([4608, 3072]) is resident at once: a row that waits for a
+// second round of workgroups costs a full memory latency at the tail.
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -17,8 +19,8 @@
 namespace dit {
 namespace {
 
-template <typename T, int VPL, bool FULL>
-__global__ __launch_bounds__(256) void adaln_wave_kernel(
+template <typename T, int VPL, bool FULL, int WPB>
+__global__ __launch_bounds__(WPB * kWave) void adaln_wave_kernel(
     const T* __restrict__ x, int64_t xs, const float* __restrict__ shift,
     const float* __restrict__ scale, T* __restrict__ y, int64_t ys, int rows,
     int nvec, float cols_f, float eps, float addend) {
@@ -26,29 +28,22 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
     // (scale + addend, shift) interleaved per 4 columns: [nvec * EPV / 4][8].
     extern __shared__ float4 mod_lds[];
     const int lane = threadIdx.x & (kWave - 1);
-    const int r = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const int r = (int)(blockIdx.x * WPB + threadIdx.x / kWave);
     const bool active = r < rows;
     const T* xr = x + (int64_t)r * xs;
     T* yr = y + (int64_t)r * ys;
 
     // The whole row is in flight at once: VPL independent 16-byte loads.
-    float v[VPL][EPV];
-    float s = 0.f;
+    uint4 raw[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
-        if (active && (FULL || vi < nvec)) {
-            Io<T>::load(xr + (int64_t)vi * EPV, v[j]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) v[j][e] = 0.f;
-        }
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) s += v[j][e];
+        raw[j] = make_uint4(0, 0, 0, 0);
+        if (active && (FULL || vi < nvec)) raw[j] = ld_stream(xr + (int64_t)vi * EPV);
     }
     // Meanwhile the workgroup stages the modulation vectors (L2 hits) in LDS.
     const int n4 = nvec * EPV / 4;
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+    for (int i = threadIdx.x; i < n4; i += WPB * kWave) {
         float4 sc = reinterpret_cast<const float4*>(scale)[i];
         sc.x += addend; sc.y += addend; sc.z += addend; sc.w += addend;
         mod_lds[2 * i] = sc;
@@ -56,16 +51,25 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
     }
     __syncthreads();
     if (!active) return;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        float v[EPV];
+        Io<T>::unpack(raw[j], v);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) s += v[e];
+    }
     s = wave_sum(s);
     const float mean = s / cols_f;
     float s2 = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         if (FULL || lane + kWave * j < nvec) {
+            float v[EPV];
+            Io<T>::unpack(raw[j], v);
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
-                const float d = v[j][e] - mean;
-                v[j][e] = d;
+                const float d = v[e] - mean;
                 s2 += d * d;
             }
         }
@@ -76,17 +80,18 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
         if (FULL || vi < nvec) {
-            float o[EPV];
+            float v[EPV], o[EPV];
+            Io<T>::unpack(raw[j], v);
 #pragma unroll
             for (int e = 0; e < EPV; e += 4) {
                 const int i4 = (vi * EPV + e) / 4;
                 const float4 t = mod_lds[2 * i4], sh = mod_lds[2 * i4 + 1];
-                o[e + 0] = add_rn(mul_rn(mul_rn(v[j][e + 0], rstd), t.x), sh.x);
-                o[e + 1] = add_rn(mul_rn(mul_rn(v[j][e + 1], rstd), t.y), sh.y);
-                o[e + 2] = add_rn(mul_rn(mul_rn(v[j][e + 2], rstd), t.z), sh.z);
-                o[e + 3] = add_rn(mul_rn(mul_rn(v[j][e + 3], rstd), t.w), sh.w);
+                o[e + 0] = add_rn(mul_rn(mul_rn(v[e + 0] - mean, rstd), t.x), sh.x);
+                o[e + 1] = add_rn(mul_rn(mul_rn(v[e + 1] - mean, rstd), t.y), sh.y);
+                o[e + 2] = add_rn(mul_rn(mul_rn(v[e + 2] - mean, rstd), t.z), sh.z);
+                o[e + 3] = add_rn(mul_rn(mul_rn(v[e + 3] - mean, rstd), t.w), sh.w);
             }
-            Io<T>::store(yr + (int64_t)vi * EPV, o);
+            st_stream(yr + (int64_t)vi * EPV, Io<T>::pack(o));
         }
     }
 }
@@ -96,32 +101,33 @@ __global__ __launch_bounds__(256) void adaln_wave_kernel(
 //   y = (1 + scale) * LayerNorm(r) + shift   (the next block's adaLN, :50-54 / :91-92)
 // r is rounded to the I/O type before it is normalised, exactly as the
 // unfused graph stores the ADD node and the NORM node reads it back.  One
-// wave per row; (gate, 1 + scale, shift) staged in LDS per workgroup.
-template <typename T, int VPL, bool FULL>
-__global__ __launch_bounds__(256) void residual_adaln_kernel(
+// wave per row; h and o arrive as raw vectors and are replaced by the stored
+// r (for bf16 the stored bits are exactly the rounded value); (gate,
+// 1 + scale, shift) staged in LDS per workgroup (36 KB at 3072 columns, so
+// six rows per workgroup keep 4608 rows resident).
+template <typename T, int VPL, bool FULL, int WPB>
+__global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residual_adaln_kernel(
     const T* __restrict__ h, int64_t hs, const T* __restrict__ o, int64_t os, const float* __restrict__ gate,
     T* __restrict__ r_out, int64_t rs, const float* __restrict__ shift, const float* __restrict__ scale,
     T* __restrict__ y, int64_t ys, int rows, int nvec, float cols_f, float eps, float addend) {
     constexpr int EPV = Io<T>::EPV;
     extern __shared__ float4 mod_lds[];  // per 4 columns: (gate, scale + addend, shift)
     const int lane = threadIdx.x & (kWave - 1);
-    const int row = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const int row = (int)(blockIdx.x * WPB + threadIdx.x / kWave);
     const bool active = row < rows;
 
-    float hv[VPL][EPV], ov[VPL][EPV];
+    uint4 hr[VPL], orw[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
+        hr[j] = orw[j] = make_uint4(0, 0, 0, 0);
         if (active && (FULL || vi < nvec)) {
-            Io<T>::load(h + (int64_t)row * hs + (int64_t)vi * EPV, hv[j]);
-            Io<T>::load(o + (int64_t)row * os + (int64_t)vi * EPV, ov[j]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) hv[j][e] = ov[j][e] = 0.f;
+            hr[j] = ld_stream(h + (int64_t)row * hs + (int64_t)vi * EPV);
+            orw[j] = ld_stream(o + (int64_t)row * os + (int64_t)vi * EPV);
         }
     }
     const int n4 = nvec * EPV / 4;
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+    for (int i = threadIdx.x; i < n4; i += WPB * kWave) {
         float4 sc = reinterpret_cast<const float4*>(scale)[i];
         sc.x += addend; sc.y += addend; sc.z += addend; sc.w += addend;
         mod_lds[3 * i] = reinterpret_cast<const float4*>(gate)[i];
@@ -131,25 +137,29 @@ __global__ __launch_bounds__(256) void residual_adaln_kernel(
     __syncthreads();
     if (!active) return;
 
-    // r = h + (o * gate), stored, and kept as the rounded value for the norm.
+    // r = h + (o * gate), stored; its stored bits replace h in registers.
     T* rr = r_out + (int64_t)row * rs;
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
         if (FULL || vi < nvec) {
+            float hv[EPV], ov[EPV];
+            Io<T>::unpack(hr[j], hv);
+            Io<T>::unpack(orw[j], ov);
 #pragma unroll
             for (int e = 0; e < EPV; e += 4) {
                 const float4 g = mod_lds[3 * ((vi * EPV + e) / 4)];
-                hv[j][e + 0] = add_rn(hv[j][e + 0], mul_rn(ov[j][e + 0], g.x));
-                hv[j][e + 1] = add_rn(hv[j][e + 1], mul_rn(ov[j][e + 1], g.y));
-                hv[j][e + 2] = add_rn(hv[j][e + 2], mul_rn(ov[j][e + 2], g.z));
-                hv[j][e + 3] = add_rn(hv[j][e + 3], mul_rn(ov[j][e + 3], g.w));
+                hv[e + 0] = add_rn(hv[e + 0], mul_rn(ov[e + 0], g.x));
+                hv[e + 1] = add_rn(hv[e + 1], mul_rn(ov[e + 1], g.y));
+                hv[e + 2] = add_rn(hv[e + 2], mul_rn(ov[e + 2], g.z));
+                hv[e + 3] = add_rn(hv[e + 3], mul_rn(ov[e + 3], g.w));
             }
-            Io<T>::round(hv[j]);
-            Io<T>::store(rr + (int64_t)vi * EPV, hv[j]);
+            hr[j] = Io<T>::pack(hv);
+            st_stream(rr + (int64_t)vi * EPV, hr[j]);
+            Io<T>::unpack(hr[j], hv);
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) s += hv[j][e];
+            for (int e = 0; e < EPV; ++e) s += hv[e];
         }
     }
     s = wave_sum(s);
@@ -158,10 +168,11 @@ __global__ __launch_bounds__(256) void residual_adaln_kernel(
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         if (FULL || lane + kWave * j < nvec) {
+            float v[EPV];
+            Io<T>::unpack(hr[j], v);
 #pragma unroll
             for (int e = 0; e < EPV; ++e) {
-                const float d = hv[j][e] - mean;
-                hv[j][e] = d;
+                const float d = v[e] - mean;
                 s2 += d * d;
             }
         }
@@ -173,17 +184,18 @@ __global__ __launch_bounds__(256) void residual_adaln_kernel(
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
         if (FULL || vi < nvec) {
-            float out[EPV];
+            float v[EPV], out[EPV];
+            Io<T>::unpack(hr[j], v);
 #pragma unroll
             for (int e = 0; e < EPV; e += 4) {
                 const int i4 = (vi * EPV + e) / 4;
                 const float4 t = mod_lds[3 * i4 + 1], sh = mod_lds[3 * i4 + 2];
-                out[e + 0] = add_rn(mul_rn(mul_rn(hv[j][e + 0], rstd), t.x), sh.x);
-                out[e + 1] = add_rn(mul_rn(mul_rn(hv[j][e + 1], rstd), t.y), sh.y);
-                out[e + 2] = add_rn(mul_rn(mul_rn(hv[j][e + 2], rstd), t.z), sh.z);
-                out[e + 3] = add_rn(mul_rn(mul_rn(hv[j][e + 3], rstd), t.w), sh.w);
+                out[e + 0] = add_rn(mul_rn(mul_rn(v[e + 0] - mean, rstd), t.x), sh.x);
+                out[e + 1] = add_rn(mul_rn(mul_rn(v[e + 1] - mean, rstd), t.y), sh.y);
+                out[e + 2] = add_rn(mul_rn(mul_rn(v[e + 2] - mean, rstd), t.z), sh.z);
+                out[e + 3] = add_rn(mul_rn(mul_rn(v[e + 3] - mean, rstd), t.w), sh.w);
             }
-            Io<T>::store(yr + (int64_t)vi * EPV, out);
+            st_stream(yr + (int64_t)vi * EPV, Io<T>::pack(out));
         }
     }
 }
@@ -218,14 +230,15 @@ void launch_wave(const void* x, int64_t xs, const float* shift, const float* sca
     // One wave per row, four rows per workgroup; LDS holds the block's copy
     // of (scale + addend, shift): 8 bytes per column.  FULL rows (every lane
     // owns exactly VPL vectors) carry no bounds branches.
-    const int blocks = (rows + 3) / 4;
+    constexpr int WPB = 4;
+    const int blocks = (rows + WPB - 1) / WPB;
     const size_t lds = (size_t)nvec * Io<T>::EPV * 2 * sizeof(float);
     if (nvec == VPL * kWave)
-        hipLaunchKernelGGL((adaln_wave_kernel<T, VPL, true>), dim3(blocks), dim3(256), lds, st, (const T*)x, xs,
-                           shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps, addend);
+        hipLaunchKernelGGL((adaln_wave_kernel<T, VPL, true, WPB>), dim3(blocks), dim3(WPB * kWave), lds, st,
+                           (const T*)x, xs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps, addend);
     else
-        hipLaunchKernelGGL((adaln_wave_kernel<T, VPL, false>), dim3(blocks), dim3(256), lds, st, (const T*)x, xs,
-                           shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps, addend);
+        hipLaunchKernelGGL((adaln_wave_kernel<T, VPL, false, WPB>), dim3(blocks), dim3(WPB * kWave), lds, st,
+                           (const T*)x, xs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps, addend);
 }
 
 template <typename T>
@@ -258,16 +271,19 @@ template <typename T, int VPL>
 void launch_res(const void* h, int64_t hs, const void* o, int64_t os, const float* gate, void* r, int64_t rs,
                 const float* shift, const float* scale, void* y, int64_t ys, int rows, int nvec, int64_t cols,
                 float eps, float addend, hipStream_t st) {
-    const int blocks = (rows + 3) / 4;
+    // Six rows per workgroup: with (gate, 1 + scale, shift) in LDS, 12 bytes
+    // per column, four workgroups of six rows fit a CU at 3072 columns.
+    constexpr int WPB = 6;
+    const int blocks = (rows + WPB - 1) / WPB;
     const size_t lds = (size_t)nvec * Io<T>::EPV * 3 * sizeof(float);
     if (nvec == VPL * kWave)
-        hipLaunchKernelGGL((residual_adaln_kernel<T, VPL, true>), dim3(blocks), dim3(256), lds, st, (const T*)h, hs,
-                           (const T*)o, os, gate, (T*)r, rs, shift, scale, (T*)y, ys, rows, nvec, (float)cols, eps,
-                           addend);
+        hipLaunchKernelGGL((residual_adaln_kernel<T, VPL, true, WPB>), dim3(blocks), dim3(WPB * kWave), lds, st,
+                           (const T*)h, hs, (const T*)o, os, gate, (T*)r, rs, shift, scale, (T*)y, ys, rows, nvec,
+                           (float)cols, eps, addend);
     else
-        hipLaunchKernelGGL((residual_adaln_kernel<T, VPL, false>), dim3(blocks), dim3(256), lds, st, (const T*)h,
-                           hs, (const T*)o, os, gate, (T*)r, rs, shift, scale, (T*)y, ys, rows, nvec, (float)cols,
-                           eps, addend);
+        hipLaunchKernelGGL((residual_adaln_kernel<T, VPL, false, WPB>), dim3(blocks), dim3(WPB * kWave), lds, st,
+                           (const T*)h, hs, (const T*)o, os, gate, (T*)r, rs, shift, scale, (T*)y, ys, rows, nvec,
+                           (float)cols, eps, addend);
 }
 
 template <typename T>

@@ -20,15 +20,27 @@ struct bf16 {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Round-to-nearest-even fp32 -> bf16 bits; NaN stays NaN (quiet bit set).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+// Round-to-nearest-even fp32 -> bf16 by gfx950's packed convert
+// (v_cvt_pk_bf16_f32): ties to even, a NaN keeps its upper payload bits with
+// the quiet bit set -- (u >> 16) | 0x40, ggml's fp32 -> bf16 rule.  Checked
+// bit for bit against that integer formulation over all 2^32 fp32 patterns,
+// in both halves of the pair.
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const f32x2_cvt v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_cvt));
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16x2(f, 0.f) & 0xFFFFu; }
+
+// The same rounding in integer arithmetic (the reference formulation the
+// hardware convert is checked against).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits_int(float f) {
     uint32_t u = __float_as_uint(f);
     if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -81,6 +93,10 @@ template <> struct Io<float> {
     }
     // The values the type stores (identity for fp32).
     __device__ __forceinline__ static void round(float*) {}
+    // One 16-byte vector of stored values from EPV floats.
+    __device__ __forceinline__ static uint4 pack(const float* v) {
+        return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+    }
 };
 
 template <> struct Io<bf16> {
@@ -109,10 +125,18 @@ template <> struct Io<bf16> {
         v[4] = bf16_lo(t.z); v[5] = bf16_hi(t.z);
         v[6] = bf16_lo(t.w); v[7] = bf16_hi(t.w);
     }
+    __device__ __forceinline__ static uint4 pack(const float* v) {
+        return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                          pack_bf16x2(v[6], v[7]));
+    }
     // The values the type stores: RNE to bf16 and back.
     __device__ __forceinline__ static void round(float* v) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = __uint_as_float(f32_to_bf16_bits(v[e]) << 16);
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t t = pack_bf16x2(v[e], v[e + 1]);
+            v[e] = bf16_lo(t);
+            v[e + 1] = bf16_hi(t);
+        }
     }
 };
 
