@@ -102,7 +102,7 @@ unsigned generic_blocks(int64_t n) {
     return (unsigned)(b < 1 ? 1 : (b > cap ? cap : b));
 }
 
-constexpr int kUnroll = 2;
+constexpr int kUnroll = 1;
 
 template <typename T>
 int run_swiglu(const void* g, int64_t gs, const void* u, int64_t us, void* y, int64_t ys,

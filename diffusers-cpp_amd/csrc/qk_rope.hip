@@ -101,11 +101,11 @@ __device__ __forceinline__ void store8<float>(float* p, const float* v) {
 // position, its cos/sin table row and the lane's 8 norm weights are loaded
 // once per wave, and all HPG head loads are in flight before the first
 // reduction.
-template <typename T, int HPG>
+template <typename T, int HPG, int NT>
 __device__ __forceinline__ void qk_rope128_body(const QkHalf& a, const QkShape& sh, const float* __restrict__ table,
                                                 int chunks, int block) {
     if (a.x == nullptr) return;
-    const int wv = (int)((block * 256 + threadIdx.x) / kWave);
+    const int wv = (int)((block * NT + threadIdx.x) / kWave);
     if (wv >= sh.tokens * chunks) return;  // whole waves leave together
     const int lane16 = threadIdx.x & 15;
     const int row = (threadIdx.x & (kWave - 1)) >> 4;
@@ -171,8 +171,10 @@ __device__ __forceinline__ void qk_rope128_body(const QkHalf& a, const QkShape& 
 template <typename T, int HPG>
 __global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkShape sh,
                                                          const float* __restrict__ table, int chunks) {
-    qk_rope128_body<T, HPG>(blockIdx.y == 0 ? q : k, sh, table, chunks, blockIdx.x);
+    qk_rope128_body<T, HPG, 256>(blockIdx.y == 0 ? q : k, sh, table, chunks, blockIdx.x);
 }
+
+constexpr int kQkSwigluThreads = 512;  // the SwiGLU body's best workgroup
 
 // QK-RMSNorm+RoPE of q and k and the SwiGLU of the same block in one launch
 // (Flux2ParallelSelfAttention.hpp:55-93: all three read the outputs of the
@@ -180,13 +182,15 @@ __global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkS
 // qk_blocks k, the rest stream the SwiGLU.  The bodies are the standalone
 // kernels', so the results are bit-identical to three separate launches.
 template <typename T, int HPG>
-__global__ __launch_bounds__(256) void qk_swiglu_kernel(QkHalf q, QkHalf k, QkShape sh, const float* __restrict__ table,
-                                                        int chunks, int qk_blocks, SwigluArgs sw) {
+__global__ __launch_bounds__(kQkSwigluThreads) void qk_swiglu_kernel(QkHalf q, QkHalf k, QkShape sh,
+                                                                     const float* __restrict__ table, int chunks,
+                                                                     int qk_blocks, SwigluArgs sw) {
     const int b = blockIdx.x;
     if (b < 2 * qk_blocks)
-        qk_rope128_body<T, HPG>(b < qk_blocks ? q : k, sh, table, chunks, b < qk_blocks ? b : b - qk_blocks);
+        qk_rope128_body<T, HPG, kQkSwigluThreads>(b < qk_blocks ? q : k, sh, table, chunks,
+                                                  b < qk_blocks ? b : b - qk_blocks);
     else
-        swiglu_body<T, 256>(sw, b - 2 * qk_blocks);
+        swiglu_body<T, kQkSwigluThreads>(sw, b - 2 * qk_blocks);
 }
 
 // Any head_dim / axis_dim (even) / stride: one thread per (token, head).
@@ -302,12 +306,13 @@ int run_qk_swiglu(const QkHalf& hq, const QkHalf& hk, const QkShape& sh, const f
         if (rc) return rc;
         return dt_swiglu(g, gs, u, us, y, ys, rows, cols, Io<T>::kType, st);
     }
+    constexpr int NT = kQkSwigluThreads, WAVES = NT / kWave;
     const int chunks = (sh.heads + 4 * kHPG - 1) / (4 * kHPG);
-    const int64_t qk_blocks = ((int64_t)sh.tokens * chunks + 3) / 4;
-    const int64_t blocks = 2 * qk_blocks + swiglu_blocks<T, 256>((uint32_t)total);
+    const int64_t qk_blocks = ((int64_t)sh.tokens * chunks + WAVES - 1) / WAVES;
+    const int64_t blocks = 2 * qk_blocks + swiglu_blocks<T, NT>((uint32_t)total);
     DT_REQUIRE(blocks < (1ll << 31), "dt_qk_rmsnorm_rope_swiglu: grid too large");
     const SwigluArgs sw{g, gs, u, us, y, ys, (uint32_t)total, make_fastdiv((uint32_t)(nvec ? nvec : 1))};
-    hipLaunchKernelGGL((qk_swiglu_kernel<T, kHPG>), dim3((unsigned)blocks), dim3(256), 0, st, hq, hk, sh, table,
+    hipLaunchKernelGGL((qk_swiglu_kernel<T, kHPG>), dim3((unsigned)blocks), dim3(NT), 0, st, hq, hk, sh, table,
                        chunks, (int)qk_blocks, sw);
     return check_launch("dt_qk_rmsnorm_rope_swiglu");
 }
