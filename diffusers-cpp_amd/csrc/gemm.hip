@@ -8,7 +8,7 @@
 // of a block), whose tiles share the grid: no wave of workgroups is left
 // half-empty at the end of each small GEMM.
 //
-// Two tile configurations (gfx950):
+// Three tile configurations (gfx950):
 //  * 256 x 256, 8 waves of 128 x 64: A and B travel global -> LDS by direct
 //    DMA (global_load_lds_dwordx4: lane i of an instruction writes its 16
 //    bytes to LDS base + 16 i) through four stages of K = 32, so the loads for
@@ -17,6 +17,9 @@
 //    bf16); chunk c of row r is stored at chunk c ^ swz(r), swz(r) =
 //    ((r >> 1) ^ (r >> 2)) & 3, which makes the 16-byte reads of 8 (32-bank)
 //    or 16 (64-bank) consecutive rows at one logical chunk hit distinct banks.
+//  * 256 x 256, 4 waves of 128 x 128, two stages of K = 64: whole 128-byte
+//    rows per DMA segment and operand reads software-pipelined one k-step
+//    ahead; chosen for long K.
 //  * 128 x 128, 4 waves of 64 x 64, two workgroups per CU: K = 64 per step
 //    through two register-staged LDS stages (rows padded to 144 bytes), for
 //    GEMMs too small to fill the CUs with 256 x 256 tiles.
@@ -229,6 +232,130 @@ __global__ __launch_bounds__(512) void gemm_dma256_kernel(const Group grp) {
     epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
 }
 
+// ---- 256 x 256, 4 waves of 128 x 128, K = 64 per stage, 2 stages -------------
+// Each wave owns a 128 x 128 quarter of the tile (4 x 4 blocks of 32 x 32,
+// 256 fp32 accumulators, one wave per SIMD): per k-step it reads 8 operands
+// for 16 MFMAs, against 6 for 8 in the 8-wave kernel, which keeps the LDS
+// port that the DMA writes share below the MFMA time.
+// Rows of 64 bf16 = 128 bytes per stage, so each DMA row segment is one whole
+// L2 line (the 64-byte segments of K = 32 stages issue twice the requests and
+// feed LDS at ~14 TB/s against ~22 TB/s with full lines, measured on gfx950
+// for this tile shape).  Two stages of 64 KB; chunk c of row r is stored at
+// chunk c ^ swz8(r), swz8(r) = (r ^ (r >> 3)) & 7, so the 16-byte reads of 8
+// (32-bank) or 16 (64-bank) consecutive rows at one logical chunk hit
+// distinct banks.  Operand reads are software-pipelined one k-step ahead.
+constexpr int EBK = 64, EROWB = EBK * 2, EOPB = 256 * EROWB, ESTAGEB = 2 * EOPB;
+
+__device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
+
+template <typename TC>
+__global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
+    constexpr int FM = 4, FN = 4, NS = 2;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * ESTAGEB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    const Problem& p = locate<256, 256>(grp, &tm, &tn);
+    const int m0 = tm * 256, n0 = tn * 256;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+
+    // DMA sources: wave w fills rows [64 w, 64 w + 64) of both operands, eight
+    // instructions of 8 rows each; lane i covers row + i / 8, stored chunk i % 8.
+    const uint16_t* ga[8];
+    const uint16_t* gb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int row = 64 * wave + 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        ga[j] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + c * 8;
+        gb[j] = p.B + (int64_t)min(n0 + row, p.N - 1) * p.ldb + c * 8;
+    }
+    auto issue = [&](int kt, int s) {
+        uint8_t* base = smem + s * ESTAGEB + 64 * wave * EROWB;
+        const int k0 = kt * EBK;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            __builtin_amdgcn_global_load_lds(ga[j] + k0, base + 8 * j * EROWB, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(gb[j] + k0, base + EOPB + 8 * j * EROWB, 16, 0, 0);
+        }
+    };
+
+    f32x16_t acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.f;
+
+    const int lrow = lane & 31, g = lane >> 5;
+    // Per-fragment swizzle of the rows this lane reads (rows wn + 32 j + lrow
+    // and wm + 32 i + lrow; 32 j only changes bit 5, which swz8 ignores except
+    // through r >> 3).
+    int sb[FN], sa[FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) sb[j] = swz8(wn + 32 * j + lrow);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sa[i] = swz8(wm + 32 * i + lrow);
+    bf16x8_t wa[FN], xa[FM], wb[FN], xb[FM];
+    auto read_ops = [&](int s, int kk, bf16x8_t (&wf)[FN], bf16x8_t (&xf)[FM]) {
+        const uint8_t* As = smem + s * ESTAGEB;
+        const uint8_t* Bs = As + EOPB;
+        const int c = 2 * kk + g;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            wf[j] = *reinterpret_cast<const bf16x8_t*>(Bs + (wn + 32 * j + lrow) * EROWB + ((c ^ sb[j]) << 4));
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            xf[i] = *reinterpret_cast<const bf16x8_t*>(As + (wm + 32 * i + lrow) * EROWB + ((c ^ sa[i]) << 4));
+    };
+    auto mfma = [&](const bf16x8_t (&wf)[FN], const bf16x8_t (&xf)[FM]) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+    };
+
+    const int nk = p.K / EBK;
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    if (nk > 1) wait_vm<16>();
+    else wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    read_ops(0, 0, wa, xa);
+    // The last k-tile is peeled off so the loop body has no join between the
+    // next tile's operand reads and the MFMAs that run meanwhile.
+    for (int kt = 0; kt < nk - 1; ++kt) {
+        const int s = kt & 1;
+        read_ops(s, 1, wb, xb);
+        mfma(wa, xa);
+        read_ops(s, 2, wa, xa);
+        mfma(wb, xb);
+        read_ops(s, 3, wb, xb);
+        mfma(wa, xa);
+        // Stage s is refilled with k-tile kt + 2 once every wave's reads of
+        // it have returned; k-tile kt + 1 (the other stage) must have landed.
+        wait_vm<0>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (kt + 2 < nk) issue(kt + 2, s);
+        read_ops(s ^ 1, 0, wa, xa);
+        mfma(wb, xb);
+    }
+    {
+        const int s = (nk - 1) & 1;
+        read_ops(s, 1, wb, xb);
+        mfma(wa, xa);
+        read_ops(s, 2, wa, xa);
+        mfma(wb, xb);
+        read_ops(s, 3, wb, xb);
+        mfma(wa, xa);
+        mfma(wb, xb);
+    }
+    epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
+}
+
 // ---- 128 x 128, register-staged, 2 stages --------------------------------------
 constexpr int SBK = 64;
 constexpr int SLDSW = SBK + 8;  // padded LDS row, in bf16 elements
@@ -332,8 +459,9 @@ struct Config {
     int bm, bn, threads, per_cu;
     double rate;  // measured per-CU rate when the CUs are full (PFLOP/s, gfx950)
 };
-// 0: 256 x 256 pipelined (one workgroup per CU); 1: 128 x 128 (two per CU).
-constexpr Config kConfigs[2] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}};
+// 0: 256 x 256, 8 waves, K = 32 stages (one workgroup per CU); 1: 128 x 128
+// (two per CU); 2: 256 x 256, 4 waves, K = 64 stages.
+constexpr Config kConfigs[3] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -341,7 +469,11 @@ int64_t tiles_of(const Problem& p, int cfg) {
 }
 
 // Estimated time: ceil(tiles / concurrent workgroups) waves, each lasting the
-// tile area x workgroups per CU / the per-CU rate.
+// tile area x workgroups per CU / the per-CU rate, between the 256 x 256 and
+// 128 x 128 tiles.  Among the 256 x 256 kernels the K = 64 one streams whole
+// L2 lines and wins on long K (gfx950, M = 4608: +4-6% at K >= 6144); at
+// K = 3072 the 8-wave kernel is as fast or faster, also for the grouped
+// q/k/v/gate/up projections of a single-stream block (814 vs 855 us).
 int pick_config(const Problem* ps, int n, int cus) {
     int best = 1;
     double best_t = 1e300;
@@ -356,6 +488,11 @@ int pick_config(const Problem* ps, int n, int cus) {
             best_t = t;
             best = cfg;
         }
+    }
+    if (best == 0) {
+        int max_k = 0;
+        for (int i = 0; i < n; ++i) max_k = max(max_k, ps[i].K);
+        if (max_k >= 6144) best = 2;
     }
     return best;
 }
@@ -376,6 +513,8 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
     const dim3 grid((unsigned)total), block((unsigned)kConfigs[cfg].threads);
     if (cfg == 0)
         hipLaunchKernelGGL((gemm_dma256_kernel<TC>), grid, block, 0, st, g);
+    else if (cfg == 2)
+        hipLaunchKernelGGL((gemm_k64_kernel<TC>), grid, block, 0, st, g);
     else
         hipLaunchKernelGGL((gemm_128_kernel<TC>), grid, block, 0, st, g);
     return check_launch("dt_gemm_bf16");
@@ -407,7 +546,7 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
                                     int32_t config, dt_stream_t stream) {
     using namespace dit;
     DT_REQUIRE(c_type == DT_TYPE_BF16 || c_type == DT_TYPE_F32, "dt_gemm_bf16: c_type %d unsupported", c_type);
-    DT_REQUIRE(config >= -1 && config <= 1, "dt_gemm_bf16: config %d out of range", config);
+    DT_REQUIRE(config >= -1 && config <= 2, "dt_gemm_bf16: config %d out of range", config);
     DT_REQUIRE(count >= 0 && count <= kMaxGroup, "dt_gemm_bf16_grouped: count %d outside 0..%d", count,
                kMaxGroup);
     DT_REQUIRE(problems || count == 0, "dt_gemm_bf16_grouped: null problem list");

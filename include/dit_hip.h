@@ -215,9 +215,10 @@ int dt_gemm_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C
                  int64_t M, int64_t N, int64_t K, const float *bias, const void *addend,
                  int64_t ldd, int32_t c_type, dt_stream_t stream);
 /* dt_gemm_bf16 with an explicit tile configuration: 0 = 256x256 per
- * workgroup with direct global->LDS loads in four stages, 1 = 128x128 with two
- * workgroups per CU; -1 picks by shape as dt_gemm_bf16 does.  For tuning and
- * tests; no counterpart in the reference. */
+ * workgroup with direct global->LDS loads in four K = 32 stages, 1 = 128x128
+ * with two workgroups per CU, 2 = 256x256 with two K = 64 stages; -1 picks by
+ * shape as dt_gemm_bf16 does.  For tuning and tests; no counterpart in the
+ * reference. */
 int dt_gemm_bf16_config(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float *bias,
                         const void *addend, int64_t ldd, int32_t c_type, int32_t config,
