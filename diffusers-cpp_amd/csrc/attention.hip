@@ -14,10 +14,10 @@
 // that same permutation (keys {4g..4g+3, 8+4g..8+4g+3} for lane half g).
 //
 // A 256-thread workgroup (4 waves, 128 queries) shares 64-key K and V tiles
-// in LDS; V is stored transposed (Vt[d][key]) so the A operand is two 8-byte
-// LDS reads.  The next tile is fetched into registers while the MFMAs run.
-// Workgroups are ordered so that each XCD (8 per MI355X, one L2 each) works
-// through a contiguous range of (batch, head) slices.
+// in LDS, double-buffered and filled by direct DMA; two workgroups per CU
+// give each SIMD two waves, so one wave's softmax overlaps the other's
+// MFMAs.  Workgroups are ordered so that each XCD (8 per MI355X, one L2 each)
+// works through a contiguous range of (batch, head) slices.
 #include "capi_util.hpp"
 #include "common.hpp"
 
@@ -30,9 +30,6 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int D = 128;       // head dim
 constexpr int QB = 128;      // queries per workgroup
-constexpr int KB = 64;       // keys per tile
-constexpr int KS = D + 8;    // Ks row, bf16 elements (272 B: conflict-free 16-byte reads)
-constexpr int VS = KB + 4;   // Vt row, bf16 elements (136 B: conflict-free 8-byte reads)
 
 struct AttnArgs {
     const uint16_t* q;
@@ -47,13 +44,43 @@ struct AttnArgs {
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
-template <typename TO>
-__global__ __launch_bounds__(256) void flash_attn_d128_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[KB * KS];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VS];
+// ---- K/V by direct DMA, two workgroups per CU ---------------------------------
+// K and V tiles move global -> LDS by direct DMA (global_load_lds_dwordx4)
+// into two 32 KB buffers, so no registers are spent on staging.  At most 256 registers per lane (two waves per SIMD):
+// one wave's softmax (VALU) runs while the other wave on the SIMD issues
+// MFMAs.  V stays [key][d] in LDS; the V^T A operand is read with
+// ds_read_tr16_b64, which gives lane i of a 16-lane group element c = i % 4
+// of lane 4 j + i / 4's 4 x b16: with lane s addressing V[k0 + s / 4][d0 +
+// 4 (s % 4) ..], lane i receives V[k0 + j][d0 + i] for j = 0..3, i.e. four
+// keys of one d.  Rows of 256 bytes are XOR-swizzled in 16-byte chunks:
+// K chunk c of row r at c ^ (r & 15) (16 rows read one logical chunk),
+// V chunk c at c ^ 4 (r & 3) (4 rows x 4 consecutive chunks per transposed
+// read).
+constexpr int DKB = 64;                 // keys per tile
+constexpr int DROW = D * 2;             // bytes per K / V row
+constexpr int DTILE = DKB * DROW;       // 16 KB
 
-    // XCD-aware order: workgroup i runs on XCD i % 8; give each XCD a
-    // contiguous range of logical tiles so (batch, head) slices stay in one L2.
+__device__ __forceinline__ int kswz(int r) { return r & 15; }
+__device__ __forceinline__ int vswz(int r) { return (r & 3) << 2; }
+
+template <int N_OUT>
+__device__ __forceinline__ void attn_wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N_OUT & 15) | ((N_OUT >> 4) << 14) | 0x0F70);
+}
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t* lds_short4_p;
+
+// ds_read_tr16_b64 of the 8 bytes at p (an LDS address).
+__device__ __forceinline__ uint2 read_tr16(const uint8_t* p) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_p)(p)));
+}
+
+template <typename TO>
+__global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
+    // [buffer][K | V][64 rows][256 B]
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * DTILE];
+
     uint32_t bid = blockIdx.x;
     const uint32_t nb = gridDim.x;
     if ((nb & 7u) == 0) bid = (bid & 7u) * (nb >> 3) + (bid >> 3);
@@ -69,7 +96,6 @@ __global__ __launch_bounds__(256) void flash_attn_d128_kernel(AttnArgs a) {
     const uint16_t* Kp = a.k + b * a.ks[0] + h * a.ks[2];
     const uint16_t* Vp = a.v + b * a.vs[0] + h * a.vs[2];
 
-    // Q^T as the B operand of S^T = K Q^T: lane (r, g) holds Q[q0 + r][16 c + 8 g .. +8].
     bf16x8_t qf[8];
     {
         const int qrow = q0 + r;
@@ -80,46 +106,22 @@ __global__ __launch_bounds__(256) void flash_attn_d128_kernel(AttnArgs a) {
         }
     }
 
-    // Tile fetch: K rows are 16 threads x 16 bytes; V is fetched as key pairs
-    // (2p, 2p+1) of one 8-wide d chunk so the transposed LDS store packs two
-    // keys per 32-bit word.
-    uint4 kr[4], vr[2][2];
-    auto fetch = [&](int kv0) {
+    // DMA: wave w fills rows [16 w, 16 w + 16) of the K and the V tile, four
+    // instructions of 4 rows each; lane i covers row + i / 16, stored chunk
+    // i % 16, loaded from the swizzled source chunk.  Rows past seq_kv load
+    // the last valid row (finite data; their scores are masked to -inf).
+    const int drow = 16 * wave + (lane >> 4), dpos = lane & 15;
+    auto issue = [&](int kv0, int buf) {
+        uint8_t* kb = smem + buf * 2 * DTILE + 16 * wave * DROW;
+        uint8_t* vb = kb + DTILE;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i, key = c >> 4, ch = c & 15;
-            kr[i] = kv0 + key < a.seq_kv ? ld16(Kp + (int64_t)(kv0 + key) * a.ks[1] + ch * 8)
-                                         : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int p = tid & 31, ch = (tid >> 5) + 8 * j;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int key = kv0 + 2 * p + e;
-                vr[j][e] = key < a.seq_kv ? ld16(Vp + (int64_t)key * a.vs[1] + ch * 8) : make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    auto stash = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + 256 * i, key = c >> 4, ch = c & 15;
-            *reinterpret_cast<uint4*>(&Ks[key * KS + ch * 8]) = kr[i];
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int p = tid & 31, ch = (tid >> 5) + 8 * j;
-            const uint32_t* lo = reinterpret_cast<const uint32_t*>(&vr[j][0]);
-            const uint32_t* hi = reinterpret_cast<const uint32_t*>(&vr[j][1]);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                // d = 8 ch + 2 w (+1): low / high halves of word w of each key's chunk
-                const uint32_t d0 = (lo[w] & 0xFFFFu) | (hi[w] << 16);
-                const uint32_t d1 = (lo[w] >> 16) | (hi[w] & 0xFFFF0000u);
-                *reinterpret_cast<uint32_t*>(&Vt[(8 * ch + 2 * w) * VS + 2 * p]) = d0;
-                *reinterpret_cast<uint32_t*>(&Vt[(8 * ch + 2 * w + 1) * VS + 2 * p]) = d1;
-            }
+        for (int j = 0; j < 4; ++j) {
+            const int row = drow + 4 * j;
+            const int key = min(kv0 + row, a.seq_kv - 1);
+            __builtin_amdgcn_global_load_lds(Kp + (int64_t)key * a.ks[1] + (dpos ^ kswz(row)) * 8,
+                                             kb + 4 * j * DROW, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Vp + (int64_t)key * a.vs[1] + (dpos ^ vswz(row)) * 8,
+                                             vb + 4 * j * DROW, 16, 0, 0);
         }
     };
 
@@ -130,37 +132,46 @@ __global__ __launch_bounds__(256) void flash_attn_d128_kernel(AttnArgs a) {
         for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
-    fetch(0);
-    for (int kv0 = 0; kv0 < a.seq_kv; kv0 += KB) {
-        stash();
-        __syncthreads();
-        if (kv0 + KB < a.seq_kv) fetch(kv0 + KB);
+    // Transposed-read addressing (lane s of a 16-lane group): group gi = lane / 16
+    // takes lane half g = gi / 2 and d half dsub = gi % 2.
+    const int s16 = lane & 15, gi = lane >> 4, tg = gi >> 1, dsub = gi & 1;
+    const int trow = s16 >> 2;                  // row within the 4-key block
+    const int tcol = 16 * dsub + 4 * (s16 & 3);  // d offset within a 32-d tile
 
-        // S^T[key][q] for the two 32-key halves of the tile.
-        f32x16_t s[2];
+    const int ntiles = (a.seq_kv + DKB - 1) / DKB;
+    issue(0, 0);
+    if (ntiles > 1) issue(DKB, 1);
+    for (int t = 0; t < ntiles; ++t) {
+        const int kv0 = t * DKB, buf = t & 1;
+        if (t + 1 < ntiles) attn_wait_vm<8>();
+        else attn_wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        const uint8_t* Kt = smem + buf * 2 * DTILE;
+        const uint8_t* Vt_ = Kt + DTILE;
+
+        f32x16_t sacc[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[hh][e] = 0.f;
+            for (int e = 0; e < 16; ++e) sacc[hh][e] = 0.f;
+            const int row = 32 * hh + r;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&Ks[(32 * hh + r) * KS + 16 * c + 8 * g]);
-                s[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], s[hh], 0, 0, 0);
+                const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(Kt + row * DROW + (((2 * c + g) ^ kswz(row)) << 4));
+                sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], sacc[hh], 0, 0, 0);
             }
         }
 
-        // Online softmax for query q0 + r; element i of s[hh] is key
-        // kv0 + 32 hh + 8 (i / 4) + 4 g + i % 4.
         float mx = -INFINITY;
+        const bool partial = kv0 + DKB > a.seq_kv;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int key = kv0 + 32 * hh + 8 * (i >> 2) + 4 * g + (i & 3);
-                float t = s[hh][i] * a.scale_log2;
-                if (key >= a.seq_kv) t = -INFINITY;
-                s[hh][i] = t;
-                mx = fmaxf(mx, t);
+                float tv = sacc[hh][i] * a.scale_log2;
+                if (partial && kv0 + 32 * hh + 8 * (i >> 2) + 4 * g + (i & 3) >= a.seq_kv) tv = -INFINITY;
+                sacc[hh][i] = tv;
+                mx = fmaxf(mx, tv);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
@@ -172,46 +183,52 @@ __global__ __launch_bounds__(256) void flash_attn_d128_kernel(AttnArgs a) {
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float p = __builtin_amdgcn_exp2f(s[j >> 1][8 * (j & 1) + e] - m_new);
-                psum += p;
-                pf[j][e] = (__bf16)p;
+                const float pv = __builtin_amdgcn_exp2f(sacc[j >> 1][8 * (j & 1) + e] - m_new);
+                psum += pv;
+                pf[j][e] = (__bf16)pv;
             }
         }
         l_run = l_run * alpha + psum;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+            for (int e = 0; e < 16; ++e) o[tt][e] *= alpha;
 
-        // O^T[d][q] += V^T[d][key] P^T[key][q], 16 keys per MFMA.
+        // O^T[d][q] += V^T[d][key] P^T[key][q]: MFMA j covers keys 16 j ..;
+        // lane half g supplies keys {16 j + 4 g + e, 16 j + 8 + 4 g + e}.
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+            const int r0 = 16 * j + 4 * tg + trow, r1 = r0 + 8;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint16_t* vrow = &Vt[(32 * t + r) * VS + 16 * j + 4 * g];
-                const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-                const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+            for (int tt = 0; tt < 4; ++tt) {
+                const int dcol = 32 * tt + tcol;            // multiple of 4
+                const int ch = dcol >> 3, half = (dcol >> 2) & 1;
+                const uint2 lo = read_tr16(Vt_ + r0 * DROW + ((ch ^ vswz(r0)) << 4) + 8 * half);
+                const uint2 hi = read_tr16(Vt_ + r1 * DROW + ((ch ^ vswz(r1)) << 4) + 8 * half);
                 const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                o[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[t], 0, 0, 0);
+                o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[tt], 0, 0, 0);
             }
         }
-        __syncthreads();
+        // Every wave's reads of this buffer have returned before any wave
+        // passes the barrier, so it can take tile t + 2.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (t + 2 < ntiles) issue(kv0 + 2 * DKB, buf);
     }
 
-    // Normalise and store O[q][d]: element i of o[t] is d = 32 t + 8 (i / 4) + 4 g + i % 4.
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     const float inv = 1.0f / l_tot;
     const int q = q0 + r;
     if (q < a.seq_q) {
         TO* op = reinterpret_cast<TO*>(a.o) + b * a.os[0] + (int64_t)q * a.os[1] + h * a.os[2];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
-                const int d = 32 * t + 8 * i4 + 4 * g;
+                const int d = 32 * tt + 8 * i4 + 4 * g;
                 float v4[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v4[e] = o[t][4 * i4 + e] * inv;
+                for (int e = 0; e < 4; ++e) v4[e] = o[tt][4 * i4 + e] * inv;
                 if constexpr (sizeof(TO) == 4) {
                     *reinterpret_cast<float4*>(reinterpret_cast<float*>(op) + d) =
                         make_float4(v4[0], v4[1], v4[2], v4[3]);
@@ -264,8 +281,8 @@ extern "C" int dt_flash_attn_bf16(const void* q, const void* k, const void* v, v
     DT_REQUIRE(nblocks < (1ll << 31), "dt_flash_attn_bf16: grid too large");
     hipStream_t st = (hipStream_t)stream;
     if (o_type == DT_TYPE_F32)
-        hipLaunchKernelGGL((dit::flash_attn_d128_kernel<float>), dim3((unsigned)nblocks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((dit::flash_attn_dma_kernel<float>), dim3((unsigned)nblocks), dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((dit::flash_attn_d128_kernel<uint16_t>), dim3((unsigned)nblocks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((dit::flash_attn_dma_kernel<uint16_t>), dim3((unsigned)nblocks), dim3(256), 0, st, a);
     return dit::check_launch("dt_flash_attn_bf16");
 }
