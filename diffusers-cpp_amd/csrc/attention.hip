@@ -18,6 +18,8 @@
 // give each SIMD two waves, so one wave's softmax overlaps the other's
 // MFMAs.  Workgroups are ordered so that each XCD (8 per MI355X, one L2 each)
 // works through a contiguous range of (batch, head) slices.
+#include <type_traits>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 
@@ -109,44 +111,70 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
     // DMA: wave w fills rows [16 w, 16 w + 16) of the K and the V tile, four
     // instructions of 4 rows each; lane i covers row + i / 16, stored chunk
     // i % 16, loaded from the swizzled source chunk.  Rows past seq_kv load
-    // the last valid row (finite data; their scores are masked to -inf).
+    // the last valid row (finite data; their scores are masked).
     const int drow = 16 * wave + (lane >> 4), dpos = lane & 15;
+    const uint16_t* kq[4];
+    const uint16_t* vq[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = drow + 4 * j;
+        kq[j] = Kp + (int64_t)row * a.ks[1] + (dpos ^ kswz(row)) * 8;
+        vq[j] = Vp + (int64_t)row * a.vs[1] + (dpos ^ vswz(row)) * 8;
+    }
     auto issue = [&](int kv0, int buf) {
         uint8_t* kb = smem + buf * 2 * DTILE + 16 * wave * DROW;
         uint8_t* vb = kb + DTILE;
+        if (kv0 + DKB <= a.seq_kv) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = drow + 4 * j;
-            const int key = min(kv0 + row, a.seq_kv - 1);
-            __builtin_amdgcn_global_load_lds(Kp + (int64_t)key * a.ks[1] + (dpos ^ kswz(row)) * 8,
-                                             kb + 4 * j * DROW, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Vp + (int64_t)key * a.vs[1] + (dpos ^ vswz(row)) * 8,
-                                             vb + 4 * j * DROW, 16, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                __builtin_amdgcn_global_load_lds(kq[j] + (int64_t)kv0 * a.ks[1], kb + 4 * j * DROW, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(vq[j] + (int64_t)kv0 * a.vs[1], vb + 4 * j * DROW, 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = drow + 4 * j;
+                const int key = min(kv0 + row, a.seq_kv - 1);
+                __builtin_amdgcn_global_load_lds(Kp + (int64_t)key * a.ks[1] + (dpos ^ kswz(row)) * 8,
+                                                 kb + 4 * j * DROW, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(Vp + (int64_t)key * a.vs[1] + (dpos ^ vswz(row)) * 8,
+                                                 vb + 4 * j * DROW, 16, 0, 0);
+            }
         }
     };
+
+    // Per-lane LDS offsets, the same for every tile.  K: row 32 hh + r, chunk
+    // 2 c + g at (2 c + g) ^ (r & 15) (32 hh is an immediate).  V (transposed
+    // reads): lane s of 16-lane group gi reads row 16 j + 4 tg + s / 4 (+ 8),
+    // d = 32 tt + 16 dsub + 4 (s % 4), whose swizzled chunk is
+    // 4 (tt ^ s / 4) + (16 dsub + 4 (s % 4)) / 8.
+    int koff[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) koff[c] = r * DROW + (((2 * c + g) ^ (r & 15)) << 4);
+    const int s16 = lane & 15, gi = lane >> 4, tg = gi >> 1, dsub = gi & 1;
+    const int trow = s16 >> 2, tcol = 16 * dsub + 4 * (s16 & 3);
+    int voff[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+        voff[tt] = (4 * tg + trow) * DROW + ((4 * (tt ^ trow) + (tcol >> 3)) << 4) + 8 * ((tcol >> 2) & 1);
 
     f32x16_t o[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
-
-    // Transposed-read addressing (lane s of a 16-lane group): group gi = lane / 16
-    // takes lane half g = gi / 2 and d half dsub = gi % 2.
-    const int s16 = lane & 15, gi = lane >> 4, tg = gi >> 1, dsub = gi & 1;
-    const int trow = s16 >> 2;                  // row within the 4-key block
-    const int tcol = 16 * dsub + 4 * (s16 & 3);  // d offset within a 32-d tile
+    float m_run = -INFINITY, l_run = 0.f;  // running max in units of scale * log2(e)
+    const float sc = a.scale_log2;          // >= 0, so max(sc * s) = sc * max(s)
 
     const int ntiles = (a.seq_kv + DKB - 1) / DKB;
-    issue(0, 0);
-    if (ntiles > 1) issue(DKB, 1);
-    for (int t = 0; t < ntiles; ++t) {
-        const int kv0 = t * DKB, buf = t & 1;
+    auto tile = [&](int t, auto buf_c, auto mask_c) {
+        constexpr int BUF = decltype(buf_c)::value;
+        constexpr bool MASK = decltype(mask_c)::value;
+        const int kv0 = t * DKB;
         if (t + 1 < ntiles) attn_wait_vm<8>();
         else attn_wait_vm<0>();
         __builtin_amdgcn_s_barrier();
-        const uint8_t* Kt = smem + buf * 2 * DTILE;
+        const uint8_t* Kt = smem + BUF * 2 * DTILE;
         const uint8_t* Vt_ = Kt + DTILE;
 
         f32x16_t sacc[2];
@@ -154,57 +182,63 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) sacc[hh][e] = 0.f;
-            const int row = 32 * hh + r;
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
-                const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(Kt + row * DROW + (((2 * c + g) ^ kswz(row)) << 4));
+                const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(Kt + 32 * hh * DROW + koff[c]);
                 sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], sacc[hh], 0, 0, 0);
             }
         }
-
+        // Element i of sacc[hh] is key kv0 + 32 hh + 8 (i / 4) + 4 g + i % 4.
         float mx = -INFINITY;
-        const bool partial = kv0 + DKB > a.seq_kv;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float tv = sacc[hh][i] * a.scale_log2;
-                if (partial && kv0 + 32 * hh + 8 * (i >> 2) + 4 * g + (i & 3) >= a.seq_kv) tv = -INFINITY;
-                sacc[hh][i] = tv;
-                mx = fmaxf(mx, tv);
+                if (MASK && kv0 + 32 * hh + 8 * (i >> 2) + 4 * g + (i & 3) >= a.seq_kv) continue;
+                mx = fmaxf(mx, sacc[hh][i]);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        const float m_new = fmaxf(m_run, mx * sc);
+        // Rescale only when some lane's running max moved (alpha is then exactly 1 elsewhere).
+        if (__builtin_amdgcn_ballot_w64(m_new != m_run)) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) o[tt][e] *= alpha;
+        }
         m_run = m_new;
         float psum = 0.f;
         bf16x8_t pf[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float pv = __builtin_amdgcn_exp2f(sacc[j >> 1][8 * (j & 1) + e] - m_new);
-                psum += pv;
-                pf[j][e] = (__bf16)pv;
+            for (int e = 0; e < 8; e += 2) {
+                float p2[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int i = 8 * (j & 1) + e + u;
+                    float arg = __builtin_fmaf(sacc[j >> 1][i], sc, -m_new);
+                    if (MASK && kv0 + 32 * (j >> 1) + 8 * (i >> 2) + 4 * g + (i & 3) >= a.seq_kv) arg = -INFINITY;
+                    p2[u] = __builtin_amdgcn_exp2f(arg);
+                    psum += p2[u];
+                }
+                const uint32_t pk = pack_bf16x2(p2[0], p2[1]);
+                pf[j][e] = __builtin_bit_cast(__bf16, (uint16_t)(pk & 0xFFFFu));
+                pf[j][e + 1] = __builtin_bit_cast(__bf16, (uint16_t)(pk >> 16));
             }
         }
-        l_run = l_run * alpha + psum;
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) o[tt][e] *= alpha;
+        l_run += psum;
 
         // O^T[d][q] += V^T[d][key] P^T[key][q]: MFMA j covers keys 16 j ..;
         // lane half g supplies keys {16 j + 4 g + e, 16 j + 8 + 4 g + e}.
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int r0 = 16 * j + 4 * tg + trow, r1 = r0 + 8;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
-                const int dcol = 32 * tt + tcol;            // multiple of 4
-                const int ch = dcol >> 3, half = (dcol >> 2) & 1;
-                const uint2 lo = read_tr16(Vt_ + r0 * DROW + ((ch ^ vswz(r0)) << 4) + 8 * half);
-                const uint2 hi = read_tr16(Vt_ + r1 * DROW + ((ch ^ vswz(r1)) << 4) + 8 * half);
+                const uint2 lo = read_tr16(Vt_ + 16 * j * DROW + voff[tt]);
+                const uint2 hi = read_tr16(Vt_ + (16 * j + 8) * DROW + voff[tt]);
                 const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
                 o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[tt], 0, 0, 0);
             }
@@ -213,7 +247,29 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
         // passes the barrier, so it can take tile t + 2.
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (t + 2 < ntiles) issue(kv0 + 2 * DKB, buf);
+        if (t + 2 < ntiles) issue(kv0 + 2 * DKB, BUF);
+    };
+
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using Full = std::integral_constant<bool, false>;
+    using Part = std::integral_constant<bool, true>;
+    // Full tiles in pairs (the buffer of each is then a constant), then the
+    // last tile, masked when seq_kv is not a multiple of the tile.
+    const int nfull = a.seq_kv / DKB;
+    issue(0, 0);
+    if (ntiles > 1) issue(DKB, 1);
+    int t = 0;
+    for (; t + 1 < nfull; t += 2) {
+        tile(t, B0{}, Full{});
+        tile(t + 1, B1{}, Full{});
+    }
+    if (t < nfull) {
+        tile(t, B0{}, Full{});
+        ++t;
+        if (t < ntiles) tile(t, B1{}, Part{});
+    } else if (t < ntiles) {
+        tile(t, B0{}, Part{});
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -276,6 +332,7 @@ extern "C" int dt_flash_attn_bf16(const void* q, const void* k, const void* v, v
     a.seq_q = (int32_t)seq_q;
     a.seq_kv = (int32_t)seq_kv;
     a.q_blocks = (int32_t)((seq_q + dit::QB - 1) / dit::QB);
+    DT_REQUIRE(scale >= 0.f, "dt_flash_attn_bf16: scale must be >= 0 (got %g)", (double)scale);
     a.scale_log2 = scale * 1.4426950408889634f;
     const int64_t nblocks = (int64_t)a.q_blocks * heads * batch;
     DT_REQUIRE(nblocks < (1ll << 31), "dt_flash_attn_bf16: grid too large");
