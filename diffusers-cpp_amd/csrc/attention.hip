@@ -177,17 +177,20 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
         const uint8_t* Kt = smem + BUF * 2 * DTILE;
         const uint8_t* Vt_ = Kt + DTILE;
 
+        // The two 32-key halves are independent accumulator chains; issuing
+        // them alternately keeps the MFMA pipe from waiting on each result.
         f32x16_t sacc[2];
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
+        for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int e = 0; e < 16; ++e) sacc[hh][e] = 0.f;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
+        for (int c = 0; c < 8; ++c)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
                 const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(Kt + 32 * hh * DROW + koff[c]);
                 sacc[hh] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[c], sacc[hh], 0, 0, 0);
             }
-        }
         // Element i of sacc[hh] is key kv0 + 32 hh + 8 (i / 4) + 4 g + i % 4.
         float mx = -INFINITY;
 #pragma unroll
