@@ -201,17 +201,23 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
                 mx = fmaxf(mx, sacc[hh][i]);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx * sc);
-        // Rescale only when some lane's running max moved (alpha is then exactly 1 elsewhere).
-        if (__builtin_amdgcn_ballot_w64(m_new != m_run)) {
+        // The reference max moves only when a score exceeds it by more than
+        // 2^8: every exponent argument stays <= 8, so P <= 256 (exact in bf16
+        // range, no fp32 overflow), and O and l share the same reference, so
+        // O / l is unchanged.  Most tiles then skip the 64 rescales.
+        const float m_cand = fmaxf(m_run, mx * sc);
+        const bool move = m_cand > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(move)) {
+            const float m_new = move ? m_cand : m_run;
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) o[tt][e] *= alpha;
+            m_run = m_new;
         }
-        m_run = m_new;
+        const float m_new = m_run;
         float psum = 0.f;
         bf16x8_t pf[4];
 #pragma unroll
