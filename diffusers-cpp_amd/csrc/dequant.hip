@@ -187,8 +187,54 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float* __restr
     }
 }
 
+// Q8_0 -> the split layout the Q8_0 GEMM reads: codes u = q + 128 as uint8
+// [rows][ld_codes] (the +128 bias lets the GEMM convert a byte with one
+// v_cvt_f32_ubyte), and the block scales as fp32 transposed,
+// scales[blk * ld_scales + row], so the scales of one k-block for a run of
+// rows are contiguous.  One thread per block of 32.
+__global__ __launch_bounds__(256) void q8_0_split_kernel(const uint8_t* __restrict__ src, int64_t row_bytes,
+                                                         uint8_t* __restrict__ codes, int64_t ld_codes,
+                                                         float* __restrict__ scales, int64_t ld_scales,
+                                                         uint32_t total, FastDiv blocks_per_row) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t r = fdiv(idx, blocks_per_row);
+    const uint32_t blk = idx - r * blocks_per_row.d;
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(src + (int64_t)r * row_bytes + (int64_t)blk * 34);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t lo = h[1 + 2 * i], hi = h[2 + 2 * i];
+        w[i] = (lo | (hi << 16)) ^ 0x80808080u;  // int8 q -> uint8 q + 128, per byte
+    }
+    uint4* out = reinterpret_cast<uint4*>(codes + (int64_t)r * ld_codes + (int64_t)blk * 32);
+    out[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    out[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    scales[(int64_t)blk * ld_scales + r] = f16_bits_to_f32(h[0]);
+}
+
 }  // namespace
 }  // namespace dit
+
+extern "C" int dt_q8_0_split(const void* src, int64_t rows, int64_t cols, int64_t row_bytes, void* codes,
+                             int64_t ld_codes, float* scales, int64_t ld_scales, dt_stream_t stream) {
+    DT_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "dt_q8_0_split: cols %lld must be a positive multiple of 32",
+               (long long)cols);
+    DT_REQUIRE(row_bytes >= cols / 32 * 34 && row_bytes % 2 == 0, "dt_q8_0_split: bad row_bytes %lld",
+               (long long)row_bytes);
+    DT_REQUIRE(ld_codes >= cols && ld_codes % 16 == 0, "dt_q8_0_split: ld_codes must be >= cols and a multiple of 16");
+    DT_REQUIRE(ld_scales >= rows, "dt_q8_0_split: ld_scales < rows");
+    if (rows == 0) return DT_OK;
+    DT_REQUIRE(src && codes && scales, "dt_q8_0_split: null pointer");
+    DT_REQUIRE((reinterpret_cast<uintptr_t>(src) & 1) == 0 && dit::aligned16(codes),
+               "dt_q8_0_split: src must be 2-byte and codes 16-byte aligned");
+    const int64_t total = rows * (cols / 32);
+    DT_REQUIRE(total < (1ll << 32), "dt_q8_0_split: too many blocks");
+    hipLaunchKernelGGL(dit::q8_0_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const uint8_t*)src, row_bytes, (uint8_t*)codes, ld_codes, scales,
+                       ld_scales, (uint32_t)total, dit::make_fastdiv((uint32_t)(cols / 32)));
+    return dit::check_launch("dt_q8_0_split");
+}
 
 extern "C" int dt_quantize_q8_0(const float* src, int64_t rows, int64_t cols, int64_t src_stride, void* dst,
                                 int64_t row_bytes, dt_stream_t stream) {

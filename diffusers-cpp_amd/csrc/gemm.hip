@@ -36,6 +36,8 @@
 // groups of GROUP_M tile rows so concurrently running tiles share A rows and
 // B columns.  Rows past M or N load a clamped valid row: their products only
 // reach C entries that are never stored.
+#include <type_traits>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 
@@ -56,6 +58,10 @@ struct Problem {
     const float* bias;
     int64_t lda, ldb, ldc, ldd;
     int M, N, K;
+    // Q8_0 weights (split layout): B holds biased uint8 codes [N][ldb bytes],
+    // Bs the fp32 block scales transposed, Bs[blk * ldbs + n]; null for bf16 B.
+    const float* Bs;
+    int64_t ldbs;
 };
 
 struct Group {
@@ -356,6 +362,194 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
 }
 
+// ---- Q8_0 weights: 256 x 256, 8 waves of 128 x 64, K = 64, 3 stages -----------
+// The weight operand stays Q8_0 in HBM, in the split layout of
+// dt_q8_0_split: uint8 codes u = q + 128 ([N][K], 1 byte per weight) and the
+// fp32 block scales transposed ([K/32][N]).  A stage holds 256 A rows x 128 B
+// (bf16, swizzled as in gemm_k64_kernel), 256 B rows x 64 B (codes) and the
+// 2 x 256 scales of its two k-blocks: 50 KB, so three stages fit in LDS.
+// Each B fragment is dequantised in registers, w = fma(u, d, -128 d) = d * q
+// (exact in fp32: 11-bit x 8-bit significands), then rounded to bf16 by
+// v_cvt_pk_bf16_f32 -- the same bf16 weights dt_dequant writes -- and fed to
+// the same MFMA sequence as gemm_k64_kernel, so the result equals dt_dequant
+// followed by the bf16 GEMM bit for bit.
+// Eight waves, two per SIMD: each code is converted by the two waves that
+// share its weight rows, but one wave's conversion (VALU) overlaps the other
+// wave's MFMAs.  Measured on gfx950 at 4608 x {3072, 27648} x 3072: 90-93% of
+// the bf16 GEMM's rate, against 70-78% for four waves of 256 x 64 (one per
+// SIMD, each code converted once) with the conversion serialised behind the
+// wave's own MFMAs, with or without explicit MFMA/VALU interleaving.
+// B rows of 64 bytes: chunk kk of row n at kk ^ ((n >> 2) & 3), which makes
+// the 16-byte reads of 16 consecutive rows at one chunk hit distinct banks.
+constexpr int QBK = 64, QA_ROWB = QBK * 2, QA_OPB = 256 * QA_ROWB;  // 32 KB
+constexpr int QB_ROWB = QBK, QB_OPB = 256 * QB_ROWB;               // 16 KB
+constexpr int QS_OPB = 2 * 256 * 4;                                 // 2 KB
+constexpr int QSTAGEB = QA_OPB + QB_OPB + QS_OPB, QSTAGES = 3;
+constexpr int QDMA = 4 + 2 + 1;  // DMA instructions per wave per stage: A, B, scales
+
+__device__ __forceinline__ int qswz(int n) { return (n >> 2) & 3; }
+
+template <typename TC>
+__global__ __launch_bounds__(512) void gemm_q8_kernel(const Group grp) {
+    constexpr int FM = 4, FN = 2;  // wave sub-tile 128 (m) x 64 (n)
+    __shared__ __attribute__((aligned(16))) uint8_t smem[QSTAGES * QSTAGEB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    const Problem& p = locate<256, 256>(grp, &tm, &tn);
+    const int m0 = tm * 256, n0 = tn * 256;
+    const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+    const uint8_t* Bq = reinterpret_cast<const uint8_t*>(p.B);
+
+    // DMA sources.  A: wave w fills rows [32 w, +32), 4 instructions of 8 rows
+    // (lane i: row + i / 8, chunk i % 8).  B: the same rows, 2 instructions of
+    // 16 rows (lane i: row + i / 4, chunk i % 4).  Scales: the 64 scales of
+    // k-block w / 4 for rows 64 (w % 4) + i, 4 bytes a lane, so every wave
+    // issues the same QDMA instructions with every lane active.
+    const uint16_t* ga[4];
+    const uint8_t* gb[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 32 * wave + 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        ga[j] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + c * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 32 * wave + 16 * j + (lane >> 2);
+        const int c = (lane & 3) ^ qswz(row);
+        gb[j] = Bq + (int64_t)min(n0 + row, p.N - 1) * p.ldb + c * 16;
+    }
+    const int sblk = wave >> 2;
+    const float* gs = p.Bs + (int64_t)sblk * p.ldbs + min(n0 + 64 * (wave & 3) + lane, p.N - 1);
+    const int s_lds = QA_OPB + QB_OPB + sblk * 1024 + 256 * (wave & 3);
+    auto issue = [&](int kt, int s) {
+        uint8_t* st = smem + s * QSTAGEB;
+        const int k0 = kt * QBK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_global_load_lds(ga[j] + k0, st + (32 * wave + 8 * j) * QA_ROWB, 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            __builtin_amdgcn_global_load_lds(gb[j] + k0, st + QA_OPB + (32 * wave + 16 * j) * QB_ROWB, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(gs + (int64_t)(2 * kt) * p.ldbs, st + s_lds, 4, 0, 0);
+    };
+
+    f32x16_t acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.f;
+
+    const int lrow = lane & 31, g = lane >> 5;
+    int sa[FM], bofs[FN], qsw[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) sa[i] = swz8(wm + 32 * i + lrow);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = wn + 32 * j + lrow;
+        bofs[j] = n * QB_ROWB;
+        qsw[j] = qswz(n);
+    }
+    bf16x8_t wa[FN], xa[FM], wb[FN], xb[FM];
+    uint2 braw[FN];
+    float dsc[FN];
+    // Operands of k-step kk (16 of K) of the k-tile in stage s: activations
+    // straight from LDS, this lane's 8 weight codes and their scale into
+    // registers.
+    auto load_ops = [&](int s, int kk, bf16x8_t (&xf)[FM]) {
+        const uint8_t* As = smem + s * QSTAGEB;
+        const uint8_t* Bs_ = As + QA_OPB;
+        const float* Ss = reinterpret_cast<const float*>(As + QA_OPB + QB_OPB) + (kk >> 1) * 256;
+        const int c = 2 * kk + g;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            braw[j] = *reinterpret_cast<const uint2*>(Bs_ + bofs[j] + ((kk ^ qsw[j]) << 4) + 8 * g);
+            dsc[j] = Ss[wn + 32 * j + lrow];
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            xf[i] = *reinterpret_cast<const bf16x8_t*>(As + (wm + 32 * i + lrow) * QA_ROWB + ((c ^ sa[i]) << 4));
+    };
+    auto convert = [&](bf16x8_t (&wf)[FN]) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const uint32_t lo = braw[j].x, hi = braw[j].y;
+            const float d = dsc[j], m = -128.0f * d;
+            float w[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                w[e] = __builtin_fmaf((float)((lo >> (8 * e)) & 0xFFu), d, m);
+                w[4 + e] = __builtin_fmaf((float)((hi >> (8 * e)) & 0xFFu), d, m);
+            }
+            wf[j] = __builtin_bit_cast(bf16x8_t, make_uint4(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]),
+                                                            pack_bf16x2(w[4], w[5]), pack_bf16x2(w[6], w[7])));
+        }
+    };
+    auto mfma = [&](const bf16x8_t (&wf)[FN], const bf16x8_t (&xf)[FM]) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+    };
+
+    const int nk = p.K / QBK;
+#pragma unroll
+    for (int s = 0; s < QSTAGES; ++s)
+        if (s < nk) issue(s, s);
+    // k-tile 0 landed, with min(nk - 1, 2) later k-tiles still in flight.
+    if (nk >= 3) wait_vm<2 * QDMA>();
+    else if (nk == 2) wait_vm<QDMA>();
+    else wait_vm<0>();
+    __builtin_amdgcn_s_barrier();
+    load_ops(0, 0, xa);
+    convert(wa);
+    int st = 0;  // stage of k-tile kt
+    // One k-tile: k-steps 0..3 of stage st (each reads the next k-step's
+    // operands, runs this one's MFMAs and converts the next one's codes),
+    // then the switch to the next stage.  `last`: k-tile kt + 1 is the final
+    // one (nothing in flight after it, nothing more to issue).
+    auto tile = [&](int kt, auto last) {
+        load_ops(st, 1, xb);
+        mfma(wa, xa);
+        convert(wb);
+        load_ops(st, 2, xa);
+        mfma(wb, xb);
+        convert(wa);
+        load_ops(st, 3, xb);
+        mfma(wa, xa);
+        convert(wb);
+        if constexpr (last.value) wait_vm<0>();
+        else wait_vm<QDMA>();
+        // Every wave's reads of stage st have returned before any wave passes
+        // the barrier, so it can take k-tile kt + 3.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if constexpr (!last.value)
+            if (kt + QSTAGES < nk) issue(kt + QSTAGES, st);
+        st = st == QSTAGES - 1 ? 0 : st + 1;
+        load_ops(st, 0, xa);
+        mfma(wb, xb);
+        convert(wa);
+    };
+    for (int kt = 0; kt < nk - 2; ++kt) tile(kt, std::false_type{});
+    if (nk >= 2) tile(nk - 2, std::true_type{});
+    load_ops(st, 1, xb);
+    mfma(wa, xa);
+    convert(wb);
+    load_ops(st, 2, xa);
+    mfma(wb, xb);
+    convert(wa);
+    load_ops(st, 3, xb);
+    mfma(wa, xa);
+    convert(wb);
+    mfma(wb, xb);
+    epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
+}
+
 // ---- 128 x 128, register-staged, 2 stages --------------------------------------
 constexpr int SBK = 64;
 constexpr int SLDSW = SBK + 8;  // padded LDS row, in bf16 elements
@@ -460,8 +654,10 @@ struct Config {
     double rate;  // measured per-CU rate when the CUs are full (PFLOP/s, gfx950)
 };
 // 0: 256 x 256, 8 waves, K = 32 stages (one workgroup per CU); 1: 128 x 128
-// (two per CU); 2: 256 x 256, 4 waves, K = 64 stages.
-constexpr Config kConfigs[3] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15}};
+// (two per CU); 2: 256 x 256, 4 waves, K = 64 stages; 3: Q8_0 weights,
+// 256 x 256, 8 waves, K = 64, three stages (the only one for Q8_0 B).
+constexpr Config kConfigs[4] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
+                                {256, 256, 512, 1, 1.0}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -515,6 +711,8 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
         hipLaunchKernelGGL((gemm_dma256_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == 2)
         hipLaunchKernelGGL((gemm_k64_kernel<TC>), grid, block, 0, st, g);
+    else if (cfg == 3)
+        hipLaunchKernelGGL((gemm_q8_kernel<TC>), grid, block, 0, st, g);
     else
         hipLaunchKernelGGL((gemm_128_kernel<TC>), grid, block, 0, st, g);
     return check_launch("dt_gemm_bf16");
@@ -525,8 +723,14 @@ int validate(const dt_gemm_problem& q, int32_t c_type, Problem* out) {
     DT_REQUIRE(q.K % 64 == 0, "dt_gemm_bf16: K (%lld) must be a multiple of 64", (long long)q.K);
     DT_REQUIRE(q.M < (1ll << 31) && q.N < (1ll << 31) && q.K < (1ll << 31), "dt_gemm_bf16: shape too large");
     if (q.M > 0 && q.N > 0) {  // an empty problem's leading dimensions are never used
-        DT_REQUIRE(q.lda >= q.K && q.ldb >= q.K && q.ldc >= q.N && q.lda % 8 == 0 && q.ldb % 8 == 0,
+        // bf16 B: ldb in elements, % 8; Q8_0 codes: ldb in bytes, % 16.
+        const int64_t ldb_align = q.b_scale ? 16 : 8;
+        DT_REQUIRE(q.lda >= q.K && q.ldb >= q.K && q.ldc >= q.N && q.lda % 8 == 0 && q.ldb % ldb_align == 0,
                    "dt_gemm_bf16: leading dimensions must cover the rows and keep 16-byte alignment");
+        if (q.b_scale) {
+            DT_REQUIRE(q.ld_scale >= q.N && (reinterpret_cast<uintptr_t>(q.b_scale) & 3) == 0,
+                       "dt_gemm_bf16: Q8_0 scales must be 4-byte aligned with ld_scale >= N");
+        }
         DT_REQUIRE(!q.addend || q.ldd >= q.N, "dt_gemm_bf16: ldd < N");
         DT_REQUIRE(q.A && q.B && q.C, "dt_gemm_bf16: null pointer");
         DT_REQUIRE(aligned16(q.A) && aligned16(q.B), "dt_gemm_bf16: A and B must be 16-byte aligned");
@@ -535,7 +739,7 @@ int validate(const dt_gemm_problem& q, int32_t c_type, Problem* out) {
                    "dt_gemm_bf16: C must be %d-byte aligned with ldc %% 4 == 0", 4 * es);
     }
     *out = Problem{(const uint16_t*)q.A, (const uint16_t*)q.B, q.C, q.addend, q.bias, q.lda, q.ldb,
-                   q.ldc, q.ldd, (int)q.M, (int)q.N, (int)q.K};
+                   q.ldc, q.ldd, (int)q.M, (int)q.N, (int)q.K, q.b_scale, q.ld_scale};
     return DT_OK;
 }
 
@@ -546,20 +750,24 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
                                     int32_t config, dt_stream_t stream) {
     using namespace dit;
     DT_REQUIRE(c_type == DT_TYPE_BF16 || c_type == DT_TYPE_F32, "dt_gemm_bf16: c_type %d unsupported", c_type);
-    DT_REQUIRE(config >= -1 && config <= 2, "dt_gemm_bf16: config %d out of range", config);
+    DT_REQUIRE(config >= -1 && config <= 3, "dt_gemm_bf16: config %d out of range", config);
     DT_REQUIRE(count >= 0 && count <= kMaxGroup, "dt_gemm_bf16_grouped: count %d outside 0..%d", count,
                kMaxGroup);
     DT_REQUIRE(problems || count == 0, "dt_gemm_bf16_grouped: null problem list");
     Problem ps[kMaxGroup];
-    int n = 0;
+    int n = 0, n_q8 = 0;
     for (int i = 0; i < count; ++i) {
         Problem p;
         int rc = validate(problems[i], c_type, &p);
         if (rc) return rc;
+        n_q8 += p.Bs != nullptr;
         if (p.M > 0 && p.N > 0) ps[n++] = p;
     }
+    DT_REQUIRE(n_q8 == 0 || n_q8 == count, "dt_gemm_bf16_grouped: a group mixes Q8_0 and bf16 weights");
+    DT_REQUIRE((n_q8 > 0) == (config == 3) || config == -1,
+               "dt_gemm_bf16: config %d does not take %s weights", config, n_q8 ? "Q8_0" : "bf16");
     if (n == 0) return DT_OK;
-    const int cfg = config >= 0 ? config : pick_config(ps, n, cu_count());
+    const int cfg = config >= 0 ? config : n_q8 ? 3 : pick_config(ps, n, cu_count());
     hipStream_t st = (hipStream_t)stream;
     return c_type == DT_TYPE_F32 ? launch<float>(ps, n, cfg, st) : launch<bf16>(ps, n, cfg, st);
 }
@@ -569,6 +777,14 @@ extern "C" int dt_gemm_bf16_config(const void* A, int64_t lda, const void* B, in
                                    int64_t ldd, int32_t c_type, int32_t config, dt_stream_t stream) {
     const dt_gemm_problem p{A, lda, B, ldb, C, ldc, addend, ldd, bias, M, N, K};
     return dt_gemm_bf16_grouped(&p, 1, c_type, config, stream);
+}
+
+extern "C" int dt_gemm_q8_0(const void* A, int64_t lda, const void* codes, int64_t ld_codes, const float* scales,
+                            int64_t ld_scales, void* C, int64_t ldc, int64_t M, int64_t N, int64_t K, const float* bias,
+                            const void* addend, int64_t ldd, int32_t c_type, dt_stream_t stream) {
+    dt_gemm_problem p{A, lda, codes, ld_codes, C, ldc, addend, ldd, bias, M, N, K, scales, ld_scales};
+    DT_REQUIRE(scales != nullptr || M == 0 || N == 0, "dt_gemm_q8_0: null scales");
+    return dt_gemm_bf16_grouped(&p, 1, c_type, -1, stream);
 }
 
 extern "C" int dt_gemm_bf16(const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,

@@ -88,6 +88,11 @@ _SIGS = {
                                       c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32,
                                       c_int32, _S]),
     "dt_gemm_bf16_grouped": (c_int32, [c_void_p, c_int32, c_int32, c_int32, _S]),
+    "dt_gemm_q8_0": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                               c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int32,
+                               _S]),
+    "dt_q8_0_split": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
+                                c_int64, _S]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                      c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
                                      POINTER(c_int64), POINTER(c_int64), c_float, c_int32, _S]),
@@ -374,7 +379,7 @@ def quantize_q8_0(x, out=None):
 def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None, config=-1):
     """a: bf16 [M, K], b: bf16 [N, K] (rows K-contiguous) -> a @ b.T (+ bias) (+ addend).
     config: tile configuration (0: 256x256, 8 waves, K = 32 stages; 1: 128x128;
-    2: 256x256, 4 waves, K = 64 stages; -1: by shape)."""
+    2: 256x256, 4 waves, K = 64 stages; -1: by shape).  Q8_0 weights: gemm_q8_0."""
     torch = _torch()
     M, K = a.shape
     N = b.shape[0]
@@ -392,15 +397,55 @@ def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None, config=-1):
 class GemmProblem(ctypes.Structure):
     _fields_ = [("A", c_void_p), ("lda", c_int64), ("B", c_void_p), ("ldb", c_int64),
                 ("C", c_void_p), ("ldc", c_int64), ("addend", c_void_p), ("ldd", c_int64),
-                ("bias", c_void_p), ("M", c_int64), ("N", c_int64), ("K", c_int64)]
+                ("bias", c_void_p), ("M", c_int64), ("N", c_int64), ("K", c_int64),
+                ("b_scale", c_void_p), ("ld_scale", c_int64)]
+
+
+class Q8Weight:
+    """A Q8_0 weight [N, K] in the split layout dt_gemm_q8_0 reads: uint8 codes
+    (q + 128) [N, K] and fp32 block scales [K/32, N]."""
+
+    def __init__(self, codes, scales):
+        self.codes, self.scales = codes, scales
+        self.shape = (codes.shape[0], codes.shape[1])
+
+
+def q8_0_split(blocks, rows, cols):
+    """blocks: uint8 device tensor of rows * cols/32 Q8_0 blocks -> Q8Weight."""
+    torch = _torch()
+    codes = torch.empty((rows, cols), dtype=torch.uint8, device=blocks.device)
+    scales = torch.empty((cols // 32, rows), dtype=torch.float32, device=blocks.device)
+    check(load().dt_q8_0_split(_p(blocks), rows, cols, cols // 32 * 34, _p(codes), codes.stride(0),
+                               _p(scales), scales.stride(0), stream()), "dt_q8_0_split")
+    return Q8Weight(codes, scales)
+
+
+def gemm_q8_0(a, w, bias=None, addend=None, out=None, out_dtype=None):
+    """a: bf16 [M, K]; w: Q8Weight [N, K] -> a @ dequant(w).T (+ bias) (+ addend)."""
+    torch = _torch()
+    M, K = a.shape
+    N = w.shape[0]
+    assert w.shape[1] == K and a.stride(1) == 1
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=a.device)
+    ldd = addend.stride(0) if addend is not None else 0
+    check(load().dt_gemm_q8_0(_p(a), a.stride(0), _p(w.codes), w.codes.stride(0), _p(w.scales),
+                              w.scales.stride(0), _p(out), out.stride(0), M, N, K, _p(bias), _p(addend), ldd,
+                              io_type(out), stream()), "dt_gemm_q8_0")
+    return out
 
 
 def gemm_grouped(items, config=-1):
-    """items: list of (a [M,K] bf16, b [N,K] bf16, out [M,N]) -> one launch."""
+    """items: list of (a [M,K] bf16, b [N,K] bf16 or Q8Weight, out [M,N]) -> one launch."""
     probs = (GemmProblem * len(items))()
     for i, (a, b, out) in enumerate(items):
-        probs[i] = GemmProblem(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(),
-                               out.stride(0), None, 0, None, a.shape[0], b.shape[0], a.shape[1])
+        if isinstance(b, Q8Weight):
+            probs[i] = GemmProblem(a.data_ptr(), a.stride(0), b.codes.data_ptr(), b.codes.stride(0),
+                                   out.data_ptr(), out.stride(0), None, 0, None, a.shape[0], b.shape[0],
+                                   a.shape[1], b.scales.data_ptr(), b.scales.stride(0))
+        else:
+            probs[i] = GemmProblem(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), out.data_ptr(),
+                                   out.stride(0), None, 0, None, a.shape[0], b.shape[0], a.shape[1], None, 0)
     ct = io_type(items[0][2])
     check(load().dt_gemm_bf16_grouped(ctypes.cast(probs, c_void_p), len(items), ct, config, stream()),
           "dt_gemm_bf16_grouped")

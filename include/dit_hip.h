@@ -187,6 +187,14 @@ int dt_groupnorm_silu(const void *x, int64_t N, int64_t C, int64_t HW, int64_t g
 int dt_euler_step(const void *x, const void *v, float dt, void *y, int64_t n,
                   int32_t io_type, dt_stream_t stream);
 
+/* Q8_0 blocks (rows x cols/32 blocks of {fp16 d; int8 qs[32]}, row_bytes
+ * apart) -> the split layout dt_gemm_q8_0 reads: codes[r][c] = qs + 128 as
+ * uint8 ([rows][ld_codes], ld_codes % 16 == 0) and scales[c / 32][r] = d as
+ * fp32 ([cols/32][ld_scales]).  A one-time weight repack (the reference reads
+ * the blocks from GGUF, src/ggml/GGUFLoaderVisitor.cpp:214-281). */
+int dt_q8_0_split(const void *src, int64_t rows, int64_t cols, int64_t row_bytes, void *codes,
+                  int64_t ld_codes, float *scales, int64_t ld_scales, dt_stream_t stream);
+
 /* Q8_0 quantisation of fp32 rows (ggml quantize_row_q8_0_ref semantics:
  * d = amax/127, q = roundf(x / d), d stored as RNE fp16).  cols % 32 == 0;
  * dst row r starts at dst + r*row_bytes.  Makes Q8_0 weight bytes on the
@@ -214,17 +222,34 @@ int dt_fill_randn(float *y, int64_t n, uint64_t seed, float mean, float std,
 int dt_gemm_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C, int64_t ldc,
                  int64_t M, int64_t N, int64_t K, const float *bias, const void *addend,
                  int64_t ldd, int32_t c_type, dt_stream_t stream);
+/* dt_gemm_bf16 with the weight B kept as Q8_0 (GGUF Q8_0 blocks repacked
+ * once by dt_q8_0_split): each weight is dequantised in the GEMM's load path,
+ * d * q rounded to bf16, so C equals dt_dequant to bf16 followed by
+ * dt_gemm_bf16 bit for bit (finite scales).  The weight stays 1.125 bytes per
+ * element in HBM.  Replaces the same Runtime::mul_mat call as dt_gemm_bf16
+ * for the reference's Q8_0 Linear weights (src/nn/Linear.cpp:17-36;
+ * flux2-klein-9b-q8.json), whose CPU path dequantises inside ggml's matmul.
+ * ld_codes % 16 == 0, scales 4-byte aligned with ld_scales >= N, K % 64 == 0. */
+int dt_gemm_q8_0(const void *A, int64_t lda, const void *codes, int64_t ld_codes, const float *scales,
+                 int64_t ld_scales, void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                 const float *bias, const void *addend, int64_t ldd, int32_t c_type,
+                 dt_stream_t stream);
+
 /* dt_gemm_bf16 with an explicit tile configuration: 0 = 256x256 per
  * workgroup with direct global->LDS loads in four K = 32 stages, 1 = 128x128
- * with two workgroups per CU, 2 = 256x256 with two K = 64 stages; -1 picks by
- * shape as dt_gemm_bf16 does.  For tuning and tests; no counterpart in the
- * reference. */
+ * with two workgroups per CU, 2 = 256x256 with two K = 64 stages, 3 = Q8_0
+ * weights (required for them); -1 picks by shape as dt_gemm_bf16 does.
+ * For tuning and tests; no counterpart in the reference. */
 int dt_gemm_bf16_config(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float *bias,
                         const void *addend, int64_t ldd, int32_t c_type, int32_t config,
                         dt_stream_t stream);
 
-/* One GEMM of a group: the arguments of dt_gemm_bf16. */
+/* One GEMM of a group: the arguments of dt_gemm_bf16.  With b_scale set, B
+ * is a Q8_0 weight in the split layout of dt_q8_0_split (uint8 codes, ldb in
+ * bytes, a multiple of 16) and b_scale its fp32 block scales
+ * [K/32][ld_scale] (ld_scale >= N, 4-byte aligned); every problem of a group
+ * must then be Q8_0. */
 typedef struct dt_gemm_problem {
     const void *A;
     int64_t lda;
@@ -236,6 +261,8 @@ typedef struct dt_gemm_problem {
     int64_t ldd;
     const float *bias;
     int64_t M, N, K;
+    const float *b_scale;
+    int64_t ld_scale;
 } dt_gemm_problem;
 
 /* Up to 8 independent GEMMs (same c_type) in one launch whose tiles share

@@ -1,5 +1,6 @@
-"""GPU parity of the step-time kernels (Linear GEMM, attention) and the Q8_0
-quantiser against the oracle, through the C ABI.
+"""GPU parity of the step-time kernels (Linear GEMM with bf16 or Q8_0
+weights, attention) and the Q8_0 quantiser against the oracle, through the C
+ABI.
 
 Bars: the GEMM with fp32 output is held to |d| <= 1e-5 * max(|ref|, 1) (its
 products of bf16 inputs are exact in fp32 and only the accumulation order
@@ -143,6 +144,95 @@ def test_gemm_rejects_bad_shapes(dev):
     z = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
     w = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
     assert dit_hip.gemm(z, w).shape == (0, 8)
+
+
+# ------------------------------------------------------- Q8_0 weight GEMM --
+def _q8_weight(orc, seed, N, K):
+    """Q8_0 blocks of N(0, 0.02) weights (the device quantiser), their split
+    layout and their bf16 dequantisation."""
+    w = orc.randn(seed, (N, K), std=0.02)
+    blocks = dit_hip.quantize_q8_0(dev_tensor(w, torch.float32))
+    return blocks, dit_hip.q8_0_split(blocks, N, K), dit_hip.dequant(blocks, dit_hip.Q8_0, N, K)
+
+
+def test_q8_0_split_layout(orc, dev):
+    """codes = q + 128 as uint8 and scales = fp32(d) transposed, decoded from
+    the block bytes on the host."""
+    N, K = 37 * 4, 320
+    blocks, q8, _ = _q8_weight(orc, SEED + 260, N, K)
+    torch.cuda.synchronize()
+    raw = blocks.cpu().numpy().reshape(N, K // 32, 34)
+    d = raw[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float32)
+    qs = raw[:, :, 2:].view(np.int8).reshape(N, K)
+    assert np.array_equal(q8.codes.cpu().numpy(), (qs.astype(np.int16) + 128).astype(np.uint8))
+    assert np.array_equal(q8.scales.cpu().numpy(), d.T)
+
+
+Q8_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192), (300, 522, 256)]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,N,K", Q8_SHAPES)
+def test_gemm_q8_0_equals_dequant_then_gemm(orc, dev, M, N, K, out_dtype):
+    """Dequantising in the GEMM's load path gives the bf16 weights dt_dequant
+    writes and the same fp32 accumulation order, so C is bit-identical to
+    dt_dequant followed by the bf16 GEMM; and within the bar of the oracle on
+    the dequantised weights."""
+    print(f"gemm_q8_0 M={M} N={N} K={K} {out_dtype}", flush=True)
+    a = orc.randn(SEED + 261, (M, K))
+    _, q8, wd = _q8_weight(orc, SEED + 262, N, K)
+    ad = dev_tensor(a, torch.bfloat16)
+    y = dit_hip.gemm_q8_0(ad, q8, out_dtype=out_dtype)
+    y_ref = dit_hip.gemm(ad, wd, out_dtype=out_dtype, config=2)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref), "Q8_0 GEMM differs from dequant + bf16 GEMM"
+    check(host(y), orc.linear(orc.round_bf16(a), host(wd)), out_dtype, f"gemm_q8_0 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_q8_0_bias_addend_strided(orc, dev, out_dtype):
+    M, N, K = 300, 384, 512
+    big_a = orc.randn(SEED + 263, (M, K + 128))
+    _, q8, wd = _q8_weight(orc, SEED + 264, N, K)
+    bias = dev_tensor(orc.randn(SEED + 265, (N,), std=0.1), torch.float32)
+    add = dev_tensor(orc.randn(SEED + 266, (M, N + 8)), out_dtype)[:, :N]
+    ad = dev_tensor(big_a, torch.bfloat16)[:, 64:64 + K]
+    out = torch.zeros((M, N + 16), dtype=out_dtype, device="cuda")
+    dit_hip.gemm_q8_0(ad, q8, bias=bias, addend=add, out=out[:, :N])
+    ref = dit_hip.gemm(ad, wd, bias=bias, addend=add, out_dtype=out_dtype, config=2)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :N], ref)
+    assert not out[:, N:].any(), "wrote past N"
+
+
+def test_gemm_q8_0_grouped_and_large(orc, dev):
+    """The five projections of a single-stream block as one grouped Q8_0
+    launch (4608 rows, N = 3072 x 3 + 9216 x 2, K = 3072), bit-identical to
+    the bf16 grouped GEMM on the dequantised weights."""
+    M, K = 4608, 3072
+    a = dev_tensor(orc.randn(SEED + 267, (M, K)), torch.bfloat16)
+    items_q, items_b = [], []
+    for i, N in enumerate([3072, 3072, 3072, 9216, 9216]):
+        _, q8, wd = _q8_weight(orc, SEED + 270 + i, N, K)
+        items_q.append((a, q8, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
+        items_b.append((a, wd, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
+    outs_q = dit_hip.gemm_grouped(items_q)
+    outs_b = dit_hip.gemm_grouped(items_b, config=2)
+    torch.cuda.synchronize()
+    for oq, ob in zip(outs_q, outs_b):
+        assert torch.equal(oq, ob)
+
+
+def test_gemm_q8_0_rejects(orc, dev):
+    a = torch.zeros((64, 64), dtype=torch.bfloat16, device="cuda")
+    _, q8, wd = _q8_weight(orc, SEED + 280, 64, 64)
+    with pytest.raises(RuntimeError, match="mixes Q8_0 and bf16"):
+        dit_hip.gemm_grouped([(a, q8, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda")),
+                              (a, wd, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))])
+    with pytest.raises(RuntimeError, match="does not take Q8_0"):
+        dit_hip.gemm_grouped([(a, q8, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))], config=2)
+    with pytest.raises(RuntimeError, match="does not take bf16"):
+        dit_hip.gemm_grouped([(a, wd, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))], config=3)
 
 
 # ---------------------------------------------------------------- attention --
