@@ -30,6 +30,8 @@ sample, timed on this host's cores.
 driver (diffusers-cpp_amd/bin/dit_cli) as a child process: Q8_0 weights
 drawn N(0, 0.02) and dequantised once to bf16, bf16 activations, inputs and
 weights resident in HBM, median wall time per step of the recorded graph.
+`denoise_step_q8_0_weights` is the same step with the Linear weights kept as
+Q8_0 (dequantised inside the GEMMs; same outputs bit for bit).
 
 Prints ONE JSON line.
 """
@@ -257,14 +259,16 @@ def denoise_flops(n_img=4096, n_txt=512, d=3072, mlp=9216, blocks=25, txt_width=
     return 2 * lin + blocks * 4 * s * s * d
 
 
-def denoise_step(steps, warmup):
-    """Run the full-step driver as a child process; None if it is missing."""
+def denoise_step(steps, warmup, weight_format="bf16"):
+    """Run the full-step driver as a child process; None if it is missing.
+    weight_format: what the GEMMs read, bf16 copies of the Q8_0 weights or
+    the Q8_0 weights themselves (dequantised inside the GEMM)."""
     import subprocess
     cli = os.path.join(PKG, "bin", "dit_cli")
     if not os.path.exists(cli):
         return None
     cmd = [cli, "Flux2Transformer2DModel", "--random-weights", "1", "--random-inputs", "2",
-           "--steps", str(steps), "--warmup", str(warmup)]
+           "--steps", str(steps), "--warmup", str(warmup), "--weight-format", weight_format]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         raise RuntimeError(f"dit_cli failed ({r.returncode}): {r.stderr.strip()[-500:]}")
@@ -275,7 +279,11 @@ def denoise_step(steps, warmup):
         "workload": "Flux2-klein-4B-shaped transformer step at 1024^2: 5 double + 20 single blocks, "
                     "hidden 3072, 24x128 heads, MLP 9216, 4096 image + 512 text tokens (text width 2560), "
                     "timestep 0.5, no guidance embedding",
-        "weights": "Q8_0 (N(0,0.02) quantised on device) dequantised once to bf16; RMSNorm weights N(1,0.02)",
+        "weights": ("Q8_0 (N(0,0.02) quantised on device) dequantised once to bf16"
+                    if weight_format == "bf16" else
+                    "Q8_0 (N(0,0.02) quantised on device) kept as Q8_0 (codes + fp32 scales, 1.125 B/weight), "
+                    "dequantised inside the GEMM") + "; RMSNorm weights N(1,0.02)",
+        "linear_weight_bytes": res["linear_weight_bytes"],
         "s_per_step": round(t, 5),
         "ms_per_step_min": res["ms_per_step_min"],
         "ms_per_step_mean": res["ms_per_step_mean"],
@@ -313,6 +321,8 @@ def main():
 
     # The full step runs in its own process before this one touches the GPU.
     denoise = denoise_step(args.denoise_steps, args.denoise_warmup) if args.denoise_steps > 0 else None
+    denoise_q8 = (denoise_step(args.denoise_steps, args.denoise_warmup, "q8_0")
+                  if args.denoise_steps > 0 and args.secondary else None)
 
     import torch
     import dit_hip
@@ -457,6 +467,7 @@ def main():
         "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "sec_per_denoise_step": denoise["s_per_step"] if denoise else None,
         "denoise_step": denoise,
+        "denoise_step_q8_0_weights": denoise_q8,
         "copy_ceiling_GBs": round(ceiling, 1),
         "kernels": kernels,
         "kernels_standalone": kernels_standalone,

@@ -130,9 +130,46 @@ Args parse(int argc, char** argv) {
     return a;
 }
 
+// Device buffers the CLI binds to leaves itself (resident weights and
+// inputs), freed when the session ends.
+struct DeviceBuffers {
+    dt_backend* be = nullptr;
+    std::vector<void*> ptrs;
+    void* alloc(size_t bytes) {
+        void* p = nullptr;
+        check(dt_buffer_alloc(be, bytes ? bytes : 1, &p), "dt_buffer_alloc");
+        ptrs.push_back(p);
+        return p;
+    }
+    void release(void* p) {
+        auto it = std::find(ptrs.begin(), ptrs.end(), p);
+        if (it != ptrs.end()) ptrs.erase(it);
+        check(dt_buffer_free(be, p), "dt_buffer_free");
+    }
+    ~DeviceBuffers() {
+        for (void* p : ptrs) dt_buffer_free(be, p);
+    }
+};
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// fp32 Linear weight rows on the device -> Q8_0 blocks (dt_quantize_q8_0: the
+// bytes a GGUF Q8_0 tensor holds) -> the DT_TYPE_Q8_0_SPLIT layout at dst,
+// through a temporary block buffer `q8` of rows * cols / 32 * 34 bytes.
+void q8_split_from_f32(const float* f32, int64_t rows, int64_t cols, void* q8, void* dst) {
+    const int64_t rb = cols / 32 * 34;
+    check(dt_quantize_q8_0(f32, rows, cols, cols, q8, rb, nullptr), "dt_quantize_q8_0");
+    check(dt_q8_0_split(q8, rows, cols, rb, dst, cols,
+                        reinterpret_cast<float*>((char*)dst + dt_q8_0_split_scale_offset(rows, cols)), rows,
+                        nullptr),
+          "dt_q8_0_split");
+}
+
 class Session {
 public:
-    explicit Session(const Args& a) : args(a), plan_only(a.flag("plan-only", false)), rt(plan_only ? -1 : 0), scope(rt) {}
+    explicit Session(const Args& a) : args(a), plan_only(a.flag("plan-only", false)), rt(plan_only ? -1 : 0), scope(rt) {
+        dev.be = rt.backend();
+    }
 
     Tensor input(const std::string& key) {
         Blob b = read_blob(args.str(key));
@@ -168,9 +205,38 @@ public:
         for (auto& p : ps) {
             Blob b = read_blob(dir + "/" + p.first + ".dtb");
             if (b.shape != p.second.shape()) throw std::runtime_error("shape mismatch for " + p.first);
+            if (p.second.dtype() == DT_TYPE_Q8_0_SPLIT) {
+                load_q8_weight(p.second, b, p.first);
+                continue;
+            }
             auto bytes = convert_blob(b, p.second.dtype());
             rt.bind(*p.second, bytes.data(), bytes.size());
         }
+    }
+    // A Q8_0_SPLIT Linear weight from fp32 values: quantised to Q8_0 and
+    // repacked on the device into a buffer the weight keeps.
+    void load_q8_weight(const Tensor& t, const Blob& b, const std::string& name) {
+        if (b.type != DT_TYPE_F32 || t.ndim() != 2 || t.shape()[1] % 32)
+            throw std::runtime_error("Q8_0 weight " + name + ": needs F32 rows of a multiple of 32");
+        const int64_t rows = t.shape()[0], cols = t.shape()[1];
+        void* f32 = dev.alloc((size_t)(rows * cols * 4));
+        void* q8 = dev.alloc((size_t)(rows * (cols / 32) * 34));
+        dt_tensor tmp{};
+        tmp.type = DT_TYPE_F32;
+        tmp.ne[0] = cols;
+        tmp.ne[1] = rows;
+        tmp.ne[2] = tmp.ne[3] = 1;
+        tmp.nb[0] = 4;
+        tmp.nb[1] = cols * 4;
+        tmp.nb[2] = tmp.nb[3] = rows * cols * 4;
+        tmp.data = f32;
+        check(dt_tensor_set(&tmp, b.bytes.data(), 0, b.bytes.size(), nullptr), "dt_tensor_set");
+        void* dst = dev.alloc((size_t)dt_q8_0_split_bytes(rows, cols));
+        q8_split_from_f32((const float*)f32, rows, cols, q8, dst);
+        check(dt_backend_synchronize(rt.backend()), "dt_backend_synchronize");
+        dev.release(q8);
+        dev.release(f32);
+        rt.bind_device(*t, dst);
     }
     // --plan-only: record and plan the graph without a device.
     void print_plan() {
@@ -202,6 +268,7 @@ public:
     bool plan_only;
     HipRuntime rt;
     RuntimeScope scope;
+    DeviceBuffers dev;  // after rt: freed before the backend
     std::vector<std::pair<Tensor, std::string>> outs;
 };
 
@@ -209,30 +276,18 @@ public:
 //
 // Weights come from --weights DIR (one .dtb per parameter) or, with
 // --random-weights SEED, are generated on the device: every Linear weight is
-// drawn N(0, 0.02) in fp32, quantised to Q8_0 and dequantised once to the
-// BF16 copy the GEMMs read (the Q8_0 bytes are what a GGUF file would hold);
-// RMSNorm weights are N(1, 0.02).  Inputs come from files or, with
-// --random-inputs SEED, are drawn N(0, 1) (latents, text) with the pipeline's
-// position ids (Flux2KleinPipeline.cpp:27-72): text [0, 0, 0, l], image
-// [0, y, x, 0] on a square grid.  Inputs and weights are device-resident
-// before the first step; --warmup W and --steps K run the recorded graph W + K
-// times and report the per-step wall time of the last K.
+// drawn N(0, 0.02) in fp32 and quantised to Q8_0 (the bytes a GGUF file would
+// hold); RMSNorm weights are N(1, 0.02).  --weight-format picks what the GEMMs
+// read: bf16 (default; Q8_0 dequantised once to a BF16 copy, 2 bytes per
+// weight) or q8_0 (repacked once into DT_TYPE_Q8_0_SPLIT, 1.125 bytes per
+// weight, dequantised inside the GEMM to the same bf16 values; weights from
+// --weights DIR are quantised on the device first).  Inputs come from files
+// or, with --random-inputs SEED, are drawn N(0, 1) (latents, text) with the
+// pipeline's position ids (Flux2KleinPipeline.cpp:27-72): text [0, 0, 0, l],
+// image [0, y, x, 0] on a square grid.  Inputs and weights are
+// device-resident before the first step; --warmup W and --steps K run the
+// recorded graph W + K times and report the per-step wall time of the last K.
 
-struct DeviceBuffers {
-    dt_backend* be = nullptr;
-    std::vector<void*> ptrs;
-    void* alloc(size_t bytes) {
-        void* p = nullptr;
-        check(dt_buffer_alloc(be, bytes ? bytes : 1, &p), "dt_buffer_alloc");
-        ptrs.push_back(p);
-        return p;
-    }
-    ~DeviceBuffers() {
-        for (void* p : ptrs) dt_buffer_free(be, p);
-    }
-};
-
-size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Upload host bytes once into a device buffer that `leaf` keeps.
 void resident_input(HipRuntime& rt, DeviceBuffers& bufs, const Tensor& leaf, const void* host, size_t bytes) {
@@ -241,14 +296,21 @@ void resident_input(HipRuntime& rt, DeviceBuffers& bufs, const Tensor& leaf, con
     check(dt_tensor_set(*leaf, host, 0, bytes, nullptr), "dt_tensor_set");
 }
 
-void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffers& bufs, size_t* bf16_bytes,
+void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffers& bufs, size_t* resident_bytes,
                     size_t* q8_bytes, size_t* n_params) {
     std::vector<std::pair<std::string, Tensor>> ps;
     m.named_parameters(ps);
+    auto linear = [](const Tensor& t) { return t.dtype() == DT_TYPE_BF16 || t.dtype() == DT_TYPE_Q8_0_SPLIT; };
+    auto resident = [](const Tensor& t) {
+        return t.dtype() == DT_TYPE_BF16 ? (size_t)t.numel() * 2
+                                         : (size_t)dt_q8_0_split_bytes(t.shape()[0], t.shape()[1]);
+    };
     size_t total = 0, max_n = 0;
     for (auto& p : ps)
-        if (p.second.dtype() == DT_TYPE_BF16) {
-            total += align256((size_t)p.second.numel() * 2);
+        if (linear(p.second)) {
+            if (p.second.ndim() != 2 || p.second.shape()[1] % 32)
+                throw std::runtime_error("random weight layout: " + p.first);
+            total += align256(resident(p.second));
             max_n = std::max(max_n, (size_t)p.second.numel());
         }
     char* big = (char*)bufs.alloc(total);
@@ -257,20 +319,24 @@ void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffer
     std::mt19937_64 gen(seed);
     std::normal_distribution<float> nd(1.0f, 0.02f);
     size_t off = 0, idx = 0;
-    *bf16_bytes = *q8_bytes = *n_params = 0;
+    *resident_bytes = *q8_bytes = *n_params = 0;
     for (auto& p : ps) {
         const Tensor& t = p.second;
         *n_params += (size_t)t.numel();
         ++idx;
-        if (t.dtype() == DT_TYPE_BF16) {
-            if (t.ndim() != 2 || t.shape()[1] % 32) throw std::runtime_error("random weight layout: " + p.first);
+        if (linear(t)) {
             const int64_t rows = t.shape()[0], cols = t.shape()[1], rb = cols / 32 * 34;
             check(dt_fill_randn(f32, rows * cols, seed * 1000003ull + idx, 0.0f, 0.02f, nullptr), "dt_fill_randn");
-            check(dt_quantize_q8_0(f32, rows, cols, cols, q8, rb, nullptr), "dt_quantize_q8_0");
-            check(dt_dequant(q8, DT_TYPE_Q8_0, rows, cols, rb, big + off, cols, DT_TYPE_BF16, nullptr), "dt_dequant");
+            if (t.dtype() == DT_TYPE_BF16) {
+                check(dt_quantize_q8_0(f32, rows, cols, cols, q8, rb, nullptr), "dt_quantize_q8_0");
+                check(dt_dequant(q8, DT_TYPE_Q8_0, rows, cols, rb, big + off, cols, DT_TYPE_BF16, nullptr),
+                      "dt_dequant");
+            } else {
+                q8_split_from_f32(f32, rows, cols, q8, big + off);
+            }
             rt.bind_device(*t, big + off);
-            off += align256((size_t)t.numel() * 2);
-            *bf16_bytes += (size_t)t.numel() * 2;
+            off += align256(resident(t));
+            *resident_bytes += resident(t);
             *q8_bytes += (size_t)(rows * rb);
         } else if (t.dtype() == DT_TYPE_F32) {
             std::vector<float> h((size_t)t.numel());
@@ -298,9 +364,10 @@ void run_model(Session& s, const Args& a) {
     const int steps = (int)a.i64("steps", 1), warmup = (int)a.i64("warmup", 0);
 
     HipRuntime& rt = s.rt;
-    DeviceBuffers bufs;
-    bufs.be = rt.backend();
-    LinearWeightType wt(DT_TYPE_BF16);
+    DeviceBuffers& bufs = s.dev;
+    const std::string format = a.str("weight-format", "bf16");
+    if (format != "bf16" && format != "q8_0") throw std::runtime_error("--weight-format must be bf16 or q8_0");
+    LinearWeightType wt(format == "q8_0" ? DT_TYPE_Q8_0_SPLIT : DT_TYPE_BF16);
     Flux2Transformer2DModel model(cfg);
 
     Tensor hidden = Tensor::empty({1, n_img, cfg.in_channels}, DT_TYPE_BF16);
@@ -310,7 +377,7 @@ void run_model(Session& s, const Args& a) {
     Tensor txt_ids = Tensor::empty({n_txt, 4}, DT_TYPE_I32);
     for (const Tensor* t : {&hidden, &text, &timestep, &img_ids, &txt_ids}) rt.set_input(**t);
 
-    size_t bf16_bytes = 0, q8_bytes = 0, n_params = 0;
+    size_t resident_bytes = 0, q8_bytes = 0, n_params = 0;
     if (s.plan_only) {
         std::vector<std::pair<std::string, Tensor>> ps;
         model.named_parameters(ps);
@@ -327,7 +394,7 @@ void run_model(Session& s, const Args& a) {
         return;
     }
     if (a.has("random-weights")) {
-        random_weights(rt, model, (uint64_t)a.i64("random-weights"), bufs, &bf16_bytes, &q8_bytes, &n_params);
+        random_weights(rt, model, (uint64_t)a.i64("random-weights"), bufs, &resident_bytes, &q8_bytes, &n_params);
     } else {
         s.load_weights(model, a.str("weights"));
     }
@@ -395,10 +462,11 @@ void run_model(Session& s, const Args& a) {
     std::printf("{\"command\": \"Flux2Transformer2DModel\", \"steps\": %d, \"warmup\": %d, "
                 "\"ms_per_step_median\": %.4f, \"ms_per_step_mean\": %.4f, \"ms_per_step_min\": %.4f, "
                 "\"nodes\": %d, \"kernels\": %d, \"fused_nodes\": %d, \"arena_bytes\": %zu, "
-                "\"params\": %zu, \"bf16_weight_bytes\": %zu, \"q8_0_weight_bytes\": %zu}\n",
+                "\"params\": %zu, \"weight_format\": \"%s\", \"linear_weight_bytes\": %zu, "
+                "\"q8_0_weight_bytes\": %zu}\n",
                 steps, warmup, sorted.empty() ? 0.0 : sorted[sorted.size() / 2], mean,
                 sorted.empty() ? 0.0 : sorted.front(), st.nodes, st.kernels, st.fused_nodes, st.arena_bytes,
-                n_params, bf16_bytes, q8_bytes);
+                n_params, format.c_str(), resident_bytes, q8_bytes);
 }
 
 void run(const Args& a) {

@@ -236,6 +236,12 @@ extern "C" int dt_q8_0_split(const void* src, int64_t rows, int64_t cols, int64_
     return dit::check_launch("dt_q8_0_split");
 }
 
+extern "C" int64_t dt_q8_0_split_scale_offset(int64_t rows, int64_t cols) { return (rows * cols + 255) / 256 * 256; }
+
+extern "C" int64_t dt_q8_0_split_bytes(int64_t rows, int64_t cols) {
+    return dt_q8_0_split_scale_offset(rows, cols) + cols / 32 * rows * 4;
+}
+
 extern "C" int dt_quantize_q8_0(const float* src, int64_t rows, int64_t cols, int64_t src_stride, void* dst,
                                 int64_t row_bytes, dt_stream_t stream) {
     DT_REQUIRE(rows >= 0 && cols > 0 && cols % 32 == 0, "dt_quantize_q8_0: cols must be a positive multiple of 32");

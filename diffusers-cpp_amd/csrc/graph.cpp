@@ -470,28 +470,50 @@ bool match_qk(Graph& g, const dt_tensor* y, Plan& p) {
     return true;
 }
 
-// Operands of MUL_MAT node t as a dt_gemm_bf16 call: weight rows [N][K],
-// activation rows [M][K], output rows [M][N].
+// Operands of MUL_MAT node t as a dt_gemm_bf16 / dt_gemm_q8_0 call: weight
+// rows [N][K] (BF16, or a whole DT_TYPE_Q8_0_SPLIT weight: codes, then
+// scales bs [K/32][N]), activation rows [M][K], output rows [M][N].
 struct GemmArgs {
     const void *a, *b;
     int64_t lda, ldb, M, N, K;
+    const float* bs;
+    int64_t ldbs;
 };
+
+bool q8_weight(const dt_tensor* t) { return t->src[0] && t->src[0]->type == DT_TYPE_Q8_0_SPLIT; }
 
 bool gemm_args(const dt_tensor* t, GemmArgs* g) {
     const dt_tensor* w = t->src[0];
     const dt_tensor* x = t->src[1];
-    if (!w || !x || w->type != DT_TYPE_BF16 || x->type != DT_TYPE_BF16) return false;
-    if (w->ne[2] != 1 || w->ne[3] != 1 || w->nb[0] != 2 || x->ne[0] != w->ne[0]) return false;
+    if (!w || !x || x->type != DT_TYPE_BF16) return false;
+    const bool q8 = w->type == DT_TYPE_Q8_0_SPLIT;
+    if (!q8 && w->type != DT_TYPE_BF16) return false;
+    if (w->ne[2] != 1 || w->ne[3] != 1 || x->ne[0] != w->ne[0]) return false;
+    if (q8) {
+        // The scales sit after all N rows of codes: only the whole weight.
+        if (w->op == DT_OP_VIEW || w->nb[0] != 1 || (w->ne[1] > 1 && w->nb[1] != w->ne[0])) return false;
+    } else if (w->nb[0] != 2 || (w->ne[1] > 1 && w->nb[1] % 2)) {
+        return false;
+    }
     int64_t rows, xs;
     if (!row_layout(x, &rows, &xs)) return false;
-    if (w->ne[1] > 1 && w->nb[1] % 2) return false;
     g->a = x->data;
     g->lda = xs;
     g->b = w->data;
-    g->ldb = w->ne[1] > 1 ? w->nb[1] / 2 : w->ne[0];
     g->M = rows;
     g->N = w->ne[1];
     g->K = w->ne[0];
+    if (q8) {
+        g->ldb = g->K;
+        g->bs = w->data ? reinterpret_cast<const float*>((const char*)w->data +
+                                                         dt_q8_0_split_scale_offset(g->N, g->K))
+                        : nullptr;
+        g->ldbs = g->N;
+    } else {
+        g->ldb = w->ne[1] > 1 ? w->nb[1] / 2 : w->ne[0];
+        g->bs = nullptr;
+        g->ldbs = 0;
+    }
     return true;
 }
 
@@ -521,12 +543,18 @@ bool match_gemm_add(Graph& g, const dt_tensor* a, Plan& p) {
     return false;
 }
 
+constexpr const char* kMulMatOperands =
+    "dt_graph_compute: MUL_MAT needs BF16 or whole Q8_0_SPLIT weight rows and BF16 activation rows";
+
 int run_mul_mat(hipStream_t st, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
     GemmArgs g;
     int64_t ldc = 0, ldd = 0;
-    DT_REQUIRE(gemm_args(mm, &g), "dt_graph_compute: MUL_MAT needs BF16 weight rows and BF16 activation rows");
+    DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
     DT_REQUIRE(out_rows(out, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
     if (addend) DT_REQUIRE(out_rows(addend, g.N, &ldd), "dt_graph_compute: bad GEMM addend");
+    if (g.bs)
+        return dt_gemm_q8_0(g.a, g.lda, g.b, g.ldb, g.bs, g.ldbs, out->data, ldc, g.M, g.N, g.K, nullptr,
+                            addend ? addend->data : nullptr, ldd, out->type, st);
     return dt_gemm_bf16(g.a, g.lda, g.b, g.ldb, out->data, ldc, g.M, g.N, g.K, nullptr,
                         addend ? addend->data : nullptr, ldd, out->type, st);
 }
@@ -550,17 +578,18 @@ int run_gemm_group(hipStream_t st, const std::vector<const dt_tensor*>& members)
         const dt_tensor* mm = members[i];
         GemmArgs g;
         int64_t ldc = 0;
-        DT_REQUIRE(gemm_args(mm, &g), "dt_graph_compute: MUL_MAT needs BF16 weight rows and BF16 activation rows");
+        DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
         DT_REQUIRE(out_rows(mm, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
         ps[i] = dt_gemm_problem{data_of(mm->src[1]), g.lda, data_of(mm->src[0]), g.ldb, mm->data, ldc, nullptr, 0,
-                                nullptr, g.M, g.N, g.K};
+                                nullptr, g.M, g.N, g.K, g.bs, g.ldbs};
     }
     return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
 }
 
 // Forward pass over unfused MUL_MATs: node i starts a group of the MUL_MATs
 // that follow it with only VIEWs in between, whose inputs all run before i
-// and whose output type matches; the later members run in i's launch.
+// and whose output type and weight kind (BF16 or Q8_0_SPLIT) match; the later
+// members run in i's launch.
 void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
     auto ready_before = [&](const dt_tensor* t, int pos) {
         while (t && t->op == DT_OP_VIEW) t = t->src[0];
@@ -579,8 +608,8 @@ void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
         for (int j = i + 1; j < n && members.size() < 8; ++j) {
             const dt_tensor* t = nodes[j];
             if (t->op == DT_OP_VIEW) continue;
-            if (!groupable(j) || t->type != nodes[i]->type || !ready_before(t->src[0], i) ||
-                !ready_before(t->src[1], i))
+            if (!groupable(j) || t->type != nodes[i]->type || q8_weight(t) != q8_weight(nodes[i]) ||
+                !ready_before(t->src[0], i) || !ready_before(t->src[1], i))
                 break;
             members.push_back(j);
         }

@@ -93,6 +93,8 @@ _SIGS = {
                                _S]),
     "dt_q8_0_split": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                 c_int64, _S]),
+    "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
+    "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                      c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
                                      POINTER(c_int64), POINTER(c_int64), c_float, c_int32, _S]),

@@ -39,6 +39,8 @@ int64_t elem_size(int32_t type) {
         case DT_TYPE_F16:
         case DT_TYPE_BF16:
             return 2;
+        case DT_TYPE_Q8_0_SPLIT:  // one code byte per element; scales follow the codes
+            return 1;
         default:
             return 0;
     }
@@ -156,6 +158,7 @@ HipRuntime::~HipRuntime() {
 }
 
 size_t HipRuntime::nbytes(const Node* t) {
+    if (t->type == DT_TYPE_Q8_0_SPLIT) return (size_t)dt_q8_0_split_bytes(t->ne[1] * t->ne[2] * t->ne[3], t->ne[0]);
     int64_t qk, bs;
     block_layout(t->type, &qk, &bs);
     return (size_t)(nelements(t) / qk * bs);
@@ -296,17 +299,19 @@ Node* HipRuntime::scale(Node* t, float value) {
 Node* HipRuntime::clamp(Node* t, float mn, float mx) { return unary(t, DT_UN_CLAMP, mn, mx); }
 
 // ggml_mul_mat(w, x) (Runtime.hpp:136-139; Linear.cpp:24): y = x W^T over
-// ne0.  The MFMA GEMM takes BF16 operands: an F32 operand is cast to BF16 by
-// a CPY node first (ggml's CPU backend likewise converts the activation to
+// ne0.  The MFMA GEMM takes BF16 activations and BF16 or Q8_0_SPLIT weights
+// (Q8_0 dequantised to bf16 inside the GEMM): an F32 operand is cast to BF16
+// by a CPY node first (ggml's CPU backend likewise converts the activation to
 // the weight's vec_dot type), and the result is F32 when the activation was
 // F32 (ggml's result type) or BF16 for BF16 activations.
 Node* HipRuntime::mul_mat(Node* w, Node* x) {
     if (w->ne[0] != x->ne[0]) throw std::invalid_argument("mul_mat: ne0 (K) of weight and input differ");
     if (w->ne[2] != 1 || w->ne[3] != 1) throw Unsupported("mul_mat: batched weights are not supported");
     if (w->type == DT_TYPE_Q8_0 || w->type == DT_TYPE_Q4_K)
-        throw Unsupported("mul_mat: dequantise Q8_0/Q4_K weights to BF16 once at load (dt_dequant)");
+        throw Unsupported("mul_mat: repack Q8_0 weights once at load (dt_q8_0_split -> DT_TYPE_Q8_0_SPLIT) or "
+                          "dequantise them to BF16 (dt_dequant)");
     const int32_t out_type = x->type == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32;
-    if (w->type != DT_TYPE_BF16) w = cast(w, DT_TYPE_BF16);
+    if (w->type != DT_TYPE_BF16 && w->type != DT_TYPE_Q8_0_SPLIT) w = cast(w, DT_TYPE_BF16);
     if (x->type != DT_TYPE_BF16) x = cast(x, DT_TYPE_BF16);
     else if (x->nb[0] != 2) x = cont(x);
     const int64_t ne[4] = {w->ne[1], x->ne[1], x->ne[2], x->ne[3]};

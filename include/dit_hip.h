@@ -40,14 +40,21 @@
 extern "C" {
 #endif
 
-/* ggml type ids (ggml.h enum ggml_type), kept numerically identical. */
+/* ggml type ids (ggml.h enum ggml_type), kept numerically identical, plus
+ * DT_TYPE_Q8_0_SPLIT: a Q8_0 Linear weight [N][K] repacked once at load by
+ * dt_q8_0_split for dt_gemm_q8_0 (no ggml counterpart; ggml likewise
+ * repacks weights into backend layouts through its "extra" buffer types).
+ * A tensor of this type has ne = {K, N, 1, 1}, nb = {1, K, N K, N K}; its
+ * data holds the uint8 codes [N][K] at offset 0 and the fp32 block scales
+ * [K/32][N] at dt_q8_0_split_scale_offset(N, K). */
 enum {
     DT_TYPE_F32 = 0,
     DT_TYPE_F16 = 1,
     DT_TYPE_Q8_0 = 8,
     DT_TYPE_Q4_K = 12,
     DT_TYPE_I32 = 26,
-    DT_TYPE_BF16 = 30
+    DT_TYPE_BF16 = 30,
+    DT_TYPE_Q8_0_SPLIT = 100
 };
 
 enum {
@@ -194,6 +201,10 @@ int dt_euler_step(const void *x, const void *v, float dt, void *y, int64_t n,
  * the blocks from GGUF, src/ggml/GGUFLoaderVisitor.cpp:214-281). */
 int dt_q8_0_split(const void *src, int64_t rows, int64_t cols, int64_t row_bytes, void *codes,
                   int64_t ld_codes, float *scales, int64_t ld_scales, dt_stream_t stream);
+/* Layout of a DT_TYPE_Q8_0_SPLIT weight of `rows` x `cols`: byte offset of
+ * its scales (the codes rounded up to 256 bytes) and its total size. */
+int64_t dt_q8_0_split_scale_offset(int64_t rows, int64_t cols);
+int64_t dt_q8_0_split_bytes(int64_t rows, int64_t cols);
 
 /* Q8_0 quantisation of fp32 rows (ggml quantize_row_q8_0_ref semantics:
  * d = amax/127, q = roundf(x / d), d stored as RNE fp16).  cols % 32 == 0;

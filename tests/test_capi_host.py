@@ -144,3 +144,13 @@ def test_fastdiv_arithmetic():
         ns = [0, 1, d - 1, d, d + 1, (1 << 31) - 1] + [int(v) for v in rng.randint(0, 1 << 31, 50)]
         for n in ns:
             assert (((n * m) >> 32) + n) >> s == n // d
+
+
+def test_q8_0_split_layout_sizes():
+    """DT_TYPE_Q8_0_SPLIT: codes [N][K] then fp32 scales [K/32][N] at the
+    codes rounded up to 256 bytes."""
+    lib = dit_hip.load()
+    assert lib.dt_q8_0_split_scale_offset(3072, 3072) == 3072 * 3072
+    assert lib.dt_q8_0_split_scale_offset(33, 64) == 2304          # 2112 -> 2304
+    assert lib.dt_q8_0_split_bytes(33, 64) == 2304 + 2 * 33 * 4
+    assert lib.dt_q8_0_split_bytes(9216, 3072) == 9216 * 3072 + 96 * 9216 * 4

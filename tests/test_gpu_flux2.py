@@ -130,32 +130,77 @@ def test_double_block_small(orc, tmp, dtype):
     check(read_dtb(f["oe"]).reshape(n_txt, D), we, f"double block encoder {dtype}")
 
 
-def test_model_small(orc, tmp):
-    """Flux2Transformer2DModel end to end at a small width: 1 double + 2
-    single blocks, 2 x 128 heads, 64 image tokens (8 x 8) and 16 text tokens,
-    timestep 0.5, no guidance embedding."""
-    import oracle.flux2 as of
-    cfg = dict(num_layers=1, num_single_layers=2, num_attention_heads=2, attention_head_dim=128,
-               in_channels=128, joint_attention_dim=128, timestep_guidance_channels=256, mlp_ratio=3.0,
-               rope_theta=2000, axes_dims_rope=[32, 32, 32, 32], eps=1e-6)
-    n_txt, grid = 16, 8
+SMALL_MODEL = dict(num_layers=1, num_single_layers=2, num_attention_heads=2, attention_head_dim=128,
+                   in_channels=128, joint_attention_dim=128, timestep_guidance_channels=256, mlp_ratio=3.0,
+                   rope_theta=2000, axes_dims_rope=[32, 32, 32, 32], eps=1e-6)
+
+
+def _small_model_inputs(orc, tmp, n_txt=16, grid=8):
     n_img = grid * grid
-    P = make_params(orc, of.model_param_shapes(cfg), 5000)
     hid = orc.round_bf16(orc.randn(orc.tensor_seed(4990), (n_img, 128)))
     txt = orc.round_bf16(orc.randn(orc.tensor_seed(4991), (n_txt, 128)))
     pos = flux_positions(n_txt, grid)
-    wd = write_params(tmp, P)
-    f = {n: os.path.join(tmp, n + ".dtb") for n in ("h", "t", "ts", "ii", "ti", "o")}
+    f = {n: os.path.join(tmp, n + ".dtb") for n in ("h", "t", "ts", "ii", "ti")}
     write_dtb(f["h"], hid.reshape(1, n_img, 128), 0)
     write_dtb(f["t"], txt.reshape(1, n_txt, 128), 0)
     write_dtb(f["ts"], np.array([0.5], np.float32), 0)
     write_dtb(f["ii"], pos[n_txt:], 26)
     write_dtb(f["ti"], pos[:n_txt], 26)
-    stats = run_cli("Flux2Transformer2DModel", "--num_layers", 1, "--num_single_layers", 2,
-                    "--num_attention_heads", 2, "--joint_attention_dim", 128, "--img_tokens", n_img,
-                    "--txt_tokens", n_txt, "--weights", wd, "--hidden_states", f["h"],
-                    "--encoder_hidden_states", f["t"], "--timestep", f["ts"], "--img_ids", f["ii"],
-                    "--txt_ids", f["ti"], "--steps", 2, "--out", f["o"])
+    return hid, txt, pos, f
+
+
+def _run_small_model(f, wd, out, n_img, n_txt, *extra):
+    return run_cli("Flux2Transformer2DModel", "--num_layers", 1, "--num_single_layers", 2,
+                   "--num_attention_heads", 2, "--joint_attention_dim", 128, "--img_tokens", n_img,
+                   "--txt_tokens", n_txt, "--weights", wd, "--hidden_states", f["h"],
+                   "--encoder_hidden_states", f["t"], "--timestep", f["ts"], "--img_ids", f["ii"],
+                   "--txt_ids", f["ti"], "--steps", 2, "--out", out, *extra)
+
+
+def test_model_small(orc, tmp):
+    """Flux2Transformer2DModel end to end at a small width: 1 double + 2
+    single blocks, 2 x 128 heads, 64 image tokens (8 x 8) and 16 text tokens,
+    timestep 0.5, no guidance embedding."""
+    import oracle.flux2 as of
+    cfg = SMALL_MODEL
+    P = make_params(orc, of.model_param_shapes(cfg), 5000)
+    hid, txt, pos, f = _small_model_inputs(orc, tmp)
+    n_txt, n_img = txt.shape[0], hid.shape[0]
+    out = os.path.join(tmp, "o.dtb")
+    stats = _run_small_model(f, write_params(tmp, P), out, n_img, n_txt)
     print(f"  {stats}", flush=True)
     want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], P, cfg)
-    check(read_dtb(f["o"]).reshape(n_img, 128), want, "model 1+2 blocks")
+    check(read_dtb(out).reshape(n_img, 128), want, "model 1+2 blocks")
+
+
+def test_model_small_q8_0_weights(orc, tmp):
+    """The same model with --weight-format q8_0: every Linear weight is
+    quantised to Q8_0 on the device, repacked (DT_TYPE_Q8_0_SPLIT) and
+    dequantised inside the GEMMs.  The output equals, bit for bit, the bf16
+    path run on the oracle's bf16 rounding of dequantize(quantize(W)), and is
+    held to the bf16 bar against the oracle's fp32 model on those weights."""
+    import oracle.flux2 as of
+    cfg = SMALL_MODEL
+    P = make_params(orc, of.model_param_shapes(cfg), 5000)
+    Pq = {}
+    for name, a in P.items():
+        if a.ndim == 2:
+            rows, cols = a.shape
+            Pq[name] = orc.round_bf16(orc.dequantize(orc.quantize(a, 8), rows * cols, 8).reshape(rows, cols))
+        else:
+            Pq[name] = a
+    hid, txt, pos, f = _small_model_inputs(orc, tmp)
+    n_txt, n_img = txt.shape[0], hid.shape[0]
+    oq, ob = os.path.join(tmp, "oq.dtb"), os.path.join(tmp, "ob.dtb")
+    sq = _run_small_model(f, write_params(tmp, P), oq, n_img, n_txt, "--weight-format", "q8_0")
+    print(f"  {sq}", flush=True)
+    assert sq["weight_format"] == "q8_0"
+    qdir = os.path.join(tmp, "dequantized")
+    os.makedirs(qdir)
+    sb = _run_small_model(f, write_params(qdir, Pq), ob, n_img, n_txt)
+    assert sb["weight_format"] == "bf16" and sb["kernels"] == sq["kernels"]
+    got_q, got_b = read_dtb(oq), read_dtb(ob)
+    assert np.array_equal(got_q.view(np.uint32), got_b.view(np.uint32)), \
+        f"Q8_0 path differs from bf16 on dequantised weights: max |d| {np.abs(got_q - got_b).max()}"
+    want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], Pq, cfg)
+    check(got_q.reshape(n_img, 128), want, "model 1+2 blocks, Q8_0 weights")

@@ -41,6 +41,13 @@ def test_full_step_graph():
     assert p["arena_bytes"] < 1 << 30 and p["arena_bytes"] * 50 < p["naive_bytes"], p
 
 
+def test_q8_0_weights_plan_like_bf16():
+    """Q8_0 Linear weights (DT_TYPE_Q8_0_SPLIT) take the same MUL_MAT, GEMM
+    accumulate and grouped-projection paths as BF16 ones: identical plan."""
+    q, b = plan(**{"weight-format": "q8_0"}), plan(**{"weight-format": "bf16"})
+    assert q == b
+
+
 @pytest.mark.parametrize("kind,layers,nodes,fused,mm,grouped,deferred", [
     ("single", dict(num_layers=0), 58, 30, 7, 6, 1),
     ("double", dict(num_single_layers=0), 110, 46, 14, 8, 4),
