@@ -103,42 +103,13 @@ __global__ __launch_bounds__(WPB * kWave) void adaln_wave_kernel(
 // unfused graph stores the ADD node and the NORM node reads it back.  One
 // wave per row; h and o arrive as raw vectors and are replaced by the stored
 // r (for bf16 the stored bits are exactly the rounded value); (gate,
-// 1 + scale, shift) staged in LDS per workgroup (36 KB at 3072 columns, so
-// six rows per workgroup keep 4608 rows resident).
-template <typename T, int VPL, bool FULL, int WPB>
-__global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residual_adaln_kernel(
-    const T* __restrict__ h, int64_t hs, const T* __restrict__ o, int64_t os, const float* __restrict__ gate,
-    T* __restrict__ r_out, int64_t rs, const float* __restrict__ shift, const float* __restrict__ scale,
-    T* __restrict__ y, int64_t ys, int rows, int nvec, float cols_f, float eps, float addend) {
+// 1 + scale, shift) are staged in LDS per workgroup, 12 bytes per column.
+template <typename T, int VPL, bool FULL>
+__device__ __forceinline__ void residual_adaln_row(uint4 (&hr)[VPL], const uint4 (&orw)[VPL],
+                                                   const float4* __restrict__ mod, int lane, int nvec, T* rr,
+                                                   T* yr, float cols_f, float eps) {
     constexpr int EPV = Io<T>::EPV;
-    extern __shared__ float4 mod_lds[];  // per 4 columns: (gate, scale + addend, shift)
-    const int lane = threadIdx.x & (kWave - 1);
-    const int row = (int)(blockIdx.x * WPB + threadIdx.x / kWave);
-    const bool active = row < rows;
-
-    uint4 hr[VPL], orw[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const int vi = lane + kWave * j;
-        hr[j] = orw[j] = make_uint4(0, 0, 0, 0);
-        if (active && (FULL || vi < nvec)) {
-            hr[j] = ld_stream(h + (int64_t)row * hs + (int64_t)vi * EPV);
-            orw[j] = ld_stream(o + (int64_t)row * os + (int64_t)vi * EPV);
-        }
-    }
-    const int n4 = nvec * EPV / 4;
-    for (int i = threadIdx.x; i < n4; i += WPB * kWave) {
-        float4 sc = reinterpret_cast<const float4*>(scale)[i];
-        sc.x += addend; sc.y += addend; sc.z += addend; sc.w += addend;
-        mod_lds[3 * i] = reinterpret_cast<const float4*>(gate)[i];
-        mod_lds[3 * i + 1] = sc;
-        mod_lds[3 * i + 2] = reinterpret_cast<const float4*>(shift)[i];
-    }
-    __syncthreads();
-    if (!active) return;
-
     // r = h + (o * gate), stored; its stored bits replace h in registers.
-    T* rr = r_out + (int64_t)row * rs;
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
@@ -149,7 +120,7 @@ __global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residua
             Io<T>::unpack(orw[j], ov);
 #pragma unroll
             for (int e = 0; e < EPV; e += 4) {
-                const float4 g = mod_lds[3 * ((vi * EPV + e) / 4)];
+                const float4 g = mod[3 * ((vi * EPV + e) / 4)];
                 hv[e + 0] = add_rn(hv[e + 0], mul_rn(ov[e + 0], g.x));
                 hv[e + 1] = add_rn(hv[e + 1], mul_rn(ov[e + 1], g.y));
                 hv[e + 2] = add_rn(hv[e + 2], mul_rn(ov[e + 2], g.z));
@@ -179,7 +150,6 @@ __global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residua
     }
     s2 = wave_sum(s2);
     const float rstd = 1.0f / sqrtf(s2 / cols_f + eps);
-    T* yr = y + (int64_t)row * ys;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int vi = lane + kWave * j;
@@ -189,7 +159,7 @@ __global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residua
 #pragma unroll
             for (int e = 0; e < EPV; e += 4) {
                 const int i4 = (vi * EPV + e) / 4;
-                const float4 t = mod_lds[3 * i4 + 1], sh = mod_lds[3 * i4 + 2];
+                const float4 t = mod[3 * i4 + 1], sh = mod[3 * i4 + 2];
                 out[e + 0] = add_rn(mul_rn(mul_rn(v[e + 0] - mean, rstd), t.x), sh.x);
                 out[e + 1] = add_rn(mul_rn(mul_rn(v[e + 1] - mean, rstd), t.y), sh.y);
                 out[e + 2] = add_rn(mul_rn(mul_rn(v[e + 2] - mean, rstd), t.z), sh.z);
@@ -198,6 +168,52 @@ __global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residua
             st_stream(yr + (int64_t)vi * EPV, Io<T>::pack(out));
         }
     }
+}
+
+// (gate, scale + addend, shift) per 4 columns into LDS, by the whole workgroup.
+__device__ __forceinline__ void stage_residual_mod(float4* mod_lds, const float* gate, const float* scale,
+                                                   const float* shift, float addend, int n4, int threads) {
+    for (int i = threadIdx.x; i < n4; i += threads) {
+        float4 sc = reinterpret_cast<const float4*>(scale)[i];
+        sc.x += addend; sc.y += addend; sc.z += addend; sc.w += addend;
+        mod_lds[3 * i] = reinterpret_cast<const float4*>(gate)[i];
+        mod_lds[3 * i + 1] = sc;
+        mod_lds[3 * i + 2] = reinterpret_cast<const float4*>(shift)[i];
+    }
+}
+
+// Every row resident at once: 36 KB of LDS at 3072 columns, so six rows per
+// workgroup keep 4608 rows resident.  Measured on gfx950 at [4608, 3072]
+// bf16: the bound of six waves per SIMD (80 VGPRs, 9 of them spilled) runs
+// 4-6% faster than a bound of five (79 VGPRs, no spill); a persistent
+// variant in which each wave walks several rows and prefetches the next
+// row's h and o ran 25% slower, and 30% slower inside the Flux2 step.
+template <typename T, int VPL, bool FULL, int WPB>
+__global__ __launch_bounds__(WPB * kWave, FULL && VPL <= 6 ? 6 : 1) void residual_adaln_kernel(
+    const T* __restrict__ h, int64_t hs, const T* __restrict__ o, int64_t os, const float* __restrict__ gate,
+    T* __restrict__ r_out, int64_t rs, const float* __restrict__ shift, const float* __restrict__ scale,
+    T* __restrict__ y, int64_t ys, int rows, int nvec, float cols_f, float eps, float addend) {
+    constexpr int EPV = Io<T>::EPV;
+    extern __shared__ float4 mod_lds[];  // per 4 columns: (gate, scale + addend, shift)
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = (int)(blockIdx.x * WPB + threadIdx.x / kWave);
+    const bool active = row < rows;
+
+    uint4 hr[VPL], orw[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int vi = lane + kWave * j;
+        hr[j] = orw[j] = make_uint4(0, 0, 0, 0);
+        if (active && (FULL || vi < nvec)) {
+            hr[j] = ld_stream(h + (int64_t)row * hs + (int64_t)vi * EPV);
+            orw[j] = ld_stream(o + (int64_t)row * os + (int64_t)vi * EPV);
+        }
+    }
+    stage_residual_mod(mod_lds, gate, scale, shift, addend, nvec * EPV / 4, WPB * kWave);
+    __syncthreads();
+    if (!active) return;
+    residual_adaln_row<T, VPL, FULL>(hr, orw, mod_lds, lane, nvec, r_out + (int64_t)row * rs, y + (int64_t)row * ys,
+                                     cols_f, eps);
 }
 
 // Any cols / stride / alignment: one 256-thread block per row, LDS reductions.

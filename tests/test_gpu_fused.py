@@ -242,8 +242,8 @@ def test_gated_residual(orc, dev, dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", DT)
-@pytest.mark.parametrize("rows,cols", [(4608, 3072), (77, 3072), (40, 1000), (9, 512), (6, 6144), (5, 8192),
-                                       (7, 1001)])
+@pytest.mark.parametrize("rows,cols", [(4608, 3072), (77, 3072), (3000, 1024), (40, 1000), (9, 512), (6, 6144),
+                                       (5, 8192), (7, 1001)])
 def test_gated_residual_adaln(orc, dev, dtype, rows, cols):
     """Block i's residual r = h + gate * o feeding block i+1's adaLN, one
     pass.  Reference: the oracle's gated residual, rounded to the I/O type as
@@ -265,6 +265,11 @@ def test_gated_residual_adaln(orc, dev, dtype, rows, cols):
     r_alone = dit_hip.gated_residual(dev_tensor(h, dtype), dev_tensor(o, dtype), f(g))
     torch.cuda.synchronize()
     assert torch.equal(r, r_alone), "fused residual differs from the standalone kernel"
+    # and y bit-identical to the standalone adaLN of that r (same reduction
+    # order), which also pins that every row is written exactly once
+    y_alone = dit_hip.adaln_mod(r_alone, f(sh), f(sc), 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_alone), "fused adaLN differs from the standalone kernel"
     check(host(y), orc.adaln(host(r), sh, sc, 1e-6), dtype, "adaln of r")
     check(host(y), orc.adaln(r_stored, sh, sc, 1e-6), dtype, "adaln of oracle r", one_rounding=False)
 
