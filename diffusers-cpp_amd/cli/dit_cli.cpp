@@ -8,7 +8,11 @@
 // ndim, int32 reserved, int64 shape[ndim] (PyTorch order), raw contiguous
 // data.  Parameters are passed as --param-<name>, outputs as --out[-<name>].
 // One JSON line with graph statistics is printed on success; errors print a
-// message on stderr and exit non-zero.
+// message on stderr and exit non-zero.  Checkpoints: `--gguf PATH` loads a
+// GGUF file (or a directory's first .gguf) as the reference's
+// GGUFLoaderVisitor does; `GgufInfo --gguf PATH` prints a file's header,
+// metadata and tensor table, and `Flux2Transformer2DModel --plan-only true
+// --gguf PATH` the file tensor and range each parameter would be read from.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -24,6 +28,7 @@
 #include <vector>
 
 #include "flux2.hpp"
+#include "gguf.hpp"
 
 using namespace dit::host;
 
@@ -274,8 +279,9 @@ public:
 
 // ---- Flux2Transformer2DModel: one denoising step --------------------------
 //
-// Weights come from --weights DIR (one .dtb per parameter) or, with
-// --random-weights SEED, are generated on the device: every Linear weight is
+// Weights come from --weights DIR (one .dtb per parameter), from --gguf PATH
+// (a FLUX.2 GGUF checkpoint, fused tensors split as the reference's loader
+// splits them) or, with --random-weights SEED, are generated on the device: every Linear weight is
 // drawn N(0, 0.02) in fp32 and quantised to Q8_0 (the bytes a GGUF file would
 // hold); RMSNorm weights are N(1, 0.02).  --weight-format picks what the GEMMs
 // read: bf16 (default; Q8_0 dequantised once to a BF16 copy, 2 bytes per
@@ -348,6 +354,30 @@ void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffer
     }
 }
 
+std::string json_str(const std::string& s) {
+    std::string r = "\"";
+    for (unsigned char ch : s) {
+        if (ch == '"' || ch == '\\') {
+            r += '\\';
+            r += (char)ch;
+        } else if (ch < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", ch);
+            r += buf;
+        } else {
+            r += (char)ch;
+        }
+    }
+    return r + "\"";
+}
+
+std::string json_num(double v) {
+    if (!std::isfinite(v)) return "null";
+    char buf[40];
+    std::snprintf(buf, sizeof buf, "%.17g", v);
+    return buf;
+}
+
 void run_model(Session& s, const Args& a) {
     Flux2Config cfg;
     cfg.num_layers = a.i64("num_layers", 5);
@@ -378,6 +408,34 @@ void run_model(Session& s, const Args& a) {
     for (const Tensor* t : {&hidden, &text, &timestep, &img_ids, &txt_ids}) rt.set_input(**t);
 
     size_t resident_bytes = 0, q8_bytes = 0, n_params = 0;
+    if (s.plan_only && a.has("gguf")) {
+        // Where each parameter would be read from (no device): the file
+        // tensor, rows or columns, and the range; then the unused tensors.
+        GgufFile f(a.str("gguf"));
+        std::vector<std::pair<std::string, Tensor>> ps;
+        model.named_parameters(ps);
+        std::map<std::string, std::vector<int64_t>> shapes;
+        for (auto& p : ps) shapes[p.first] = p.second.shape();
+        std::map<std::string, int> used;
+        std::string out = "{\"command\": \"Flux2Transformer2DModel\", \"gguf_plan\": {";
+        for (size_t i = 0; i < ps.size(); ++i) {
+            const GgufSource src = gguf_source(f, ps[i].first, shapes);
+            used[src.tensor->name] = 1;
+            out += std::string(i ? ", " : "") + json_str(ps[i].first) + ": [" + json_str(src.tensor->name) + ", \"" +
+                   (src.by_cols ? "cols" : "rows") + "\", " + std::to_string(src.begin) + ", " +
+                   std::to_string(src.end) + "]";
+        }
+        out += "}, \"unused\": [";
+        bool first = true;
+        for (const GgufTensor& t : f.tensors())
+            if (!used.count(t.name)) {
+                out += (first ? "" : ", ") + json_str(t.name);
+                first = false;
+            }
+        out += "]}";
+        std::printf("%s\n", out.c_str());
+        return;
+    }
     if (s.plan_only) {
         std::vector<std::pair<std::string, Tensor>> ps;
         model.named_parameters(ps);
@@ -393,8 +451,20 @@ void run_model(Session& s, const Args& a) {
                     st.attention_nodes, st.arena_bytes, st.naive_bytes, n_params);
         return;
     }
+    std::string gguf_note;
     if (a.has("random-weights")) {
         random_weights(rt, model, (uint64_t)a.i64("random-weights"), bufs, &resident_bytes, &q8_bytes, &n_params);
+    } else if (a.has("gguf")) {
+        // A GGUF checkpoint, placed as the reference's GGUFLoaderVisitor
+        // reads it (fused q/k/v/mlp, to_out and linear_in tensors split).
+        GgufFile f(a.str("gguf"));
+        const GgufLoadStats st = load_gguf(model, f, rt, [&](size_t n) { return bufs.alloc(n); });
+        gguf_note = ", \"gguf_tensors_used\": " + std::to_string(st.file_tensors_used) +
+                    ", \"gguf_tensors_unused\": " + std::to_string(st.unused.size()) +
+                    ", \"gguf_bytes_read\": " + std::to_string(st.bytes_read);
+        std::vector<std::pair<std::string, Tensor>> ps;
+        model.named_parameters(ps);
+        for (auto& p : ps) n_params += (size_t)p.second.numel();
     } else {
         s.load_weights(model, a.str("weights"));
     }
@@ -463,13 +533,61 @@ void run_model(Session& s, const Args& a) {
                 "\"ms_per_step_median\": %.4f, \"ms_per_step_mean\": %.4f, \"ms_per_step_min\": %.4f, "
                 "\"nodes\": %d, \"kernels\": %d, \"fused_nodes\": %d, \"arena_bytes\": %zu, "
                 "\"params\": %zu, \"weight_format\": \"%s\", \"linear_weight_bytes\": %zu, "
-                "\"q8_0_weight_bytes\": %zu}\n",
+                "\"q8_0_weight_bytes\": %zu%s}\n",
                 steps, warmup, sorted.empty() ? 0.0 : sorted[sorted.size() / 2], mean,
                 sorted.empty() ? 0.0 : sorted.front(), st.nodes, st.kernels, st.fused_nodes, st.arena_bytes,
-                n_params, format.c_str(), resident_bytes, q8_bytes);
+                n_params, format.c_str(), resident_bytes, q8_bytes, gguf_note.c_str());
+}
+
+// GgufInfo --gguf PATH: the file's header, metadata and tensor table as one
+// JSON line (no device needed).
+void gguf_info(const Args& a) {
+    GgufFile f(a.str("gguf"));
+    std::string out = "{\"command\": \"GgufInfo\", \"path\": " + json_str(f.path()) +
+                      ", \"version\": " + std::to_string(f.version()) +
+                      ", \"alignment\": " + std::to_string(f.alignment()) +
+                      ", \"data_offset\": " + std::to_string(f.data_offset()) +
+                      ", \"file_size\": " + std::to_string(f.file_size()) + ", \"metadata\": {";
+    bool first = true;
+    for (const auto& kv : f.metadata()) {
+        const GgufValue& v = kv.second;
+        out += (first ? "" : ", ") + json_str(kv.first) + ": ";
+        first = false;
+        if (v.type == 8) {
+            out += json_str(v.s);
+        } else if (v.type == 9) {
+            out += "{\"array_type\": " + std::to_string(v.array_type) + ", \"count\": " +
+                   std::to_string(v.array_count) + ", \"values\": [";
+            if (v.array_type == 8)
+                for (size_t i = 0; i < v.array_strings.size(); ++i) out += (i ? ", " : "") + json_str(v.array_strings[i]);
+            else
+                for (size_t i = 0; i < v.array_numbers.size(); ++i) out += (i ? ", " : "") + json_num(v.array_numbers[i]);
+            out += "]}";
+        } else if (v.type == 10) {
+            out += std::to_string(v.u);
+        } else if (v.type == 11) {
+            out += std::to_string(v.i);
+        } else {
+            out += json_num(v.f);
+        }
+    }
+    out += "}, \"tensors\": [";
+    for (size_t i = 0; i < f.tensors().size(); ++i) {
+        const GgufTensor& t = f.tensors()[i];
+        out += std::string(i ? ", " : "") + "{\"name\": " + json_str(t.name) + ", \"type\": " +
+               std::to_string(t.type) + ", \"type_name\": \"" + ggml_type_label(t.type) + "\", \"ne\": [";
+        for (int d = 0; d < t.n_dims; ++d) out += (d ? ", " : "") + std::to_string(t.ne[d]);
+        out += "], \"offset\": " + std::to_string(t.offset) + ", \"nbytes\": " + std::to_string(t.nbytes) + "}";
+    }
+    out += "]}";
+    std::printf("%s\n", out.c_str());
 }
 
 void run(const Args& a) {
+    if (a.command == "GgufInfo") {
+        gguf_info(a);
+        return;
+    }
     Session s(a);
     const std::string& c = a.command;
     if (c == "LayerNorm") {

@@ -204,3 +204,69 @@ def test_model_small_q8_0_weights(orc, tmp):
         f"Q8_0 path differs from bf16 on dequantised weights: max |d| {np.abs(got_q - got_b).max()}"
     want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], Pq, cfg)
     check(got_q.reshape(n_img, 128), want, "model 1+2 blocks, Q8_0 weights")
+
+
+def _gguf_checkpoint(orc, tmp, P, type_of, fname):
+    """P as a FLUX.2 GGUF checkpoint (fused tensors, per-tensor types) and the
+    parameter values a reader decodes from it."""
+    import gguf_writer as gw
+    tensors, where = gw.fuse_flux2(P)
+    items, decoded = [], {}
+    for name, a in sorted(tensors.items()):
+        raw, dec = gw.encode(orc, a, type_of(name, a))
+        items.append((name, type_of(name, a), list(a.shape[::-1]), raw))
+        decoded[name] = dec
+    path = os.path.join(tmp, fname)
+    gw.write_gguf(path, items, [("general.architecture", gw.STRING, "flux2")])
+    return path, {p: gw.split_like(decoded[w[0]], w) for p, w in where.items()}
+
+
+@pytest.mark.parametrize("weight_format", ["bf16", "q8_0"])
+def test_model_small_from_gguf(orc, tmp, weight_format):
+    """The small model from a GGUF checkpoint (dit_cli --gguf), the fused
+    tensors split as the reference's loader splits them.  Linear weights are
+    Q8_0, except (bf16 weights) x_embedder as BF16 and the second single
+    block's to_out as Q4_K; norm weights F32, one F16 and one BF16.  The
+    output equals, bit for bit, the same model run from --weights files
+    holding the decoded values, and is held to the bf16 bar against the
+    oracle on them."""
+    import oracle.flux2 as of
+    cfg = SMALL_MODEL
+    P = make_params(orc, of.model_param_shapes(cfg), 5000)
+
+    def type_of(name, a):
+        if a.ndim == 1:
+            if weight_format == "bf16" and name.endswith("blocks.0.attn.norm_q.weight"):
+                return "F16"
+            if weight_format == "bf16" and name.endswith("blocks.0.attn.norm_k.weight"):
+                return "BF16"
+            return "F32"
+        if weight_format == "bf16" and name == "x_embedder.weight":
+            return "BF16"
+        if weight_format == "bf16" and name == "single_transformer_blocks.1.attn.to_out.weight":
+            return "Q4_K"
+        return "Q8_0"
+
+    path, dec = _gguf_checkpoint(orc, tmp, P, type_of, "model.gguf")
+    Pexp = {k: (orc.round_bf16(v) if v.ndim == 2 else v) for k, v in dec.items()}
+    hid, txt, pos, f = _small_model_inputs(orc, tmp)
+    n_txt, n_img = txt.shape[0], hid.shape[0]
+    og, ow = os.path.join(tmp, "og.dtb"), os.path.join(tmp, "ow.dtb")
+    sg = run_cli("Flux2Transformer2DModel", "--num_layers", 1, "--num_single_layers", 2,
+                 "--num_attention_heads", 2, "--joint_attention_dim", 128, "--img_tokens", n_img,
+                 "--txt_tokens", n_txt, "--gguf", path, "--hidden_states", f["h"],
+                 "--encoder_hidden_states", f["t"], "--timestep", f["ts"], "--img_ids", f["ii"],
+                 "--txt_ids", f["ti"], "--steps", 2, "--out", og, "--weight-format", weight_format)
+    print(f"  {sg}", flush=True)
+    assert sg["gguf_tensors_unused"] == 0 and sg["weight_format"] == weight_format
+    wdir = os.path.join(tmp, "decoded")
+    os.makedirs(wdir)
+    # The files hold the decoded values themselves: the bf16 route rounds them
+    # as dt_dequant does, the q8_0 route re-quantises d * q to the same blocks.
+    sw = _run_small_model(f, write_params(wdir, dec), ow, n_img, n_txt, "--weight-format", weight_format)
+    assert sw["kernels"] == sg["kernels"]
+    got_g, got_w = read_dtb(og), read_dtb(ow)
+    assert np.array_equal(got_g.view(np.uint32), got_w.view(np.uint32)), \
+        f"GGUF path differs from the decoded weights: max |d| {np.abs(got_g - got_w).max()}"
+    want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], Pexp, cfg)
+    check(got_g.reshape(n_img, 128), want, f"model 1+2 blocks from GGUF ({weight_format})")
