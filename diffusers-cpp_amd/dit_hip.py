@@ -93,6 +93,10 @@ _SIGS = {
                                _S]),
     "dt_q8_0_split": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
                                 c_int64, _S]),
+    "dt_conv2d_packed_bytes": (ctypes.c_size_t, [c_int64, c_int64, c_int64]),
+    "dt_conv2d_pack_weights": (c_int32, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, _S]),
+    "dt_conv2d": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32,
+                            c_void_p, c_void_p, c_int32, _S]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
     "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
@@ -452,6 +456,38 @@ def gemm_grouped(items, config=-1):
     check(load().dt_gemm_bf16_grouped(ctypes.cast(probs, c_void_p), len(items), ct, config, stream()),
           "dt_gemm_bf16_grouped")
     return [it[2] for it in items]
+
+
+class ConvWeight:
+    """Conv2d weights [Co, Ci, K, K] packed for dt_conv2d."""
+
+    def __init__(self, packed, co, ci, k):
+        self.packed, self.co, self.ci, self.k = packed, co, ci, k
+
+
+def conv2d_pack(w):
+    """w: fp32 or bf16 device tensor [Co, Ci, K, K] -> ConvWeight."""
+    torch = _torch()
+    co, ci, k, k2 = w.shape
+    assert k == k2 and w.is_contiguous()
+    n = load().dt_conv2d_packed_bytes(co, ci, k)
+    assert n > 0, "unsupported conv weight shape"
+    packed = torch.empty(n, dtype=torch.uint8, device=w.device)
+    check(load().dt_conv2d_pack_weights(_p(w), io_type(w), co, ci, k, _p(packed), stream()),
+          "dt_conv2d_pack_weights")
+    return ConvWeight(packed, co, ci, k)
+
+
+def conv2d(x, w, bias=None, upscale2=False, out=None):
+    """x: [N, Ci, H, W] (fp32/bf16, contiguous); w: ConvWeight -> [N, Co, H', W']."""
+    torch = _torch()
+    N, ci, H, W = x.shape
+    assert ci == w.ci and x.is_contiguous()
+    Hs, Ws = (2 * H, 2 * W) if upscale2 else (H, W)
+    y = torch.empty((N, w.co, Hs, Ws), dtype=x.dtype, device=x.device) if out is None else out
+    check(load().dt_conv2d(_p(x), N, ci, H, W, _p(w.packed), w.co, w.k, 1 if upscale2 else 0, _p(bias), _p(y),
+                           io_type(x), stream()), "dt_conv2d")
+    return y
 
 
 def flash_attn(q, k, v, scale=None, out=None, out_dtype=None):

@@ -213,6 +213,24 @@ int64_t dt_q8_0_split_bytes(int64_t rows, int64_t cols);
 int dt_quantize_q8_0(const float *src, int64_t rows, int64_t cols, int64_t src_stride,
                      void *dst, int64_t row_bytes, dt_stream_t stream);
 
+/* ---- VAE decoder convolutions ------------------------------------------------ */
+
+/* Conv2d::forward (src/nn/modules/conv/Conv2d.cpp:37-108): ggml_conv_2d_direct
+ * with stride 1, dilation 1, a square kernel K in {1, 3} and padding
+ * (K - 1) / 2, then + bias[co]; NCHW, x [N][Ci][H][W] of io_type, y
+ * [N][Co][H'][W'] of io_type.  With upscale2 the conv reads the nearest 2x
+ * upscale of x (H' = 2H, W' = 2W), the `upscale(x, 2, NEAREST)` of
+ * Upsample2D::forward (src/diffusers/models/resnet/Upsample2D.cpp:36-63),
+ * which is then never stored.  Operands are rounded to bf16 (as in
+ * dt_gemm_bf16), sums are fp32.  The weights must first be packed by
+ * dt_conv2d_pack_weights into a buffer of dt_conv2d_packed_bytes. */
+size_t dt_conv2d_packed_bytes(int64_t Co, int64_t Ci, int64_t K);
+int dt_conv2d_pack_weights(const void *w, int32_t w_type, int64_t Co, int64_t Ci, int64_t K,
+                           void *packed, dt_stream_t stream);
+int dt_conv2d(const void *x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void *packed_w,
+              int64_t Co, int64_t K, int32_t upscale2, const float *bias, void *y, int32_t io_type,
+              dt_stream_t stream);
+
 /* Synthetic N(mean, std^2) fp32 data on the device (benchmark weights and
  * inputs; a seeded splitmix64 + Box-Muller stream).  No counterpart in the
  * reference, which reads weights from GGUF files. */

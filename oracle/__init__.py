@@ -64,6 +64,8 @@ def load():
         "or_quantize_q4_K": (None, [P, c_int64, P]),
         "or_dequant_q4_K_f32": (None, [P, c_int64, P]),
         "or_q4_K_scale_min": (None, [c_int, P, P, P]),
+        "or_conv2d_f32": (None, [P, c_int64, c_int64, c_int64, c_int64, P, c_int64, c_int64, c_int64, P,
+                                 c_int, P, c_int]),
         "or_linear_f32": (None, [P, c_int64, c_int64, c_int64, P, c_int64, c_int64, P, P, c_int64,
                                  c_int]),
         "or_attention_f32": (None, [P, P, P, P, c_int64, c_int64, c_int64, c_int64, P, P, P, P,
@@ -270,6 +272,21 @@ def euler(x, v, dt):
 
 
 # ---- matmul and attention ------------------------------------------------------
+
+def conv2d(x, w, b=None, padding=None, up2=False, threads=0):
+    """x: [N, Ci, H, W]; w: [Co, Ci, K, K]; b: [Co] or None -> [N, Co, OH, OW]
+    (stride 1; padding (K-1)/2 by default; up2: on the nearest 2x upscale)."""
+    x, w = _f32(x), _f32(w)
+    N, Ci, H, W = x.shape
+    Co, Ci2, K, K2 = w.shape
+    assert Ci2 == Ci and K2 == K
+    P = (K - 1) // 2 if padding is None else padding
+    Hs, Ws = (2 * H, 2 * W) if up2 else (H, W)
+    y = np.empty((N, Co, Hs + 2 * P - K + 1, Ws + 2 * P - K + 1), dtype=np.float32)
+    bp = _p(_f32(b)) if b is not None else None
+    load().or_conv2d_f32(_p(x), N, Ci, H, W, _p(w), Co, K, P, bp, 1 if up2 else 0, _p(y), threads)
+    return y
+
 
 def linear(x, w, b=None, threads=0):
     """x: [..., K]; w: [N, K] (PyTorch Linear weight); b: [N] or None -> [..., N]."""

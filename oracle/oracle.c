@@ -750,3 +750,50 @@ void or_attention_f32(const float *q, const float *k, const float *v, float *o,
         free(acc);
     }
 }
+
+/* ======================================================================== */
+/* conv2d                                                                   */
+/* ======================================================================== */
+
+/* ggml_conv_2d_direct(w, x, 1, 1, P, P, 1, 1) followed by the bias ADD of
+ * Conv2d::forward (src/nn/modules/conv/Conv2d.cpp:37-108), NCHW, square
+ * kernel K; with up2 the input is first the nearest 2x upscale of x, the
+ * `upscale(x, 2, NEAREST)` of Upsample2D::forward (Upsample2D.cpp:36-63):
+ * xs[n][c][i][j] = x[n][c][i/2][j/2].  Each output is one fp64 sum over
+ * (ci, kh, kw) in that order, rounded to fp32, then + b[co] in fp32 (the
+ * separate ADD node).  Out-of-image taps read zero. */
+void or_conv2d_f32(const float *x, int64_t N, int64_t Ci, int64_t H, int64_t W,
+                   const float *w, int64_t Co, int64_t K, int64_t P, const float *b,
+                   int up2, float *y, int nthreads) {
+    const int64_t Hs = up2 ? 2 * H : H, Ws = up2 ? 2 * W : W;
+    const int64_t OH = Hs + 2 * P - K + 1, OW = Ws + 2 * P - K + 1;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1) OR_OMP_THREADS(nthreads)
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t co = 0; co < Co; ++co) {
+            const float *wc = w + co * Ci * K * K;
+            float *yc = y + (n * Co + co) * OH * OW;
+            for (int64_t oh = 0; oh < OH; ++oh) {
+                for (int64_t ow = 0; ow < OW; ++ow) {
+                    double acc = 0.0;
+                    for (int64_t ci = 0; ci < Ci; ++ci) {
+                        const float *xp = x + (n * Ci + ci) * H * W;
+                        for (int64_t kh = 0; kh < K; ++kh) {
+                            const int64_t ih = oh + kh - P;
+                            if (ih < 0 || ih >= Hs) continue;
+                            for (int64_t kw = 0; kw < K; ++kw) {
+                                const int64_t iw = ow + kw - P;
+                                if (iw < 0 || iw >= Ws) continue;
+                                const float xv = up2 ? xp[(ih / 2) * W + iw / 2] : xp[ih * W + iw];
+                                acc += (double)wc[(ci * K + kh) * K + kw] * (double)xv;
+                            }
+                        }
+                    }
+                    float v = (float)acc;
+                    if (b) v = v + b[co];
+                    yc[oh * OW + ow] = v;
+                }
+            }
+        }
+    }
+}
+

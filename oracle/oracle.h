@@ -121,6 +121,12 @@ void or_q4_K_scale_min(int j, const uint8_t *scales12, uint8_t *sc, uint8_t *m);
  * Each dot product accumulates in double over 4 interleaved lanes (lane l
  * takes k = l mod 4), the lanes are summed in order, and the sum is rounded
  * once to fp32.  Strides are in elements. */
+/* conv_2d_direct (stride 1, padding P, square kernel K) + bias, NCHW; up2:
+ * on the nearest 2x upscale of x.  See oracle.c. */
+void or_conv2d_f32(const float *x, int64_t N, int64_t Ci, int64_t H, int64_t W,
+                   const float *w, int64_t Co, int64_t K, int64_t P, const float *b,
+                   int up2, float *y, int nthreads);
+
 void or_linear_f32(const float *x, int64_t M, int64_t K, int64_t x_stride,
                    const float *w, int64_t N, int64_t w_stride, const float *b,
                    float *y, int64_t y_stride, int nthreads);

@@ -1,0 +1,74 @@
+"""GPU parity of the VAE decoder convolution (dt_conv2d) against the oracle's
+conv_2d_direct + bias (oracle.conv2d), through the C ABI.
+
+The conv rounds its operands to bf16 (as the Linear GEMM does), so the
+reference is the oracle on the bf16-rounded input and weights: fp32 outputs
+are held to |d| <= 1e-5 * max(|ref|, 1) (only the fp32 accumulation order
+differs), bf16 outputs to the bf16 bar (rel L2 <= 1e-2, cos >= 0.9999) plus
+one bf16 ulp for the single output rounding."""
+import numpy as np
+import pytest
+import torch
+
+import dit_hip
+from test_gpu_fused import SEED, as_input, check, dev_tensor, host
+
+pytestmark = pytest.mark.gpu
+
+# (N, Ci, H, W), Co, K, upscale2: one tile; several output-channel tiles with
+# a partial one and two input-channel chunks; 1x1; the upscale with a partial
+# tile along the width; narrow images (16-wide tiles); a VAE mid-block shape.
+SHAPES = [((1, 5, 7, 9), 4, 3, False), ((2, 40, 13, 70), 130, 3, False), ((1, 64, 16, 16), 64, 1, False),
+          ((1, 32, 10, 33), 48, 3, True), ((1, 24, 5, 3), 16, 3, True), ((1, 512, 16, 32), 512, 3, False),
+          ((1, 96, 9, 130), 32, 1, True)]
+
+
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,co,k,up2", SHAPES)
+def test_conv2d(orc, dev, shape, co, k, up2, io):
+    print(f"conv2d x={shape} co={co} k={k} up2={up2} {io}", flush=True)
+    x = orc.randn(SEED + 300, shape)
+    w = orc.randn(SEED + 301, (co, shape[1], k, k), std=0.05)
+    b = orc.randn(SEED + 302, (co,), std=0.1)
+    wp = dit_hip.conv2d_pack(dev_tensor(w, torch.float32))
+    y = dit_hip.conv2d(dev_tensor(x, io), wp, bias=dev_tensor(b, torch.float32), upscale2=up2)
+    torch.cuda.synchronize()
+    ref = orc.conv2d(orc.round_bf16(as_input(x, io)), orc.round_bf16(w), b, up2=up2)
+    assert tuple(y.shape) == ref.shape
+    check(host(y), ref, io, f"conv2d {shape} -> {co} k{k}{' up2' if up2 else ''}")
+
+
+def test_conv2d_bf16_weights_and_no_bias(orc, dev):
+    """bf16 weights pack to the same operands as their fp32 values; no bias."""
+    x = orc.randn(SEED + 303, (1, 48, 12, 20))
+    w = orc.round_bf16(orc.randn(SEED + 304, (40, 48, 3, 3), std=0.05))
+    y32 = dit_hip.conv2d(dev_tensor(x, torch.float32), dit_hip.conv2d_pack(dev_tensor(w, torch.float32)))
+    y16 = dit_hip.conv2d(dev_tensor(x, torch.float32), dit_hip.conv2d_pack(dev_tensor(w, torch.bfloat16)))
+    torch.cuda.synchronize()
+    assert torch.equal(y32, y16)
+    check(host(y32), orc.conv2d(orc.round_bf16(x), w), torch.float32, "conv2d no bias")
+
+
+def test_conv2d_vae_shape_sampled(orc, dev):
+    """[1, 128, 128, 128] -> 128 channels, 3x3 (the last up-block's resnet
+    convs at 1/8 of the 1024^2 area): 16 output channels spread over both
+    halves of the tile checked against the oracle."""
+    x = orc.randn(SEED + 305, (1, 128, 128, 128))
+    w = orc.randn(SEED + 306, (128, 128, 3, 3), std=0.03)
+    b = orc.randn(SEED + 307, (128,), std=0.1)
+    y = dit_hip.conv2d(dev_tensor(x, torch.bfloat16), dit_hip.conv2d_pack(dev_tensor(w, torch.float32)),
+                       bias=dev_tensor(b, torch.float32))
+    torch.cuda.synchronize()
+    sel = np.arange(0, 128, 8)
+    ref = orc.conv2d(orc.round_bf16(x), orc.round_bf16(w[sel]), b[sel])
+    check(host(y)[:, sel], ref, torch.bfloat16, "conv2d 128x128x128 sampled")
+
+
+def test_conv2d_rejects(dev):
+    x = torch.zeros((1, 4, 8, 8), dtype=torch.float32, device="cuda")
+    with pytest.raises(AssertionError):
+        dit_hip.conv2d_pack(torch.zeros((4, 4, 5, 5), dtype=torch.float32, device="cuda"))
+    wp = dit_hip.conv2d_pack(torch.zeros((4, 4, 3, 3), dtype=torch.float32, device="cuda"))
+    wp.k = 5
+    with pytest.raises(RuntimeError, match="kernel size 5 unsupported"):
+        dit_hip.conv2d(x, wp)

@@ -298,3 +298,40 @@ def test_attention_closed_forms(orc):
     qd = np.ones((3, 2, 8), np.float32)
     out = orc.attention(qd, kd, v, scale=100.0)
     assert np.allclose(out, np.broadcast_to(v[4], out.shape), atol=1e-6)
+
+
+# ------------------------------------------------------------------ conv2d --
+@pytest.mark.parametrize("shape,co,k,up2", [((2, 5, 7, 9), 4, 3, False), ((1, 3, 6, 5), 2, 3, True),
+                                            ((1, 6, 4, 4), 7, 1, False), ((1, 2, 3, 3), 3, 1, True)])
+def test_conv2d_matches_torch(orc, shape, co, k, up2):
+    """conv_2d_direct + bias (stride 1, padding (k-1)/2), optionally on the
+    nearest 2x upscale, against torch's float64 conv2d."""
+    torch = pytest.importorskip("torch")
+    x = orc.randn(901, shape)
+    w = orc.randn(902, (co, shape[1], k, k))
+    b = orc.randn(903, (co,))
+    y = orc.conv2d(x, w, b, up2=up2)
+    xt = torch.from_numpy(x).double()
+    if up2:
+        xt = torch.nn.functional.interpolate(xt, scale_factor=2, mode="nearest")
+    t = torch.nn.functional.conv2d(xt, torch.from_numpy(w).double(), torch.from_numpy(b).double(),
+                                   padding=(k - 1) // 2).numpy()
+    assert y.shape == t.shape
+    assert np.abs(y - t).max() <= 1e-5 * max(1.0, np.abs(t).max())
+
+
+def test_conv2d_closed_forms(orc):
+    """A centre-tap kernel returns x (+ b) exactly; an all-ones kernel on
+    ones counts the taps inside the image: 9 inside, 6 on an edge, 4 at a
+    corner; the same on the upscale sees each source pixel twice per axis."""
+    x = orc.randn(904, (1, 3, 5, 6))
+    w = np.zeros((3, 3, 3, 3), np.float32)
+    for c in range(3):
+        w[c, c, 1, 1] = 1.0
+    b = np.array([0.5, -1.0, 2.0], np.float32)
+    assert np.array_equal(orc.conv2d(x, w, b), x + b[None, :, None, None])
+    ones = np.ones((1, 1, 4, 5), np.float32)
+    y = orc.conv2d(ones, np.ones((1, 1, 3, 3), np.float32))[0, 0]
+    assert y[0, 0] == 4 and y[0, 2] == 6 and y[2, 0] == 6 and y[1, 1] == 9 and y[3, 4] == 4
+    yu = orc.conv2d(np.arange(4, dtype=np.float32).reshape(1, 1, 2, 2), np.ones((1, 1, 1, 1), np.float32), up2=True)
+    assert np.array_equal(yu[0, 0], np.array([[0, 0, 1, 1], [0, 0, 1, 1], [2, 2, 3, 3], [2, 2, 3, 3]], np.float32))
