@@ -21,8 +21,11 @@
 //     that 8 consecutive pixels or output channels read distinct banks.
 //   - Operands are rounded to bf16 (as the Linear GEMM's); sums are fp32 in
 //     MFMA order; the epilogue adds the bias in fp32 and stores fp32 or bf16.
+#include <algorithm>
+
 #include "capi_util.hpp"
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace dit {
 namespace {
@@ -45,6 +48,8 @@ struct ConvArgs {
     int Hs, Ws;          // the convolved image (upscaled or not) = output size
     int Ci_pad, KK;
     int TR, TC, tiles_w; // pixel tile geometry; tiles along the width
+    float4* stats;       // GroupNorm tile records [N][G][pixel tiles] (dt_conv2d_gn), or null
+    int G, cg;           // groups over Co and channels per group (cg divides 128)
 };
 
 template <typename TI>
@@ -56,14 +61,87 @@ __device__ __forceinline__ float load_in<bf16>(const bf16* p) {
     return __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(p) << 16);
 }
 
-template <typename T, int K>
+// The value a store of v as T keeps.
+template <typename T>
+__device__ __forceinline__ float stored_value(float v);
+template <>
+__device__ __forceinline__ float stored_value<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float stored_value<bf16>(float v) { return bf16_lo(pack_bf16x2(v, 0.f)); }
+
+// GroupNorm statistics of one output tile, as the stored (rounded) values:
+// per group of cg channels, the tile's mean and M2 = sum (v - mean)^2 over
+// its valid pixels (two passes over the values parked in LDS, fp32), written
+// as one (mean, M2, count, 0) record.  Every thread of the workgroup calls it.
+template <typename T>
+__device__ __forceinline__ void conv_group_stats(const ConvArgs& a, const f32x16_t (&acc)[2][2], uint8_t* smem,
+                                                 int co0, int oh0, int ow0, int wco, int wpx, int lrow, int g) {
+    float* tb = reinterpret_cast<float*>(smem);  // [128 co][128 px]
+    float* red = tb + kTileCo * kTilePx;
+    const int rows_valid = min(a.TR, a.Hs - oh0), cols_valid = min(a.TC, a.Ws - ow0);
+    // The main loop ended with a barrier: LDS is free.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int p = wpx + 32 * i + lrow;
+        const bool valid = p / a.TC < rows_valid && p % a.TC < cols_valid;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int cl = wco + 32 * j + 8 * (r >> 2) + 4 * g + (r & 3);
+                float v = acc[j][i][r];
+                if (a.bias && co0 + cl < a.Co) v = add_rn(v, a.bias[co0 + cl]);
+                tb[cl * kTilePx + p] = valid ? stored_value<T>(v) : 0.f;
+            }
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    const int tpg = 256 / (kTileCo / a.cg);  // threads per group (a power of two)
+    const int gi = tid / tpg, ti = tid - gi * tpg;
+    const float* gv = tb + gi * a.cg * kTilePx;  // the group's rows are contiguous
+    const int n_el = a.cg * kTilePx;
+    const int vp = rows_valid * cols_valid;
+    auto seg_sum = [&](float v) {
+        red[tid] = v;
+        __syncthreads();
+        for (int h = tpg / 2; h > 0; h >>= 1) {
+            if (ti < h) red[tid] += red[tid + h];
+            __syncthreads();
+        }
+        const float r = red[gi * tpg];
+        __syncthreads();
+        return r;
+    };
+    float s1 = 0.f;
+    for (int e = ti; e < n_el; e += tpg) s1 += gv[e];  // invalid pixels hold 0
+    const float mean = seg_sum(s1) / (float)(a.cg * vp);
+    float s2 = 0.f;
+    for (int e = ti; e < n_el; e += tpg) {
+        const int p = e & (kTilePx - 1);
+        if (p / a.TC < rows_valid && p % a.TC < cols_valid) {
+            const float d = gv[e] - mean;
+            s2 += d * d;
+        }
+    }
+    const float m2 = seg_sum(s2);
+    const int grp = co0 / a.cg + gi;
+    if (ti == 0 && grp < a.G)
+        a.stats[((int64_t)blockIdx.z * a.G + grp) * gridDim.x + blockIdx.x] =
+            make_float4(mean, m2, (float)(a.cg * vp), 0.f);
+}
+
+template <typename T, int K, bool STATS>
 __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
     constexpr int KK = K * K, PAD = (K - 1) / 2;
     constexpr int W_BYTES = kTileCo * KK * kRec;
     // input patch: up to (TR + K - 1) x (TC + K - 1) pixels; TR x TC = 128
     constexpr int X_MAX = (128 + K - 1) * (1 + K - 1) > (16 + K - 1) * (8 + K - 1)
                               ? (128 + K - 1) * (1 + K - 1) : (16 + K - 1) * (8 + K - 1);
-    __shared__ __attribute__((aligned(16))) uint8_t smem[W_BYTES + X_MAX * kRec];
+    // With STATS the epilogue reuses LDS for the tile's stored values (64 KB)
+    // and a 256-float reduction array.
+    constexpr int MAIN_BYTES = W_BYTES + X_MAX * kRec;
+    constexpr int STAT_BYTES = kTileCo * kTilePx * 4 + 256 * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[STATS && STAT_BYTES > MAIN_BYTES ? STAT_BYTES : MAIN_BYTES];
     uint8_t* Ws_ = smem;
     uint8_t* Xs = smem + W_BYTES;
 
@@ -166,6 +244,7 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
             }
         }
     }
+    if constexpr (STATS) conv_group_stats<T>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g);
 }
 
 // Repack [Co][Ci][K][K] (fp32 or bf16) to bf16 [Co_pad][K*K][Ci_pad], zeros
@@ -214,19 +293,29 @@ extern "C" int dt_conv2d_pack_weights(const void* w, int32_t w_type, int64_t Co,
     return check_launch("dt_conv2d_pack_weights");
 }
 
-extern "C" int dt_conv2d(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w,
-                         int64_t Co, int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type,
-                         dt_stream_t stream) {
-    using namespace dit;
-    DT_REQUIRE(is_io_type(io_type), "dt_conv2d: io_type %d unsupported", io_type);
-    DT_REQUIRE(N > 0 && Ci > 0 && H > 0 && W > 0 && Co > 0, "dt_conv2d: bad shape");
-    DT_REQUIRE(K == 1 || K == 3, "dt_conv2d: kernel size %lld unsupported (1 or 3)", (long long)K);
-    DT_REQUIRE(x && packed_w && y, "dt_conv2d: null pointer");
-    DT_REQUIRE(aligned16(packed_w), "dt_conv2d: packed weights must be 16-byte aligned");
+namespace dit {
+namespace {
+
+// Tile geometry of an output image of Hs x Ws: TC = 128, 64, 32 or 16 columns.
+void conv_geometry(int64_t Hs, int64_t Ws, int* TR, int* TC, int64_t* tiles_w, int64_t* tiles_h) {
+    *TC = Ws >= 128 ? 128 : Ws >= 64 ? 64 : Ws >= 32 ? 32 : 16;
+    *TR = kTilePx / *TC;
+    *tiles_w = (Ws + *TC - 1) / *TC;
+    *tiles_h = (Hs + *TR - 1) / *TR;
+}
+
+int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
+                int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type, float4* stats,
+                int64_t groups, hipStream_t st, const char* what) {
+    DT_REQUIRE(is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
+    DT_REQUIRE(N > 0 && Ci > 0 && H > 0 && W > 0 && Co > 0, "%s: bad shape", what);
+    DT_REQUIRE(K == 1 || K == 3, "%s: kernel size %lld unsupported (1 or 3)", what, (long long)K);
+    DT_REQUIRE(x && packed_w && y, "%s: null pointer", what);
+    DT_REQUIRE(aligned16(packed_w), "%s: packed weights must be 16-byte aligned", what);
     const int64_t Hs = upscale2 ? 2 * H : H, Ws = upscale2 ? 2 * W : W;
     DT_REQUIRE(N < 65536 && Co < (1 << 24) && Ci < (1 << 24) && Hs * Ws < (1ll << 31) &&
                    N * Ci * H * W < (1ll << 40),
-               "dt_conv2d: shape too large");
+               "%s: shape too large", what);
     ConvArgs a{};
     a.x = x;
     a.w = (const uint16_t*)packed_w;
@@ -237,19 +326,66 @@ extern "C" int dt_conv2d(const void* x, int64_t N, int64_t Ci, int64_t H, int64_
     a.Hs = (int)Hs; a.Ws = (int)Ws;
     a.Ci_pad = (int)pad_to(Ci, kCi);
     a.KK = (int)(K * K);
-    a.TC = Ws >= 128 ? 128 : Ws >= 64 ? 64 : Ws >= 32 ? 32 : 16;
-    a.TR = kTilePx / a.TC;
-    a.tiles_w = (int)((Ws + a.TC - 1) / a.TC);
-    const int64_t tiles_h = (Hs + a.TR - 1) / a.TR;
-    DT_REQUIRE(tiles_h * a.tiles_w < (1ll << 31), "dt_conv2d: too many tiles");
-    const dim3 grid((unsigned)(tiles_h * a.tiles_w), (unsigned)((Co + kTileCo - 1) / kTileCo), (unsigned)N);
-    hipStream_t st = (hipStream_t)stream;
+    int64_t tiles_w, tiles_h;
+    conv_geometry(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
+    a.tiles_w = (int)tiles_w;
+    a.stats = stats;
+    a.G = (int)groups;
+    a.cg = groups > 0 ? (int)(Co / groups) : 0;
+    DT_REQUIRE(tiles_h * tiles_w < (1ll << 31), "%s: too many tiles", what);
+    const dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)((Co + kTileCo - 1) / kTileCo), (unsigned)N);
+#define DT_CONV_LAUNCH(TT, KS, ST) hipLaunchKernelGGL((conv2d_kernel<TT, KS, ST>), grid, dim3(256), 0, st, a)
     if (io_type == DT_TYPE_F32) {
-        if (K == 3) hipLaunchKernelGGL((conv2d_kernel<float, 3>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((conv2d_kernel<float, 1>), grid, dim3(256), 0, st, a);
+        if (K == 3) { if (stats) DT_CONV_LAUNCH(float, 3, true); else DT_CONV_LAUNCH(float, 3, false); }
+        else { if (stats) DT_CONV_LAUNCH(float, 1, true); else DT_CONV_LAUNCH(float, 1, false); }
     } else {
-        if (K == 3) hipLaunchKernelGGL((conv2d_kernel<bf16, 3>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((conv2d_kernel<bf16, 1>), grid, dim3(256), 0, st, a);
+        if (K == 3) { if (stats) DT_CONV_LAUNCH(bf16, 3, true); else DT_CONV_LAUNCH(bf16, 3, false); }
+        else { if (stats) DT_CONV_LAUNCH(bf16, 1, true); else DT_CONV_LAUNCH(bf16, 1, false); }
     }
-    return check_launch("dt_conv2d");
+#undef DT_CONV_LAUNCH
+    return check_launch(what);
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_conv2d(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w,
+                         int64_t Co, int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type,
+                         dt_stream_t stream) {
+    return dit::conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, nullptr, 0,
+                            (hipStream_t)stream, "dt_conv2d");
+}
+
+extern "C" size_t dt_conv2d_gn_stats_bytes(int64_t N, int64_t Co, int64_t OH, int64_t OW, int64_t groups) {
+    if (N <= 0 || Co <= 0 || OH <= 0 || OW <= 0 || groups <= 0 || Co % groups) return 0;
+    int tr, tc;
+    int64_t tw, th;
+    dit::conv_geometry(OH, OW, &tr, &tc, &tw, &th);
+    return (size_t)(dit::gn_tile_stats_head_bytes(N, groups) + N * groups * th * tw * 16);
+}
+
+extern "C" int dt_conv2d_gn(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w,
+                            int64_t Co, int64_t K, int32_t upscale2, const float* bias, void* y, int64_t groups,
+                            void* stats, size_t stats_bytes, int32_t io_type, dt_stream_t stream) {
+    using namespace dit;
+    DT_REQUIRE(groups > 0 && Co % groups == 0, "dt_conv2d_gn: Co %lld not a multiple of groups %lld",
+               (long long)Co, (long long)groups);
+    const int64_t cg = Co / groups;
+    DT_REQUIRE(cg <= kTileCo && kTileCo % cg == 0,
+               "dt_conv2d_gn: %lld channels per group must divide %d", (long long)cg, kTileCo);
+    DT_REQUIRE(stats && ((uintptr_t)stats & 15) == 0, "dt_conv2d_gn: stats must be 16-byte aligned");
+    const int64_t Hs = upscale2 ? 2 * H : H, Ws = upscale2 ? 2 * W : W;
+    const size_t need = dt_conv2d_gn_stats_bytes(N, Co, Hs, Ws, groups);
+    DT_REQUIRE(need > 0 && stats_bytes >= need, "dt_conv2d_gn: stats buffer too small (%zu < %zu)", stats_bytes,
+               need);
+    DT_REQUIRE(N * groups < 65536, "dt_conv2d_gn: N*groups must be < 65536");
+    hipStream_t st = (hipStream_t)stream;
+    float4* recs = (float4*)((char*)stats + gn_tile_stats_head_bytes(N, groups));
+    int rc = conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, recs, groups, st,
+                         "dt_conv2d_gn");
+    if (rc) return rc;
+    int tr, tc;
+    int64_t tw, th;
+    conv_geometry(Hs, Ws, &tr, &tc, &tw, &th);
+    return gn_tile_stats_finalize(stats, N, groups, th * tw, st);
 }

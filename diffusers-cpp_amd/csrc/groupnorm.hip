@@ -16,6 +16,7 @@
 // fit the 256 MB last-level cache are re-read from there.
 #include "capi_util.hpp"
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace dit {
 namespace {
@@ -73,30 +74,13 @@ __global__ __launch_bounds__(kBlock) void gn_stats_kernel(const T* __restrict__ 
     }
 }
 
+// y = silu(((x - mean) * rstd) * w_c + b_c) over this workgroup's chunk of
+// group (n, g).
 template <typename T, bool VEC>
-__global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
-                                                          const double* __restrict__ ws,
-                                                          const float* __restrict__ w,
-                                                          const float* __restrict__ b, T* y,
-                                                          FastDiv hw_vecs) {
+__device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int n, int g, float mean, float rstd,
+                                               const float* __restrict__ w, const float* __restrict__ b, T* y,
+                                               FastDiv hw_vecs) {
     constexpr int EPV = VEC ? Io<T>::EPV : 1;
-    __shared__ double red[kBlock / kWave];
-    const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
-    const double* slot = ws + (int64_t)ng * (2 * s.nchunks + 1);
-    double s1 = 0.0, s2 = 0.0;
-    for (int i = threadIdx.x; i < s.nchunks; i += kBlock) {
-        s1 += slot[1 + 2 * i];
-        s2 += slot[2 + 2 * i];
-    }
-    s1 = block_sum_f64(s1, red);
-    s2 = block_sum_f64(s2, red);
-    const double inv_len = 1.0 / (double)s.group_len;
-    const double dm = s1 * inv_len;
-    double var = s2 * inv_len - dm * dm;
-    if (var < 0.0) var = 0.0;
-    const float mean = (float)(slot[0] + dm);
-    const float rstd = 1.0f / sqrtf((float)var + s.eps);
-
     const int64_t off = (int64_t)n * s.C * s.HW + (int64_t)g * s.group_len;
     const T* xg = x + off;
     T* yg = y + off;
@@ -121,6 +105,83 @@ __global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
         if constexpr (VEC) Io<T>::store(yg + v * EPV, a);
         else Io<T>::put(yg + v, a[0]);
     }
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
+                                                          const double* __restrict__ ws,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ b, T* y,
+                                                          FastDiv hw_vecs) {
+    __shared__ double red[kBlock / kWave];
+    const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
+    const double* slot = ws + (int64_t)ng * (2 * s.nchunks + 1);
+    double s1 = 0.0, s2 = 0.0;
+    for (int i = threadIdx.x; i < s.nchunks; i += kBlock) {
+        s1 += slot[1 + 2 * i];
+        s2 += slot[2 + 2 * i];
+    }
+    s1 = block_sum_f64(s1, red);
+    s2 = block_sum_f64(s2, red);
+    const double inv_len = 1.0 / (double)s.group_len;
+    const double dm = s1 * inv_len;
+    double var = s2 * inv_len - dm * dm;
+    if (var < 0.0) var = 0.0;
+    const float mean = (float)(slot[0] + dm);
+    const float rstd = 1.0f / sqrtf((float)var + s.eps);
+    gn_apply_chunk<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs);
+}
+
+// Statistics from per-tile (mean, M2, count) records, as dt_conv2d_gn writes
+// them: one workgroup per (n, g) merges its group's records with Chan's
+// pairwise update in fp64 -- each thread a fixed strided subset in order,
+// then a fixed-shape tree -- and stores (mean, variance).
+__device__ __forceinline__ void chan_merge(double& n, double& m, double& m2, double nb, double mb, double m2b) {
+    if (nb == 0.0) return;
+    const double t = n + nb, d = mb - m;
+    m += d * (nb / t);
+    m2 += m2b + d * d * (n * nb / t);
+    n = t;
+}
+
+__global__ __launch_bounds__(kBlock) void gn_tile_stats_finalize_kernel(const float4* __restrict__ tiles,
+                                                                        int n_tiles, double2* __restrict__ out) {
+    __shared__ double sn[kBlock], sm[kBlock], s2[kBlock];
+    const int ng = blockIdx.x;
+    const float4* rec = tiles + (int64_t)ng * n_tiles;
+    double n = 0.0, m = 0.0, m2 = 0.0;
+    for (int i = threadIdx.x; i < n_tiles; i += kBlock) {
+        const float4 r = rec[i];
+        chan_merge(n, m, m2, (double)r.z, (double)r.x, (double)r.y);
+    }
+    sn[threadIdx.x] = n;
+    sm[threadIdx.x] = m;
+    s2[threadIdx.x] = m2;
+    __syncthreads();
+    for (int h = kBlock / 2; h > 0; h >>= 1) {
+        if ((int)threadIdx.x < h) {
+            double a = sn[threadIdx.x], am = sm[threadIdx.x], a2 = s2[threadIdx.x];
+            chan_merge(a, am, a2, sn[threadIdx.x + h], sm[threadIdx.x + h], s2[threadIdx.x + h]);
+            sn[threadIdx.x] = a;
+            sm[threadIdx.x] = am;
+            s2[threadIdx.x] = a2;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[ng] = make_double2(sm[0], sn[0] > 0.0 ? s2[0] / sn[0] : 0.0);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void gn_apply_stats_kernel(const T* x, GnShape s,
+                                                                const double2* __restrict__ mv,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ b, T* y,
+                                                                FastDiv hw_vecs) {
+    const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
+    const double2 r = mv[ng];
+    const float mean = (float)r.x;
+    const float rstd = 1.0f / sqrtf((float)r.y + s.eps);
+    gn_apply_chunk<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs);
 }
 
 int64_t chunks_for(int64_t group_vecs) { return (group_vecs + kChunkVecs - 1) / kChunkVecs; }
@@ -187,4 +248,56 @@ extern "C" int dt_groupnorm_silu(const void* x, int64_t N, int64_t C, int64_t HW
                    : dit::launch<float, false>(x, s, N, w, b, y, ws, st);
     return vec ? dit::launch<dit::bf16, true>(x, s, N, w, b, y, ws, st)
                : dit::launch<dit::bf16, false>(x, s, N, w, b, y, ws, st);
+}
+
+namespace dit {
+
+int gn_tile_stats_finalize(const void* stats, int64_t N, int64_t groups, int64_t n_tiles, hipStream_t st) {
+    hipLaunchKernelGGL(gn_tile_stats_finalize_kernel, dim3((unsigned)(N * groups)), dim3(kBlock), 0, st,
+                       (const float4*)((const char*)stats + gn_tile_stats_head_bytes(N, groups)), (int)n_tiles,
+                       (double2*)stats);
+    return check_launch("dt_conv2d_gn(stats)");
+}
+
+}  // namespace dit
+
+extern "C" int dt_groupnorm_silu_from_stats(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups,
+                                            const void* stats, const float* w, const float* b, float eps,
+                                            int32_t apply_silu, void* y, int32_t io_type, dt_stream_t stream) {
+    DT_REQUIRE(dit::is_io_type(io_type), "dt_groupnorm_silu_from_stats: io_type %d unsupported", io_type);
+    DT_REQUIRE(N > 0 && C > 0 && HW > 0 && groups > 0 && C % groups == 0,
+               "dt_groupnorm_silu_from_stats: bad shape");
+    DT_REQUIRE(x && y && stats, "dt_groupnorm_silu_from_stats: null pointer");
+    DT_REQUIRE(((uintptr_t)stats & 15) == 0, "dt_groupnorm_silu_from_stats: stats must be 16-byte aligned");
+    DT_REQUIRE(N * groups < 65536, "dt_groupnorm_silu_from_stats: N*groups must be < 65536");
+    const bool vec = gn_vec_ok(HW, io_type) && dit::aligned16(x) && dit::aligned16(y);
+    const int epv = vec ? (io_type == DT_TYPE_BF16 ? 8 : 4) : 1;
+    dit::GnShape s;
+    s.C = C;
+    s.HW = HW;
+    s.cg = C / groups;
+    s.group_len = s.cg * HW;
+    s.group_vecs = s.group_len / epv;
+    s.G = (int)groups;
+    s.nchunks = (int)dit::chunks_for(s.group_vecs);
+    s.eps = eps;
+    s.apply_silu = apply_silu ? 1 : 0;
+    DT_REQUIRE(s.group_vecs < (1ll << 31), "dt_groupnorm_silu_from_stats: group too large");
+    const dim3 grid((unsigned)s.nchunks, (unsigned)(N * s.G));
+    const dit::FastDiv hv = dit::make_fastdiv((uint32_t)(s.HW / epv));
+    hipStream_t st = (hipStream_t)stream;
+    const double2* mv = (const double2*)stats;
+    using dit::bf16;
+    if (io_type == DT_TYPE_F32) {
+        if (vec) hipLaunchKernelGGL((dit::gn_apply_stats_kernel<float, true>), grid, dim3(dit::kBlock), 0, st,
+                                    (const float*)x, s, mv, w, b, (float*)y, hv);
+        else hipLaunchKernelGGL((dit::gn_apply_stats_kernel<float, false>), grid, dim3(dit::kBlock), 0, st,
+                                (const float*)x, s, mv, w, b, (float*)y, hv);
+    } else {
+        if (vec) hipLaunchKernelGGL((dit::gn_apply_stats_kernel<bf16, true>), grid, dim3(dit::kBlock), 0, st,
+                                    (const bf16*)x, s, mv, w, b, (bf16*)y, hv);
+        else hipLaunchKernelGGL((dit::gn_apply_stats_kernel<bf16, false>), grid, dim3(dit::kBlock), 0, st,
+                                (const bf16*)x, s, mv, w, b, (bf16*)y, hv);
+    }
+    return dit::check_launch("dt_groupnorm_silu_from_stats");
 }

@@ -46,6 +46,13 @@ int qk_swiglu_launch(const void* q, const void* k, void* q_out, void* k_out, con
                      const float* table, int n_pos, const void* g, int64_t gs, const void* u, int64_t us, void* y,
                      int64_t ys, int64_t rows, int64_t cols, int32_t io, hipStream_t st);
 
+// GroupNorm statistics written by the conv epilogue (dt_conv2d_gn): a head
+// of N * G (mean, variance) double2, padded to 256 bytes, then the per-tile
+// (mean, M2, count, 0) float4 records [N][G][pixel tiles].  The finalize step
+// (groupnorm.hip) merges the records into the head.
+inline int64_t gn_tile_stats_head_bytes(int64_t N, int64_t G) { return (N * G * 16 + 255) / 256 * 256; }
+int gn_tile_stats_finalize(const void* stats, int64_t N, int64_t groups, int64_t n_tiles, hipStream_t st);
+
 // Backend accessors (capi.cpp).
 hipStream_t backend_stream(dt_backend* be);
 int backend_device(dt_backend* be);

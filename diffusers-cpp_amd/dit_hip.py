@@ -97,6 +97,11 @@ _SIGS = {
     "dt_conv2d_pack_weights": (c_int32, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, _S]),
     "dt_conv2d": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32,
                             c_void_p, c_void_p, c_int32, _S]),
+    "dt_conv2d_gn_stats_bytes": (ctypes.c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "dt_conv2d_gn": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32,
+                               c_void_p, c_void_p, c_int64, c_void_p, ctypes.c_size_t, c_int32, _S]),
+    "dt_groupnorm_silu_from_stats": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                               c_void_p, c_float, c_int32, c_void_p, c_int32, _S]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
     "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
@@ -487,6 +492,33 @@ def conv2d(x, w, bias=None, upscale2=False, out=None):
     y = torch.empty((N, w.co, Hs, Ws), dtype=x.dtype, device=x.device) if out is None else out
     check(load().dt_conv2d(_p(x), N, ci, H, W, _p(w.packed), w.co, w.k, 1 if upscale2 else 0, _p(bias), _p(y),
                            io_type(x), stream()), "dt_conv2d")
+    return y
+
+
+def conv2d_gn(x, w, groups, bias=None, upscale2=False, out=None):
+    """dt_conv2d + GroupNorm statistics of the output -> (y, stats); stats[:N*groups*16]
+    viewed as float64 pairs holds (mean, variance) per (n, g)."""
+    torch = _torch()
+    N, ci, H, W = x.shape
+    assert ci == w.ci and x.is_contiguous()
+    Hs, Ws = (2 * H, 2 * W) if upscale2 else (H, W)
+    y = torch.empty((N, w.co, Hs, Ws), dtype=x.dtype, device=x.device) if out is None else out
+    nb = load().dt_conv2d_gn_stats_bytes(N, w.co, Hs, Ws, groups)
+    assert nb > 0, "unsupported conv/GroupNorm shape"
+    stats = torch.empty(nb, dtype=torch.uint8, device=x.device)
+    check(load().dt_conv2d_gn(_p(x), N, ci, H, W, _p(w.packed), w.co, w.k, 1 if upscale2 else 0, _p(bias), _p(y),
+                              groups, _p(stats), nb, io_type(x), stream()), "dt_conv2d_gn")
+    return y, stats
+
+
+def groupnorm_silu_from_stats(x, stats, groups, w=None, b=None, eps=1e-6, silu=True, out=None):
+    torch = _torch()
+    N, C = x.shape[0], x.shape[1]
+    HW = x.numel() // (N * C)
+    y = torch.empty_like(x) if out is None else out
+    check(load().dt_groupnorm_silu_from_stats(_p(x), N, C, HW, groups, _p(stats), _p(w), _p(b), eps,
+                                              1 if silu else 0, _p(y), io_type(x), stream()),
+          "dt_groupnorm_silu_from_stats")
     return y
 
 

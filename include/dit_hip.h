@@ -231,6 +231,26 @@ int dt_conv2d(const void *x, int64_t N, int64_t Ci, int64_t H, int64_t W, const 
               int64_t Co, int64_t K, int32_t upscale2, const float *bias, void *y, int32_t io_type,
               dt_stream_t stream);
 
+/* dt_conv2d whose epilogue also reduces GroupNorm(groups) statistics of the
+ * output it stores: per output tile and group a (mean, M2, count) record,
+ * merged at the end into a head of N * groups (mean, variance) double pairs
+ * at the start of `stats` (dt_conv2d_gn_stats_bytes; 16-byte aligned).  The
+ * GroupNorm + SiLU that follows (ResnetBlock2D.inl:111-122, 160-171;
+ * Decoder.hpp:147-160) is then one read and one write of the tensor,
+ * dt_groupnorm_silu_from_stats, instead of dt_groupnorm_silu's statistics
+ * pass plus apply pass.  Co / groups must divide 128.  The statistics are
+ * merged in a fixed order (Chan's pairwise update, fp64): deterministic. */
+size_t dt_conv2d_gn_stats_bytes(int64_t N, int64_t Co, int64_t OH, int64_t OW, int64_t groups);
+int dt_conv2d_gn(const void *x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void *packed_w,
+                 int64_t Co, int64_t K, int32_t upscale2, const float *bias, void *y, int64_t groups,
+                 void *stats, size_t stats_bytes, int32_t io_type, dt_stream_t stream);
+/* GroupNorm(groups) + affine + optional SiLU of x with the statistics
+ * dt_conv2d_gn wrote for it: y = silu(((x - mean) * rstd) * w_c + b_c),
+ * rstd = 1 / sqrt(var + eps), as dt_groupnorm_silu applies them. */
+int dt_groupnorm_silu_from_stats(const void *x, int64_t N, int64_t C, int64_t HW, int64_t groups,
+                                 const void *stats, const float *w, const float *b, float eps,
+                                 int32_t apply_silu, void *y, int32_t io_type, dt_stream_t stream);
+
 /* Synthetic N(mean, std^2) fp32 data on the device (benchmark weights and
  * inputs; a seeded splitmix64 + Box-Muller stream).  No counterpart in the
  * reference, which reads weights from GGUF files. */

@@ -72,3 +72,58 @@ def test_conv2d_rejects(dev):
     wp.k = 5
     with pytest.raises(RuntimeError, match="kernel size 5 unsupported"):
         dit_hip.conv2d(x, wp)
+
+
+# ---------------------------------------------- conv + GroupNorm statistics --
+# (N, Ci, H, W), Co, K, upscale2, groups: the decoder's group sizes (16, 8, 4
+# channels per group at 512, 256, 128 channels), a partial output-channel tile,
+# partial pixel tiles, the upscale, 1x1, and one group per channel.
+GN_CASES = [((1, 64, 12, 40), 512, 3, False, 32), ((2, 32, 9, 70), 256, 3, False, 32),
+            ((1, 48, 16, 16), 128, 3, True, 32), ((1, 40, 7, 150), 192, 1, False, 48),
+            ((1, 16, 5, 6), 64, 3, False, 64), ((1, 128, 64, 64), 128, 3, False, 32)]
+
+
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,co,k,up2,groups", GN_CASES)
+def test_conv2d_gn_statistics_and_apply(orc, dev, shape, co, k, up2, groups, io):
+    """dt_conv2d_gn stores the same output as dt_conv2d and the (mean,
+    variance) of each group of that stored output; dt_groupnorm_silu_from_stats
+    then matches the oracle's GroupNorm+SiLU of the stored output (the fp32 /
+    bf16 bar of one fused kernel) and the two-pass dt_groupnorm_silu on it."""
+    print(f"conv2d_gn x={shape} co={co} k={k} up2={up2} groups={groups} {io}", flush=True)
+    x = orc.randn(SEED + 310, shape)
+    w = orc.randn(SEED + 311, (co, shape[1], k, k), std=0.05)
+    b = orc.randn(SEED + 312, (co,), std=0.5)
+    gw = orc.randn(SEED + 313, (co,), mean=1.0, std=0.1)
+    gb = orc.randn(SEED + 314, (co,), std=0.1)
+    wp = dit_hip.conv2d_pack(dev_tensor(w, torch.float32))
+    xd, bd = dev_tensor(x, io), dev_tensor(b, torch.float32)
+    y, stats = dit_hip.conv2d_gn(xd, wp, groups, bias=bd, upscale2=up2)
+    y_plain = dit_hip.conv2d(xd, wp, bias=bd, upscale2=up2)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_plain), "the statistics epilogue changed the stored output"
+    yh = host(y).astype(np.float64)
+    N = shape[0]
+    mv = stats[: N * groups * 16].cpu().numpy().view(np.float64).reshape(N, groups, 2)
+    grp = yh.reshape(N, groups, -1)
+    assert np.allclose(mv[..., 0], grp.mean(axis=2), rtol=1e-6, atol=1e-6), "group means"
+    assert np.allclose(mv[..., 1], grp.var(axis=2), rtol=1e-5, atol=1e-7), "group variances"
+    gwd, gbd = dev_tensor(gw, torch.float32), dev_tensor(gb, torch.float32)
+    out = dit_hip.groupnorm_silu_from_stats(y, stats, groups, gwd, gbd, eps=1e-6)
+    torch.cuda.synchronize()
+    ref = orc.groupnorm_silu(host(y), groups, gw, gb, eps=1e-6)
+    check(host(out), ref, io, "GroupNorm+SiLU from conv statistics")
+    ws = torch.empty(dit_hip.load().dt_groupnorm_workspace_bytes(N, co, yh[0, 0].size, groups), dtype=torch.uint8,
+                     device="cuda")
+    two_pass = dit_hip.groupnorm_silu(y, groups, gwd, gbd, eps=1e-6, workspace=ws)
+    torch.cuda.synchronize()
+    check(host(out), host(two_pass), io, "against the two-pass GroupNorm", one_rounding=False)
+
+
+def test_conv2d_gn_rejects_groups_not_dividing_the_tile(dev):
+    x = torch.zeros((1, 8, 8, 8), dtype=torch.float32, device="cuda")
+    wp = dit_hip.conv2d_pack(torch.zeros((96, 8, 3, 3), dtype=torch.float32, device="cuda"))
+    with pytest.raises(AssertionError):
+        dit_hip.conv2d_gn(x, wp, 5)  # 96 % 5 != 0: no stats layout
+    with pytest.raises(RuntimeError, match="must divide 128"):
+        dit_hip.conv2d_gn(x, wp, 2)  # 48 channels per group
