@@ -83,7 +83,7 @@ __device__ __forceinline__ void conv_group_stats(const ConvArgs& a, const f32x16
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int p = wpx + 32 * i + lrow;
-        const bool valid = p / a.TC < rows_valid && p % a.TC < cols_valid;
+        const bool valid = (p >> __builtin_ctz(a.TC)) < rows_valid && (p & (a.TC - 1)) < cols_valid;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -101,7 +101,15 @@ __device__ __forceinline__ void conv_group_stats(const ConvArgs& a, const f32x16
     const float* gv = tb + gi * a.cg * kTilePx;  // the group's rows are contiguous
     const int n_el = a.cg * kTilePx;
     const int vp = rows_valid * cols_valid;
+    const bool full = vp == kTilePx;
+    const int lt = __builtin_ctz(a.TC);  // TC is a power of two
+    // Sum over the tpg threads of a group: xor shuffles when the group lies in
+    // one wave (tpg <= 64, every decoder shape), else through LDS.
     auto seg_sum = [&](float v) {
+        if (tpg <= kWave) {
+            for (int o = tpg / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+            return v;
+        }
         red[tid] = v;
         __syncthreads();
         for (int h = tpg / 2; h > 0; h >>= 1) {
@@ -116,11 +124,18 @@ __device__ __forceinline__ void conv_group_stats(const ConvArgs& a, const f32x16
     for (int e = ti; e < n_el; e += tpg) s1 += gv[e];  // invalid pixels hold 0
     const float mean = seg_sum(s1) / (float)(a.cg * vp);
     float s2 = 0.f;
-    for (int e = ti; e < n_el; e += tpg) {
-        const int p = e & (kTilePx - 1);
-        if (p / a.TC < rows_valid && p % a.TC < cols_valid) {
+    if (full) {
+        for (int e = ti; e < n_el; e += tpg) {
             const float d = gv[e] - mean;
             s2 += d * d;
+        }
+    } else {
+        for (int e = ti; e < n_el; e += tpg) {
+            const int p = e & (kTilePx - 1);
+            if ((p >> lt) < rows_valid && (p & (a.TC - 1)) < cols_valid) {
+                const float d = gv[e] - mean;
+                s2 += d * d;
+            }
         }
     }
     const float m2 = seg_sum(s2);
@@ -128,6 +143,103 @@ __device__ __forceinline__ void conv_group_stats(const ConvArgs& a, const f32x16
     if (ti == 0 && grp < a.G)
         a.stats[((int64_t)blockIdx.z * a.G + grp) * gridDim.x + blockIdx.x] =
             make_float4(mean, m2, (float)(a.cg * vp), 0.f);
+}
+
+// The same statistics straight from the accumulators, for CG = 4 .. 64
+// channels per group (the decoder's 4, 8 and 16): each lane sums the rows of
+// its FN pixels that share a group ("slots": the lane's 32 rows are
+// 32 j + 8 q + 4 g + t of its wave's 64), xor-shuffles the slot sums across
+// the 32 (CG = 4) or 64 lanes holding the group, and the two waves covering
+// the tile's two pixel halves (wave and wave ^ 1) add theirs through LDS; then the same for
+// M2 around the group mean.  Two barriers, no LDS tile.
+template <typename T, int CG, int FN = 2>
+__device__ __forceinline__ void conv_group_stats_reg(const ConvArgs& a, const f32x16_t (&acc)[2][FN], float* red,
+                                                     int co0, int oh0, int ow0, int wco, int wpx, int lrow, int g,
+                                                     int wave) {
+    constexpr int S = CG <= 8 ? 8 : CG == 16 ? 4 : CG == 32 ? 2 : 1;  // slots per lane
+    constexpr int WIDTH = CG == 4 ? 32 : 64;                            // lanes holding one slot's group
+    const int rows_valid = min(a.TR, a.Hs - oh0), cols_valid = min(a.TC, a.Ws - ow0);
+    const int lt = __builtin_ctz(a.TC);
+    bool valid[FN];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+        const int p = wpx + 32 * i + lrow;
+        valid[i] = (p >> lt) < rows_valid && (p & (a.TC - 1)) < cols_valid;
+    }
+    // The stored values (bias added, rounded to T).
+    float v[2][FN][16];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co0 + wco + 32 * j + 8 * (r >> 2) + 4 * g + (r & 3);
+            const float bv = a.bias && co < a.Co ? a.bias[co] : 0.f;
+#pragma unroll
+            for (int i = 0; i < FN; ++i) {
+                float t = acc[j][i][r];
+                if (a.bias) t = add_rn(t, bv);
+                v[j][i][r] = stored_value<T>(t);
+            }
+        }
+    auto slot_of = [](int j, int q) { return CG <= 8 ? 4 * j + q : CG == 16 ? 2 * j + (q >> 1) : CG == 32 ? j : 0; };
+    auto entry = [&](int s) { return CG == 4 ? 2 * s + g : s; };  // LDS entry of slot s
+    const int vp = rows_valid * cols_valid;
+    // Pass 1: sums.
+    float part[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) part[s] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+                if (valid[i]) part[slot_of(j, r >> 2)] += v[j][i][r];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int o = WIDTH / 2; o > 0; o >>= 1) part[s] += __shfl_xor(part[s], o, kWave);
+    if (lrow == 0 && (CG == 4 || g == 0))
+#pragma unroll
+        for (int s = 0; s < S; ++s) red[wave * 16 + entry(s)] = part[s];
+    __syncthreads();
+    float mean[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        mean[s] = (red[wave * 16 + entry(s)] + red[(wave ^ 1) * 16 + entry(s)]) / (float)(CG * vp);
+    __syncthreads();
+    // Pass 2: M2 around the group mean.
+#pragma unroll
+    for (int s = 0; s < S; ++s) part[s] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+                if (valid[i]) {
+                    const float d = v[j][i][r] - mean[slot_of(j, r >> 2)];
+                    part[slot_of(j, r >> 2)] += d * d;
+                }
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int o = WIDTH / 2; o > 0; o >>= 1) part[s] += __shfl_xor(part[s], o, kWave);
+    if (lrow == 0 && (CG == 4 || g == 0))
+#pragma unroll
+        for (int s = 0; s < S; ++s) red[wave * 16 + entry(s)] = part[s];
+    __syncthreads();
+    if ((wave & 1) == 0 && lrow == 0 && (CG == 4 || g == 0)) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const float m2 = red[wave * 16 + entry(s)] + red[(wave ^ 1) * 16 + entry(s)];
+            // the slot's group: its first row wco + (32 j + 8 q + 4 g) / CG * CG
+            const int grp = co0 / CG + wco / CG + (CG == 4 ? 2 * s + g : s);
+            if (grp < a.G)
+                a.stats[((int64_t)blockIdx.z * a.G + grp) * gridDim.x + blockIdx.x] =
+                    make_float4(mean[s], m2, (float)(CG * vp), 0.f);
+        }
+    }
 }
 
 template <typename T, int K, bool STATS>
@@ -244,7 +356,224 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
             }
         }
     }
-    if constexpr (STATS) conv_group_stats<T>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g);
+    if constexpr (STATS) {
+        float* red = reinterpret_cast<float*>(smem);  // free after the main loop's last barrier
+        switch (a.cg) {
+            case 4: conv_group_stats_reg<T, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 8: conv_group_stats_reg<T, 8>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 16: conv_group_stats_reg<T, 16>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 32: conv_group_stats_reg<T, 32>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 64: conv_group_stats_reg<T, 64>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            default: conv_group_stats<T>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g); break;
+        }
+    }
+}
+
+// ---- with a workspace (3x3): channel-last input, direct global -> LDS DMA ---
+// Measured on gfx950 (bf16, 3x3, Co = Ci): [1,512,128,128] 463, [1,512,256,256]
+// 474, [1,256,512,512] 385, [1,128,1024,1024] 288 TFLOP/s, and 610 on the
+// 2x upscale of [1,512,128,128]; the register-staged kernel 99-125.
+// The input is first transposed to bf16 NHWC with channels zero-padded to a
+// multiple of 16 (to_nhwc16_kernel, one bandwidth-bound pass), so a 16-channel
+// slice of one pixel is a contiguous 32-byte record and both operands stream
+// into LDS by global_load_lds with no per-element work: the input patch of a
+// 256-pixel tile (every lane computes its own source pixel, which also
+// applies the nearest 2x upscale and sends out-of-image taps to a zeroed
+// 256-byte tail of the workspace) and the [128 co][K*K] weight records.  Two
+// LDS stages of 16 channels, filled one chunk ahead; four waves of
+// 64 co x 128 px (2 x 4 MFMA 32x32x16 per tap).  Each 32-byte record's two
+// 16-byte units are swapped by the DMA source for records whose bit 2 of the
+// index (pixels) or of co (weights) is set, so 8 consecutive records read
+// distinct banks.
+constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
+constexpr int kXLanesMax3 = 7 * 256, kXLanesMax1 = 2 * 256;  // DMA lanes per X stage (3x3, 1x1)
+
+template <typename TI>
+__global__ __launch_bounds__(256) void to_nhwc16_kernel(const TI* __restrict__ x, int C, int H, int W, int C16,
+                                                        uint16_t* __restrict__ out, int64_t tail_offset) {
+    // block: (w tile of 64, h, n); 16 channels at a time through LDS.
+    __shared__ float t[16][65];
+    const int w0 = blockIdx.x * 64, h = blockIdx.y, n = blockIdx.z;
+    const TI* xn = x + (int64_t)n * C * H * W;
+    uint16_t* on = out + (((int64_t)n * H + h) * W) * C16;
+    for (int c0 = 0; c0 < C16; c0 += 16) {
+        for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+            const int c = i >> 6, w = i & 63;
+            float v = 0.f;
+            if (c0 + c < C && w0 + w < W) v = load_in<TI>(xn + ((int64_t)(c0 + c) * H + h) * W + w0 + w);
+            t[c][w] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < 128) {
+            const int w = threadIdx.x >> 1, half = threadIdx.x & 1;
+            if (w0 + w < W) {
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = t[half * 8 + e][w];
+                *reinterpret_cast<uint4*>(on + (int64_t)(w0 + w) * C16 + c0 + half * 8) =
+                    make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                               pack_bf16x2(v[6], v[7]));
+            }
+        }
+        __syncthreads();
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 16)
+        reinterpret_cast<uint4*>(out + tail_offset)[threadIdx.x] = make_uint4(0, 0, 0, 0);
+}
+
+struct Conv2Extra {
+    const uint16_t* xh;  // NHWC bf16 [N][H][W][C16]
+    const uint16_t* zero;  // 256 zero bytes
+    int C16, Cp32;       // channels of xh; Ci_pad of the packed weights
+    int lt;              // log2(TC)
+};
+
+__device__ __forceinline__ void dma16(const void* src, void* lds) { __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0); }
+
+template <int N_OUT>
+__device__ __forceinline__ void conv_wait_vm() {
+    // s_waitcnt vmcnt(N_OUT) with expcnt / lgkmcnt left at their maxima.
+    __builtin_amdgcn_s_waitcnt((N_OUT & 15) | ((N_OUT >> 4) << 14) | 0x0F70);
+}
+
+template <typename T, int K, bool STATS>
+__global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const Conv2Extra e) {
+    constexpr int KK = K * K, PAD = (K - 1) / 2;
+    constexpr int XL = K == 3 ? kXLanesMax3 : kXLanesMax1;  // X DMA lanes per stage
+    constexpr int NX = XL / 256, NW = 2 * kTileCo * KK / 256;  // DMA instructions per wave per stage
+    constexpr int XB = XL * 16, WB = kTileCo * KK * kRec2, STAGE = XB + WB;
+    constexpr int QD = NX + NW;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = blockIdx.z, co0 = blockIdx.y * kTileCo;
+    const int th = blockIdx.x / a.tiles_w, tw = blockIdx.x - th * a.tiles_w;
+    const int oh0 = th * a.TR, ow0 = tw * a.TC;
+    const int PC = a.TC + K - 1, npatch = (a.TR + K - 1) * PC;
+    const int wco = (wave >> 1) * 64, wpx = (wave & 1) * 128;
+    const int lrow = lane & 31, g = lane >> 5;
+
+    // DMA sources, fixed for the whole K loop up to the channel offset.
+    const uint16_t* xsrc[NX];
+    int xstep[NX];  // 1 for an in-image record (advances with the channel chunk), 0 for the zero tail
+#pragma unroll
+    for (int m = 0; m < NX; ++m) {
+        const int L = (m * 4 + wave) * 64 + lane, rec = L >> 1, u = L & 1;
+        const uint16_t* src = e.zero;
+        xstep[m] = 0;
+        if (rec < npatch) {
+            const int pr = rec / PC, pc = rec - pr * PC;
+            const int ih = oh0 + pr - PAD, iw = ow0 + pc - PAD;
+            if (ih >= 0 && ih < a.Hs && iw >= 0 && iw < a.Ws) {
+                const int sh = a.up2 ? ih >> 1 : ih, sw = a.up2 ? iw >> 1 : iw;
+                const int su = u ^ ((rec >> 2) & 1);
+                src = e.xh + (((int64_t)n * a.H + sh) * a.W + sw) * e.C16 + su * 8;
+                xstep[m] = 1;
+            }
+        }
+        xsrc[m] = src;
+    }
+    const uint16_t* wsrc[NW];
+#pragma unroll
+    for (int m = 0; m < NW; ++m) {
+        const int L = (m * 4 + wave) * 64 + lane, rec = L >> 1, u = L & 1;
+        const int co = rec / KK, tap = rec - co * KK;
+        const int su = u ^ ((co >> 2) & 1);
+        wsrc[m] = a.w + ((int64_t)(co0 + co) * KK + tap) * e.Cp32 + su * 8;
+    }
+    auto issue = [&](int c0, int s) {
+        uint8_t* st = smem + s * STAGE;
+#pragma unroll
+        for (int m = 0; m < NX; ++m)  // out-of-image taps read the zero tail at every chunk
+            dma16(xsrc[m] + xstep[m] * c0, st + (m * 4 + wave) * 64 * 16);
+#pragma unroll
+        for (int m = 0; m < NW; ++m) dma16(wsrc[m] + c0, st + XB + (m * 4 + wave) * 64 * 16);
+    };
+
+    f32x16_t acc[2][4];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[j][i][q] = 0.f;
+
+    int pbase[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = wpx + 32 * i + lrow;
+        pbase[i] = (p >> e.lt) * PC + (p & (a.TC - 1));
+    }
+    int wrec[2], wsw[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int co = wco + 32 * j + lrow;
+        wrec[j] = co * KK;
+        wsw[j] = (g ^ ((co >> 2) & 1)) << 4;
+    }
+
+    const int nch = e.C16 / kCi2;
+    issue(0, 0);
+    if (nch > 1) issue(kCi2, 1);
+    for (int ch = 0; ch < nch; ++ch) {
+        if (ch + 1 < nch) conv_wait_vm<QD>();
+        else conv_wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        const uint8_t* Xs = smem + (ch & 1) * STAGE;
+        const uint8_t* Ws_ = Xs + XB;
+#pragma unroll
+        for (int tap = 0; tap < KK; ++tap) {
+            const int kh = tap / K, kw = tap - kh * K;
+            bf16x8_t wf[2], xf[4];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                wf[j] = *reinterpret_cast<const bf16x8_t*>(Ws_ + (wrec[j] + tap) * kRec2 + wsw[j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rec = pbase[i] + kh * PC + kw;
+                xf[i] = *reinterpret_cast<const bf16x8_t*>(Xs + rec * kRec2 + ((g ^ ((rec >> 2) & 1)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+        }
+        // every wave's reads of this stage are done before it is refilled
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (ch + 2 < nch) issue((ch + 2) * kCi2, ch & 1);
+    }
+
+    T* y = reinterpret_cast<T*>(a.y) + (int64_t)n * a.Co * a.Hs * a.Ws;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int p = wpx + 32 * i + lrow;
+        const int oh = oh0 + (p >> e.lt), ow = ow0 + (p & (a.TC - 1));
+        if (oh >= a.Hs || ow >= a.Ws) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int co = co0 + wco + 32 * j + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (co >= a.Co) continue;
+                float v = acc[j][i][r];
+                if (a.bias) v = add_rn(v, a.bias[co]);
+                Io<T>::put(y + ((int64_t)co * a.Hs + oh) * a.Ws + ow, v);
+            }
+        }
+    }
+    if constexpr (STATS) {
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(smem);
+        switch (a.cg) {
+            case 4: conv_group_stats_reg<T, 4, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 8: conv_group_stats_reg<T, 8, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 16: conv_group_stats_reg<T, 16, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            case 32: conv_group_stats_reg<T, 32, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+            default: conv_group_stats_reg<T, 64, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
+        }
+    }
 }
 
 // Repack [Co][Ci][K][K] (fp32 or bf16) to bf16 [Co_pad][K*K][Ci_pad], zeros
@@ -304,9 +633,23 @@ void conv_geometry(int64_t Hs, int64_t Ws, int* TR, int* TC, int64_t* tiles_w, i
     *tiles_h = (Hs + *TR - 1) / *TR;
 }
 
+int64_t nhwc_elems(int64_t N, int64_t Ci, int64_t H, int64_t W) { return N * H * W * pad_to(Ci, kCi2); }
+
+// Tile geometry of the DMA kernel: 256-pixel tiles, TC = 256 .. 16 columns.
+void conv_geometry2(int64_t Hs, int64_t Ws, int* TR, int* TC, int64_t* tiles_w, int64_t* tiles_h) {
+    *TC = Ws >= 256 ? 256 : Ws >= 128 ? 128 : Ws >= 64 ? 64 : Ws >= 32 ? 32 : 16;
+    *TR = kTilePx2 / *TC;
+    *tiles_w = (Ws + *TC - 1) / *TC;
+    *tiles_h = (Hs + *TR - 1) / *TR;
+}
+
+// Launches the conv; with a workspace of dt_conv2d_workspace_bytes (and, for
+// statistics, 4..64 channels per group) the transpose + DMA kernel, else the
+// register-staged one.  *n_tiles: the pixel tiles of the launch.
 int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
                 int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type, float4* stats,
-                int64_t groups, hipStream_t st, const char* what) {
+                int64_t groups, const void* ws, size_t ws_bytes, hipStream_t st, const char* what,
+                int64_t* n_tiles) {
     DT_REQUIRE(is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
     DT_REQUIRE(N > 0 && Ci > 0 && H > 0 && W > 0 && Co > 0, "%s: bad shape", what);
     DT_REQUIRE(K == 1 || K == 3, "%s: kernel size %lld unsupported (1 or 3)", what, (long long)K);
@@ -326,14 +669,49 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
     a.Hs = (int)Hs; a.Ws = (int)Ws;
     a.Ci_pad = (int)pad_to(Ci, kCi);
     a.KK = (int)(K * K);
-    int64_t tiles_w, tiles_h;
-    conv_geometry(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
-    a.tiles_w = (int)tiles_w;
     a.stats = stats;
     a.G = (int)groups;
     a.cg = groups > 0 ? (int)(Co / groups) : 0;
+    // 1x1 convs keep the staged path: the channel-last copy costs more than
+    // their single tap (gfx950, [1, 256, 512, 512] -> 128: 260-312 us with
+    // the copy against 135-225 us staged).
+    const bool dma = K == 3 && ws && ws_bytes >= (size_t)(nhwc_elems(N, Ci, H, W) * 2 + 256) && aligned16(ws) &&
+                     (!stats || (a.cg >= 4 && a.cg <= 64));
+    int64_t tiles_w, tiles_h;
+    if (dma) conv_geometry2(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
+    else conv_geometry(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
+    a.tiles_w = (int)tiles_w;
     DT_REQUIRE(tiles_h * tiles_w < (1ll << 31), "%s: too many tiles", what);
+    *n_tiles = tiles_h * tiles_w;
     const dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)((Co + kTileCo - 1) / kTileCo), (unsigned)N);
+    if (dma) {
+        Conv2Extra e{};
+        const int64_t elems = nhwc_elems(N, Ci, H, W);
+        e.xh = (const uint16_t*)ws;
+        e.zero = (const uint16_t*)ws + elems;
+        e.C16 = (int)pad_to(Ci, kCi2);
+        e.Cp32 = a.Ci_pad;
+        e.lt = __builtin_ctz((unsigned)a.TC);
+        const dim3 tg((unsigned)((W + 63) / 64), (unsigned)H, (unsigned)N);
+        if (io_type == DT_TYPE_F32)
+            hipLaunchKernelGGL((to_nhwc16_kernel<float>), tg, dim3(256), 0, st, (const float*)x, (int)Ci, (int)H,
+                               (int)W, e.C16, (uint16_t*)ws, elems);
+        else
+            hipLaunchKernelGGL((to_nhwc16_kernel<bf16>), tg, dim3(256), 0, st, (const bf16*)x, (int)Ci, (int)H,
+                               (int)W, e.C16, (uint16_t*)ws, elems);
+        int rc = check_launch(what);
+        if (rc) return rc;
+#define DT_CONV2_LAUNCH(TT, KS, ST) hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST>), grid, dim3(256), 0, st, a, e)
+        if (io_type == DT_TYPE_F32) {
+            if (K == 3) { if (stats) DT_CONV2_LAUNCH(float, 3, true); else DT_CONV2_LAUNCH(float, 3, false); }
+            else { if (stats) DT_CONV2_LAUNCH(float, 1, true); else DT_CONV2_LAUNCH(float, 1, false); }
+        } else {
+            if (K == 3) { if (stats) DT_CONV2_LAUNCH(bf16, 3, true); else DT_CONV2_LAUNCH(bf16, 3, false); }
+            else { if (stats) DT_CONV2_LAUNCH(bf16, 1, true); else DT_CONV2_LAUNCH(bf16, 1, false); }
+        }
+#undef DT_CONV2_LAUNCH
+        return check_launch(what);
+    }
 #define DT_CONV_LAUNCH(TT, KS, ST) hipLaunchKernelGGL((conv2d_kernel<TT, KS, ST>), grid, dim3(256), 0, st, a)
     if (io_type == DT_TYPE_F32) {
         if (K == 3) { if (stats) DT_CONV_LAUNCH(float, 3, true); else DT_CONV_LAUNCH(float, 3, false); }
@@ -349,24 +727,31 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
 }  // namespace
 }  // namespace dit
 
+extern "C" size_t dt_conv2d_workspace_bytes(int64_t N, int64_t Ci, int64_t H, int64_t W) {
+    if (N <= 0 || Ci <= 0 || H <= 0 || W <= 0) return 0;
+    return (size_t)(dit::nhwc_elems(N, Ci, H, W) * 2 + 256);
+}
+
 extern "C" int dt_conv2d(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w,
-                         int64_t Co, int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type,
-                         dt_stream_t stream) {
-    return dit::conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, nullptr, 0,
-                            (hipStream_t)stream, "dt_conv2d");
+                         int64_t Co, int64_t K, int32_t upscale2, const float* bias, void* y, void* workspace,
+                         size_t workspace_bytes, int32_t io_type, dt_stream_t stream) {
+    int64_t tiles;
+    return dit::conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, nullptr, 0, workspace,
+                            workspace_bytes, (hipStream_t)stream, "dt_conv2d", &tiles);
 }
 
 extern "C" size_t dt_conv2d_gn_stats_bytes(int64_t N, int64_t Co, int64_t OH, int64_t OW, int64_t groups) {
     if (N <= 0 || Co <= 0 || OH <= 0 || OW <= 0 || groups <= 0 || Co % groups) return 0;
     int tr, tc;
     int64_t tw, th;
-    dit::conv_geometry(OH, OW, &tr, &tc, &tw, &th);
+    dit::conv_geometry(OH, OW, &tr, &tc, &tw, &th);  // the finer tiling: enough records for either kernel
     return (size_t)(dit::gn_tile_stats_head_bytes(N, groups) + N * groups * th * tw * 16);
 }
 
 extern "C" int dt_conv2d_gn(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w,
                             int64_t Co, int64_t K, int32_t upscale2, const float* bias, void* y, int64_t groups,
-                            void* stats, size_t stats_bytes, int32_t io_type, dt_stream_t stream) {
+                            void* stats, size_t stats_bytes, void* workspace, size_t workspace_bytes,
+                            int32_t io_type, dt_stream_t stream) {
     using namespace dit;
     DT_REQUIRE(groups > 0 && Co % groups == 0, "dt_conv2d_gn: Co %lld not a multiple of groups %lld",
                (long long)Co, (long long)groups);
@@ -381,11 +766,9 @@ extern "C" int dt_conv2d_gn(const void* x, int64_t N, int64_t Ci, int64_t H, int
     DT_REQUIRE(N * groups < 65536, "dt_conv2d_gn: N*groups must be < 65536");
     hipStream_t st = (hipStream_t)stream;
     float4* recs = (float4*)((char*)stats + gn_tile_stats_head_bytes(N, groups));
-    int rc = conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, recs, groups, st,
-                         "dt_conv2d_gn");
+    int64_t tiles;
+    int rc = conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, recs, groups, workspace,
+                         workspace_bytes, st, "dt_conv2d_gn", &tiles);
     if (rc) return rc;
-    int tr, tc;
-    int64_t tw, th;
-    conv_geometry(Hs, Ws, &tr, &tc, &tw, &th);
-    return gn_tile_stats_finalize(stats, N, groups, th * tw, st);
+    return gn_tile_stats_finalize(stats, N, groups, tiles, st);
 }

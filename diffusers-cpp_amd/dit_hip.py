@@ -95,11 +95,13 @@ _SIGS = {
                                 c_int64, _S]),
     "dt_conv2d_packed_bytes": (ctypes.c_size_t, [c_int64, c_int64, c_int64]),
     "dt_conv2d_pack_weights": (c_int32, [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, _S]),
+    "dt_conv2d_workspace_bytes": (ctypes.c_size_t, [c_int64, c_int64, c_int64, c_int64]),
     "dt_conv2d": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32,
-                            c_void_p, c_void_p, c_int32, _S]),
+                            c_void_p, c_void_p, c_void_p, ctypes.c_size_t, c_int32, _S]),
     "dt_conv2d_gn_stats_bytes": (ctypes.c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "dt_conv2d_gn": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int32,
-                               c_void_p, c_void_p, c_int64, c_void_p, ctypes.c_size_t, c_int32, _S]),
+                               c_void_p, c_void_p, c_int64, c_void_p, ctypes.c_size_t, c_void_p, ctypes.c_size_t,
+                               c_int32, _S]),
     "dt_groupnorm_silu_from_stats": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                                c_void_p, c_float, c_int32, c_void_p, c_int32, _S]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
@@ -483,19 +485,30 @@ def conv2d_pack(w):
     return ConvWeight(packed, co, ci, k)
 
 
-def conv2d(x, w, bias=None, upscale2=False, out=None):
+def _conv_ws(x, workspace):
+    """A workspace for the DMA conv path: True allocates one, a tensor is used
+    as given, None selects the path without one."""
+    torch = _torch()
+    if workspace is True:
+        N, ci, H, W = x.shape
+        return torch.empty(load().dt_conv2d_workspace_bytes(N, ci, H, W), dtype=torch.uint8, device=x.device)
+    return workspace
+
+
+def conv2d(x, w, bias=None, upscale2=False, out=None, workspace=True):
     """x: [N, Ci, H, W] (fp32/bf16, contiguous); w: ConvWeight -> [N, Co, H', W']."""
     torch = _torch()
     N, ci, H, W = x.shape
     assert ci == w.ci and x.is_contiguous()
     Hs, Ws = (2 * H, 2 * W) if upscale2 else (H, W)
     y = torch.empty((N, w.co, Hs, Ws), dtype=x.dtype, device=x.device) if out is None else out
+    ws = _conv_ws(x, workspace)
     check(load().dt_conv2d(_p(x), N, ci, H, W, _p(w.packed), w.co, w.k, 1 if upscale2 else 0, _p(bias), _p(y),
-                           io_type(x), stream()), "dt_conv2d")
+                           _p(ws), ws.numel() if ws is not None else 0, io_type(x), stream()), "dt_conv2d")
     return y
 
 
-def conv2d_gn(x, w, groups, bias=None, upscale2=False, out=None):
+def conv2d_gn(x, w, groups, bias=None, upscale2=False, out=None, workspace=True):
     """dt_conv2d + GroupNorm statistics of the output -> (y, stats); stats[:N*groups*16]
     viewed as float64 pairs holds (mean, variance) per (n, g)."""
     torch = _torch()
@@ -506,8 +519,10 @@ def conv2d_gn(x, w, groups, bias=None, upscale2=False, out=None):
     nb = load().dt_conv2d_gn_stats_bytes(N, w.co, Hs, Ws, groups)
     assert nb > 0, "unsupported conv/GroupNorm shape"
     stats = torch.empty(nb, dtype=torch.uint8, device=x.device)
+    ws = _conv_ws(x, workspace)
     check(load().dt_conv2d_gn(_p(x), N, ci, H, W, _p(w.packed), w.co, w.k, 1 if upscale2 else 0, _p(bias), _p(y),
-                              groups, _p(stats), nb, io_type(x), stream()), "dt_conv2d_gn")
+                              groups, _p(stats), nb, _p(ws), ws.numel() if ws is not None else 0, io_type(x),
+                              stream()), "dt_conv2d_gn")
     return y, stats
 
 

@@ -227,9 +227,14 @@ int dt_quantize_q8_0(const float *src, int64_t rows, int64_t cols, int64_t src_s
 size_t dt_conv2d_packed_bytes(int64_t Co, int64_t Ci, int64_t K);
 int dt_conv2d_pack_weights(const void *w, int32_t w_type, int64_t Co, int64_t Ci, int64_t K,
                            void *packed, dt_stream_t stream);
+/* The caller's workspace of dt_conv2d_workspace_bytes (16-byte aligned)
+ * holds a bf16 channel-last copy of x, from which both operands stream into
+ * LDS by direct DMA; workspace NULL selects a slower path that stages x from
+ * NCHW itself (same results). */
+size_t dt_conv2d_workspace_bytes(int64_t N, int64_t Ci, int64_t H, int64_t W);
 int dt_conv2d(const void *x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void *packed_w,
-              int64_t Co, int64_t K, int32_t upscale2, const float *bias, void *y, int32_t io_type,
-              dt_stream_t stream);
+              int64_t Co, int64_t K, int32_t upscale2, const float *bias, void *y, void *workspace,
+              size_t workspace_bytes, int32_t io_type, dt_stream_t stream);
 
 /* dt_conv2d whose epilogue also reduces GroupNorm(groups) statistics of the
  * output it stores: per output tile and group a (mean, M2, count) record,
@@ -243,7 +248,8 @@ int dt_conv2d(const void *x, int64_t N, int64_t Ci, int64_t H, int64_t W, const 
 size_t dt_conv2d_gn_stats_bytes(int64_t N, int64_t Co, int64_t OH, int64_t OW, int64_t groups);
 int dt_conv2d_gn(const void *x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void *packed_w,
                  int64_t Co, int64_t K, int32_t upscale2, const float *bias, void *y, int64_t groups,
-                 void *stats, size_t stats_bytes, int32_t io_type, dt_stream_t stream);
+                 void *stats, size_t stats_bytes, void *workspace, size_t workspace_bytes,
+                 int32_t io_type, dt_stream_t stream);
 /* GroupNorm(groups) + affine + optional SiLU of x with the statistics
  * dt_conv2d_gn wrote for it: y = silu(((x - mean) * rstd) * w_c + b_c),
  * rstd = 1 / sqrt(var + eps), as dt_groupnorm_silu applies them. */

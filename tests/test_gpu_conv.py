@@ -20,18 +20,20 @@ pytestmark = pytest.mark.gpu
 # tile along the width; narrow images (16-wide tiles); a VAE mid-block shape.
 SHAPES = [((1, 5, 7, 9), 4, 3, False), ((2, 40, 13, 70), 130, 3, False), ((1, 64, 16, 16), 64, 1, False),
           ((1, 32, 10, 33), 48, 3, True), ((1, 24, 5, 3), 16, 3, True), ((1, 512, 16, 32), 512, 3, False),
-          ((1, 96, 9, 130), 32, 1, True)]
+          ((1, 96, 9, 130), 32, 1, True), ((1, 40, 5, 300), 64, 3, False), ((1, 20, 40, 20), 24, 1, False)]
 
 
+@pytest.mark.parametrize("ws", [True, None], ids=["dma", "staged"])
 @pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape,co,k,up2", SHAPES)
-def test_conv2d(orc, dev, shape, co, k, up2, io):
-    print(f"conv2d x={shape} co={co} k={k} up2={up2} {io}", flush=True)
+def test_conv2d(orc, dev, shape, co, k, up2, io, ws):
+    """Both paths: with a workspace (channel-last copy, DMA-fed) and without."""
+    print(f"conv2d x={shape} co={co} k={k} up2={up2} {io} ws={ws}", flush=True)
     x = orc.randn(SEED + 300, shape)
     w = orc.randn(SEED + 301, (co, shape[1], k, k), std=0.05)
     b = orc.randn(SEED + 302, (co,), std=0.1)
     wp = dit_hip.conv2d_pack(dev_tensor(w, torch.float32))
-    y = dit_hip.conv2d(dev_tensor(x, io), wp, bias=dev_tensor(b, torch.float32), upscale2=up2)
+    y = dit_hip.conv2d(dev_tensor(x, io), wp, bias=dev_tensor(b, torch.float32), upscale2=up2, workspace=ws)
     torch.cuda.synchronize()
     ref = orc.conv2d(orc.round_bf16(as_input(x, io)), orc.round_bf16(w), b, up2=up2)
     assert tuple(y.shape) == ref.shape
@@ -83,14 +85,15 @@ GN_CASES = [((1, 64, 12, 40), 512, 3, False, 32), ((2, 32, 9, 70), 256, 3, False
             ((1, 16, 5, 6), 64, 3, False, 64), ((1, 128, 64, 64), 128, 3, False, 32)]
 
 
+@pytest.mark.parametrize("ws", [True, None], ids=["dma", "staged"])
 @pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape,co,k,up2,groups", GN_CASES)
-def test_conv2d_gn_statistics_and_apply(orc, dev, shape, co, k, up2, groups, io):
+def test_conv2d_gn_statistics_and_apply(orc, dev, shape, co, k, up2, groups, io, ws):
     """dt_conv2d_gn stores the same output as dt_conv2d and the (mean,
     variance) of each group of that stored output; dt_groupnorm_silu_from_stats
     then matches the oracle's GroupNorm+SiLU of the stored output (the fp32 /
     bf16 bar of one fused kernel) and the two-pass dt_groupnorm_silu on it."""
-    print(f"conv2d_gn x={shape} co={co} k={k} up2={up2} groups={groups} {io}", flush=True)
+    print(f"conv2d_gn x={shape} co={co} k={k} up2={up2} groups={groups} {io} ws={ws}", flush=True)
     x = orc.randn(SEED + 310, shape)
     w = orc.randn(SEED + 311, (co, shape[1], k, k), std=0.05)
     b = orc.randn(SEED + 312, (co,), std=0.5)
@@ -98,8 +101,8 @@ def test_conv2d_gn_statistics_and_apply(orc, dev, shape, co, k, up2, groups, io)
     gb = orc.randn(SEED + 314, (co,), std=0.1)
     wp = dit_hip.conv2d_pack(dev_tensor(w, torch.float32))
     xd, bd = dev_tensor(x, io), dev_tensor(b, torch.float32)
-    y, stats = dit_hip.conv2d_gn(xd, wp, groups, bias=bd, upscale2=up2)
-    y_plain = dit_hip.conv2d(xd, wp, bias=bd, upscale2=up2)
+    y, stats = dit_hip.conv2d_gn(xd, wp, groups, bias=bd, upscale2=up2, workspace=ws)
+    y_plain = dit_hip.conv2d(xd, wp, bias=bd, upscale2=up2, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(y, y_plain), "the statistics epilogue changed the stored output"
     yh = host(y).astype(np.float64)
