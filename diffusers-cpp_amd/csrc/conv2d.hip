@@ -386,36 +386,52 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
 // index (pixels) or of co (weights) is set, so 8 consecutive records read
 // distinct banks.
 constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
-constexpr int kXLanesMax3 = 7 * 256, kXLanesMax1 = 2 * 256;  // DMA lanes per X stage (3x3, 1x1)
+constexpr int kXLanesMax3 = 7 * 256;  // DMA lanes per X stage: 2 per record, up to 3 x 258 records
 
-template <typename TI>
-__global__ __launch_bounds__(256) void to_nhwc16_kernel(const TI* __restrict__ x, int C, int H, int W, int C16,
+// NCHW (fp32 or bf16) -> bf16 NHWC with C16 channels (zeros past C), over
+// the flattened H*W plane in tiles of 64 pixels x 64 channels: 16-byte loads
+// along the pixels of each channel (VEC; scalar when the plane is not a
+// multiple of 8 pixels), a transpose through LDS, and 16-byte stores of 8
+// channels of one pixel.  Block (0, 0, 0) also zeroes the 256-byte tail the
+// conv reads for out-of-image taps.
+template <typename TI, bool VEC>
+__global__ __launch_bounds__(256) void to_nhwc16_kernel(const TI* __restrict__ x, int C, int64_t HW, int C16,
                                                         uint16_t* __restrict__ out, int64_t tail_offset) {
-    // block: (w tile of 64, h, n); 16 channels at a time through LDS.
-    __shared__ float t[16][65];
-    const int w0 = blockIdx.x * 64, h = blockIdx.y, n = blockIdx.z;
-    const TI* xn = x + (int64_t)n * C * H * W;
-    uint16_t* on = out + (((int64_t)n * H + h) * W) * C16;
-    for (int c0 = 0; c0 < C16; c0 += 16) {
-        for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-            const int c = i >> 6, w = i & 63;
-            float v = 0.f;
-            if (c0 + c < C && w0 + w < W) v = load_in<TI>(xn + ((int64_t)(c0 + c) * H + h) * W + w0 + w);
-            t[c][w] = v;
-        }
-        __syncthreads();
-        if (threadIdx.x < 128) {
-            const int w = threadIdx.x >> 1, half = threadIdx.x & 1;
-            if (w0 + w < W) {
-                float v[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = t[half * 8 + e][w];
-                *reinterpret_cast<uint4*>(on + (int64_t)(w0 + w) * C16 + c0 + half * 8) =
-                    make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                               pack_bf16x2(v[6], v[7]));
+    __shared__ uint16_t t[64][64 + 2];  // [channel][pixel] (+2: spread the per-pixel column reads)
+    const int64_t p0 = (int64_t)blockIdx.x * 64;
+    const int c0 = blockIdx.y * 64, n = blockIdx.z;
+    const TI* xn = x + (int64_t)n * C * HW;
+    uint16_t* on = out + (int64_t)n * HW * C16;
+    constexpr int EPV = VEC ? 16 / (int)sizeof(TI) : 1;  // pixels per load
+    constexpr int VPR = 64 / EPV;                          // loads per channel row
+    for (int u = threadIdx.x; u < 64 * VPR; u += 256) {
+        const int c = u / VPR, q = u - c * VPR;
+        const int64_t p = p0 + q * EPV;
+        float v[EPV];
+        if (c0 + c < C && p < HW) {
+            if constexpr (VEC) {
+                Io<TI>::load(xn + (int64_t)(c0 + c) * HW + p, v);
+            } else {
+                v[0] = load_in<TI>(xn + (int64_t)(c0 + c) * HW + p);
             }
+        } else {
+#pragma unroll
+            for (int k = 0; k < EPV; ++k) v[k] = 0.f;
         }
-        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < EPV; ++k) t[c][q * EPV + k] = (uint16_t)(pack_bf16x2(v[k], 0.f) & 0xFFFFu);
+    }
+    __syncthreads();
+    for (int u = threadIdx.x; u < 64 * 8; u += 256) {
+        const int px = u >> 3, part = u & 7;  // pixel, 8-channel unit
+        const int64_t p = p0 + px;
+        const int c = c0 + part * 8;
+        if (p >= HW || c >= C16) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = (uint32_t)t[part * 8 + 2 * k][px] | ((uint32_t)t[part * 8 + 2 * k + 1][px] << 16);
+        *reinterpret_cast<uint4*>(on + p * C16 + c) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 16)
         reinterpret_cast<uint4*>(out + tail_offset)[threadIdx.x] = make_uint4(0, 0, 0, 0);
@@ -438,8 +454,9 @@ __device__ __forceinline__ void conv_wait_vm() {
 
 template <typename T, int K, bool STATS>
 __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const Conv2Extra e) {
+    static_assert(K == 3, "the DMA kernel is sized for 3x3 patches");
     constexpr int KK = K * K, PAD = (K - 1) / 2;
-    constexpr int XL = K == 3 ? kXLanesMax3 : kXLanesMax1;  // X DMA lanes per stage
+    constexpr int XL = kXLanesMax3;  // X DMA lanes per stage
     constexpr int NX = XL / 256, NW = 2 * kTileCo * KK / 256;  // DMA instructions per wave per stage
     constexpr int XB = XL * 16, WB = kTileCo * KK * kRec2, STAGE = XB + WB;
     constexpr int QD = NX + NW;
@@ -692,22 +709,28 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
         e.C16 = (int)pad_to(Ci, kCi2);
         e.Cp32 = a.Ci_pad;
         e.lt = __builtin_ctz((unsigned)a.TC);
-        const dim3 tg((unsigned)((W + 63) / 64), (unsigned)H, (unsigned)N);
-        if (io_type == DT_TYPE_F32)
-            hipLaunchKernelGGL((to_nhwc16_kernel<float>), tg, dim3(256), 0, st, (const float*)x, (int)Ci, (int)H,
-                               (int)W, e.C16, (uint16_t*)ws, elems);
-        else
-            hipLaunchKernelGGL((to_nhwc16_kernel<bf16>), tg, dim3(256), 0, st, (const bf16*)x, (int)Ci, (int)H,
-                               (int)W, e.C16, (uint16_t*)ws, elems);
+        const int64_t HW = H * W;
+        const dim3 tg((unsigned)((HW + 63) / 64), (unsigned)((e.C16 + 63) / 64), (unsigned)N);
+        const bool vec = HW % 8 == 0 && aligned16(x);
+#define DT_NHWC(TT, VV) hipLaunchKernelGGL((to_nhwc16_kernel<TT, VV>), tg, dim3(256), 0, st, (const TT*)x, (int)Ci, \
+                                           HW, e.C16, (uint16_t*)ws, elems)
+        if (io_type == DT_TYPE_F32) {
+            if (vec) DT_NHWC(float, true);
+            else DT_NHWC(float, false);
+        } else {
+            if (vec) DT_NHWC(bf16, true);
+            else DT_NHWC(bf16, false);
+        }
+#undef DT_NHWC
         int rc = check_launch(what);
         if (rc) return rc;
 #define DT_CONV2_LAUNCH(TT, KS, ST) hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST>), grid, dim3(256), 0, st, a, e)
         if (io_type == DT_TYPE_F32) {
-            if (K == 3) { if (stats) DT_CONV2_LAUNCH(float, 3, true); else DT_CONV2_LAUNCH(float, 3, false); }
-            else { if (stats) DT_CONV2_LAUNCH(float, 1, true); else DT_CONV2_LAUNCH(float, 1, false); }
+            if (stats) DT_CONV2_LAUNCH(float, 3, true);
+            else DT_CONV2_LAUNCH(float, 3, false);
         } else {
-            if (K == 3) { if (stats) DT_CONV2_LAUNCH(bf16, 3, true); else DT_CONV2_LAUNCH(bf16, 3, false); }
-            else { if (stats) DT_CONV2_LAUNCH(bf16, 1, true); else DT_CONV2_LAUNCH(bf16, 1, false); }
+            if (stats) DT_CONV2_LAUNCH(bf16, 3, true);
+            else DT_CONV2_LAUNCH(bf16, 3, false);
         }
 #undef DT_CONV2_LAUNCH
         return check_launch(what);
