@@ -47,6 +47,7 @@ PKG = os.path.join(ROOT, "diffusers-cpp_amd")
 sys.path.insert(0, PKG)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 NSETS = 4
 S, D, H, HD, I = 4608, 3072, 24, 128, 9216
 N_TXT, GRID = 512, 64
@@ -194,6 +195,52 @@ def secondary(torch, dev, flush):
             out[name] = {"us": round(t * 1e6, 2), "alg_MB": round(nbytes / 1e6, 2),
                          "GBs": round(nbytes / t / 1e9, 1), "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3)}
             del x, y
+    out["vae"] = vae_measurements(torch, dev, flush)
+    return out
+
+
+def vae_measurements(torch, dev, flush, reps=6):
+    """The VAE decoder's 3x3 convs (dt_conv2d with a workspace: channel-last
+    copy + DMA-fed MFMA kernel; bias) and their GroupNorm(32)+SiLU at the
+    decoder's shapes: GroupNorm two-pass (statistics + apply) against the
+    statistics from the conv epilogue (dt_conv2d_gn) + one apply pass."""
+    import dit_hip
+    out = {}
+    for shape, co in (((1, 512, 128, 128), 512), ((1, 512, 256, 256), 512), ((1, 256, 512, 512), 256),
+                      ((1, 128, 1024, 1024), 128)):
+        for dt, tag, es in ((torch.bfloat16, "bf16", 2), (torch.float32, "f32", 4)):
+            x = torch.randn(shape, device=dev).to(dt)
+            wp = dit_hip.conv2d_pack(torch.randn(co, shape[1], 3, 3, device=dev) * 0.02)
+            b = torch.randn(co, device=dev) * 0.1
+            gw = torch.randn(co, device=dev) * 0.02 + 1
+            gb = torch.randn(co, device=dev) * 0.02
+            y = torch.empty((1, co) + shape[2:], dtype=dt, device=dev)
+            z = torch.empty_like(y)
+            cws = dit_hip._conv_ws(x, True)
+            gws = torch.empty(dit_hip.load().dt_groupnorm_workspace_bytes(1, co, shape[2] * shape[3], 32),
+                              dtype=torch.uint8, device=dev)
+            _, stats = dit_hip.conv2d_gn(x, wp, 32, bias=b, out=y, workspace=cws)
+            t_conv = time_cold(torch, lambda: dit_hip.conv2d(x, wp, bias=b, out=y, workspace=cws), reps, flush)
+            t_convgn = time_cold(torch, lambda: dit_hip.conv2d_gn(x, wp, 32, bias=b, out=y, workspace=cws), reps,
+                                 flush)
+            t_gn2 = time_cold(torch, lambda: dit_hip.groupnorm_silu(y, 32, gw, gb, 1e-6, out=z, workspace=gws), reps,
+                              flush)
+            t_gn1 = time_cold(torch, lambda: dit_hip.groupnorm_silu_from_stats(y, stats, 32, gw, gb, 1e-6, out=z),
+                              reps, flush)
+            flop = 2.0 * co * shape[1] * 9 * shape[2] * shape[3]
+            gn_bytes = 2 * y.numel() * es
+            name = f"conv3x3_{shape[1]}x{shape[2]}x{shape[3]}_to_{co}_{tag}"
+            out[name] = {
+                "conv_us": round(t_conv * 1e6, 1), "conv_tflops": round(flop / t_conv / 1e12, 1),
+                "conv_frac_mfma": round(flop / t_conv / 1e12 / MFMA_PEAK_TFLOPS, 3),
+                "conv_with_gn_stats_us": round(t_convgn * 1e6, 1),
+                "groupnorm_two_pass_us": round(t_gn2 * 1e6, 1),
+                "groupnorm_from_stats_us": round(t_gn1 * 1e6, 1),
+                "groupnorm_from_stats_frac_hbm": round(gn_bytes / t_gn1 / 1e9 / HBM_PEAK_GBS, 3),
+                "conv_plus_groupnorm_us": {"two_pass": round((t_conv + t_gn2) * 1e6, 1),
+                                           "stats_in_conv": round((t_convgn + t_gn1) * 1e6, 1)},
+            }
+            del x, y, z, cws
     return out
 
 
@@ -312,12 +359,22 @@ def main():
     ap.add_argument("--denoise-steps", type=int, default=5,
                     help="timed full denoising steps (0 skips the step measurement)")
     ap.add_argument("--denoise-warmup", type=int, default=2)
+    ap.add_argument("--vae-only", action="store_true",
+                    help="print only the VAE conv / GroupNorm measurements (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "the chain is row-independent and would shard tokens across GPUs with no exchange",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.vae_only:
+        import torch
+        import dit_hip
+        dit_hip.load()
+        dev = torch.device("cuda:0")
+        print(json.dumps({"vae": vae_measurements(torch, dev, Flusher(torch, dev))}), flush=True)
+        return
 
     # The full step runs in its own process before this one touches the GPU.
     denoise = denoise_step(args.denoise_steps, args.denoise_warmup) if args.denoise_steps > 0 else None
