@@ -614,6 +614,25 @@ void run(const Args& a) {
         Tensor y = m.forward(x);
         if (a.flag("silu", false)) y = SiLU().forward(y);   // ResnetBlock2D.inl:111-122
         s.output(y, "out");
+    } else if (c == "Conv2d") {
+        // Conv2d.py: --in_channels, --out_channels, --kernel_size, --stride, --padding, --bias
+        const bool bias = a.flag("bias", true);
+        Conv2d m(a.i64("in_channels"), a.i64("out_channels"), a.i64("kernel_size"), a.i64("stride", 1),
+                 a.i64("padding", 0), bias);
+        Tensor x = s.input("x");
+        s.param(m.weight, "weight");
+        if (bias) s.param(m.bias, "bias");
+        s.output(m.forward(x), "out");
+    } else if (c == "Upsample2D") {
+        // Upsample2D.py: --channels, --use_conv, --out_channels
+        const bool use_conv = a.flag("use_conv", false);
+        Upsample2D m(a.i64("channels"), use_conv, a.i64("out_channels", -1));
+        Tensor x = s.input("hidden_states");
+        if (use_conv) {
+            s.param(m.conv()->weight, "conv.weight");
+            s.param(m.conv()->bias, "conv.bias");
+        }
+        s.output(m.forward(x), "out");
     } else if (c == "SiLU") {
         s.output(SiLU().forward(s.input("x")), "out");
     } else if (c == "Flux2PosEmbed") {

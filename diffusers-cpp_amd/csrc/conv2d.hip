@@ -795,3 +795,36 @@ extern "C" int dt_conv2d_gn(const void* x, int64_t N, int64_t Ci, int64_t H, int
     if (rc) return rc;
     return gn_tile_stats_finalize(stats, N, groups, tiles, st);
 }
+
+namespace dit {
+namespace {
+
+template <typename T>
+__global__ void upscale_nearest_kernel(const T* __restrict__ x, int64_t H, int64_t W, int f, T* __restrict__ y,
+                                       int64_t total) {
+    const int64_t Wo = W * f, Ho = H * f;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t j = i % Wo, r = i / Wo, oi = r % Ho, plane = r / Ho;
+        y[i] = x[(plane * H + oi / f) * W + j / f];
+    }
+}
+
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_op_upscale_nearest(const void* src, int64_t N, int64_t C, int64_t H, int64_t W, int32_t factor,
+                                     void* dst, int32_t io_type, dt_stream_t stream) {
+    using namespace dit;
+    DT_REQUIRE(is_io_type(io_type), "dt_op_upscale_nearest: io_type %d unsupported", io_type);
+    DT_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && factor >= 1, "dt_op_upscale_nearest: bad shape");
+    DT_REQUIRE(src && dst, "dt_op_upscale_nearest: null pointer");
+    const int64_t total = N * C * H * W * factor * factor;
+    const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+    if (io_type == DT_TYPE_F32)
+        hipLaunchKernelGGL((upscale_nearest_kernel<float>), dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                           (const float*)src, H, W, factor, (float*)dst, total);
+    else
+        hipLaunchKernelGGL((upscale_nearest_kernel<uint16_t>), dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t*)src, H, W, factor, (uint16_t*)dst, total);
+    return check_launch("dt_op_upscale_nearest");
+}

@@ -19,6 +19,10 @@
 //   GEMM accumulate ADD(y, MUL_MAT(w, x)): the second projection of
 //                   Flux2FusedAttentionOutput.hpp:31-36 accumulates onto the
 //                   first in the GEMM epilogue (dt_gemm_bf16 with addend).
+//   Conv2d          ADD(CONV_2D_DIRECT(w, x), VIEW(bias)) with x optionally
+//                   UPSCALE(x0, 2): Conv2d.cpp:38-102 and Upsample2D.cpp:50-72
+//                   as one dt_conv2d (bias in the epilogue, the nearest
+//                   upsample in the input addressing).
 //
 // After fusion, runs of independent MUL_MATs (only VIEWs between them, every
 // input computed before the first) become one grouped GEMM launch at the
@@ -91,6 +95,12 @@ bool contiguous_f32(const dt_tensor* t) {
            (t->ne[3] == 1 || t->nb[3] == 4 * t->ne[0] * t->ne[1] * t->ne[2]);
 }
 
+// Every element in order, no gaps (any element type).
+bool dense(const dt_tensor* t) {
+    int64_t rows, stride;
+    return row_layout(t, &rows, &stride) && stride == t->ne[0];
+}
+
 // fp32 vector of n contiguous elements whose single non-unit dim is `dim`.
 bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
     if (!t || !contiguous_f32(t)) return false;
@@ -99,7 +109,10 @@ bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
     return true;
 }
 
-enum Kind { K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD, K_GEMM_GROUP, K_RES_ADALN, K_QK_SWIGLU, K_DEFERRED };
+enum Kind {
+    K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD, K_GEMM_GROUP, K_RES_ADALN, K_QK_SWIGLU,
+    K_CONV, K_DEFERRED
+};
 
 struct QkSeg {
     const dt_tensor* q;   // RMS_NORM input
@@ -113,6 +126,7 @@ struct Plan {
     const dt_tensor* in[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     float eps = 0.f;
     int silu = 0;
+    int up2 = 0;  // CONV: the input is upsampled 2x (nearest) on the fly
     // QK
     std::vector<QkSeg> segs;
     std::vector<const dt_tensor*> pos;  // per axis
@@ -357,6 +371,46 @@ bool match_groupnorm(Graph& g, const dt_tensor* root, Plan& p) {
     p.in[3] = v;
     p.eps = fparam(n, 0);
     p.silu = silu;
+    return true;
+}
+
+// Conv2d::forward (Conv2d.cpp:38-102): CONV_2D_DIRECT, or ADD(conv, bias
+// reshaped to [1, Co, 1, 1]) with the conv used only there.  An UPSCALE x2
+// input used only by the conv (Upsample2D.cpp:50-72) is read through the
+// conv's upsampled addressing instead of being materialised.  Operand checks
+// happen at execution (run_conv), where a mismatch is reported.
+bool match_conv(Graph& g, const dt_tensor* t, Plan& p) {
+    const dt_tensor* c = nullptr;
+    const dt_tensor* bias = nullptr;
+    if (t->op == DT_OP_CONV_2D_DIRECT) {
+        c = t;
+    } else if (t->op == DT_OP_ADD) {
+        for (int k = 0; k < 2 && !c; ++k) {
+            const dt_tensor* a = t->src[k];
+            const dt_tensor* b = t->src[1 - k];
+            if (a && a->op == DT_OP_CONV_2D_DIRECT && g.internal(a) && same_shape(a, t) && a->type == t->type &&
+                is_vec(b, a->ne[2], 2) && dense(t)) {
+                c = a;
+                bias = b;
+            }
+        }
+    }
+    if (!c || !c->src[0] || !c->src[1]) return false;
+    const dt_tensor* x = c->src[1];
+    const dt_tensor* up = nullptr;
+    if (x->op == DT_OP_UPSCALE && x->op_params[0] == 2 && x->src[0] && g.internal(x) &&
+        x->src[0]->type == x->type && dense(x->src[0])) {
+        up = x;
+        x = x->src[0];
+    }
+    if (c != t) g.claim(c);
+    if (up) g.claim(up);
+    p.kind = K_CONV;
+    p.in[0] = x;
+    p.in[1] = c->src[0];
+    p.in[2] = bias;
+    p.in[3] = c;
+    p.up2 = up != nullptr;
     return true;
 }
 
@@ -703,6 +757,50 @@ int run_flash_attn(hipStream_t st, const dt_tensor* t) {
                               q->ne[0], qs, ks, vs, os, fparam(t, 0), t->type, st);
 }
 
+// One convolution: the weights packed into the backend's scratch (bf16
+// [Co][K*K][Ci] tiles; a few MB, re-packed per call), the channel-last copy
+// of x after them, then dt_conv2d into root.
+int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt_tensor* w, const dt_tensor* bias,
+             const dt_tensor* conv, int up2) {
+    hipStream_t st = backend_stream(be);
+    const int64_t K = w->ne[0], Ci = w->ne[2], Co = w->ne[3];
+    const int64_t W = x->ne[0], H = x->ne[1], N = x->ne[3], f = up2 ? 2 : 1;
+    const int32_t* prm = conv->op_params;
+    DT_REQUIRE(prm[0] == 1 && prm[1] == 1 && prm[4] == 1 && prm[5] == 1,
+               "dt_graph_compute: CONV_2D_DIRECT with stride %d,%d / dilation %d,%d (1 only)", prm[0], prm[1],
+               prm[4], prm[5]);
+    DT_REQUIRE((K == 1 || K == 3) && w->ne[1] == K && prm[2] == (K - 1) / 2 && prm[3] == (K - 1) / 2,
+               "dt_graph_compute: CONV_2D_DIRECT needs a square 1x1 / 3x3 kernel with padding (K - 1) / 2");
+    DT_REQUIRE(w->type == DT_TYPE_F32 || w->type == DT_TYPE_BF16, "dt_graph_compute: CONV_2D_DIRECT weight type %d",
+               w->type);
+    DT_REQUIRE(is_io_type(x->type) && x->type == root->type, "dt_graph_compute: CONV_2D_DIRECT input/output types");
+    DT_REQUIRE(dense(x) && dense(w) && dense(root), "dt_graph_compute: CONV_2D_DIRECT operands must be contiguous");
+    DT_REQUIRE(x->ne[2] == Ci && root->ne[0] == W * f && root->ne[1] == H * f && root->ne[2] == Co &&
+                   root->ne[3] == N,
+               "dt_graph_compute: CONV_2D_DIRECT shapes disagree");
+    const size_t packed = (dt_conv2d_packed_bytes(Co, Ci, K) + 255) / 256 * 256;
+    const size_t ws = K == 3 ? dt_conv2d_workspace_bytes(N, Ci, H, W) : 0;
+    void* scratch = nullptr;
+    int rc = backend_scratch(be, packed + ws, &scratch);
+    if (rc) return rc;
+    rc = dt_conv2d_pack_weights(data_of(w), w->type, Co, Ci, K, scratch, st);
+    if (rc) return rc;
+    g_kernels += K == 3 ? 3 : 2;  // pack, channel-last copy (3x3), conv
+    return dt_conv2d(data_of(x), N, Ci, H, W, scratch, Co, K, up2, bias ? (const float*)data_of(bias) : nullptr,
+                     root->data, ws ? (char*)scratch + packed : nullptr, ws, root->type, st);
+}
+
+int run_upscale(hipStream_t st, const dt_tensor* t) {
+    const dt_tensor* x = t->src[0];
+    const int f = t->op_params[0];
+    DT_REQUIRE(x && x->type == t->type && is_io_type(t->type) && dense(x) && dense(t),
+               "dt_graph_compute: UPSCALE operands must be contiguous F32 / BF16 of one type");
+    DT_REQUIRE(f >= 1 && t->ne[0] == x->ne[0] * f && t->ne[1] == x->ne[1] * f && t->ne[2] == x->ne[2] &&
+                   t->ne[3] == x->ne[3],
+               "dt_graph_compute: UPSCALE shapes disagree");
+    return dt_op_upscale_nearest(data_of(x), x->ne[3], x->ne[2], x->ne[1], x->ne[0], f, t->data, t->type, st);
+}
+
 int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
     hipStream_t st = backend_stream(be);
     switch (p.kind) {
@@ -808,6 +906,8 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
                                          (const float*)data_of(p.in[4]), 0.0f, root->data, ys, rows, root->ne[0],
                                          p.eps, root->type, st);
         }
+        case K_CONV:
+            return run_conv(be, root, p.in[0], p.in[1], p.in[2], p.in[3], p.up2);
         case K_DEFERRED:
             return DT_OK;  // ran in its group's launch
         default:
@@ -869,6 +969,12 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
         case DT_OP_FLASH_ATTN_EXT:
             ++g_kernels;
             return run_flash_attn(st, t);
+        case DT_OP_CONV_2D_DIRECT:
+            DT_REQUIRE(t->src[0] && t->src[1], "dt_graph_compute: CONV_2D_DIRECT needs a weight and an input");
+            return run_conv(be, t, t->src[1], t->src[0], nullptr, t, 0);
+        case DT_OP_UPSCALE:
+            ++g_kernels;
+            return run_upscale(st, t);
         default:
             return fail(DT_ERR_UNSUPPORTED, "dt_graph_compute: op %d not supported", t->op);
     }
@@ -904,7 +1010,7 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
         g.current_root = i;
         if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_res_adaln(g, t, p) || match_adaln(g, t, p) ||
             match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p) ||
-            match_gemm_add(g, t, p))
+            match_gemm_add(g, t, p) || match_conv(g, t, p))
             continue;
         p = Plan();
     }

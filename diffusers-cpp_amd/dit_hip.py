@@ -21,7 +21,8 @@ F32, F16, Q8_0, Q4_K, I32, BF16 = 0, 1, 8, 12, 26, 30
 
 # dt_tensor.op ids
 (OP_NONE, OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_SCALE, OP_SIGMOID, OP_NORM, OP_RMS_NORM,
- OP_ROPE, OP_CONCAT, OP_CPY, OP_VIEW, OP_FILL, OP_UNARY) = range(15)
+ OP_ROPE, OP_CONCAT, OP_CPY, OP_VIEW, OP_FILL, OP_UNARY, OP_MUL_MAT, OP_FLASH_ATTN_EXT, OP_CONV_2D_DIRECT,
+ OP_UPSCALE) = range(19)
 FLAG_OUTPUT = 1
 
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = range(4)
@@ -104,6 +105,7 @@ _SIGS = {
                                c_int32, _S]),
     "dt_groupnorm_silu_from_stats": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                                c_void_p, c_float, c_int32, c_void_p, c_int32, _S]),
+    "dt_op_upscale_nearest": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_void_p, c_int32, _S]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
     "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,

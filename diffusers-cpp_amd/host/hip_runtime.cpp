@@ -421,8 +421,30 @@ Node* HipRuntime::flash_attn_ext(Node* q, Node* k, Node* v, Node* mask, float sc
     r->op_params[0] = fbits(scale);
     return r;
 }
-Node* HipRuntime::conv_2d_direct(Node*, Node*, int, int, int, int, int, int) {
-    throw Unsupported("conv_2d_direct: not part of the DiT elementwise chain");
+// ggml_conv_2d_direct (Runtime.hpp, Conv2d.cpp:38-52): weight a ne {K, K, Ci, Co},
+// contiguous input b ne {W, H, Ci, N} -> ne {W', H', Co, N} of b's type.  The
+// VAE decoder's convolutions only: stride 1, dilation 1, K in {1, 3} with
+// "same" padding (K - 1) / 2.
+Node* HipRuntime::conv_2d_direct(Node* a, Node* b, int s0, int s1, int p0, int p1, int d0, int d1) {
+    const int64_t K = a->ne[0];
+    if (s0 != 1 || s1 != 1 || d0 != 1 || d1 != 1)
+        throw Unsupported("conv_2d_direct: stride and dilation 1 only");
+    if (a->ne[1] != K || (K != 1 && K != 3) || p0 != (K - 1) / 2 || p1 != (K - 1) / 2)
+        throw Unsupported("conv_2d_direct: square 1x1 / 3x3 kernels with padding (K - 1) / 2 only");
+    if (a->ne[2] != b->ne[2]) throw std::invalid_argument("conv_2d_direct: weight and input channels differ");
+    if (a->type != DT_TYPE_F32 && a->type != DT_TYPE_BF16)
+        throw Unsupported("conv_2d_direct: F32 / BF16 weights only");
+    if (b->type != DT_TYPE_F32 && b->type != DT_TYPE_BF16)
+        throw Unsupported("conv_2d_direct: F32 / BF16 input only");
+    if (!is_contiguous(a)) a = cont(a);
+    if (!is_contiguous(b)) b = cont(b);
+    const int64_t ne[4] = {b->ne[0], b->ne[1], a->ne[3], b->ne[3]};
+    Node* r = make(b->type, ne, DT_OP_CONV_2D_DIRECT);
+    r->src[0] = a;
+    r->src[1] = b;
+    const int32_t params[6] = {s0, s1, p0, p1, d0, d1};
+    for (int i = 0; i < 6; ++i) r->op_params[i] = params[i];
+    return r;
 }
 Node* HipRuntime::get_rows(Node*, Node*) { throw Unsupported("get_rows: not part of the DiT elementwise chain"); }
 Node* HipRuntime::pool_2d(Node*, PoolOp, int, int, int, int, float, float) {
@@ -431,8 +453,17 @@ Node* HipRuntime::pool_2d(Node*, PoolOp, int, int, int, int, float, float) {
 Node* HipRuntime::interpolate(Node*, int64_t, int64_t, int64_t, int64_t, uint32_t) {
     throw Unsupported("interpolate: not part of the DiT elementwise chain");
 }
-Node* HipRuntime::upscale(Node*, int, ScaleMode) {
-    throw Unsupported("upscale: not part of the DiT elementwise chain");
+// ggml_upscale(a, factor, NEAREST) (Upsample2D.cpp:36-63): ne {W, H, C, N}
+// -> {factor W, factor H, C, N}, each output pixel its source pixel's value.
+Node* HipRuntime::upscale(Node* a, int scale_factor, ScaleMode mode) {
+    if (mode != ScaleMode::Nearest) throw Unsupported("upscale: nearest mode only");
+    if (scale_factor < 1) throw std::invalid_argument("upscale: factor must be >= 1");
+    if (!is_contiguous(a)) a = cont(a);
+    const int64_t ne[4] = {a->ne[0] * scale_factor, a->ne[1] * scale_factor, a->ne[2], a->ne[3]};
+    Node* r = make(a->type, ne, DT_OP_UPSCALE);
+    r->src[0] = a;
+    r->op_params[0] = scale_factor;
+    return r;
 }
 
 // ---- norms / rope ----------------------------------------------------------------

@@ -5,6 +5,8 @@
 //   RMSNorm        src/nn/modules/normalization/RMSNorm.cpp:12-22
 //   GroupNorm      src/nn/modules/normalization/GroupNorm.cpp:79-161
 //   SiLU           src/nn/SiLU.hpp:9-13
+//   Conv2d         src/nn/modules/conv/Conv2d.cpp:5-102
+//   Upsample2D     src/diffusers/models/resnet/Upsample2D.cpp:5-75
 //   Flux2PosEmbed  src/diffusers/models/transformers/flux2/Flux2PosEmbed.hpp:18-109
 //   Flux2SwiGLU    src/diffusers/models/transformers/flux2/Flux2SwiGLU.hpp:17-21
 //   Flux2Modulation::split  Flux2Modulation.hpp:24-41
@@ -15,6 +17,7 @@
 #pragma once
 
 #include <array>
+#include <memory>
 #include <string>
 #include <utility>
 #include <vector>
@@ -142,6 +145,64 @@ private:
 struct SiLU {
     // x * sigmoid(x): the composite the reference emits instead of ggml_silu.
     Tensor forward(const Tensor& x) const { return x * x.sigmoid(); }
+};
+
+// Conv2d (src/nn/modules/conv/Conv2d.cpp:5-102): weight [Co, Ci, K, K] and
+// bias [Co]; forward = conv_2d_direct on the contiguous input, then the bias
+// broadcast as [1, Co, 1, 1].  The executor runs the pair as one convolution
+// with the bias in its epilogue.
+class Conv2d : public Module {
+public:
+    Conv2d(int64_t in_channels, int64_t out_channels, int64_t kernel_size, int64_t stride = 1, int64_t padding = 0,
+           bool bias = true)
+        : stride_(stride), padding_(padding), bias_(bias) {
+        weight = parameter({out_channels, in_channels, kernel_size, kernel_size});
+        register_parameter("weight", weight);
+        if (bias_) {
+            this->bias = parameter({out_channels});
+            register_parameter("bias", this->bias);
+        }
+    }
+    Tensor forward(Tensor x) const {
+        if (!x.is_contiguous()) x = x.contiguous();
+        const Tensor::Shape& ws = weight.shape();
+        Tensor::Shape shape = x.shape();
+        Node* y = current_runtime().conv_2d_direct(*weight, *x, (int)stride_, (int)stride_, (int)padding_,
+                                                   (int)padding_, 1, 1);
+        shape[1] = ws[0];
+        shape[2] = (shape[2] + 2 * padding_ - ws[2]) / stride_ + 1;
+        shape[3] = (shape[3] + 2 * padding_ - ws[3]) / stride_ + 1;
+        Tensor out(y, shape);
+        if (bias_) out = out + bias.reshape({1, ws[0], 1, 1});
+        return out;
+    }
+    Tensor weight, bias;
+
+private:
+    int64_t stride_, padding_;
+    bool bias_;
+};
+
+// Upsample2D (src/diffusers/models/resnet/Upsample2D.cpp:5-75): nearest 2x
+// upscale, then an optional 3x3 conv (padding 1).  With the conv, the
+// executor folds the upscale into the conv's input addressing.
+class Upsample2D : public Module {
+public:
+    explicit Upsample2D(int64_t channels, bool use_conv = false, int64_t out_channels = -1) {
+        if (use_conv) {
+            conv_.reset(new Conv2d(channels, out_channels > 0 ? out_channels : channels, 3, 1, 1));
+            register_module("conv", *conv_);
+        }
+    }
+    Tensor forward(const Tensor& hidden_states) const {
+        const Tensor::Shape& s = hidden_states.shape();
+        Tensor h(current_runtime().upscale(*hidden_states, 2, ScaleMode::Nearest), {s[0], s[1], s[2] * 2, s[3] * 2});
+        return conv_ ? conv_->forward(h) : h;
+    }
+    Conv2d* conv() const { return conv_.get(); }
+
+private:
+    std::unique_ptr<Conv2d> conv_;
 };
 
 class Flux2PosEmbed {

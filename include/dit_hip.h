@@ -257,6 +257,12 @@ int dt_groupnorm_silu_from_stats(const void *x, int64_t N, int64_t C, int64_t HW
                                  const void *stats, const float *w, const float *b, float eps,
                                  int32_t apply_silu, void *y, int32_t io_type, dt_stream_t stream);
 
+/* ggml_upscale(x, factor, GGML_SCALE_MODE_NEAREST) of a contiguous NCHW
+ * tensor: dst[n][c][i][j] = src[n][c][i / factor][j / factor]
+ * (Upsample2D::forward, Upsample2D.cpp:36-63, when no conv consumes it). */
+int dt_op_upscale_nearest(const void *src, int64_t N, int64_t C, int64_t H, int64_t W, int32_t factor, void *dst,
+                          int32_t io_type, dt_stream_t stream);
+
 /* Synthetic N(mean, std^2) fp32 data on the device (benchmark weights and
  * inputs; a seeded splitmix64 + Box-Muller stream).  No counterpart in the
  * reference, which reads weights from GGUF files. */
@@ -434,6 +440,11 @@ enum {
     DT_OP_FLASH_ATTN_EXT,/* ggml_flash_attn_ext(q ne {D, Sq, H, B}, k, v ne {D, Skv, H, B},
                             src[3] = mask, must be NULL) -> ne {D, H, Sq, B};
                             op_params[0] = scale bits; BF16 q/k/v, D = 128 */
+    DT_OP_CONV_2D_DIRECT,/* ggml_conv_2d_direct(src0 = weight ne {K, K, Ci, Co} F32/BF16,
+                            src1 = x ne {W, H, Ci, N} contiguous) -> ne {W', H', Co, N} of
+                            x's type; op_params = s0, s1, p0, p1, d0, d1 (stride and
+                            dilation 1, K in {1, 3}, padding (K - 1) / 2) */
+    DT_OP_UPSCALE,       /* ggml_upscale(x, factor, NEAREST): op_params[0] = factor */
     DT_OP_COUNT
     /* DT_OP_CPY: src[0] is copied (converted) into the node; src[1], when
        set, is the destination tensor the node aliases (ggml_cpy). */

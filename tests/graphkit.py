@@ -132,6 +132,17 @@ class Graph:
     def cont(self, a, type_=None):
         return self._new(dh.OP_CPY, a.ne, type_ if type_ is not None else a.d.type, [a])
 
+    def conv_2d_direct(self, w, x, s0=1, s1=1, p0=1, p1=1, d0=1, d1=1):
+        """ggml_conv_2d_direct: w ne {K, K, Ci, Co}, x ne {W, H, Ci, N}."""
+        K = w.ne[0]
+        ow = (x.ne[0] + 2 * p0 - d0 * (K - 1) - 1) // s0 + 1
+        oh = (x.ne[1] + 2 * p1 - d1 * (K - 1) - 1) // s1 + 1
+        return self._new(dh.OP_CONV_2D_DIRECT, [ow, oh, w.ne[3], x.ne[3]], x.d.type, [w, x], [s0, s1, p0, p1, d0, d1])
+
+    def upscale(self, a, factor):
+        ne = a.ne
+        return self._new(dh.OP_UPSCALE, [ne[0] * factor, ne[1] * factor, ne[2], ne[3]], a.d.type, [a], [factor])
+
     # ---- execution ---------------------------------------------------------
     def _array(self):
         return (ctypes.POINTER(dh.DtTensor) * len(self.nodes))(*[ctypes.pointer(n.d) for n in self.nodes])

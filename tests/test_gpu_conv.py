@@ -130,3 +130,92 @@ def test_conv2d_gn_rejects_groups_not_dividing_the_tile(dev):
         dit_hip.conv2d_gn(x, wp, 5)  # 96 % 5 != 0: no stats layout
     with pytest.raises(RuntimeError, match="must divide 128"):
         dit_hip.conv2d_gn(x, wp, 2)  # 48 channels per group
+
+
+# ------------------------------------------------ through dt_graph_compute --
+@pytest.fixture
+def be(dev):
+    from graphkit import Backend
+    b = Backend()
+    yield b.h
+    torch.cuda.synchronize()
+    b.close()
+
+
+def _graph_conv(orc, io, shape, co, k, up, bias=True, seed=SEED + 320):
+    from graphkit import Graph
+    g = Graph()
+    x = orc.randn(seed, shape)
+    w = orc.randn(seed + 1, (co, shape[1], k, k), std=0.05)
+    b = orc.randn(seed + 2, (co,), std=0.1)
+    X = g.leaf(dev_tensor(x, io))
+    Wt = g.leaf(dev_tensor(w, torch.float32))
+    u = g.upscale(X, up) if up else X
+    c = g.conv_2d_direct(Wt, u, p0=(k - 1) // 2, p1=(k - 1) // 2)
+    y = g.add(c, g.reshape(g.leaf(dev_tensor(b, torch.float32)), [1, 1, co, 1])) if bias else c
+    return g, (x, w, b), u, c, y
+
+
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,co,k,up", [((1, 24, 9, 20), 40, 3, 2), ((2, 16, 7, 5), 8, 1, 2),
+                                           ((1, 64, 16, 24), 128, 3, None)])
+def test_graph_conv2d_bias_upscale(orc, be, shape, co, k, up, io):
+    """Conv2d::forward's CONV_2D_DIRECT + bias ADD, behind Upsample2D's
+    nearest 2x UPSCALE: one convolution (weights packed, channel-last copy for
+    3x3, conv) with the bias and the upsample folded in."""
+    print(f"graph conv x={shape} co={co} k={k} up={up} {io}", flush=True)
+    g, (x, w, b), u, c, y = _graph_conv(orc, io, shape, co, k, up)
+    kernels, fused = g.compute(be, outputs=[y])
+    torch.cuda.synchronize()
+    assert fused == (2 if up else 1) and kernels == (3 if k == 3 else 2), (kernels, fused)
+    ref = orc.conv2d(orc.round_bf16(as_input(x, io)), orc.round_bf16(w), b, up2=bool(up))
+    check(host(y.torch()), ref, io, f"graph conv {shape}")
+
+
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+def test_graph_upscale_kept_and_factor_3(orc, be, io):
+    """An UPSCALE that is itself an output runs the nearest-neighbour kernel
+    (bit-exact repeat); the conv then reads it like any input.  Factor 3 is
+    never folded into the conv."""
+    for f in (2, 3):
+        g, (x, w, b), u, c, y = _graph_conv(orc, io, (1, 16, 5, 7), 24, 3, f, seed=SEED + 330)
+        kernels, fused = g.compute(be, outputs=[y, u])
+        torch.cuda.synchronize()
+        assert fused == 1 and kernels == 4, (f, kernels, fused)
+        xs = as_input(x, io)
+        up = np.repeat(np.repeat(xs, f, axis=2), f, axis=3)
+        assert np.array_equal(host(u.torch()), up), f"upscale x{f}"
+        ref = orc.conv2d(orc.round_bf16(up), orc.round_bf16(w), b)
+        check(host(y.torch()), ref, io, f"conv after upscale x{f}")
+
+
+def test_graph_conv_then_groupnorm_silu(orc, be):
+    """A decoder resnet step: conv (+bias) -> GroupNorm(32) + SiLU; the conv
+    output stays a real tensor between the two fused launches."""
+    from graphkit import Graph
+    io, N, Ci, Co, H, W, G = torch.bfloat16, 1, 32, 64, 12, 16, 32
+    g, (x, w, b), u, c, y = _graph_conv(orc, io, (N, Ci, H, W), Co, 3, None, seed=SEED + 340)
+    gw = orc.randn(SEED + 345, (Co,), mean=1.0, std=0.1)
+    gb = orc.randn(SEED + 346, (Co,), std=0.1)
+    v = g.reshape(y, [Co // G * H * W, G, N])
+    r = g.reshape(g.norm(v, 1e-6), [W, H, Co, N])
+    a = g.add(g.mul(r, g.leaf(dev_tensor(gw.reshape(1, Co, 1, 1), torch.float32))),
+              g.leaf(dev_tensor(gb.reshape(1, Co, 1, 1), torch.float32)))
+    out = g.mul(a, g.sigmoid(a))
+    kernels, fused = g.compute(be, outputs=[out])
+    torch.cuda.synchronize()
+    assert kernels == 3 + 2, kernels
+    conv_out = host(y.torch())
+    check(conv_out, orc.conv2d(orc.round_bf16(x), orc.round_bf16(w), b), io, "conv")
+    check(host(out.torch()), orc.groupnorm_silu(conv_out, G, gw, gb, 1e-6), io, "GroupNorm+SiLU after conv")
+
+
+def test_graph_conv_rejects_stride_2(dev, be):
+    from graphkit import Graph
+    import dit_hip as dh
+    g = Graph()
+    X = g.leaf(torch.zeros((1, 4, 8, 8), dtype=torch.float32, device="cuda"))
+    Wt = g.leaf(torch.zeros((4, 4, 3, 3), dtype=torch.float32, device="cuda"))
+    y = g.conv_2d_direct(Wt, X, s0=2, s1=2)
+    with pytest.raises(dh.DtError, match="stride 2,2"):
+        g.compute(be, outputs=[y])

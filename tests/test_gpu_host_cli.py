@@ -241,6 +241,62 @@ def test_double_stream_qk(orc, cli):
     assert st["kernels"] == 4 + 2, st      # 4 position CONTs + one fused launch per segment
 
 
+# ---- VAE decoder convolutions (test/src/nn/modules/conv/Conv2d.py,
+# test/src/diffusers/models/resnet/Upsample2D.py) -------------------------------
+# The conv multiplies bf16-rounded operands (fp32 accumulation), so the
+# oracle runs on the rounded input and weights.
+
+@pytest.mark.parametrize("x_shape,ci,co,k,pad,bias", [((1, 3, 8, 8), 3, 4, 3, 1, True),
+                                                     ((1, 4, 5, 5), 4, 2, 1, 0, False),
+                                                     ((2, 64, 20, 24), 64, 96, 3, 1, True)])
+def test_conv2d(orc, cli, x_shape, ci, co, k, pad, bias):
+    x = orc.randn(SEED + 40, x_shape)
+    w = orc.randn(SEED + 41, (co, ci, k, k), std=0.2)
+    b = orc.randn(SEED + 42, (co,), std=0.1)
+    xp, xv = cli.act(x)
+    args = ["--in_channels", ci, "--out_channels", co, "--kernel_size", k, "--stride", 1, "--padding", pad,
+            "--bias", str(bias).lower(), "--x", xp, "--param-weight", cli.f32(w), "--out", cli.out()]
+    if bias:
+        args += ["--param-bias", cli.f32(b)]
+    st = cli.run("Conv2d", *args)
+    want = orc.conv2d(orc.round_bf16(xv), orc.round_bf16(w), b if bias else None)
+    check(read_dtb(cli.out()), want, cli.bf16, "Conv2d")
+    assert st["fused_nodes"] == (1 if bias else 0), st      # the bias ADD folds into the conv
+    assert st["kernels"] == (3 if k == 3 else 2), st         # pack, channel-last copy (3x3), conv
+
+
+def test_conv2d_stride_2_is_reported(orc, cli):
+    """Conv2d.py test_stride2: strided convolutions (the VAE encoder's
+    downsampling) are outside the decoder path and fail with a message."""
+    xp, _ = cli.act(orc.randn(SEED + 43, (2, 3, 16, 16)))
+    r = subprocess.run([CLI, "Conv2d", "--in_channels", "3", "--out_channels", "5", "--kernel_size", "3",
+                        "--stride", "2", "--padding", "1", "--x", xp, "--param-weight",
+                        cli.f32(np.zeros((5, 3, 3, 3))), "--param-bias", cli.f32(np.zeros(5)), "--out",
+                        cli.out()], capture_output=True, text=True, timeout=60)
+    assert r.returncode != 0 and "stride and dilation 1 only" in r.stderr, r.stderr
+
+
+@pytest.mark.parametrize("use_conv,shape", [(False, (1, 4, 4, 4)), (True, (1, 4, 4, 4)), (True, (1, 128, 24, 20))])
+def test_upsample2d(orc, cli, use_conv, shape):
+    C = shape[1]
+    x = orc.randn(SEED + 44, shape)
+    w = orc.randn(SEED + 45, (C, C, 3, 3), std=0.05)
+    b = orc.randn(SEED + 46, (C,), std=0.1)
+    xp, xv = cli.act(x)
+    args = ["--channels", C, "--use_conv", str(use_conv).lower(), "--hidden_states", xp, "--out", cli.out()]
+    if use_conv:
+        args += ["--param-conv.weight", cli.f32(w), "--param-conv.bias", cli.f32(b)]
+    st = cli.run("Upsample2D", *args)
+    got = read_dtb(cli.out())
+    if not use_conv:
+        assert np.array_equal(got, np.repeat(np.repeat(xv, 2, axis=2), 2, axis=3))
+        assert st["kernels"] == 1, st
+        return
+    want = orc.conv2d(orc.round_bf16(xv), orc.round_bf16(w), b, up2=True)
+    check(got, want, cli.bf16, "Upsample2D")
+    assert st["fused_nodes"] == 2 and st["kernels"] == 3, st  # upscale + conv folded under the bias ADD
+
+
 def test_cli_rejects_bad_input(dev):
     with tempfile.TemporaryDirectory() as d:
         r = subprocess.run([CLI, "NoSuchCommand"], capture_output=True, text=True, timeout=60)
