@@ -17,9 +17,17 @@ all, far above the 256 MB last-level cache), so every step reads its inputs
 from HBM.  Three schedules of the same step are timed: eager launches, a
 HIP graph of the two launches, and a HIP graph with the two launches on
 parallel branches; `value` = whole-step algorithmic GB/s of the fastest
-(all three are reported).  The same block order with the four standalone
-kernels (gated residual, adaLN of r, QK, SwiGLU) is timed as a graph for
-comparison.  `roofline` is the dominant launch (QK+SwiGLU) timed alone
+(all three are reported).  Each schedule is timed after at least --warmup
+untimed steps of itself and at least 0.2 s of them, so the clocks have
+settled (`warmup_steps_run` reports how many ran).  The same block order
+with the four standalone kernels (gated residual, adaLN of r, QK, SwiGLU)
+is timed as a graph for comparison.
+
+`stream_probe_*` is the streaming ceiling the chain is set beside: trivial
+launches with the two fused launches' exact access shapes on the same
+buffers (16-byte non-temporal loads and stores), timed the same ways;
+`frac_of_stream_probe` = probe time / chain time (per step, and per launch
+under `kernels`).  `roofline` is the dominant launch (QK+SwiGLU) timed alone
 with HIP events on the stream it is launched on; `cpu_baseline` is the
 oracle's C restatement of the same chain (fp32, OpenMP) on a bounded
 sample, timed on this host's cores.
@@ -47,6 +55,7 @@ PKG = os.path.join(ROOT, "diffusers-cpp_amd")
 sys.path.insert(0, PKG)
 
 HBM_PEAK_GBS = 8000.0
+MIN_WARM_S = 0.2  # least untimed load before each timed schedule
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16
 NSETS = 4
 S, D, H, HD, I = 4608, 3072, 24, 128, 9216
@@ -153,6 +162,42 @@ def time_cold(torch, fn, n, flush):
         b.record(st)
     torch.cuda.synchronize()
     return statistics.median(a.elapsed_time(b) for a, b in ev) * 1e-3
+
+
+def probe_kernels(t):
+    """Trivial-math launches with the two fused launches' access shapes on
+    the same buffers (diffusers-cpp_amd/probe/stream_probe.hip): h, o -> r, y;
+    then q, k -> q', k' plus the two 85 MB halves of gate|up -> the SwiGLU
+    output.  Each stream is read or written once with 16-byte non-temporal
+    accesses, as in the kernels."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(PKG, "lib", "libdit_probe.so"))
+    fn = lib.dt_stream_probe
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+                   ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p]
+    gu, half = t["gu"], t["gu"].numel() // 2
+
+    def launch(ins, outs, ns):
+        a_in = (ctypes.c_void_p * 4)(*ins)
+        a_out = (ctypes.c_void_p * 4)(*outs)
+        a_n = (ctypes.c_int64 * 2)(*ns)
+
+        def run():
+            import torch
+            rc = fn(a_in, a_out, a_n, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc:
+                raise RuntimeError(f"dt_stream_probe failed ({rc})")
+        return run
+
+    p = lambda x: x.data_ptr()
+    v = lambda x: x.numel() * x.element_size() // 16
+    return {
+        "residual_adaln": launch([p(t["h"]), p(t["o"]), None, None], [p(t["r"]), p(t["y"]), None, None],
+                                 [v(t["h"]), 0]),
+        "qk_swiglu": launch([p(t["q"]), p(t["k"]), p(gu), p(gu) + half * gu.element_size()],
+                            [p(t["qo"]), p(t["ko"]), p(t["sw"]), None], [v(t["q"]), half * gu.element_size() // 16]),
+    }
 
 
 def copy_ceiling(torch, dev, flush):
@@ -350,8 +395,8 @@ def denoise_step(steps, warmup, weight_format="bf16"):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU-baseline sampling (0 disables)")
     ap.add_argument("--no-secondary", dest="secondary", action="store_false",
@@ -393,9 +438,20 @@ def main():
         for f in chains[i % NSETS].values():
             f()
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
+    def warm(run_step):
+        """--warmup untimed steps, continued until at least MIN_WARM_S of
+        them have run: the GPU's clocks take tens of milliseconds of load to
+        settle, and a short warm-up times the ramp instead of the kernels."""
+        torch.cuda.synchronize()
+        t0, n = time.perf_counter(), 0
+        while n < args.warmup or time.perf_counter() - t0 < MIN_WARM_S:
+            for _ in range(max(args.warmup, 50)):
+                run_step(n)
+                n += 1
+            torch.cuda.synchronize()
+        return n
+
+    warm_steps = {"eager": warm(step)}
     st = torch.cuda.current_stream()
 
     def timed(run_step):
@@ -426,12 +482,11 @@ def main():
             with torch.cuda.graph(g):
                 fn(i)
             out.append(g)
-        for i in range(args.warmup):
-            out[i % NSETS].replay()
         return out
 
     # The step's two launches captured back to back.
     graphs = capture(step)
+    warm_steps["graph"] = warm(lambda i: graphs[i % NSETS].replay())
     seq_s, seq_wall = timed(lambda i: graphs[i % NSETS].replay())
 
     # The same step with the two (independent) launches on parallel branches.
@@ -447,11 +502,23 @@ def main():
         main.wait_stream(branch_stream)
 
     bgraphs = capture(branched)
+    warm_steps["graph_branched"] = warm(lambda i: bgraphs[i % NSETS].replay())
     br_s, br_wall = timed(lambda i: bgraphs[i % NSETS].replay())
     schedules = {"eager": eager_s, "graph": seq_s, "graph_branched": br_s}
     best = min(schedules, key=schedules.get)
     step_s = schedules[best]
     wall = {"eager": None, "graph": seq_wall, "graph_branched": br_wall}[best]
+
+    # The streaming ceiling: the probe launches with the chain's shapes, timed
+    # the same ways (eager steps over the rotating buffer sets; cold launches).
+    probes = [probe_kernels(t) for t in sets]
+
+    def probe_step(i):
+        for f in probes[i % NSETS].values():
+            f()
+
+    warm(probe_step)
+    probe_s, _ = timed(probe_step)
 
     # Block order with the four standalone kernels, as a graph, for comparison.
     singles = [standalone_kernels(t) for t in sets]
@@ -461,6 +528,7 @@ def main():
             f()
 
     ugraphs = capture(unfused)
+    warm(lambda i: ugraphs[i % NSETS].replay())
     unfused_s, _ = timed(lambda i: ugraphs[i % NSETS].replay())
     del graphs, bgraphs, ugraphs
 
@@ -478,6 +546,10 @@ def main():
         return res
 
     kernels = cold(chains[0], fused_ab)
+    probe_cold = {name: time_cold(torch, fn, 20, flush) for name, fn in probes[0].items()}
+    for name, k in kernels.items():
+        k["stream_probe_us"] = round(probe_cold[name] * 1e6, 2)
+        k["frac_of_stream_probe"] = round(probe_cold[name] * 1e6 / k["us"], 3)
     kernels_standalone = cold(singles[0], single_ab)
     ceiling = copy_ceiling(torch, dev, flush)
     extra = secondary(torch, dev, flush) if args.secondary else None
@@ -506,6 +578,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": warm_steps,
         "ms_per_step": round(step_s * 1e3, 4),
         "schedule": best,
         "schedules_ms_per_step": {k: round(v * 1e3, 4) for k, v in schedules.items()},
@@ -526,6 +599,9 @@ def main():
         "denoise_step": denoise,
         "denoise_step_q8_0_weights": denoise_q8,
         "copy_ceiling_GBs": round(ceiling, 1),
+        "stream_probe_ms_per_step": round(probe_s * 1e3, 4),
+        "stream_probe_GBs": round(total / probe_s / 1e9, 1),
+        "frac_of_stream_probe": round(probe_s / step_s, 4),
         "kernels": kernels,
         "kernels_standalone": kernels_standalone,
         "secondary": extra,
