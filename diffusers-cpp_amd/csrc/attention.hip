@@ -18,10 +18,15 @@
 // give each SIMD two waves, so one wave's softmax overlaps the other's
 // MFMAs.  Workgroups are ordered so that each XCD (8 per MI355X, one L2 each)
 // works through a contiguous range of (batch, head) slices.
+#include <math.h>
+
+#include <algorithm>
 #include <type_traits>
 
 #include "capi_util.hpp"
 #include "common.hpp"
+#include "kernels.hpp"
+#include "rope_angles.hpp"
 
 namespace dit {
 namespace {
@@ -44,7 +49,101 @@ struct AttnArgs {
     float scale_log2;                     // scale * log2(e)
 };
 
+// The Q prologue's operands: q before its QK-RMSNorm + RoPE, in up to two
+// token segments with their own norm weights (the txt | img concatenation of
+// Flux2Attention.hpp:93-116; one segment: split = seq_q), and the RoPE
+// positions of the joint sequence.
+struct AttnPro {
+    const uint16_t* q0;
+    const uint16_t* q1;
+    int64_t q0_bs, q0_ts, q0_hs, q1_bs, q1_ts, q1_hs;  // batch, token, head strides (elements)
+    const float* w0;
+    const float* w1;
+    int32_t split;       // queries [0, split) from q0, [split, seq_q) from q1 (token - split)
+    int32_t axis_dim, n_pos;
+    float theta_scale, eps;
+    const float* table;  // [n_pos][axis_dim] (cos, sin); NULL: angles on the device
+    RopeAxisPos pos;     // position of joint token t on axis a: pos.ptr[a][t * pos.stride[a]]
+};
+
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Position of token t on axis `axis`, through an unrolled select so the
+// kernel-argument arrays are never indexed dynamically.
+__device__ __forceinline__ int pro_position(const RopeAxisPos& pos, int axis, int t) {
+    const int32_t* p = pos.ptr[0];
+    int64_t st = pos.stride[0];
+#pragma unroll
+    for (int a = 1; a < kMaxRopeAxes; ++a)
+        if (axis == a) {
+            p = pos.ptr[a];
+            st = pos.stride[a];
+        }
+    return p[(int64_t)t * st];
+}
+
+// Query `qrow` of the wave with QK-RMSNorm + RoPE applied, written as bf16
+// to `row` (256 bytes of LDS): lane half g owns dims 16 c + 8 g + [0, 8) of
+// chunk c, as in the B operand it is read back into.  Every operation is
+// the QK kernel's (qk_rope.hip), in its order: per 8-dim chunk the sum of
+// squares, the 16 chunk sums added as its 16-lane DPP tree does (pairs,
+// quads, halves, whole), 1 / sqrt(ss / 128 + eps), (x * r) * w, the
+// rotation, one bf16 rounding -- so the q used here is bit-identical to the
+// stored output of dt_qk_rmsnorm_rope.  The chunk loop writes LDS rather than
+// registers, so it need not unroll and adds nothing to the main loop's
+// register budget; the second pass re-reads the chunks (cache hits).
+__device__ __forceinline__ void q_prologue(const AttnPro& pro, int b, int h, int qrow, int seq_q, int g,
+                                           uint8_t* row) {
+    const bool valid = qrow < seq_q;
+    const int seg = valid && qrow >= pro.split;
+    const int tok = seg ? qrow - pro.split : qrow;
+    const uint16_t* src = seg ? pro.q1 + b * pro.q1_bs + (int64_t)tok * pro.q1_ts + h * pro.q1_hs
+                              : pro.q0 + b * pro.q0_bs + (int64_t)tok * pro.q0_ts + h * pro.q0_hs;
+    float part[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        float v[8];
+        Io<bf16>::unpack(valid ? ld16(src + 16 * c + 8 * g) : make_uint4(0, 0, 0, 0), v);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+        part[c] = ss;
+    }
+    // Chunk 2 c + g is here, 2 c + (1 - g) in lane l ^ 32: their sum is the
+    // tree's first level whichever half holds which.
+    float s1[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s1[c] = part[c] + __shfl_xor(part[c], 32);
+    const float ss = ((s1[0] + s1[1]) + (s1[2] + s1[3])) + ((s1[4] + s1[5]) + (s1[6] + s1[7]));
+    const float r = 1.0f / sqrtf(ss / (float)D + pro.eps);
+    const float* w = seg ? pro.w1 : pro.w0;
+    for (int c = 0; c < 8; ++c) {
+        const int d0 = 16 * c + 8 * g;
+        uint4 out = make_uint4(0, 0, 0, 0);
+        if (valid) {
+            const int axis = d0 / pro.axis_dim, i0 = d0 - axis * pro.axis_dim;
+            float cs[8];
+            rope_angles<4>(pro_position(pro.pos, axis, qrow), i0, pro.table, pro.n_pos, pro.axis_dim,
+                           pro.theta_scale, cs);
+            float v[8], wv[8], o[8];
+            Io<bf16>::unpack(ld16(src + d0), v);
+            const float4 wa = *reinterpret_cast<const float4*>(w + d0);
+            const float4 wb = *reinterpret_cast<const float4*>(w + d0 + 4);
+            wv[0] = wa.x; wv[1] = wa.y; wv[2] = wa.z; wv[3] = wa.w;
+            wv[4] = wb.x; wv[5] = wb.y; wv[6] = wb.z; wv[7] = wb.w;
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const float x0 = mul_rn(mul_rn(v[2 * qd], r), wv[2 * qd]);
+                const float x1 = mul_rn(mul_rn(v[2 * qd + 1], r), wv[2 * qd + 1]);
+                const float cn = cs[2 * qd], sn = cs[2 * qd + 1];
+                o[2 * qd] = sub_rn(mul_rn(x0, cn), mul_rn(x1, sn));
+                o[2 * qd + 1] = add_rn(mul_rn(x0, sn), mul_rn(x1, cn));
+            }
+            out = Io<bf16>::pack(o);
+        }
+        *reinterpret_cast<uint4*>(row + 2 * d0) = out;
+    }
+}
 
 // ---- K/V by direct DMA, two workgroups per CU ---------------------------------
 // K and V tiles move global -> LDS by direct DMA (global_load_lds_dwordx4)
@@ -78,8 +177,8 @@ __device__ __forceinline__ uint2 read_tr16(const uint8_t* p) {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4_p)(p)));
 }
 
-template <typename TO>
-__global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
+template <typename TO, bool PRO>
+__global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a, AttnPro pro) {
     // [buffer][K | V][64 rows][256 B]
     __shared__ __attribute__((aligned(16))) uint8_t smem[2 * 2 * DTILE];
 
@@ -99,7 +198,17 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
     const uint16_t* Vp = a.v + b * a.vs[0] + h * a.vs[2];
 
     bf16x8_t qf[8];
-    {
+    if constexpr (PRO) {
+        // Staged through the (still idle) second K/V buffer: wave w's rows
+        // at [32 w, 32 w + 32) x 256 B; every wave has read its rows back
+        // before the barrier, and the buffer's first DMA comes after it.
+        uint8_t* row = smem + 2 * DTILE + (32 * wave + r) * DROW;
+        q_prologue(pro, b, h, q0 + r, a.seq_q, g, row);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qf[c] = *reinterpret_cast<const bf16x8_t*>(row + 2 * (16 * c + 8 * g));
+        __syncthreads();
+    } else {
         const int qrow = q0 + r;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -308,47 +417,166 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a) {
 }  // namespace
 }  // namespace dit
 
-extern "C" int dt_flash_attn_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
-                                  int64_t heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
-                                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
-                                  const int64_t* o_strides, float scale, int32_t o_type, dt_stream_t stream) {
-    DT_REQUIRE(head_dim == dit::D, "dt_flash_attn_bf16: head_dim %lld unsupported (128 only)", (long long)head_dim);
-    DT_REQUIRE(o_type == DT_TYPE_BF16 || o_type == DT_TYPE_F32, "dt_flash_attn_bf16: o_type %d unsupported", o_type);
-    DT_REQUIRE(batch >= 0 && heads >= 0 && seq_q >= 0 && seq_kv >= 0, "dt_flash_attn_bf16: negative size");
-    if (batch == 0 || heads == 0 || seq_q == 0) return DT_OK;
-    DT_REQUIRE(seq_kv > 0, "dt_flash_attn_bf16: seq_kv must be positive");
-    DT_REQUIRE(q && k && v && o && q_strides && k_strides && v_strides && o_strides,
-               "dt_flash_attn_bf16: null pointer");
+namespace dit {
+namespace {
+
+// Shared checks of k, v, o, the sizes and the strides; q and its strides are
+// checked only when given (the prologue takes its own).
+int attn_prepare(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
+                 int64_t seq_q, int64_t seq_kv, int64_t head_dim, const int64_t* q_strides,
+                 const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides, float scale,
+                 int32_t o_type, const char* who, AttnArgs* out) {
+    DT_REQUIRE(head_dim == D, "%s: head_dim %lld unsupported (128 only)", who, (long long)head_dim);
+    DT_REQUIRE(o_type == DT_TYPE_BF16 || o_type == DT_TYPE_F32, "%s: o_type %d unsupported", who, o_type);
+    DT_REQUIRE(batch >= 0 && heads >= 0 && seq_q >= 0 && seq_kv >= 0, "%s: negative size", who);
+    DT_REQUIRE(seq_kv > 0 || batch == 0 || heads == 0 || seq_q == 0, "%s: seq_kv must be positive", who);
+    DT_REQUIRE(k && v && o && k_strides && v_strides && o_strides && (!q || q_strides), "%s: null pointer", who);
     DT_REQUIRE(seq_q < (1ll << 30) && seq_kv < (1ll << 30) && heads < (1 << 20) && batch < (1 << 20),
-               "dt_flash_attn_bf16: size too large");
-    dit::AttnArgs a{};
+               "%s: size too large", who);
+    AttnArgs a{};
     a.q = (const uint16_t*)q;
     a.k = (const uint16_t*)k;
     a.v = (const uint16_t*)v;
     a.o = o;
     for (int i = 0; i < 3; ++i) {
-        a.qs[i] = q_strides[i];
+        a.qs[i] = q ? q_strides[i] : 0;
         a.ks[i] = k_strides[i];
         a.vs[i] = v_strides[i];
         a.os[i] = o_strides[i];
         DT_REQUIRE(a.qs[i] % 8 == 0 && a.ks[i] % 8 == 0 && a.vs[i] % 8 == 0 && a.os[i] % 4 == 0,
-                   "dt_flash_attn_bf16: strides must keep rows 16-byte aligned");
+                   "%s: strides must keep rows 16-byte aligned", who);
     }
-    DT_REQUIRE(dit::aligned16(q) && dit::aligned16(k) && dit::aligned16(v) && dit::aligned16(o),
-               "dt_flash_attn_bf16: pointers must be 16-byte aligned");
+    DT_REQUIRE((!q || aligned16(q)) && aligned16(k) && aligned16(v) && aligned16(o),
+               "%s: pointers must be 16-byte aligned", who);
     a.batch = (int32_t)batch;
     a.heads = (int32_t)heads;
     a.seq_q = (int32_t)seq_q;
     a.seq_kv = (int32_t)seq_kv;
-    a.q_blocks = (int32_t)((seq_q + dit::QB - 1) / dit::QB);
-    DT_REQUIRE(scale >= 0.f, "dt_flash_attn_bf16: scale must be >= 0 (got %g)", (double)scale);
+    a.q_blocks = (int32_t)((seq_q + QB - 1) / QB);
+    DT_REQUIRE(scale >= 0.f, "%s: scale must be >= 0 (got %g)", who, (double)scale);
     a.scale_log2 = scale * 1.4426950408889634f;
-    const int64_t nblocks = (int64_t)a.q_blocks * heads * batch;
-    DT_REQUIRE(nblocks < (1ll << 31), "dt_flash_attn_bf16: grid too large");
-    hipStream_t st = (hipStream_t)stream;
+    DT_REQUIRE((int64_t)a.q_blocks * heads * batch < (1ll << 31), "%s: grid too large", who);
+    *out = a;
+    return DT_OK;
+}
+
+template <bool PRO>
+int attn_launch(const AttnArgs& a, const AttnPro& pro, int32_t o_type, hipStream_t st, const char* who) {
+    const unsigned nblocks = (unsigned)((int64_t)a.q_blocks * a.heads * a.batch);
+    if (nblocks == 0) return DT_OK;
     if (o_type == DT_TYPE_F32)
-        hipLaunchKernelGGL((dit::flash_attn_dma_kernel<float>), dim3((unsigned)nblocks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((flash_attn_dma_kernel<float, PRO>), dim3(nblocks), dim3(256), 0, st, a, pro);
     else
-        hipLaunchKernelGGL((dit::flash_attn_dma_kernel<uint16_t>), dim3((unsigned)nblocks), dim3(256), 0, st, a);
-    return dit::check_launch("dt_flash_attn_bf16");
+        hipLaunchKernelGGL((flash_attn_dma_kernel<uint16_t, PRO>), dim3(nblocks), dim3(256), 0, st, a, pro);
+    return check_launch(who);
+}
+
+}  // namespace
+
+int flash_attn_qk_launch(const AttnQk& qk, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
+                         int64_t seq_q, int64_t seq_kv, const int64_t* k_strides, const int64_t* v_strides,
+                         const int64_t* o_strides, float scale, int32_t o_type, hipStream_t st) {
+    const char* who = "dt_flash_attn_qk_bf16";
+    AttnArgs a;
+    int rc = attn_prepare(nullptr, k, v, o, batch, heads, seq_q, seq_kv, D, nullptr, k_strides, v_strides,
+                          o_strides, scale, o_type, who, &a);
+    if (rc || a.q_blocks == 0 || heads == 0 || batch == 0) return rc;
+    DT_REQUIRE(qk.n_axes > 0 && qk.n_axes <= kMaxRopeAxes && qk.axis_dim > 0 && qk.axis_dim % 8 == 0 &&
+                   qk.n_axes * qk.axis_dim == D,
+               "%s: need n_axes <= %d, axis_dim %% 8 == 0 and n_axes * axis_dim == 128 (%d * %d)", who,
+               kMaxRopeAxes, qk.n_axes, qk.axis_dim);
+    DT_REQUIRE(qk.split >= 0, "%s: split < 0", who);
+    const bool two = qk.split < seq_q;
+    DT_REQUIRE(qk.q[0] && qk.w[0] && (!two || (qk.q[1] && qk.w[1])), "%s: null q or norm weight", who);
+    for (int sgi = 0; sgi < (two ? 2 : 1); ++sgi) {
+        DT_REQUIRE(aligned16(qk.q[sgi]) && aligned16(qk.w[sgi]), "%s: q / weights must be 16-byte aligned", who);
+        for (int i = 0; i < 3; ++i)
+            DT_REQUIRE(qk.qs[sgi][i] % 8 == 0, "%s: q strides must keep rows 16-byte aligned", who);
+    }
+    for (int ax = 0; ax < qk.n_axes; ++ax)
+        DT_REQUIRE(qk.pos.ptr[ax] != nullptr, "%s: null position pointer for axis %d", who, ax);
+    DT_REQUIRE(!qk.table || (aligned16(qk.table) && qk.n_pos >= 0), "%s: rope table must be 16-byte aligned", who);
+    AttnPro pro{};
+    pro.q0 = (const uint16_t*)qk.q[0];
+    pro.q0_bs = qk.qs[0][0];
+    pro.q0_ts = qk.qs[0][1];
+    pro.q0_hs = qk.qs[0][2];
+    pro.w0 = qk.w[0];
+    if (two) {
+        pro.q1 = (const uint16_t*)qk.q[1];
+        pro.q1_bs = qk.qs[1][0];
+        pro.q1_ts = qk.qs[1][1];
+        pro.q1_hs = qk.qs[1][2];
+        pro.w1 = qk.w[1];
+    }
+    pro.split = (int32_t)std::min<int64_t>(qk.split, seq_q);
+    pro.axis_dim = qk.axis_dim;
+    pro.n_pos = qk.table ? qk.n_pos : 0;
+    pro.theta_scale = powf(qk.freq_base, -2.0f / (float)qk.axis_dim);
+    pro.eps = qk.eps;
+    pro.table = qk.table;
+    pro.pos = qk.pos;
+    for (int ax = qk.n_axes; ax < kMaxRopeAxes; ++ax) {
+        pro.pos.ptr[ax] = qk.pos.ptr[0];
+        pro.pos.stride[ax] = qk.pos.stride[0];
+    }
+    a.q = pro.q0;
+    return attn_launch<true>(a, pro, o_type, st, who);
+}
+
+}  // namespace dit
+
+extern "C" int dt_flash_attn_bf16(const void* q, const void* k, const void* v, void* o, int64_t batch,
+                                  int64_t heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                                  const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                                  const int64_t* o_strides, float scale, int32_t o_type, dt_stream_t stream) {
+    using namespace dit;
+    const char* who = "dt_flash_attn_bf16";
+    DT_REQUIRE(head_dim == D, "%s: head_dim %lld unsupported (128 only)", who, (long long)head_dim);
+    if (batch == 0 || heads == 0 || seq_q == 0) return DT_OK;
+    DT_REQUIRE(q != nullptr, "%s: null pointer", who);
+    AttnArgs a;
+    int rc = attn_prepare(q, k, v, o, batch, heads, seq_q, seq_kv, head_dim, q_strides, k_strides, v_strides,
+                          o_strides, scale, o_type, who, &a);
+    if (rc) return rc;
+    return attn_launch<false>(a, AttnPro{}, o_type, (hipStream_t)stream, who);
+}
+
+extern "C" int dt_flash_attn_qk_bf16(const void* q0, const int64_t* q0_strides, const float* w0, const void* q1,
+                                     const int64_t* q1_strides, const float* w1, int64_t split, float eps,
+                                     const int32_t* pos, int64_t pos_stride, int32_t n_axes, int32_t axis_dim,
+                                     float freq_base, const float* rope_table, int32_t n_pos, const void* k,
+                                     const void* v, void* o, int64_t batch, int64_t heads, int64_t seq_q,
+                                     int64_t seq_kv, int64_t head_dim, const int64_t* k_strides,
+                                     const int64_t* v_strides, const int64_t* o_strides, float scale,
+                                     int32_t o_type, dt_stream_t stream) {
+    using namespace dit;
+    const char* who = "dt_flash_attn_qk_bf16";
+    DT_REQUIRE(head_dim == D, "%s: head_dim %lld unsupported (128 only)", who, (long long)head_dim);
+    if (batch == 0 || heads == 0 || seq_q == 0) return DT_OK;
+    DT_REQUIRE(q0_strides && (split >= seq_q || q1_strides), "%s: null q strides", who);
+    DT_REQUIRE(pos != nullptr && pos_stride >= n_axes && n_axes > 0 && n_axes <= kMaxRopeAxes,
+               "%s: bad positions (pos_stride %lld, n_axes %d)", who, (long long)pos_stride, n_axes);
+    AttnQk qk{};
+    qk.q[0] = q0;
+    qk.q[1] = q1;
+    qk.w[0] = w0;
+    qk.w[1] = w1;
+    for (int i = 0; i < 3; ++i) {
+        qk.qs[0][i] = q0_strides[i];
+        qk.qs[1][i] = split < seq_q ? q1_strides[i] : 0;
+    }
+    qk.split = split;
+    qk.eps = eps;
+    for (int ax = 0; ax < n_axes; ++ax) {
+        qk.pos.ptr[ax] = pos + ax;
+        qk.pos.stride[ax] = pos_stride;
+    }
+    qk.n_axes = n_axes;
+    qk.axis_dim = axis_dim;
+    qk.freq_base = freq_base;
+    qk.table = n_pos > 0 ? rope_table : nullptr;
+    qk.n_pos = n_pos;
+    return flash_attn_qk_launch(qk, k, v, o, batch, heads, seq_q, seq_kv, k_strides, v_strides, o_strides, scale,
+                                o_type, (hipStream_t)stream);
 }

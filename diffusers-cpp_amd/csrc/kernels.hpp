@@ -38,6 +38,32 @@ int qk_launch(const void* q, const void* k, void* q_out, void* k_out, const floa
               int n_axes, int axis_dim, float freq_base, const float* table, int n_pos, int32_t io,
               hipStream_t st);
 
+// The (cos, sin) table of dt_rope_table_fill's layout, [n_pos][axis_dim],
+// computed on the device by the same recurrence the QK kernels use when they
+// have no table: a kernel reading it gets the same bits as one computing the
+// angles itself.  axis_dim % 8 == 0.
+int rope_table_device(float* table, int n_pos, int axis_dim, float freq_base, hipStream_t st);
+
+// Attention whose q is taken before its QK-RMSNorm + RoPE (dt_flash_attn_qk_bf16):
+// q segment i covers queries [0, split) (i = 0) or [split, seq_q) (i = 1,
+// token - split), with strides qs[i] = {batch, token, head} and norm
+// weights w[i]; pos holds the joint sequence's positions per axis.
+struct AttnQk {
+    const void* q[2];
+    int64_t qs[2][3];
+    const float* w[2];
+    int64_t split;
+    float eps;
+    RopeAxisPos pos;
+    int n_axes, axis_dim;
+    float freq_base;
+    const float* table;
+    int n_pos;
+};
+int flash_attn_qk_launch(const AttnQk& qk, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
+                         int64_t seq_q, int64_t seq_kv, const int64_t* k_strides, const int64_t* v_strides,
+                         const int64_t* o_strides, float scale, int32_t o_type, hipStream_t st);
+
 // QK-RMSNorm+RoPE of q and k (qk_launch's arguments) and a SwiGLU over
 // gate/up rows -> y, in one launch when both take their fast paths.
 int qk_swiglu_launch(const void* q, const void* k, void* q_out, void* k_out, const float* wq, const float* wk,

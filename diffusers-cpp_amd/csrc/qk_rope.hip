@@ -18,6 +18,7 @@
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "rope_angles.hpp"
 #include "swiglu_body.hpp"
 
 namespace dit {
@@ -47,31 +48,6 @@ __device__ __forceinline__ void axis_pos(const QkShape& sh, int axis, const int3
         if (axis == a) {
             p = sh.pos.ptr[a];
             stride = sh.pos.stride[a];
-        }
-    }
-}
-
-// cos/sin of pairs [i0/2, i0/2 + NP) of an axis at position p.
-template <int NP>
-__device__ __forceinline__ void rope_angles(int p, int i0, const float* __restrict__ table,
-                                            int n_pos, int axis_dim, float theta_scale,
-                                            float* cs) {
-    if (table != nullptr && p >= 0 && p < n_pos) {
-        const float* t = table + (int64_t)p * axis_dim + i0;
-#pragma unroll
-        for (int e = 0; e < 2 * NP; e += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(t + e);
-            cs[e] = a.x; cs[e + 1] = a.y; cs[e + 2] = a.z; cs[e + 3] = a.w;
-        }
-    } else {
-        // Same fp32 recurrence as the table: theta_0 = p, theta *= scale.
-        float theta = (float)p;
-        for (int k = 0; k < i0 / 2; ++k) theta = mul_rn(theta, theta_scale);
-#pragma unroll
-        for (int q = 0; q < NP; ++q) {
-            cs[2 * q] = cosf(theta);
-            cs[2 * q + 1] = sinf(theta);
-            theta = mul_rn(theta, theta_scale);
         }
     }
 }
@@ -374,6 +350,34 @@ int qk_prepare(const void* q, const void* k, void* q_out, void* k_out, const flo
     *hk_out = hk;
     *sh_out = sh;
     return DT_OK;
+}
+
+namespace {
+
+// One thread per (position, 8-dim chunk): the chunk's four pairs by the
+// device recurrence, exactly as the QK kernels compute them without a table.
+__global__ __launch_bounds__(256) void rope_table_device_kernel(float* __restrict__ table, int n_pos, int axis_dim,
+                                                                float theta_scale) {
+    const int chunks = axis_dim / 8;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n_pos * chunks) return;
+    const int p = (int)(i / chunks), i0 = (int)(i % chunks) * 8;
+    float cs[8];
+    rope_angles<4>(p, i0, nullptr, 0, axis_dim, theta_scale, cs);
+    float* t = table + (int64_t)p * axis_dim + i0;
+    *reinterpret_cast<float4*>(t) = make_float4(cs[0], cs[1], cs[2], cs[3]);
+    *reinterpret_cast<float4*>(t + 4) = make_float4(cs[4], cs[5], cs[6], cs[7]);
+}
+
+}  // namespace
+
+int rope_table_device(float* table, int n_pos, int axis_dim, float freq_base, hipStream_t st) {
+    DT_REQUIRE(table && aligned16(table) && n_pos > 0 && axis_dim > 0 && axis_dim % 8 == 0,
+               "rope_table_device: bad arguments");
+    const int64_t n = (int64_t)n_pos * (axis_dim / 8);
+    hipLaunchKernelGGL(rope_table_device_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, table, n_pos,
+                       axis_dim, powf(freq_base, -2.0f / (float)axis_dim));
+    return check_launch("rope_table_device");
 }
 
 }  // namespace dit

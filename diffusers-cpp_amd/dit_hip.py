@@ -52,6 +52,7 @@ DtTensor._fields_ = [
 
 # Every exported symbol with (restype, argtypes).
 _S = c_void_p
+_I64P = POINTER(c_int64)
 _SIGS = {
     "dt_last_error": (c_char_p, []),
     "dt_version": (c_char_p, []),
@@ -106,6 +107,10 @@ _SIGS = {
     "dt_groupnorm_silu_from_stats": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                                c_void_p, c_float, c_int32, c_void_p, c_int32, _S]),
     "dt_op_upscale_nearest": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int32, c_void_p, c_int32, _S]),
+    "dt_flash_attn_qk_bf16": (c_int32, [c_void_p, _I64P, c_void_p, c_void_p, _I64P, c_void_p, c_int64, c_float,
+                                        c_void_p, c_int64, c_int32, c_int32, c_float, c_void_p, c_int32,
+                                        c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                        c_int64, _I64P, _I64P, _I64P, c_float, c_int32, _S]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
     "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
@@ -552,6 +557,30 @@ def flash_attn(q, k, v, scale=None, out=None, out_dtype=None):
     check(load().dt_flash_attn_bf16(_p(q), _p(k), _p(v), _p(out), B, H, Sq, Skv, D, st(q), st(k),
                                     st(v), st(out), scale, io_type(out), stream()),
           "dt_flash_attn_bf16")
+    return out
+
+
+def flash_attn_qk(q_segments, k, v, pos, axis_dim, freq_base, eps=1e-6, table=None, scale=None, out=None,
+                  out_dtype=None):
+    """flash_attn with q taken before its QK-RMSNorm + RoPE.  q_segments:
+    one or two (q, w) pairs, q bf16 [B, S_i, H, 128] (strides honoured), w
+    fp32 [128]; the segments are the query sequence in order (txt then img).
+    pos: int32 [sum S_i, n_axes] of the joint sequence."""
+    torch = _torch()
+    (q0, w0) = q_segments[0]
+    q1, w1 = q_segments[1] if len(q_segments) > 1 else (None, None)
+    B, S0, H, D = q0.shape
+    Sq = S0 + (q1.shape[1] if q1 is not None else 0)
+    Skv = k.shape[1]
+    if out is None:
+        out = torch.empty((B, Sq, H, D), dtype=out_dtype or torch.bfloat16, device=k.device)
+    st = lambda t: (c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+    scale = 1.0 / D ** 0.5 if scale is None else scale
+    n_pos = 0 if table is None else table.shape[0]
+    check(load().dt_flash_attn_qk_bf16(
+        _p(q0), st(q0), _p(w0), _p(q1), st(q1) if q1 is not None else None, _p(w1), S0 if q1 is not None else Sq,
+        eps, _p(pos), pos.stride(0), pos.shape[1], axis_dim, freq_base, _p(table), n_pos, _p(k), _p(v), _p(out),
+        B, H, Sq, Skv, D, st(k), st(v), st(out), scale, io_type(out), stream()), "dt_flash_attn_qk_bf16")
     return out
 
 

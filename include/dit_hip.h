@@ -347,6 +347,30 @@ int dt_flash_attn_bf16(const void *q, const void *k, const void *v, void *o, int
                        const int64_t *v_strides, const int64_t *o_strides, float scale,
                        int32_t o_type, dt_stream_t stream);
 
+/* dt_flash_attn_bf16 with q taken BEFORE its QK-RMSNorm + RoPE: the kernel
+ * applies dt_qk_rmsnorm_rope's transform (RMSNorm over the 128 dims with
+ * eps and the fp32 weights, then the n_axes x axis_dim NORMAL-mode
+ * rotations at the query's positions) to each query as it loads it, so the
+ * normalised q is never stored and read back -- the q half of
+ * Flux2Attention.hpp:93-122 / Flux2ParallelSelfAttention.hpp:181-194 folded
+ * into FlashAttentionOp::operator() (FlashAttentionOp.cpp:84-94).
+ * Queries [0, split) come from q0 (token t at q0 + b*q0_strides[0] +
+ * t*q0_strides[1] + h*q0_strides[2], weights w0), queries [split, seq_q)
+ * from q1 (token t - split, weights w1): the txt | img concatenation of the
+ * double-stream attention; split >= seq_q leaves q1 / q1_strides / w1 unused.
+ * pos, pos_stride, n_axes, axis_dim, freq_base, rope_table and n_pos are
+ * dt_qk_rmsnorm_rope's (positions of the joint sequence; axis_dim % 8 == 0).
+ * The result is bit-identical to dt_qk_rmsnorm_rope with the same table
+ * followed by dt_flash_attn_bf16. */
+int dt_flash_attn_qk_bf16(const void *q0, const int64_t *q0_strides, const float *w0,
+                          const void *q1, const int64_t *q1_strides, const float *w1, int64_t split,
+                          float eps, const int32_t *pos, int64_t pos_stride, int32_t n_axes,
+                          int32_t axis_dim, float freq_base, const float *rope_table, int32_t n_pos,
+                          const void *k, const void *v, void *o, int64_t batch, int64_t heads,
+                          int64_t seq_q, int64_t seq_kv, int64_t head_dim, const int64_t *k_strides,
+                          const int64_t *v_strides, const int64_t *o_strides, float scale,
+                          int32_t o_type, dt_stream_t stream);
+
 /* ======================================================================== */
 /* (iii) unfused ggml-op kernels on ggml-shaped descriptors                 */
 /* ======================================================================== */

@@ -310,3 +310,88 @@ def test_flash_attn_flux2_shape_sampled(orc, dev):
         ref = orc.attention(orc.round_bf16(q[0, rows, h:h + 1]), orc.round_bf16(k[0, :, h:h + 1]),
                             orc.round_bf16(v[0, :, h:h + 1]))
         assert_bf16(o[0, rows, h:h + 1], ref, f"attn 4608x24 head {h}")
+
+
+# ---------------------------------------------- attention with the QK prologue --
+# dt_flash_attn_qk_bf16 normalises and rotates q as it loads it.  Its q is
+# built from the same operations in the same order as dt_qk_rmsnorm_rope's
+# stored output, so the attention output is compared bit for bit with that
+# kernel followed by dt_flash_attn_bf16 (and with the oracle at the bf16 bar).
+from test_gpu_fused import flux_positions  # noqa: E402
+
+
+def _qk_then_attn(q_segs, k, v, pos, table, axis_dim=32, base=10000.0, eps=1e-6, out_dtype=torch.bfloat16):
+    B, _, H, D = q_segs[0][0].shape
+    Sq = sum(q.shape[1] for q, _ in q_segs)
+    qn = torch.empty((B, Sq, H, D), dtype=torch.bfloat16, device="cuda")
+    t0 = 0
+    for q, w in q_segs:
+        n = q.shape[1]
+        for b in range(B):
+            dit_hip.qk_rmsnorm_rope(q[b], None, w, None, pos[t0:t0 + n], axis_dim, base, eps, table=table,
+                                    q_out=qn[b, t0:t0 + n])
+        t0 += n
+    return dit_hip.flash_attn(qn, k, v, out_dtype=out_dtype), qn
+
+
+PRO_CASES = [  # (B, txt, img, Skv, H, table n_pos or None)
+    (1, 0, 300, 300, 3, 512), (2, 77, 223, 290, 2, 40), (1, 16, 48, 64, 1, None), (1, 5, 1, 129, 4, 512)]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,n_txt,n_img,Skv,H,n_pos", PRO_CASES)
+def test_flash_attn_qk_prologue_bit_exact(orc, dev, B, n_txt, n_img, Skv, H, n_pos, out_dtype):
+    """One segment or txt | img with their own norm weights; q as column
+    views of a wider projection; a table that covers every position, one
+    that covers only some (the rest computed on the device), or none."""
+    print(f"attn+qk B={B} txt={n_txt} img={n_img} Skv={Skv} H={H} n_pos={n_pos} {out_dtype}", flush=True)
+    Sq = n_txt + n_img
+    grid = max(1, int(np.ceil(np.sqrt(max(n_img, 1)))))
+    img = [[0, i // grid, i % grid, 0] for i in range(n_img)]
+    pos_np = np.array([[0, 0, 0, l] for l in range(n_txt)] + img, dtype=np.int32).reshape(Sq, 4)
+    pos = torch.from_numpy(np.ascontiguousarray(pos_np)).cuda()
+    table = dit_hip.rope_table(n_pos, 32, 10000.0) if n_pos else None
+    proj = dev_tensor(orc.randn(SEED + 240, (B, Sq, 2 * H * 128)), torch.bfloat16).view(B, Sq, 2, H, 128)
+    w_txt = dev_tensor(orc.randn(SEED + 241, (128,), mean=1.0, std=0.1), torch.float32)
+    w_img = dev_tensor(orc.randn(SEED + 242, (128,), mean=1.0, std=0.1), torch.float32)
+    segs = ([(proj[:, :n_txt, 1], w_txt)] if n_txt else []) + [(proj[:, n_txt:, 1], w_img)]
+    k = dev_tensor(orc.randn(SEED + 243, (B, Skv, H, 128)), torch.bfloat16)
+    v = dev_tensor(orc.randn(SEED + 244, (B, Skv, H, 128)), torch.bfloat16)
+    got = dit_hip.flash_attn_qk(segs, k, v, pos, 32, 10000.0, table=table, out_dtype=out_dtype)
+    want, qn = _qk_then_attn(segs, k, v, pos, table, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"max |d| {(got.float() - want.float()).abs().max().item():g}"
+    if B == 1 and n_txt and n_img:  # and against the oracle's QK + attention
+        x = host(proj)[0, :, 1]
+        qo = np.concatenate([orc.qk_rmsnorm_rope(x[:n_txt], host(w_txt), pos_np[:n_txt], 32, 10000.0, 1e-6),
+                             orc.qk_rmsnorm_rope(x[n_txt:], host(w_img), pos_np[n_txt:], 32, 10000.0, 1e-6)])
+        ref = orc.attention(orc.round_bf16(qo), orc.round_bf16(host(k)[0]), orc.round_bf16(host(v)[0]))
+        assert_bf16(host(got)[0], ref, "attn+qk vs oracle")
+
+
+def test_flash_attn_qk_prologue_flux2_shape(orc, dev):
+    """A single-stream block's attention at 1024^2: q [4608, 24, 128] taken
+    from the fused projection before its norm, 512 txt + 64x64 img positions,
+    theta 1e4, the host-built table: bit-identical to the two-kernel path."""
+    S, H = 4608, 24
+    pos_np = flux_positions(512, 64)
+    pos = torch.from_numpy(pos_np).cuda()
+    table = dit_hip.rope_table(512, 32, 10000.0)
+    q = dev_tensor(orc.randn(SEED + 245, (1, S, H, 128)), torch.bfloat16)
+    w = dev_tensor(orc.randn(SEED + 246, (128,), mean=1.0, std=0.02), torch.float32)
+    k = dev_tensor(orc.randn(SEED + 247, (1, S, H, 128)), torch.bfloat16)
+    v = dev_tensor(orc.randn(SEED + 248, (1, S, H, 128)), torch.bfloat16)
+    got = dit_hip.flash_attn_qk([(q, w)], k, v, pos, 32, 10000.0, table=table)
+    want, _ = _qk_then_attn([(q, w)], k, v, pos, table)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_flash_attn_qk_prologue_rejects(dev):
+    z = torch.zeros((1, 8, 1, 128), dtype=torch.bfloat16, device="cuda")
+    w = torch.ones(128, dtype=torch.float32, device="cuda")
+    pos = torch.zeros((8, 4), dtype=torch.int32, device="cuda")
+    with pytest.raises(dit_hip.DtError, match="axis_dim"):
+        dit_hip.flash_attn_qk([(z, w)], z, z, pos, 24, 10000.0)      # 4 x 24 != 128
+    with pytest.raises(dit_hip.DtError, match="axis_dim"):
+        dit_hip.flash_attn_qk([(z, w)], z, z, pos[:, :2], 36, 10000.0)  # axis_dim % 8 != 0
