@@ -61,6 +61,9 @@ struct dt_backend {
     hipStream_t stream;
     void* scratch;
     size_t scratch_bytes;
+    float* rope_table;  // (cos, sin) of positions [0, kBackendRopePositions), built on the device
+    int rope_axis_dim;
+    float rope_base;
 };
 
 extern "C" const char* dt_last_error(void) { return dit::g_last_error.c_str(); }
@@ -80,17 +83,18 @@ extern "C" int dt_backend_init(int32_t device_ordinal, dt_backend** out) {
     DT_REQUIRE(device_ordinal >= 0 && device_ordinal < n, "dt_backend_init: device %d of %d",
                device_ordinal, n);
     DT_HIP(hipSetDevice(device_ordinal), "dt_backend_init");
-    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0};
+    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f};
     *out = be;
     return DT_OK;
 }
 
 extern "C" int dt_backend_free(dt_backend* be) {
     if (!be) return DT_OK;
-    if (be->scratch) {
+    if (be->scratch || be->rope_table) {
         (void)hipSetDevice(be->device);
         (void)hipStreamSynchronize(be->stream);
-        (void)hipFree(be->scratch);
+        if (be->scratch) (void)hipFree(be->scratch);
+        if (be->rope_table) (void)hipFree(be->rope_table);
     }
     delete be;
     return DT_OK;
@@ -163,6 +167,28 @@ namespace dit {
 hipStream_t backend_stream(dt_backend* be) { return be ? be->stream : nullptr; }
 
 int backend_device(dt_backend* be) { return be ? be->device : 0; }
+
+int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out) {
+    DT_REQUIRE(be != nullptr && out != nullptr, "backend_rope_table: null argument");
+    if (!be->rope_table || be->rope_axis_dim != axis_dim || be->rope_base != freq_base) {
+        if (be->rope_table) {
+            DT_HIP(hipStreamSynchronize(be->stream), "backend_rope_table");
+            DT_HIP(hipFree(be->rope_table), "backend_rope_table");
+            be->rope_table = nullptr;
+        }
+        const size_t bytes = (size_t)kBackendRopePositions * axis_dim * sizeof(float);
+        const hipError_t e = hipMalloc(&be->rope_table, bytes);
+        if (e != hipSuccess) return fail(DT_ERR_OOM, "backend_rope_table(%zu): %s", bytes, hipGetErrorString(e));
+        int rc = rope_table_device(be->rope_table, kBackendRopePositions, axis_dim, freq_base, be->stream);
+        if (rc) return rc;
+        // Built once; later graphs may run on another stream.
+        DT_HIP(hipStreamSynchronize(be->stream), "backend_rope_table");
+        be->rope_axis_dim = axis_dim;
+        be->rope_base = freq_base;
+    }
+    *out = be->rope_table;
+    return DT_OK;
+}
 
 int backend_scratch(dt_backend* be, size_t bytes, void** out) {
     DT_REQUIRE(be != nullptr && out != nullptr, "backend_scratch: null argument");

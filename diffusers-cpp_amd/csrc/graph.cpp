@@ -32,7 +32,11 @@
 // places outputs accordingly.
 //
 // MUL_MAT and FLASH_ATTN_EXT (Linear.cpp:24, FlashAttentionOp.cpp:84-94) run
-// the bf16 MFMA kernels of gemm.hip and attention.hip.
+// the bf16 MFMA kernels of gemm.hip and attention.hip.  An attention whose q
+// is a QK-RMSNorm+RoPE chain used nowhere else takes that chain as its
+// prologue (dt_flash_attn_qk_bf16: q is normalised and rotated as it is
+// loaded, never stored); the block's k chain then joins its SwiGLU in one
+// launch.
 //
 // A chain is fused only when every interior node is consumed solely inside
 // the chain and is not flagged DT_FLAG_OUTPUT; everything else runs the
@@ -111,7 +115,7 @@ bool is_vec(const dt_tensor* t, int64_t n, int dim = 0) {
 
 enum Kind {
     K_NONE, K_ADALN, K_GATED, K_SWIGLU, K_GN, K_QK, K_SILU, K_GEMM_ADD, K_GEMM_GROUP, K_RES_ADALN, K_QK_SWIGLU,
-    K_CONV, K_DEFERRED
+    K_CONV, K_ATTN_QK, K_DEFERRED
 };
 
 struct QkSeg {
@@ -371,6 +375,42 @@ bool match_groupnorm(Graph& g, const dt_tensor* root, Plan& p) {
     p.in[3] = v;
     p.eps = fparam(n, 0);
     p.silu = silu;
+    return true;
+}
+
+// FLASH_ATTN_EXT whose q is VIEW(y) with y's token and head axes swapped
+// (the [B, S, H, D] -> ggml q layout of FlashAttentionOp.cpp:84-94) and y a
+// BF16 QK-RMSNorm+RoPE root (match_qk) used only there: the chain becomes
+// the attention's prologue.  One or two segments (txt | img, one eps),
+// head_dim 128, axis_dim % 8 == 0; otherwise nothing is claimed.
+bool match_qk(Graph& g, const dt_tensor* y, Plan& p);
+
+bool match_attn_qk(Graph& g, const dt_tensor* t, Plan& p) {
+    if (t->op != DT_OP_FLASH_ATTN_EXT || t->src[3] || t->type != DT_TYPE_BF16) return false;
+    const dt_tensor* qv = t->src[0];
+    if (!qv || qv->op != DT_OP_VIEW || !g.internal(qv) || view_offset(qv) != 0) return false;
+    const dt_tensor* y = qv->src[0];
+    if (!y || y->op != DT_OP_CONCAT || y->type != DT_TYPE_BF16 || !g.internal(y)) return false;
+    if (qv->ne[0] != 128 || y->ne[0] != 128 || qv->ne[1] != y->ne[2] || qv->ne[2] != y->ne[1] ||
+        qv->ne[3] != y->ne[3] || qv->nb[0] != 2 || qv->nb[1] != y->nb[2] || qv->nb[2] != y->nb[1])
+        return false;
+    const std::vector<char> claimed = g.claimed;
+    const std::vector<int> root = g.root;
+    Plan qp;
+    bool ok = match_qk(g, y, qp) && qp.segs.size() <= 2 && qp.axis_dim % 8 == 0 &&
+              (qp.segs.size() == 1 || qp.segs[0].eps == qp.segs[1].eps);
+    for (const QkSeg& sg : qp.segs)
+        ok = ok && sg.q->type == DT_TYPE_BF16 && sg.q->nb[1] % 16 == 0 && sg.q->nb[2] % 16 == 0;
+    if (!ok) {
+        g.claimed = claimed;
+        g.root = root;
+        return false;
+    }
+    g.claim(y);
+    g.claim(qv);
+    p = qp;
+    p.kind = K_ATTN_QK;
+    p.in[0] = qv;
     return true;
 }
 
@@ -686,6 +726,8 @@ void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
 // precede it (q and k of the same block) and inputs computed before the
 // first of them, the three run as one launch at the first QK's position
 // (dt_qk_rmsnorm_rope_swiglu).  The other two roots keep their outputs.
+// When the block's q went into its attention (K_ATTN_QK), the nearest QK
+// root (k) and the SwiGLU run as one launch at the QK's position.
 void merge_qk_swiglu(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
     auto ready_before = [&](const dt_tensor* t, int pos) {
         while (t && t->op == DT_OP_VIEW) t = t->src[0];
@@ -705,17 +747,35 @@ void merge_qk_swiglu(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plan
         int found = 0;
         for (int j = sidx - 1; j >= 0 && found < 2; --j)
             if (plans[j].kind == K_QK) qk[found++] = j;
-        if (found < 2) continue;
+        if (found == 0) continue;
+        const Plan& S = plans[sidx];
+        const dt_tensor* ys = nodes[sidx];
+        auto merge_one = [&]() {  // the nearest QK root alone with the SwiGLU
+            Plan& B = plans[qk[0]];
+            if (B.segs.size() != 1 || nodes[qk[0]]->type != ys->type || !ready_before(S.in[0], qk[0]) ||
+                !ready_before(S.in[1], qk[0]))
+                return;
+            B.kind = K_QK_SWIGLU;
+            B.kroot = nullptr;
+            B.sw[0] = S.in[0];
+            B.sw[1] = S.in[1];
+            B.sw[2] = ys;
+            move_to(sidx, qk[0]);
+        };
+        if (found < 2) {
+            merge_one();
+            continue;
+        }
         const int qa = qk[1], qb = qk[0];  // qa first in order
         Plan& A = plans[qa];
         Plan& B = plans[qb];
-        const Plan& S = plans[sidx];
         const dt_tensor* ya = nodes[qa];
         const dt_tensor* yb = nodes[qb];
-        const dt_tensor* ys = nodes[sidx];
         if (A.segs.size() != 1 || B.segs.size() != 1 || A.pos != B.pos || A.axis_dim != B.axis_dim ||
-            A.base != B.base || A.segs[0].eps != B.segs[0].eps || ya->type != yb->type || ys->type != ya->type)
+            A.base != B.base || A.segs[0].eps != B.segs[0].eps || ya->type != yb->type || ys->type != ya->type) {
+            merge_one();
             continue;
+        }
         const dt_tensor* qa_in = A.segs[0].q;
         const dt_tensor* qb_in = B.segs[0].q;
         bool same = true;
@@ -723,8 +783,10 @@ void merge_qk_swiglu(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plan
             same = same && qa_in->ne[d] == qb_in->ne[d] && qa_in->nb[d] == qb_in->nb[d] && ya->nb[d] == yb->nb[d] &&
                    ya->ne[d] == yb->ne[d];
         if (!same || !ready_before(qb_in, qa) || !ready_before(B.segs[0].w, qa) || !ready_before(S.in[0], qa) ||
-            !ready_before(S.in[1], qa))
+            !ready_before(S.in[1], qa)) {
+            merge_one();
             continue;
+        }
         A.kind = K_QK_SWIGLU;
         A.kseg = B.segs[0];
         A.kroot = yb;
@@ -799,6 +861,48 @@ int run_upscale(hipStream_t st, const dt_tensor* t) {
                    t->ne[3] == x->ne[3],
                "dt_graph_compute: UPSCALE shapes disagree");
     return dt_op_upscale_nearest(data_of(x), x->ne[3], x->ne[2], x->ne[1], x->ne[0], f, t->data, t->type, st);
+}
+
+// FLASH_ATTN_EXT t with its q chain as the prologue (match_attn_qk): the
+// segments' pre-norm q, norm weights and eps, the positions of the joint
+// sequence, and the backend's device-built RoPE table, whose entries are
+// the bits the QK kernels compute without a table.
+int run_attn_qk(dt_backend* be, const dt_tensor* t, const Plan& p) {
+    const dt_tensor *qv = p.in[0], *k = t->src[1], *v = t->src[2];
+    DT_REQUIRE(k && v && k->type == DT_TYPE_BF16 && v->type == DT_TYPE_BF16 && k->nb[0] == 2 && v->nb[0] == 2 &&
+                   t->nb[0] == elem_size(t->type),
+               "dt_graph_compute: FLASH_ATTN_EXT k / v must be BF16 with contiguous rows");
+    DT_REQUIRE(t->ne[0] == 128 && t->ne[1] == qv->ne[2] && t->ne[2] == qv->ne[1] && t->ne[3] == qv->ne[3] &&
+                   k->ne[1] == v->ne[1] && k->ne[2] == qv->ne[2] && v->ne[2] == qv->ne[2] && k->ne[3] == qv->ne[3] &&
+                   v->ne[3] == qv->ne[3] && k->ne[0] == 128 && v->ne[0] == 128,
+               "dt_graph_compute: FLASH_ATTN_EXT shapes disagree");
+    AttnQk qk{};
+    for (size_t i = 0; i < p.segs.size(); ++i) {
+        const dt_tensor* q = p.segs[i].q;
+        qk.q[i] = data_of(q);
+        qk.qs[i][0] = q->nb[3] / 2;
+        qk.qs[i][1] = q->nb[2] / 2;
+        qk.qs[i][2] = q->nb[1] / 2;
+        qk.w[i] = (const float*)data_of(p.segs[i].w);
+    }
+    qk.split = p.segs.size() == 2 ? p.segs[1].tok0 : qv->ne[1];
+    qk.eps = p.segs[0].eps;
+    qk.n_axes = (int)p.pos.size();
+    for (int a = 0; a < qk.n_axes; ++a) {
+        qk.pos.stride[a] = p.pos[a]->nb[0] / 4;
+        qk.pos.ptr[a] = (const int32_t*)data_of(p.pos[a]);
+    }
+    qk.axis_dim = p.axis_dim;
+    qk.freq_base = p.base;
+    int rc = backend_rope_table(be, p.axis_dim, p.base, &qk.table);
+    if (rc) return rc;
+    qk.n_pos = kBackendRopePositions;
+    const int64_t es = elem_size(t->type);
+    const int64_t ks[3] = {k->nb[3] / 2, k->nb[1] / 2, k->nb[2] / 2};
+    const int64_t vs[3] = {v->nb[3] / 2, v->nb[1] / 2, v->nb[2] / 2};
+    const int64_t os[3] = {t->nb[3] / es, t->nb[2] / es, t->nb[1] / es};
+    return flash_attn_qk_launch(qk, k->data, v->data, t->data, qv->ne[3], qv->ne[2], qv->ne[1], k->ne[1], ks, vs,
+                                os, fparam(t, 0), t->type, backend_stream(be));
 }
 
 int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
@@ -887,8 +991,10 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
             row_layout(p.sw[1], &rows, &us);
             row_layout(p.sw[2], &rows, &ys);
             ++g_kernels;
-            return qk_swiglu_launch(data_of(q), data_of(p.kseg.q), root->data, p.kroot->data,
-                                    (const float*)data_of(qs.w), (const float*)data_of(p.kseg.w), qs.tokens,
+            const bool two = p.kroot != nullptr;  // else the root alone (its block's q is in the attention)
+            return qk_swiglu_launch(data_of(q), two ? data_of(p.kseg.q) : nullptr, root->data,
+                                    two ? p.kroot->data : nullptr, (const float*)data_of(qs.w),
+                                    two ? (const float*)data_of(p.kseg.w) : nullptr, qs.tokens,
                                     q->ne[1], q->ne[0], q->nb[2] / es, q->nb[1] / es, root->nb[2] / es,
                                     root->nb[1] / es, qs.eps, ap, n_axes, p.axis_dim, p.base, nullptr, 0,
                                     data_of(p.sw[0]), gs, data_of(p.sw[1]), us, p.sw[2]->data, ys, rows,
@@ -908,6 +1014,9 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
         }
         case K_CONV:
             return run_conv(be, root, p.in[0], p.in[1], p.in[2], p.in[3], p.up2);
+        case K_ATTN_QK:
+            ++g_kernels;
+            return run_attn_qk(be, root, p);
         case K_DEFERRED:
             return DT_OK;  // ran in its group's launch
         default:
@@ -1008,7 +1117,8 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
         dt_tensor* t = nodes[i];
         Plan& p = plans[i];
         g.current_root = i;
-        if (match_qk(g, t, p) || match_groupnorm(g, t, p) || match_res_adaln(g, t, p) || match_adaln(g, t, p) ||
+        if (match_attn_qk(g, t, p) || match_qk(g, t, p) || match_groupnorm(g, t, p) || match_res_adaln(g, t, p) ||
+            match_adaln(g, t, p) ||
             match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p) ||
             match_gemm_add(g, t, p) || match_conv(g, t, p))
             continue;

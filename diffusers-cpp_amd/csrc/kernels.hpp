@@ -85,4 +85,9 @@ int backend_device(dt_backend* be);
 // Backend-owned scratch of at least `bytes` (grown on demand, freed with the backend).
 int backend_scratch(dt_backend* be, size_t bytes, void** out);
 
+// The backend's RoPE (cos, sin) table for positions [0, kBackendRopePositions)
+// of one axis_dim / freq_base (rope_table_device; rebuilt when they change).
+constexpr int kBackendRopePositions = 4096;
+int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out);
+
 }  // namespace dit

@@ -155,18 +155,19 @@ constexpr int kQkSwigluThreads = 512;  // the SwiGLU body's best workgroup
 // QK-RMSNorm+RoPE of q and k and the SwiGLU of the same block in one launch
 // (Flux2ParallelSelfAttention.hpp:55-93: all three read the outputs of the
 // block's input projections): blocks [0, qk_blocks) take q, the next
-// qk_blocks k, the rest stream the SwiGLU.  The bodies are the standalone
-// kernels', so the results are bit-identical to three separate launches.
+// qk_blocks k (when k is given: n_qk = 2 qk_blocks, else qk_blocks), the
+// rest stream the SwiGLU.  The bodies are the standalone kernels', so the
+// results are bit-identical to separate launches.
 template <typename T, int HPG>
 __global__ __launch_bounds__(kQkSwigluThreads) void qk_swiglu_kernel(QkHalf q, QkHalf k, QkShape sh,
                                                                      const float* __restrict__ table, int chunks,
-                                                                     int qk_blocks, SwigluArgs sw) {
+                                                                     int qk_blocks, int n_qk, SwigluArgs sw) {
     const int b = blockIdx.x;
-    if (b < 2 * qk_blocks)
+    if (b < n_qk)
         qk_rope128_body<T, HPG, kQkSwigluThreads>(b < qk_blocks ? q : k, sh, table, chunks,
                                                   b < qk_blocks ? b : b - qk_blocks);
     else
-        swiglu_body<T, kQkSwigluThreads>(sw, b - 2 * qk_blocks);
+        swiglu_body<T, kQkSwigluThreads>(sw, b - n_qk);
 }
 
 // Any head_dim / axis_dim (even) / stride: one thread per (token, head).
@@ -276,7 +277,7 @@ int run_qk_swiglu(const QkHalf& hq, const QkHalf& hk, const QkShape& sh, const f
     const int64_t nvec = cols / EPV, total = rows * nvec;
     const bool sw_vec = cols % EPV == 0 && gs % EPV == 0 && us % EPV == 0 && ys % EPV == 0 && aligned16(g) &&
                         aligned16(u) && aligned16(y) && total < (1ll << 31);
-    if (!sw_vec || !hq.x || !hk.x || sh.tokens == 0 || !qk_fast<T>(hq, hk, sh, table)) {
+    if (!sw_vec || !hq.x || sh.tokens == 0 || !qk_fast<T>(hq, hk, sh, table)) {
         // shapes the combined kernel does not take: the two launches it replaces
         int rc = run<T>(hq, hk, sh, table, st);
         if (rc) return rc;
@@ -285,11 +286,12 @@ int run_qk_swiglu(const QkHalf& hq, const QkHalf& hk, const QkShape& sh, const f
     constexpr int NT = kQkSwigluThreads, WAVES = NT / kWave;
     const int chunks = (sh.heads + 4 * kHPG - 1) / (4 * kHPG);
     const int64_t qk_blocks = ((int64_t)sh.tokens * chunks + WAVES - 1) / WAVES;
-    const int64_t blocks = 2 * qk_blocks + swiglu_blocks<T, NT>((uint32_t)total);
+    const int64_t n_qk = (hk.x ? 2 : 1) * qk_blocks;
+    const int64_t blocks = n_qk + swiglu_blocks<T, NT>((uint32_t)total);
     DT_REQUIRE(blocks < (1ll << 31), "dt_qk_rmsnorm_rope_swiglu: grid too large");
     const SwigluArgs sw{g, gs, u, us, y, ys, (uint32_t)total, make_fastdiv((uint32_t)(nvec ? nvec : 1))};
     hipLaunchKernelGGL((qk_swiglu_kernel<T, kHPG>), dim3((unsigned)blocks), dim3(NT), 0, st, hq, hk, sh, table,
-                       chunks, (int)qk_blocks, sw);
+                       chunks, (int)qk_blocks, (int)n_qk, sw);
     return check_launch("dt_qk_rmsnorm_rope_swiglu");
 }
 

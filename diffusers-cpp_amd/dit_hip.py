@@ -290,22 +290,28 @@ def qk_rmsnorm_rope(q, k, wq, wk, pos, axis_dim, freq_base, eps=1e-6, table=None
 
 def qk_rmsnorm_rope_swiglu(q, k, wq, wk, pos, axis_dim, freq_base, gate, up, eps=1e-6, table=None,
                            q_out=None, k_out=None, out=None):
-    """qk_rmsnorm_rope(q, k) and swiglu(gate, up) in one launch -> (q_out, k_out, y)."""
+    """qk_rmsnorm_rope(q, k) and swiglu(gate, up) in one launch -> (q_out,
+    k_out, y); q or k may be None (that half is skipped)."""
     torch = _torch()
-    tokens, heads, head_dim = q.shape
-    q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device) if q_out is None else q_out
-    k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device) if k_out is None else k_out
+    x = q if q is not None else k
+    tokens, heads, head_dim = x.shape
+    if q is not None and q_out is None:
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    if k is not None and k_out is None:
+        k_out = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    o = q_out if q is not None else k_out
     y = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device) if out is None else out
-    if q.stride() != k.stride() or q_out.stride() != k_out.stride():
-        raise DtError("q and k (and their outputs) must share strides")
+    for a, b in ((q, k), (q_out, k_out)):
+        if a is not None and b is not None and a.stride() != b.stride():
+            raise DtError("q and k (and their outputs) must share strides")
     rows, inner, gs = _rows(gate)
     us, ys = _rows(up)[2], _rows(y)[2]
     n_pos = 0 if table is None else table.shape[0]
     check(load().dt_qk_rmsnorm_rope_swiglu(
-        _p(q), _p(k), _p(q_out), _p(k_out), tokens, heads, head_dim, q.stride(0), q.stride(1),
-        q_out.stride(0), q_out.stride(1), _p(wq), _p(wk), eps, _p(pos), pos.stride(0), pos.shape[1],
+        _p(q), _p(k), _p(q_out), _p(k_out), tokens, heads, head_dim, x.stride(0), x.stride(1),
+        o.stride(0), o.stride(1), _p(wq), _p(wk), eps, _p(pos), pos.stride(0), pos.shape[1],
         axis_dim, freq_base, _p(table), n_pos, _p(gate), gs, _p(up), us, _p(y), ys, rows, inner,
-        io_type(q), stream()), "dt_qk_rmsnorm_rope_swiglu")
+        io_type(x), stream()), "dt_qk_rmsnorm_rope_swiglu")
     return q_out, k_out, y
 
 

@@ -138,9 +138,11 @@ int dt_gated_residual(const void *h, int64_t h_stride, const void *o, int64_t o_
 /* dt_qk_rmsnorm_rope (q and k) and dt_swiglu in one launch: the three
  * elementwise ops a Flux2 single-stream block applies to the outputs of its
  * input projections (Flux2ParallelSelfAttention.hpp:55-93), which are all
- * ready at once.  Arguments are those of the two functions; results are
- * bit-identical to calling them separately (which is what happens for
- * shapes the combined kernel does not take). */
+ * ready at once.  Arguments are those of the two functions (q or k may be
+ * NULL: with the block's q taken by dt_flash_attn_qk_bf16, k and the SwiGLU
+ * still share one launch); results are bit-identical to calling them
+ * separately (which is what happens for shapes the combined kernel does not
+ * take). */
 int dt_qk_rmsnorm_rope_swiglu(const void *q, const void *k, void *q_out, void *k_out, int64_t tokens,
                               int64_t heads, int64_t head_dim, int64_t in_tok_stride,
                               int64_t in_head_stride, int64_t out_tok_stride, int64_t out_head_stride,

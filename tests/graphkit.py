@@ -139,6 +139,16 @@ class Graph:
         oh = (x.ne[1] + 2 * p1 - d1 * (K - 1) - 1) // s1 + 1
         return self._new(dh.OP_CONV_2D_DIRECT, [ow, oh, w.ne[3], x.ne[3]], x.d.type, [w, x], [s0, s1, p0, p1, d0, d1])
 
+    def flash_attn_ext(self, q, k, v, scale):
+        """q ne {D, Sq, H, B}, k / v ne {D, Skv, H, B} -> ne {D, H, Sq, B}."""
+        ne = q.ne
+        return self._new(dh.OP_FLASH_ATTN_EXT, [ne[0], ne[2], ne[1], ne[3]], dh.BF16, [q, k, v], [fbits(scale)])
+
+    def permute_tokens_heads(self, x):
+        """View of x ne {D, A, B, C} as ne {D, B, A, C} (axes 1 and 2 swapped)."""
+        ne, nb = x.ne, list(x.d.nb)
+        return self.view(x, [ne[0], ne[2], ne[1], ne[3]], [nb[0], nb[2], nb[1], nb[3]], 0)
+
     def upscale(self, a, factor):
         ne = a.ne
         return self._new(dh.OP_UPSCALE, [ne[0] * factor, ne[1] * factor, ne[2], ne[3]], a.d.type, [a], [factor])

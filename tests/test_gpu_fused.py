@@ -205,6 +205,11 @@ def test_qk_rmsnorm_rope_swiglu(orc, dev, dtype, n_txt, grid, heads, head_dim, i
     torch.cuda.synchronize()
     assert torch.equal(qo, qs) and torch.equal(ko, ks), "fused q/k differ from the QK kernel"
     assert torch.equal(y, ys), "fused SwiGLU differs from the SwiGLU kernel"
+    # k alone with the SwiGLU (the block's q taken by its attention)
+    _, ko1, y1 = dit_hip.qk_rmsnorm_rope_swiglu(None, dk, None, dwk, pt, axis_dim, 10000.0,
+                                                dgu[:, :inner], dgu[:, inner:], 1e-6, table=tab)
+    torch.cuda.synchronize()
+    assert torch.equal(ko1, ks) and torch.equal(y1, ys), "k-only fused launch differs"
     check(host(qo), orc.qk_rmsnorm_rope(as_input(q, dtype), wq, pos, axis_dim, 10000.0, 1e-6), dtype, "q")
     check(host(ko), orc.qk_rmsnorm_rope(as_input(k, dtype), wk, pos, axis_dim, 10000.0, 1e-6), dtype, "k")
     g, u = as_input(gu[:, :inner], dtype), as_input(gu[:, inner:], dtype)

@@ -325,3 +325,43 @@ def test_graph_groupnorm_silu(orc, be, dtype, affine, silu):
                               1e-6, silu=silu)
     check(host(cur.torch()), want, dtype, "gn graph")
     assert kernels == 2, kernels          # stats + apply
+
+
+@pytest.mark.parametrize("segments", [1, 2])
+def test_graph_attention_takes_the_q_chain(orc, be, segments):
+    """FLASH_ATTN_EXT on the permuted QK-RMSNorm+RoPE root (one segment, or
+    txt | img with their own weights as in Flux2Attention.hpp:93-116): the
+    chain becomes the attention's prologue -- one launch instead of one per
+    segment plus the attention -- and the output is bit-identical to the
+    graph that keeps q (the root flagged as an output)."""
+    n_txt, n_img, H = (0, 200, 3) if segments == 1 else (24, 136, 2)
+    S = n_txt + n_img
+    pos = seq_positions(n_txt, n_img, 16)
+    raw = {"q": orc.randn(SEED + 60, (1, S, H, 128)), "k": orc.randn(SEED + 61, (1, S, H, 128)),
+           "v": orc.randn(SEED + 62, (1, S, H, 128)),
+           "w0": orc.randn(SEED + 63, (128,), mean=1.0, std=0.1), "w1": orc.randn(SEED + 64, (128,), mean=1.0, std=0.1)}
+    outs = []
+    for keep_q in (False, True):
+        g = Graph()
+        L = {k: g.leaf(dev_tensor(v, torch.float32 if k[0] == "w" else torch.bfloat16)) for k, v in raw.items()}
+        P = g.leaf(torch.from_numpy(pos).cuda())
+        if segments == 1:
+            y = emit_qk(g, L["q"], L["w0"], pos_columns(g, P, S), 32, 10000.0, 2)
+        else:
+            qt = g.leaf(dev_tensor(raw["q"][:, :n_txt], torch.bfloat16))
+            qi = g.leaf(dev_tensor(raw["q"][:, n_txt:], torch.bfloat16))
+            z = g.concat(g.mul(g.rms_norm(qt, 1e-6), L["w0"]), g.mul(g.rms_norm(qi, 1e-6), L["w1"]), 2)
+            y = emit_rope(g, z, pos_columns(g, P, S), 32, 10000.0, 2)
+        o = g.flash_attn_ext(g.permute_tokens_heads(y), g.permute_tokens_heads(L["k"]),
+                             g.permute_tokens_heads(L["v"]), 1.0 / 128 ** 0.5)
+        kernels, fused = g.compute(be, outputs=[o, y] if keep_q else [o])
+        torch.cuda.synchronize()
+        # 4 position CONTs + the attention (+ one QK launch per segment when q is kept)
+        assert kernels == 5 + (segments if keep_q else 0), (keep_q, kernels)
+        outs.append(o.torch().clone())
+    assert torch.equal(outs[0], outs[1])
+    x = as_input(raw["q"], torch.bfloat16)[0]
+    segs = [(0, n_txt, raw["w0"]), (n_txt, S, raw["w1"])] if segments == 2 else [(0, S, raw["w0"])]
+    qn = np.concatenate([orc.qk_rmsnorm_rope(x[a:b], w, pos[a:b], 32, 10000.0, 1e-6) for a, b, w in segs])
+    ref = orc.attention(orc.round_bf16(qn), as_input(raw["k"], torch.bfloat16)[0], as_input(raw["v"], torch.bfloat16)[0])
+    assert_bf16(host(outs[0]).reshape(S, H, 128), ref, "attention with the q chain")

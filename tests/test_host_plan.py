@@ -3,12 +3,13 @@ planned without a device (dit_cli --plan-only): graph size, the GEMM and
 attention node counts, the parameter count of the 4B-shaped configuration,
 and how many nodes each block type hands to fused kernels.
 
-Per single-stream block 30 nodes are absorbed: adaLN 2 (NORM, MUL), each of
-q and k 12 (RMS_NORM, MUL, 4 x (VIEW, ROPE), 2 inner CONCATs), SwiGLU 2
+Per single-stream block 32 nodes are absorbed: adaLN 2 (NORM, MUL), each of
+q and k 12 (RMS_NORM, MUL, 4 x (VIEW, ROPE), 2 inner CONCATs), q's root
+CONCAT and its permuted VIEW into the attention's prologue 2, SwiGLU 2
 (SIGMOID, MUL), gated residual 1 (MUL), GEMM accumulate 1 (MUL_MAT).  Per
-double-stream block 46: 4 adaLNs x 2, q and k 15 each (two RMS_NORM + MUL
-segments joined by the txt|img CONCAT, plus the RoPE tree), 2 SwiGLUs x 2,
-4 gated residuals x 1."""
+double-stream block 48: 4 adaLNs x 2, q and k 15 each (two RMS_NORM + MUL
+segments joined by the txt|img CONCAT, plus the RoPE tree), q's root and
+view 2, 2 SwiGLUs x 2, 4 gated residuals x 1."""
 import json
 import os
 import subprocess
@@ -49,13 +50,14 @@ def test_q8_0_weights_plan_like_bf16():
 
 
 @pytest.mark.parametrize("kind,layers,nodes,fused,mm,grouped,deferred", [
-    ("single", dict(num_layers=0), 58, 30, 7, 6, 1),
-    ("double", dict(num_single_layers=0), 110, 46, 14, 8, 4),
+    ("single", dict(num_layers=0), 58, 32, 7, 5, 1),
+    ("double", dict(num_single_layers=0), 110, 48, 14, 8, 4),
 ])
 def test_per_block_fusion(kind, layers, nodes, fused, mm, grouped, deferred):
     """A second block adds its nodes, fusions and GEMMs; `grouped` roots run
     in an earlier node's launch (single: k, v, gate, up with q's projection,
-    and k's QK-RMSNorm+RoPE and the SwiGLU with q's QK-RMSNorm+RoPE; double:
+    and the SwiGLU with k's QK-RMSNorm+RoPE, q's being the attention's
+    prologue; double:
     k, v and the three txt projections with q, up with gate on each stream,
     to_out with to_add_out), and `deferred` residuals are written by the next
     adaLN's fused kernel (one per block boundary: single 1; double 2 inside
