@@ -99,11 +99,25 @@ __device__ __forceinline__ void q_prologue(const AttnPro& pro, int b, int h, int
     const int tok = seg ? qrow - pro.split : qrow;
     const uint16_t* src = seg ? pro.q1 + b * pro.q1_bs + (int64_t)tok * pro.q1_ts + h * pro.q1_hs
                               : pro.q0 + b * pro.q0_bs + (int64_t)tok * pro.q0_ts + h * pro.q0_hs;
+    // Every independent load first: the positions (their table rows are the
+    // one dependent load), the 8 chunks of q.
+    int p[8];
+    bool hit = valid && pro.table != nullptr;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int d0 = 16 * c + 8 * g;
+        p[c] = valid ? pro_position(pro.pos, d0 / pro.axis_dim, qrow) : 0;
+    }
+    uint4 raw[8];
     float part[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) raw[c] = valid ? ld16(src + 16 * c + 8 * g) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) hit = hit && p[c] >= 0 && p[c] < pro.n_pos;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         float v[8];
-        Io<bf16>::unpack(valid ? ld16(src + 16 * c + 8 * g) : make_uint4(0, 0, 0, 0), v);
+        Io<bf16>::unpack(raw[c], v);
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
@@ -117,31 +131,48 @@ __device__ __forceinline__ void q_prologue(const AttnPro& pro, int b, int h, int
     const float ss = ((s1[0] + s1[1]) + (s1[2] + s1[3])) + ((s1[4] + s1[5]) + (s1[6] + s1[7]));
     const float r = 1.0f / sqrtf(ss / (float)D + pro.eps);
     const float* w = seg ? pro.w1 : pro.w0;
-    for (int c = 0; c < 8; ++c) {
+    auto emit = [&](int c, const float* v, const float* cs) {
         const int d0 = 16 * c + 8 * g;
-        uint4 out = make_uint4(0, 0, 0, 0);
-        if (valid) {
+        float wv[8], o[8];
+        const float4 wa = *reinterpret_cast<const float4*>(w + d0);
+        const float4 wb = *reinterpret_cast<const float4*>(w + d0 + 4);
+        wv[0] = wa.x; wv[1] = wa.y; wv[2] = wa.z; wv[3] = wa.w;
+        wv[4] = wb.x; wv[5] = wb.y; wv[6] = wb.z; wv[7] = wb.w;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const float x0 = mul_rn(mul_rn(v[2 * qd], r), wv[2 * qd]);
+            const float x1 = mul_rn(mul_rn(v[2 * qd + 1], r), wv[2 * qd + 1]);
+            const float cn = cs[2 * qd], sn = cs[2 * qd + 1];
+            o[2 * qd] = sub_rn(mul_rn(x0, cn), mul_rn(x1, sn));
+            o[2 * qd + 1] = add_rn(mul_rn(x0, sn), mul_rn(x1, cn));
+        }
+        *reinterpret_cast<uint4*>(row + 2 * d0) = Io<bf16>::pack(o);
+    };
+    if (hit) {  // every angle from the table: unrolled, its loads issued together
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int d0 = 16 * c + 8 * g;
+            const int i0 = d0 - (d0 / pro.axis_dim) * pro.axis_dim;
+            const float* t = pro.table + (int64_t)p[c] * pro.axis_dim + i0;  // rope_angles' table branch
+            const float4 ca = *reinterpret_cast<const float4*>(t), cb = *reinterpret_cast<const float4*>(t + 4);
+            const float cs[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+            float v[8];
+            Io<bf16>::unpack(raw[c], v);
+            emit(c, v, cs);
+        }
+    } else if (valid) {  // some angle off the table: the device recurrence
+        for (int c = 0; c < 8; ++c) {
+            const int d0 = 16 * c + 8 * g;
             const int axis = d0 / pro.axis_dim, i0 = d0 - axis * pro.axis_dim;
-            float cs[8];
+            float cs[8], v[8];
             rope_angles<4>(pro_position(pro.pos, axis, qrow), i0, pro.table, pro.n_pos, pro.axis_dim,
                            pro.theta_scale, cs);
-            float v[8], wv[8], o[8];
             Io<bf16>::unpack(ld16(src + d0), v);
-            const float4 wa = *reinterpret_cast<const float4*>(w + d0);
-            const float4 wb = *reinterpret_cast<const float4*>(w + d0 + 4);
-            wv[0] = wa.x; wv[1] = wa.y; wv[2] = wa.z; wv[3] = wa.w;
-            wv[4] = wb.x; wv[5] = wb.y; wv[6] = wb.z; wv[7] = wb.w;
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-                const float x0 = mul_rn(mul_rn(v[2 * qd], r), wv[2 * qd]);
-                const float x1 = mul_rn(mul_rn(v[2 * qd + 1], r), wv[2 * qd + 1]);
-                const float cn = cs[2 * qd], sn = cs[2 * qd + 1];
-                o[2 * qd] = sub_rn(mul_rn(x0, cn), mul_rn(x1, sn));
-                o[2 * qd + 1] = add_rn(mul_rn(x0, sn), mul_rn(x1, cn));
-            }
-            out = Io<bf16>::pack(o);
+            emit(c, v, cs);
         }
-        *reinterpret_cast<uint4*>(row + 2 * d0) = out;
+    } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<uint4*>(row + 2 * (16 * c + 8 * g)) = make_uint4(0, 0, 0, 0);
     }
 }
 
@@ -198,17 +229,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a, Attn
     const uint16_t* Vp = a.v + b * a.vs[0] + h * a.vs[2];
 
     bf16x8_t qf[8];
-    if constexpr (PRO) {
-        // Staged through the (still idle) second K/V buffer: wave w's rows
-        // at [32 w, 32 w + 32) x 256 B; every wave has read its rows back
-        // before the barrier, and the buffer's first DMA comes after it.
-        uint8_t* row = smem + 2 * DTILE + (32 * wave + r) * DROW;
-        q_prologue(pro, b, h, q0 + r, a.seq_q, g, row);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS
-#pragma unroll
-        for (int c = 0; c < 8; ++c) qf[c] = *reinterpret_cast<const bf16x8_t*>(row + 2 * (16 * c + 8 * g));
-        __syncthreads();
-    } else {
+    if constexpr (!PRO) {
         const int qrow = q0 + r;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
@@ -376,6 +397,18 @@ __global__ __launch_bounds__(256, 2) void flash_attn_dma_kernel(AttnArgs a, Attn
     // last tile, masked when seq_kv is not a multiple of the tile.
     const int nfull = a.seq_kv / DKB;
     issue(0, 0);
+    if constexpr (PRO) {
+        // q goes through the second K/V buffer, still idle while the first
+        // tile's DMA (above) is in flight: wave w's rows at [32 w, 32 w +
+        // 32) x 256 B.  Every wave has read its rows back before the
+        // barrier, and the buffer's first DMA comes after it.
+        uint8_t* row = smem + 2 * DTILE + (32 * wave + r) * DROW;
+        q_prologue(pro, b, h, q0 + r, a.seq_q, g, row);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's rows are in LDS
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qf[c] = *reinterpret_cast<const bf16x8_t*>(row + 2 * (16 * c + 8 * g));
+        __syncthreads();
+    }
     if (ntiles > 1) issue(DKB, 1);
     int t = 0;
     for (; t + 1 < nfull; t += 2) {
