@@ -3,6 +3,11 @@
 //
 // Work unit: one lane produces 8 consecutive outputs (one 16-byte bf16 store,
 // two for fp32), so a wave writes 1 KB of contiguous output per instruction.
+// Rows that are 16-byte aligned (every GGUF tensor; Q4_K always) are staged:
+// a workgroup copies its run of blocks into LDS with 16-byte streaming loads
+// (the 34-byte Q8_0 block has no wider alignment than 2 bytes, and the Q4_K
+// header is shared by 32 lanes), then decodes from LDS.  Otherwise each lane
+// gathers its block from global memory directly.
 //   Q8_0  block = {fp16 d; int8 qs[32]} (34 B): 4 lanes share a block, each
 //         reads d and 8 quant bytes (2-byte aligned -> four u16 loads).
 //         d*q is exact in fp32 (11-bit x 8-bit significands).
@@ -89,9 +94,196 @@ __global__ __launch_bounds__(256) void dequant_q4_K_kernel(const uint8_t* __rest
     store_out8<T>(dst + (int64_t)r * dst_stride + (int64_t)k * 8, v);
 }
 
+constexpr int kStageThreads = 256;
+constexpr int kQ8SegBlocks = kStageThreads / 4;   // 64 blocks = 2176 B = 136 x 16 B
+constexpr int kQ4SegBlocks = kStageThreads / 32;  // 8 super-blocks = 1152 B = 72 x 16 B
+
+// Q8_0, staged: workgroup (seg, row) decodes blocks [64 seg, 64 seg + 64) of
+// the row.  64 blocks start at a multiple of 2176 bytes, so with 16-byte
+// aligned rows the run starts aligned, and its rounded-up end stays inside
+// the row (row_bytes is a multiple of 16 and at least 34 * blocks).
+template <typename T>
+__global__ __launch_bounds__(kStageThreads) void dequant_q8_0_staged_kernel(const uint8_t* __restrict__ src,
+                                                                            int64_t row_bytes, T* __restrict__ dst,
+                                                                            int64_t dst_stride, int blocks_per_row,
+                                                                            int segs) {
+    __shared__ __attribute__((aligned(16))) uint4 stage[kQ8SegBlocks * 34 / 16];
+    const int row = blockIdx.x / segs, seg = blockIdx.x - row * segs, t = threadIdx.x;
+    const int b0 = seg * kQ8SegBlocks, nblk = min(kQ8SegBlocks, blocks_per_row - b0);
+    const uint8_t* base = src + (int64_t)row * row_bytes + (int64_t)b0 * 34;
+    if (t < (nblk * 34 + 15) / 16) stage[t] = ld_stream(base + 16 * t);
+    __syncthreads();
+    const int blk = t >> 2, part = t & 3;
+    if (blk >= nblk) return;
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(stage) + blk * 17;
+    const float d = f16_bits_to_f32(h[0]);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t two = h[1 + part * 4 + i];
+        v[2 * i] = mul_rn(d, (float)(int8_t)(two & 0xFF));
+        v[2 * i + 1] = mul_rn(d, (float)(int8_t)(two >> 8));
+    }
+    store_out8<T>(dst + (int64_t)row * dst_stride + (int64_t)(b0 + blk) * 32 + part * 8, v);
+}
+
+// Q4_K, staged: workgroup (seg, row) decodes super-blocks [8 seg, 8 seg + 8)
+// of the row (144 B each, 16-byte aligned), 32 lanes per super-block.
+template <typename T>
+__global__ __launch_bounds__(kStageThreads) void dequant_q4_K_staged_kernel(const uint8_t* __restrict__ src,
+                                                                            int64_t row_bytes, T* __restrict__ dst,
+                                                                            int64_t dst_stride, int blocks_per_row,
+                                                                            int segs) {
+    __shared__ __attribute__((aligned(16))) uint4 stage[kQ4SegBlocks * 9];
+    const int row = blockIdx.x / segs, seg = blockIdx.x - row * segs, t = threadIdx.x;
+    const int b0 = seg * kQ4SegBlocks, nblk = min(kQ4SegBlocks, blocks_per_row - b0);
+    const uint8_t* base = src + (int64_t)row * row_bytes + (int64_t)b0 * 144;
+    if (t < nblk * 9) stage[t] = ld_stream(base + 16 * t);
+    __syncthreads();
+    const int sb = t >> 5, k = t & 31;
+    if (sb >= nblk) return;
+    const uint32_t e0 = k * 8;                            // element offset in the super-block
+    const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
+    const uint8_t* b = reinterpret_cast<const uint8_t*>(stage) + sb * 144;
+    const uint4 hdr = *reinterpret_cast<const uint4*>(b);
+    const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
+    const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);
+    const uint32_t by = (hdr.y >> sh) & 0xFF, bz = (hdr.z >> sh) & 0xFF, bw = (hdr.w >> sh) & 0xFF;
+    uint32_t sc, m;
+    if (j < 4) {
+        sc = by & 63;
+        m = bz & 63;
+    } else {
+        sc = (bw & 0xF) | ((by >> 6) << 4);
+        m = (bw >> 4) | ((bz >> 6) << 4);
+    }
+    const float d1 = mul_rn(f16_bits_to_f32(hdr.x & 0xFFFF), (float)sc);
+    const float m1 = mul_rn(f16_bits_to_f32(hdr.x >> 16), (float)m);
+    const uint32_t shift = hi * 4;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[i] = sub_rn(mul_rn(d1, (float)((q8.x >> (8 * i + shift)) & 0xF)), m1);
+        v[4 + i] = sub_rn(mul_rn(d1, (float)((q8.y >> (8 * i + shift)) & 0xF)), m1);
+    }
+    store_out8<T>(dst + (int64_t)row * dst_stride + (int64_t)(b0 + sb) * 256 + e0, v);
+}
+
+// Dense tensors (rows packed back to back in the source and the output) are
+// one stream of blocks: workgroup i decodes blocks [SEG * i, SEG * i + SEG)
+// with SEG = kFlatUnroll x the staged kernels' run, so each workgroup keeps
+// 8.5 KB (Q8_0) / 4.5 KB (Q4_K) of loads in flight -- a run of one row per
+// workgroup leaves too little in flight per CU to cover HBM latency.  The
+// bytes past the last whole 16-byte vector of the tensor are copied in 2-byte
+// pieces, so nothing past the tensor is read.
+constexpr int kFlatUnroll = 4;
+
+template <typename T>
+__global__ __launch_bounds__(kStageThreads) void dequant_q8_0_flat_kernel(const uint8_t* __restrict__ src,
+                                                                          int64_t nblocks, T* __restrict__ dst) {
+    constexpr int SEG = kQ8SegBlocks * kFlatUnroll;
+    __shared__ __attribute__((aligned(16))) uint4 stage[SEG * 34 / 16];
+    const int t = threadIdx.x;
+    const int64_t b0 = (int64_t)blockIdx.x * SEG;
+    const int nblk = (int)min<int64_t>(SEG, nblocks - b0);
+    const uint8_t* base = src + b0 * 34;
+    const int bytes = nblk * 34, nvec = bytes >> 4;
+    for (int i = t; i < nvec; i += kStageThreads) stage[i] = ld_stream(base + 16 * i);
+    if (t < (bytes & 15) / 2)
+        reinterpret_cast<uint16_t*>(stage)[nvec * 8 + t] = reinterpret_cast<const uint16_t*>(base + 16 * nvec)[t];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kFlatUnroll; ++u) {
+        const int blk = u * kQ8SegBlocks + (t >> 2), part = t & 3;
+        if (blk < nblk) {
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(stage) + blk * 17;
+            const float d = f16_bits_to_f32(h[0]);
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t two = h[1 + part * 4 + i];
+                v[2 * i] = mul_rn(d, (float)(int8_t)(two & 0xFF));
+                v[2 * i + 1] = mul_rn(d, (float)(int8_t)(two >> 8));
+            }
+            store_out8<T>(dst + (b0 + blk) * 32 + part * 8, v);
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kStageThreads) void dequant_q4_K_flat_kernel(const uint8_t* __restrict__ src,
+                                                                          int64_t nblocks, T* __restrict__ dst) {
+    constexpr int SEG = kQ4SegBlocks * kFlatUnroll;
+    __shared__ __attribute__((aligned(16))) uint4 stage[SEG * 9];
+    const int t = threadIdx.x;
+    const int64_t b0 = (int64_t)blockIdx.x * SEG;
+    const int nblk = (int)min<int64_t>(SEG, nblocks - b0);
+    const uint8_t* base = src + b0 * 144;
+    for (int i = t; i < nblk * 9; i += kStageThreads) stage[i] = ld_stream(base + 16 * i);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kFlatUnroll; ++u) {
+        const int sb = u * kQ4SegBlocks + (t >> 5), k = t & 31;
+        if (sb < nblk) {
+            const uint32_t e0 = k * 8;
+            const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
+            const uint8_t* b = reinterpret_cast<const uint8_t*>(stage) + sb * 144;
+            const uint4 hdr = *reinterpret_cast<const uint4*>(b);
+            const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
+            const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);
+            const uint32_t by = (hdr.y >> sh) & 0xFF, bz = (hdr.z >> sh) & 0xFF, bw = (hdr.w >> sh) & 0xFF;
+            uint32_t sc, m;
+            if (j < 4) {
+                sc = by & 63;
+                m = bz & 63;
+            } else {
+                sc = (bw & 0xF) | ((by >> 6) << 4);
+                m = (bw >> 4) | ((bz >> 6) << 4);
+            }
+            const float d1 = mul_rn(f16_bits_to_f32(hdr.x & 0xFFFF), (float)sc);
+            const float m1 = mul_rn(f16_bits_to_f32(hdr.x >> 16), (float)m);
+            const uint32_t shift = hi * 4;
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[i] = sub_rn(mul_rn(d1, (float)((q8.x >> (8 * i + shift)) & 0xF)), m1);
+                v[4 + i] = sub_rn(mul_rn(d1, (float)((q8.y >> (8 * i + shift)) & 0xF)), m1);
+            }
+            store_out8<T>(dst + (b0 + sb) * 256 + e0, v);
+        }
+    }
+}
+
 template <typename T>
 int run(const void* src, int32_t qtype, int64_t rows, int64_t cols, int64_t row_bytes, void* dst,
         int64_t dst_stride, hipStream_t st) {
+    {
+        const bool q8 = qtype == DT_TYPE_Q8_0;
+        const int64_t qk = q8 ? 32 : 256, bsz = q8 ? 34 : 144;
+        const int64_t seg = (q8 ? kQ8SegBlocks : kQ4SegBlocks) * kFlatUnroll;
+        const int64_t nblocks = rows * (cols / qk), wgs = (nblocks + seg - 1) / seg;
+        if (aligned16(src) && row_bytes == cols / qk * bsz && dst_stride == cols && wgs < (1ll << 31)) {
+            if (q8)
+                hipLaunchKernelGGL((dequant_q8_0_flat_kernel<T>), dim3((unsigned)wgs), dim3(kStageThreads), 0, st,
+                                   (const uint8_t*)src, nblocks, (T*)dst);
+            else
+                hipLaunchKernelGGL((dequant_q4_K_flat_kernel<T>), dim3((unsigned)wgs), dim3(kStageThreads), 0, st,
+                                   (const uint8_t*)src, nblocks, (T*)dst);
+            return check_launch("dt_dequant");
+        }
+    }
+    const int64_t qk = qtype == DT_TYPE_Q8_0 ? 32 : 256, per = qtype == DT_TYPE_Q8_0 ? kQ8SegBlocks : kQ4SegBlocks;
+    const int64_t bpr = cols / qk, segs = (bpr + per - 1) / per;
+    if (aligned16(src) && row_bytes % 16 == 0 && rows * segs < (1ll << 31)) {
+        const dim3 grid((unsigned)(rows * segs));
+        if (qtype == DT_TYPE_Q8_0)
+            hipLaunchKernelGGL((dequant_q8_0_staged_kernel<T>), grid, dim3(kStageThreads), 0, st,
+                               (const uint8_t*)src, row_bytes, (T*)dst, dst_stride, (int)bpr, (int)segs);
+        else
+            hipLaunchKernelGGL((dequant_q4_K_staged_kernel<T>), grid, dim3(kStageThreads), 0, st,
+                               (const uint8_t*)src, row_bytes, (T*)dst, dst_stride, (int)bpr, (int)segs);
+        return check_launch("dt_dequant");
+    }
     const int64_t cpr = cols / 8, total = rows * cpr;
     DT_REQUIRE(total < (1ll << 31), "dt_dequant: %lld chunks exceed the 32-bit index range",
                (long long)total);

@@ -333,6 +333,35 @@ def test_dequant_bit_exact(orc, dev, qtype, rows, cols):
     assert np.array_equal(ybf.cpu().view(torch.int16).numpy().view(np.uint16), orc.to_bf16_bits(ref))
 
 
+@pytest.mark.parametrize("qtype", [dit_hip.Q8_0, dit_hip.Q4_K])
+def test_dequant_strided_output_rows(orc, dev, qtype):
+    """Output rows wider than the tensor (one row per workgroup run, not the
+    dense stream): same bits, and nothing written past each row."""
+    rows, cols = 33, 3072
+    blocks = orc.quantize(orc.randn(SEED + 39, (rows, cols), std=0.02), qtype)
+    ref = orc.dequantize(blocks, rows * cols, qtype).reshape(rows, cols)
+    y = torch.full((rows, cols + 64), 7.0, dtype=torch.float32, device="cuda")
+    dit_hip.dequant(torch.from_numpy(blocks).cuda(), qtype, rows, cols, out=y[:, :cols])
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.array_equal(got[:, :cols].view(np.uint32), ref.view(np.uint32))
+    assert (got[:, cols:] == 7.0).all()
+
+
+def test_dequant_q8_0_unaligned_rows(orc, dev):
+    """Rows of 3 blocks (102 bytes, not a multiple of 16) and a source at a
+    2-byte offset take the per-lane gather path: same bits."""
+    rows, cols = 37, 96
+    blocks = orc.quantize(orc.randn(SEED + 38, (rows, cols), std=0.02), dit_hip.Q8_0)
+    ref = orc.dequantize(blocks, rows * cols, dit_hip.Q8_0).reshape(rows, cols)
+    for off in (0, 2):
+        buf = torch.zeros(blocks.size + 16, dtype=torch.uint8, device="cuda")
+        buf[off:off + blocks.size] = torch.from_numpy(blocks).cuda()
+        y = dit_hip.dequant(buf[off:off + blocks.size], dit_hip.Q8_0, rows, cols, torch.float32)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), ref.view(np.uint32)), off
+
+
 def test_dequant_q8_0_exhaustive(orc, dev):
     # every fp16 scale pattern x every int8 code: 65536 blocks of 32 -> 8 blocks per d
     d = np.arange(65536, dtype=np.uint32).astype(np.uint16)
