@@ -37,9 +37,12 @@ sample, timed on this host's cores.
 128 features + 512 text tokens of width 2560, timestep 0.5) run by the C++
 driver (diffusers-cpp_amd/bin/dit_cli) as a child process: Q8_0 weights
 drawn N(0, 0.02) and dequantised once to bf16, bf16 activations, inputs and
-weights resident in HBM, median wall time per step of the recorded graph.
+weights resident in HBM, median wall time per step of the recorded graph,
+replayed as one HIP graph per step (host inputs uploaded before each).
 `denoise_step_q8_0_weights` is the same step with the Linear weights kept as
-Q8_0 (dequantised inside the GEMMs; same outputs bit for bit).
+Q8_0 (dequantised inside the GEMMs; same outputs bit for bit);
+`denoise_step_eager_launches` the bf16 step launched kernel by kernel after
+the fusion pass each step.
 
 Prints ONE JSON line.
 """
@@ -351,16 +354,20 @@ def denoise_flops(n_img=4096, n_txt=512, d=3072, mlp=9216, blocks=25, txt_width=
     return 2 * lin + blocks * 4 * s * s * d
 
 
-def denoise_step(steps, warmup, weight_format="bf16"):
+def denoise_step(steps, warmup, weight_format="bf16", hip_graph=True):
     """Run the full-step driver as a child process; None if it is missing.
     weight_format: what the GEMMs read, bf16 copies of the Q8_0 weights or
-    the Q8_0 weights themselves (dequantised inside the GEMM)."""
+    the Q8_0 weights themselves (dequantised inside the GEMM).  hip_graph:
+    the step's launches recorded once and replayed as one HIP graph (the
+    first warm-up step runs eagerly and records), else launched one by one
+    after the fusion pass every step."""
     import subprocess
     cli = os.path.join(PKG, "bin", "dit_cli")
     if not os.path.exists(cli):
         return None
     cmd = [cli, "Flux2Transformer2DModel", "--random-weights", "1", "--random-inputs", "2",
-           "--steps", str(steps), "--warmup", str(warmup), "--weight-format", weight_format]
+           "--steps", str(steps), "--warmup", str(warmup), "--weight-format", weight_format,
+           "--hip-graph", "true" if hip_graph else "false"]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         raise RuntimeError(f"dit_cli failed ({r.returncode}): {r.stderr.strip()[-500:]}")
@@ -376,6 +383,7 @@ def denoise_step(steps, warmup, weight_format="bf16"):
                     "Q8_0 (N(0,0.02) quantised on device) kept as Q8_0 (codes + fp32 scales, 1.125 B/weight), "
                     "dequantised inside the GEMM") + "; RMSNorm weights N(1,0.02)",
         "linear_weight_bytes": res["linear_weight_bytes"],
+        "launch": "one HIP graph replay per step" if hip_graph else "eager launches after the fusion pass",
         "s_per_step": round(t, 5),
         "ms_per_step_min": res["ms_per_step_min"],
         "ms_per_step_mean": res["ms_per_step_mean"],
@@ -423,6 +431,8 @@ def main():
 
     # The full step runs in its own process before this one touches the GPU.
     denoise = denoise_step(args.denoise_steps, args.denoise_warmup) if args.denoise_steps > 0 else None
+    denoise_eager = (denoise_step(args.denoise_steps, args.denoise_warmup, hip_graph=False)
+                     if args.denoise_steps > 0 and args.secondary else None)
     denoise_q8 = (denoise_step(args.denoise_steps, args.denoise_warmup, "q8_0")
                   if args.denoise_steps > 0 and args.secondary else None)
 
@@ -598,6 +608,7 @@ def main():
         "sec_per_denoise_step": denoise["s_per_step"] if denoise else None,
         "denoise_step": denoise,
         "denoise_step_q8_0_weights": denoise_q8,
+        "denoise_step_eager_launches": denoise_eager,
         "copy_ceiling_GBs": round(ceiling, 1),
         "stream_probe_ms_per_step": round(probe_s * 1e3, 4),
         "stream_probe_GBs": round(total / probe_s / 1e9, 1),

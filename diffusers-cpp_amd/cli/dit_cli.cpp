@@ -511,10 +511,15 @@ void run_model(Session& s, const Args& a) {
     if (!out.is_contiguous()) out = out.contiguous();
     rt.set_output(*out);
 
+    // --hip-graph true: the step is recorded once and replayed as a HIP graph.
+    const bool replay = a.flag("hip-graph", false);
     std::vector<double> ms;
     for (int i = 0; i < warmup + steps; ++i) {
         const auto t0 = std::chrono::steady_clock::now();
-        rt.compute();
+        if (replay)
+            rt.compute_graph();
+        else
+            rt.compute();
         const auto t1 = std::chrono::steady_clock::now();
         if (i >= warmup) ms.push_back(std::chrono::duration<double, std::milli>(t1 - t0).count());
     }
@@ -533,10 +538,10 @@ void run_model(Session& s, const Args& a) {
                 "\"ms_per_step_median\": %.4f, \"ms_per_step_mean\": %.4f, \"ms_per_step_min\": %.4f, "
                 "\"nodes\": %d, \"kernels\": %d, \"fused_nodes\": %d, \"arena_bytes\": %zu, "
                 "\"params\": %zu, \"weight_format\": \"%s\", \"linear_weight_bytes\": %zu, "
-                "\"q8_0_weight_bytes\": %zu%s}\n",
+                "\"q8_0_weight_bytes\": %zu, \"hip_graph\": %s%s}\n",
                 steps, warmup, sorted.empty() ? 0.0 : sorted[sorted.size() / 2], mean,
                 sorted.empty() ? 0.0 : sorted.front(), st.nodes, st.kernels, st.fused_nodes, st.arena_bytes,
-                n_params, format.c_str(), resident_bytes, q8_bytes, gguf_note.c_str());
+                n_params, format.c_str(), resident_bytes, q8_bytes, replay ? "true" : "false", gguf_note.c_str());
 }
 
 // GgufInfo --gguf PATH: the file's header, metadata and tensor table as one

@@ -64,6 +64,11 @@ struct dt_backend {
     float* rope_table;  // (cos, sin) of positions [0, kBackendRopePositions), built on the device
     int rope_axis_dim;
     float rope_base;
+    bool own_stream;    // created by dt_graph_capture
+};
+
+struct dt_graph_exec {
+    hipGraphExec_t exec;
 };
 
 extern "C" const char* dt_last_error(void) { return dit::g_last_error.c_str(); }
@@ -83,7 +88,7 @@ extern "C" int dt_backend_init(int32_t device_ordinal, dt_backend** out) {
     DT_REQUIRE(device_ordinal >= 0 && device_ordinal < n, "dt_backend_init: device %d of %d",
                device_ordinal, n);
     DT_HIP(hipSetDevice(device_ordinal), "dt_backend_init");
-    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f};
+    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f, false};
     *out = be;
     return DT_OK;
 }
@@ -95,6 +100,10 @@ extern "C" int dt_backend_free(dt_backend* be) {
         (void)hipStreamSynchronize(be->stream);
         if (be->scratch) (void)hipFree(be->scratch);
         if (be->rope_table) (void)hipFree(be->rope_table);
+    }
+    if (be->own_stream) {
+        (void)hipStreamSynchronize(be->stream);
+        (void)hipStreamDestroy(be->stream);
     }
     delete be;
     return DT_OK;
@@ -209,3 +218,46 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out) {
 }
 
 }  // namespace dit
+
+extern "C" int dt_graph_capture(dt_backend* be, dt_tensor** nodes, int32_t n_nodes, dt_graph_exec** out) {
+    DT_REQUIRE(be != nullptr && out != nullptr && n_nodes >= 0 && (nodes || n_nodes == 0),
+               "dt_graph_capture: bad arguments");
+    DT_HIP(hipSetDevice(be->device), "dt_graph_capture");
+    if (be->stream == nullptr) {  // the legacy NULL stream cannot be captured
+        hipStream_t s = nullptr;
+        DT_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "dt_graph_capture");
+        be->stream = s;
+        be->own_stream = true;
+    }
+    DT_HIP(hipStreamSynchronize(be->stream), "dt_graph_capture");
+    DT_HIP(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "dt_graph_capture");
+    const int rc = dt_graph_compute(be, nodes, n_nodes);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(be->stream, &graph);
+    if (rc) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess || !graph)
+        return dit::fail(DT_ERR_HIP, "dt_graph_capture: %s (run dt_graph_compute once before capturing)",
+                         hipGetErrorString(e));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) return dit::fail(DT_ERR_HIP, "dt_graph_capture: instantiate: %s", hipGetErrorString(ei));
+    *out = new dt_graph_exec{exec};
+    return DT_OK;
+}
+
+extern "C" int dt_graph_exec_launch(dt_backend* be, dt_graph_exec* exec) {
+    DT_REQUIRE(be != nullptr && exec != nullptr, "dt_graph_exec_launch: null argument");
+    DT_HIP(hipGraphLaunch(exec->exec, be->stream), "dt_graph_exec_launch");
+    return DT_OK;
+}
+
+extern "C" int dt_graph_exec_free(dt_graph_exec* exec) {
+    if (!exec) return DT_OK;
+    (void)hipGraphExecDestroy(exec->exec);
+    delete exec;
+    return DT_OK;
+}

@@ -111,6 +111,9 @@ _SIGS = {
                                         c_void_p, c_int64, c_int32, c_int32, c_float, c_void_p, c_int32,
                                         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_int64, _I64P, _I64P, _I64P, c_float, c_int32, _S]),
+    "dt_graph_capture": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32, POINTER(c_void_p)]),
+    "dt_graph_exec_launch": (c_int32, [c_void_p, c_void_p]),
+    "dt_graph_exec_free": (c_int32, [c_void_p]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
     "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,

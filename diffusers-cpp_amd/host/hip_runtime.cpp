@@ -154,6 +154,7 @@ HipRuntime::~HipRuntime() {
         reset();
     } catch (...) {
     }
+    if (exec_) dt_graph_exec_free(exec_);
     if (be_) dt_backend_free(be_);
 }
 
@@ -529,14 +530,34 @@ const ComputeStats& HipRuntime::plan() {
     return stats_;
 }
 
-void HipRuntime::compute() {
-    if (!be_) throw Error("compute: this runtime has no device");
-    if (!prepared_) prepare();
+void HipRuntime::upload_leaves() {
     for (Node* l : leaves_) {
         auto h = host_data_.find(l);
         if (h != host_data_.end())
             check(dt_tensor_set(l, h->second.data(), 0, h->second.size(), nullptr), "dt_tensor_set");
     }
+}
+
+void HipRuntime::compute_graph() {
+    if (!be_) throw Error("compute_graph: this runtime has no device");
+    if (!prepared_ || !exec_ || exec_gen_ != plan_gen_) {
+        compute();  // plans, allocates and creates the backend's scratch before the recording
+        if (exec_) check(dt_graph_exec_free(exec_), "dt_graph_exec_free");
+        exec_ = nullptr;
+        const int n = (int)order_.size();
+        if (n) check(dt_graph_capture(be_, order_.data(), n, &exec_), "dt_graph_capture");
+        exec_gen_ = plan_gen_;
+        return;
+    }
+    upload_leaves();
+    check(dt_graph_exec_launch(be_, exec_), "dt_graph_exec_launch");
+    check(dt_backend_synchronize(be_), "dt_backend_synchronize");
+}
+
+void HipRuntime::compute() {
+    if (!be_) throw Error("compute: this runtime has no device");
+    if (!prepared_) prepare();
+    upload_leaves();
     const int n = (int)order_.size();
     if (n) check(dt_graph_compute(be_, order_.data(), n), "dt_graph_compute");
     check(dt_backend_synchronize(be_), "dt_backend_synchronize");
@@ -547,6 +568,7 @@ void HipRuntime::compute() {
 }
 
 void HipRuntime::prepare(bool allocate) {
+    ++plan_gen_;
     const int n = (int)order_.size();
     // 1. fusion plan: which nodes are absorbed (no storage) and where every
     //    node's kernel runs (absorbed -> its root, grouped GEMMs -> the
@@ -664,6 +686,8 @@ void HipRuntime::read(const Node* node, void* host, size_t bytes) const {
 }
 
 void HipRuntime::reset() {
+    if (exec_) dt_graph_exec_free(exec_);
+    exec_ = nullptr;
     if (be_ && leaf_buf_) dt_buffer_free(be_, leaf_buf_);
     if (be_ && arena_) dt_buffer_free(be_, arena_);
     leaf_buf_ = arena_ = nullptr;

@@ -205,6 +205,10 @@ public:
     // The plan and the device memory are kept while no node is added, so
     // repeated calls on the same graph only upload host-bound leaves and run.
     void compute();
+    // compute(), replayed as one HIP graph (dt_graph_capture): the first call
+    // after the plan changes runs eagerly and records the launches; later
+    // calls upload host-bound leaves and submit the graph.  Same results.
+    void compute_graph();
     // Fusion and memory plan of the recorded graph without touching a device;
     // fills stats() except `kernels`.
     const ComputeStats& plan();
@@ -237,6 +241,9 @@ private:
     void* arena_ = nullptr;
     size_t arena_cap_ = 0;
     ComputeStats stats_;
+    dt_graph_exec* exec_ = nullptr;  // compute_graph's recording
+    size_t plan_gen_ = 0, exec_gen_ = 0;  // prepare() count when it was recorded
+    void upload_leaves();
 };
 
 // The runtime that module code uses (the reference's thread-local Scope,

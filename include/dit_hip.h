@@ -503,6 +503,21 @@ int dt_graph_plan_ex(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into, in
  * and nodes absorbed into fused kernels. */
 int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);
 
+/* The launches of one dt_graph_compute recorded as a HIP graph, replayed by
+ * dt_graph_exec_launch on the backend's stream: one submission per step
+ * instead of the fusion pass plus a launch per kernel (the role of the
+ * reference's repeated ggml_backend_graph_compute, ExecutionRuntime.cpp:227,
+ * 254).  Call dt_graph_compute on the same nodes once first, so the
+ * backend's scratch and RoPE table exist (capture allocates nothing).  The
+ * replay reads and writes the node data pointers given at capture: inputs
+ * are updated in place between replays.  A backend on the NULL stream gets
+ * a stream of its own (default priority), used from then on.  The graph
+ * records no memset nodes. */
+typedef struct dt_graph_exec dt_graph_exec;
+int dt_graph_capture(dt_backend *be, dt_tensor **nodes, int32_t n_nodes, dt_graph_exec **out);
+int dt_graph_exec_launch(dt_backend *be, dt_graph_exec *exec);
+int dt_graph_exec_free(dt_graph_exec *exec);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,3 +63,38 @@ def test_graph_replays_match_eager(orc, dev):
         torch.cuda.synchronize()
         for i, (o, e) in enumerate(zip(outs, eager)):
             assert torch.equal(o.view(torch.int16), e.view(torch.int16)), f"replay {rep} output {i}"
+
+
+def test_dt_graph_capture_replays_match_eager(orc, dev):
+    """dt_graph_capture records one dt_graph_compute of a single-stream
+    block's chain (fused adaLN, q/k QK-RMSNorm+RoPE with the SwiGLU, gated
+    residual); each replay, after eager torch work has overwritten the
+    outputs, reproduces the eager results bit for bit."""
+    import ctypes
+
+    import dit_hip as dh
+    from graphkit import Backend
+    from test_gpu_graph_ops import build_single_block_chain
+    lib = dh.load()
+    be = Backend()
+    g, _, _, outs, _ = build_single_block_chain(orc, torch.bfloat16, 48, 3072, 24, 9216)
+    for o in outs.values():
+        o.d.flags |= dh.FLAG_OUTPUT
+    arr, n = g._array(), len(g.nodes)
+    dh.check(lib.dt_graph_compute(be.h, arr, n), "dt_graph_compute")
+    dh.check(lib.dt_backend_synchronize(be.h), "sync")
+    eager = {k: o.torch().clone() for k, o in outs.items()}
+    ex = ctypes.c_void_p()
+    dh.check(lib.dt_graph_capture(be.h, arr, n, ctypes.byref(ex)), "dt_graph_capture")
+    try:
+        for rep in range(3):
+            for o in outs.values():
+                o.torch().fill_(float("nan"))
+            torch.cuda.synchronize()
+            dh.check(lib.dt_graph_exec_launch(be.h, ex), "dt_graph_exec_launch")
+            dh.check(lib.dt_backend_synchronize(be.h), "sync")
+            for k, o in outs.items():
+                assert torch.equal(o.torch().view(torch.int16), eager[k].view(torch.int16)), f"replay {rep} {k}"
+    finally:
+        lib.dt_graph_exec_free(ex)
+        be.close()

@@ -173,6 +173,22 @@ def test_model_small(orc, tmp):
     check(read_dtb(out).reshape(n_img, 128), want, "model 1+2 blocks")
 
 
+def test_model_small_hip_graph(orc, tmp):
+    """--hip-graph true: the step is recorded once (dt_graph_capture) and
+    replayed; after three replays, with the inputs uploaded again before each,
+    the output equals the eager run's bit for bit."""
+    import oracle.flux2 as of
+    P = make_params(orc, of.model_param_shapes(SMALL_MODEL), 5001)
+    hid, txt, pos, f = _small_model_inputs(orc, tmp)
+    wd = write_params(tmp, P)
+    eager, graph = os.path.join(tmp, "e.dtb"), os.path.join(tmp, "g.dtb")
+    _run_small_model(f, wd, eager, hid.shape[0], txt.shape[0])
+    st = _run_small_model(f, wd, graph, hid.shape[0], txt.shape[0], "--hip-graph", "true", "--warmup", 2)
+    assert st["hip_graph"] is True
+    a, b = read_dtb(eager), read_dtb(graph)
+    assert a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_model_small_q8_0_weights(orc, tmp):
     """The same model with --weight-format q8_0: every Linear weight is
     quantised to Q8_0 on the device, repacked (DT_TYPE_Q8_0_SPLIT) and
