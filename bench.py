@@ -416,7 +416,7 @@ def main():
                     help="print only the VAE conv / GroupNorm measurements (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+        print(f"bench.py: this benchmark measures one GPU only (--gpus {args.gpus} requested); "
               "the chain is row-independent and would shard tokens across GPUs with no exchange",
               file=sys.stderr)
         sys.exit(2)

@@ -37,7 +37,7 @@ def as_input(a, dtype):
 
 
 def check(got, ref, dtype, what, one_rounding=True):
-    """bf16: the north-star bar (rel L2 <= 1e-2, cos >= 0.9999) and, for a
+    """bf16: the bf16 bar (rel L2 <= 1e-2, cos >= 0.9999) and, for a
     single fused kernel (one rounding of an fp32 result), at most one bf16
     ulp per element; fp32: |d| <= 1e-5 * max(|ref|, 1)."""
     if dtype == torch.bfloat16:
