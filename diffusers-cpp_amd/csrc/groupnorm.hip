@@ -50,9 +50,22 @@ __global__ __launch_bounds__(kBlock) void gn_stats_kernel(const T* __restrict__ 
     int64_t v1 = v0 + kChunkVecs;
     if (v1 > s.group_vecs) v1 = s.group_vecs;
     double s1 = 0.0, s2 = 0.0;
-    for (int64_t v = v0 + threadIdx.x; v < v1; v += kBlock) {
+    // The thread's vectors are all requested before the first is used (kept
+    // packed, 4 registers each), so a wave has kVecsPerThread in flight.
+    uint4 raw[kVecsPerThread];
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < kVecsPerThread; ++i) {
+            const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
+            if (v < v1) raw[i] = ld_stream(xg + v * EPV);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kVecsPerThread; ++i) {
+        const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
+        if (v >= v1) break;
         float a[EPV];
-        if constexpr (VEC) Io<T>::load(xg + v * EPV, a);
+        if constexpr (VEC) Io<T>::unpack(raw[i], a);
         else a[0] = Io<T>::get(xg + v);
         float p1 = 0.f, p2 = 0.f;
 #pragma unroll
@@ -88,9 +101,20 @@ __device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int
     const int64_t v0 = (int64_t)blockIdx.x * kChunkVecs;
     int64_t v1 = v0 + kChunkVecs;
     if (v1 > s.group_vecs) v1 = s.group_vecs;
-    for (int64_t v = v0 + threadIdx.x; v < v1; v += kBlock) {
+    uint4 raw[kVecsPerThread];  // every load first, packed (see gn_stats_kernel)
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < kVecsPerThread; ++i) {
+            const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
+            if (v < v1) raw[i] = ld_stream(xg + v * EPV);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < kVecsPerThread; ++i) {
+        const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
+        if (v >= v1) break;
         float a[EPV];
-        if constexpr (VEC) Io<T>::load(xg + v * EPV, a);
+        if constexpr (VEC) Io<T>::unpack(raw[i], a);
         else a[0] = Io<T>::get(xg + v);
         const int64_t c = c0 + (int64_t)fdiv((uint32_t)v, hw_vecs);
         const float wc = w ? w[c] : 1.0f, bc = b ? b[c] : 0.0f;
