@@ -172,11 +172,12 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_staged_kernel(cons
 // Dense tensors (rows packed back to back in the source and the output) are
 // one stream of blocks: workgroup i decodes blocks [SEG * i, SEG * i + SEG)
 // with SEG = kFlatUnroll x the staged kernels' run, so each workgroup keeps
-// 8.5 KB (Q8_0) / 4.5 KB (Q4_K) of loads in flight -- a run of one row per
-// workgroup leaves too little in flight per CU to cover HBM latency.  The
+// 17 KB (Q8_0) / 9 KB (Q4_K) of loads in flight -- a run of one row per
+// workgroup leaves too little in flight per CU to cover HBM latency (runs
+// of 4x and 16x measured slower than 8x).  The
 // bytes past the last whole 16-byte vector of the tensor are copied in 2-byte
 // pieces, so nothing past the tensor is read.
-constexpr int kFlatUnroll = 4;
+constexpr int kFlatUnroll = 8;
 
 template <typename T>
 __global__ __launch_bounds__(kStageThreads) void dequant_q8_0_flat_kernel(const uint8_t* __restrict__ src,
