@@ -208,6 +208,20 @@ __global__ __launch_bounds__(kBlock) void concat_raw_kernel(Desc a, Desc b, Desc
     }
 }
 
+// Same-type concat of dense tensors whose runs are whole 16-byte vectors:
+// d is `rows` runs of (ca + cb) vectors, a's run then b's (the dims above
+// `dim` index the runs).  Non-temporal 16-byte copies.
+__global__ __launch_bounds__(kBlock) void concat_dense16_kernel(const uint4* __restrict__ a, const uint4* __restrict__ b,
+                                                                uint4* __restrict__ d, int64_t ca, int64_t cb,
+                                                                int64_t n) {
+    const int64_t run = ca + cb;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / run, off = i - row * run;
+        st_stream(d + i, off < ca ? ld_stream(a + row * ca + off) : ld_stream(b + row * cb + (off - ca)));
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void cpy_raw_kernel(Desc a, Desc d, int es, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
@@ -347,6 +361,30 @@ extern "C" int dt_op_concat(const dt_tensor* a, const dt_tensor* b, int32_t dim,
             DT_REQUIRE(a->ne[i] == b->ne[i] && dst->ne[i] == a->ne[i], "dt_op_concat: ne[%d] mismatch", i);
     }
     const int64_t n = dit::nelem(dst);
+    if (raw) {
+        const int es = dit::elem_size(a->type);
+        auto dense = [es](const dt_tensor* t) {
+            int64_t want = es;
+            for (int i = 0; i < 4; ++i) {
+                if (t->ne[i] > 1 && t->nb[i] != want) return false;
+                want *= t->ne[i];
+            }
+            return true;
+        };
+        int64_t ca = es, cb = es;  // bytes of one run of a / b: dims 0..dim
+        for (int i = 0; i <= dim; ++i) {
+            ca *= a->ne[i];
+            cb *= b->ne[i];
+        }
+        if (n > 0 && dense(a) && dense(b) && dense(dst) && ca % 16 == 0 && cb % 16 == 0 && dit::aligned16(a->data) &&
+            dit::aligned16(b->data) && dit::aligned16(dst->data)) {
+            const int64_t nv = n * es / 16;
+            hipLaunchKernelGGL(dit::concat_dense16_kernel, dim3(dit::blocks_for(nv)), dim3(256), 0,
+                               (hipStream_t)stream, (const uint4*)a->data, (const uint4*)b->data, (uint4*)dst->data,
+                               ca / 16, cb / 16, nv);
+            return dit::check_launch("dt_op_concat");
+        }
+    }
     if (raw)
         hipLaunchKernelGGL(dit::concat_raw_kernel, dim3(dit::blocks_for(n)), dim3(256), 0,
                            (hipStream_t)stream, dit::desc_of(a), dit::desc_of(b), dit::desc_of(dst),

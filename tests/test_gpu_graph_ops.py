@@ -143,6 +143,14 @@ def test_concat_and_cpy(orc, dev):
     dh.op_concat(pos, pos, 1, cat)
     torch.cuda.synchronize()
     assert torch.equal(col, pos[:, 3]) and torch.equal(cat, torch.cat([pos, pos]))
+    # dense bf16 runs of whole 16-byte vectors (the txt | img token concat of
+    # the single-stream input): the vector-copy path, bit for bit
+    t_ = dev_tensor(orc.randn(SEED + 9, (1, 512, 3072)), torch.bfloat16)
+    i_ = dev_tensor(orc.randn(SEED + 10, (1, 4096, 3072)), torch.bfloat16)
+    j = torch.empty((1, 4608, 3072), dtype=torch.bfloat16, device="cuda")
+    dh.op_concat(t_, i_, 1, j)
+    torch.cuda.synchronize()
+    assert torch.equal(j, torch.cat([t_, i_], 1))
 
 
 # ------------------------------------------------------------------ graphs ----
