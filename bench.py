@@ -150,10 +150,10 @@ class Flusher:
         self.buf.fill_(self.i & 0xFF)
 
 
-def time_cold(torch, fn, n, flush):
+def time_cold(torch, fn, n, flush, samples=False):
     """Median duration of fn() over n launches, each bracketed by its own HIP
     events on the launch stream, with the cache flushed before (outside) each
-    bracket."""
+    bracket (samples=True: every duration, in seconds)."""
     st = torch.cuda.current_stream()
     fn()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -164,7 +164,8 @@ def time_cold(torch, fn, n, flush):
         fn()
         b.record(st)
     torch.cuda.synchronize()
-    return statistics.median(a.elapsed_time(b) for a, b in ev) * 1e-3
+    ts = [a.elapsed_time(b) * 1e-3 for a, b in ev]
+    return ts if samples else statistics.median(ts)
 
 
 def probe_kernels(t):
@@ -372,6 +373,8 @@ def denoise_step(steps, warmup, weight_format="bf16", hip_graph=True):
     if r.returncode != 0:
         raise RuntimeError(f"dit_cli failed ({r.returncode}): {r.stderr.strip()[-500:]}")
     res = json.loads(r.stdout.strip().splitlines()[-1])
+    if res["output"]["nonfinite"]:
+        raise RuntimeError(f"denoise step output holds {res['output']['nonfinite']} non-finite values")
     t = res["ms_per_step_median"] * 1e-3
     flops = denoise_flops()
     return {
@@ -395,6 +398,7 @@ def denoise_step(steps, warmup, weight_format="bf16", hip_graph=True):
         "fused_nodes": res["fused_nodes"],
         "arena_bytes": res["arena_bytes"],
         "tflop_per_step": round(flops / 1e12, 3),
+        "output": res["output"],
         "roofline": {"bound": "mfma", "achieved": round(flops / t / 1e12, 1), "peak": 2500.0,
                      "unit": "TFLOP/s", "frac": round(flops / t / 1e12 / 2500.0, 4)},
     }
@@ -435,6 +439,13 @@ def main():
                      if args.denoise_steps > 0 and args.secondary else None)
     denoise_q8 = (denoise_step(args.denoise_steps, args.denoise_warmup, "q8_0")
                   if args.denoise_steps > 0 and args.secondary else None)
+    # The three runs compute the same step on the same weights and inputs:
+    # graph replay, eager launches and Q8_0 weights must agree bit for bit.
+    ref_hash = denoise["output"]["fnv64"] if denoise else None
+    for name, other in (("eager launches", denoise_eager), ("Q8_0 weights", denoise_q8)):
+        if other and other["output"]["fnv64"] != ref_hash:
+            raise RuntimeError(f"denoise step with {name} differs from the graph-replayed bf16 step "
+                               f"({other['output']} vs {denoise['output']})")
 
     import torch
     import dit_hip
@@ -475,7 +486,7 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3 / args.steps, time.perf_counter() - w0
 
-    eager_s, _ = timed(step)
+    eager_s, eager_wall = timed(step)
 
     def capture(fn):
         """One HIP graph per buffer set of fn(i)."""
@@ -517,7 +528,7 @@ def main():
     schedules = {"eager": eager_s, "graph": seq_s, "graph_branched": br_s}
     best = min(schedules, key=schedules.get)
     step_s = schedules[best]
-    wall = {"eager": None, "graph": seq_wall, "graph_branched": br_wall}[best]
+    wall = {"eager": eager_wall, "graph": seq_wall, "graph_branched": br_wall}[best]
 
     # The streaming ceiling: the probe launches with the chain's shapes, timed
     # the same ways (eager steps over the rotating buffer sets; cold launches).
@@ -549,8 +560,10 @@ def main():
     def cold(fns, ab):
         res = {}
         for name, fn in fns.items():
-            tk = time_cold(torch, fn, 20, flush)
-            res[name] = {"us": round(tk * 1e6, 2), "alg_MB": round(ab[name] / 1e6, 2),
+            ts = time_cold(torch, fn, 20, flush, samples=True)
+            tk = statistics.median(ts)
+            res[name] = {"us": round(tk * 1e6, 2), "us_mean": round(statistics.mean(ts) * 1e6, 2),
+                         "us_min": round(min(ts) * 1e6, 2), "alg_MB": round(ab[name] / 1e6, 2),
                          "GBs": round(ab[name] / tk / 1e9, 1),
                          "frac_hbm": round(ab[name] / tk / 1e9 / HBM_PEAK_GBS, 3)}
         return res
@@ -570,9 +583,14 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
-    roofline = {"bound": "hbm", "achieved": kernels[dom]["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(kernels[dom]["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "qk_swiglu_kernel<bf16,3>", "alg_bytes_per_launch": fused_ab[dom]}
+    kd = kernels[dom]
+    roofline = {"bound": "hbm", "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "qk_swiglu_kernel<bf16,3>", "alg_bytes_per_launch": fused_ab[dom],
+                "statistic": "median of 20 launches, each timed by HIP events on its launch stream after a "
+                             "1 GiB cache flush",
+                "launch_us": {"median": kd["us"], "mean": kd["us_mean"], "min": kd["us_min"]},
+                "frac_at_mean": round(fused_ab[dom] / (kd["us_mean"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
     cpu = None
     if args.cpu_budget > 0:

@@ -174,6 +174,12 @@ class Session {
 public:
     explicit Session(const Args& a) : args(a), plan_only(a.flag("plan-only", false)), rt(plan_only ? -1 : 0), scope(rt) {
         dev.be = rt.backend();
+        // --alloc node-order: node memory placed as ggml_gallocr places it
+        // (node order, in place where allowed); the executor checks its
+        // fusion plan against those addresses.
+        const std::string alloc = a.str("alloc", "fused");
+        if (alloc == "node-order") rt.set_allocation(HipRuntime::Allocation::NodeOrder);
+        else if (alloc != "fused") throw std::runtime_error("--alloc must be fused or node-order");
     }
 
     Tensor input(const std::string& key) {
@@ -378,6 +384,81 @@ std::string json_num(double v) {
     return buf;
 }
 
+// Count of each recorded op (unary ops by kind), as a JSON object: the op
+// set a ggml-side translation of the same graph has to map.
+std::string op_histogram(const HipRuntime& rt) {
+    static const char* kOps[] = {"NONE", "ADD", "SUB", "MUL", "DIV", "SCALE", "SIGMOID", "NORM", "RMS_NORM",
+                                 "ROPE", "CONCAT", "CPY", "VIEW", "FILL", "UNARY", "MUL_MAT", "FLASH_ATTN_EXT",
+                                 "CONV_2D_DIRECT", "UPSCALE"};
+    static const char* kUnary[] = {"SIGMOID", "EXP", "LOG", "SQRT", "SIN", "COS", "SCALE", "CLAMP", "SILU",
+                                   "FILL"};
+    std::map<std::string, int> h;
+    for (const Node* t : rt.nodes()) {
+        std::string name = t->op >= 0 && t->op < (int)(sizeof kOps / sizeof *kOps) ? kOps[t->op] : "?";
+        if (t->op == DT_OP_UNARY) {
+            const int k = t->op_params[0];
+            name += std::string(".") + (k >= 0 && k < (int)(sizeof kUnary / sizeof *kUnary) ? kUnary[k] : "?");
+        }
+        ++h[name];
+    }
+    std::string out = "{";
+    for (const auto& kv : h) out += (out.size() > 1 ? ", " : "") + json_str(kv.first) + ": " + std::to_string(kv.second);
+    return out + "}";
+}
+
+float bf16_bits_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Summary of an output tensor's bytes: element count, mean and standard
+// deviation (fp64), count of NaN/Inf, and the FNV-1a hash of the bytes (equal
+// hashes = bit-identical outputs across runs).
+struct OutputCheck {
+    int64_t n = 0, nonfinite = 0;
+    double mean = 0, std = 0;
+    uint64_t fnv = 1469598103934665603ull;
+};
+
+OutputCheck check_output(const std::vector<uint8_t>& bytes, int32_t type) {
+    OutputCheck c;
+    for (uint8_t b : bytes) c.fnv = (c.fnv ^ b) * 1099511628211ull;
+    double s = 0, s2 = 0;
+    const size_t es = type == DT_TYPE_F32 ? 4 : 2;
+    for (size_t i = 0; i + es <= bytes.size(); i += es) {
+        float f;
+        if (type == DT_TYPE_F32) {
+            std::memcpy(&f, bytes.data() + i, 4);
+        } else {
+            uint16_t h;
+            std::memcpy(&h, bytes.data() + i, 2);
+            f = bf16_bits_to_f32(h);
+        }
+        ++c.n;
+        if (!std::isfinite(f)) {
+            ++c.nonfinite;
+            continue;
+        }
+        s += f;
+        s2 += (double)f * f;
+    }
+    const int64_t m = c.n - c.nonfinite;
+    if (m > 0) {
+        c.mean = s / m;
+        c.std = std::sqrt(std::max(0.0, s2 / m - c.mean * c.mean));
+    }
+    return c;
+}
+
+std::string output_json(const OutputCheck& c) {
+    char buf[64];
+    std::snprintf(buf, sizeof buf, "\"%016llx\"", (unsigned long long)c.fnv);
+    return "{\"elements\": " + std::to_string(c.n) + ", \"mean\": " + json_num(c.mean) + ", \"std\": " +
+           json_num(c.std) + ", \"nonfinite\": " + std::to_string(c.nonfinite) + ", \"fnv64\": " + buf + "}";
+}
+
 void run_model(Session& s, const Args& a) {
     Flux2Config cfg;
     cfg.num_layers = a.i64("num_layers", 5);
@@ -446,9 +527,11 @@ void run_model(Session& s, const Args& a) {
         std::printf("{\"command\": \"Flux2Transformer2DModel\", \"plan_only\": true, \"nodes\": %d, "
                     "\"fused_nodes\": %d, \"grouped_nodes\": %d, \"deferred_nodes\": %d, "
                     "\"mul_mat_nodes\": %d, \"attention_nodes\": %d, "
-                    "\"arena_bytes\": %zu, \"naive_bytes\": %zu, \"params\": %zu}\n",
+                    "\"arena_bytes\": %zu, \"naive_bytes\": %zu, \"params\": %zu, \"alloc\": \"%s\", "
+                    "\"launches_held\": %d, \"fused_nodes_checked\": %d, \"ops\": %s}\n",
                     st.nodes, st.fused_nodes, st.grouped_nodes, st.deferred_nodes, st.mul_mat_nodes,
-                    st.attention_nodes, st.arena_bytes, st.naive_bytes, n_params);
+                    st.attention_nodes, st.arena_bytes, st.naive_bytes, n_params, a.str("alloc", "fused").c_str(),
+                    st.launches_held, st.fused_nodes_checked, op_histogram(rt).c_str());
         return;
     }
     std::string gguf_note;
@@ -523,11 +606,10 @@ void run_model(Session& s, const Args& a) {
         const auto t1 = std::chrono::steady_clock::now();
         if (i >= warmup) ms.push_back(std::chrono::duration<double, std::milli>(t1 - t0).count());
     }
-    if (a.has("out")) {
-        std::vector<uint8_t> host(HipRuntime::nbytes(*out));
-        rt.read(*out, host.data(), host.size());
-        write_blob(a.str("out"), out.dtype(), out.shape(), host);
-    }
+    std::vector<uint8_t> host(HipRuntime::nbytes(*out));
+    rt.read(*out, host.data(), host.size());
+    if (a.has("out")) write_blob(a.str("out"), out.dtype(), out.shape(), host);
+    const OutputCheck oc = check_output(host, out.dtype());
     std::vector<double> sorted = ms;
     std::sort(sorted.begin(), sorted.end());
     double mean = 0;
@@ -538,10 +620,15 @@ void run_model(Session& s, const Args& a) {
                 "\"ms_per_step_median\": %.4f, \"ms_per_step_mean\": %.4f, \"ms_per_step_min\": %.4f, "
                 "\"nodes\": %d, \"kernels\": %d, \"fused_nodes\": %d, \"arena_bytes\": %zu, "
                 "\"params\": %zu, \"weight_format\": \"%s\", \"linear_weight_bytes\": %zu, "
-                "\"q8_0_weight_bytes\": %zu, \"hip_graph\": %s%s}\n",
+                "\"q8_0_weight_bytes\": %zu, \"hip_graph\": %s, \"alloc\": \"%s\", \"launches_held\": %d, "
+                "\"output\": %s%s}\n",
                 steps, warmup, sorted.empty() ? 0.0 : sorted[sorted.size() / 2], mean,
                 sorted.empty() ? 0.0 : sorted.front(), st.nodes, st.kernels, st.fused_nodes, st.arena_bytes,
-                n_params, format.c_str(), resident_bytes, q8_bytes, replay ? "true" : "false", gguf_note.c_str());
+                n_params, format.c_str(), resident_bytes, q8_bytes, replay ? "true" : "false",
+                a.str("alloc", "fused").c_str(), st.launches_held, output_json(oc).c_str(), gguf_note.c_str());
+    std::fflush(stdout);
+    if (oc.nonfinite)
+        throw std::runtime_error("the step's output holds " + std::to_string(oc.nonfinite) + " non-finite values");
 }
 
 // GgufInfo --gguf PATH: the file's header, metadata and tensor table as one

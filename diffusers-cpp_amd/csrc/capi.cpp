@@ -65,10 +65,12 @@ struct dt_backend {
     int rope_axis_dim;
     float rope_base;
     bool own_stream;    // created by dt_graph_capture
+    uint64_t generation;  // bumped whenever scratch or rope_table move
 };
 
 struct dt_graph_exec {
     hipGraphExec_t exec;
+    uint64_t generation;  // the backend's generation at capture
 };
 
 extern "C" const char* dt_last_error(void) { return dit::g_last_error.c_str(); }
@@ -88,7 +90,7 @@ extern "C" int dt_backend_init(int32_t device_ordinal, dt_backend** out) {
     DT_REQUIRE(device_ordinal >= 0 && device_ordinal < n, "dt_backend_init: device %d of %d",
                device_ordinal, n);
     DT_HIP(hipSetDevice(device_ordinal), "dt_backend_init");
-    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f, false};
+    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f, false, 0};
     *out = be;
     return DT_OK;
 }
@@ -111,6 +113,12 @@ extern "C" int dt_backend_free(dt_backend* be) {
 
 extern "C" int dt_backend_set_stream(dt_backend* be, dt_stream_t stream) {
     DT_REQUIRE(be != nullptr, "dt_backend_set_stream: null backend");
+    if (be->own_stream && be->stream != (hipStream_t)stream) {
+        DT_HIP(hipSetDevice(be->device), "dt_backend_set_stream");
+        DT_HIP(hipStreamSynchronize(be->stream), "dt_backend_set_stream");
+        DT_HIP(hipStreamDestroy(be->stream), "dt_backend_set_stream");
+        be->own_stream = false;
+    }
     be->stream = (hipStream_t)stream;
     return DT_OK;
 }
@@ -140,6 +148,26 @@ extern "C" int dt_buffer_free(dt_backend* be, void* ptr) {
     return DT_OK;
 }
 
+// Bytes of a contiguous tensor (ggml_nbytes): whole blocks for block types.
+static bool tensor_bytes(const dt_tensor* t, size_t* out) {
+    int64_t n = 1;
+    for (int i = 1; i < 4; ++i) {
+        if (t->ne[i] < 0) return false;
+        n *= t->ne[i];
+    }
+    int64_t row;
+    const int es = dit::elem_size(t->type);
+    if (es) row = t->ne[0] * es;
+    else if (t->type == DT_TYPE_Q8_0) row = (t->ne[0] + 31) / 32 * 34;
+    else if (t->type == DT_TYPE_Q4_K) row = (t->ne[0] + 255) / 256 * 144;
+    else if (t->type == DT_TYPE_Q8_0_SPLIT) row = -1;
+    else return false;
+    if (t->ne[0] < 0) return false;
+    *out = row < 0 ? dt_q8_0_split_bytes(t->ne[1], t->ne[0]) * (size_t)(t->ne[2] * t->ne[3])
+                   : (size_t)(row * n);
+    return true;
+}
+
 static bool contiguous(const dt_tensor* t) {
     const int es = dit::elem_size(t->type);
     if (es == 0) return true;  // block types: caller addresses raw bytes
@@ -155,6 +183,10 @@ extern "C" int dt_tensor_set(const dt_tensor* t, const void* host, size_t offset
                              dt_stream_t stream) {
     DT_REQUIRE(t && t->data && (host || n == 0), "dt_tensor_set: null argument");
     DT_REQUIRE(contiguous(t), "dt_tensor_set: tensor is not contiguous");
+    size_t total = 0;
+    DT_REQUIRE(tensor_bytes(t, &total), "dt_tensor_set: tensor type %d / shape not supported", t->type);
+    DT_REQUIRE(offset <= total && n <= total - offset,
+               "dt_tensor_set: %zu bytes at offset %zu exceed the tensor's %zu bytes", n, offset, total);
     DT_HIP(hipMemcpyAsync((char*)t->data + offset, host, n, hipMemcpyHostToDevice, (hipStream_t)stream),
            "dt_tensor_set");
     DT_HIP(hipStreamSynchronize((hipStream_t)stream), "dt_tensor_set");
@@ -165,6 +197,10 @@ extern "C" int dt_tensor_get(const dt_tensor* t, void* host, size_t offset, size
                              dt_stream_t stream) {
     DT_REQUIRE(t && t->data && (host || n == 0), "dt_tensor_get: null argument");
     DT_REQUIRE(contiguous(t), "dt_tensor_get: tensor is not contiguous");
+    size_t total = 0;
+    DT_REQUIRE(tensor_bytes(t, &total), "dt_tensor_get: tensor type %d / shape not supported", t->type);
+    DT_REQUIRE(offset <= total && n <= total - offset,
+               "dt_tensor_get: %zu bytes at offset %zu exceed the tensor's %zu bytes", n, offset, total);
     DT_HIP(hipMemcpyAsync(host, (const char*)t->data + offset, n, hipMemcpyDeviceToHost, (hipStream_t)stream),
            "dt_tensor_get");
     DT_HIP(hipStreamSynchronize((hipStream_t)stream), "dt_tensor_get");
@@ -188,6 +224,7 @@ int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const floa
         const size_t bytes = (size_t)kBackendRopePositions * axis_dim * sizeof(float);
         const hipError_t e = hipMalloc(&be->rope_table, bytes);
         if (e != hipSuccess) return fail(DT_ERR_OOM, "backend_rope_table(%zu): %s", bytes, hipGetErrorString(e));
+        ++be->generation;
         int rc = rope_table_device(be->rope_table, kBackendRopePositions, axis_dim, freq_base, be->stream);
         if (rc) return rc;
         // Built once; later graphs may run on another stream.
@@ -209,6 +246,7 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out) {
             be->scratch = nullptr;
             be->scratch_bytes = 0;
         }
+        ++be->generation;
         const hipError_t e = hipMalloc(&be->scratch, bytes);
         if (e != hipSuccess) return fail(DT_ERR_OOM, "backend_scratch(%zu): %s", bytes, hipGetErrorString(e));
         be->scratch_bytes = bytes;
@@ -220,6 +258,11 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out) {
 }  // namespace dit
 
 extern "C" int dt_graph_capture(dt_backend* be, dt_tensor** nodes, int32_t n_nodes, dt_graph_exec** out) {
+    return dt_graph_capture_ex(be, nodes, n_nodes, 0, out);
+}
+
+extern "C" int dt_graph_capture_ex(dt_backend* be, dt_tensor** nodes, int32_t n_nodes, uint32_t flags,
+                                   dt_graph_exec** out) {
     DT_REQUIRE(be != nullptr && out != nullptr && n_nodes >= 0 && (nodes || n_nodes == 0),
                "dt_graph_capture: bad arguments");
     DT_HIP(hipSetDevice(be->device), "dt_graph_capture");
@@ -231,7 +274,8 @@ extern "C" int dt_graph_capture(dt_backend* be, dt_tensor** nodes, int32_t n_nod
     }
     DT_HIP(hipStreamSynchronize(be->stream), "dt_graph_capture");
     DT_HIP(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "dt_graph_capture");
-    const int rc = dt_graph_compute(be, nodes, n_nodes);
+    const uint64_t gen = be->generation;
+    const int rc = dt_graph_compute_ex(be, nodes, n_nodes, flags);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(be->stream, &graph);
     if (rc) {
@@ -245,12 +289,21 @@ extern "C" int dt_graph_capture(dt_backend* be, dt_tensor** nodes, int32_t n_nod
     const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     if (ei != hipSuccess) return dit::fail(DT_ERR_HIP, "dt_graph_capture: instantiate: %s", hipGetErrorString(ei));
-    *out = new dt_graph_exec{exec};
+    if (be->generation != gen) {  // the capture itself moved the scratch or the table
+        (void)hipGraphExecDestroy(exec);
+        return dit::fail(DT_ERR_INVALID_ARG,
+                         "dt_graph_capture: the backend's scratch or RoPE table was (re)allocated during capture; "
+                         "run dt_graph_compute once before capturing");
+    }
+    *out = new dt_graph_exec{exec, gen};
     return DT_OK;
 }
 
 extern "C" int dt_graph_exec_launch(dt_backend* be, dt_graph_exec* exec) {
     DT_REQUIRE(be != nullptr && exec != nullptr, "dt_graph_exec_launch: null argument");
+    DT_REQUIRE(exec->generation == be->generation,
+               "dt_graph_exec_launch: the backend's scratch or RoPE table moved since this graph was captured; "
+               "capture it again");
     DT_HIP(hipGraphLaunch(exec->exec, be->stream), "dt_graph_exec_launch");
     return DT_OK;
 }

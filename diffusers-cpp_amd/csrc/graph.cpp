@@ -11,7 +11,7 @@
 //                   the normalised output (r runs at the adaLN's position)
 //   SwiGLU          MUL(MUL(g, SIGMOID(g)), u)        Flux2SwiGLU.hpp:20, SiLU.hpp:12
 //   GroupNorm+SiLU  MUL(a, SIGMOID(a)), a = ADD(MUL(VIEW(NORM(VIEW(x))), w), b)
-//                   GroupNorm.cpp:98-156 + SiLU.hpp:12 (affine / SiLU optional)
+//                   GroupNorm.cpp:44-103 + SiLU.hpp:12 (affine / SiLU optional)
 //   QK-RMSNorm+RoPE CONCAT*(ROPE(VIEW_a(MUL(RMS_NORM(q), w))), ...) along ne0
 //                   RMSNorm.cpp:13-20 + Flux2PosEmbed.hpp:29-108, optionally
 //                   with the txt|img CONCAT of Flux2Attention.hpp:114-116
@@ -43,6 +43,8 @@
 // unfused per-op kernels of ops.hip.
 #include <algorithm>
 #include <cstring>
+#include <iterator>
+#include <map>
 #include <unordered_map>
 #include <vector>
 
@@ -152,13 +154,19 @@ struct Graph {
     std::vector<int> runs_at;  // position where node i's kernel runs
     std::vector<char> deferred;  // node i keeps its output but runs inside another node's kernel
     std::unordered_map<const dt_tensor*, std::vector<int>> consumers;
+    // Set by the memory-hazard check (check_plan_memory) for launches that
+    // would read clobbered memory under the caller's allocation: `nomove`
+    // keeps node i's launch at its own position and output set (no deferral,
+    // grouping, merging or attention prologue rooted at or absorbing i);
+    // `banned` also keeps i out of every fused kernel.
+    std::vector<char> nomove, banned;
     dt_tensor** nodes = nullptr;
     int current_root = -1;
 
     bool internal(const dt_tensor* t, int n_uses = 1) const {
         if (!t || (t->flags & DT_FLAG_OUTPUT)) return false;
         auto i = index.find(t);
-        if (i == index.end() || claimed[i->second]) return false;
+        if (i == index.end() || claimed[i->second] || banned[i->second]) return false;
         auto u = uses.find(t);
         return u != uses.end() && u->second == n_uses;
     }
@@ -233,7 +241,9 @@ bool match_res_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     if (!n || n->op != DT_OP_NORM || !g.internal(n)) return false;
     const dt_tensor* x = n->src[0];
     auto xi = g.index.find(x);
-    if (xi == g.index.end() || g.claimed[xi->second] || g.deferred[xi->second]) return false;
+    if (xi == g.index.end() || g.claimed[xi->second] || g.deferred[xi->second] || g.nomove[xi->second] ||
+        g.banned[xi->second] || g.nomove[g.current_root])
+        return false;
     const int64_t cols = x->ne[0];
     int64_t r1, s1, r2, s2;
     if (!is_vec(t, cols) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
@@ -386,11 +396,13 @@ bool match_groupnorm(Graph& g, const dt_tensor* root, Plan& p) {
 bool match_qk(Graph& g, const dt_tensor* y, Plan& p);
 
 bool match_attn_qk(Graph& g, const dt_tensor* t, Plan& p) {
-    if (t->op != DT_OP_FLASH_ATTN_EXT || t->src[3] || t->type != DT_TYPE_BF16) return false;
+    if (t->op != DT_OP_FLASH_ATTN_EXT || t->src[3] || t->type != DT_TYPE_BF16 || g.nomove[g.current_root])
+        return false;
     const dt_tensor* qv = t->src[0];
     if (!qv || qv->op != DT_OP_VIEW || !g.internal(qv) || view_offset(qv) != 0) return false;
     const dt_tensor* y = qv->src[0];
-    if (!y || y->op != DT_OP_CONCAT || y->type != DT_TYPE_BF16 || !g.internal(y)) return false;
+    if (!y || y->op != DT_OP_CONCAT || y->type != DT_TYPE_BF16 || !g.internal(y) || g.nomove[g.index.at(y)])
+        return false;
     if (qv->ne[0] != 128 || y->ne[0] != 128 || qv->ne[1] != y->ne[2] || qv->ne[2] != y->ne[1] ||
         qv->ne[3] != y->ne[3] || qv->nb[0] != 2 || qv->nb[1] != y->nb[2] || qv->nb[2] != y->nb[1])
         return false;
@@ -694,7 +706,8 @@ void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
     auto groupable = [&](int j) {
         const dt_tensor* t = nodes[j];
         GemmArgs ga;
-        return t->op == DT_OP_MUL_MAT && !g.claimed[j] && plans[j].kind == K_NONE && gemm_args(t, &ga);
+        return t->op == DT_OP_MUL_MAT && !g.claimed[j] && !g.nomove[j] && !g.banned[j] && plans[j].kind == K_NONE &&
+               gemm_args(t, &ga);
     };
     for (int i = 0; i < n; ++i) {
         if (!groupable(i) || !ready_before(nodes[i]->src[0], i) || !ready_before(nodes[i]->src[1], i)) continue;
@@ -742,12 +755,13 @@ void merge_qk_swiglu(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plan
             if (g.claimed[i] && g.root[i] == root) g.runs_at[i] = pos;
     };
     for (int sidx = 0; sidx < n; ++sidx) {
-        if (plans[sidx].kind != K_SWIGLU) continue;
+        if (plans[sidx].kind != K_SWIGLU || g.nomove[sidx]) continue;
         int qk[2] = {-1, -1};
         int found = 0;
         for (int j = sidx - 1; j >= 0 && found < 2; --j)
             if (plans[j].kind == K_QK) qk[found++] = j;
-        if (found == 0) continue;
+        if (found == 0 || g.nomove[qk[0]]) continue;
+        if (found == 2 && g.nomove[qk[1]]) found = 1;
         const Plan& S = plans[sidx];
         const dt_tensor* ys = nodes[sidx];
         auto merge_one = [&]() {  // the nearest QK root alone with the SwiGLU
@@ -1095,8 +1109,220 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
 namespace dit {
 namespace {
 
+// ---- memory hazards of a plan under the caller's allocation -------------------
+//
+// A fused launch reads its external inputs at its own position and writes
+// every output it keeps there.  Some launches move work relative to node
+// order: a chain reads its first node's inputs at its last node, residual +
+// adaLN writes r later, grouped GEMMs and QK+SwiGLU write later nodes'
+// outputs earlier, an attention reads q's pre-norm input at the attention.
+// An allocator that follows only node order (ggml_gallocr, Context.hpp:118-135)
+// may hand an input's memory to another node after the input's last reader
+// in node order, or give a later node's output memory that is still live
+// earlier.  check_plan_memory replays the plan's launches in execution order
+// over the nodes' actual address ranges and reports every launch that would
+// read memory another node has overwritten (or that another launch overwrote
+// too early); plan_checked then keeps those launches from moving work, and
+// as a last step from fusing, until the replay is clean.
+
+struct Span {
+    uintptr_t lo = 0, hi = 0;
+};
+
+// Bytes a tensor's elements span from its data address (views resolved).
+bool span_of(const dt_tensor* t, Span* s) {
+    const void* d = data_of(t);
+    if (!d) return false;
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] <= 0) return false;
+    int64_t ext = 0;
+    if (t->type == DT_TYPE_Q8_0_SPLIT) {
+        ext = (int64_t)dt_q8_0_split_bytes(t->ne[1], t->ne[0]);
+    } else {
+        const int es = elem_size(t->type);
+        int d0 = 1;
+        if (es) {
+            ext = es;
+        } else if (t->type == DT_TYPE_Q8_0 || t->type == DT_TYPE_Q4_K) {
+            const int64_t blk = t->type == DT_TYPE_Q8_0 ? 32 : 256, bb = t->type == DT_TYPE_Q8_0 ? 34 : 144;
+            ext = (t->ne[0] + blk - 1) / blk * bb;
+        } else {
+            return false;
+        }
+        if (es) d0 = 0;
+        for (int i = d0; i < 4; ++i) ext += (t->ne[i] - 1) * (int64_t)t->nb[i];
+    }
+    s->lo = (uintptr_t)d;
+    s->hi = s->lo + (uintptr_t)ext;
+    return s->hi > s->lo;
+}
+
+// Which tensor's value lives at each address: disjoint [lo, hi) segments.
+class OwnerMap {
+public:
+    struct Seg {
+        uintptr_t hi;
+        int owner;   // value identity (a node index, or kLeaf)
+        int writer;  // node whose launch wrote it
+    };
+    void write(const Span& s, int owner, int writer) {
+        auto it = m_.lower_bound(s.lo);
+        if (it != m_.begin()) {
+            auto pv = std::prev(it);
+            if (pv->second.hi > s.lo) {
+                const Seg tail = pv->second;
+                pv->second.hi = s.lo;
+                if (tail.hi > s.hi) m_[s.hi] = tail;
+            }
+        }
+        it = m_.lower_bound(s.lo);
+        while (it != m_.end() && it->first < s.hi) {
+            const Seg seg = it->second;
+            it = m_.erase(it);
+            if (seg.hi > s.hi) {
+                m_[s.hi] = seg;
+                break;
+            }
+        }
+        m_[s.lo] = Seg{s.hi, owner, writer};
+    }
+    // A segment inside s holding another value than `owner` (bytes nobody
+    // wrote are taken as intact), or nullptr.
+    const Seg* foreign(const Span& s, int owner) const {
+        auto it = m_.upper_bound(s.lo);
+        if (it != m_.begin()) --it;
+        for (; it != m_.end() && it->first < s.hi; ++it)
+            if (it->second.hi > s.lo && it->second.owner != owner) return &it->second;
+        return nullptr;
+    }
+
+private:
+    std::map<uintptr_t, Seg> m_;
+};
+
+constexpr int kLeaf = -2;
+
+// Value identity of the memory t reads: its storage root (VIEW chains
+// resolved), a node index or kLeaf for tensors outside the list.
+int value_of(const Graph& g, const dt_tensor* t) {
+    while (t && t->op == DT_OP_VIEW) t = t->src[0];
+    if (!t) return kLeaf;
+    auto it = g.index.find(t);
+    return it == g.index.end() ? kLeaf : it->second;
+}
+
+bool launch_moves(const Plan& p) {
+    return p.kind == K_RES_ADALN || p.kind == K_ATTN_QK || p.kind == K_GEMM_GROUP || p.kind == K_QK_SWIGLU;
+}
+
+// Launches (by position) that read clobbered memory or clobber live memory.
+void check_plan_memory(const Graph& g, dt_tensor** nodes, int n, const std::vector<Plan>& plans,
+                       std::vector<int>& blamed) {
+    std::vector<std::vector<int>> members(n);
+    for (int j = 0; j < n; ++j) members[g.runs_at[j]].push_back(j);
+    std::vector<char> is_blamed(n, 0);
+    auto blame = [&](int pos) {
+        if (pos >= 0 && pos < n && !is_blamed[pos]) {
+            is_blamed[pos] = 1;
+            blamed.push_back(pos);
+        }
+    };
+    // A CPY into a destination writes on behalf of the destination's value.
+    auto write_identity = [&](int j) {
+        const dt_tensor* t = nodes[j];
+        return t->op == DT_OP_CPY && t->src[1] ? value_of(g, t->src[1]) : j;
+    };
+    OwnerMap owners;
+    std::vector<std::pair<Span, int>> reads, writes;
+    for (int p = 0; p < n; ++p) {
+        if (g.claimed[p] || plans[p].kind == K_DEFERRED) continue;  // not a launch position
+        reads.clear();
+        writes.clear();
+        const bool fused = plans[p].kind != K_NONE;
+        for (int j : members[p]) {
+            const dt_tensor* t = nodes[j];
+            for (int k = 0; k < 4; ++k) {
+                const dt_tensor* s = t->src[k];
+                if (!s) continue;
+                auto si = g.index.find(s);
+                if (si != g.index.end() && g.runs_at[si->second] == p) continue;  // produced in this launch
+                Span sp;
+                if (!span_of(s, &sp)) continue;
+                const int want = value_of(g, s);
+                if (const OwnerMap::Seg* f = owners.foreign(sp, want)) {
+                    bool found = false;
+                    if (j < p) {  // the read moved later than its node
+                        blame(p);
+                        found = true;
+                    }
+                    if (g.runs_at[f->writer] < f->writer) {  // the overwrite moved earlier
+                        blame(g.runs_at[f->writer]);
+                        found = true;
+                    }
+                    if (want >= 0 && g.runs_at[want] < want) {  // the value was written early, then reused
+                        blame(g.runs_at[want]);
+                        found = true;
+                    }
+                    (void)found;  // nothing moved: the node order itself reads it so
+                }
+                reads.push_back({sp, want});
+            }
+        }
+        for (int j : members[p]) {
+            const dt_tensor* t = nodes[j];
+            if (g.claimed[j] || t->op == DT_OP_VIEW || t->op == DT_OP_NONE) continue;
+            Span sp;
+            if (span_of(t, &sp)) writes.push_back({sp, j});
+        }
+        // A fused kernel may write over an input only element for element.
+        if (fused)
+            for (const auto& w : writes)
+                for (const auto& r : reads) {
+                    const bool overlap = w.first.lo < r.first.hi && r.first.lo < w.first.hi;
+                    const bool same = w.first.lo == r.first.lo && w.first.hi == r.first.hi;
+                    if (overlap && (!same || plans[p].kind == K_ATTN_QK || plans[p].kind == K_GEMM_GROUP ||
+                                    plans[p].kind == K_CONV))
+                        blame(p);
+                }
+        for (const auto& w : writes) owners.write(w.first, write_identity(w.second), w.second);
+    }
+}
+
+int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& plans);
+
+// The fusion plan, then (check) the memory replay, repeated with the blamed
+// launches held at their positions (then unfused) until it is clean.
+int plan_checked(dt_tensor** nodes, int32_t n, Graph& g, std::vector<Plan>& plans, bool check, int* kept_apart) {
+    std::vector<char> nomove(n, 0), banned(n, 0);
+    if (kept_apart) *kept_apart = 0;
+    for (;;) {
+        g = Graph();
+        g.nomove = nomove;
+        g.banned = banned;
+        int rc = plan_graph(nodes, n, g, plans);
+        if (rc || !check) return rc;
+        std::vector<int> blamed;
+        check_plan_memory(g, nodes, n, plans, blamed);
+        bool changed = false;
+        for (int p : blamed) {
+            if (!nomove[p] && launch_moves(plans[p])) {
+                nomove[p] = 1;
+            } else if (!banned[p] && plans[p].kind != K_NONE) {
+                banned[p] = nomove[p] = 1;
+            } else {
+                continue;
+            }
+            changed = true;
+            if (kept_apart) ++*kept_apart;
+        }
+        if (!changed) return DT_OK;
+    }
+}
+
 int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& plans) {
     g.nodes = nodes;
+    if ((int)g.nomove.size() != n_nodes) g.nomove.assign(n_nodes, 0);
+    if ((int)g.banned.size() != n_nodes) g.banned.assign(n_nodes, 0);
     g.claimed.assign(n_nodes, 0);
     g.deferred.assign(n_nodes, 0);
     g.root.assign(n_nodes, -1);
@@ -1113,7 +1339,7 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
     }
     plans.assign(n_nodes, Plan());
     for (int i = n_nodes - 1; i >= 0; --i) {
-        if (g.claimed[i] || g.deferred[i]) continue;
+        if (g.claimed[i] || g.deferred[i] || g.banned[i]) continue;
         dt_tensor* t = nodes[i];
         Plan& p = plans[i];
         g.current_root = i;
@@ -1142,7 +1368,7 @@ extern "C" int dt_graph_plan_ex(dt_tensor** nodes, int32_t n_nodes, int32_t* fus
                "dt_graph_plan: bad arguments");
     Graph g;
     std::vector<Plan> plans;
-    int rc = plan_graph(nodes, n_nodes, g, plans);
+    int rc = plan_checked(nodes, n_nodes, g, plans, false, nullptr);
     if (rc) return rc;
     for (int i = 0; i < n_nodes; ++i) {
         fused_into[i] = g.claimed[i] ? g.root[i] : -1;
@@ -1155,15 +1381,41 @@ extern "C" int dt_graph_plan(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_
     return dt_graph_plan_ex(nodes, n_nodes, fused_into, nullptr);
 }
 
-extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nodes) {
+extern "C" int dt_graph_plan_checked(dt_tensor** nodes, int32_t n_nodes, int32_t* fused_into, int32_t* runs_at,
+                                     int32_t* launches_held) {
+    using namespace dit;
+    DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0) && (fused_into || n_nodes == 0),
+               "dt_graph_plan_checked: bad arguments");
+    Graph g;
+    std::vector<Plan> plans;
+    int held = 0;
+    int rc = plan_checked(nodes, n_nodes, g, plans, true, &held);
+    if (rc) return rc;
+    for (int i = 0; i < n_nodes; ++i) {
+        fused_into[i] = g.claimed[i] ? g.root[i] : -1;
+        if (runs_at) runs_at[i] = g.runs_at[i];
+    }
+    if (launches_held) *launches_held = held;
+    return DT_OK;
+}
+
+namespace dit {
+namespace {
+thread_local int g_held = 0;
+}  // namespace
+}  // namespace dit
+
+extern "C" int dt_graph_compute_ex(dt_backend* be, dt_tensor** nodes, int32_t n_nodes, uint32_t flags) {
     using namespace dit;
     DT_REQUIRE(be != nullptr, "dt_graph_compute: null backend");
     DT_REQUIRE(n_nodes >= 0 && (nodes || n_nodes == 0), "dt_graph_compute: bad node list");
+    DT_REQUIRE((flags & ~(uint32_t)DT_GRAPH_ALLOC_RUNS_AT) == 0, "dt_graph_compute: unknown flags 0x%x", flags);
     g_kernels = 0;
     g_fused = 0;
+    g_held = 0;
     Graph g;
     std::vector<Plan> plans;
-    int rc = plan_graph(nodes, n_nodes, g, plans);
+    int rc = plan_checked(nodes, n_nodes, g, plans, !(flags & DT_GRAPH_ALLOC_RUNS_AT), &g_held);
     if (rc) return rc;
     for (int i = 0; i < n_nodes; ++i) {
         if (g.claimed[i]) {
@@ -1176,8 +1428,18 @@ extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nod
     return DT_OK;
 }
 
+extern "C" int dt_graph_compute(dt_backend* be, dt_tensor** nodes, int32_t n_nodes) {
+    return dt_graph_compute_ex(be, nodes, n_nodes, 0);
+}
+
 extern "C" int dt_graph_last_stats(int32_t* kernels_launched, int32_t* nodes_fused) {
     if (kernels_launched) *kernels_launched = dit::g_kernels;
     if (nodes_fused) *nodes_fused = dit::g_fused;
+    return DT_OK;
+}
+
+extern "C" int dt_graph_last_stats_ex(int32_t* kernels_launched, int32_t* nodes_fused, int32_t* launches_held) {
+    dt_graph_last_stats(kernels_launched, nodes_fused);
+    if (launches_held) *launches_held = dit::g_held;
     return DT_OK;
 }

@@ -1,6 +1,6 @@
 // groupnorm.hip -- GroupNorm(G, eps) + per-channel affine + SiLU over NCHW,
 // the NORM -> MUL -> ADD -> SIGMOID -> MUL chain of GroupNorm::forward
-// (GroupNorm.cpp:79-161) followed by SiLU::forward (SiLU.hpp:9-13) in the
+// (GroupNorm.cpp:25-108) followed by SiLU::forward (SiLU.hpp:9-13) in the
 // VAE decoder (ResnetBlock2D.inl:111-122, 160-171; Decoder.hpp:147-160).
 //
 // A group is C/G contiguous channels = up to 16.8 M elements, far beyond one

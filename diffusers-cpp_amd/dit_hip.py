@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint32, c_uint64, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libdit_hip.so")
@@ -24,6 +24,7 @@ F32, F16, Q8_0, Q4_K, I32, BF16 = 0, 1, 8, 12, 26, 30
  OP_ROPE, OP_CONCAT, OP_CPY, OP_VIEW, OP_FILL, OP_UNARY, OP_MUL_MAT, OP_FLASH_ATTN_EXT, OP_CONV_2D_DIRECT,
  OP_UPSCALE) = range(19)
 FLAG_OUTPUT = 1
+GRAPH_ALLOC_RUNS_AT = 1
 
 BIN_ADD, BIN_SUB, BIN_MUL, BIN_DIV = range(4)
 (UN_SIGMOID, UN_EXP, UN_LOG, UN_SQRT, UN_SIN, UN_COS, UN_SCALE, UN_CLAMP, UN_SILU,
@@ -112,6 +113,7 @@ _SIGS = {
                                         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_int64, _I64P, _I64P, _I64P, c_float, c_int32, _S]),
     "dt_graph_capture": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32, POINTER(c_void_p)]),
+    "dt_graph_capture_ex": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32, c_uint32, POINTER(c_void_p)]),
     "dt_graph_exec_launch": (c_int32, [c_void_p, c_void_p]),
     "dt_graph_exec_free": (c_int32, [c_void_p]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
@@ -136,10 +138,14 @@ _SIGS = {
     "dt_tensor_set": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
     "dt_tensor_get": (c_int32, [POINTER(DtTensor), c_void_p, c_size_t, c_size_t, _S]),
     "dt_graph_compute": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32]),
+    "dt_graph_compute_ex": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32, c_uint32]),
+    "dt_graph_plan_checked": (c_int32, [POINTER(POINTER(DtTensor)), c_int32, POINTER(c_int32), POINTER(c_int32),
+                                        POINTER(c_int32)]),
     "dt_graph_plan": (c_int32, [POINTER(POINTER(DtTensor)), c_int32, POINTER(c_int32)]),
     "dt_graph_plan_ex": (c_int32, [POINTER(POINTER(DtTensor)), c_int32, POINTER(c_int32),
                                    POINTER(c_int32)]),
     "dt_graph_last_stats": (c_int32, [POINTER(c_int32), POINTER(c_int32)]),
+    "dt_graph_last_stats_ex": (c_int32, [POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
 }
 
 _lib = None

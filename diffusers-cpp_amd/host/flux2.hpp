@@ -4,12 +4,12 @@
 // flash_attn_ext, the elementwise chain -> the fused kernels):
 //   Linear                         src/nn/Linear.cpp:8-36
 //   Timesteps                      src/diffusers/models/embeddings/Timesteps.cpp:6-45
-//   TimestepEmbedding              src/diffusers/models/embeddings/TimestepEmbedding.inl:7-48
+//   TimestepEmbedding              src/diffusers/models/embeddings/TimestepEmbedding.inl:6-44
 //   Flux2TimestepGuidanceEmbeddings  .../transformers/flux2/Flux2TimestepGuidanceEmbeddings.hpp:8-43
 //   Flux2Modulation::forward       .../flux2/Flux2Modulation.hpp:10-22
 //   ScaledDotProductAttention<FlashAttentionOp>
 //                                  src/nn/attention/ScaledDotProductAttention.hpp:6-38,
-//                                  src/nn/attention/FlashAttentionOp.cpp:6-120
+//                                  src/nn/attention/FlashAttentionOp.cpp:6-105
 //   Flux2Attention                 .../flux2/Flux2Attention.hpp:12-173
 //   Flux2FeedForward               .../flux2/Flux2FeedForward.hpp:8-82
 //   Flux2TransformerBlock          .../flux2/Flux2TransformerBlock.hpp:9-118

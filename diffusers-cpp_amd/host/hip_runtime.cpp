@@ -545,7 +545,7 @@ void HipRuntime::compute_graph() {
         if (exec_) check(dt_graph_exec_free(exec_), "dt_graph_exec_free");
         exec_ = nullptr;
         const int n = (int)order_.size();
-        if (n) check(dt_graph_capture(be_, order_.data(), n, &exec_), "dt_graph_capture");
+        if (n) check(dt_graph_capture_ex(be_, order_.data(), n, compute_flags(), &exec_), "dt_graph_capture");
         exec_gen_ = plan_gen_;
         return;
     }
@@ -559,13 +559,40 @@ void HipRuntime::compute() {
     if (!prepared_) prepare();
     upload_leaves();
     const int n = (int)order_.size();
-    if (n) check(dt_graph_compute(be_, order_.data(), n), "dt_graph_compute");
+    if (n) check(dt_graph_compute_ex(be_, order_.data(), n, compute_flags()), "dt_graph_compute");
     check(dt_backend_synchronize(be_), "dt_backend_synchronize");
-    int32_t k = 0, f = 0;
-    dt_graph_last_stats(&k, &f);
+    int32_t k = 0, f = 0, held = 0;
+    dt_graph_last_stats_ex(&k, &f, &held);
     stats_.kernels = k;
     stats_.fused_nodes = f;
+    stats_.launches_held = held;
 }
+
+void HipRuntime::set_allocation(Allocation a) {
+    if (a != alloc_) prepared_ = false;
+    alloc_ = a;
+}
+
+namespace {
+// Ops whose kernels may write their output over src[0] element for element
+// (ggml-alloc's in-place candidates among the ops recorded here).
+bool inplace_op(const Node* t) {
+    switch (t->op) {
+        case DT_OP_ADD:
+        case DT_OP_SUB:
+        case DT_OP_MUL:
+        case DT_OP_DIV:
+        case DT_OP_SCALE:
+        case DT_OP_SIGMOID:
+        case DT_OP_UNARY:
+        case DT_OP_NORM:
+        case DT_OP_RMS_NORM:
+            return true;
+        default:
+            return false;
+    }
+}
+}  // namespace
 
 void HipRuntime::prepare(bool allocate) {
     ++plan_gen_;
@@ -575,6 +602,13 @@ void HipRuntime::prepare(bool allocate) {
     //    group's first member)
     std::vector<int32_t> fused_into(n, -1), runs_at(n, 0);
     if (n) check(dt_graph_plan_ex(order_.data(), n, fused_into.data(), runs_at.data()), "dt_graph_plan_ex");
+    const bool node_order = alloc_ == Allocation::NodeOrder;
+    std::vector<int32_t> plan_fused = fused_into, plan_runs = runs_at;
+    if (node_order)  // memory follows node order; the executor adapts its plan to it
+        for (int i = 0; i < n; ++i) {
+            fused_into[i] = -1;
+            runs_at[i] = i;
+        }
 
     // 2. last use of every storage root, at the position where the reading
     //    kernel runs
@@ -608,6 +642,20 @@ void HipRuntime::prepare(bool allocate) {
     }
     for (int p = 0; p < n; ++p) {
         for (const Node* t : alloc_at[p]) {
+            // NodeOrder: over src[0]'s memory when t is its last reader and
+            // the op can run in place (same size, not an output).
+            const Node* s0 = t->src[0] ? root_of(const_cast<Node*>(t->src[0])) : nullptr;
+            if (node_order && s0 && inplace_op(t) && s0 == t->src[0] && offset.count(s0) &&
+                nbytes(s0) == nbytes(t) && last_use.count(s0) && last_use.at(s0) == p &&
+                !(s0->flags & DT_FLAG_OUTPUT)) {
+                offset[t] = offset.at(s0);
+                auto& rel = release_at[p];
+                rel.erase(std::remove(rel.begin(), rel.end(), s0), rel.end());
+                auto lu = last_use.find(t);
+                const int end = lu == last_use.end() ? p : lu->second;
+                if (end != kForever) release_at[std::max(end, p)].push_back(t);
+                continue;
+            }
             offset[t] = planner.alloc(nbytes(t));
             auto lu = last_use.find(t);
             const int end = lu == last_use.end() ? p : lu->second;
@@ -623,13 +671,39 @@ void HipRuntime::prepare(bool allocate) {
     stats_.fused_nodes = 0;
     stats_.mul_mat_nodes = stats_.attention_nodes = stats_.grouped_nodes = stats_.deferred_nodes = 0;
     for (int i = 0; i < n; ++i) {
-        stats_.fused_nodes += fused_into[i] >= 0;
-        stats_.grouped_nodes += fused_into[i] < 0 && runs_at[i] < i;
-        stats_.deferred_nodes += fused_into[i] < 0 && runs_at[i] > i;
+        stats_.fused_nodes += plan_fused[i] >= 0;
+        stats_.grouped_nodes += plan_fused[i] < 0 && plan_runs[i] < i;
+        stats_.deferred_nodes += plan_fused[i] < 0 && plan_runs[i] > i;
         stats_.mul_mat_nodes += order_[i]->op == DT_OP_MUL_MAT;
         stats_.attention_nodes += order_[i]->op == DT_OP_FLASH_ATTN_EXT;
     }
-    if (!allocate) return;
+    stats_.launches_held = 0;
+    if (!allocate) {
+        if (node_order && n) {
+            // The executor's plan for this placement, on stand-in addresses
+            // (leaves apart from the arena), without a device.
+            const uintptr_t kLeafBase = (uintptr_t)1 << 44, kArenaBase = (uintptr_t)1 << 40;
+            size_t off = 0;
+            for (Node* l : leaves_) {
+                l->data = (void*)(kLeafBase + off);
+                off += align_up(nbytes(l));
+            }
+            for (int i = 0; i < n; ++i) {
+                auto o = offset.find(order_[i]);
+                order_[i]->data = o != offset.end() ? (void*)(kArenaBase + o->second) : nullptr;
+            }
+            resolve_alias_data();
+            std::vector<int32_t> cf(n), cr(n);
+            int32_t held = 0;
+            check(dt_graph_plan_checked(order_.data(), n, cf.data(), cr.data(), &held), "dt_graph_plan_checked");
+            stats_.launches_held = held;
+            stats_.fused_nodes_checked = 0;
+            for (int i = 0; i < n; ++i) stats_.fused_nodes_checked += cf[i] >= 0;
+            for (Node* l : leaves_) l->data = nullptr;
+            for (Node* t : order_) t->data = nullptr;
+        }
+        return;
+    }
 
     // 4. device memory: leaves in their own buffer, op nodes in the arena
     if (leaf_buf_) {
@@ -662,22 +736,23 @@ void HipRuntime::prepare(bool allocate) {
         auto o = offset.find(t);
         t->data = o != offset.end() ? (char*)arena_ + o->second : nullptr;
     }
-    for (int i = 0; i < n; ++i) {
-        Node* t = order_[i];
-        if (alias_.count(t)) {
-            Node* dst = t->src[1];
-            // the destination may itself be a view: resolve its address
-            Node* r = dst;
-            int64_t extra = 0;
-            while (r->op == DT_OP_VIEW) {
-                extra += (int64_t)(uint32_t)r->op_params[0] | ((int64_t)r->op_params[1] << 32);
-                r = r->src[0];
-            }
-            t->data = r->data ? (char*)r->data + extra : nullptr;
-        }
-    }
-
+    resolve_alias_data();
     prepared_ = true;
+}
+
+// A CPY into a destination writes the destination's memory (a view's
+// address resolved through its chain).
+void HipRuntime::resolve_alias_data() {
+    for (Node* t : order_) {
+        if (!alias_.count(t)) continue;
+        Node* r = t->src[1];
+        int64_t extra = 0;
+        while (r->op == DT_OP_VIEW) {
+            extra += (int64_t)(uint32_t)r->op_params[0] | ((int64_t)r->op_params[1] << 32);
+            r = r->src[0];
+        }
+        t->data = r->data ? (char*)r->data + extra : nullptr;
+    }
 }
 
 void HipRuntime::read(const Node* node, void* host, size_t bytes) const {

@@ -3,10 +3,10 @@
 // the same node graph the reference records through its Runtime:
 //   LayerNorm      src/nn/modules/normalization/LayerNorm.cpp:16-32
 //   RMSNorm        src/nn/modules/normalization/RMSNorm.cpp:12-22
-//   GroupNorm      src/nn/modules/normalization/GroupNorm.cpp:79-161
+//   GroupNorm      src/nn/modules/normalization/GroupNorm.cpp:25-108
 //   SiLU           src/nn/SiLU.hpp:9-13
 //   Conv2d         src/nn/modules/conv/Conv2d.cpp:5-102
-//   Upsample2D     src/diffusers/models/resnet/Upsample2D.cpp:5-75
+//   Upsample2D     src/diffusers/models/resnet/Upsample2D.cpp:6-73
 //   Flux2PosEmbed  src/diffusers/models/transformers/flux2/Flux2PosEmbed.hpp:18-109
 //   Flux2SwiGLU    src/diffusers/models/transformers/flux2/Flux2SwiGLU.hpp:17-21
 //   Flux2Modulation::split  Flux2Modulation.hpp:24-41
@@ -183,7 +183,7 @@ private:
     bool bias_;
 };
 
-// Upsample2D (src/diffusers/models/resnet/Upsample2D.cpp:5-75): nearest 2x
+// Upsample2D (src/diffusers/models/resnet/Upsample2D.cpp:6-73): nearest 2x
 // upscale, then an optional 3x3 conv (padding 1).  With the conv, the
 // executor folds the upscale into the conv's input addressing.
 class Upsample2D : public Module {

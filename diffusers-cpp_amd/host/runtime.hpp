@@ -131,6 +131,8 @@ struct ComputeStats {
     int deferred_nodes = 0;     // stored outputs computed by a later node's fused kernel
     size_t arena_bytes = 0;     // op-node memory after liveness reuse
     size_t naive_bytes = 0;     // the same nodes without reuse or fusion
+    int launches_held = 0;      // fused launches the executor kept in node order (Allocation::NodeOrder)
+    int fused_nodes_checked = 0;  // plan(): nodes fused after that check (Allocation::NodeOrder)
 };
 
 // The Runtime that records dt_tensor nodes and runs them on one HIP device.
@@ -217,8 +219,21 @@ public:
     // Drop the recorded graph and its memory.
     void reset();
 
+    // How node memory is placed.  Fused (the default): the arena follows the
+    // fusion plan (absorbed nodes get no memory; outputs are placed where
+    // their kernel runs, inputs kept until their last reader's kernel), so
+    // the executor runs the plan as is (DT_GRAPH_ALLOC_RUNS_AT).  NodeOrder:
+    // every op node gets memory at its own position, released after its last
+    // reader in node order, in place over an input it is the last reader of
+    // when the op allows -- ggml_gallocr's policy (Context.hpp:118-135); the
+    // executor then checks its plan against those addresses.
+    enum class Allocation { Fused, NodeOrder };
+    void set_allocation(Allocation a);
+
     const ComputeStats& stats() const { return stats_; }
     dt_backend* backend() const { return be_; }
+    // The recorded op and view nodes in creation (= execution) order.
+    const std::vector<Node*>& nodes() const { return order_; }
     static size_t nbytes(const Node* t);
 
 private:
@@ -243,7 +258,10 @@ private:
     ComputeStats stats_;
     dt_graph_exec* exec_ = nullptr;  // compute_graph's recording
     size_t plan_gen_ = 0, exec_gen_ = 0;  // prepare() count when it was recorded
+    Allocation alloc_ = Allocation::Fused;
+    uint32_t compute_flags() const { return alloc_ == Allocation::Fused ? (uint32_t)DT_GRAPH_ALLOC_RUNS_AT : 0u; }
     void upload_leaves();
+    void resolve_alias_data();
 };
 
 // The runtime that module code uses (the reference's thread-local Scope,

@@ -90,7 +90,7 @@ int dt_adaln_mod(const void *x, int64_t rows, int64_t cols, int64_t x_stride,
  *   z = RMSNorm_eps(x[t,h,:]) * w ;  y[t,h,:] = cat_a RoPE_NORMAL(z[a-th section], pos[t,a])
  * Replaces RMSNorm::forward (src/nn/modules/normalization/RMSNorm.cpp:12-22,
  * Runtime::rms_norm at src/ggml/Runtime.hpp:277-279) on the unflattened q/k
- * (Flux2Attention.hpp:93-112, Flux2ParallelSelfAttention.hpp:181-189) and
+ * (Flux2Attention.hpp:93-112, Flux2ParallelSelfAttention.hpp:63-76) and
  * Flux2PosEmbed::forward (Flux2PosEmbed.hpp:18-109: four Runtime::rope_ext,
  * src/ggml/Runtime.hpp:281-293, mode NORMAL, plus Tensor::cat).
  * Layout: element (t, h, d) of q/k at t*tok_stride + h*head_stride + d.
@@ -179,7 +179,7 @@ int dt_dequant(const void *src, int32_t qtype, int64_t rows, int64_t cols,
 
 /* GroupNorm(groups, eps) over x[N][C][HW] (NCHW, contiguous), optional
  * per-channel affine (w, b may be NULL), then SiLU when apply_silu.
- * Replaces GroupNorm::forward (src/nn/modules/normalization/GroupNorm.cpp:79-161:
+ * Replaces GroupNorm::forward (src/nn/modules/normalization/GroupNorm.cpp:25-108:
  * reshape -> NORM -> reshape -> MUL -> ADD) and SiLU::forward
  * (SiLU.hpp:9-13) as used in ResnetBlock2D.inl:111-122, 160-171 and
  * Decoder.hpp:147-160.  `workspace` is caller-owned device memory of at
@@ -354,7 +354,7 @@ int dt_flash_attn_bf16(const void *q, const void *k, const void *v, void *o, int
  * eps and the fp32 weights, then the n_axes x axis_dim NORMAL-mode
  * rotations at the query's positions) to each query as it loads it, so the
  * normalised q is never stored and read back -- the q half of
- * Flux2Attention.hpp:93-122 / Flux2ParallelSelfAttention.hpp:181-194 folded
+ * Flux2Attention.hpp:93-122 / Flux2ParallelSelfAttention.hpp:63-76 folded
  * into FlashAttentionOp::operator() (FlashAttentionOp.cpp:84-94).
  * Queries [0, split) come from q0 (token t at q0 + b*q0_strides[0] +
  * t*q0_strides[1] + h*q0_strides[2], weights w0), queries [split, seq_q)
@@ -439,10 +439,16 @@ typedef struct dt_backend dt_backend;
  * Backend.hpp:5-31, Buffer.hpp:8-42). */
 int dt_backend_init(int32_t device_ordinal, dt_backend **out);
 int dt_backend_free(dt_backend *be);
+/* The caller's stream from now on.  A stream the backend created itself
+ * (dt_graph_capture on the NULL stream) is synchronised and destroyed; the
+ * caller's stream is never destroyed by the library. */
 int dt_backend_set_stream(dt_backend *be, dt_stream_t stream);
 int dt_backend_synchronize(dt_backend *be);
 int dt_buffer_alloc(dt_backend *be, size_t bytes, void **out);
 int dt_buffer_free(dt_backend *be, void *ptr);
+/* ggml_backend_tensor_set / get: n bytes at byte offset of a contiguous
+ * tensor; offset + n must lie within the tensor's bytes (DT_ERR_INVALID_ARG
+ * otherwise, as ggml asserts offset + size <= ggml_nbytes). */
 int dt_tensor_set(const dt_tensor *t, const void *host, size_t offset, size_t n, dt_stream_t stream);
 int dt_tensor_get(const dt_tensor *t, void *host, size_t offset, size_t n, dt_stream_t stream);
 
@@ -476,15 +482,30 @@ enum {
        set, is the destination tensor the node aliases (ggml_cpy). */
 };
 
-/* Execute nodes in order.  Before dispatch a fusion pass rewrites the
- * chains listed for the fused entry points above into single kernels when
- * the intermediate nodes are not flagged DT_FLAG_OUTPUT; every other node
- * runs its unfused kernel.  Node data is allocated by the caller
- * (ggml_gallocr's role in the reference), except that a VIEW's data is set
- * to its source's data plus its offset when the node is reached, and the
- * nodes dt_graph_plan reports as absorbed are never read or written. */
+/* Execute nodes in order (ggml_backend_graph_compute,
+ * src/ggml/ExecutionRuntime.cpp:227, 254).  Before dispatch a fusion pass
+ * rewrites the chains listed for the fused entry points above into single
+ * kernels when the intermediate nodes are not flagged DT_FLAG_OUTPUT; every
+ * other node runs its unfused kernel.  Node data is allocated by the caller
+ * (ggml_gallocr's role in the reference, Context.hpp:118-135), except that a
+ * VIEW's data is set to its source's data plus its offset when the node is
+ * reached, and the nodes the plan absorbs are never read or written.
+ *
+ * A fused launch reads its inputs and writes the outputs it keeps at its
+ * own position, which can differ from node order (a chain reads its first
+ * node's inputs at its last node; grouped GEMMs write later nodes' outputs
+ * early; see dt_graph_plan_ex).  With flags = 0 (and in dt_graph_compute)
+ * the executor therefore replays the plan over the nodes' actual address
+ * ranges first, and keeps every launch that would read memory another node
+ * has taken over (an allocator that frees after the last reader in node
+ * order, like ggml_gallocr, may do that) at its own position, or unfused:
+ * any allocation that is valid for the unfused node order is safe.
+ * DT_GRAPH_ALLOC_RUNS_AT skips that replay for callers whose allocator
+ * already follows dt_graph_plan_ex's runs_at (HipRuntime's arena). */
 enum { DT_FLAG_OUTPUT = 1 };
+enum { DT_GRAPH_ALLOC_RUNS_AT = 1 };
 int dt_graph_compute(dt_backend *be, dt_tensor **nodes, int32_t n_nodes);
+int dt_graph_compute_ex(dt_backend *be, dt_tensor **nodes, int32_t n_nodes, uint32_t flags);
 
 /* Run only the fusion pass: fused_into[i] = index of the node whose fused
  * kernel absorbs node i (node i's data is then never read or written, so it
@@ -499,9 +520,17 @@ int dt_graph_plan(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into);
  * that allocates node memory places each output at min(i, runs_at[i]) and
  * keeps inputs alive until the runs_at of their last reader. */
 int dt_graph_plan_ex(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into, int32_t *runs_at);
+/* The plan dt_graph_compute(_ex with flags = 0) runs for the nodes' current
+ * data pointers, without a device: dt_graph_plan_ex after the address-range
+ * replay; launches_held = how many launches it held at their position or
+ * kept unfused. */
+int dt_graph_plan_checked(dt_tensor **nodes, int32_t n_nodes, int32_t *fused_into, int32_t *runs_at,
+                          int32_t *launches_held);
 /* Statistics of the last dt_graph_compute on this thread: kernels launched
- * and nodes absorbed into fused kernels. */
+ * and nodes absorbed into fused kernels (_ex: and launches the address-range
+ * replay held back). */
 int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);
+int dt_graph_last_stats_ex(int32_t *kernels_launched, int32_t *nodes_fused, int32_t *launches_held);
 
 /* The launches of one dt_graph_compute recorded as a HIP graph, replayed by
  * dt_graph_exec_launch on the backend's stream: one submission per step
@@ -515,6 +544,11 @@ int dt_graph_last_stats(int32_t *kernels_launched, int32_t *nodes_fused);
  * records no memset nodes. */
 typedef struct dt_graph_exec dt_graph_exec;
 int dt_graph_capture(dt_backend *be, dt_tensor **nodes, int32_t n_nodes, dt_graph_exec **out);
+/* dt_graph_capture with dt_graph_compute_ex's flags. */
+int dt_graph_capture_ex(dt_backend *be, dt_tensor **nodes, int32_t n_nodes, uint32_t flags, dt_graph_exec **out);
+/* Refuses (DT_ERR_INVALID_ARG) an exec captured before the backend's scratch
+ * or RoPE table was last reallocated: the recorded launches hold their old
+ * addresses.  Capture again after such a change. */
 int dt_graph_exec_launch(dt_backend *be, dt_graph_exec *exec);
 int dt_graph_exec_free(dt_graph_exec *exec);
 

@@ -336,7 +336,7 @@ void or_adaln_f32(const float *x, int64_t rows, int64_t cols,
 
 /* QK-RMSNorm + Flux2PosEmbed: y = cat_a rope_a(rms_norm(x) * w).
  * Reference: RMSNorm::forward (RMSNorm.cpp:12-22) on the unflattened q/k
- * (Flux2Attention.hpp:93-112, Flux2ParallelSelfAttention.hpp:181-189), then
+ * (Flux2Attention.hpp:93-112, Flux2ParallelSelfAttention.hpp:63-76), then
  * Flux2PosEmbed::forward (Flux2PosEmbed.hpp:29-108): for axis a the dims
  * [a*axis_dim, (a+1)*axis_dim) go through rope_ext with n_dims = axis_dim
  * and position column a, and the sections are concatenated back. */
@@ -408,7 +408,7 @@ void or_gated_residual_f32(const float *h, const float *o, const float *gate,
     }
 }
 
-/* GroupNorm::forward (GroupNorm.cpp:79-161): reshape [N, G, C/G*HW], norm
+/* GroupNorm::forward (GroupNorm.cpp:25-108): reshape [N, G, C/G*HW], norm
  * per (n, g) row, reshape back, mul(x, w[1,C,1,1]), add(., b[1,C,1,1]);
  * followed by SiLU::forward (SiLU.hpp:12) as in ResnetBlock2D.inl:111-122,
  * 160-171 and Decoder.hpp:147-160. */

@@ -165,13 +165,30 @@ class Graph:
         dh.check(dh.load().dt_graph_plan(self._array(), len(self.nodes), roots), "dt_graph_plan")
         return list(roots)
 
-    def compute(self, backend, outputs=()):
+    def plan_checked(self, outputs=()):
+        """dt_graph_plan_checked on the nodes' current data pointers:
+        (per-node fused-into indices, runs_at, launches held back)."""
         for o in outputs:
             o.d.flags |= dh.FLAG_OUTPUT
-        dh.check(dh.load().dt_graph_compute(backend, self._array(), len(self.nodes)), "dt_graph_compute")
+        n = len(self.nodes)
+        roots = (ctypes.c_int32 * n)()
+        runs = (ctypes.c_int32 * n)()
+        held = ctypes.c_int32()
+        dh.check(dh.load().dt_graph_plan_checked(self._array(), n, roots, runs, ctypes.byref(held)),
+                 "dt_graph_plan_checked")
+        return list(roots), list(runs), held.value
+
+    def compute(self, backend, outputs=(), flags=0):
+        """dt_graph_compute_ex: (kernels launched, nodes fused); the launches
+        the address replay held back are in self.last_held."""
+        for o in outputs:
+            o.d.flags |= dh.FLAG_OUTPUT
+        dh.check(dh.load().dt_graph_compute_ex(backend, self._array(), len(self.nodes), flags), "dt_graph_compute")
         k = ctypes.c_int32()
         f = ctypes.c_int32()
-        dh.load().dt_graph_last_stats(ctypes.byref(k), ctypes.byref(f))
+        h = ctypes.c_int32()
+        dh.load().dt_graph_last_stats_ex(ctypes.byref(k), ctypes.byref(f), ctypes.byref(h))
+        self.last_held = h.value
         return k.value, f.value
 
 

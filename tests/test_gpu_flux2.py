@@ -92,14 +92,16 @@ def test_single_block_small(orc, tmp, dtype):
     assert stats["fused_nodes"] > 0
 
 
-def test_single_block_full_size(orc, tmp):
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_single_block_full_size(orc, tmp, dtype):
     """One Flux2-style single-stream block: hidden 3072, 24 x 128 heads, MLP
     9216, 1536 tokens (512 text with zero positions, then a 32 x 32 image
     grid), theta 2000; modulation from a N(0, 1) conditioning vector through
-    SiLU + Linear."""
-    print("single block S=512+1024 D=3072 bf16", flush=True)
-    got, want, stats = _single_block_case(orc, tmp, 512, 32, 3072, 24, 2000, "bf16", txt_zero=True)
-    check(got, want, "single block 1536x3072")
+    SiLU + Linear.  f32: fp32 activations (the elementwise kernels in fp32;
+    the GEMM and attention take bf16 operands, so the bf16 bar applies)."""
+    print(f"single block S=512+1024 D=3072 {dtype}", flush=True)
+    got, want, stats = _single_block_case(orc, tmp, 512, 32, 3072, 24, 2000, dtype, txt_zero=True)
+    check(got, want, f"single block 1536x3072 {dtype}")
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
@@ -171,6 +173,24 @@ def test_model_small(orc, tmp):
     print(f"  {stats}", flush=True)
     want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], P, cfg)
     check(read_dtb(out).reshape(n_img, 128), want, "model 1+2 blocks")
+
+
+def test_model_small_node_order_alloc(orc, tmp):
+    """--alloc node-order: node memory placed as ggml_gallocr places it (node
+    order, in place where allowed), so the executor's address replay holds
+    back fused launches that would read reused memory.  Held to the bf16 bar
+    against the oracle like the fused placement."""
+    import oracle.flux2 as of
+    cfg = SMALL_MODEL
+    P = make_params(orc, of.model_param_shapes(cfg), 5002)
+    hid, txt, pos, f = _small_model_inputs(orc, tmp)
+    n_txt, n_img = txt.shape[0], hid.shape[0]
+    out = os.path.join(tmp, "o.dtb")
+    stats = _run_small_model(f, write_params(tmp, P), out, n_img, n_txt, "--alloc", "node-order")
+    print(f"  {stats}", flush=True)
+    assert stats["alloc"] == "node-order"
+    want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], P, cfg)
+    check(read_dtb(out).reshape(n_img, 128), want, "model 1+2 blocks, node-order memory")
 
 
 def test_model_small_hip_graph(orc, tmp):

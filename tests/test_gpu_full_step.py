@@ -1,0 +1,123 @@
+"""The full Flux2-klein-4B-shaped denoising step at 1024^2 on the GPU:
+5 double + 20 single blocks, hidden 3072, 24 x 128 heads, MLP 9216, 4096
+image tokens (a 64 x 64 grid of 128-feature latents) + 512 text tokens of
+width 2560, timestep 0.5, Q8_0 random weights (Flux2Transformer2DModel::forward,
+src/diffusers/models/transformers/flux2/Flux2Transformer2DModel.cpp:111-231),
+run by dit_cli as the benchmark runs it.
+
+The full step is too large for the CPU oracle, so it is held to properties
+that do not depend on size:
+  - the output is finite, and its spread is what the random weights give:
+    proj_out has 3072 inputs of unit-variance rows times N(0, 0.02) weights,
+    std ~ 0.02 * sqrt(3072) = 1.11 (band 0.7 .. 1.6);
+  - keeping the weights as Q8_0 (dequantised inside the GEMMs) gives the bf16
+    copy path's output bit for bit;
+  - replaying the step as a HIP graph gives the eager output bit for bit;
+  - node memory placed as ggml_gallocr places it (node order), with the
+    executor holding back the launches that would read reused memory, agrees
+    with the fused placement at the bf16 bar.
+One double block at the step's shape (4608 tokens, width 3072) is checked
+against the oracle's fp32 composition (oracle/flux2.py double_block)."""
+import json
+import os
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+from conftest import bf16_metrics
+from test_gpu_flux2 import check, make_params, run_cli, write_params
+from test_gpu_fused import flux_positions
+from test_gpu_host_cli import CLI, read_dtb, write_dtb
+
+pytestmark = pytest.mark.gpu
+
+_runs = {}
+
+
+def step(tag, *extra):
+    """One full step through dit_cli (cached per flag set): (stats, output)."""
+    if tag in _runs:
+        return _runs[tag]
+    d = tempfile.mkdtemp()
+    out = os.path.join(d, "out.dtb")
+    print(f"full step [{tag}]: dit_cli Flux2Transformer2DModel {' '.join(map(str, extra))}", flush=True)
+    r = subprocess.run([CLI, "Flux2Transformer2DModel", "--random-weights", "1", "--random-inputs", "2",
+                        "--out", out, *map(str, extra)], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, f"dit_cli failed ({r.returncode}): {r.stderr[-800:]}"
+    stats = json.loads(r.stdout.strip().splitlines()[-1])
+    o = read_dtb(out)
+    print(f"  {stats['ms_per_step_median']:.2f} ms/step, output {stats['output']}", flush=True)
+    _runs[tag] = (stats, o)
+    return _runs[tag]
+
+
+def test_full_step_output_is_finite_with_the_expected_spread():
+    st, o = step("bf16")
+    assert o.shape == (1, 4096, 128)
+    out = st["output"]
+    assert out["elements"] == 4096 * 128 and out["nonfinite"] == 0
+    assert np.isfinite(o).all()
+    assert abs(out["mean"]) < 0.1 and 0.7 < out["std"] < 1.6, out
+    assert abs(float(np.std(o.astype(np.float64))) - out["std"]) < 1e-3 * out["std"]
+
+
+def test_full_step_q8_0_weights_equal_bf16_copies_bit_for_bit():
+    sb, ob = step("bf16")
+    sq, oq = step("q8_0", "--weight-format", "q8_0")
+    assert sq["weight_format"] == "q8_0" and sq["kernels"] == sb["kernels"]
+    assert sq["output"]["fnv64"] == sb["output"]["fnv64"]
+    assert np.array_equal(oq.view(np.uint32), ob.view(np.uint32))
+
+
+def test_full_step_hip_graph_replay_equals_eager_bit_for_bit():
+    sb, ob = step("bf16")
+    sg, og = step("graph", "--hip-graph", "true", "--warmup", "1", "--steps", "3")
+    assert sg["hip_graph"] is True
+    assert sg["output"]["fnv64"] == sb["output"]["fnv64"]
+    assert np.array_equal(og.view(np.uint32), ob.view(np.uint32))
+
+
+def test_full_step_node_order_allocation():
+    sb, ob = step("bf16")
+    sn, on = step("node-order", "--alloc", "node-order")
+    assert sn["alloc"] == "node-order" and sn["launches_held"] > 0
+    assert sn["output"]["nonfinite"] == 0
+    rel, cos = bf16_metrics(on, ob)
+    print(f"  node-order vs fused placement: rel_l2={rel:.3e} cos={cos:.7f}, "
+          f"{sn['launches_held']} launches held, {sn['kernels']} vs {sb['kernels']} kernels", flush=True)
+    assert rel <= 1e-2 and cos >= 0.9999
+
+
+def test_double_block_at_the_step_shape(orc):
+    """One Flux2TransformerBlock at the full step's shape: 4096 image tokens
+    (64 x 64 grid) + 512 text tokens, hidden 3072, 24 x 128 heads, MLP 9216,
+    theta 2000, bf16 activations, against oracle.flux2.double_block in fp32
+    (Flux2TransformerBlock.hpp:45-117)."""
+    import oracle.flux2 as of
+    D, heads, n_txt, grid = 3072, 24, 512, 64
+    n_img = grid * grid
+    with tempfile.TemporaryDirectory() as tmp:
+        print("double block 512+4096 D=3072 bf16", flush=True)
+        pos = flux_positions(n_txt, grid)
+        P = make_params(orc, of.double_block_param_shapes(D, heads), 6000)
+        h = orc.round_bf16(orc.randn(orc.tensor_seed(5990), (n_img, D)))
+        e = orc.round_bf16(orc.randn(orc.tensor_seed(5991), (n_txt, D)))
+        mi = orc.randn(orc.tensor_seed(5992), (6 * D,), std=0.5)
+        mt = orc.randn(orc.tensor_seed(5993), (6 * D,), std=0.5)
+        wd = write_params(tmp, P)
+        f = {n: os.path.join(tmp, n + ".dtb") for n in ("h", "e", "mi", "mt", "pos", "oe", "oh")}
+        write_dtb(f["h"], h.reshape(1, n_img, D), 0)
+        write_dtb(f["e"], e.reshape(1, n_txt, D), 0)
+        write_dtb(f["mi"], mi.reshape(1, -1), 0)
+        write_dtb(f["mt"], mt.reshape(1, -1), 0)
+        write_dtb(f["pos"], pos, 26)
+        run_cli("Flux2TransformerBlock", "--heads", heads, "--theta", 2000,
+                *sum((["--axes_dim", 32] for _ in range(4)), []), "--weights", wd, "--hidden_states", f["h"],
+                "--encoder_hidden_states", f["e"], "--temb_mod_img", f["mi"], "--temb_mod_txt", f["mt"],
+                "--position_ids", f["pos"], "--dtype", "bf16", "--out-encoder", f["oe"], "--out-hidden", f["oh"])
+        print("  oracle ...", flush=True)
+        we, wh = of.double_block(h, e, mi, mt, pos, P, heads, 2000.0, 32)
+        check(read_dtb(f["oh"]).reshape(n_img, D), wh, "double block 4608x3072 hidden")
+        check(read_dtb(f["oe"]).reshape(n_txt, D), we, "double block 4608x3072 encoder")

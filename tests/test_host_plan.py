@@ -71,3 +71,15 @@ def test_per_block_fusion(kind, layers, nodes, fused, mm, grouped, deferred):
     assert b["attention_nodes"] - a["attention_nodes"] == 1
     assert b["grouped_nodes"] - a["grouped_nodes"] == grouped
     assert b["deferred_nodes"] - a["deferred_nodes"] == deferred
+
+
+def test_node_order_allocation_keeps_most_fusion():
+    """The full step with node memory placed as ggml_gallocr places it (node
+    order, in place where allowed; dit_cli --alloc node-order): the
+    executor's address replay holds back the launches that would read
+    memory another node took over, and keeps the rest fused."""
+    p = plan(alloc="node-order")
+    f = plan()
+    assert f["launches_held"] == 0 and p["fused_nodes"] == f["fused_nodes"]
+    assert 0 < p["launches_held"] < 100, p
+    assert p["fused_nodes_checked"] > 0.7 * p["fused_nodes"], p
