@@ -151,8 +151,8 @@ def _small_model_inputs(orc, tmp, n_txt=16, grid=8):
     return hid, txt, pos, f
 
 
-def _run_small_model(f, wd, out, n_img, n_txt, *extra):
-    return run_cli("Flux2Transformer2DModel", "--num_layers", 1, "--num_single_layers", 2,
+def _run_small_model(f, wd, out, n_img, n_txt, *extra, layers=(1, 2)):
+    return run_cli("Flux2Transformer2DModel", "--num_layers", layers[0], "--num_single_layers", layers[1],
                    "--num_attention_heads", 2, "--joint_attention_dim", 128, "--img_tokens", n_img,
                    "--txt_tokens", n_txt, "--weights", wd, "--hidden_states", f["h"],
                    "--encoder_hidden_states", f["t"], "--timestep", f["ts"], "--img_ids", f["ii"],
