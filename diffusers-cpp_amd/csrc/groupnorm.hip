@@ -12,8 +12,18 @@
 //   2. apply: each workgroup first sums its group's partials in a fixed
 //      order (every workgroup of a group gets bit-identical statistics),
 //      then streams its chunk: y = silu(((x - mean) * rstd) * w_c + b_c).
-// The second read of x is launched right behind the first, so tensors that
-// fit the 256 MB last-level cache are re-read from there.
+// x is read twice (1.5x the algorithmic bytes).  Measured on gfx950: stats
+// loads that allocate in the caches, and running the two passes group batch
+// by group batch so the re-read could come from the 256 MB last-level cache,
+// were both slower than streaming both reads; a single pass holding the whole
+// map in registers across the chip (per-group barrier) was no faster on the
+// maps that fit, where fixed launch and ramp costs dominate.
+//
+// The apply math is y = silu((x - mean) * (rstd * w_c) + b_c): one exact
+// subtraction and one fma, then x / (1 + 2^(-x log2 e)) by the hardware exp2
+// and reciprocal (relative error ~1e-6 against the graph's separately
+// rounded NORM, MUL, ADD, SIGMOID, MUL).  The exactly rounded form took
+// ~35 VALU instructions per element and made the bf16 passes VALU-bound.
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -22,7 +32,7 @@ namespace dit {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kVecsPerThread = 8;            // vectors per thread per chunk
+constexpr int kVecsPerThread = 4;            // vectors per thread per chunk
 constexpr int kChunkVecs = kBlock * kVecsPerThread;
 
 struct GnShape {
@@ -87,7 +97,14 @@ __global__ __launch_bounds__(kBlock) void gn_stats_kernel(const T* __restrict__ 
     }
 }
 
-// y = silu(((x - mean) * rstd) * w_c + b_c) over this workgroup's chunk of
+// x / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal.  Large
+// negative x: the exponential overflows to inf and the result is -0.
+__device__ __forceinline__ float silu_fast(float t) {
+    const float e = __builtin_amdgcn_exp2f(t * -1.4426950408889634f);
+    return t * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// y = silu((x - mean) * (rstd * w_c) + b_c) over this workgroup's chunk of
 // group (n, g).
 template <typename T, bool VEC>
 __device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int n, int g, float mean, float rstd,
@@ -117,14 +134,11 @@ __device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int
         if constexpr (VEC) Io<T>::unpack(raw[i], a);
         else a[0] = Io<T>::get(xg + v);
         const int64_t c = c0 + (int64_t)fdiv((uint32_t)v, hw_vecs);
-        const float wc = w ? w[c] : 1.0f, bc = b ? b[c] : 0.0f;
+        const float sa = w ? rstd * w[c] : rstd, bc = b ? b[c] : 0.0f;
 #pragma unroll
         for (int e = 0; e < EPV; ++e) {
-            float t = mul_rn(sub_rn(a[e], mean), rstd);
-            if (w) t = mul_rn(t, wc);
-            if (b) t = add_rn(t, bc);
-            if (s.apply_silu) t = mul_rn(t, sigmoid_ref(t));
-            a[e] = t;
+            const float t = __builtin_fmaf(a[e] - mean, sa, bc);
+            a[e] = s.apply_silu ? silu_fast(t) : t;
         }
         if constexpr (VEC) Io<T>::store(yg + v * EPV, a);
         else Io<T>::put(yg + v, a[0]);
@@ -238,20 +252,36 @@ extern "C" size_t dt_groupnorm_workspace_bytes(int64_t N, int64_t C, int64_t HW,
     return (size_t)(N * groups * (2 * nchunks + 1)) * sizeof(double);
 }
 
+static int gn_check_shape(const char* what, const void* x, const void* y, int64_t N, int64_t C, int64_t HW,
+                          int64_t groups, int32_t io_type) {
+    DT_REQUIRE(dit::is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
+    DT_REQUIRE(N > 0 && C > 0 && HW > 0 && groups > 0 && C % groups == 0,
+               "%s: bad shape N=%lld C=%lld HW=%lld groups=%lld", what, (long long)N, (long long)C,
+               (long long)HW, (long long)groups);
+    DT_REQUIRE(x && y, "%s: null pointer", what);
+    DT_REQUIRE(N * groups < 65536, "%s: N*groups must be < 65536", what);
+    return DT_OK;
+}
+
+static int gn_run(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups, const float* w, const float* b,
+                  float eps, int32_t apply_silu, void* y, void* workspace, int32_t io_type, dt_stream_t stream);
+
 extern "C" int dt_groupnorm_silu(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups,
                                  const float* w, const float* b, float eps, int32_t apply_silu,
                                  void* y, void* workspace, size_t workspace_bytes, int32_t io_type,
                                  dt_stream_t stream) {
-    DT_REQUIRE(dit::is_io_type(io_type), "dt_groupnorm_silu: io_type %d unsupported", io_type);
-    DT_REQUIRE(N > 0 && C > 0 && HW > 0 && groups > 0 && C % groups == 0,
-               "dt_groupnorm_silu: bad shape N=%lld C=%lld HW=%lld groups=%lld", (long long)N,
-               (long long)C, (long long)HW, (long long)groups);
-    DT_REQUIRE(x && y && workspace, "dt_groupnorm_silu: null pointer");
+    int rc = gn_check_shape("dt_groupnorm_silu", x, y, N, C, HW, groups, io_type);
+    if (rc) return rc;
+    DT_REQUIRE(workspace, "dt_groupnorm_silu: null workspace");
     DT_REQUIRE(workspace_bytes >= dt_groupnorm_workspace_bytes(N, C, HW, groups),
                "dt_groupnorm_silu: workspace too small (%zu < %zu)", workspace_bytes,
                dt_groupnorm_workspace_bytes(N, C, HW, groups));
     DT_REQUIRE(((uintptr_t)workspace & 7) == 0, "dt_groupnorm_silu: workspace must be 8-byte aligned");
-    DT_REQUIRE(N * groups < 65536, "dt_groupnorm_silu: N*groups must be < 65536");
+    return gn_run(x, N, C, HW, groups, w, b, eps, apply_silu, y, workspace, io_type, stream);
+}
+
+static int gn_run(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups, const float* w, const float* b,
+                  float eps, int32_t apply_silu, void* y, void* workspace, int32_t io_type, dt_stream_t stream) {
     const bool vec = gn_vec_ok(HW, io_type) && dit::aligned16(x) && dit::aligned16(y);
     const int epv = vec ? (io_type == DT_TYPE_BF16 ? 8 : 4) : 1;
     dit::GnShape s;

@@ -190,6 +190,7 @@ int dt_groupnorm_silu(const void *x, int64_t N, int64_t C, int64_t HW, int64_t g
                       void *y, void *workspace, size_t workspace_bytes,
                       int32_t io_type, dt_stream_t stream);
 
+
 /* Euler step of FlowMatchEulerDiscreteScheduler::integrate
  * (src/diffusers/schedulers/FlowMatchEulerDiscreteScheduler.cpp:210-222):
  * y = x + dt * v over n contiguous elements. */

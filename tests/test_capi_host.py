@@ -124,8 +124,8 @@ def test_rope_table_matches_oracle_cache(orc):
 
 def test_groupnorm_workspace_bytes():
     lib = dit_hip.load()
-    # one (K, sum, sumsq per chunk) record per (n, g), chunks of 2048 elements
-    assert lib.dt_groupnorm_workspace_bytes(1, 128, 1024 * 1024, 32) == 32 * (2 * 2048 + 1) * 8
+    # one (K, sum, sumsq per chunk) record per (n, g), chunks of 1024 elements (the scalar path's)
+    assert lib.dt_groupnorm_workspace_bytes(1, 128, 1024 * 1024, 32) == 32 * (2 * 4096 + 1) * 8
     assert lib.dt_groupnorm_workspace_bytes(2, 4, 9, 2) == 2 * 2 * (2 * 1 + 1) * 8
     assert lib.dt_groupnorm_workspace_bytes(1, 30, 16, 32) == 0
 
