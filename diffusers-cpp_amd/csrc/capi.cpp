@@ -90,6 +90,9 @@ extern "C" int dt_backend_init(int32_t device_ordinal, dt_backend** out) {
     DT_REQUIRE(device_ordinal >= 0 && device_ordinal < n, "dt_backend_init: device %d of %d",
                device_ordinal, n);
     DT_HIP(hipSetDevice(device_ordinal), "dt_backend_init");
+    void* noalloc = nullptr;  // dt_groupnorm_silu_noalloc's device scratch, resolved for this device now
+    const int rc = dit::noalloc_scratch(&noalloc);
+    if (rc) return rc;
     auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f, false, 0};
     *out = be;
     return DT_OK;

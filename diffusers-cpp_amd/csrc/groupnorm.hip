@@ -24,6 +24,8 @@
 // and reciprocal (relative error ~1e-6 against the graph's separately
 // rounded NORM, MUL, ADD, SIGMOID, MUL).  The exactly rounded form took
 // ~35 VALU instructions per element and made the bf16 passes VALU-bound.
+#include <mutex>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -252,6 +254,16 @@ extern "C" size_t dt_groupnorm_workspace_bytes(int64_t N, int64_t C, int64_t HW,
     return (size_t)(N * groups * (2 * nchunks + 1)) * sizeof(double);
 }
 
+// Workspace bytes the launch for these pointers needs: the vector path's
+// chunk count when x and y take 16-byte vectors, else the scalar path's.
+static size_t gn_workspace_needed(const void* x, const void* y, int64_t N, int64_t C, int64_t HW, int64_t groups,
+                                  int32_t io_type) {
+    const bool vec = gn_vec_ok(HW, io_type) && dit::aligned16(x) && dit::aligned16(y);
+    const int epv = vec ? (io_type == DT_TYPE_BF16 ? 8 : 4) : 1;
+    const int64_t nchunks = dit::chunks_for(C / groups * HW / epv);
+    return (size_t)(N * groups * (2 * nchunks + 1)) * sizeof(double);
+}
+
 static int gn_check_shape(const char* what, const void* x, const void* y, int64_t N, int64_t C, int64_t HW,
                           int64_t groups, int32_t io_type) {
     DT_REQUIRE(dit::is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
@@ -278,6 +290,64 @@ extern "C" int dt_groupnorm_silu(const void* x, int64_t N, int64_t C, int64_t HW
                dt_groupnorm_workspace_bytes(N, C, HW, groups));
     DT_REQUIRE(((uintptr_t)workspace & 7) == 0, "dt_groupnorm_silu: workspace must be 8-byte aligned");
     return gn_run(x, N, C, HW, groups, w, b, eps, apply_silu, y, workspace, io_type, stream);
+}
+
+// ---- the variant that allocates nothing ---------------------------------------
+//
+// Its statistics workspace is this file-scope device array: each device the
+// library runs on holds one copy, at its own address, until the process
+// ends.  Host code uses the address hipGetSymbolAddress reports for the
+// current device (resolved once per device, at dt_backend_init or at the
+// first call), never the array's name.  Every call on a device shares that
+// device's copy: calls that overlap on one device (other streams) race.
+// Nothing in it has to start at zero: each call's statistics pass writes
+// every slot its apply pass reads.
+static __device__ __align__(256) unsigned char scratch[DT_GROUPNORM_NOALLOC_SCRATCH_BYTES];
+
+namespace dit {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// The current device's address of `scratch`, resolved once per device.
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(DT_ERR_HIP, "dt_groupnorm_silu_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    DT_REQUIRE(dev >= 0 && dev < kMaxDevices, "dt_groupnorm_silu_noalloc: device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (r != hipSuccess || !p)
+            return fail(DT_ERR_HIP, "dt_groupnorm_silu_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                        hipGetErrorString(r));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DT_OK;
+}
+
+}  // namespace dit
+
+extern "C" int dt_groupnorm_silu_noalloc(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups,
+                                         const float* w, const float* b, float eps, int32_t apply_silu, void* y,
+                                         int32_t io_type, dt_stream_t stream) {
+    int rc = gn_check_shape("dt_groupnorm_silu_noalloc", x, y, N, C, HW, groups, io_type);
+    if (rc) return rc;
+    const size_t need = gn_workspace_needed(x, y, N, C, HW, groups, io_type);
+    DT_REQUIRE(need <= (size_t)DT_GROUPNORM_NOALLOC_SCRATCH_BYTES,
+               "dt_groupnorm_silu_noalloc: N=%lld C=%lld HW=%lld groups=%lld needs %zu bytes of statistics, "
+               "beyond its %zu-byte device scratch (use dt_groupnorm_silu with a workspace)",
+               (long long)N, (long long)C, (long long)HW, (long long)groups, need,
+               (size_t)DT_GROUPNORM_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    rc = dit::noalloc_scratch(&ws);
+    if (rc) return rc;
+    return gn_run(x, N, C, HW, groups, w, b, eps, apply_silu, y, ws, io_type, stream);
 }
 
 static int gn_run(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups, const float* w, const float* b,

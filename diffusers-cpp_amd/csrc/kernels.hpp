@@ -78,6 +78,9 @@ int qk_swiglu_launch(const void* q, const void* k, void* q_out, void* k_out, con
 // (groupnorm.hip) merges the records into the head.
 inline int64_t gn_tile_stats_head_bytes(int64_t N, int64_t G) { return (N * G * 16 + 255) / 256 * 256; }
 int gn_tile_stats_finalize(const void* stats, int64_t N, int64_t groups, int64_t n_tiles, hipStream_t st);
+// The current device's address of dt_groupnorm_silu_noalloc's scratch array
+// (resolved once per device).
+int noalloc_scratch(void** out);
 
 // Backend accessors (capi.cpp).
 hipStream_t backend_stream(dt_backend* be);

@@ -82,6 +82,8 @@ _SIGS = {
     "dt_groupnorm_silu": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p,
                                     c_void_p, c_float, c_int32, c_void_p, c_void_p, c_size_t,
                                     c_int32, _S]),
+    "dt_groupnorm_silu_noalloc": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                            c_float, c_int32, c_void_p, c_int32, _S]),
     "dt_euler_step": (c_int32, [c_void_p, c_void_p, c_float, c_void_p, c_int64, c_int32, _S]),
     "dt_fill_randn": (c_int32, [c_void_p, c_int64, c_uint64, c_float, c_float, _S]),
     "dt_quantize_q8_0": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, _S]),
@@ -389,6 +391,18 @@ def groupnorm_silu(x, groups, w=None, b=None, eps=1e-6, silu=True, out=None, wor
     check(lib.dt_groupnorm_silu(_p(x), N, C, HW, groups, _p(w), _p(b), eps, 1 if silu else 0,
                                 _p(y), _p(workspace), workspace.numel(), io_type(x), stream()),
           "dt_groupnorm_silu")
+    return y
+
+
+def groupnorm_silu_noalloc(x, groups, w=None, b=None, eps=1e-6, silu=True, out=None):
+    """groupnorm_silu through dt_groupnorm_silu_noalloc (the library's own
+    device scratch; nothing allocated but the output when out is None)."""
+    torch = _torch()
+    N, C, H, W = x.shape
+    y = torch.empty_like(x) if out is None else out
+    check(load().dt_groupnorm_silu_noalloc(_p(x), N, C, H * W, groups, _p(w), _p(b), eps, 1 if silu else 0,
+                                           _p(y), io_type(x), stream()),
+          "dt_groupnorm_silu_noalloc")
     return y
 
 

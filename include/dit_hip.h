@@ -190,6 +190,21 @@ int dt_groupnorm_silu(const void *x, int64_t N, int64_t C, int64_t HW, int64_t g
                       void *y, void *workspace, size_t workspace_bytes,
                       int32_t io_type, dt_stream_t stream);
 
+/* dt_groupnorm_silu without a workspace argument and without allocating:
+ * no counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The statistics live in a device array of
+ * DT_GROUPNORM_NOALLOC_SCRATCH_BYTES the library holds on every device it
+ * runs on until the process ends; maps needing more statistics space (the
+ * bytes dt_groupnorm_workspace_bytes would give for the vector path, e.g.
+ * fp32 [1, 256, 1024, 1024] needs 1.05 MB) return DT_ERR_INVALID_ARG.  All
+ * calls on one device share that array: calls that overlap on one device
+ * (concurrent streams) race.  Same results as dt_groupnorm_silu, bit for
+ * bit. */
+#define DT_GROUPNORM_NOALLOC_SCRATCH_BYTES (2u << 20)
+int dt_groupnorm_silu_noalloc(const void *x, int64_t N, int64_t C, int64_t HW, int64_t groups,
+                              const float *w, const float *b, float eps, int32_t apply_silu, void *y,
+                              int32_t io_type, dt_stream_t stream);
 
 /* Euler step of FlowMatchEulerDiscreteScheduler::integrate
  * (src/diffusers/schedulers/FlowMatchEulerDiscreteScheduler.cpp:210-222):
