@@ -14,10 +14,9 @@ written once at its I/O dtype (broadcast vectors and tables counted once).
 
 Timed steps rotate through NSETS independent buffer sets (about 1.9 GB in
 all, far above the 256 MB last-level cache), so every step reads its inputs
-from HBM.  Three schedules of the same step are timed: eager launches, a
-HIP graph of the two launches, and a HIP graph with the two launches on
-parallel branches; `value` = whole-step algorithmic GB/s of the fastest
-(all three are reported).  Each schedule is timed after at least --warmup
+from HBM.  Two schedules of the same step are timed: eager launches and a
+HIP graph of the two launches; `value` = whole-step algorithmic GB/s of the
+faster (both are reported).  Each schedule is timed after at least --warmup
 untimed steps of itself and at least 0.2 s of them, so the clocks have
 settled (`warmup_steps_run` reports how many ran).  The same block order
 with the four standalone kernels (gated residual, adaLN of r, QK, SwiGLU)
@@ -27,10 +26,15 @@ is timed as a graph for comparison.
 launches with the two fused launches' exact access shapes on the same
 buffers (16-byte non-temporal loads and stores), timed the same ways;
 `frac_of_stream_probe` = probe time / chain time (per step, and per launch
-under `kernels`).  `roofline` is the dominant launch (QK+SwiGLU) timed alone
-with HIP events on the stream it is launched on; `cpu_baseline` is the
+under `kernels`).  `roofline` is the dominant launch (QK+SwiGLU): its mean
+duration over back-to-back launches cycling the buffer sets, HIP events
+around the run on the stream it is launched on (single cold launches, which
+add the dispatch latency, are reported beside it).  `cpu_baseline` is the
 oracle's C restatement of the same chain (fp32, OpenMP) on a bounded
-sample, timed on this host's cores.
+sample, timed on this host's cores; `other_workloads` holds the same for the
+single-stream block (1536 x 3072, with the block's GPU time beside it), the
+weight dequantisation and the GroupNorm maps.  `secondary` times the
+dequantisation and GroupNorm kernels the same two ways.
 
 `sec_per_denoise_step` is one full Flux2-klein-4B-shaped transformer step
 (5 double + 20 single blocks, hidden 3072, 24x128 heads, 4096 image tokens of
@@ -50,6 +54,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -168,6 +173,30 @@ def time_cold(torch, fn, n, flush, samples=False):
     return ts if samples else statistics.median(ts)
 
 
+def time_stream(torch, fns, reps):
+    """Per-launch time of back-to-back launches cycling over fns (one closure
+    per buffer set; the sets together exceed the 256 MB last-level cache, so
+    every launch reads from HBM), HIP events around the whole run on the
+    launch stream: what a kernel costs inside a step, without the dispatch
+    latency an event pair around a single launch adds."""
+    st = torch.cuda.current_stream()
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(reps):
+        fns[i % len(fns)]()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def _sets_for(set_bytes, cap=16):
+    """Buffer sets whose total exceeds 1 GiB (4x the last-level cache)."""
+    return int(max(2, min(cap, -(-(1 << 30) // set_bytes))))
+
+
 def probe_kernels(t):
     """Trivial-math launches with the two fused launches' access shapes on
     the same buffers (diffusers-cpp_amd/probe/stream_probe.hip): h, o -> r, y;
@@ -212,39 +241,58 @@ def copy_ceiling(torch, dev, flush):
     return 2 * src.numel() / t / 1e9
 
 
+DEQ_SHAPES = ((3072, 9216), (9216, 3072), (3072, 3072))      # the weight-dequantisation workload
+GN_SHAPES = ((1, 512, 128, 128), (1, 512, 256, 256), (1, 256, 512, 512), (1, 128, 1024, 1024))
+GN_DECODER_EXTRA = ((1, 512, 512, 512), (1, 256, 1024, 1024))   # the decoder's other GroupNorm maps
+
+
 def secondary(torch, dev, flush):
-    """Configs measured beside the chain: weight dequantisation (3072x9216,
-    Q8_0 and Q4_K -> bf16) and the VAE GroupNorm(32)+SiLU shapes."""
+    """Configs measured beside the chain: weight dequantisation (Q8_0 and
+    Q4_K -> bf16 at the three matrix shapes) and GroupNorm(32)+SiLU at the
+    four VAE-decoder workload shapes and the decoder's two other map sizes."""
     import dit_hip
     out = {}
-    rows, cols = 3072, 9216
-    for name, qt, qk, bs in (("dequant_q8_0_3072x9216_bf16", dit_hip.Q8_0, 32, 34),
-                             ("dequant_q4_K_3072x9216_bf16", dit_hip.Q4_K, 256, 144)):
-        src = torch.randint(0, 256, (rows * cols // qk * bs,), dtype=torch.uint8, device=dev)
-        view = src.view(-1, bs)
-        view[:, 1] &= 0x3B                    # keep fp16 scales finite
-        if qt == dit_hip.Q4_K:
-            view[:, 3] &= 0x3B
-        y = torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)
-        t = time_cold(torch, lambda: dit_hip.dequant(src, qt, rows, cols, out=y), 10, flush)
-        nbytes = src.numel() + y.numel() * 2
-        out[name] = {"us": round(t * 1e6, 2), "alg_MB": round(nbytes / 1e6, 2),
-                     "GBs": round(nbytes / t / 1e9, 1), "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3)}
-    for shape in ((1, 512, 128, 128), (1, 512, 256, 256), (1, 256, 512, 512), (1, 128, 1024, 1024)):
+    def entry(nbytes, t_stream, t_single):
+        return {"us": round(t_stream * 1e6, 2), "alg_MB": round(nbytes / 1e6, 2),
+                "GBs": round(nbytes / t_stream / 1e9, 1), "frac_hbm": round(nbytes / t_stream / 1e9 / HBM_PEAK_GBS, 3),
+                "us_single_launch": round(t_single * 1e6, 2),
+                "frac_hbm_single_launch": round(nbytes / t_single / 1e9 / HBM_PEAK_GBS, 3)}
+
+    for rows, cols in DEQ_SHAPES:
+        for tag, qt, qk, bs in (("q8_0", dit_hip.Q8_0, 32, 34), ("q4_K", dit_hip.Q4_K, 256, 144)):
+            name = f"dequant_{tag}_{rows}x{cols}_bf16"
+            nbytes = rows * cols // qk * bs + rows * cols * 2
+            sets = []
+            for _ in range(_sets_for(nbytes)):
+                src = torch.randint(0, 256, (rows * cols // qk * bs,), dtype=torch.uint8, device=dev)
+                view = src.view(-1, bs)
+                view[:, 1] &= 0x3B                    # keep fp16 scales finite
+                if qt == dit_hip.Q4_K:
+                    view[:, 3] &= 0x3B
+                sets.append((src, torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)))
+            fns = [lambda s_=s_, y_=y_: dit_hip.dequant(s_, qt, rows, cols, out=y_) for s_, y_ in sets]
+            t = time_stream(torch, fns, 4 * len(fns))
+            t1 = time_cold(torch, fns[0], 10, flush)
+            out[name] = entry(nbytes, t, t1)
+            del sets, fns
+    for shape in GN_SHAPES + GN_DECODER_EXTRA:
         for dt, es in ((torch.float32, 4), (torch.bfloat16, 2)):
-            x = torch.randn(shape, device=dev).to(dt)
+            numel = shape[0] * shape[1] * shape[2] * shape[3]
+            nbytes = 2 * numel * es
             w = torch.randn(shape[1], device=dev) * 0.02 + 1
             b = torch.randn(shape[1], device=dev) * 0.02
-            y = torch.empty_like(x)
             ws = torch.empty(dit_hip.load().dt_groupnorm_workspace_bytes(1, shape[1], shape[2] * shape[3], 32),
                              dtype=torch.uint8, device=dev)
-            t = time_cold(torch, lambda: dit_hip.groupnorm_silu(x, 32, w, b, 1e-6, out=y, workspace=ws), 6, flush)
-            nbytes = 2 * x.numel() * es
+            sets = [(torch.randn(shape, device=dev).to(dt), torch.empty(shape, dtype=dt, device=dev))
+                    for _ in range(_sets_for(nbytes, 8))]
+            fns = [lambda x_=x_, y_=y_: dit_hip.groupnorm_silu(x_, 32, w, b, 1e-6, out=y_, workspace=ws)
+                   for x_, y_ in sets]
+            t = time_stream(torch, fns, 4 * len(fns))
+            t1 = time_cold(torch, fns[0], 6, flush)
             name = "groupnorm_silu_" + "x".join(map(str, shape)) + ("_f32" if es == 4 else "_bf16")
-            out[name] = {"us": round(t * 1e6, 2), "alg_MB": round(nbytes / 1e6, 2),
-                         "GBs": round(nbytes / t / 1e9, 1), "frac_hbm": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 3)}
-            del x, y
-    out["vae"] = vae_measurements(torch, dev, flush)
+            out[name] = entry(nbytes, t, t1)
+            del sets, fns
+            torch.cuda.empty_cache()
     return out
 
 
@@ -345,6 +393,167 @@ def cpu_baseline(budget_s):
     return total / t_all / 1e9, threads, sample, total / t_4 / 1e9
 
 
+def _threads():
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    return max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+
+
+def _median_time(fn, budget, max_runs=50):
+    """Median wall time of fn() over as many runs as fit in `budget` seconds
+    (at least one, after one untimed run when the budget allows)."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    times = [first]
+    if first * 3 < budget:
+        times = []
+        t_end = time.perf_counter() + budget
+        while time.perf_counter() < t_end and len(times) < max_runs:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+CFG1 = dict(n_txt=512, grid=32, dim=3072, heads=24, theta=2000.0)
+
+
+def config1_inputs():
+    """The single-stream block workload: 1536 tokens (512 text tokens at
+    position 0, then a 32 x 32 image grid), hidden 3072, 24 x 128 heads, MLP
+    9216, theta 2000; Linear weights N(0, 0.02), RMSNorm weights N(1, 0.02),
+    activations N(0, 1), modulation = SiLU + Linear of a N(0, 1) vector."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    import oracle.flux2 as of
+    D, heads = CFG1["dim"], CFG1["heads"]
+    txt = [[0, 0, 0, 0]] * CFG1["n_txt"]
+    img = [[0, y, x, 0] for y in range(CFG1["grid"]) for x in range(CFG1["grid"])]
+    pos = np.array(txt + img, dtype=np.int32)
+    from concurrent.futures import ThreadPoolExecutor
+
+    def draw(item):  # one seeded stream per tensor, drawn in parallel (the C generator releases the GIL)
+        i, (name, shape) = item
+        seed = oracle.tensor_seed(100 + i)
+        return name, (oracle.randn(seed, shape, std=0.02) if len(shape) == 2 else
+                      oracle.randn(seed, shape, mean=1.0, std=0.02))
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        P = dict(ex.map(draw, enumerate(sorted(of.single_block_param_shapes(D, heads).items()))))
+    x = oracle.randn(oracle.tensor_seed(90), (pos.shape[0], D))
+    cond = oracle.randn(oracle.tensor_seed(91), (1, D))
+    mod = oracle.linear(of.silu(cond), oracle.randn(oracle.tensor_seed(92), (3 * D, D), std=0.02))
+    return x, mod.reshape(-1), pos, P
+
+
+def config1_gpu(x, mod, pos, P, dtype):
+    """The same block through dit_cli Flux2SingleTransformerBlock (weights
+    uploaded once and kept in HBM; inputs uploaded before each run): median
+    ms per forward, or None when the driver is missing."""
+    import tempfile
+    import numpy as np
+    cli = os.path.join(PKG, "bin", "dit_cli")
+    if not os.path.exists(cli):
+        return None
+
+    def dtb(path, a, type_id):
+        a = np.ascontiguousarray(a)
+        with open(path, "wb") as f:
+            f.write(np.array([0x31425444, type_id, a.ndim, 0], np.int32).tobytes())
+            f.write(np.array(a.shape, np.int64).tobytes())
+            f.write(a.tobytes())
+
+    with tempfile.TemporaryDirectory() as d:
+        wd = os.path.join(d, "w")
+        os.makedirs(wd)
+        for name, a in P.items():
+            dtb(os.path.join(wd, name + ".dtb"), a.astype(np.float32), 0)
+        S, D = x.shape
+        dtb(os.path.join(d, "x.dtb"), x.reshape(1, S, D).astype(np.float32), 0)
+        dtb(os.path.join(d, "mod.dtb"), mod.reshape(1, -1).astype(np.float32), 0)
+        dtb(os.path.join(d, "pos.dtb"), pos, 26)
+        cmd = [cli, "Flux2SingleTransformerBlock", "--heads", str(CFG1["heads"]), "--theta", str(int(CFG1["theta"]))]
+        for _ in range(4):
+            cmd += ["--axes_dim", "32"]
+        cmd += ["--weights", wd, "--hidden_states", os.path.join(d, "x.dtb"), "--temb_mod",
+                os.path.join(d, "mod.dtb"), "--position_ids", os.path.join(d, "pos.dtb"), "--dtype", dtype,
+                "--out", os.path.join(d, "out.dtb"), "--resident-weights", "true", "--warmup", "3", "--steps", "10"]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            raise RuntimeError(f"dit_cli block failed ({r.returncode}): {r.stderr.strip()[-500:]}")
+        return json.loads(r.stdout.strip().splitlines()[-1])["ms_per_compute_median"]
+
+
+def cpu_configs(budget, with_gpu_block):
+    """CPU baselines of the other workloads on the oracle's C restatement
+    (fp32), each at all of this host's cores and at 4 threads (ggml's default
+    n_threads): the single-stream block (1536 x 3072, timed beside the same
+    block on the GPU), the dequantisation of the three weight matrices (Q8_0
+    and Q4_K to fp32 values) and GroupNorm(32)+SiLU at the four decoder map
+    shapes."""
+    import numpy as np
+    sys.path.insert(0, ROOT)
+    import oracle
+    import oracle.flux2 as of
+    threads = _threads()
+    out = {}
+
+    x, mod, pos, P = config1_inputs()
+    flop = 2.0 * x.shape[0] * sum(a.size for a in P.values() if a.ndim == 2) + 4.0 * x.shape[0] ** 2 * x.shape[1]
+    blk = lambda t: of.single_block(x, mod, pos, P, CFG1["heads"], CFG1["theta"], 32, threads=t)
+    t_all, n_all = _median_time(lambda: blk(threads), budget / 3)
+    t_4, n_4 = _median_time(lambda: blk(4), budget / 3, max_runs=3)
+    c1 = {"unit": "s per block forward", "value": round(t_all, 4), "cores": threads, "value_4_threads": round(t_4, 4),
+          "gflop_per_forward": round(flop / 1e9, 1), "cpu_gflops": round(flop / t_all / 1e9, 1),
+          "sample": f"one Flux2 single-stream block forward, fp32, 1536 tokens x 3072 (median of {n_all} runs at "
+                    f"{threads} threads / {n_4} at 4 threads)"}
+    if with_gpu_block:
+        for dt in ("bf16", "f32"):
+            ms = config1_gpu(x, mod, pos, P, dt)
+            if ms is not None:
+                c1[f"gpu_ms_{dt}_activations"] = round(ms, 3)
+                c1[f"gpu_speedup_{dt}_vs_all_cores"] = round(t_all / (ms * 1e-3), 1)
+    out["single_block_1536x3072_f32"] = c1
+    del P, x
+
+    deq = {}
+    w = oracle.randn(oracle.tensor_seed(200), (3072 * 9216,), std=0.02)
+    # block k covers flat elements [qk k, qk (k + 1)) for any row width that is a multiple of qk
+    quant = {qt: oracle.quantize(w.reshape(-1, 3072), qt) for qt in (8, 12)}
+    for rows, cols in DEQ_SHAPES:
+        for tag, qt, qk, bs in (("q8_0", 8, 32, 34), ("q4_K", 12, 256, 144)):
+            blocks = quant[qt][:rows * cols // qk * bs]     # the same bytes a [rows, cols] matrix quantises to
+            nbytes = blocks.size + rows * cols * 2          # the GPU's bytes: blocks in, bf16 out
+            y = np.zeros(rows * cols, np.float32)            # reused, as ggml reuses its buffers
+            ta, _ = _median_time(lambda: oracle.dequantize(blocks, rows * cols, qt, threads, y), budget / 30)
+            t4, _ = _median_time(lambda: oracle.dequantize(blocks, rows * cols, qt, 4, y), budget / 30)
+            deq[f"{tag}_{rows}x{cols}"] = {"GBs": round(nbytes / ta / 1e9, 2), "GBs_4_threads": round(nbytes / t4 / 1e9, 2),
+                                            "ms": round(ta * 1e3, 2)}
+    out["dequant"] = {"unit": "GB/s over the GPU kernel's bytes (blocks in, bf16 out)", "cores": threads,
+                      "sample": "each matrix dequantised whole to fp32 (median over ~1/30 of the budget each)",
+                      "matrices": deq}
+
+    gn = {}
+    for shape in GN_SHAPES:
+        xg = oracle.randn(oracle.tensor_seed(300), shape)
+        wg = oracle.randn(oracle.tensor_seed(301), (shape[1],), mean=1.0, std=0.02)
+        bg = oracle.randn(oracle.tensor_seed(302), (shape[1],), std=0.02)
+        nbytes = 2 * xg.size * 4
+        yg = np.zeros_like(xg)                               # reused, as ggml reuses its buffers
+        ta, _ = _median_time(lambda: oracle.groupnorm_silu(xg, 32, wg, bg, 1e-6, True, threads, yg), budget / 16)
+        t4, _ = _median_time(lambda: oracle.groupnorm_silu(xg, 32, wg, bg, 1e-6, True, 4, yg), budget / 16)
+        gn["x".join(map(str, shape))] = {"GBs": round(nbytes / ta / 1e9, 2), "GBs_4_threads": round(nbytes / t4 / 1e9, 2),
+                                          "ms": round(ta * 1e3, 2)}
+        del xg, yg
+    out["groupnorm_silu_f32"] = {"unit": "GB/s over fp32 in + out", "cores": threads,
+                                 "sample": "each map normalised whole (median over ~1/16 of the budget each)",
+                                 "maps": gn}
+    return out
+
+
 def denoise_flops(n_img=4096, n_txt=512, d=3072, mlp=9216, blocks=25, txt_width=2560, ch=128):
     """FLOP of one step: every Linear (2*M*N*K) and attention (4*S^2*d per block)."""
     s = n_img + n_txt
@@ -418,6 +627,12 @@ def main():
     ap.add_argument("--denoise-warmup", type=int, default=2)
     ap.add_argument("--vae-only", action="store_true",
                     help="print only the VAE conv / GroupNorm measurements (one JSON line)")
+    ap.add_argument("--secondary-only", action="store_true",
+                    help="print only the dequantisation / GroupNorm measurements and the copy calibration "
+                         "(one JSON line; the profiled workload of the dequant and GroupNorm summaries)")
+    ap.add_argument("--cpu-configs-budget", type=float, default=24.0,
+                    help="seconds of CPU baselines for the block, dequantisation and GroupNorm workloads "
+                         "(0 disables)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this benchmark measures one GPU only (--gpus {args.gpus} requested); "
@@ -425,13 +640,22 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    if args.vae_only:
+    if args.vae_only or args.secondary_only:
         import torch
         import dit_hip
         dit_hip.load()
         dev = torch.device("cuda:0")
-        print(json.dumps({"vae": vae_measurements(torch, dev, Flusher(torch, dev))}), flush=True)
+        flush = Flusher(torch, dev)
+        if args.vae_only:
+            print(json.dumps({"vae": vae_measurements(torch, dev, flush)}), flush=True)
+        else:
+            print(json.dumps({"secondary": secondary(torch, dev, flush),
+                              "copy_ceiling_GBs": round(copy_ceiling(torch, dev, flush), 1)}), flush=True)
         return
+
+    # The CPU baselines of the other workloads run before this process
+    # touches the GPU (the block's GPU timing is a child process).
+    cpu_other = cpu_configs(args.cpu_configs_budget, args.denoise_steps > 0) if args.cpu_configs_budget > 0 else None
 
     # The full step runs in its own process before this one touches the GPU.
     denoise = denoise_step(args.denoise_steps, args.denoise_warmup) if args.denoise_steps > 0 else None
@@ -510,25 +734,10 @@ def main():
     warm_steps["graph"] = warm(lambda i: graphs[i % NSETS].replay())
     seq_s, seq_wall = timed(lambda i: graphs[i % NSETS].replay())
 
-    # The same step with the two (independent) launches on parallel branches.
-    branch_stream = torch.cuda.Stream()
-
-    def branched(i):
-        c = chains[i % NSETS]
-        main = torch.cuda.current_stream()
-        branch_stream.wait_stream(main)
-        with torch.cuda.stream(branch_stream):
-            c["qk_swiglu"]()
-        c["residual_adaln"]()
-        main.wait_stream(branch_stream)
-
-    bgraphs = capture(branched)
-    warm_steps["graph_branched"] = warm(lambda i: bgraphs[i % NSETS].replay())
-    br_s, br_wall = timed(lambda i: bgraphs[i % NSETS].replay())
-    schedules = {"eager": eager_s, "graph": seq_s, "graph_branched": br_s}
+    schedules = {"eager": eager_s, "graph": seq_s}
     best = min(schedules, key=schedules.get)
     step_s = schedules[best]
-    wall = {"eager": eager_wall, "graph": seq_wall, "graph_branched": br_wall}[best]
+    wall = {"eager": eager_wall, "graph": seq_wall}[best]
 
     # The streaming ceiling: the probe launches with the chain's shapes, timed
     # the same ways (eager steps over the rotating buffer sets; cold launches).
@@ -551,7 +760,7 @@ def main():
     ugraphs = capture(unfused)
     warm(lambda i: ugraphs[i % NSETS].replay())
     unfused_s, _ = timed(lambda i: ugraphs[i % NSETS].replay())
-    del graphs, bgraphs, ugraphs
+    del graphs, ugraphs
 
     fused_ab, single_ab = alg_bytes()
     total = sum(fused_ab.values())
@@ -569,13 +778,26 @@ def main():
         return res
 
     kernels = cold(chains[0], fused_ab)
+    # Each launch alone, back to back over the buffer sets (HIP events around
+    # the run): its average duration inside a stream of launches.
+    for name in kernels:
+        ts = time_stream(torch, [c[name] for c in chains], 40 * NSETS)
+        kernels[name]["us_stream_mean"] = round(ts * 1e6, 2)
+        kernels[name]["GBs_stream"] = round(fused_ab[name] / ts / 1e9, 1)
+        kernels[name]["frac_hbm_stream"] = round(fused_ab[name] / ts / 1e9 / HBM_PEAK_GBS, 4)
     probe_cold = {name: time_cold(torch, fn, 20, flush) for name, fn in probes[0].items()}
     for name, k in kernels.items():
         k["stream_probe_us"] = round(probe_cold[name] * 1e6, 2)
         k["frac_of_stream_probe"] = round(probe_cold[name] * 1e6 / k["us"], 3)
     kernels_standalone = cold(singles[0], single_ab)
+    for name in kernels_standalone:
+        ts = time_stream(torch, [c[name] for c in singles], 40 * NSETS)
+        kernels_standalone[name]["us_stream_mean"] = round(ts * 1e6, 2)
+        kernels_standalone[name]["frac_hbm_stream"] = round(single_ab[name] / ts / 1e9 / HBM_PEAK_GBS, 4)
     ceiling = copy_ceiling(torch, dev, flush)
     extra = secondary(torch, dev, flush) if args.secondary else None
+    if extra is not None:
+        extra["vae"] = vae_measurements(torch, dev, flush)
 
     dom = "qk_swiglu"
     traffic = None
@@ -584,19 +806,24 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("bytes_per_launch")
     kd = kernels[dom]
-    roofline = {"bound": "hbm", "achieved": kd["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(kd["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+    roofline = {"bound": "hbm", "achieved": kd["GBs_stream"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(kd["GBs_stream"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": "qk_swiglu_kernel<bf16,3>", "alg_bytes_per_launch": fused_ab[dom],
-                "statistic": "median of 20 launches, each timed by HIP events on its launch stream after a "
-                             "1 GiB cache flush",
-                "launch_us": {"median": kd["us"], "mean": kd["us_mean"], "min": kd["us_min"]},
-                "frac_at_mean": round(fused_ab[dom] / (kd["us_mean"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                "statistic": f"mean launch duration over {40 * NSETS} back-to-back launches cycling {NSETS} buffer "
+                             f"sets (HIP events around the run, on the launch stream)",
+                "launch_us_stream_mean": kd["us_stream_mean"],
+                "single_cold_launch_us": {"median": kd["us"], "mean": kd["us_mean"], "min": kd["us_min"],
+                                          "statistic": "20 launches, each bracketed by HIP events after a "
+                                                       "1 GiB cache flush (adds the dispatch latency)"},
+                "frac_single_cold_median": round(kd["GBs"] / HBM_PEAK_GBS, 4)}
 
     cpu = None
     if args.cpu_budget > 0:
         v, cores, sample, v4 = cpu_baseline(args.cpu_budget)
         cpu = {"value": round(v, 2), "unit": "GB/s", "cores": cores, "kind": "port",
                "sample": sample, "value_4_threads": round(v4, 2)}
+        if cpu_other:
+            cpu["other_workloads"] = cpu_other
 
     value = total / step_s / 1e9
     out = {

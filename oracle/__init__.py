@@ -60,9 +60,9 @@ def load():
                                          c_int, P, c_int]),
         "or_euler_f32": (None, [P, P, c_float, c_int64, P]),
         "or_quantize_q8_0": (None, [P, c_int64, P]),
-        "or_dequant_q8_0_f32": (None, [P, c_int64, P]),
+        "or_dequant_q8_0_f32": (None, [P, c_int64, P, c_int]),
         "or_quantize_q4_K": (None, [P, c_int64, P]),
-        "or_dequant_q4_K_f32": (None, [P, c_int64, P]),
+        "or_dequant_q4_K_f32": (None, [P, c_int64, P, c_int]),
         "or_q4_K_scale_min": (None, [c_int, P, P, P]),
         "or_conv2d_f32": (None, [P, c_int64, c_int64, c_int64, c_int64, P, c_int64, c_int64, c_int64, P,
                                  c_int, P, c_int]),
@@ -252,11 +252,12 @@ def gated_residual(h, o, gate, threads=0):
     return y
 
 
-def groupnorm_silu(x, groups, w=None, b=None, eps=1e-6, silu=True, threads=0):
+def groupnorm_silu(x, groups, w=None, b=None, eps=1e-6, silu=True, threads=0, out=None):
     x = _f32(x)
     N, C = x.shape[0], x.shape[1]
     HW = x.size // (N * C)
-    y = np.empty_like(x)
+    y = np.empty_like(x) if out is None else out
+    assert y.shape == x.shape and y.dtype == np.float32 and y.flags["C_CONTIGUOUS"]
     wp = _p(_f32(w)) if w is not None else None
     bp = _p(_f32(b)) if b is not None else None
     load().or_groupnorm_silu_f32(_p(x), N, C, HW, groups, wp, bp, eps, 1 if silu else 0, _p(y),
@@ -327,11 +328,12 @@ def quantize(x, qtype: int) -> np.ndarray:
     return out
 
 
-def dequantize(b, n: int, qtype: int) -> np.ndarray:
+def dequantize(b, n: int, qtype: int, threads=0, out=None) -> np.ndarray:
     b = np.ascontiguousarray(b, dtype=np.uint8)
-    out = np.empty(n, dtype=np.float32)
+    out = np.empty(n, dtype=np.float32) if out is None else out
+    assert out.size == n and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
     fn = load().or_dequant_q8_0_f32 if qtype == 8 else load().or_dequant_q4_K_f32
-    fn(_p(b), n, _p(out))
+    fn(_p(b), n, _p(out), threads)
     return out
 
 

@@ -99,9 +99,9 @@ def _adaln_mul_first(x, shift, scale, eps):
     return adaln(x, shift, scale, eps)
 
 
-def _qk(x, w, pos, heads, axes_dim, theta, eps):
+def _qk(x, w, pos, heads, axes_dim, theta, eps, threads=0):
     S = x.shape[0]
-    return qk_rmsnorm_rope(x.reshape(S, heads, -1), w, pos, axes_dim, theta, eps)
+    return qk_rmsnorm_rope(x.reshape(S, heads, -1), w, pos, axes_dim, theta, eps, threads)
 
 
 def timestep_proj(t, channels=256, flip_sin_to_cos=True, shift=0.0):
@@ -116,24 +116,27 @@ def timestep_proj(t, channels=256, flip_sin_to_cos=True, shift=0.0):
 
 # ---- blocks ---------------------------------------------------------------------
 
-def single_block(x, temb_mod, pos, P, heads, theta, axes_dim=32, eps=1e-6, prefix=""):
-    """x [S, D], temb_mod [3D], pos int32 [S, 4] -> [S, D]."""
+def single_block(x, temb_mod, pos, P, heads, theta, axes_dim=32, eps=1e-6, prefix="", threads=0):
+    """x [S, D], temb_mod [3D], pos int32 [S, 4] -> [S, D] (threads: OpenMP
+    threads of every op, 0 = all)."""
     x = np.asarray(x, np.float32)
     S, D = x.shape
     a = prefix + "attn."
+    t = threads
     shift, scale, gate = _split_mod(temb_mod, 1)[0]
-    n = adaln(x, shift, scale, eps)
-    q = linear(n, P[a + "to_qkv_mlp_proj.q.weight"])
-    k = linear(n, P[a + "to_qkv_mlp_proj.k.weight"])
-    v = linear(n, P[a + "to_qkv_mlp_proj.v.weight"])
-    g = linear(n, P[a + "to_qkv_mlp_proj.mlp_in_gate.weight"])
-    u = linear(n, P[a + "to_qkv_mlp_proj.mlp_in_up.weight"])
-    q = _qk(q, P[a + "norm_q.weight"], pos, heads, axes_dim, theta, eps)
-    k = _qk(k, P[a + "norm_k.weight"], pos, heads, axes_dim, theta, eps)
-    o = attention(q, k, v.reshape(S, heads, -1)).reshape(S, D)
-    m = swiglu(g, u)
-    y = (linear(o, P[a + "to_out.attn.weight"]) + linear(m, P[a + "to_out.mlp.weight"])).astype(np.float32)
-    return gated_residual(x, y, gate)
+    n = adaln(x, shift, scale, eps, t)
+    q = linear(n, P[a + "to_qkv_mlp_proj.q.weight"], threads=t)
+    k = linear(n, P[a + "to_qkv_mlp_proj.k.weight"], threads=t)
+    v = linear(n, P[a + "to_qkv_mlp_proj.v.weight"], threads=t)
+    g = linear(n, P[a + "to_qkv_mlp_proj.mlp_in_gate.weight"], threads=t)
+    u = linear(n, P[a + "to_qkv_mlp_proj.mlp_in_up.weight"], threads=t)
+    q = _qk(q, P[a + "norm_q.weight"], pos, heads, axes_dim, theta, eps, t)
+    k = _qk(k, P[a + "norm_k.weight"], pos, heads, axes_dim, theta, eps, t)
+    o = attention(q, k, v.reshape(S, heads, -1), threads=t).reshape(S, D)
+    m = swiglu(g, u, t)
+    y = (linear(o, P[a + "to_out.attn.weight"], threads=t) +
+         linear(m, P[a + "to_out.mlp.weight"], threads=t)).astype(np.float32)
+    return gated_residual(x, y, gate, t)
 
 
 def double_block(h, e, mod_img, mod_txt, pos, P, heads, theta, axes_dim=32, eps=1e-6, prefix=""):

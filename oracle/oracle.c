@@ -468,7 +468,8 @@ void or_quantize_q8_0(const float *x, int64_t n, uint8_t *dst) {
 }
 
 /* Q8_0 dequantisation: y = fp16_to_fp32(d) * q, one IEEE rounding. */
-void or_dequant_q8_0_f32(const uint8_t *src, int64_t n, float *y) {
+void or_dequant_q8_0_f32(const uint8_t *src, int64_t n, float *y, int nthreads) {
+#pragma omp parallel for schedule(static) OR_OMP_THREADS(nthreads)
     for (int64_t blk = 0; blk < n / 32; ++blk) {
         const uint8_t *b = src + blk * 34;
         uint16_t dh;
@@ -495,7 +496,8 @@ void or_q4_K_scale_min(int j, const uint8_t *q, uint8_t *sc, uint8_t *m) {
  * qs[32c .. 32c+32) give elements [64c, 64c+32) with sub-block 2c, the high
  * nibbles give [64c+32, 64c+64) with sub-block 2c+1;
  * y = (d * sc) * q - (dmin * m), each product and the difference rounded. */
-void or_dequant_q4_K_f32(const uint8_t *src, int64_t n, float *y) {
+void or_dequant_q4_K_f32(const uint8_t *src, int64_t n, float *y, int nthreads) {
+#pragma omp parallel for schedule(static) OR_OMP_THREADS(nthreads)
     for (int64_t blk = 0; blk < n / 256; ++blk) {
         const uint8_t *b = src + blk * 144;
         uint16_t dh, mh;

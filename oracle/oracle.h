@@ -109,9 +109,9 @@ void or_euler_f32(const float *x, const float *v, float dt, int64_t n, float *y)
  * Q4_K: 256-element super-blocks {fp16 d; fp16 dmin; u8 scales[12];
  *       u8 qs[128]} = 144 bytes. n is the element count. */
 void or_quantize_q8_0(const float *x, int64_t n, uint8_t *dst);
-void or_dequant_q8_0_f32(const uint8_t *src, int64_t n, float *y);
+void or_dequant_q8_0_f32(const uint8_t *src, int64_t n, float *y, int nthreads);
 void or_quantize_q4_K(const float *x, int64_t n, uint8_t *dst);
-void or_dequant_q4_K_f32(const uint8_t *src, int64_t n, float *y);
+void or_dequant_q4_K_f32(const uint8_t *src, int64_t n, float *y, int nthreads);
 void or_q4_K_scale_min(int j, const uint8_t *scales12, uint8_t *sc, uint8_t *m);
 
 /* ---- small helpers used by the timed CPU baseline ----------------------- */
