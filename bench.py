@@ -192,6 +192,21 @@ def time_stream(torch, fns, reps):
     return e0.elapsed_time(e1) * 1e-3 / reps
 
 
+def raw_calls(fn, arg_sets):
+    """One closure per argument tuple calling the C ABI function directly,
+    so the back-to-back loop of time_stream spends no Python wrapper time
+    between launches (kernels of a few microseconds would otherwise wait on
+    the host); each call's status is checked once here."""
+    import functools
+    calls = [functools.partial(fn, *a) for a in arg_sets]
+    for c in calls:
+        rc = c()
+        if rc != 0:
+            import dit_hip
+            raise RuntimeError(f"{fn.__name__} failed ({rc}): {dit_hip.load().dt_last_error().decode()}")
+    return calls
+
+
 def _sets_for(set_bytes, cap=16):
     """Buffer sets whose total exceeds 1 GiB (4x the last-level cache)."""
     return int(max(2, min(cap, -(-(1 << 30) // set_bytes))))
@@ -270,7 +285,9 @@ def secondary(torch, dev, flush):
                 if qt == dit_hip.Q4_K:
                     view[:, 3] &= 0x3B
                 sets.append((src, torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)))
-            fns = [lambda s_=s_, y_=y_: dit_hip.dequant(s_, qt, rows, cols, out=y_) for s_, y_ in sets]
+            fns = raw_calls(dit_hip.load().dt_dequant,
+                            [(s_.data_ptr(), qt, rows, cols, cols // qk * bs, y_.data_ptr(), cols, dit_hip.BF16,
+                              dit_hip.stream()) for s_, y_ in sets])
             t = time_stream(torch, fns, 4 * len(fns))
             t1 = time_cold(torch, fns[0], 10, flush)
             out[name] = entry(nbytes, t, t1)
@@ -285,8 +302,10 @@ def secondary(torch, dev, flush):
                              dtype=torch.uint8, device=dev)
             sets = [(torch.randn(shape, device=dev).to(dt), torch.empty(shape, dtype=dt, device=dev))
                     for _ in range(_sets_for(nbytes, 8))]
-            fns = [lambda x_=x_, y_=y_: dit_hip.groupnorm_silu(x_, 32, w, b, 1e-6, out=y_, workspace=ws)
-                   for x_, y_ in sets]
+            fns = raw_calls(dit_hip.load().dt_groupnorm_silu,
+                            [(x_.data_ptr(), shape[0], shape[1], shape[2] * shape[3], 32, w.data_ptr(), b.data_ptr(),
+                              1e-6, 1, y_.data_ptr(), ws.data_ptr(), ws.numel(), dit_hip.io_type(x_),
+                              dit_hip.stream()) for x_, y_ in sets])
             t = time_stream(torch, fns, 4 * len(fns))
             t1 = time_cold(torch, fns[0], 6, flush)
             name = "groupnorm_silu_" + "x".join(map(str, shape)) + ("_f32" if es == 4 else "_bf16")

@@ -192,7 +192,35 @@ public:
     void param(const Tensor& p, const std::string& key) {
         Blob b = read_blob(args.str("param-" + key));
         if (b.type != DT_TYPE_F32) throw std::runtime_error("parameters are F32");
+        if (p.dtype() == DT_TYPE_CONV2D_PACKED) {
+            if (!plan_only) pack_conv_weight(p, b);
+            return;
+        }
         rt.bind(*p, b.bytes.data(), b.bytes.size());
+    }
+    // A Conv2d weight [Co, Ci, K, K] from fp32 values, packed once on the
+    // device into the layout dt_conv2d reads, in a buffer the weight keeps.
+    void pack_conv_weight(const Tensor& p, const Blob& b) {
+        const Tensor::Shape& s = p.shape();
+        const int64_t Co = s[0], Ci = s[1], K = s[2];
+        if (b.shape != s || b.bytes.size() != (size_t)(Co * Ci * K * K * 4))
+            throw std::runtime_error("packed conv weight: shape mismatch");
+        dt_tensor tmp{};
+        tmp.type = DT_TYPE_F32;
+        tmp.ne[0] = tmp.ne[1] = K;
+        tmp.ne[2] = Ci;
+        tmp.ne[3] = Co;
+        tmp.nb[0] = 4;
+        tmp.nb[1] = K * 4;
+        tmp.nb[2] = K * K * 4;
+        tmp.nb[3] = Ci * K * K * 4;
+        tmp.data = dev.alloc(b.bytes.size());
+        check(dt_tensor_set(&tmp, b.bytes.data(), 0, b.bytes.size(), nullptr), "dt_tensor_set");
+        void* dst = dev.alloc(dt_conv2d_packed_bytes(Co, Ci, K));
+        check(dt_conv2d_pack_weights(tmp.data, DT_TYPE_F32, Co, Ci, K, dst, nullptr), "dt_conv2d_pack_weights");
+        check(dt_backend_synchronize(rt.backend()), "dt_backend_synchronize");
+        dev.release(tmp.data);
+        rt.bind_device(*p, dst);
     }
     // An input converted to `type` on the host (e.g. F32 files for BF16 graphs).
     Tensor input_as(const std::string& key, int32_t type) {
@@ -727,8 +755,10 @@ void run(const Args& a) {
         if (a.flag("silu", false)) y = SiLU().forward(y);   // ResnetBlock2D.inl:111-122
         s.output(y, "out");
     } else if (c == "Conv2d") {
-        // Conv2d.py: --in_channels, --out_channels, --kernel_size, --stride, --padding, --bias
+        // Conv2d.py: --in_channels, --out_channels, --kernel_size, --stride, --padding, --bias;
+        // --packed-weights true packs the weight once at load (DT_TYPE_CONV2D_PACKED)
         const bool bias = a.flag("bias", true);
+        ConvWeightType cw(a.flag("packed-weights", false) ? DT_TYPE_CONV2D_PACKED : DT_TYPE_F32);
         Conv2d m(a.i64("in_channels"), a.i64("out_channels"), a.i64("kernel_size"), a.i64("stride", 1),
                  a.i64("padding", 0), bias);
         Tensor x = s.input("x");
@@ -738,6 +768,7 @@ void run(const Args& a) {
     } else if (c == "Upsample2D") {
         // Upsample2D.py: --channels, --use_conv, --out_channels
         const bool use_conv = a.flag("use_conv", false);
+        ConvWeightType cw(a.flag("packed-weights", false) ? DT_TYPE_CONV2D_PACKED : DT_TYPE_F32);
         Upsample2D m(a.i64("channels"), use_conv, a.i64("out_channels", -1));
         Tensor x = s.input("hidden_states");
         if (use_conv) {

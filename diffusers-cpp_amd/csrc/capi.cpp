@@ -164,7 +164,10 @@ static bool tensor_bytes(const dt_tensor* t, size_t* out) {
     else if (t->type == DT_TYPE_Q8_0) row = (t->ne[0] + 31) / 32 * 34;
     else if (t->type == DT_TYPE_Q4_K) row = (t->ne[0] + 255) / 256 * 144;
     else if (t->type == DT_TYPE_Q8_0_SPLIT) row = -1;
-    else return false;
+    else if (t->type == DT_TYPE_CONV2D_PACKED) {
+        *out = dt_conv2d_packed_bytes(t->ne[3], t->ne[2], t->ne[0]);
+        return t->ne[1] == t->ne[0] && *out > 0;
+    } else return false;
     if (t->ne[0] < 0) return false;
     *out = row < 0 ? dt_q8_0_split_bytes(t->ne[1], t->ne[0]) * (size_t)(t->ne[2] * t->ne[3])
                    : (size_t)(row * n);

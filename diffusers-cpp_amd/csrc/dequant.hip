@@ -171,18 +171,18 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_staged_kernel(cons
 
 // Dense tensors (rows packed back to back in the source and the output) are
 // one stream of blocks: workgroup i decodes blocks [SEG * i, SEG * i + SEG)
-// with SEG = kFlatUnroll x the staged kernels' run, so each workgroup keeps
-// 17 KB (Q8_0) / 9 KB (Q4_K) of loads in flight -- a run of one row per
-// workgroup leaves too little in flight per CU to cover HBM latency (runs
-// of 4x and 16x measured slower than 8x).  The
-// bytes past the last whole 16-byte vector of the tensor are copied in 2-byte
-// pieces, so nothing past the tensor is read.
+// with SEG = U x the staged kernels' run.  At U = 8 a workgroup keeps 17 KB
+// (Q8_0) / 9 KB (Q4_K) of loads in flight, the fastest run for tensors that
+// fill the chip (4x and 16x measured slower at 3072 x 9216); smaller tensors
+// take a shorter run (flat_unroll).  The bytes past the last whole 16-byte
+// vector of the tensor are copied in 2-byte pieces, so nothing past the
+// tensor is read.
 constexpr int kFlatUnroll = 8;
 
-template <typename T>
+template <typename T, int U>
 __global__ __launch_bounds__(kStageThreads) void dequant_q8_0_flat_kernel(const uint8_t* __restrict__ src,
                                                                           int64_t nblocks, T* __restrict__ dst) {
-    constexpr int SEG = kQ8SegBlocks * kFlatUnroll;
+    constexpr int SEG = kQ8SegBlocks * U;
     __shared__ __attribute__((aligned(16))) uint4 stage[SEG * 34 / 16];
     const int t = threadIdx.x;
     const int64_t b0 = (int64_t)blockIdx.x * SEG;
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q8_0_flat_kernel(const 
         reinterpret_cast<uint16_t*>(stage)[nvec * 8 + t] = reinterpret_cast<const uint16_t*>(base + 16 * nvec)[t];
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < kFlatUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
         const int blk = u * kQ8SegBlocks + (t >> 2), part = t & 3;
         if (blk < nblk) {
             const uint16_t* h = reinterpret_cast<const uint16_t*>(stage) + blk * 17;
@@ -211,19 +211,22 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q8_0_flat_kernel(const 
     }
 }
 
-template <typename T>
+template <typename T, int U>
 __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_flat_kernel(const uint8_t* __restrict__ src,
                                                                           int64_t nblocks, T* __restrict__ dst) {
-    constexpr int SEG = kQ4SegBlocks * kFlatUnroll;
+    constexpr int SEG = kQ4SegBlocks * U;
     __shared__ __attribute__((aligned(16))) uint4 stage[SEG * 9];
     const int t = threadIdx.x;
     const int64_t b0 = (int64_t)blockIdx.x * SEG;
     const int nblk = (int)min<int64_t>(SEG, nblocks - b0);
     const uint8_t* base = src + b0 * 144;
-    for (int i = t; i < nblk * 9; i += kStageThreads) stage[i] = ld_stream(base + 16 * i);
+    // default (cache-allocating) loads: the super-blocks are 22% of the bytes
+    // moved, and measured 4% faster than streaming loads at 3072 x 3072 (equal
+    // at 3072 x 9216); Q8_0's blocks stay streamed (faster at both sizes)
+    for (int i = t; i < nblk * 9; i += kStageThreads) stage[i] = *reinterpret_cast<const uint4*>(base + 16 * i);
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < kFlatUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
         const int sb = u * kQ4SegBlocks + (t >> 5), k = t & 31;
         if (sb < nblk) {
             const uint32_t e0 = k * 8;
@@ -255,21 +258,48 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_flat_kernel(const 
     }
 }
 
+// Runs per workgroup of the flat kernels: the smallest unroll whose
+// workgroups are all resident at once (8 workgroups of 4 waves per CU), so no
+// CU starts a second round while others idle; a tensor too large for one
+// round runs in rounds of kFlatUnroll.  Measured back to back on 3072 x 3072:
+// U = 4 (1152 workgroups) 6.2 / 5.4 us against U = 8 (576, two or three per
+// CU) 7.5 / 6.4 us for Q8_0 / Q4_K, and U = 2 (2304, a second round) slower
+// again; on 3072 x 9216, U = 8 (1728) is the fastest.
+constexpr int kFlatResidentPerCu = 8;
+
+int flat_unroll(int64_t nblocks, int64_t seg_blocks) {
+    const int64_t slots = (int64_t)cu_count() * kFlatResidentPerCu;
+    for (int u = 1; u < kFlatUnroll; u *= 2)
+        if ((nblocks + seg_blocks * u - 1) / (seg_blocks * u) <= slots) return u;
+    return kFlatUnroll;
+}
+
+template <typename T, int U>
+void launch_flat(bool q8, const void* src, int64_t nblocks, void* dst, hipStream_t st) {
+    const int64_t seg = (q8 ? kQ8SegBlocks : kQ4SegBlocks) * U;
+    const dim3 grid((unsigned)((nblocks + seg - 1) / seg));
+    if (q8)
+        hipLaunchKernelGGL((dequant_q8_0_flat_kernel<T, U>), grid, dim3(kStageThreads), 0, st, (const uint8_t*)src,
+                           nblocks, (T*)dst);
+    else
+        hipLaunchKernelGGL((dequant_q4_K_flat_kernel<T, U>), grid, dim3(kStageThreads), 0, st, (const uint8_t*)src,
+                           nblocks, (T*)dst);
+}
+
 template <typename T>
 int run(const void* src, int32_t qtype, int64_t rows, int64_t cols, int64_t row_bytes, void* dst,
         int64_t dst_stride, hipStream_t st) {
     {
         const bool q8 = qtype == DT_TYPE_Q8_0;
-        const int64_t qk = q8 ? 32 : 256, bsz = q8 ? 34 : 144;
-        const int64_t seg = (q8 ? kQ8SegBlocks : kQ4SegBlocks) * kFlatUnroll;
-        const int64_t nblocks = rows * (cols / qk), wgs = (nblocks + seg - 1) / seg;
-        if (aligned16(src) && row_bytes == cols / qk * bsz && dst_stride == cols && wgs < (1ll << 31)) {
-            if (q8)
-                hipLaunchKernelGGL((dequant_q8_0_flat_kernel<T>), dim3((unsigned)wgs), dim3(kStageThreads), 0, st,
-                                   (const uint8_t*)src, nblocks, (T*)dst);
-            else
-                hipLaunchKernelGGL((dequant_q4_K_flat_kernel<T>), dim3((unsigned)wgs), dim3(kStageThreads), 0, st,
-                                   (const uint8_t*)src, nblocks, (T*)dst);
+        const int64_t qk = q8 ? 32 : 256, bsz = q8 ? 34 : 144, per = q8 ? kQ8SegBlocks : kQ4SegBlocks;
+        const int64_t nblocks = rows * (cols / qk);
+        if (aligned16(src) && row_bytes == cols / qk * bsz && dst_stride == cols && nblocks / per < (1ll << 31)) {
+            switch (flat_unroll(nblocks, per)) {
+                case 1: launch_flat<T, 1>(q8, src, nblocks, dst, st); break;
+                case 2: launch_flat<T, 2>(q8, src, nblocks, dst, st); break;
+                case 4: launch_flat<T, 4>(q8, src, nblocks, dst, st); break;
+                default: launch_flat<T, kFlatUnroll>(q8, src, nblocks, dst, st); break;
+            }
             return check_launch("dt_dequant");
         }
     }
@@ -422,7 +452,8 @@ extern "C" int dt_q8_0_split(const void* src, int64_t rows, int64_t cols, int64_
     DT_REQUIRE((reinterpret_cast<uintptr_t>(src) & 1) == 0 && dit::aligned16(codes),
                "dt_q8_0_split: src must be 2-byte and codes 16-byte aligned");
     const int64_t total = rows * (cols / 32);
-    DT_REQUIRE(total < (1ll << 32), "dt_q8_0_split: too many blocks");
+    // the row of a block comes from fdiv, which is exact for numerators below 2^31
+    DT_REQUIRE(total < (1ll << 31), "dt_q8_0_split: %lld blocks exceed the 2^31 limit", (long long)total);
     hipLaunchKernelGGL(dit::q8_0_split_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, (const uint8_t*)src, row_bytes, (uint8_t*)codes, ld_codes, scales,
                        ld_scales, (uint32_t)total, dit::make_fastdiv((uint32_t)(cols / 32)));

@@ -6,8 +6,9 @@
 // issued before any math) with non-temporal (streaming) accesses;
 // consecutive threads take consecutive vectors so every wave instruction
 // touches 1 KB of contiguous HBM, and the row index of a vector comes from a
-// multiply-high invariant division.  U = 2 with 512-thread workgroups was
-// the best of a sweep over U in {1,2,4,8} x {256,512,1024} threads.
+// multiply-high invariant division.  The gated residual runs U = 1 with
+// 512-thread workgroups (kUnroll): one vector per thread and more
+// workgroups measured faster than U = 2 at [4608, 3072].
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "swiglu_body.hpp"

@@ -833,9 +833,10 @@ int run_flash_attn(hipStream_t st, const dt_tensor* t) {
                               q->ne[0], qs, ks, vs, os, fparam(t, 0), t->type, st);
 }
 
-// One convolution: the weights packed into the backend's scratch (bf16
-// [Co][K*K][Ci] tiles; a few MB, re-packed per call), the channel-last copy
-// of x after them, then dt_conv2d into root.
+// One convolution: F32 / BF16 weights packed into the backend's scratch
+// (bf16 [Co][K*K][Ci] tiles; a few MB, re-packed per call) unless they come
+// packed once at load (DT_TYPE_CONV2D_PACKED), the channel-last copy of x
+// after them, then dt_conv2d into root.
 int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt_tensor* w, const dt_tensor* bias,
              const dt_tensor* conv, int up2) {
     hipStream_t st = backend_stream(be);
@@ -847,22 +848,29 @@ int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt
                prm[4], prm[5]);
     DT_REQUIRE((K == 1 || K == 3) && w->ne[1] == K && prm[2] == (K - 1) / 2 && prm[3] == (K - 1) / 2,
                "dt_graph_compute: CONV_2D_DIRECT needs a square 1x1 / 3x3 kernel with padding (K - 1) / 2");
-    DT_REQUIRE(w->type == DT_TYPE_F32 || w->type == DT_TYPE_BF16, "dt_graph_compute: CONV_2D_DIRECT weight type %d",
-               w->type);
+    const bool prepacked = w->type == DT_TYPE_CONV2D_PACKED;
+    DT_REQUIRE(w->type == DT_TYPE_F32 || w->type == DT_TYPE_BF16 || prepacked,
+               "dt_graph_compute: CONV_2D_DIRECT weight type %d", w->type);
     DT_REQUIRE(is_io_type(x->type) && x->type == root->type, "dt_graph_compute: CONV_2D_DIRECT input/output types");
-    DT_REQUIRE(dense(x) && dense(w) && dense(root), "dt_graph_compute: CONV_2D_DIRECT operands must be contiguous");
+    DT_REQUIRE(dense(x) && (prepacked || dense(w)) && dense(root),
+               "dt_graph_compute: CONV_2D_DIRECT operands must be contiguous");
     DT_REQUIRE(x->ne[2] == Ci && root->ne[0] == W * f && root->ne[1] == H * f && root->ne[2] == Co &&
                    root->ne[3] == N,
                "dt_graph_compute: CONV_2D_DIRECT shapes disagree");
-    const size_t packed = (dt_conv2d_packed_bytes(Co, Ci, K) + 255) / 256 * 256;
+    const size_t packed = prepacked ? 0 : (dt_conv2d_packed_bytes(Co, Ci, K) + 255) / 256 * 256;
     const size_t ws = K == 3 ? dt_conv2d_workspace_bytes(N, Ci, H, W) : 0;
     void* scratch = nullptr;
-    int rc = backend_scratch(be, packed + ws, &scratch);
-    if (rc) return rc;
-    rc = dt_conv2d_pack_weights(data_of(w), w->type, Co, Ci, K, scratch, st);
-    if (rc) return rc;
-    g_kernels += K == 3 ? 3 : 2;  // pack, channel-last copy (3x3), conv
-    return dt_conv2d(data_of(x), N, Ci, H, W, scratch, Co, K, up2, bias ? (const float*)data_of(bias) : nullptr,
+    if (packed + ws) {
+        const int rc = backend_scratch(be, packed + ws, &scratch);
+        if (rc) return rc;
+    }
+    const void* wp = prepacked ? data_of(w) : scratch;
+    if (!prepacked) {
+        const int rc = dt_conv2d_pack_weights(data_of(w), w->type, Co, Ci, K, scratch, st);
+        if (rc) return rc;
+    }
+    g_kernels += (prepacked ? 0 : 1) + (K == 3 ? 1 : 0) + 1;  // pack, channel-last copy (3x3), conv
+    return dt_conv2d(data_of(x), N, Ci, H, W, wp, Co, K, up2, bias ? (const float*)data_of(bias) : nullptr,
                      root->data, ws ? (char*)scratch + packed : nullptr, ws, root->type, st);
 }
 
@@ -1138,6 +1146,8 @@ bool span_of(const dt_tensor* t, Span* s) {
     int64_t ext = 0;
     if (t->type == DT_TYPE_Q8_0_SPLIT) {
         ext = (int64_t)dt_q8_0_split_bytes(t->ne[1], t->ne[0]);
+    } else if (t->type == DT_TYPE_CONV2D_PACKED) {
+        ext = (int64_t)dt_conv2d_packed_bytes(t->ne[3], t->ne[2], t->ne[0]);
     } else {
         const int es = elem_size(t->type);
         int d0 = 1;

@@ -41,6 +41,8 @@ int64_t elem_size(int32_t type) {
             return 2;
         case DT_TYPE_Q8_0_SPLIT:  // one code byte per element; scales follow the codes
             return 1;
+        case DT_TYPE_CONV2D_PACKED:  // bf16 elements in dt_conv2d's padded tile order
+            return 2;
         default:
             return 0;
     }
@@ -160,6 +162,7 @@ HipRuntime::~HipRuntime() {
 
 size_t HipRuntime::nbytes(const Node* t) {
     if (t->type == DT_TYPE_Q8_0_SPLIT) return (size_t)dt_q8_0_split_bytes(t->ne[1] * t->ne[2] * t->ne[3], t->ne[0]);
+    if (t->type == DT_TYPE_CONV2D_PACKED) return dt_conv2d_packed_bytes(t->ne[3], t->ne[2], t->ne[0]);
     int64_t qk, bs;
     block_layout(t->type, &qk, &bs);
     return (size_t)(nelements(t) / qk * bs);
@@ -433,10 +436,12 @@ Node* HipRuntime::conv_2d_direct(Node* a, Node* b, int s0, int s1, int p0, int p
     if (a->ne[1] != K || (K != 1 && K != 3) || p0 != (K - 1) / 2 || p1 != (K - 1) / 2)
         throw Unsupported("conv_2d_direct: square 1x1 / 3x3 kernels with padding (K - 1) / 2 only");
     if (a->ne[2] != b->ne[2]) throw std::invalid_argument("conv_2d_direct: weight and input channels differ");
-    if (a->type != DT_TYPE_F32 && a->type != DT_TYPE_BF16)
-        throw Unsupported("conv_2d_direct: F32 / BF16 weights only");
+    if (a->type != DT_TYPE_F32 && a->type != DT_TYPE_BF16 && a->type != DT_TYPE_CONV2D_PACKED)
+        throw Unsupported("conv_2d_direct: F32 / BF16 or packed weights only");
     if (b->type != DT_TYPE_F32 && b->type != DT_TYPE_BF16)
         throw Unsupported("conv_2d_direct: F32 / BF16 input only");
+    if (a->type == DT_TYPE_CONV2D_PACKED && (a->op != DT_OP_NONE || !is_contiguous(a)))
+        throw std::invalid_argument("conv_2d_direct: a packed weight must be the whole leaf");
     if (!is_contiguous(a)) a = cont(a);
     if (!is_contiguous(b)) b = cont(b);
     const int64_t ne[4] = {b->ne[0], b->ne[1], a->ne[3], b->ne[3]};

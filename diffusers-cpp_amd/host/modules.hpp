@@ -147,6 +147,23 @@ struct SiLU {
     Tensor forward(const Tensor& x) const { return x * x.sigmoid(); }
 };
 
+inline int32_t& conv_weight_type_slot() {
+    thread_local int32_t t = DT_TYPE_F32;
+    return t;
+}
+
+// Scoped choice of the type new Conv2d weights are created with: F32 (the
+// reference's parameters) or DT_TYPE_CONV2D_PACKED, a weight the loader packs
+// once (dt_conv2d_pack_weights) so the executor does not repack it per call.
+class ConvWeightType {
+public:
+    explicit ConvWeightType(int32_t type) : prev_(conv_weight_type_slot()) { conv_weight_type_slot() = type; }
+    ~ConvWeightType() { conv_weight_type_slot() = prev_; }
+
+private:
+    int32_t prev_;
+};
+
 // Conv2d (src/nn/modules/conv/Conv2d.cpp:5-102): weight [Co, Ci, K, K] and
 // bias [Co]; forward = conv_2d_direct on the contiguous input, then the bias
 // broadcast as [1, Co, 1, 1].  The executor runs the pair as one convolution
@@ -156,7 +173,7 @@ public:
     Conv2d(int64_t in_channels, int64_t out_channels, int64_t kernel_size, int64_t stride = 1, int64_t padding = 0,
            bool bias = true)
         : stride_(stride), padding_(padding), bias_(bias) {
-        weight = parameter({out_channels, in_channels, kernel_size, kernel_size});
+        weight = parameter({out_channels, in_channels, kernel_size, kernel_size}, conv_weight_type_slot());
         register_parameter("weight", weight);
         if (bias_) {
             this->bias = parameter({out_channels});

@@ -24,8 +24,8 @@ int64_t ggml_dim(const Tensor::Shape& s, int64_t i) {
     return i < r ? s[r - 1 - i] : 1;
 }
 
-// True if `a` is a broadcast superset of `b` in ggml's sense: every dim of a
-// is a multiple of the matching dim of b (missing dims count as 1).
+// Whether ggml can repeat b to a's shape: dim by dim (ggml order, absent
+// dims taken as 1), b's extent has to divide a's, and an empty b never fits.
 bool ggml_broadcasts(const Tensor::Shape& a, const Tensor::Shape& b) {
     const int64_t rank = (int64_t)std::max(a.size(), b.size());
     for (int64_t i = 0; i < rank; ++i) {

@@ -41,12 +41,17 @@ extern "C" {
 #endif
 
 /* ggml type ids (ggml.h enum ggml_type), kept numerically identical, plus
- * DT_TYPE_Q8_0_SPLIT: a Q8_0 Linear weight [N][K] repacked once at load by
- * dt_q8_0_split for dt_gemm_q8_0 (no ggml counterpart; ggml likewise
- * repacks weights into backend layouts through its "extra" buffer types).
- * A tensor of this type has ne = {K, N, 1, 1}, nb = {1, K, N K, N K}; its
- * data holds the uint8 codes [N][K] at offset 0 and the fp32 block scales
- * [K/32][N] at dt_q8_0_split_scale_offset(N, K). */
+ * two backend weight layouts made once at load (no ggml counterpart; ggml
+ * likewise repacks weights into backend layouts through its "extra" buffer
+ * types):
+ * DT_TYPE_Q8_0_SPLIT: a Q8_0 Linear weight [N][K] repacked by dt_q8_0_split
+ * for dt_gemm_q8_0.  A tensor of this type has ne = {K, N, 1, 1}, nb = {1, K,
+ * N K, N K}; its data holds the uint8 codes [N][K] at offset 0 and the fp32
+ * block scales [K/32][N] at dt_q8_0_split_scale_offset(N, K).
+ * DT_TYPE_CONV2D_PACKED: a Conv2d weight [Co][Ci][K][K] packed by
+ * dt_conv2d_pack_weights, the layout dt_conv2d reads (ne = {K, K, Ci, Co},
+ * dt_conv2d_packed_bytes(Co, Ci, K) bytes; nb is not used).  As src0 of
+ * DT_OP_CONV_2D_DIRECT it spares the executor a repack per call. */
 enum {
     DT_TYPE_F32 = 0,
     DT_TYPE_F16 = 1,
@@ -54,7 +59,8 @@ enum {
     DT_TYPE_Q4_K = 12,
     DT_TYPE_I32 = 26,
     DT_TYPE_BF16 = 30,
-    DT_TYPE_Q8_0_SPLIT = 100
+    DT_TYPE_Q8_0_SPLIT = 100,
+    DT_TYPE_CONV2D_PACKED = 101
 };
 
 enum {
@@ -488,7 +494,8 @@ enum {
     DT_OP_FLASH_ATTN_EXT,/* ggml_flash_attn_ext(q ne {D, Sq, H, B}, k, v ne {D, Skv, H, B},
                             src[3] = mask, must be NULL) -> ne {D, H, Sq, B};
                             op_params[0] = scale bits; BF16 q/k/v, D = 128 */
-    DT_OP_CONV_2D_DIRECT,/* ggml_conv_2d_direct(src0 = weight ne {K, K, Ci, Co} F32/BF16,
+    DT_OP_CONV_2D_DIRECT,/* ggml_conv_2d_direct(src0 = weight ne {K, K, Ci, Co} F32/BF16
+                            or CONV2D_PACKED,
                             src1 = x ne {W, H, Ci, N} contiguous) -> ne {W', H', Co, N} of
                             x's type; op_params = s0, s1, p0, p1, d0, d1 (stride and
                             dilation 1, K in {1, 3}, padding (K - 1) / 2) */

@@ -146,6 +146,31 @@ def test_fastdiv_arithmetic():
             assert (((n * m) >> 32) + n) >> s == n // d
 
 
+def test_conv2d_packed_weight_type():
+    """DT_TYPE_CONV2D_PACKED (101): a conv weight {K, K, Ci, Co} packed once
+    at load, dt_conv2d_packed_bytes long (Co to 128, Ci to 32, bf16); the
+    descriptor calls size it by that count (a copy past it is refused before
+    any device call)."""
+    lib = dit_hip.load()
+    text = open(HEADER).read()
+    assert "DT_TYPE_CONV2D_PACKED = 101" in text
+    assert lib.dt_conv2d_packed_bytes(512, 512, 3) == 512 * 9 * 512 * 2      # 4.7 MB, no padding
+    assert lib.dt_conv2d_packed_bytes(3, 3, 3) == 128 * 9 * 32 * 2
+    assert lib.dt_conv2d_packed_bytes(4, 4, 2) == 0                          # K in {1, 3} only
+    t = dit_hip.DtTensor()
+    t.type = 101
+    for i, n in enumerate((3, 3, 512, 512)):
+        t.ne[i] = n
+    t.data = 0x10000  # never dereferenced: the size check fails first
+    buf = ctypes.create_string_buffer(16)
+    total = 512 * 9 * 512 * 2
+    assert lib.dt_tensor_set(ctypes.byref(t), buf, total, 1, None) != 0
+    assert "exceed the tensor's %d bytes" % total in lib.dt_last_error().decode()
+    t.ne[1] = 1  # not a square kernel: not a packed weight
+    assert lib.dt_tensor_set(ctypes.byref(t), buf, 0, 1, None) != 0
+    assert "not supported" in lib.dt_last_error().decode()
+
+
 def test_q8_0_split_layout_sizes():
     """DT_TYPE_Q8_0_SPLIT: codes [N][K] then fp32 scales [K/32][N] at the
     codes rounded up to 256 bytes."""

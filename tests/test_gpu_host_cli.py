@@ -259,10 +259,15 @@ def test_conv2d(orc, cli, x_shape, ci, co, k, pad, bias):
     if bias:
         args += ["--param-bias", cli.f32(b)]
     st = cli.run("Conv2d", *args)
+    got = read_dtb(cli.out())
     want = orc.conv2d(orc.round_bf16(xv), orc.round_bf16(w), b if bias else None)
-    check(read_dtb(cli.out()), want, cli.bf16, "Conv2d")
+    check(got, want, cli.bf16, "Conv2d")
     assert st["fused_nodes"] == (1 if bias else 0), st      # the bias ADD folds into the conv
     assert st["kernels"] == (3 if k == 3 else 2), st         # pack, channel-last copy (3x3), conv
+    # the weight packed once at load (DT_TYPE_CONV2D_PACKED): no pack per call, same bits
+    sp = cli.run("Conv2d", *args, "--packed-weights", "true")
+    assert np.array_equal(read_dtb(cli.out()).view(np.uint32), got.view(np.uint32))
+    assert sp["kernels"] == st["kernels"] - 1 and sp["fused_nodes"] == st["fused_nodes"], sp
 
 
 def test_conv2d_stride_2_is_reported(orc, cli):
@@ -295,6 +300,9 @@ def test_upsample2d(orc, cli, use_conv, shape):
     want = orc.conv2d(orc.round_bf16(xv), orc.round_bf16(w), b, up2=True)
     check(got, want, cli.bf16, "Upsample2D")
     assert st["fused_nodes"] == 2 and st["kernels"] == 3, st  # upscale + conv folded under the bias ADD
+    sp = cli.run("Upsample2D", *args, "--packed-weights", "true")
+    assert np.array_equal(read_dtb(cli.out()).view(np.uint32), got.view(np.uint32))
+    assert sp["fused_nodes"] == 2 and sp["kernels"] == 2, sp
 
 
 def test_cli_rejects_bad_input(dev):
