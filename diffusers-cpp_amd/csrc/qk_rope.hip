@@ -71,83 +71,115 @@ __device__ __forceinline__ void store8<float>(float* p, const float* v) {
     Io<float>::store(p + 4, v + 4);
 }
 
-// A wave owns one token and up to 4*HPG of its heads: its four 16-lane DPP
-// rows take heads h0 + row + 4*i (i < HPG), so each load/store instruction
-// covers four consecutive heads = 1 KB of contiguous bf16.  The token's
-// position, its cos/sin table row and the lane's 8 norm weights are loaded
-// once per wave, and all HPG head loads are in flight before the first
-// reduction.
-template <typename T, int HPG, int NT>
+// A work item is one token and up to 4*HPG of its heads: a wave's four
+// 16-lane DPP rows take heads h0 + row + 4*i (i < HPG), so each load/store
+// instruction covers four consecutive heads = 1 KB of contiguous bf16.  Wave
+// w of the W waves of a tensor takes items w, w + W, ... (at most ITER), and
+// issues the next item's position and head loads before the current item's
+// reduction and rotation, so the loads of every resident wave stay in flight
+// while it computes (one item per wave left HBM idle while all resident
+// waves computed at once: 23.0 -> 22.2 us for q and k of [4608, 24, 128]).
+// The position goes out before the heads: loads retire in issue order, so
+// the dependent cos/sin lookup can start while the head loads are still in
+// flight.  The lane's 8 norm weights are loaded once per wave.
+template <typename T>
+struct QkRaw {
+    static constexpr int NV = 8 / Io<T>::EPV;  // 16-byte vectors per 8 elements
+    uint4 r[NV];
+};
+
+template <typename T, int HPG, int NT, int ITER>
 __device__ __forceinline__ void qk_rope128_body(const QkHalf& a, const QkShape& sh, const float* __restrict__ table,
-                                                int chunks, int block) {
+                                                int chunks, int block, int W) {
     if (a.x == nullptr) return;
-    const int wv = (int)((block * NT + threadIdx.x) / kWave);
-    if (wv >= sh.tokens * chunks) return;  // whole waves leave together
+    const int w = (int)((block * NT + threadIdx.x) / kWave);
+    if (w >= W) return;  // whole waves leave together
+    constexpr int NV = QkRaw<T>::NV, EPV = Io<T>::EPV;
+    const int64_t total = (int64_t)sh.tokens * chunks;
     const int lane16 = threadIdx.x & 15;
     const int row = (threadIdx.x & (kWave - 1)) >> 4;
     const int d0 = lane16 * 8;
     const int axis = d0 / sh.axis_dim;
     const int i0 = d0 - axis * sh.axis_dim;
-    const int t = wv / chunks;
-    const int h0 = (wv - t * chunks) * 4 * HPG + row;
-    const T* __restrict__ xb = (const T*)a.x + t * sh.in_ts + d0;
-    T* __restrict__ yb = (T*)a.y + t * sh.out_ts + d0;
-
-    // The position goes out first: loads retire in issue order, so the
-    // dependent table lookup below can start while the head loads are
-    // still in flight instead of after all of them.
+    const T* __restrict__ xb = (const T*)a.x + d0;
+    T* __restrict__ yb = (T*)a.y + d0;
     const int32_t* pax;
     int64_t pst;
     axis_pos(sh, axis, pax, pst);
-    const int p = pax[t * pst];
-    float v[HPG][8];
+
+    QkRaw<T> cur[HPG], nxt[HPG];
+    int tc = 0, hc = 0, pc = 0, tn = 0, hn = 0, pn = 0;
+    // items < tokens * chunks < 2^31 (qk_fast), so an item index fits an int
+    auto issue = [&](int j, QkRaw<T>* raw, int& t, int& h0, int& p) {
+        t = j / chunks;
+        h0 = (j - t * chunks) * 4 * HPG + row;
+        p = pax[(int64_t)t * pst];
 #pragma unroll
-    for (int hh = 0; hh < HPG; ++hh) {
-        const int h = h0 + 4 * hh;
-        if (h < sh.heads) {
-            load8<T>(xb + (int64_t)h * sh.in_hs, v[hh]);
-        } else {
+        for (int hh = 0; hh < HPG; ++hh) {
+            const int h = h0 + 4 * hh;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[hh][e] = 0.f;
+            for (int u = 0; u < NV; ++u)
+                raw[hh].r[u] = h < sh.heads ? ld_stream(xb + (int64_t)t * sh.in_ts + (int64_t)h * sh.in_hs + u * EPV)
+                                            : make_uint4(0, 0, 0, 0);
         }
-    }
+    };
+    issue(w, cur, tc, hc, pc);
     float cs[8];
-    rope_angles<4>(p, i0, table, sh.n_pos, sh.axis_dim, sh.theta_scale, cs);
-    float w[8];
+    rope_angles<4>(pc, i0, table, sh.n_pos, sh.axis_dim, sh.theta_scale, cs);
+    float wt[8];
 #pragma unroll
     for (int e = 0; e < 8; e += 4) {  // shared by every head: default (cached) policy
         const float4 t4 = *reinterpret_cast<const float4*>(a.w + d0 + e);
-        w[e] = t4.x; w[e + 1] = t4.y; w[e + 2] = t4.z; w[e + 3] = t4.w;
+        wt[e] = t4.x; wt[e + 1] = t4.y; wt[e + 2] = t4.z; wt[e + 3] = t4.w;
     }
-    const float hd_f = (float)sh.head_dim;
+    // mean of squares over the 128 dims: the division by 128 is exact, so a
+    // multiply by 1/128 gives the quotient's bits
+    constexpr float kInvHeadDim = 1.0f / 128.0f;
 
 #pragma unroll
-    for (int hh = 0; hh < HPG; ++hh) {
-        const int h = h0 + 4 * hh;
-        if (h < sh.heads) {  // uniform across the 16 lanes of a DPP row
-            float ss = 0.f;
+    for (int kk = 0; kk < ITER; ++kk) {
+        const int64_t j = w + (int64_t)kk * W;
+        if (j >= total) break;
+        const bool more = kk + 1 < ITER && j + W < total;
+        if (more) issue((int)(j + W), nxt, tn, hn, pn);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) ss += v[hh][e] * v[hh][e];
-            ss = row16_sum(ss);
-            const float r = 1.0f / sqrtf(ss / hd_f + sh.eps);
-            float o[8];
+        for (int hh = 0; hh < HPG; ++hh) {
+            const int h = hc + 4 * hh;
+            if (h < sh.heads) {  // uniform across the 16 lanes of a DPP row
+                float v[8];
 #pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-                const float x0 = mul_rn(mul_rn(v[hh][2 * qd], r), w[2 * qd]);
-                const float x1 = mul_rn(mul_rn(v[hh][2 * qd + 1], r), w[2 * qd + 1]);
-                const float c = cs[2 * qd], sn = cs[2 * qd + 1];
-                o[2 * qd] = sub_rn(mul_rn(x0, c), mul_rn(x1, sn));
-                o[2 * qd + 1] = add_rn(mul_rn(x0, sn), mul_rn(x1, c));
+                for (int u = 0; u < NV; ++u) Io<T>::unpack(cur[hh].r[u], v + u * EPV);
+                float ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+                ss = row16_sum(ss);
+                const float r = 1.0f / sqrtf(ss * kInvHeadDim + sh.eps);
+                float o[8];
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    const float x0 = mul_rn(mul_rn(v[2 * qd], r), wt[2 * qd]);
+                    const float x1 = mul_rn(mul_rn(v[2 * qd + 1], r), wt[2 * qd + 1]);
+                    const float c = cs[2 * qd], sn = cs[2 * qd + 1];
+                    o[2 * qd] = sub_rn(mul_rn(x0, c), mul_rn(x1, sn));
+                    o[2 * qd + 1] = add_rn(mul_rn(x0, sn), mul_rn(x1, c));
+                }
+                store8<T>(yb + (int64_t)tc * sh.out_ts + (int64_t)h * sh.out_hs, o);
             }
-            store8<T>(yb + (int64_t)h * sh.out_hs, o);
+        }
+        if (more) {
+            rope_angles<4>(pn, i0, table, sh.n_pos, sh.axis_dim, sh.theta_scale, cs);
+#pragma unroll
+            for (int hh = 0; hh < HPG; ++hh) cur[hh] = nxt[hh];
+            tc = tn;
+            hc = hn;
         }
     }
 }
 
-template <typename T, int HPG>
+template <typename T, int HPG, int ITER>
 __global__ __launch_bounds__(256) void qk_rope128_kernel(QkHalf q, QkHalf k, QkShape sh,
-                                                         const float* __restrict__ table, int chunks) {
-    qk_rope128_body<T, HPG, 256>(blockIdx.y == 0 ? q : k, sh, table, chunks, blockIdx.x);
+                                                         const float* __restrict__ table, int chunks, int W) {
+    qk_rope128_body<T, HPG, 256, ITER>(blockIdx.y == 0 ? q : k, sh, table, chunks, blockIdx.x, W);
 }
 
 constexpr int kQkSwigluThreads = 512;  // the SwiGLU body's best workgroup
@@ -158,14 +190,14 @@ constexpr int kQkSwigluThreads = 512;  // the SwiGLU body's best workgroup
 // qk_blocks k (when k is given: n_qk = 2 qk_blocks, else qk_blocks), the
 // rest stream the SwiGLU.  The bodies are the standalone kernels', so the
 // results are bit-identical to separate launches.
-template <typename T, int HPG>
+template <typename T, int HPG, int ITER>
 __global__ __launch_bounds__(kQkSwigluThreads) void qk_swiglu_kernel(QkHalf q, QkHalf k, QkShape sh,
                                                                      const float* __restrict__ table, int chunks,
-                                                                     int qk_blocks, int n_qk, SwigluArgs sw) {
+                                                                     int W, int qk_blocks, int n_qk, SwigluArgs sw) {
     const int b = blockIdx.x;
     if (b < n_qk)
-        qk_rope128_body<T, HPG, kQkSwigluThreads>(b < qk_blocks ? q : k, sh, table, chunks,
-                                                  b < qk_blocks ? b : b - qk_blocks);
+        qk_rope128_body<T, HPG, kQkSwigluThreads, ITER>(b < qk_blocks ? q : k, sh, table, chunks,
+                                                        b < qk_blocks ? b : b - qk_blocks, W);
     else
         swiglu_body<T, kQkSwigluThreads>(sw, b - n_qk);
 }
@@ -209,7 +241,19 @@ __global__ __launch_bounds__(256) void qk_rope_generic_kernel(QkHalf q, QkHalf k
     }
 }
 
-constexpr int kHPG = 3;  // 12 heads per wave: best of HPG in {1, 2, 3, 6} on [4608, 24, 128]
+constexpr int kHPG = 3;  // 12 heads per item: best of HPG in {1, 2, 3, 6} on [4608, 24, 128]
+// Items per wave of the standalone launch: 3 keeps every wave of
+// [4608, 24, 128] resident at once (6 per SIMD); 2 leaves a second round, 4
+// and 8 too few waves (q and k: 22.2 us against 23.0 / 23.9 / 23.7 / 30.5 us
+// for 1 / 2 / 4 / 8).  The fused QK+SwiGLU launch takes one item per wave:
+// the deeper pipeline's registers (81 against 58 VGPRs) cost its SwiGLU
+// blocks occupancy (59.9 us at 1, 61.3 at 2, 67.6 at 3; 62.1-64.4 us for the
+// previous single-item body at 71 VGPRs).
+constexpr int kQkIter = 3;
+constexpr int kQkSwigluIter = 1;
+
+// Waves per tensor for `items` work items at `iter` items per wave.
+int64_t qk_waves(int64_t items, int iter) { return (items + iter - 1) / iter; }
 
 template <typename T>
 bool qk_fast(const QkHalf& q, const QkHalf& k, const QkShape& sh, const float* table) {
@@ -233,10 +277,10 @@ int run(QkHalf q, QkHalf k, const QkShape& sh, const float* table, hipStream_t s
     if (fast) {
         constexpr int HPG = kHPG;
         const int chunks = (sh.heads + 4 * HPG - 1) / (4 * HPG);
-        const int64_t waves = (int64_t)sh.tokens * chunks;
+        const int64_t waves = qk_waves((int64_t)sh.tokens * chunks, kQkIter);
         const int64_t blocks = (waves + 3) / 4;
-        hipLaunchKernelGGL((qk_rope128_kernel<T, HPG>), dim3((unsigned)blocks, ny), dim3(256), 0, st,
-                           q, k, sh, table, chunks);
+        hipLaunchKernelGGL((qk_rope128_kernel<T, HPG, kQkIter>), dim3((unsigned)blocks, ny), dim3(256), 0, st,
+                           q, k, sh, table, chunks, (int)waves);
     } else {
         const int64_t groups = (int64_t)sh.tokens * sh.heads;
         const int64_t blocks = (groups + 255) / 256;
@@ -285,13 +329,14 @@ int run_qk_swiglu(const QkHalf& hq, const QkHalf& hk, const QkShape& sh, const f
     }
     constexpr int NT = kQkSwigluThreads, WAVES = NT / kWave;
     const int chunks = (sh.heads + 4 * kHPG - 1) / (4 * kHPG);
-    const int64_t qk_blocks = ((int64_t)sh.tokens * chunks + WAVES - 1) / WAVES;
+    const int64_t waves = qk_waves((int64_t)sh.tokens * chunks, kQkSwigluIter);
+    const int64_t qk_blocks = (waves + WAVES - 1) / WAVES;
     const int64_t n_qk = (hk.x ? 2 : 1) * qk_blocks;
     const int64_t blocks = n_qk + swiglu_blocks<T, NT>((uint32_t)total);
     DT_REQUIRE(blocks < (1ll << 31), "dt_qk_rmsnorm_rope_swiglu: grid too large");
     const SwigluArgs sw{g, gs, u, us, y, ys, (uint32_t)total, make_fastdiv((uint32_t)(nvec ? nvec : 1))};
-    hipLaunchKernelGGL((qk_swiglu_kernel<T, kHPG>), dim3((unsigned)blocks), dim3(NT), 0, st, hq, hk, sh, table,
-                       chunks, (int)qk_blocks, (int)n_qk, sw);
+    hipLaunchKernelGGL((qk_swiglu_kernel<T, kHPG, kQkSwigluIter>), dim3((unsigned)blocks), dim3(NT), 0, st, hq, hk, sh,
+                       table, chunks, (int)waves, (int)qk_blocks, (int)n_qk, sw);
     return check_launch("dt_qk_rmsnorm_rope_swiglu");
 }
 
