@@ -220,10 +220,10 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_flat_kernel(const 
     const int64_t b0 = (int64_t)blockIdx.x * SEG;
     const int nblk = (int)min<int64_t>(SEG, nblocks - b0);
     const uint8_t* base = src + b0 * 144;
-    // default (cache-allocating) loads: the super-blocks are 22% of the bytes
-    // moved, and measured 4% faster than streaming loads at 3072 x 3072 (equal
-    // at 3072 x 9216); Q8_0's blocks stay streamed (faster at both sizes)
-    for (int i = t; i < nblk * 9; i += kStageThreads) stage[i] = *reinterpret_cast<const uint4*>(base + 16 * i);
+    // streaming loads: default (cache-allocating) ones measured 3% faster back
+    // to back at 3072 x 3072 but 14-21% slower as single launches after other
+    // work filled the caches (3072 x 9216: 15.5 -> 18.8 us)
+    for (int i = t; i < nblk * 9; i += kStageThreads) stage[i] = ld_stream(base + 16 * i);
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
