@@ -192,21 +192,6 @@ def time_stream(torch, fns, reps):
     return e0.elapsed_time(e1) * 1e-3 / reps
 
 
-def raw_calls(fn, arg_sets):
-    """One closure per argument tuple calling the C ABI function directly,
-    so the back-to-back loop of time_stream spends no Python wrapper time
-    between launches (kernels of a few microseconds would otherwise wait on
-    the host); each call's status is checked once here."""
-    import functools
-    calls = [functools.partial(fn, *a) for a in arg_sets]
-    for c in calls:
-        rc = c()
-        if rc != 0:
-            import dit_hip
-            raise RuntimeError(f"{fn.__name__} failed ({rc}): {dit_hip.load().dt_last_error().decode()}")
-    return calls
-
-
 def _sets_for(set_bytes, cap=16):
     """Buffer sets whose total exceeds 1 GiB (4x the last-level cache)."""
     return int(max(2, min(cap, -(-(1 << 30) // set_bytes))))
@@ -285,9 +270,7 @@ def secondary(torch, dev, flush):
                 if qt == dit_hip.Q4_K:
                     view[:, 3] &= 0x3B
                 sets.append((src, torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)))
-            fns = raw_calls(dit_hip.load().dt_dequant,
-                            [(s_.data_ptr(), qt, rows, cols, cols // qk * bs, y_.data_ptr(), cols, dit_hip.BF16,
-                              dit_hip.stream()) for s_, y_ in sets])
+            fns = [dit_hip.prepare(dit_hip.dequant, s_, qt, rows, cols, out=y_)[1] for s_, y_ in sets]
             t = time_stream(torch, fns, 4 * len(fns))
             t1 = time_cold(torch, fns[0], 10, flush)
             out[name] = entry(nbytes, t, t1)
@@ -302,10 +285,8 @@ def secondary(torch, dev, flush):
                              dtype=torch.uint8, device=dev)
             sets = [(torch.randn(shape, device=dev).to(dt), torch.empty(shape, dtype=dt, device=dev))
                     for _ in range(_sets_for(nbytes, 8))]
-            fns = raw_calls(dit_hip.load().dt_groupnorm_silu,
-                            [(x_.data_ptr(), shape[0], shape[1], shape[2] * shape[3], 32, w.data_ptr(), b.data_ptr(),
-                              1e-6, 1, y_.data_ptr(), ws.data_ptr(), ws.numel(), dit_hip.io_type(x_),
-                              dit_hip.stream()) for x_, y_ in sets])
+            fns = [dit_hip.prepare(dit_hip.groupnorm_silu, x_, 32, w, b, 1e-6, out=y_, workspace=ws)[1]
+                   for x_, y_ in sets]
             t = time_stream(torch, fns, 4 * len(fns))
             t1 = time_cold(torch, fns[0], 6, flush)
             name = "groupnorm_silu_" + "x".join(map(str, shape)) + ("_f32" if es == 4 else "_bf16")
@@ -696,10 +677,20 @@ def main():
     dit_hip.load()
     dev = torch.device("cuda:0")
     sets = [make_inputs(torch, dev, 0x5EED0000 + 97 * i) for i in range(NSETS)]
-    chains = [chain_kernels(t) for t in sets]
+    # The launches through the Python binding's wrappers (captured into the
+    # HIP graphs, which take the capturing stream), and the same launches
+    # prepared once (dit_hip.prepare: the C-ABI call with its arguments
+    # converted) for the eager step and the back-to-back timings, so that no
+    # Python work sits between launches, as for a C++ caller.
+    chain_calls = [chain_kernels(t) for t in sets]
+    chains = [{k: dit_hip.prepare(f)[1] for k, f in c.items()} for c in chain_calls]
 
     def step(i):
         for f in chains[i % NSETS].values():
+            f()
+
+    def step_w(i):
+        for f in chain_calls[i % NSETS].values():
             f()
 
     def warm(run_step):
@@ -749,7 +740,7 @@ def main():
         return out
 
     # The step's two launches captured back to back.
-    graphs = capture(step)
+    graphs = capture(step_w)
     warm_steps["graph"] = warm(lambda i: graphs[i % NSETS].replay())
     seq_s, seq_wall = timed(lambda i: graphs[i % NSETS].replay())
 
@@ -770,10 +761,11 @@ def main():
     probe_s, _ = timed(probe_step)
 
     # Block order with the four standalone kernels, as a graph, for comparison.
-    singles = [standalone_kernels(t) for t in sets]
+    single_calls = [standalone_kernels(t) for t in sets]
+    singles = [{k: dit_hip.prepare(f)[1] for k, f in c.items()} for c in single_calls]
 
     def unfused(i):
-        for f in singles[i % NSETS].values():
+        for f in single_calls[i % NSETS].values():
             f()
 
     ugraphs = capture(unfused)
@@ -827,7 +819,7 @@ def main():
     kd = kernels[dom]
     roofline = {"bound": "hbm", "achieved": kd["GBs_stream"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(kd["GBs_stream"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "qk_swiglu_kernel<bf16,3>", "alg_bytes_per_launch": fused_ab[dom],
+                "kernel": "qk_swiglu_kernel<bf16,3,1>", "alg_bytes_per_launch": fused_ab[dom],
                 "statistic": f"mean launch duration over {40 * NSETS} back-to-back launches cycling {NSETS} buffer "
                              f"sets (HIP events around the run, on the launch stream)",
                 "launch_us_stream_mean": kd["us_stream_mean"],

@@ -174,6 +174,54 @@ def exported_symbols():
     return list(_SIGS)
 
 
+class _Recorder:
+    """Stands in for the loaded library while prepare() runs a wrapper:
+    forwards every call and keeps (function, converted arguments)."""
+
+    def __init__(self, lib):
+        self._lib = lib
+        self.calls = []
+
+    def __getattr__(self, name):
+        fn = getattr(self._lib, name)
+
+        def call(*args):
+            conv = tuple(a if t is None or isinstance(a, t) else t(a)
+                         for a, t in zip(args, fn.argtypes or [None] * len(args)))
+            self.calls.append((fn, conv))
+            return fn(*conv)
+
+        return call
+
+
+def prepare(wrapper, *args, **kwargs):
+    """Run `wrapper(*args, **kwargs)` once (arguments checked, outputs
+    allocated, the launch made) and return (result, launch): launch() repeats
+    the C-ABI calls that run made, with the same pointers, sizes and stream,
+    and no Python work between launches -- for tight loops such as timing
+    back-to-back launches.  The tensors the call used must stay alive and
+    unchanged in shape while launch is in use; status codes of the repeats
+    are not checked (the first call's were)."""
+    global _lib
+    real = load()
+    rec = _Recorder(real)
+    _lib = rec
+    try:
+        result = wrapper(*args, **kwargs)
+    finally:
+        _lib = real
+    calls = rec.calls
+    if len(calls) == 1:
+        fn, conv = calls[0]
+        import functools
+        return result, functools.partial(fn, *conv)
+
+    def launch():
+        for fn, conv in calls:
+            fn(*conv)
+    return result, launch
+
+
 def check(rc: int, what: str = ""):
     if rc != 0:
         msg = load().dt_last_error().decode()

@@ -171,6 +171,19 @@ def test_conv2d_packed_weight_type():
     assert "not supported" in lib.dt_last_error().decode()
 
 
+def test_prepare_repeats_the_recorded_call():
+    """dit_hip.prepare runs a wrapper once and returns a launch that repeats
+    the same C-ABI call with the converted arguments (here the host-side
+    RoPE table fill, so no device is needed)."""
+    import torch
+    table, launch = dit_hip.prepare(dit_hip.rope_table, 16, 32, 10000.0, device="cpu")
+    want = table.clone()
+    table.zero_()
+    assert launch() == 0                       # the same pointer, filled again
+    assert torch.equal(table, want)
+    assert dit_hip.load() is not None and not isinstance(dit_hip.load(), dit_hip._Recorder)
+
+
 def test_q8_0_split_layout_sizes():
     """DT_TYPE_Q8_0_SPLIT: codes [N][K] then fp32 scales [K/32][N] at the
     codes rounded up to 256 bytes."""
