@@ -267,9 +267,10 @@ static size_t gn_workspace_needed(const void* x, const void* y, int64_t N, int64
 static int gn_check_shape(const char* what, const void* x, const void* y, int64_t N, int64_t C, int64_t HW,
                           int64_t groups, int32_t io_type) {
     DT_REQUIRE(dit::is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
-    DT_REQUIRE(N > 0 && C > 0 && HW > 0 && groups > 0 && C % groups == 0,
+    DT_REQUIRE(N >= 0 && C > 0 && HW >= 0 && groups > 0 && C % groups == 0,
                "%s: bad shape N=%lld C=%lld HW=%lld groups=%lld", what, (long long)N, (long long)C,
                (long long)HW, (long long)groups);
+    if (N == 0 || HW == 0) return DT_OK;  // empty: the caller returns before touching anything
     DT_REQUIRE(x && y, "%s: null pointer", what);
     DT_REQUIRE(N * groups < 65536, "%s: N*groups must be < 65536", what);
     return DT_OK;
@@ -284,6 +285,7 @@ extern "C" int dt_groupnorm_silu(const void* x, int64_t N, int64_t C, int64_t HW
                                  dt_stream_t stream) {
     int rc = gn_check_shape("dt_groupnorm_silu", x, y, N, C, HW, groups, io_type);
     if (rc) return rc;
+    if (N == 0 || HW == 0) return DT_OK;
     DT_REQUIRE(workspace, "dt_groupnorm_silu: null workspace");
     DT_REQUIRE(workspace_bytes >= dt_groupnorm_workspace_bytes(N, C, HW, groups),
                "dt_groupnorm_silu: workspace too small (%zu < %zu)", workspace_bytes,
@@ -338,6 +340,7 @@ extern "C" int dt_groupnorm_silu_noalloc(const void* x, int64_t N, int64_t C, in
                                          int32_t io_type, dt_stream_t stream) {
     int rc = gn_check_shape("dt_groupnorm_silu_noalloc", x, y, N, C, HW, groups, io_type);
     if (rc) return rc;
+    if (N == 0 || HW == 0) return DT_OK;
     const size_t need = gn_workspace_needed(x, y, N, C, HW, groups, io_type);
     DT_REQUIRE(need <= (size_t)DT_GROUPNORM_NOALLOC_SCRATCH_BYTES,
                "dt_groupnorm_silu_noalloc: N=%lld C=%lld HW=%lld groups=%lld needs %zu bytes of statistics, "

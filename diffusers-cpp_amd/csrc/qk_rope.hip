@@ -321,10 +321,13 @@ int run_qk_swiglu(const QkHalf& hq, const QkHalf& hk, const QkShape& sh, const f
     const int64_t nvec = cols / EPV, total = rows * nvec;
     const bool sw_vec = cols % EPV == 0 && gs % EPV == 0 && us % EPV == 0 && ys % EPV == 0 && aligned16(g) &&
                         aligned16(u) && aligned16(y) && total < (1ll << 31);
-    if (!sw_vec || !hq.x || sh.tokens == 0 || !qk_fast<T>(hq, hk, sh, table)) {
-        // shapes the combined kernel does not take: the two launches it replaces
-        int rc = run<T>(hq, hk, sh, table, st);
-        if (rc) return rc;
+    if (!sw_vec || !hq.x || sh.tokens == 0 || rows == 0 || !qk_fast<T>(hq, hk, sh, table)) {
+        // shapes the combined kernel does not take: the two launches it
+        // replaces, each skipped when its part is empty
+        if (hq.x && sh.tokens > 0) {
+            const int rc = run<T>(hq, hk, sh, table, st);
+            if (rc) return rc;
+        }
         return dt_swiglu(g, gs, u, us, y, ys, rows, cols, Io<T>::kType, st);
     }
     constexpr int NT = kQkSwigluThreads, WAVES = NT / kWave;

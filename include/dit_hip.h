@@ -189,7 +189,8 @@ int dt_dequant(const void *src, int32_t qtype, int64_t rows, int64_t cols,
  * reshape -> NORM -> reshape -> MUL -> ADD) and SiLU::forward
  * (SiLU.hpp:9-13) as used in ResnetBlock2D.inl:111-122, 160-171 and
  * Decoder.hpp:147-160.  `workspace` is caller-owned device memory of at
- * least dt_groupnorm_workspace_bytes(...) bytes.  y may alias x. */
+ * least dt_groupnorm_workspace_bytes(...) bytes.  y may alias x.  An empty
+ * input (N == 0 or HW == 0) is a no-op that touches no pointer. */
 size_t dt_groupnorm_workspace_bytes(int64_t N, int64_t C, int64_t HW, int64_t groups);
 int dt_groupnorm_silu(const void *x, int64_t N, int64_t C, int64_t HW, int64_t groups,
                       const float *w, const float *b, float eps, int32_t apply_silu,

@@ -171,6 +171,39 @@ def test_conv2d_packed_weight_type():
     assert "not supported" in lib.dt_last_error().decode()
 
 
+def test_zero_sized_calls_are_no_ops_without_a_device():
+    """Every entry point of the chain, the dequantisation and GroupNorm takes
+    an empty input (zero rows, tokens or images) as a successful no-op: it
+    launches nothing, so in this container (no GPU) any HIP call it made
+    would fail.  The data pointers are dummies that must not be touched."""
+    lib = dit_hip.load()
+    P = ctypes.c_void_p(0x10000)           # 64 KiB-aligned, never dereferenced
+    BF16, Q8, Q4 = dit_hip.BF16, dit_hip.Q8_0, dit_hip.Q4_K
+    D, I = 3072, 9216
+    calls = {
+        "dt_adaln_mod": (P, 0, D, D, P, P, P, D, 1e-6, BF16, None),
+        "dt_gated_residual_adaln": (P, D, P, D, P, P, D, P, P, P, D, 0, D, 1e-6, BF16, None),
+        "dt_gated_residual": (P, D, P, D, P, P, D, 0, D, BF16, None),
+        "dt_swiglu": (P, 2 * I, P, 2 * I, P, I, 0, I, BF16, None),
+        "dt_euler_step": (P, P, 0.1, P, 0, BF16, None),
+        "dt_qk_rmsnorm_rope": (P, P, P, P, 0, 24, 128, D, 128, D, 128, P, P, 1e-6, P, 4, 4, 32, 1e4,
+                               None, 0, BF16, None),
+        "dt_qk_rmsnorm_rope_swiglu": (P, P, P, P, 0, 24, 128, D, 128, D, 128, P, P, 1e-6, P, 4, 4, 32, 1e4,
+                                      None, 0, P, 2 * I, P, 2 * I, P, I, 0, I, BF16, None),
+        "dt_groupnorm_silu": (P, 0, 512, 128 * 128, 32, P, P, 1e-6, 1, P, P,
+                              lib.dt_groupnorm_workspace_bytes(0, 512, 128 * 128, 32), BF16, None),
+        "dt_groupnorm_silu_noalloc": (P, 0, 512, 128 * 128, 32, P, P, 1e-6, 1, P, BF16, None),
+    }
+    for qt, bs in ((Q8, 34), (Q4, 144)):
+        calls[f"dt_dequant q{qt}"] = (P, qt, 0, D, D // (32 if qt == Q8 else 256) * bs, P, D, BF16, None)
+    failed = {}
+    for name, args in calls.items():
+        rc = getattr(lib, name.split()[0])(*args)
+        if rc != 0:
+            failed[name] = lib.dt_last_error().decode()
+    assert not failed, failed
+
+
 def test_prepare_repeats_the_recorded_call():
     """dit_hip.prepare runs a wrapper once and returns a launch that repeats
     the same C-ABI call with the converted arguments (here the host-side
