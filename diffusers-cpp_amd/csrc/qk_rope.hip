@@ -380,8 +380,9 @@ int qk_prepare(const void* q, const void* k, void* q_out, void* k_out, const flo
         for (int a = 0; a < n_axes; ++a)
             DT_REQUIRE(pos.ptr[a] != nullptr, "dt_qk_rmsnorm_rope: null position pointer for axis %d", a);
     }
-    DT_REQUIRE(!q || (q_out && wq), "dt_qk_rmsnorm_rope: q given without q_out/wq");
-    DT_REQUIRE(!k || (k_out && wk), "dt_qk_rmsnorm_rope: k given without k_out/wk");
+    // an empty input (no tokens) touches no pointer, so its outputs may be null
+    DT_REQUIRE(tokens == 0 || !q || (q_out && wq), "dt_qk_rmsnorm_rope: q given without q_out/wq");
+    DT_REQUIRE(tokens == 0 || !k || (k_out && wk), "dt_qk_rmsnorm_rope: k given without k_out/wk");
     QkHalf hq{q, q_out, wq}, hk{k, k_out, wk};
     if (!q) std::swap(hq, hk);  // k alone runs as the first half
     QkShape sh;

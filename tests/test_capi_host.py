@@ -190,6 +190,9 @@ def test_zero_sized_calls_are_no_ops_without_a_device():
                                None, 0, BF16, None),
         "dt_qk_rmsnorm_rope_swiglu": (P, P, P, P, 0, 24, 128, D, 128, D, 128, P, P, 1e-6, P, 4, 4, 32, 1e4,
                                       None, 0, P, 2 * I, P, 2 * I, P, I, 0, I, BF16, None),
+        # empty outputs may come as null pointers (an empty torch tensor has none)
+        "dt_qk_rmsnorm_rope null outputs": (P, P, None, None, 0, 24, 128, D, 128, D, 128, P, P, 1e-6, P, 4, 4,
+                                            32, 1e4, None, 0, BF16, None),
         "dt_groupnorm_silu": (P, 0, 512, 128 * 128, 32, P, P, 1e-6, 1, P, P,
                               lib.dt_groupnorm_workspace_bytes(0, 512, 128 * 128, 32), BF16, None),
         "dt_groupnorm_silu_noalloc": (P, 0, 512, 128 * 128, 32, P, P, 1e-6, 1, P, BF16, None),

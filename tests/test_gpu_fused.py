@@ -216,6 +216,37 @@ def test_qk_rmsnorm_rope_swiglu(orc, dev, dtype, n_txt, grid, heads, head_dim, i
     check(host(y), orc.swiglu(g, u), dtype, "swiglu")
 
 
+@pytest.mark.parametrize("dtype", DT)
+def test_qk_rmsnorm_rope_swiglu_with_an_empty_half(orc, dev, dtype):
+    """The fused entry with zero SwiGLU rows runs the QK half alone, and with
+    zero tokens the SwiGLU half alone: each equals its separate kernel bit
+    for bit, and the empty half's outputs are left untouched."""
+    pos = flux_positions(16, 8)
+    S, H, inner = pos.shape[0], 24, 9216
+    q = orc.randn(SEED + 37, (S, H, 128))
+    k = orc.randn(SEED + 38, (S, H, 128))
+    wq = orc.randn(SEED + 39, (128,), mean=1.0, std=0.02)
+    gu = orc.randn(SEED + 40, (S, 2 * inner))
+    dq, dk, dgu = dev_tensor(q, dtype), dev_tensor(k, dtype), dev_tensor(gu, dtype)
+    dw = dev_tensor(wq, torch.float32)
+    pt = torch.from_numpy(pos).cuda()
+    tab = dit_hip.rope_table(512, 32, 10000.0)
+    qs, ks = dit_hip.qk_rmsnorm_rope(dq, dk, dw, dw, pt, 32, 10000.0, 1e-6, table=tab)
+    ys = dit_hip.swiglu(dgu[:, :inner], dgu[:, inner:])
+    # zero SwiGLU rows: q and k only
+    y0 = torch.full((0, inner), 3.0, dtype=dtype, device="cuda")
+    qo, ko, _ = dit_hip.qk_rmsnorm_rope_swiglu(dq, dk, dw, dw, pt, 32, 10000.0, dgu[:0, :inner], dgu[:0, inner:],
+                                               1e-6, table=tab, out=y0)
+    # zero tokens: the SwiGLU only; the (empty) q/k outputs are not touched
+    qe = torch.full((0, H, 128), 3.0, dtype=dtype, device="cuda")
+    _, _, y = dit_hip.qk_rmsnorm_rope_swiglu(dq[:0], dk[:0], dw, dw, pt[:0], 32, 10000.0, dgu[:, :inner],
+                                             dgu[:, inner:], 1e-6, table=tab, q_out=qe, k_out=qe.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(qo, qs) and torch.equal(ko, ks)
+    assert torch.equal(y, ys)
+    check(host(qo), orc.qk_rmsnorm_rope(as_input(q, dtype), wq, pos, 32, 10000.0, 1e-6), dtype, "q alone")
+
+
 # ------------------------------------------------------------------ SwiGLU ----
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("rows,inner", [(4608, 9216), (33, 3072), (5, 7)])
