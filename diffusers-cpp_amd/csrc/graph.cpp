@@ -652,12 +652,20 @@ bool match_gemm_add(Graph& g, const dt_tensor* a, Plan& p) {
 constexpr const char* kMulMatOperands =
     "dt_graph_compute: MUL_MAT needs BF16 or whole Q8_0_SPLIT weight rows and BF16 activation rows";
 
-int run_mul_mat(hipStream_t st, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
+// A MUL_MAT with BF16 weights, through the backend's provider: hipBLASLt
+// (the vendor library for plain GEMMs) or the library's MFMA GEMM.
+bool lib_gemm(dt_backend* be, const GemmArgs& g) { return !g.bs && backend_gemm_provider(be) == DT_GEMM_HIPBLASLT; }
+
+int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
+    hipStream_t st = backend_stream(be);
     GemmArgs g;
     int64_t ldc = 0, ldd = 0;
     DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
     DT_REQUIRE(out_rows(out, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
     if (addend) DT_REQUIRE(out_rows(addend, g.N, &ldd), "dt_graph_compute: bad GEMM addend");
+    if (lib_gemm(be, g))
+        return backend_lib_gemm(be, g.a, g.lda, g.b, g.ldb, out->data, ldc, g.M, g.N, g.K,
+                                addend ? addend->data : nullptr, ldd, out->type);
     if (g.bs)
         return dt_gemm_q8_0(g.a, g.lda, g.b, g.ldb, g.bs, g.ldbs, out->data, ldc, g.M, g.N, g.K, nullptr,
                             addend ? addend->data : nullptr, ldd, out->type, st);
@@ -676,10 +684,15 @@ const void* data_of(const dt_tensor* t) {
     return t && t->data ? (const char*)t->data + off : nullptr;
 }
 
-int run_gemm_group(hipStream_t st, const std::vector<const dt_tensor*>& members) {
+// Independent MUL_MATs at one position: one grouped MFMA launch, or one
+// hipBLASLt call each (its single calls beat the grouped MFMA launch: the
+// single-stream block's five projections 0.62 against 0.82 ms).
+int run_gemm_group(dt_backend* be, const std::vector<const dt_tensor*>& members) {
+    hipStream_t st = backend_stream(be);
     dt_gemm_problem ps[8];
     const int n = (int)members.size();
     DT_REQUIRE(n >= 1 && n <= 8, "dt_graph_compute: GEMM group of %d", n);
+    bool lib = true;
     for (int i = 0; i < n; ++i) {
         const dt_tensor* mm = members[i];
         GemmArgs g;
@@ -688,8 +701,17 @@ int run_gemm_group(hipStream_t st, const std::vector<const dt_tensor*>& members)
         DT_REQUIRE(out_rows(mm, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
         ps[i] = dt_gemm_problem{data_of(mm->src[1]), g.lda, data_of(mm->src[0]), g.ldb, mm->data, ldc, nullptr, 0,
                                 nullptr, g.M, g.N, g.K, g.bs, g.ldbs};
+        lib = lib && lib_gemm(be, g);
     }
-    return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
+    if (!lib) return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
+    for (int i = 0; i < n; ++i) {
+        const dt_gemm_problem& q = ps[i];
+        const int rc = backend_lib_gemm(be, q.A, q.lda, q.B, q.ldb, q.C, q.ldc, q.M, q.N, q.K, nullptr, 0,
+                                        members[0]->type);
+        if (rc) return rc;
+    }
+    g_kernels += n - 1;
+    return DT_OK;
 }
 
 // Forward pass over unfused MUL_MATs: node i starts a group of the MUL_MATs
@@ -994,10 +1016,10 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
             return dt_op_unary(DT_UN_SILU, p.in[0], root, 0.f, 0.f, st);
         case K_GEMM_ADD:
             ++g_kernels;
-            return run_mul_mat(st, p.in[0], root, p.in[1]);
+            return run_mul_mat(be, p.in[0], root, p.in[1]);
         case K_GEMM_GROUP:
             ++g_kernels;
-            return run_gemm_group(st, p.members);
+            return run_gemm_group(be, p.members);
         case K_QK_SWIGLU: {
             const int es = elem_size(root->type);
             const int n_axes = (int)p.pos.size();
@@ -1096,7 +1118,7 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
             return dt_op_cpy(t->src[0], t, st);
         case DT_OP_MUL_MAT:
             ++g_kernels;
-            return run_mul_mat(st, t, t, nullptr);
+            return run_mul_mat(be, t, t, nullptr);
         case DT_OP_FLASH_ATTN_EXT:
             ++g_kernels;
             return run_flash_attn(st, t);

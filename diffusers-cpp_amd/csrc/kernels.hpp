@@ -93,4 +93,11 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out);
 constexpr int kBackendRopePositions = 4096;
 int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out);
 
+// The backend's GEMM provider (DT_GEMM_HIPBLASLT or DT_GEMM_MFMA), and a
+// plain bf16 GEMM through its hipBLASLt state (made on first use; that
+// counts as a scratch move for captured graphs).
+int backend_gemm_provider(dt_backend* be);
+int backend_lib_gemm(dt_backend* be, const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K, const void* addend, int64_t ldd, int32_t out_type);
+
 }  // namespace dit

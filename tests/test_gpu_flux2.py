@@ -213,8 +213,10 @@ def test_model_small_q8_0_weights(orc, tmp):
     """The same model with --weight-format q8_0: every Linear weight is
     quantised to Q8_0 on the device, repacked (DT_TYPE_Q8_0_SPLIT) and
     dequantised inside the GEMMs.  The output equals, bit for bit, the bf16
-    path run on the oracle's bf16 rounding of dequantize(quantize(W)), and is
-    held to the bf16 bar against the oracle's fp32 model on those weights."""
+    path through the library's MFMA GEMM (--gemm mfma: the Q8_0 GEMM's own
+    accumulation order) run on the oracle's bf16 rounding of
+    dequantize(quantize(W)), and is held to the bf16 bar against the
+    oracle's fp32 model on those weights."""
     import oracle.flux2 as of
     cfg = SMALL_MODEL
     P = make_params(orc, of.model_param_shapes(cfg), 5000)
@@ -233,7 +235,7 @@ def test_model_small_q8_0_weights(orc, tmp):
     assert sq["weight_format"] == "q8_0"
     qdir = os.path.join(tmp, "dequantized")
     os.makedirs(qdir)
-    sb = _run_small_model(f, write_params(qdir, Pq), ob, n_img, n_txt)
+    sb = _run_small_model(f, write_params(qdir, Pq), ob, n_img, n_txt, "--gemm", "mfma")
     assert sb["weight_format"] == "bf16" and sb["kernels"] == sq["kernels"]
     got_q, got_b = read_dtb(oq), read_dtb(ob)
     assert np.array_equal(got_q.view(np.uint32), got_b.view(np.uint32)), \
