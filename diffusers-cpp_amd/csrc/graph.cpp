@@ -652,9 +652,30 @@ bool match_gemm_add(Graph& g, const dt_tensor* a, Plan& p) {
 constexpr const char* kMulMatOperands =
     "dt_graph_compute: MUL_MAT needs BF16 or whole Q8_0_SPLIT weight rows and BF16 activation rows";
 
-// A MUL_MAT with BF16 weights, through the backend's provider: hipBLASLt
-// (the vendor library for plain GEMMs) or the library's MFMA GEMM.
-bool lib_gemm(dt_backend* be, const GemmArgs& g) { return !g.bs && backend_gemm_provider(be) == DT_GEMM_HIPBLASLT; }
+// MUL_MATs go to the backend's provider: hipBLASLt (the vendor library for
+// plain GEMMs) or the library's MFMA GEMMs.
+bool lib_gemm(dt_backend* be) { return backend_gemm_provider(be) == DT_GEMM_HIPBLASLT; }
+
+// One MUL_MAT through hipBLASLt.  A Q8_0_SPLIT weight is first expanded to
+// its bf16 values (those of dt_dequant and the Q8_0 GEMM) in the backend's
+// scratch, so the product equals the bf16-copy path's bit for bit while only
+// the 1.125-byte weights stay resident.
+int lib_mul_mat(dt_backend* be, const GemmArgs& g, void* C, int64_t ldc, const void* addend, int64_t ldd,
+                int32_t type) {
+    const void* w = g.b;
+    int64_t ldw = g.ldb;
+    if (g.bs) {
+        void* buf = nullptr;
+        int rc = backend_scratch(be, (size_t)g.N * g.K * 2, &buf);
+        if (rc) return rc;
+        rc = q8_split_to_bf16(g.b, g.bs, g.ldbs, g.N, g.K, buf, backend_stream(be));
+        if (rc) return rc;
+        ++g_kernels;
+        w = buf;
+        ldw = g.K;
+    }
+    return backend_lib_gemm(be, g.a, g.lda, w, ldw, C, ldc, g.M, g.N, g.K, addend, ldd, type);
+}
 
 int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
     hipStream_t st = backend_stream(be);
@@ -663,9 +684,7 @@ int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const
     DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
     DT_REQUIRE(out_rows(out, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
     if (addend) DT_REQUIRE(out_rows(addend, g.N, &ldd), "dt_graph_compute: bad GEMM addend");
-    if (lib_gemm(be, g))
-        return backend_lib_gemm(be, g.a, g.lda, g.b, g.ldb, out->data, ldc, g.M, g.N, g.K,
-                                addend ? addend->data : nullptr, ldd, out->type);
+    if (lib_gemm(be)) return lib_mul_mat(be, g, out->data, ldc, addend ? addend->data : nullptr, ldd, out->type);
     if (g.bs)
         return dt_gemm_q8_0(g.a, g.lda, g.b, g.ldb, g.bs, g.ldbs, out->data, ldc, g.M, g.N, g.K, nullptr,
                             addend ? addend->data : nullptr, ldd, out->type, st);
@@ -692,22 +711,22 @@ int run_gemm_group(dt_backend* be, const std::vector<const dt_tensor*>& members)
     dt_gemm_problem ps[8];
     const int n = (int)members.size();
     DT_REQUIRE(n >= 1 && n <= 8, "dt_graph_compute: GEMM group of %d", n);
-    bool lib = true;
+    GemmArgs gs[8];
     for (int i = 0; i < n; ++i) {
         const dt_tensor* mm = members[i];
-        GemmArgs g;
+        GemmArgs& g = gs[i];
         int64_t ldc = 0;
         DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
         DT_REQUIRE(out_rows(mm, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
-        ps[i] = dt_gemm_problem{data_of(mm->src[1]), g.lda, data_of(mm->src[0]), g.ldb, mm->data, ldc, nullptr, 0,
-                                nullptr, g.M, g.N, g.K, g.bs, g.ldbs};
-        lib = lib && lib_gemm(be, g);
+        g.a = data_of(mm->src[1]);
+        g.b = data_of(mm->src[0]);
+        if (g.bs) g.bs = reinterpret_cast<const float*>((const char*)g.b + dt_q8_0_split_scale_offset(g.N, g.K));
+        ps[i] = dt_gemm_problem{g.a, g.lda, g.b, g.ldb, mm->data, ldc, nullptr, 0, nullptr, g.M, g.N, g.K, g.bs,
+                                g.ldbs};
     }
-    if (!lib) return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
+    if (!lib_gemm(be)) return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
     for (int i = 0; i < n; ++i) {
-        const dt_gemm_problem& q = ps[i];
-        const int rc = backend_lib_gemm(be, q.A, q.lda, q.B, q.ldb, q.C, q.ldc, q.M, q.N, q.K, nullptr, 0,
-                                        members[0]->type);
+        const int rc = lib_mul_mat(be, gs[i], ps[i].C, ps[i].ldc, nullptr, 0, members[0]->type);
         if (rc) return rc;
     }
     g_kernels += n - 1;

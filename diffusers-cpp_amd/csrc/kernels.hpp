@@ -93,6 +93,11 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out);
 constexpr int kBackendRopePositions = 4096;
 int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out);
 
+// The bf16 values of a DT_TYPE_Q8_0_SPLIT weight [N][K] (codes, then scales
+// [K/32][ld_scales]) into out [N][K] (dequant.hip).
+int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, int64_t N, int64_t K, void* out,
+                     hipStream_t st);
+
 // The backend's GEMM provider (DT_GEMM_HIPBLASLT or DT_GEMM_MFMA), and a
 // plain bf16 GEMM through its hipBLASLt state (made on first use; that
 // counts as a scratch move for captured graphs).

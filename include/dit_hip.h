@@ -467,16 +467,18 @@ int dt_backend_free(dt_backend *be);
  * caller's stream is never destroyed by the library. */
 int dt_backend_set_stream(dt_backend *be, dt_stream_t stream);
 int dt_backend_synchronize(dt_backend *be);
-/* Which GEMM runs dt_graph_compute's MUL_MATs with BF16 weights (no
- * counterpart in the reference, whose ggml backend picks its own kernels):
- * DT_GEMM_HIPBLASLT (the default) calls hipBLASLt, with one handle, a 32 MiB
- * workspace and per-shape algorithms kept by the backend from the first
- * compute on (so run dt_graph_compute once before dt_graph_capture);
- * DT_GEMM_MFMA runs the library's own MFMA GEMM (dt_gemm_bf16 /
- * dt_gemm_bf16_grouped).  Q8_0_SPLIT weights always take dt_gemm_q8_0, and
- * dt_gemm_q8_0 equals dt_dequant + dt_gemm_bf16 bit for bit, not hipBLASLt.
- * The two providers accumulate in different orders: results agree to fp32
- * rounding before the output's own rounding. */
+/* Which GEMM runs dt_graph_compute's MUL_MATs (no counterpart in the
+ * reference, whose ggml backend picks its own kernels): DT_GEMM_HIPBLASLT
+ * (the default) calls hipBLASLt, with one handle, a 32 MiB workspace and
+ * per-shape algorithms kept by the backend from the first compute on (so
+ * run dt_graph_compute once before dt_graph_capture);
+ * a Q8_0_SPLIT weight is expanded to its bf16 values (dt_dequant's) in the
+ * backend's scratch just before its call, so it gives the bf16-copy path's
+ * result bit for bit.  DT_GEMM_MFMA runs the library's own MFMA GEMMs
+ * (dt_gemm_bf16 / dt_gemm_bf16_grouped; dt_gemm_q8_0 for Q8_0_SPLIT
+ * weights, which equals dt_dequant + dt_gemm_bf16 bit for bit).  The two
+ * providers accumulate in different orders: results agree to fp32 rounding
+ * before the output's own rounding. */
 enum { DT_GEMM_HIPBLASLT = 0, DT_GEMM_MFMA = 1 };
 int dt_backend_set_gemm(dt_backend *be, int32_t provider);
 int dt_buffer_alloc(dt_backend *be, size_t bytes, void **out);

@@ -10,10 +10,11 @@ that do not depend on size:
   - the output is finite, and its spread is what the random weights give:
     proj_out has 3072 inputs of unit-variance rows times N(0, 0.02) weights,
     std ~ 0.02 * sqrt(3072) = 1.11 (band 0.7 .. 1.6);
-  - keeping the weights as Q8_0 (dequantised inside the GEMMs) gives the bf16
-    copy path's output bit for bit when that path runs the library's MFMA
-    GEMM (--gemm mfma); the default hipBLASLt GEMMs accumulate in another
-    order, and their step stays within rounding of it;
+  - keeping the weights as Q8_0 gives the bf16 copy path's output bit for
+    bit with either GEMM provider: hipBLASLt (the default) on the weights
+    expanded to bf16 per GEMM, or the library's MFMA GEMM with the
+    dequantisation in its load path (--gemm mfma); the two providers
+    accumulate in different orders, and their steps agree to rounding;
   - replaying the step as a HIP graph gives the eager output bit for bit;
   - node memory placed as ggml_gallocr places it (node order), with the
     executor holding back the launches that would read reused memory, stays
@@ -57,7 +58,7 @@ def step(tag, *extra):
 
 
 def test_full_step_output_is_finite_with_the_expected_spread():
-    st, o = step("bf16")
+    st, o = step("bf16", "--gemm", "hipblaslt")
     assert o.shape == (1, 4096, 128)
     out = st["output"]
     assert out["elements"] == 4096 * 128 and out["nonfinite"] == 0
@@ -66,12 +67,13 @@ def test_full_step_output_is_finite_with_the_expected_spread():
     assert abs(float(np.std(o.astype(np.float64))) - out["std"]) < 1e-3 * out["std"]
 
 
-def test_full_step_q8_0_weights_equal_bf16_copies_bit_for_bit():
-    sm, om = step("mfma", "--gemm", "mfma")
-    sq, oq = step("q8_0", "--weight-format", "q8_0")
-    assert sq["weight_format"] == "q8_0" and sq["kernels"] == sm["kernels"] and sm["gemm"] == "mfma"
-    assert sq["output"]["fnv64"] == sm["output"]["fnv64"]
-    assert np.array_equal(oq.view(np.uint32), om.view(np.uint32))
+@pytest.mark.parametrize("gemm", ["hipblaslt", "mfma"])
+def test_full_step_q8_0_weights_equal_bf16_copies_bit_for_bit(gemm):
+    sb, ob = step("bf16" if gemm == "hipblaslt" else "mfma", "--gemm", gemm)
+    sq, oq = step("q8_0 " + gemm, "--weight-format", "q8_0", "--gemm", gemm)
+    assert sq["weight_format"] == "q8_0" and sb["gemm"] == sq["gemm"] == gemm
+    assert sq["output"]["fnv64"] == sb["output"]["fnv64"]
+    assert np.array_equal(oq.view(np.uint32), ob.view(np.uint32))
 
 
 def test_full_step_hipblaslt_and_mfma_gemms_agree():
@@ -80,7 +82,7 @@ def test_full_step_hipblaslt_and_mfma_gemms_agree():
     (fp32 rounding), which 25 blocks of bf16 activations carry to the output
     as rounding noise (the same order as the node-order placement's, whose
     parity with the oracle is held at full depth below)."""
-    sb, ob = step("bf16")
+    sb, ob = step("bf16", "--gemm", "hipblaslt")
     sm, om = step("mfma", "--gemm", "mfma")
     assert sb["gemm"] == "hipblaslt" and sb["output"]["nonfinite"] == 0
     rel, cos = bf16_metrics(ob, om)
@@ -89,7 +91,7 @@ def test_full_step_hipblaslt_and_mfma_gemms_agree():
 
 
 def test_full_step_hip_graph_replay_equals_eager_bit_for_bit():
-    sb, ob = step("bf16")
+    sb, ob = step("bf16", "--gemm", "hipblaslt")
     sg, og = step("graph", "--hip-graph", "true", "--warmup", "1", "--steps", "3")
     assert sg["hip_graph"] is True
     assert sg["output"]["fnv64"] == sb["output"]["fnv64"]
@@ -104,7 +106,7 @@ def test_full_step_node_order_allocation():
     unrelated values and a cosine far below that; the placement's parity with
     the oracle is held at the bf16 bar on the same 5 + 20 block depth at
     width 256 (test_deep_model_both_placements_match_the_oracle)."""
-    sb, ob = step("bf16")
+    sb, ob = step("bf16", "--gemm", "hipblaslt")
     sn, on = step("node-order", "--alloc", "node-order")
     assert sn["alloc"] == "node-order" and sn["launches_held"] > 0
     assert sn["output"]["nonfinite"] == 0
