@@ -439,8 +439,9 @@ __global__ __launch_bounds__(256) void q8_0_split_kernel(const uint8_t* __restri
 // The bf16 values of a DT_TYPE_Q8_0_SPLIT weight (codes q + 128 [N][ld_codes
 // = K], scales [K/32][ld_scales]): w[n][k] = d * q rounded to bf16 -- d * q
 // is exact in fp32 (11-bit x 8-bit significands), so these are dt_dequant's
-// and the Q8_0 GEMM's operand values.  One thread per 8 outputs of a row;
-// default-policy stores, since the GEMM that follows reads them at once.
+// and the Q8_0 GEMM's operand values.  One thread per 16 outputs of a row
+// (one 16-byte load of codes, streamed: they are read once); default-policy
+// stores, since the GEMM that follows reads them at once.
 __global__ __launch_bounds__(256) void q8_split_to_bf16_kernel(const uint8_t* __restrict__ codes,
                                                                const float* __restrict__ scales,
                                                                int64_t ld_scales, uint32_t total, FastDiv chunks,
@@ -448,17 +449,22 @@ __global__ __launch_bounds__(256) void q8_split_to_bf16_kernel(const uint8_t* __
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= total) return;
     const uint32_t n = fdiv(idx, chunks);
-    const uint32_t k0 = (idx - n * chunks.d) * 8;
-    const uint2 c = *reinterpret_cast<const uint2*>(codes + (int64_t)n * K + k0);
+    const uint32_t k0 = (idx - n * chunks.d) * 16;
+    const uint4 c = ld_stream(codes + (int64_t)n * K + k0);
     const float d = scales[(int64_t)(k0 >> 5) * ld_scales + n];
-    float v[8];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    uint32_t pk[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = mul_rn(d, (float)((int)((c.x >> (8 * i)) & 0xFF) - 128));
-        v[4 + i] = mul_rn(d, (float)((int)((c.y >> (8 * i)) & 0xFF) - 128));
+    for (int j = 0; j < 4; ++j) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = mul_rn(d, (float)((int)((w[j] >> (8 * i)) & 0xFF) - 128));
+        pk[2 * j] = pack_bf16x2(v[0], v[1]);
+        pk[2 * j + 1] = pack_bf16x2(v[2], v[3]);
     }
-    *reinterpret_cast<uint4*>(out + (int64_t)n * K + k0) = make_uint4(
-        pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+    uint4* o = reinterpret_cast<uint4*>(out + (int64_t)n * K + k0);
+    o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
 }
 
 }  // namespace
@@ -467,13 +473,13 @@ int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, 
                      hipStream_t st) {
     DT_REQUIRE(N >= 0 && K > 0 && K % 32 == 0 && ld_scales >= N, "q8_split_to_bf16: bad shape");
     if (N == 0) return DT_OK;
-    DT_REQUIRE(codes && scales && out && aligned16(out) && (reinterpret_cast<uintptr_t>(codes) & 7) == 0,
+    DT_REQUIRE(codes && scales && out && aligned16(out) && aligned16(codes),
                "q8_split_to_bf16: null or misaligned pointer");
-    const int64_t total = N * (K / 8);
+    const int64_t total = N * (K / 16);
     DT_REQUIRE(total < (1ll << 31), "q8_split_to_bf16: %lld chunks exceed 2^31", (long long)total);
     hipLaunchKernelGGL(q8_split_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                       (const uint8_t*)codes, scales, ld_scales, (uint32_t)total, make_fastdiv((uint32_t)(K / 8)), K,
-                       (bf16*)out);
+                       (const uint8_t*)codes, scales, ld_scales, (uint32_t)total, make_fastdiv((uint32_t)(K / 16)),
+                       K, (bf16*)out);
     return check_launch("q8_split_to_bf16");
 }
 
