@@ -257,7 +257,9 @@ int backend_lib_gemm(dt_backend* be, const void* A, int64_t lda, const void* B, 
                      int64_t M, int64_t N, int64_t K, const void* addend, int64_t ldd, int32_t out_type) {
     DT_REQUIRE(be != nullptr, "backend_lib_gemm: null backend");
     if (!be->lt) {
-        const int rc = lt_create(&be->lt);
+        int rc = lt_refuse_under_capture(be->stream, "hipBLASLt: the backend's first GEMM");
+        if (rc) return rc;
+        rc = lt_create(&be->lt);
         if (rc) return rc;
         ++be->generation;  // a capture that made the state must not be kept
     }

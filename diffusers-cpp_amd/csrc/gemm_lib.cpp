@@ -119,12 +119,22 @@ void lt_destroy(LtState* st) {
     delete st;
 }
 
-static int lt_plan(LtState* st, const LtKey& k, LtPlan** out) {
+int lt_refuse_under_capture(hipStream_t stream, const char* what) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return fail(DT_ERR_HIP, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(DT_ERR_INVALID_ARG, "%s during graph capture; run dt_graph_compute once before capturing", what);
+    return DT_OK;
+}
+
+static int lt_plan(LtState* st, const LtKey& k, hipStream_t stream, LtPlan** out) {
     auto it = st->plans.find(k);
     if (it != st->plans.end()) {
         *out = &it->second;
         return DT_OK;
     }
+    if (const int rc = lt_refuse_under_capture(stream, "hipBLASLt: a GEMM shape first seen")) return rc;
     LtPlan p;
     int rc = DT_OK;
     const hipDataType ot = hip_type(k.out_type);
@@ -183,7 +193,7 @@ int lt_gemm(LtState* st, hipStream_t stream, const void* A, int64_t lda, const v
     if (M == 0 || N == 0) return DT_OK;
     DT_REQUIRE(K > 0 && lda >= K && ldb >= K && ldc >= N && (!addend || ldd >= N), "lt_gemm: bad shape");
     LtPlan* p = nullptr;
-    const int rc = lt_plan(st, LtKey{M, N, K, lda, ldb, ldc, addend ? ldd : 0, out_type}, &p);
+    const int rc = lt_plan(st, LtKey{M, N, K, lda, ldb, ldc, addend ? ldd : 0, out_type}, stream, &p);
     if (rc) return rc;
     const float alpha = 1.0f, beta = addend ? 1.0f : 0.0f;
     DT_LT(hipblasLtMatmul(st->handle, p->desc, &alpha, B, p->a, A, p->b, &beta, addend ? addend : C, p->c, C, p->d,

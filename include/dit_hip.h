@@ -471,7 +471,8 @@ int dt_backend_synchronize(dt_backend *be);
  * reference, whose ggml backend picks its own kernels): DT_GEMM_HIPBLASLT
  * (the default) calls hipBLASLt, with one handle, a 32 MiB workspace and
  * per-shape algorithms kept by the backend from the first compute on (so
- * run dt_graph_compute once before dt_graph_capture);
+ * run dt_graph_compute once before dt_graph_capture; a capture that reaches
+ * a GEMM shape no eager compute has run fails);
  * a Q8_0_SPLIT weight is expanded to its bf16 values (dt_dequant's) in the
  * backend's scratch just before its call, so it gives the bf16-copy path's
  * result bit for bit.  DT_GEMM_MFMA runs the library's own MFMA GEMMs
@@ -575,7 +576,10 @@ int dt_graph_last_stats_ex(int32_t *kernels_launched, int32_t *nodes_fused, int3
  * instead of the fusion pass plus a launch per kernel (the role of the
  * reference's repeated ggml_backend_graph_compute, ExecutionRuntime.cpp:227,
  * 254).  Call dt_graph_compute on the same nodes once first, so the
- * backend's scratch and RoPE table exist (capture allocates nothing).  The
+ * backend's scratch and RoPE table, and with DT_GEMM_HIPBLASLT its
+ * hipBLASLt handle and each GEMM shape's plan, exist (capture allocates
+ * nothing; a capture that would make hipBLASLt state fails with
+ * DT_ERR_INVALID_ARG and records nothing).  The
  * replay reads and writes the node data pointers given at capture: inputs
  * are updated in place between replays.  A backend on the NULL stream gets
  * a stream of its own (default priority), used from then on.  The graph

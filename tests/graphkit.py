@@ -139,6 +139,12 @@ class Graph:
         oh = (x.ne[1] + 2 * p1 - d1 * (K - 1) - 1) // s1 + 1
         return self._new(dh.OP_CONV_2D_DIRECT, [ow, oh, w.ne[3], x.ne[3]], x.d.type, [w, x], [s0, s1, p0, p1, d0, d1])
 
+    def mul_mat(self, w, x, type_=None):
+        """ggml_mul_mat(w, x): out[.., m, n] = sum_k x[.., m, k] * w[n, k]
+        (Runtime::mul_mat, src/ggml/Runtime.hpp:136-139), output rows of w.ne[1]."""
+        ne = [w.ne[1], x.ne[1], x.ne[2], x.ne[3]]
+        return self._new(dh.OP_MUL_MAT, ne, type_ if type_ is not None else x.d.type, [w, x])
+
     def flash_attn_ext(self, q, k, v, scale):
         """q ne {D, Sq, H, B}, k / v ne {D, Skv, H, B} -> ne {D, H, Sq, B}."""
         ne = q.ne

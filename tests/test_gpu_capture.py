@@ -98,3 +98,62 @@ def test_dt_graph_capture_replays_match_eager(orc, dev):
     finally:
         lib.dt_graph_exec_free(ex)
         be.close()
+
+
+def test_gemm_state_is_made_outside_captures(orc, dev):
+    """The hipBLASLt provider makes its handle and each GEMM shape's plan on
+    an eager compute, never inside a capture.  Capturing a MUL_MAT graph on a
+    backend that has not run it fails with an error naming the cause; so does
+    a capture that reaches a second, unplanned shape.  The same backend then
+    computes both graphs eagerly, captures them, and each replay reproduces
+    the eager product bit for bit (which agrees with the fp32 product)."""
+    import ctypes
+
+    import dit_hip as dh
+    from graphkit import Backend, Graph
+    lib = dh.load()
+
+    def mm_graph(m, n, k, seed):
+        g = Graph()
+        w = g.leaf(dev_tensor(orc.randn(seed, (n, k), std=0.02), torch.bfloat16))
+        x = g.leaf(dev_tensor(orc.randn(seed + 1, (m, k)), torch.bfloat16))
+        y = g.mul_mat(w, x)
+        y.d.flags |= dh.FLAG_OUTPUT
+        return g, w, x, y
+
+    def capture(g):
+        ex = ctypes.c_void_p()
+        rc = lib.dt_graph_capture(be.h, g._array(), len(g.nodes), ctypes.byref(ex))
+        return rc, ex
+
+    be = Backend()
+    try:
+        assert lib.dt_backend_set_gemm(be.h, dh.GEMM_HIPBLASLT) == 0
+        g1, w1, x1, y1 = mm_graph(40, 96, 64, 31)
+        g2, w2, x2, y2 = mm_graph(72, 160, 128, 41)
+        rc, _ = capture(g1)
+        assert rc != 0 and "before capturing" in lib.dt_last_error().decode()
+        g1.compute(be.h)
+        dh.check(lib.dt_backend_synchronize(be.h), "sync")
+        rc, _ = capture(g2)                 # handle made, this shape not planned
+        assert rc != 0 and "first seen during graph capture" in lib.dt_last_error().decode()
+        for g, w, x, y in ((g1, w1, x1, y1), (g2, w2, x2, y2)):
+            g.compute(be.h)
+            dh.check(lib.dt_backend_synchronize(be.h), "sync")
+            eager = y.torch().clone()
+            ref = x.torch().float() @ w.torch().float().t()
+            err = ((eager.float() - ref).norm() / ref.norm()).item()
+            assert err < 1e-2, err
+            rc, ex = capture(g)
+            dh.check(rc, "dt_graph_capture")
+            try:
+                for rep in range(3):
+                    y.torch().fill_(float("nan"))
+                    torch.cuda.synchronize()
+                    dh.check(lib.dt_graph_exec_launch(be.h, ex), "dt_graph_exec_launch")
+                    dh.check(lib.dt_backend_synchronize(be.h), "sync")
+                    assert torch.equal(y.torch().view(torch.int16), eager.view(torch.int16)), f"replay {rep}"
+            finally:
+                lib.dt_graph_exec_free(ex)
+    finally:
+        be.close()
