@@ -467,6 +467,46 @@ __global__ __launch_bounds__(256) void q8_split_to_bf16_kernel(const uint8_t* __
     o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
 }
 
+// The same values over tiles of 16 rows x 256 codes.  The scales are stored
+// [K/32][ld_scales], so one row's scales are ld_scales floats apart: a wave of
+// the kernel above reads its 32 scales from 32 cache lines.  Here the tile's
+// 8 x 16 scales arrive as 8 runs of 16 consecutive floats through LDS, and
+// each thread expands 16 codes of one row (16 threads per 256-code run).
+// Measured on 3072 x 3072 .. 3072 x 12288: 12-15% faster than the kernel
+// above, and as fast as or faster than tiles of 8 x 512, 4 x 1024 or 2 x 2048
+// codes or 2-4 runs per thread.
+constexpr int kQ8TileRows = 16, kQ8TileRun = 256;
+
+__global__ __launch_bounds__(256) void q8_split_to_bf16_tiled_kernel(const uint8_t* __restrict__ codes,
+                                                                     const float* __restrict__ scales,
+                                                                     int64_t ld_scales, int64_t K,
+                                                                     bf16* __restrict__ out) {
+    static_assert(kQ8TileRows == 16 && kQ8TileRun == 16 * 16, "the index arithmetic assumes 16 x 256 tiles");
+    __shared__ float sd[kQ8TileRun / 32][kQ8TileRows];
+    const int t = threadIdx.x;
+    const int64_t n0 = (int64_t)blockIdx.y * kQ8TileRows, k0 = (int64_t)blockIdx.x * kQ8TileRun;
+    if (t < (kQ8TileRun / 32) * kQ8TileRows)
+        sd[t >> 4][t & 15] = scales[(k0 / 32 + (t >> 4)) * ld_scales + n0 + (t & 15)];
+    const int row = t >> 4, ch = t & 15;
+    const int64_t at = (n0 + row) * K + k0 + ch * 16;
+    const uint4 c = ld_stream(codes + at);
+    __syncthreads();
+    const float d = sd[ch >> 1][row];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    uint32_t pk[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = mul_rn(d, (float)((int)((w[j] >> (8 * i)) & 0xFF) - 128));
+        pk[2 * j] = pack_bf16x2(v[0], v[1]);
+        pk[2 * j + 1] = pack_bf16x2(v[2], v[3]);
+    }
+    uint4* o = reinterpret_cast<uint4*>(out + at);
+    o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+}
+
 }  // namespace
 
 int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, int64_t N, int64_t K, void* out,
@@ -475,6 +515,12 @@ int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, 
     if (N == 0) return DT_OK;
     DT_REQUIRE(codes && scales && out && aligned16(out) && aligned16(codes),
                "q8_split_to_bf16: null or misaligned pointer");
+    if (N % kQ8TileRows == 0 && K % kQ8TileRun == 0 && N / kQ8TileRows < 65536 && K / kQ8TileRun < (1ll << 31)) {
+        const dim3 grid((unsigned)(K / kQ8TileRun), (unsigned)(N / kQ8TileRows));
+        hipLaunchKernelGGL(q8_split_to_bf16_tiled_kernel, grid, dim3(256), 0, st, (const uint8_t*)codes, scales,
+                           ld_scales, K, (bf16*)out);
+        return check_launch("q8_split_to_bf16");
+    }
     const int64_t total = N * (K / 16);
     DT_REQUIRE(total < (1ll << 31), "q8_split_to_bf16: %lld chunks exceed 2^31", (long long)total);
     hipLaunchKernelGGL(q8_split_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
