@@ -131,6 +131,7 @@ struct Plan {
     Kind kind = K_NONE;
     const dt_tensor* in[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     float eps = 0.f;
+    float addend = 0.f;  // adaLN: added to every scale (the 1 of 1 + scale)
     int silu = 0;
     int up2 = 0;  // CONV: the input is upsampled 2x (nearest) on the fly
     // QK
@@ -179,6 +180,51 @@ struct Graph {
 
 const dt_tensor* nodes_at(const Graph& g, int i) { return g.nodes[i]; }
 
+// The modulation factor t = ADD(s, FILL(c)) of n * (1 + scale): s an fp32
+// vector of `cols`, the scalar FILL of Tensor.hpp:233-236 (`1.0f + scale`
+// becomes add(scale, full(1))), both used only here, possibly seen through a
+// zero-offset VIEW of the same vector (AdaLayerNormContinuous.inl:30-40
+// indexes (1 + scale)[:, None, :]).  The adaLN kernels add c to each scale
+// as they stage it -- the ADD's own single fp32 rounding -- so the ADD and
+// the FILL need no launches.  Otherwise t itself is the factor.
+struct ScaleFactor {
+    const dt_tensor* vec = nullptr;
+    float addend = 0.f;
+    const dt_tensor* add = nullptr;   // claimed with the plan
+    const dt_tensor* fill = nullptr;
+    const dt_tensor* view = nullptr;
+};
+
+bool scale_factor(Graph& g, const dt_tensor* t, int64_t cols, ScaleFactor* out) {
+    *out = ScaleFactor{t, 0.f, nullptr, nullptr, nullptr};
+    if (!is_vec(t, cols)) return false;
+    const dt_tensor* view = nullptr;
+    const dt_tensor* a = t;
+    if (t->op == DT_OP_VIEW && view_offset(t) == 0 && g.internal(t)) {
+        view = t;
+        a = t->src[0];
+    }
+    if (a && a->op == DT_OP_ADD && is_vec(a, cols) && g.internal(a))
+        for (int k = 0; k < 2; ++k) {
+            const dt_tensor* v = a->src[k];
+            const dt_tensor* f = a->src[1 - k];
+            if (!f || f->op != DT_OP_FILL || f->type != DT_TYPE_F32 || !g.internal(f) ||
+                f->ne[0] * f->ne[1] * f->ne[2] * f->ne[3] != 1 || !is_vec(v, cols))
+                continue;
+            *out = ScaleFactor{v, fparam(f, 0), a, f, view};
+            return true;
+        }
+    return true;
+}
+
+void claim_factor(Graph& g, const ScaleFactor& f) {
+    if (f.add) {
+        if (f.view) g.claim(f.view);
+        g.claim(f.add);
+        g.claim(f.fill);
+    }
+}
+
 bool match_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     if (a->op != DT_OP_ADD) return false;
     const dt_tensor* m = a->src[0];
@@ -190,15 +236,18 @@ bool match_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     const dt_tensor* x = n->src[0];
     const int64_t cols = x->ne[0];
     int64_t r1, s1, r2, s2;
-    if (!is_vec(t, cols) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
+    ScaleFactor f;
+    if (!scale_factor(g, t, cols, &f) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
         !is_io_type(x->type) || !row_layout(x, &r1, &s1) || !row_layout(a, &r2, &s2))
         return false;
     g.claim(m);
     g.claim(n);
+    claim_factor(g, f);
     p.kind = K_ADALN;
     p.in[0] = x;
-    p.in[1] = t;
+    p.in[1] = f.vec;
     p.in[2] = sh;
+    p.addend = f.addend;
     p.eps = fparam(n, 0);
     return true;
 }
@@ -246,7 +295,8 @@ bool match_res_adaln(Graph& g, const dt_tensor* a, Plan& p) {
         return false;
     const int64_t cols = x->ne[0];
     int64_t r1, s1, r2, s2;
-    if (!is_vec(t, cols) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
+    ScaleFactor f;
+    if (!scale_factor(g, t, cols, &f) || !is_vec(sh, cols) || !same_shape(x, a) || x->type != a->type ||
         !is_io_type(x->type) || !row_layout(x, &r1, &s1) || !row_layout(a, &r2, &s2))
         return false;
     const dt_tensor *h, *o, *gate, *gm;
@@ -256,6 +306,7 @@ bool match_res_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     g.claim(m);
     g.claim(n);
     g.claim(gm);
+    claim_factor(g, f);
     g.deferred[xi->second] = 1;
     g.runs_at[xi->second] = g.current_root;
     p.kind = K_RES_ADALN;
@@ -263,8 +314,9 @@ bool match_res_adaln(Graph& g, const dt_tensor* a, Plan& p) {
     p.in[1] = o;
     p.in[2] = gate;
     p.in[3] = x;
-    p.in[4] = t;
+    p.in[4] = f.vec;
     p.in[5] = sh;
+    p.addend = f.addend;
     p.eps = fparam(n, 0);
     return true;
 }
@@ -976,8 +1028,8 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
             row_layout(p.in[0], &rows, &xs);
             row_layout(root, &rows, &ys);
             ++g_kernels;
-            return adaln_launch(p.in[0]->data, rows, root->ne[0], xs, (const float*)p.in[2]->data,
-                                (const float*)p.in[1]->data, 0.0f, root->data, ys, p.eps,
+            return adaln_launch(p.in[0]->data, rows, root->ne[0], xs, (const float*)data_of(p.in[2]),
+                                (const float*)data_of(p.in[1]), p.addend, root->data, ys, p.eps,
                                 root->type, st);
         }
         case K_GATED: {
@@ -1072,7 +1124,7 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
             ++g_kernels;
             return residual_adaln_launch(data_of(p.in[0]), hs, data_of(p.in[1]), os, (const float*)data_of(p.in[2]),
                                          p.in[3]->data, rs, (const float*)data_of(p.in[5]),
-                                         (const float*)data_of(p.in[4]), 0.0f, root->data, ys, rows, root->ne[0],
+                                         (const float*)data_of(p.in[4]), p.addend, root->data, ys, rows, root->ne[0],
                                          p.eps, root->type, st);
         }
         case K_CONV:

@@ -255,12 +255,13 @@ def test_graph_single_block_chain_fused(orc, be, dtype, S, D, H, I):
     for name, node in outs.items():
         got = host(node.torch()).reshape(want[name].shape)
         check(got, want[name], dtype, name)
-    # fill + (scale+1) + adaLN + 4 position CONTs + (q, k and SwiGLU in one
+    # adaLN with its 1 + scale + 4 position CONTs + (q, k and SwiGLU in one
     # launch) + residual
-    assert kernels == 9, kernels
-    # claimed nodes: norm + mul (2); per q/k: rms, mul, 4 views, 4 ropes and the
-    # 2 inner concats (12 each); swiglu sigmoid + mul (2); residual mul (1)
-    assert fused == 2 + 24 + 2 + 1, fused
+    assert kernels == 7, kernels
+    # claimed nodes: norm + mul and the fill + (scale+1) of the factor (4);
+    # per q/k: rms, mul, 4 views, 4 ropes and the 2 inner concats (12 each);
+    # swiglu sigmoid + mul (2); residual mul (1)
+    assert fused == 4 + 24 + 2 + 1, fused
 
 
 @pytest.mark.parametrize("dtype", DT)

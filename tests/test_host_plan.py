@@ -3,11 +3,12 @@ planned without a device (dit_cli --plan-only): graph size, the GEMM and
 attention node counts, the parameter count of the 4B-shaped configuration,
 and how many nodes each block type hands to fused kernels.
 
-Per single-stream block 32 nodes are absorbed: adaLN 2 (NORM, MUL), each of
+Per single-stream block 34 nodes are absorbed: adaLN 4 (NORM, MUL, and the
+ADD and FILL of its 1 + scale, Tensor.hpp:233-236), each of
 q and k 12 (RMS_NORM, MUL, 4 x (VIEW, ROPE), 2 inner CONCATs), q's root
 CONCAT and its permuted VIEW into the attention's prologue 2, SwiGLU 2
 (SIGMOID, MUL), gated residual 1 (MUL), GEMM accumulate 1 (MUL_MAT).  Per
-double-stream block 48: 4 adaLNs x 2, q and k 15 each (two RMS_NORM + MUL
+double-stream block 56: 4 adaLNs x 4, q and k 15 each (two RMS_NORM + MUL
 segments joined by the txt|img CONCAT, plus the RoPE tree), q's root and
 view 2, 2 SwiGLUs x 2, 4 gated residuals x 1."""
 import json
@@ -50,8 +51,8 @@ def test_q8_0_weights_plan_like_bf16():
 
 
 @pytest.mark.parametrize("kind,layers,nodes,fused,mm,grouped,deferred", [
-    ("single", dict(num_layers=0), 58, 32, 7, 5, 1),
-    ("double", dict(num_single_layers=0), 110, 48, 14, 8, 4),
+    ("single", dict(num_layers=0), 58, 34, 7, 5, 1),
+    ("double", dict(num_single_layers=0), 110, 56, 14, 8, 4),
 ])
 def test_per_block_fusion(kind, layers, nodes, fused, mm, grouped, deferred):
     """A second block adds its nodes, fusions and GEMMs; `grouped` roots run
