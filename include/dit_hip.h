@@ -26,6 +26,12 @@
  *  - Strides are in ELEMENTS unless named *_bytes / nb.
  *  - Every function returns 0 (DT_OK) or a DT_ERR_* code and never aborts;
  *    dt_last_error() returns a thread-local message for the last failure.
+ *  - Threads: the kernel entry points ((ii), (iii)) keep no state and may be
+ *    called from any thread.  A dt_backend (its scratch, RoPE table and
+ *    hipBLASLt plans) and the nodes given to its dt_graph_* calls are used
+ *    by one host thread at a time, as the reference builds and computes a
+ *    graph on the thread whose Scope holds it (thread_local, src/ggml/Scope.hpp:74-75);
+ *    separate backends may run on separate threads.
  *  - io_type selects the element type of activations: DT_TYPE_F32 or
  *    DT_TYPE_BF16 (all arithmetic is fp32 either way).  Modulation vectors,
  *    norm weights and rope tables are always fp32.
