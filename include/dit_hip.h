@@ -30,8 +30,9 @@
  *    called from any thread.  A dt_backend (its scratch, RoPE table and
  *    hipBLASLt plans) and the nodes given to its dt_graph_* calls are used
  *    by one host thread at a time, as the reference builds and computes a
- *    graph on the thread whose Scope holds it (thread_local, src/ggml/Scope.hpp:74-75);
- *    separate backends may run on separate threads.
+ *    graph on the thread whose Scope holds it (thread_local,
+ *    src/ggml/Scope.hpp:74-75); separate backends may run on separate
+ *    threads.
  *  - io_type selects the element type of activations: DT_TYPE_F32 or
  *    DT_TYPE_BF16 (all arithmetic is fp32 either way).  Modulation vectors,
  *    norm weights and rope tables are always fp32.
