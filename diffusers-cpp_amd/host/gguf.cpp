@@ -286,6 +286,10 @@ GgufFile::GgufFile(const std::string& path_in) : path_(find_gguf(path_in)) {
             if (!be)
                 fail(path_, "tensor '" + t.name + "' has unsupported ggml type " + std::to_string(t.type));
             if (t.ne[0] % be) fail(path_, "tensor '" + t.name + "': row length is not a multiple of its block size");
+            // elems < 2^63, but 2-4 bytes per element can pass 2^64: a
+            // wrapped byte count would slip past the end-of-file check below.
+            if (elems / (uint64_t)be > std::numeric_limits<uint64_t>::max() / (uint64_t)bb)
+                fail(path_, "tensor '" + t.name + "' has more bytes than 2^64");
             t.nbytes = elems / (uint64_t)be * (uint64_t)bb;
             t.offset = rel;  // made absolute below
             if (index_.count(t.name)) fail(path_, "duplicate tensor name '" + t.name + "'");

@@ -128,6 +128,9 @@ def _bad(orc, tmp, kind):
         gw.write_gguf(path, t, metadata=[("general.alignment", gw.U32, 48)])
     elif kind == "block":
         gw.write_gguf(path, [("q", "Q8_0", [48, 1], b"\0" * 34)])
+    elif kind == "bytes_overflow":
+        # 2^31 x 2^31 F32 elements: 2^64 bytes, which wraps to 0 in 64 bits
+        gw.write_gguf(path, [("x", "F32", [2 ** 31, 2 ** 31], b"\0" * 16)])
     elif kind == "string_length":
         gw.write_gguf(path, t, metadata=[("k", gw.STRING, "v")])
         with open(path, "r+b") as f:
@@ -141,7 +144,7 @@ def _bad(orc, tmp, kind):
     ("truncated_data", "past the end of the file"), ("misaligned", "not a multiple of the alignment"),
     ("unknown_type", "unsupported ggml type 99"), ("dims", "5 dimensions"), ("duplicate", "duplicate tensor name"),
     ("alignment", "power of two"), ("block", "multiple of its block size"),
-    ("string_length", "past the end of the file"),
+    ("string_length", "past the end of the file"), ("bytes_overflow", "more bytes than 2^64"),
 ])
 def test_corrupt_files_are_rejected(orc, tmp, kind, message):
     r = cli("GgufInfo", "--gguf", _bad(orc, tmp, kind))
