@@ -50,11 +50,25 @@ Blob read_blob(const std::string& path) {
     if (!f || hdr[0] != kMagic || hdr[2] < 0 || hdr[2] > 4) throw std::runtime_error("bad tensor file " + path);
     Blob b;
     b.type = hdr[1];
+    if (b.type != DT_TYPE_F32 && b.type != DT_TYPE_I32 && b.type != DT_TYPE_F16 && b.type != DT_TYPE_BF16)
+        throw std::runtime_error("tensor file " + path + ": element type " + std::to_string(b.type) +
+                                 " (F32, F16, BF16 or I32 expected)");
     b.shape.resize(hdr[2]);
     f.read((char*)b.shape.data(), sizeof(int64_t) * hdr[2]);
-    int64_t n = 1;
-    for (int64_t d : b.shape) n *= d;
-    const int64_t es = (b.type == DT_TYPE_F32 || b.type == DT_TYPE_I32) ? 4 : 2;
+    if (!f) throw std::runtime_error("truncated tensor file " + path);
+    const std::streamoff data_at = f.tellg();
+    f.seekg(0, std::ios::end);
+    const uint64_t avail = (uint64_t)(f.tellg() - data_at);
+    f.seekg(data_at);
+    // Every dimension non-negative, and the payload no larger than what the
+    // file holds (which also keeps the element count far from overflow).
+    const uint64_t es = (b.type == DT_TYPE_F32 || b.type == DT_TYPE_I32) ? 4 : 2;
+    uint64_t n = 1;
+    for (int64_t d : b.shape) {
+        if (d < 0 || (d > 0 && n > avail / es / (uint64_t)d))
+            throw std::runtime_error("tensor file " + path + ": its shape needs more bytes than the file holds");
+        n *= (uint64_t)d;
+    }
     b.bytes.resize((size_t)(n * es));
     f.read((char*)b.bytes.data(), (std::streamsize)b.bytes.size());
     if (!f) throw std::runtime_error("truncated tensor file " + path);

@@ -159,6 +159,44 @@ def test_flux2_posembed_reference_cases(orc, cli):
         check(got, want, cli.bf16, "posembed")
 
 
+@pytest.mark.parametrize("kind,message", [
+    ("negative_dim", "needs more bytes than the file holds"),
+    ("dims_overflow", "needs more bytes than the file holds"),
+    ("short_payload", "needs more bytes than the file holds"),
+    ("short_shape", "truncated tensor file"),
+    ("element_type", "element type 8"),
+])
+def test_malformed_tensor_files_are_rejected(dev, kind, message):
+    """A .dtb input whose header disagrees with its bytes (a negative or
+    overflowing shape, a payload shorter than the shape, an element type the
+    format does not carry) ends the command with a message, before any
+    allocation sized by the header."""
+    with tempfile.TemporaryDirectory() as d:
+        good = os.path.join(d, "good.dtb")
+        write_dtb(good, np.ones((2, 5, 48), np.float32), 0)
+        bad = os.path.join(d, "bad.dtb")
+        shape, type_, payload = [2, 5, 48], 0, np.ones(480, np.float32).tobytes()
+        if kind == "negative_dim":
+            shape = [2, -5, 48]
+        elif kind == "dims_overflow":
+            shape = [1 << 31, 1 << 31, 1 << 31]
+        elif kind == "short_payload":
+            payload = payload[:-4]
+        elif kind == "element_type":
+            type_ = 8
+        with open(bad, "wb") as f:
+            f.write(np.array([MAGIC, type_, len(shape), 0], dtype=np.int32).tobytes())
+            if kind == "short_shape":   # the file ends inside the shape
+                f.write(np.array(shape[:2], dtype=np.int64).tobytes())
+            else:
+                f.write(np.array(shape, dtype=np.int64).tobytes())
+                f.write(payload)
+        r = subprocess.run([CLI, "Flux2SwiGLU", "--gate", bad, "--up", good, "--out", os.path.join(d, "o.dtb")],
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode != 0, r.stdout
+        assert message in r.stderr, r.stderr
+
+
 def test_flux2_swiglu(orc, cli):
     g, u = orc.randn(SEED + 9, (2, 5, 48)), orc.randn(SEED + 10, (2, 5, 48))
     gp, gv = cli.act(g)
