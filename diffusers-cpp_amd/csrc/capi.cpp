@@ -161,25 +161,40 @@ extern "C" int dt_buffer_free(dt_backend* be, void* ptr) {
 }
 
 // Bytes of a contiguous tensor (ggml_nbytes): whole blocks for block types.
+// False for negative sizes, unknown types, or a count that overflows int64.
 static bool tensor_bytes(const dt_tensor* t, size_t* out) {
-    int64_t n = 1;
-    for (int i = 1; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i)
         if (t->ne[i] < 0) return false;
-        n *= t->ne[i];
-    }
-    int64_t row;
+    int64_t n = 1;
+    for (int i = 1; i < 4; ++i)
+        if (__builtin_mul_overflow(n, t->ne[i], &n)) return false;
+    int64_t row = 0;
     const int es = dit::elem_size(t->type);
-    if (es) row = t->ne[0] * es;
-    else if (t->type == DT_TYPE_Q8_0) row = (t->ne[0] + 31) / 32 * 34;
-    else if (t->type == DT_TYPE_Q4_K) row = (t->ne[0] + 255) / 256 * 144;
-    else if (t->type == DT_TYPE_Q8_0_SPLIT) row = -1;
-    else if (t->type == DT_TYPE_CONV2D_PACKED) {
+    if (es) {
+        if (__builtin_mul_overflow(t->ne[0], (int64_t)es, &row)) return false;
+    } else if (t->type == DT_TYPE_Q8_0) {
+        row = (t->ne[0] / 32 + (t->ne[0] % 32 != 0)) * 34;
+    } else if (t->type == DT_TYPE_Q4_K) {
+        row = (t->ne[0] / 256 + (t->ne[0] % 256 != 0)) * 144;
+    } else if (t->type == DT_TYPE_Q8_0_SPLIT) {
+        int64_t nk = 0, per = 0, planes = 0, total = 0;
+        if (__builtin_mul_overflow(t->ne[0], t->ne[1], &nk) || nk > (1ll << 60) ||
+            __builtin_mul_overflow(t->ne[2], t->ne[3], &planes))
+            return false;
+        per = dt_q8_0_split_bytes(t->ne[1], t->ne[0]);
+        if (__builtin_mul_overflow(per, planes, &total)) return false;
+        *out = (size_t)total;
+        return true;
+    } else if (t->type == DT_TYPE_CONV2D_PACKED) {
+        if (t->ne[0] > 16 || t->ne[2] > (1 << 20) || t->ne[3] > (1 << 20)) return false;
         *out = dt_conv2d_packed_bytes(t->ne[3], t->ne[2], t->ne[0]);
         return t->ne[1] == t->ne[0] && *out > 0;
-    } else return false;
-    if (t->ne[0] < 0) return false;
-    *out = row < 0 ? dt_q8_0_split_bytes(t->ne[1], t->ne[0]) * (size_t)(t->ne[2] * t->ne[3])
-                   : (size_t)(row * n);
+    } else {
+        return false;
+    }
+    int64_t bytes = 0;
+    if (__builtin_mul_overflow(row, n, &bytes)) return false;
+    *out = (size_t)bytes;
     return true;
 }
 
@@ -188,8 +203,8 @@ static bool contiguous(const dt_tensor* t) {
     if (es == 0) return true;  // block types: caller addresses raw bytes
     int64_t expect = es;
     for (int i = 0; i < 4; ++i) {
-        if (t->ne[i] > 1 && t->nb[i] != expect) return false;
-        expect *= t->ne[i];
+        if (t->ne[i] > 1 && t->nb[i] != (size_t)expect) return false;
+        if (i < 3 && __builtin_mul_overflow(expect, t->ne[i], &expect)) return false;
     }
     return true;
 }

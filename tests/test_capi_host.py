@@ -171,6 +171,35 @@ def test_conv2d_packed_weight_type():
     assert "not supported" in lib.dt_last_error().decode()
 
 
+@pytest.mark.parametrize("type_,ne", [
+    (0, (1 << 31, 1 << 31, 1 << 31, 1)),      # F32: element count past 2^63
+    (30, (1 << 62, 4, 1, 1)),                 # BF16: bytes past 2^63
+    (8, (1 << 62, 1 << 10, 1, 1)),            # Q8_0 blocks x rows past 2^63
+    (100, (1 << 31, 1 << 31, 1, 1)),          # Q8_0_SPLIT: N K past 2^60
+    (0, (4, -1, 1, 1)),                       # a negative size
+])
+def test_tensor_copies_refuse_overflowing_descriptors(type_, ne):
+    """dt_tensor_set / dt_tensor_get bound a copy by the tensor's byte extent;
+    a descriptor whose extent overflows 64 bits (or has a negative size) is
+    refused before any device call, not wrapped into a small or negative
+    bound."""
+    lib = dit_hip.load()
+    t = dit_hip.DtTensor()
+    t.type = type_
+    for i, v in enumerate(ne):
+        t.ne[i] = v
+    es = {0: 4, 30: 2}.get(type_, 1)
+    t.nb[0] = es
+    for i in range(1, 4):
+        t.nb[i] = t.nb[i - 1] * max(ne[i - 1], 1) if type_ in (0, 30) else 0
+    t.data = 0x10000  # never dereferenced
+    buf = ctypes.create_string_buffer(16)
+    for fn in (lib.dt_tensor_set, lib.dt_tensor_get):
+        assert fn(ctypes.byref(t), buf, 0, 16, None) != 0
+        msg = lib.dt_last_error().decode()
+        assert "not supported" in msg or "not contiguous" in msg, msg
+
+
 def test_zero_sized_calls_are_no_ops_without_a_device():
     """Every entry point of the chain, the dequantisation and GroupNorm takes
     an empty input (zero rows, tokens or images) as a successful no-op: it
