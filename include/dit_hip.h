@@ -19,8 +19,10 @@
  *
  * Conventions
  *  - Every pointer named x/y/src/dst/... is DEVICE memory owned by the
- *    caller; the library never allocates device memory except where a
- *    function says so (dt_buffer_alloc).
+ *    caller; the library allocates device memory only in dt_buffer_alloc
+ *    and for a dt_backend's own state, made by its first dt_graph_compute
+ *    that needs it (scratch, RoPE table, hipBLASLt handle and workspace)
+ *    and freed by dt_backend_free.
  *  - `stream` is a hipStream_t (NULL = the default stream).  All kernels are
  *    stream-ordered and asynchronous; none synchronises the device.
  *  - Strides are in ELEMENTS unless named *_bytes / nb.
