@@ -225,7 +225,7 @@ def build_single_block_chain(orc, dtype, S, D, H, I, theta=2000.0):
     go = g.mul(L["o"], gate)
     res = g.add(L["x"], go)
     outs = {"adaln": ada, "q": qr, "k": kr, "swiglu": sw, "residual": res}
-    return g, raw, pos, outs, {"n": n}
+    return g, raw, pos, outs, {"n": n, "t": t}
 
 
 def oracle_single_block(orc, raw, pos, dtype, D, theta):
@@ -262,6 +262,25 @@ def test_graph_single_block_chain_fused(orc, be, dtype, S, D, H, I):
     # per q/k: rms, mul, 4 views, 4 ropes and the 2 inner concats (12 each);
     # swiglu sigmoid + mul (2); residual mul (1)
     assert fused == 4 + 24 + 2 + 1, fused
+
+
+@pytest.mark.parametrize("dtype", DT)
+def test_graph_scale_factor_kept_when_it_is_an_output(orc, be, dtype):
+    """The adaLN absorbs the FILL + ADD of its 1 + scale only when nothing
+    else reads that factor: with the factor requested as an output, its ADD
+    and FILL run as their own kernels (2 more launches, 2 fewer absorbed
+    nodes), the adaLN reads the stored factor, and every output -- the
+    factor included -- still matches the oracle."""
+    S, D, H, I = 12, 256, 2, 512
+    g, raw, pos, outs, inner = build_single_block_chain(orc, dtype, S, D, H, I)
+    kernels, fused = g.compute(be, outputs=list(outs.values()) + [inner["t"]])
+    torch.cuda.synchronize()
+    want = oracle_single_block(orc, raw, pos, dtype, D, 2000.0)
+    for name, node in outs.items():
+        check(host(node.torch()).reshape(want[name].shape), want[name], dtype, name)
+    scale = raw["mod"].reshape(-1)[D:2 * D]
+    assert np.array_equal(host(inner["t"].torch()).reshape(D), (scale + np.float32(1.0)).astype(np.float32))
+    assert kernels == 7 + 2 and fused == 4 + 24 + 2 + 1 - 2, (kernels, fused)
 
 
 @pytest.mark.parametrize("dtype", DT)
