@@ -22,6 +22,7 @@
 #include <fstream>
 #include <iostream>
 #include <map>
+#include <optional>
 #include <random>
 #include <stdexcept>
 #include <string>
@@ -29,6 +30,7 @@
 
 #include "flux2.hpp"
 #include "gguf.hpp"
+#include "resnet.hpp"
 
 using namespace dit::host;
 
@@ -184,6 +186,83 @@ void q8_split_from_f32(const float* f32, int64_t rows, int64_t cols, void* q8, v
           "dt_q8_0_split");
 }
 
+std::string json_str(const std::string& s) {
+    std::string r = "\"";
+    for (unsigned char ch : s) {
+        if (ch == '"' || ch == '\\') {
+            r += '\\';
+            r += (char)ch;
+        } else if (ch < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", ch);
+            r += buf;
+        } else {
+            r += (char)ch;
+        }
+    }
+    return r + "\"";
+}
+
+std::string json_num(double v) {
+    if (!std::isfinite(v)) return "null";
+    char buf[40];
+    std::snprintf(buf, sizeof buf, "%.17g", v);
+    return buf;
+}
+
+float bf16_bits_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Summary of an output tensor's bytes: element count, mean and standard
+// deviation (fp64), count of NaN/Inf, and the FNV-1a hash of the bytes (equal
+// hashes = bit-identical outputs across runs).
+struct OutputCheck {
+    int64_t n = 0, nonfinite = 0;
+    double mean = 0, std = 0;
+    uint64_t fnv = 1469598103934665603ull;
+};
+
+OutputCheck check_output(const std::vector<uint8_t>& bytes, int32_t type) {
+    OutputCheck c;
+    for (uint8_t b : bytes) c.fnv = (c.fnv ^ b) * 1099511628211ull;
+    double s = 0, s2 = 0;
+    const size_t es = type == DT_TYPE_F32 ? 4 : 2;
+    for (size_t i = 0; i + es <= bytes.size(); i += es) {
+        float f;
+        if (type == DT_TYPE_F32) {
+            std::memcpy(&f, bytes.data() + i, 4);
+        } else {
+            uint16_t h;
+            std::memcpy(&h, bytes.data() + i, 2);
+            f = bf16_bits_to_f32(h);
+        }
+        ++c.n;
+        if (!std::isfinite(f)) {
+            ++c.nonfinite;
+            continue;
+        }
+        s += f;
+        s2 += (double)f * f;
+    }
+    const int64_t m = c.n - c.nonfinite;
+    if (m > 0) {
+        c.mean = s / m;
+        c.std = std::sqrt(std::max(0.0, s2 / m - c.mean * c.mean));
+    }
+    return c;
+}
+
+std::string output_json(const OutputCheck& c) {
+    char buf[64];
+    std::snprintf(buf, sizeof buf, "\"%016llx\"", (unsigned long long)c.fnv);
+    return "{\"elements\": " + std::to_string(c.n) + ", \"mean\": " + json_num(c.mean) + ", \"std\": " +
+           json_num(c.std) + ", \"nonfinite\": " + std::to_string(c.nonfinite) + ", \"fnv64\": " + buf + "}";
+}
+
 class Session {
 public:
     explicit Session(const Args& a) : args(a), plan_only(a.flag("plan-only", false)), rt(plan_only ? -1 : 0), scope(rt) {
@@ -256,29 +335,82 @@ public:
         rt.set_output(*t);
         outs.push_back({t, args.str(key)});
     }
+    // An output summarised in the printed line (element count, moments,
+    // FNV-1a of the bytes) instead of written to a file.
+    void keep(Tensor t) {
+        if (!t.is_contiguous()) t = t.contiguous();
+        rt.set_output(*t);
+        kept.push_back(t);
+    }
     // Every parameter of `m` from DIR/<dotted name>.dtb, converted to the
     // parameter's type.
     void load_weights(const Module& m, const std::string& dir) {
         std::vector<std::pair<std::string, Tensor>> ps;
         m.named_parameters(ps);
+        for (auto& p : ps) bind_weight(p.second, read_blob(dir + "/" + p.first + ".dtb"), p.first);
+    }
+    // --random-weights SEED for the VAE modules: every parameter drawn
+    // N(mean, std) in fp32 on the host (mt19937_64), with mean 1 for the
+    // GroupNorm weights and 0 otherwise, then bound as a file's values are.
+    void random_weights(const Module& m, uint64_t seed, float std) {
+        std::vector<std::pair<std::string, Tensor>> ps;
+        m.named_parameters(ps);
+        std::mt19937_64 gen(seed);
         for (auto& p : ps) {
-            Blob b = read_blob(dir + "/" + p.first + ".dtb");
-            if (b.shape != p.second.shape()) throw std::runtime_error("shape mismatch for " + p.first);
-            if (p.second.dtype() == DT_TYPE_Q8_0_SPLIT) {
-                load_q8_weight(p.second, b, p.first);
-                continue;
-            }
-            auto bytes = convert_blob(b, p.second.dtype());
-            if (args.flag("resident-weights", false)) {  // uploaded once, kept in HBM
-                void* d = dev.alloc(bytes.size());
-                dt_tensor tmp = **p.second;
-                tmp.data = d;
-                check(dt_tensor_set(&tmp, bytes.data(), 0, bytes.size(), nullptr), "dt_tensor_set");
-                rt.bind_device(*p.second, d);
-            } else {
-                rt.bind(*p.second, bytes.data(), bytes.size());
-            }
+            const bool norm_w = p.first.rfind("norm", 0) == 0 && p.first.size() > 7 &&
+                                p.first.compare(p.first.size() - 7, 7, ".weight") == 0;
+            std::normal_distribution<float> nd(norm_w ? 1.0f : 0.0f, std);
+            Blob b;
+            b.shape = p.second.shape();
+            b.bytes.resize((size_t)p.second.numel() * 4);
+            float* f = reinterpret_cast<float*>(b.bytes.data());
+            for (int64_t i = 0; i < p.second.numel(); ++i) f[i] = nd(gen);
+            bind_weight(p.second, b, p.first);
         }
+    }
+    void bind_weight(const Tensor& t, const Blob& b, const std::string& name) {
+        if (b.shape != t.shape()) throw std::runtime_error("shape mismatch for " + name);
+        if (t.dtype() == DT_TYPE_Q8_0_SPLIT) {
+            load_q8_weight(t, b, name);
+            return;
+        }
+        if (t.dtype() == DT_TYPE_CONV2D_PACKED) {
+            if (b.type != DT_TYPE_F32) throw std::runtime_error("conv weight " + name + ": F32 expected");
+            if (!plan_only) pack_conv_weight(t, b);
+            return;
+        }
+        auto bytes = convert_blob(b, t.dtype());
+        if (args.flag("resident-weights", false)) {  // uploaded once, kept in HBM
+            void* d = dev.alloc(bytes.size());
+            dt_tensor tmp = **t;
+            tmp.data = d;
+            check(dt_tensor_set(&tmp, bytes.data(), 0, bytes.size(), nullptr), "dt_tensor_set");
+            rt.bind_device(*t, d);
+        } else {
+            rt.bind(*t, bytes.data(), bytes.size());
+        }
+    }
+    // --random-inputs SEED: an N(0, 1) input of `shape` drawn on the host
+    // (mt19937_64), stored as `type` and kept resident.
+    Tensor random_input(const Tensor::Shape& shape, int32_t type, uint64_t seed) {
+        Blob b;
+        b.shape = shape;
+        int64_t n = 1;
+        for (int64_t d : shape) n *= d;
+        b.bytes.resize((size_t)n * 4);
+        float* f = reinterpret_cast<float*>(b.bytes.data());
+        std::mt19937_64 gen(seed);
+        std::normal_distribution<float> nd(0.0f, 1.0f);
+        for (int64_t i = 0; i < n; ++i) f[i] = nd(gen);
+        Tensor t = Tensor::empty(shape, type);
+        rt.set_input(*t);
+        auto bytes = convert_blob(b, type);
+        if (!plan_only) {
+            void* d = dev.alloc(bytes.size());
+            rt.bind_device(*t, d);
+            check(dt_tensor_set(*t, bytes.data(), 0, bytes.size(), nullptr), "dt_tensor_set");
+        }
+        return t;
     }
     // A Q8_0_SPLIT Linear weight from fp32 values: quantised to Q8_0 and
     // repacked on the device into a buffer the weight keeps.
@@ -336,11 +468,18 @@ public:
             rt.read(*o.first, host.data(), host.size());
             write_blob(o.second, o.first.dtype(), o.first.shape(), host);
         }
+        std::string summary;
+        for (const Tensor& t : kept) {
+            std::vector<uint8_t> host(HipRuntime::nbytes(*t));
+            rt.read(*t, host.data(), host.size());
+            summary += (summary.empty() ? ", \"output\": " : ", \"output_" + std::to_string(&t - kept.data()) + "\": ") +
+                       output_json(check_output(host, t.dtype()));
+        }
         const ComputeStats& s = rt.stats();
         std::printf("{\"command\": \"%s\", \"nodes\": %d, \"kernels\": %d, \"fused_nodes\": %d, "
-                    "\"arena_bytes\": %zu, \"naive_bytes\": %zu, \"steps\": %d, \"ms_per_compute_median\": %.4f}\n",
+                    "\"arena_bytes\": %zu, \"naive_bytes\": %zu, \"steps\": %d, \"ms_per_compute_median\": %.4f%s}\n",
                     args.command.c_str(), s.nodes, s.kernels, s.fused_nodes, s.arena_bytes, s.naive_bytes, steps,
-                    ms[ms.size() / 2]);
+                    ms[ms.size() / 2], summary.c_str());
     }
 
     const Args& args;
@@ -349,6 +488,7 @@ public:
     RuntimeScope scope;
     DeviceBuffers dev;  // after rt: freed before the backend
     std::vector<std::pair<Tensor, std::string>> outs;
+    std::vector<Tensor> kept;
 };
 
 // ---- Flux2Transformer2DModel: one denoising step --------------------------
@@ -428,30 +568,6 @@ void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffer
     }
 }
 
-std::string json_str(const std::string& s) {
-    std::string r = "\"";
-    for (unsigned char ch : s) {
-        if (ch == '"' || ch == '\\') {
-            r += '\\';
-            r += (char)ch;
-        } else if (ch < 0x20) {
-            char buf[8];
-            std::snprintf(buf, sizeof buf, "\\u%04x", ch);
-            r += buf;
-        } else {
-            r += (char)ch;
-        }
-    }
-    return r + "\"";
-}
-
-std::string json_num(double v) {
-    if (!std::isfinite(v)) return "null";
-    char buf[40];
-    std::snprintf(buf, sizeof buf, "%.17g", v);
-    return buf;
-}
-
 // Count of each recorded op (unary ops by kind), as a JSON object: the op
 // set a ggml-side translation of the same graph has to map.
 std::string op_histogram(const HipRuntime& rt) {
@@ -472,59 +588,6 @@ std::string op_histogram(const HipRuntime& rt) {
     std::string out = "{";
     for (const auto& kv : h) out += (out.size() > 1 ? ", " : "") + json_str(kv.first) + ": " + std::to_string(kv.second);
     return out + "}";
-}
-
-float bf16_bits_to_f32(uint16_t h) {
-    const uint32_t u = (uint32_t)h << 16;
-    float f;
-    std::memcpy(&f, &u, 4);
-    return f;
-}
-
-// Summary of an output tensor's bytes: element count, mean and standard
-// deviation (fp64), count of NaN/Inf, and the FNV-1a hash of the bytes (equal
-// hashes = bit-identical outputs across runs).
-struct OutputCheck {
-    int64_t n = 0, nonfinite = 0;
-    double mean = 0, std = 0;
-    uint64_t fnv = 1469598103934665603ull;
-};
-
-OutputCheck check_output(const std::vector<uint8_t>& bytes, int32_t type) {
-    OutputCheck c;
-    for (uint8_t b : bytes) c.fnv = (c.fnv ^ b) * 1099511628211ull;
-    double s = 0, s2 = 0;
-    const size_t es = type == DT_TYPE_F32 ? 4 : 2;
-    for (size_t i = 0; i + es <= bytes.size(); i += es) {
-        float f;
-        if (type == DT_TYPE_F32) {
-            std::memcpy(&f, bytes.data() + i, 4);
-        } else {
-            uint16_t h;
-            std::memcpy(&h, bytes.data() + i, 2);
-            f = bf16_bits_to_f32(h);
-        }
-        ++c.n;
-        if (!std::isfinite(f)) {
-            ++c.nonfinite;
-            continue;
-        }
-        s += f;
-        s2 += (double)f * f;
-    }
-    const int64_t m = c.n - c.nonfinite;
-    if (m > 0) {
-        c.mean = s / m;
-        c.std = std::sqrt(std::max(0.0, s2 / m - c.mean * c.mean));
-    }
-    return c;
-}
-
-std::string output_json(const OutputCheck& c) {
-    char buf[64];
-    std::snprintf(buf, sizeof buf, "\"%016llx\"", (unsigned long long)c.fnv);
-    return "{\"elements\": " + std::to_string(c.n) + ", \"mean\": " + json_num(c.mean) + ", \"std\": " +
-           json_num(c.std) + ", \"nonfinite\": " + std::to_string(c.nonfinite) + ", \"fnv64\": " + buf + "}";
 }
 
 void run_model(Session& s, const Args& a) {
@@ -797,6 +860,36 @@ void run(const Args& a) {
             s.param(m.conv()->bias, "conv.bias");
         }
         s.output(m.forward(x), "out");
+    } else if (c == "ResnetBlock2D") {
+        // ResnetBlock2D.py (the reference CLI's main.cpp:126-170 arguments): --in_channels,
+        // --out_channels, --temb_channels, --groups, --groups_out, --eps, --kernel_size,
+        // --output_scale_factor, --use_in_shortcut, --conv_shortcut_bias, --conv_2d_out_channels;
+        // inputs --hidden_states [--temb]; parameters from --weights DIR (one .dtb per dotted
+        // name); --dtype f32|bf16 for the activations; --packed-weights true packs the conv
+        // weights once at load
+        const int32_t act = a.str("dtype", "f32") == "bf16" ? DT_TYPE_BF16 : DT_TYPE_F32;
+        LinearWeightType wt(act);
+        ConvWeightType cw(a.flag("packed-weights", false) ? DT_TYPE_CONV2D_PACKED : DT_TYPE_F32);
+        auto opt = [&](const char* k) { return a.has(k) ? std::optional<int64_t>(a.i64(k)) : std::nullopt; };
+        const std::optional<bool> use_in_shortcut =
+            a.has("use_in_shortcut") ? std::optional<bool>(a.flag("use_in_shortcut", false)) : std::nullopt;
+        ResnetBlock2D<SiLU> m(a.i64("in_channels"), opt("out_channels"), std::nullopt, 0.0f, opt("temb_channels"),
+                              a.i64("groups", 32), opt("groups_out"), true, a.f32("eps", 1e-6f), false,
+                              a.i64("kernel_size", 3), a.f32("output_scale_factor", 1.0f), use_in_shortcut, false,
+                              false, a.flag("conv_shortcut_bias", true), opt("conv_2d_out_channels"));
+        // --random-inputs SEED --batch N --height H --width W [--random-weights SEED]: generated
+        // instead of read (no temb); --out is then optional
+        Tensor x = a.has("random-inputs")
+                       ? s.random_input({a.i64("batch", 1), a.i64("in_channels"), a.i64("height"), a.i64("width")},
+                                        act, (uint64_t)a.i64("random-inputs"))
+                       : s.input_as("hidden_states", act);
+        std::optional<Tensor> temb;
+        if (a.has("temb")) temb = s.input_as("temb", act);
+        if (a.has("random-weights")) s.random_weights(m, (uint64_t)a.i64("random-weights"), 0.02f);
+        else s.load_weights(m, a.str("weights"));
+        Tensor y = m.forward(x, temb ? &*temb : nullptr);
+        if (a.has("out")) s.output(y, "out");
+        else s.keep(y);
     } else if (c == "SiLU") {
         s.output(SiLU().forward(s.input("x")), "out");
     } else if (c == "Flux2PosEmbed") {

@@ -50,7 +50,13 @@ struct ConvArgs {
     int TR, TC, tiles_w; // pixel tile geometry; tiles along the width
     float4* stats;       // GroupNorm tile records [N][G][pixel tiles] (dt_conv2d_gn), or null
     int G, cg;           // groups over Co and channels per group (cg divides 128)
+    // Residual epilogue (conv2d_residual): 1: y = res + conv; 2: y = (res +
+    // conv) * res_scale.  res is an NCHW tensor of the output's shape and type.
+    const void* res;
+    int res_mode;
+    float res_scale;
 };
+
 
 template <typename TI>
 __device__ __forceinline__ float load_in(const TI* p);
@@ -68,6 +74,42 @@ template <>
 __device__ __forceinline__ float stored_value<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ float stored_value<bf16>(float v) { return bf16_lo(pack_bf16x2(v, 0.f)); }
+
+// The residual epilogue of ResnetBlock2D's `(input + hidden) /
+// output_scale_factor` for output pixel (oh, ow): its accumulator rows
+// acc[j][i][r] (j = 0, 1) are output channels co_base + 32 j + 8 (r / 4) +
+// (r % 4) of sample n.  Each value is conv + bias, then + the residual, then
+// (res_mode 2) * res_scale, rounded to T where the graph stores the node
+// (the conv output, the ADD; the SCALE by the store itself), so the fused
+// epilogue equals the nodes.  Each j's 16 residual values are loaded before
+// its first store: the output may sit on its own residual, but each element
+// is read and then written by this lane alone, so the loads need not wait
+// on earlier stores (two memory round trips per pixel instead of one per
+// element).
+template <typename T, int FN>
+__device__ __forceinline__ void conv_store_residual(const ConvArgs& a, T* y, const f32x16_t (&acc)[2][FN], int i,
+                                                    int co_base, int oh, int ow, int n) {
+    const T* res = reinterpret_cast<const T*>(a.res) + (int64_t)n * a.Co * a.Hs * a.Ws;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        float rv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co_base + 32 * j + 8 * (r >> 2) + (r & 3);
+            rv[r] = co < a.Co ? Io<T>::get(res + ((int64_t)co * a.Hs + oh) * a.Ws + ow) : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int co = co_base + 32 * j + 8 * (r >> 2) + (r & 3);
+            if (co >= a.Co) continue;
+            float v = acc[j][i][r];
+            if (a.bias) v = add_rn(v, a.bias[co]);
+            v = add_rn(rv[r], stored_value<T>(v));
+            if (a.res_mode == 2) v = mul_rn(stored_value<T>(v), a.res_scale);
+            Io<T>::put(y + ((int64_t)co * a.Hs + oh) * a.Ws + ow, v);
+        }
+    }
+}
 
 // GroupNorm statistics of one output tile, as the stored (rounded) values:
 // per group of cg channels, the tile's mean and M2 = sum (v - mean)^2 over
@@ -242,7 +284,7 @@ __device__ __forceinline__ void conv_group_stats_reg(const ConvArgs& a, const f3
     }
 }
 
-template <typename T, int K, bool STATS>
+template <typename T, int K, bool STATS, bool RES>
 __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
     constexpr int KK = K * K, PAD = (K - 1) / 2;
     constexpr int W_BYTES = kTileCo * KK * kRec;
@@ -344,6 +386,10 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
         const int p = wpx + 32 * i + lrow;
         const int oh = oh0 + p / a.TC, ow = ow0 + p % a.TC;
         if (oh >= a.Hs || ow >= a.Ws) continue;
+        if constexpr (RES) {
+            conv_store_residual<T, 2>(a, y, acc, i, co0 + wco + 4 * g, oh, ow, n);
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -452,7 +498,102 @@ __device__ __forceinline__ void conv_wait_vm() {
     __builtin_amdgcn_s_waitcnt((N_OUT & 15) | ((N_OUT >> 4) << 14) | 0x0F70);
 }
 
-template <typename T, int K, bool STATS>
+// The epilogue of the DMA kernel's 128-channel x 256-pixel tile, through
+// LDS, in two passes over the accumulator halves j (64 output channels
+// each).  Each lane parks its conv + bias values, rounded to T as the graph
+// stores the conv node, in LDS as [64 channels][256 pixels]; the block then
+// writes the pass in 16-byte pieces along the image rows (the lanes' own
+// values would be 2-byte stores).  RES adds the residual epilogue of
+// ResnetBlock2D's `(input + hidden) / output_scale_factor`: per piece the
+// residual (loaded before the LDS stage, so its latency overlaps it), the
+// ADD rounded to T, the SCALE (res_mode 2), one store.  A piece is read and
+// written by one thread only, so the output may sit on the residual.
+template <typename T, bool RES>
+__device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t (&acc)[2][4], uint8_t* smem,
+                                               int co0, int oh0, int ow0, int wco, int wpx, int lrow, int g, int lt,
+                                               int n) {
+    constexpr int E = Io<T>::EPV;             // elements per 16-byte piece
+    constexpr int S = 264;                    // LDS row stride in elements (bank-spread rows)
+    constexpr int RP = 256 / E;               // pieces per 256-pixel row
+    constexpr int PIECES = 64 * RP / 256;     // pieces per thread and pass
+    T* lds = reinterpret_cast<T*>(smem);
+    const int tid = threadIdx.x, tcm = (1 << lt) - 1;
+    const int64_t plane = (int64_t)a.Hs * a.Ws;
+    const T* res = RES ? reinterpret_cast<const T*>(a.res) + (int64_t)n * a.Co * plane : nullptr;
+    T* y = reinterpret_cast<T*>(a.y) + (int64_t)n * a.Co * plane;
+    const bool vec = a.Ws % E == 0 && (!RES || (reinterpret_cast<uintptr_t>(a.res) & 15) == 0) &&
+                     (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint4 rv[PIECES];
+#pragma unroll
+        for (int k = 0; k < PIECES && RES; ++k) {
+            const int c = tid + 256 * k, pr = c / RP, px = (c % RP) * E;
+            const int co = co0 + (pr >> 5) * 64 + 32 * j + (pr & 31);
+            const int oh = oh0 + (px >> lt), ow = ow0 + (px & tcm);
+            rv[k] = make_uint4(0, 0, 0, 0);
+            if (co >= a.Co || oh >= a.Hs || ow >= a.Ws) continue;
+            const T* src = res + co * plane + (int64_t)oh * a.Ws + ow;
+            if (vec) {
+                rv[k] = ld_stream(src);
+            } else {
+                float t[E];
+#pragma unroll
+                for (int q = 0; q < E; ++q) t[q] = ow + q < a.Ws ? Io<T>::get(src + q) : 0.f;
+                rv[k] = Io<T>::pack(t);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int q = 8 * (r >> 2) + 4 * g + (r & 3), co = co0 + wco + 32 * j + q;
+                float v = acc[j][i][r];
+                if (a.bias && co < a.Co) v = add_rn(v, a.bias[co]);
+                Io<T>::put(lds + ((wco >> 6) * 32 + q) * S + wpx + 32 * i + lrow, v);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PIECES; ++k) {
+            const int c = tid + 256 * k, pr = c / RP, px = (c % RP) * E;
+            const int co = co0 + (pr >> 5) * 64 + 32 * j + (pr & 31);
+            const int oh = oh0 + (px >> lt), ow = ow0 + (px & tcm);
+            if (co >= a.Co || oh >= a.Hs || ow >= a.Ws) continue;
+            T* dst = y + co * plane + (int64_t)oh * a.Ws + ow;
+            const uint4 hv = *reinterpret_cast<const uint4*>(lds + pr * S + px);
+            if constexpr (!RES) {
+                if (vec) {
+                    st_stream(dst, hv);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < E; ++q)
+                        if (ow + q < a.Ws) dst[q] = lds[pr * S + px + q];
+                }
+                continue;
+            }
+            float h[E], r[E];
+            Io<T>::unpack(hv, h);
+            Io<T>::unpack(rv[k], r);
+#pragma unroll
+            for (int q = 0; q < E; ++q) h[q] = add_rn(r[q], h[q]);
+            if (a.res_mode == 2) {
+                Io<T>::round(h);
+#pragma unroll
+                for (int q = 0; q < E; ++q) h[q] = mul_rn(h[q], a.res_scale);
+            }
+            if (vec) {
+                st_stream(dst, Io<T>::pack(h));
+            } else {
+#pragma unroll
+                for (int q = 0; q < E; ++q)
+                    if (ow + q < a.Ws) Io<T>::put(dst + q, h[q]);
+            }
+        }
+        __syncthreads();  // the next pass reuses the LDS rows
+    }
+}
+
+template <typename T, int K, bool STATS, bool RES>
 __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const Conv2Extra e) {
     static_assert(K == 3, "the DMA kernel is sized for 3x3 patches");
     constexpr int KK = K * K, PAD = (K - 1) / 2;
@@ -562,6 +703,10 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
         if (ch + 2 < nch) issue((ch + 2) * kCi2, ch & 1);
     }
 
+    if constexpr (!STATS) {
+        conv_store_lds<T, RES>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g, e.lt, n);
+        return;
+    }
     T* y = reinterpret_cast<T*>(a.y) + (int64_t)n * a.Co * a.Hs * a.Ws;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -666,7 +811,7 @@ void conv_geometry2(int64_t Hs, int64_t Ws, int* TR, int* TC, int64_t* tiles_w, 
 int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
                 int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type, float4* stats,
                 int64_t groups, const void* ws, size_t ws_bytes, hipStream_t st, const char* what,
-                int64_t* n_tiles) {
+                int64_t* n_tiles, const void* res = nullptr, int res_mode = 0, float res_scale = 1.0f) {
     DT_REQUIRE(is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
     DT_REQUIRE(N > 0 && Ci > 0 && H > 0 && W > 0 && Co > 0, "%s: bad shape", what);
     DT_REQUIRE(K == 1 || K == 3, "%s: kernel size %lld unsupported (1 or 3)", what, (long long)K);
@@ -689,6 +834,10 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
     a.stats = stats;
     a.G = (int)groups;
     a.cg = groups > 0 ? (int)(Co / groups) : 0;
+    DT_REQUIRE(!res_mode || (res && !stats), "%s: the residual epilogue needs a residual and no statistics", what);
+    a.res = res;
+    a.res_mode = res_mode;
+    a.res_scale = res_scale;
     // 1x1 convs keep the staged path: the channel-last copy costs more than
     // their single tap (gfx950, [1, 256, 512, 512] -> 128: 260-312 us with
     // the copy against 135-225 us staged).
@@ -724,24 +873,32 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
 #undef DT_NHWC
         int rc = check_launch(what);
         if (rc) return rc;
-#define DT_CONV2_LAUNCH(TT, KS, ST) hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST>), grid, dim3(256), 0, st, a, e)
+#define DT_CONV2_LAUNCH(TT, KS, ST, RS) \
+    hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST, RS>), grid, dim3(256), 0, st, a, e)
         if (io_type == DT_TYPE_F32) {
-            if (stats) DT_CONV2_LAUNCH(float, 3, true);
-            else DT_CONV2_LAUNCH(float, 3, false);
+            if (stats) DT_CONV2_LAUNCH(float, 3, true, false);
+            else if (res_mode) DT_CONV2_LAUNCH(float, 3, false, true);
+            else DT_CONV2_LAUNCH(float, 3, false, false);
         } else {
-            if (stats) DT_CONV2_LAUNCH(bf16, 3, true);
-            else DT_CONV2_LAUNCH(bf16, 3, false);
+            if (stats) DT_CONV2_LAUNCH(bf16, 3, true, false);
+            else if (res_mode) DT_CONV2_LAUNCH(bf16, 3, false, true);
+            else DT_CONV2_LAUNCH(bf16, 3, false, false);
         }
 #undef DT_CONV2_LAUNCH
         return check_launch(what);
     }
-#define DT_CONV_LAUNCH(TT, KS, ST) hipLaunchKernelGGL((conv2d_kernel<TT, KS, ST>), grid, dim3(256), 0, st, a)
+#define DT_CONV_LAUNCH(TT, KS)                                                                         \
+    do {                                                                                               \
+        if (stats) hipLaunchKernelGGL((conv2d_kernel<TT, KS, true, false>), grid, dim3(256), 0, st, a);   \
+        else if (res_mode) hipLaunchKernelGGL((conv2d_kernel<TT, KS, false, true>), grid, dim3(256), 0, st, a); \
+        else hipLaunchKernelGGL((conv2d_kernel<TT, KS, false, false>), grid, dim3(256), 0, st, a);        \
+    } while (0)
     if (io_type == DT_TYPE_F32) {
-        if (K == 3) { if (stats) DT_CONV_LAUNCH(float, 3, true); else DT_CONV_LAUNCH(float, 3, false); }
-        else { if (stats) DT_CONV_LAUNCH(float, 1, true); else DT_CONV_LAUNCH(float, 1, false); }
+        if (K == 3) DT_CONV_LAUNCH(float, 3);
+        else DT_CONV_LAUNCH(float, 1);
     } else {
-        if (K == 3) { if (stats) DT_CONV_LAUNCH(bf16, 3, true); else DT_CONV_LAUNCH(bf16, 3, false); }
-        else { if (stats) DT_CONV_LAUNCH(bf16, 1, true); else DT_CONV_LAUNCH(bf16, 1, false); }
+        if (K == 3) DT_CONV_LAUNCH(bf16, 3);
+        else DT_CONV_LAUNCH(bf16, 1);
     }
 #undef DT_CONV_LAUNCH
     return check_launch(what);
@@ -762,6 +919,18 @@ extern "C" int dt_conv2d(const void* x, int64_t N, int64_t Ci, int64_t H, int64_
     return dit::conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, nullptr, 0, workspace,
                             workspace_bytes, (hipStream_t)stream, "dt_conv2d", &tiles);
 }
+
+namespace dit {
+
+int conv2d_residual(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
+                    int64_t K, int32_t upscale2, const float* bias, const void* res, int scaled, float scale, void* y,
+                    void* workspace, size_t workspace_bytes, int32_t io_type, hipStream_t st) {
+    int64_t tiles;
+    return conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, nullptr, 0, workspace,
+                       workspace_bytes, st, "conv2d_residual", &tiles, res, scaled ? 2 : 1, scale);
+}
+
+}  // namespace dit
 
 extern "C" size_t dt_conv2d_gn_stats_bytes(int64_t N, int64_t Co, int64_t OH, int64_t OW, int64_t groups) {
     if (N <= 0 || Co <= 0 || OH <= 0 || OW <= 0 || groups <= 0 || Co % groups) return 0;

@@ -134,6 +134,10 @@ struct Plan {
     float addend = 0.f;  // adaLN: added to every scale (the 1 of 1 + scale)
     int silu = 0;
     int up2 = 0;  // CONV: the input is upsampled 2x (nearest) on the fly
+    // CONV with a residual (in[4]): the output is res + conv, times
+    // res_scale when res_scaled
+    int res_scaled = 0;
+    float res_scale = 1.f;
     // QK
     std::vector<QkSeg> segs;
     std::vector<const dt_tensor*> pos;  // per axis
@@ -516,6 +520,46 @@ bool match_conv(Graph& g, const dt_tensor* t, Plan& p) {
     p.in[3] = c;
     p.up2 = up != nullptr;
     return true;
+}
+
+// The tail of ResnetBlock2D::forward (ResnetBlock2D.inl:194): `(input +
+// hidden) / output_scale_factor` records ADD(res, h) then SCALE(1 / f)
+// (Tensor / float is ggml_scale); h is conv2's output, in one of
+// match_conv's forms and used only by the ADD.  The conv's epilogue adds
+// the residual and scales, with the ADD's value rounded to the node type
+// as the graph stores it, so neither full-tensor pass runs.  Without the
+// SCALE (a factor of 1 still records it; a graph may also end at the ADD)
+// the ADD alone is folded.
+bool match_conv_residual(Graph& g, const dt_tensor* t, Plan& p) {
+    const dt_tensor* add = t;
+    if (t->op == DT_OP_SCALE) {
+        add = t->src[0];
+        if (!add || add->op != DT_OP_ADD || !g.internal(add) || !same_shape(add, t) || add->type != t->type ||
+            fparam(t, 1) != 0.f)
+            return false;
+    }
+    if (add->op != DT_OP_ADD || !dense(t)) return false;
+    for (int k = 0; k < 2; ++k) {
+        const dt_tensor* h = add->src[k];
+        const dt_tensor* res = add->src[1 - k];
+        if (!h || !res || h == res || !g.internal(h) || !same_shape(h, add) || h->type != add->type ||
+            !same_shape(res, add) || res->type != add->type || !dense(res))
+            continue;
+        const bool conv = h->op == DT_OP_CONV_2D_DIRECT ||
+                          (h->op == DT_OP_ADD && ((h->src[0] && h->src[0]->op == DT_OP_CONV_2D_DIRECT) ||
+                                                  (h->src[1] && h->src[1]->op == DT_OP_CONV_2D_DIRECT)));
+        if (!conv) continue;
+        Plan cp;
+        if (!match_conv(g, h, cp)) continue;
+        g.claim(h);
+        if (add != t) g.claim(add);
+        p = cp;
+        p.in[4] = res;
+        p.res_scaled = add != t;
+        p.res_scale = add != t ? fparam(t, 0) : 1.0f;
+        return true;
+    }
+    return false;
 }
 
 // MUL(x, SIGMOID(x)): the SiLU module's composite (SiLU.hpp:12) as one kernel.
@@ -931,7 +975,8 @@ int run_flash_attn(hipStream_t st, const dt_tensor* t) {
 // packed once at load (DT_TYPE_CONV2D_PACKED), the channel-last copy of x
 // after them, then dt_conv2d into root.
 int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt_tensor* w, const dt_tensor* bias,
-             const dt_tensor* conv, int up2) {
+             const dt_tensor* conv, int up2, const dt_tensor* res = nullptr, int res_scaled = 0,
+             float res_scale = 1.f) {
     hipStream_t st = backend_stream(be);
     const int64_t K = w->ne[0], Ci = w->ne[2], Co = w->ne[3];
     const int64_t W = x->ne[0], H = x->ne[1], N = x->ne[3], f = up2 ? 2 : 1;
@@ -963,8 +1008,21 @@ int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt
         if (rc) return rc;
     }
     g_kernels += (prepacked ? 0 : 1) + (K == 3 ? 1 : 0) + 1;  // pack, channel-last copy (3x3), conv
-    return dt_conv2d(data_of(x), N, Ci, H, W, wp, Co, K, up2, bias ? (const float*)data_of(bias) : nullptr,
-                     root->data, ws ? (char*)scratch + packed : nullptr, ws, root->type, st);
+    const float* b = bias ? (const float*)data_of(bias) : nullptr;
+    void* wsp = ws ? (char*)scratch + packed : nullptr;
+    if (!res) return dt_conv2d(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, root->data, wsp, ws, root->type, st);
+    // Each output element's residual is read by the lane that then writes
+    // it, so the residual may be the output's own memory, but no other part
+    // of it.
+    const size_t bytes = (size_t)(N * Co * H * f * W * f) * (size_t)elem_size(root->type);
+    const char* r = (const char*)data_of(res);
+    const char* y = (const char*)root->data;
+    DT_REQUIRE(same_shape(res, root) && res->type == root->type && dense(res),
+               "dt_graph_compute: the conv residual must match the output");
+    DT_REQUIRE(r == y || r + bytes <= y || y + bytes <= r,
+               "dt_graph_compute: the conv residual partly overlaps the output");
+    return conv2d_residual(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, data_of(res), res_scaled, res_scale,
+                           root->data, wsp, ws, root->type, st);
 }
 
 int run_upscale(hipStream_t st, const dt_tensor* t) {
@@ -1128,7 +1186,8 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
                                          p.eps, root->type, st);
         }
         case K_CONV:
-            return run_conv(be, root, p.in[0], p.in[1], p.in[2], p.in[3], p.up2);
+            return run_conv(be, root, p.in[0], p.in[1], p.in[2], p.in[3], p.up2, p.in[4], p.res_scaled,
+                            p.res_scale);
         case K_ATTN_QK:
             ++g_kernels;
             return run_attn_qk(be, root, p);
@@ -1377,14 +1436,21 @@ void check_plan_memory(const Graph& g, dt_tensor** nodes, int n, const std::vect
             Span sp;
             if (span_of(t, &sp)) writes.push_back({sp, j});
         }
-        // A fused kernel may write over an input only element for element.
+        // A fused kernel may write over an input only element for element;
+        // a conv only over its residual, and only while its input is
+        // elsewhere.
+        const Plan& pl = plans[p];
+        Span rs{}, xs{};
+        const bool conv_res = pl.kind == K_CONV && pl.in[4] && span_of(pl.in[4], &rs) && span_of(pl.in[0], &xs);
         if (fused)
             for (const auto& w : writes)
                 for (const auto& r : reads) {
                     const bool overlap = w.first.lo < r.first.hi && r.first.lo < w.first.hi;
                     const bool same = w.first.lo == r.first.lo && w.first.hi == r.first.hi;
-                    if (overlap && (!same || plans[p].kind == K_ATTN_QK || plans[p].kind == K_GEMM_GROUP ||
-                                    plans[p].kind == K_CONV))
+                    const bool res_in_place = conv_res && same && r.first.lo == rs.lo && r.first.hi == rs.hi &&
+                                              !(w.first.lo < xs.hi && xs.lo < w.first.hi);
+                    if (overlap && (!same || pl.kind == K_ATTN_QK || pl.kind == K_GEMM_GROUP ||
+                                    (pl.kind == K_CONV && !res_in_place)))
                         blame(p);
                 }
         for (const auto& w : writes) owners.write(w.first, write_identity(w.second), w.second);
@@ -1449,7 +1515,7 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
         if (match_attn_qk(g, t, p) || match_qk(g, t, p) || match_groupnorm(g, t, p) || match_res_adaln(g, t, p) ||
             match_adaln(g, t, p) ||
             match_swiglu(g, t, p) || match_gated(g, t, p) || match_silu(g, t, p) ||
-            match_gemm_add(g, t, p) || match_conv(g, t, p))
+            match_gemm_add(g, t, p) || match_conv_residual(g, t, p) || match_conv(g, t, p))
             continue;
         p = Plan();
     }

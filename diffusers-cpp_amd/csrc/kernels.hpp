@@ -93,6 +93,17 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out);
 constexpr int kBackendRopePositions = 4096;
 int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out);
 
+// dt_conv2d (+ bias) followed by ResnetBlock2D's residual (conv2d.hip):
+// y = res + conv, or (res + conv) * scale when `scaled`, with the conv
+// output, the sum and the product each rounded to io_type as the unfused
+// nodes store them.  res has the output's shape and type; it may be y itself
+// (each element is read by the thread that then writes it) but must not
+// overlap y otherwise, and y must not overlap the conv's input x (read
+// around each output pixel).
+int conv2d_residual(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
+                    int64_t K, int32_t upscale2, const float* bias, const void* res, int scaled, float scale, void* y,
+                    void* workspace, size_t workspace_bytes, int32_t io_type, hipStream_t st);
+
 // The bf16 values of a DT_TYPE_Q8_0_SPLIT weight [N][K] (codes, then scales
 // [K/32][ld_scales]) into out [N][K] (dequant.hip).
 int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, int64_t N, int64_t K, void* out,

@@ -42,9 +42,12 @@ public:
     Tensor operator-(const Tensor& rhs) const;
     Tensor operator*(const Tensor& rhs) const;
     Tensor operator/(const Tensor& rhs) const;
+    // Scalars as the reference's Tensor.hpp:351-369 takes them: + and - go
+    // through a filled scalar tensor, * and / through ggml_scale.
     Tensor operator+(float rhs) const { return *this + scalar(rhs); }
     Tensor operator-(float rhs) const { return *this - scalar(rhs); }
-    Tensor operator*(float rhs) const { return *this * scalar(rhs); }
+    Tensor operator*(float rhs) const { return scale(rhs); }
+    Tensor operator/(float rhs) const { return scale(1.0f / rhs); }
     Tensor operator-() const { return *this * -1.0f; }
     Tensor scale(float value) const;
     Tensor sigmoid() const;

@@ -219,3 +219,60 @@ def test_graph_conv_rejects_stride_2(dev, be):
     y = g.conv_2d_direct(Wt, X, s0=2, s1=2)
     with pytest.raises(dh.DtError, match="stride 2,2"):
         g.compute(be, outputs=[y])
+
+
+# ------------------------------------------------- residual epilogue (graph) --
+# ResnetBlock2D's `(input + hidden) / output_scale_factor` (ResnetBlock2D.inl:194)
+# records ADD(res, conv2 + bias) then SCALE; the executor runs both in conv2's
+# epilogue with the ADD's value rounded where the graph stores it.
+
+def _residual_graph(x, w, b, res, scale, io, alias):
+    from graphkit import Graph
+    g = Graph()
+    Co, K = w.shape[0], w.shape[-1]
+    X = g.leaf(dev_tensor(x, io))
+    Wt = g.leaf(dev_tensor(w, torch.float32))
+    B = g.leaf(dev_tensor(b, torch.float32))
+    R = g.leaf(dev_tensor(res, io))
+    c = g.conv_2d_direct(Wt, X, p0=K // 2, p1=K // 2)
+    h = g.add(c, g.reshape(B, [1, 1, Co, 1]))
+    y = g.scale(g.add(R, h), scale)
+    if alias:      # the output in place over the residual, as an allocator may place it
+        y.d.data = R.d.data
+    return g, h, y, (R.data if alias else y.data)
+
+
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,co,k,scale,alias", [((1, 24, 9, 13), 40, 3, 0.5, False),
+                                                    ((1, 64, 16, 20), 64, 3, 1.0, True),
+                                                    ((2, 32, 7, 70), 48, 1, 1.0 / 3.0, False),
+                                                    ((1, 128, 32, 32), 128, 3, 0.7, True)])
+def test_conv_residual_epilogue_equals_the_nodes(orc, dev, io, shape, co, k, scale, alias):
+    """The fused conv + bias + ADD + SCALE launch stores the bits the nodes
+    store when run one by one (conv + bias, ADD, SCALE: conv2's output kept
+    as a graph output), in place over the residual or not, and matches
+    the oracle's (res + conv(x) + b) * scale."""
+    from graphkit import Backend
+    print(f"conv residual x={shape} co={co} k={k} scale={scale} alias={alias} {io}", flush=True)
+    x = orc.randn(SEED + 60, shape)
+    w = orc.randn(SEED + 61, (co, shape[1], k, k), std=0.1)
+    b = orc.randn(SEED + 62, (co,), std=0.1)
+    res = orc.randn(SEED + 63, (shape[0], co, shape[2], shape[3]))
+    be = Backend()
+    try:
+        g, h, y, out = _residual_graph(x, w, b, res, scale, io, alias)
+        kernels, fused = g.compute(be.h, outputs=[y])
+        torch.cuda.synchronize()
+        fused_out = out.clone()
+        g2, h2, y2, out2 = _residual_graph(x, w, b, res, scale, io, alias)
+        kernels2, fused2 = g2.compute(be.h, outputs=[y2, h2])
+        torch.cuda.synchronize()
+    finally:
+        be.close()
+    assert (kernels, fused) == ((3 if k == 3 else 2), 3), (kernels, fused)
+    assert (kernels2, fused2) == (kernels + 2, 1), (kernels2, fused2)
+    assert torch.equal(fused_out.view(torch.int16 if io == torch.bfloat16 else torch.int32),
+                       out2.view(torch.int16 if io == torch.bfloat16 else torch.int32))
+    conv = orc.conv2d(orc.round_bf16(as_input(x, io)), orc.round_bf16(w), b)
+    want = (as_input(res, io) + conv) * np.float32(scale)
+    check(host(fused_out), want, io, "conv + residual", one_rounding=False)

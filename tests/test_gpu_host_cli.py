@@ -344,6 +344,60 @@ def test_upsample2d(orc, cli, use_conv, shape):
     assert sp["fused_nodes"] == 2 and sp["kernels"] == 2, sp
 
 
+# ---- ResnetBlock2D (test/src/diffusers/models/resnet/ResnetBlock2D.py): the
+# reference's three toy cases (groups 8 on a 1x8x2x2 input: 8 -> 8, the 8 -> 16
+# channel projection, temb 16) and two decoder-sized blocks.  Interior
+# activations are rounded to bf16 where they feed a convolution's MFMA (and,
+# in bf16 mode, at every node), so both modes are held to the bf16 bar; f32
+# mode is also compared, tighter, with the oracle rounding conv operands.
+
+RESNET_CASES = [
+    dict(cin=8, cout=8, temb=None, groups=8, N=1, H=2, W=2, osf=1.0),
+    dict(cin=8, cout=16, temb=None, groups=8, N=1, H=2, W=2, osf=1.0),
+    dict(cin=8, cout=8, temb=16, groups=8, N=1, H=2, W=2, osf=1.0),
+    dict(cin=128, cout=128, temb=None, groups=32, N=1, H=24, W=40, osf=1.0),
+    dict(cin=256, cout=128, temb=None, groups=32, N=1, H=16, W=20, osf=2.0),
+]
+
+
+@pytest.mark.parametrize("c", RESNET_CASES, ids=lambda c: f"{c['cin']}-{c['cout']}-t{c['temb']}-{c['H']}x{c['W']}")
+def test_resnet_block2d(orc, cli, c):
+    import oracle.vae as vae
+    shapes = vae.resnet_block2d_param_shapes(c["cin"], c["cout"], c["temb"])
+    wdir = os.path.join(cli.tmp, "w")
+    os.makedirs(wdir, exist_ok=True)
+    P = {}
+    for i, (name, shape) in enumerate(sorted(shapes.items())):
+        mean = 1.0 if name in ("norm1.weight", "norm2.weight") else 0.0
+        std = 0.05 if name.endswith(".weight") and "norm" not in name else 0.1
+        P[name] = orc.randn(SEED + 50 + i, shape, mean=mean, std=std)
+        write_dtb(os.path.join(wdir, name + ".dtb"), P[name], 0)
+    xp, xv = cli.act(orc.randn(SEED + 48, (c["N"], c["cin"], c["H"], c["W"])))
+    args = ["--in_channels", c["cin"], "--out_channels", c["cout"], "--groups", c["groups"],
+            "--output_scale_factor", c["osf"], "--dtype", "bf16" if cli.bf16 else "f32",
+            "--hidden_states", xp, "--weights", wdir, "--out", cli.out()]
+    tv = None
+    if c["temb"]:
+        tp, tv = cli.act(orc.randn(SEED + 49, (c["N"], c["temb"])))
+        args += ["--temb_channels", c["temb"], "--temb", tp]
+    st = cli.run("ResnetBlock2D", *args)
+    got = read_dtb(cli.out())
+    want = vae.resnet_block2d(xv, P, c["groups"], None, 1e-6, c["osf"], tv)
+    assert_bf16(got, want, "ResnetBlock2D")
+    if not cli.bf16:
+        from conftest import bf16_metrics
+        rel, _ = bf16_metrics(got, vae.resnet_block2d(xv, P, c["groups"], None, 1e-6, c["osf"], tv, conv_bf16=True))
+        assert rel <= 2e-3, rel
+    shortcut = c["cin"] != c["cout"]
+    if not c["temb"]:
+        # GroupNorm+SiLU 2 each; conv1 and conv2: pack, channel-last copy, conv (conv2 with
+        # the bias, residual ADD and SCALE in its epilogue); the 1x1 shortcut: pack, conv
+        assert st["kernels"] == 10 + (2 if shortcut else 0), st
+    sp = cli.run("ResnetBlock2D", *args, "--packed-weights", "true")
+    assert np.array_equal(read_dtb(cli.out()).view(np.uint32), got.view(np.uint32))
+    assert sp["kernels"] == st["kernels"] - (3 if shortcut else 2), sp
+
+
 def test_cli_rejects_bad_input(dev):
     with tempfile.TemporaryDirectory() as d:
         r = subprocess.run([CLI, "NoSuchCommand"], capture_output=True, text=True, timeout=60)

@@ -3,7 +3,12 @@
 bias[1, Co, 1, 1]) (src/nn/modules/conv/Conv2d.cpp:38-102) becomes one
 convolution with the bias in its epilogue, and Upsample2D's nearest 2x
 UPSCALE (src/diffusers/models/resnet/Upsample2D.cpp:50-72) folds into the
-conv's input when the conv is its only consumer."""
+conv's input when the conv is its only consumer.  ResnetBlock2D's tail,
+`(input + hidden) / output_scale_factor` (src/diffusers/models/resnet/
+ResnetBlock2D.inl:194: ADD(res, conv2) then SCALE), folds into conv2's
+epilogue when conv2's output and the ADD are used nowhere else; the memory
+replay lets the output sit exactly on the residual but not on the conv's
+input."""
 import os
 import re
 
@@ -11,7 +16,7 @@ import torch
 
 import dit_hip as dh
 from conftest import ROOT
-from graphkit import Graph
+from graphkit import Graph, fbits
 
 
 def _conv_graph(up=None, bias=True, Ci=8, Co=16, K=3, H=6, W=10):
@@ -69,3 +74,64 @@ def test_op_ids_follow_the_header():
     assert names.index("CONV_2D_DIRECT") == dh.OP_CONV_2D_DIRECT
     assert names.index("UPSCALE") == dh.OP_UPSCALE
     assert names.index("MUL_MAT") == dh.OP_MUL_MAT and names.index("UNARY") == dh.OP_UNARY
+
+
+def _resnet_tail(Ci=8, Co=16, K=3, H=6, W=10, scale=0.5, res_type=torch.float32, res_shape=None):
+    """x -> conv(+bias) = h; y = SCALE(ADD(res, h), scale)."""
+    g = Graph(device="cpu")
+    x = g.leaf(torch.zeros((1, Ci, H, W)))
+    w = g.leaf(torch.zeros((Co, Ci, K, K)))
+    b = g.leaf(torch.zeros((Co,)))
+    r = g.leaf(torch.zeros(res_shape or (1, Co, H, W), dtype=res_type))
+    c = g.conv_2d_direct(w, x, p0=(K - 1) // 2, p1=(K - 1) // 2)
+    h = g.add(c, g.reshape(b, [1, 1, Co, 1]))
+    s = g.add(h, r) if res_shape else g.add(r, h)
+    y = g.scale(s, scale)
+    return g, x, r, c, h, s, y
+
+
+def test_residual_add_and_scale_fold_into_the_conv():
+    g, x, r, c, h, s, y = _resnet_tail()
+    roots = g.plan(outputs=[y])
+    iy = _index(g, y)
+    assert [roots[_index(g, t)] for t in (c, h, s)] == [iy] * 3 and roots[iy] == -1
+
+
+def test_residual_add_folds_alone_when_the_sum_is_wanted():
+    g, x, r, c, h, s, y = _resnet_tail()
+    roots = g.plan(outputs=[y, s])
+    i_s = _index(g, s)
+    assert roots[_index(g, c)] == i_s and roots[_index(g, h)] == i_s
+    assert roots[i_s] == -1 and roots[_index(g, y)] == -1
+    # a SCALE with a bias term (ggml_scale_bias) is not the module's division: the ADD folds alone
+    g, x, r, c, h, s, y = _resnet_tail()
+    y.d.op_params[1] = fbits(0.25)
+    roots = g.plan(outputs=[y])
+    assert roots[_index(g, h)] == _index(g, s) and roots[_index(g, y)] == -1
+
+
+def test_residual_not_folded_when_the_conv_output_is_wanted_or_does_not_match():
+    g, x, r, c, h, s, y = _resnet_tail()
+    roots = g.plan(outputs=[y, h])
+    assert roots[_index(g, c)] == _index(g, h)
+    assert roots[_index(g, s)] == -1 and roots[_index(g, y)] == -1
+    # a residual of another type, or one broadcast over the image, stays an ADD of its own
+    for kw in (dict(res_type=torch.bfloat16), dict(res_shape=(1, 16, 1, 1))):
+        g, x, r, c, h, s, y = _resnet_tail(**kw)
+        roots = g.plan(outputs=[y])
+        assert roots[_index(g, c)] == _index(g, h), kw
+        assert roots[_index(g, s)] == -1 and roots[_index(g, y)] == -1, kw
+
+
+def test_residual_fold_may_write_over_the_residual_only():
+    # the output exactly on the residual: each element is read by the lane that writes it
+    g, x, r, c, h, s, y = _resnet_tail()
+    y.d.data = r.d.data
+    roots, runs, held = g.plan_checked(outputs=[y])
+    assert roots[_index(g, s)] == _index(g, y) and held == 0
+    # partly over the residual, or over the conv's input (read by every tile): not fused there
+    for target, off in (("res", 128), ("input", 0)):
+        g, x, r, c, h, s, y = _resnet_tail()
+        y.d.data = (r if target == "res" else x).d.data + off
+        roots, runs, held = g.plan_checked(outputs=[y])
+        assert roots[_index(g, s)] != _index(g, y) and held >= 1, (off, roots)
