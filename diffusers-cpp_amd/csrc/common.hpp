@@ -70,6 +70,14 @@ __device__ __forceinline__ void st_stream(void* p, uint4 v) {
     __builtin_nontemporal_store(t, reinterpret_cast<v4u*>(p));
 }
 
+// x / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal (GroupNorm's
+// SiLU, wherever it is applied).  Large negative x: the exponential
+// overflows to inf and the result is -0.
+__device__ __forceinline__ float silu_fast(float t) {
+    const float e = __builtin_amdgcn_exp2f(t * -1.4426950408889634f);
+    return t * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // Row I/O in 16-byte vectors (streaming policy).  EPV = elements per vector.
 template <typename T> struct Io;
 

@@ -50,7 +50,7 @@ struct ConvArgs {
     int TR, TC, tiles_w; // pixel tile geometry; tiles along the width
     float4* stats;       // GroupNorm tile records [N][G][pixel tiles] (dt_conv2d_gn), or null
     int G, cg;           // groups over Co and channels per group (cg divides 128)
-    // Residual epilogue (conv2d_residual): 1: y = res + conv; 2: y = (res +
+    // Residual epilogue (ConvFold): 1: y = res + conv; 2: y = (res +
     // conv) * res_scale.  res is an NCHW tensor of the output's shape and type.
     const void* res;
     int res_mode;
@@ -434,15 +434,28 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
 constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
 constexpr int kXLanesMax3 = 7 * 256;  // DMA lanes per X stage: 2 per record, up to 3 x 258 records
 
+// GroupNorm applied by the channel-last copy: (mean, rstd) per (n, group),
+// the per-channel affine (or null), cg channels per group, the SiLU flag.
+struct CopyGn {
+    const float2* mr;
+    const float* w;
+    const float* b;
+    int G, cg, silu;
+};
+
 // NCHW (fp32 or bf16) -> bf16 NHWC with C16 channels (zeros past C), over
 // the flattened H*W plane in tiles of 64 pixels x 64 channels: 16-byte loads
 // along the pixels of each channel (VEC; scalar when the plane is not a
 // multiple of 8 pixels), a transpose through LDS, and 16-byte stores of 8
 // channels of one pixel.  Block (0, 0, 0) also zeroes the 256-byte tail the
-// conv reads for out-of-image taps.
-template <typename TI, bool VEC>
+// conv reads for out-of-image taps.  GN: each loaded value first becomes
+// silu((x - mean) * (rstd * w_c) + b_c), the very expression (and rounding)
+// of the GroupNorm apply pass, so the copy holds what copying that pass's
+// output would give.
+template <typename TI, bool VEC, bool GN>
 __global__ __launch_bounds__(256) void to_nhwc16_kernel(const TI* __restrict__ x, int C, int64_t HW, int C16,
-                                                        uint16_t* __restrict__ out, int64_t tail_offset) {
+                                                        uint16_t* __restrict__ out, int64_t tail_offset,
+                                                        CopyGn gn) {
     __shared__ uint16_t t[64][64 + 2];  // [channel][pixel] (+2: spread the per-pixel column reads)
     const int64_t p0 = (int64_t)blockIdx.x * 64;
     const int c0 = blockIdx.y * 64, n = blockIdx.z;
@@ -459,6 +472,16 @@ __global__ __launch_bounds__(256) void to_nhwc16_kernel(const TI* __restrict__ x
                 Io<TI>::load(xn + (int64_t)(c0 + c) * HW + p, v);
             } else {
                 v[0] = load_in<TI>(xn + (int64_t)(c0 + c) * HW + p);
+            }
+            if constexpr (GN) {
+                const int ch = c0 + c;
+                const float2 mr = gn.mr[n * gn.G + ch / gn.cg];
+                const float sa = gn.w ? mr.y * gn.w[ch] : mr.y, bc = gn.b ? gn.b[ch] : 0.0f;
+#pragma unroll
+                for (int k = 0; k < EPV; ++k) {
+                    const float t = __builtin_fmaf(v[k] - mr.x, sa, bc);
+                    v[k] = gn.silu ? silu_fast(t) : t;
+                }
             }
         } else {
 #pragma unroll
@@ -811,7 +834,10 @@ void conv_geometry2(int64_t Hs, int64_t Ws, int* TR, int* TC, int64_t* tiles_w, 
 int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
                 int64_t K, int32_t upscale2, const float* bias, void* y, int32_t io_type, float4* stats,
                 int64_t groups, const void* ws, size_t ws_bytes, hipStream_t st, const char* what,
-                int64_t* n_tiles, const void* res = nullptr, int res_mode = 0, float res_scale = 1.0f) {
+                int64_t* n_tiles, const ConvFold* fold = nullptr) {
+    const ConvFold none{};
+    if (!fold) fold = &none;
+    const int res_mode = fold->res_mode;
     DT_REQUIRE(is_io_type(io_type), "%s: io_type %d unsupported", what, io_type);
     DT_REQUIRE(N > 0 && Ci > 0 && H > 0 && W > 0 && Co > 0, "%s: bad shape", what);
     DT_REQUIRE(K == 1 || K == 3, "%s: kernel size %lld unsupported (1 or 3)", what, (long long)K);
@@ -834,16 +860,21 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
     a.stats = stats;
     a.G = (int)groups;
     a.cg = groups > 0 ? (int)(Co / groups) : 0;
-    DT_REQUIRE(!res_mode || (res && !stats), "%s: the residual epilogue needs a residual and no statistics", what);
-    a.res = res;
+    DT_REQUIRE(!res_mode || (fold->res && !stats), "%s: the residual epilogue needs a residual and no statistics",
+               what);
+    a.res = fold->res;
     a.res_mode = res_mode;
-    a.res_scale = res_scale;
+    a.res_scale = fold->res_scale;
+    const bool gn = fold->gn_mr != nullptr;
+    DT_REQUIRE(!gn || (fold->gn_groups > 0 && Ci % fold->gn_groups == 0 && !stats),
+               "%s: the GroupNorm fold needs groups dividing the input channels", what);
     // 1x1 convs keep the staged path: the channel-last copy costs more than
     // their single tap (gfx950, [1, 256, 512, 512] -> 128: 260-312 us with
     // the copy against 135-225 us staged).
     const bool dma = K == 3 && ws && ws_bytes >= (size_t)(nhwc_elems(N, Ci, H, W) * 2 + 256) && aligned16(ws) &&
                      (!stats || (a.cg >= 4 && a.cg <= 64));
     int64_t tiles_w, tiles_h;
+    DT_REQUIRE(!gn || dma, "%s: the GroupNorm fold needs a 3x3 conv with a workspace", what);
     if (dma) conv_geometry2(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
     else conv_geometry(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
     a.tiles_w = (int)tiles_w;
@@ -861,8 +892,17 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
         const int64_t HW = H * W;
         const dim3 tg((unsigned)((HW + 63) / 64), (unsigned)((e.C16 + 63) / 64), (unsigned)N);
         const bool vec = HW % 8 == 0 && aligned16(x);
-#define DT_NHWC(TT, VV) hipLaunchKernelGGL((to_nhwc16_kernel<TT, VV>), tg, dim3(256), 0, st, (const TT*)x, (int)Ci, \
-                                           HW, e.C16, (uint16_t*)ws, elems)
+        const CopyGn cgn{fold->gn_mr, fold->gn_w, fold->gn_b, fold->gn_groups,
+                         gn ? (int)(Ci / fold->gn_groups) : 1, fold->gn_silu};
+#define DT_NHWC(TT, VV)                                                                                        \
+    do {                                                                                                       \
+        if (gn)                                                                                                \
+            hipLaunchKernelGGL((to_nhwc16_kernel<TT, VV, true>), tg, dim3(256), 0, st, (const TT*)x, (int)Ci, HW, \
+                               e.C16, (uint16_t*)ws, elems, cgn);                                              \
+        else                                                                                                   \
+            hipLaunchKernelGGL((to_nhwc16_kernel<TT, VV, false>), tg, dim3(256), 0, st, (const TT*)x, (int)Ci, HW, \
+                               e.C16, (uint16_t*)ws, elems, cgn);                                              \
+    } while (0)
         if (io_type == DT_TYPE_F32) {
             if (vec) DT_NHWC(float, true);
             else DT_NHWC(float, false);
@@ -922,12 +962,12 @@ extern "C" int dt_conv2d(const void* x, int64_t N, int64_t Ci, int64_t H, int64_
 
 namespace dit {
 
-int conv2d_residual(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
-                    int64_t K, int32_t upscale2, const float* bias, const void* res, int scaled, float scale, void* y,
-                    void* workspace, size_t workspace_bytes, int32_t io_type, hipStream_t st) {
+int conv2d_fold(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
+                int64_t K, int32_t upscale2, const float* bias, const ConvFold& fold, void* y, void* workspace,
+                size_t workspace_bytes, int32_t io_type, hipStream_t st) {
     int64_t tiles;
     return conv_launch(x, N, Ci, H, W, packed_w, Co, K, upscale2, bias, y, io_type, nullptr, 0, workspace,
-                       workspace_bytes, st, "conv2d_residual", &tiles, res, scaled ? 2 : 1, scale);
+                       workspace_bytes, st, "conv2d_fold", &tiles, &fold);
 }
 
 }  // namespace dit

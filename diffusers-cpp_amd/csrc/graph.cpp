@@ -138,6 +138,12 @@ struct Plan {
     // res_scale when res_scaled
     int res_scaled = 0;
     float res_scale = 1.f;
+    // CONV with a GroupNorm (+ SiLU) of in[0] applied in its channel-last
+    // copy: gn_groups > 0, the affine gn_w / gn_b (or null), eps and silu
+    // in `eps` / `silu`
+    int64_t gn_groups = 0;
+    const dt_tensor* gn_w = nullptr;
+    const dt_tensor* gn_b = nullptr;
     // QK
     std::vector<QkSeg> segs;
     std::vector<const dt_tensor*> pos;  // per axis
@@ -482,11 +488,17 @@ bool match_attn_qk(Graph& g, const dt_tensor* t, Plan& p) {
     return true;
 }
 
+bool match_groupnorm(Graph& g, const dt_tensor* root, Plan& p);
+
 // Conv2d::forward (Conv2d.cpp:38-102): CONV_2D_DIRECT, or ADD(conv, bias
 // reshaped to [1, Co, 1, 1]) with the conv used only there.  An UPSCALE x2
 // input used only by the conv (Upsample2D.cpp:50-72) is read through the
-// conv's upsampled addressing instead of being materialised.  Operand checks
-// happen at execution (run_conv), where a mismatch is reported.
+// conv's upsampled addressing instead of being materialised.  A 3x3 conv's
+// input that is a GroupNorm (+ affine) (+ SiLU) chain read only here -- the
+// norm -> SiLU -> conv of ResnetBlock2D.inl:114-127, 163-176 and the
+// decoder's conv_out -- is normalised by the conv's channel-last copy, so
+// the normalised tensor is never stored.  Operand checks happen at
+// execution (run_conv), where a mismatch is reported.
 bool match_conv(Graph& g, const dt_tensor* t, Plan& p) {
     const dt_tensor* c = nullptr;
     const dt_tensor* bias = nullptr;
@@ -513,12 +525,25 @@ bool match_conv(Graph& g, const dt_tensor* t, Plan& p) {
     }
     if (c != t) g.claim(c);
     if (up) g.claim(up);
+    Plan gp;
+    const bool gn = c->src[0]->ne[0] == 3 && g.internal(x) && match_groupnorm(g, x, gp);
+    if (gn) {
+        g.claim(x);
+        x = gp.in[0];
+    }
     p.kind = K_CONV;
     p.in[0] = x;
     p.in[1] = c->src[0];
     p.in[2] = bias;
     p.in[3] = c;
     p.up2 = up != nullptr;
+    if (gn) {
+        p.gn_groups = gp.in[3]->ne[1];
+        p.gn_w = gp.in[1];
+        p.gn_b = gp.in[2];
+        p.eps = gp.eps;
+        p.silu = gp.silu;
+    }
     return true;
 }
 
@@ -974,9 +999,11 @@ int run_flash_attn(hipStream_t st, const dt_tensor* t) {
 // (bf16 [Co][K*K][Ci] tiles; a few MB, re-packed per call) unless they come
 // packed once at load (DT_TYPE_CONV2D_PACKED), the channel-last copy of x
 // after them, then dt_conv2d into root.
+// A CONV_2D_DIRECT (x, w, the bias or null, the conv node; up2: x is read
+// 2x upsampled) writing root, with the plan's folds when `p` is given: the
+// residual ADD / SCALE of in[4] and the GroupNorm of x (gn_groups > 0).
 int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt_tensor* w, const dt_tensor* bias,
-             const dt_tensor* conv, int up2, const dt_tensor* res = nullptr, int res_scaled = 0,
-             float res_scale = 1.f) {
+             const dt_tensor* conv, int up2, const Plan* p = nullptr) {
     hipStream_t st = backend_stream(be);
     const int64_t K = w->ne[0], Ci = w->ne[2], Co = w->ne[3];
     const int64_t W = x->ne[0], H = x->ne[1], N = x->ne[3], f = up2 ? 2 : 1;
@@ -995,11 +1022,17 @@ int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt
     DT_REQUIRE(x->ne[2] == Ci && root->ne[0] == W * f && root->ne[1] == H * f && root->ne[2] == Co &&
                    root->ne[3] == N,
                "dt_graph_compute: CONV_2D_DIRECT shapes disagree");
+    const dt_tensor* res = p ? p->in[4] : nullptr;
+    const int64_t G = p ? p->gn_groups : 0;
+    DT_REQUIRE(!G || (K == 3 && Ci % G == 0), "dt_graph_compute: GroupNorm folded into a conv needs a 3x3 kernel");
+    // Scratch: [packed weights][channel-last copy][GroupNorm partials][(mean, rstd)]
     const size_t packed = prepacked ? 0 : (dt_conv2d_packed_bytes(Co, Ci, K) + 255) / 256 * 256;
-    const size_t ws = K == 3 ? dt_conv2d_workspace_bytes(N, Ci, H, W) : 0;
+    const size_t ws = K == 3 ? (dt_conv2d_workspace_bytes(N, Ci, H, W) + 255) / 256 * 256 : 0;
+    const size_t gws = G ? (dt_groupnorm_workspace_bytes(N, Ci, H * W, G) + 255) / 256 * 256 : 0;
+    const size_t mrb = G ? (size_t)(N * G) * sizeof(float2) : 0;
     void* scratch = nullptr;
-    if (packed + ws) {
-        const int rc = backend_scratch(be, packed + ws, &scratch);
+    if (packed + ws + gws + mrb) {
+        const int rc = backend_scratch(be, packed + ws + gws + mrb, &scratch);
         if (rc) return rc;
     }
     const void* wp = prepacked ? data_of(w) : scratch;
@@ -1010,19 +1043,35 @@ int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt
     g_kernels += (prepacked ? 0 : 1) + (K == 3 ? 1 : 0) + 1;  // pack, channel-last copy (3x3), conv
     const float* b = bias ? (const float*)data_of(bias) : nullptr;
     void* wsp = ws ? (char*)scratch + packed : nullptr;
-    if (!res) return dt_conv2d(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, root->data, wsp, ws, root->type, st);
-    // Each output element's residual is read by the lane that then writes
-    // it, so the residual may be the output's own memory, but no other part
-    // of it.
-    const size_t bytes = (size_t)(N * Co * H * f * W * f) * (size_t)elem_size(root->type);
-    const char* r = (const char*)data_of(res);
-    const char* y = (const char*)root->data;
-    DT_REQUIRE(same_shape(res, root) && res->type == root->type && dense(res),
-               "dt_graph_compute: the conv residual must match the output");
-    DT_REQUIRE(r == y || r + bytes <= y || y + bytes <= r,
-               "dt_graph_compute: the conv residual partly overlaps the output");
-    return conv2d_residual(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, data_of(res), res_scaled, res_scale,
-                           root->data, wsp, ws, root->type, st);
+    if (!res && !G) return dt_conv2d(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, root->data, wsp, ws, root->type, st);
+    ConvFold fold;
+    if (G) {
+        float2* mr = (float2*)((char*)scratch + packed + ws + gws);
+        g_kernels += 2;  // GroupNorm partials, (mean, rstd)
+        const int rc = gn_mean_rstd(data_of(x), N, Ci, H * W, G, p->eps, (char*)scratch + packed + ws, mr, x->type, st);
+        if (rc) return rc;
+        fold.gn_mr = mr;
+        fold.gn_w = p->gn_w ? (const float*)data_of(p->gn_w) : nullptr;
+        fold.gn_b = p->gn_b ? (const float*)data_of(p->gn_b) : nullptr;
+        fold.gn_groups = (int)G;
+        fold.gn_silu = p->silu;
+    }
+    if (res) {
+        // Each output element's residual is read by the thread that then
+        // writes it, so the residual may be the output's own memory, but no
+        // other part of it.
+        const size_t bytes = (size_t)(N * Co * H * f * W * f) * (size_t)elem_size(root->type);
+        const char* r = (const char*)data_of(res);
+        const char* y = (const char*)root->data;
+        DT_REQUIRE(same_shape(res, root) && res->type == root->type && dense(res),
+                   "dt_graph_compute: the conv residual must match the output");
+        DT_REQUIRE(r == y || r + bytes <= y || y + bytes <= r,
+                   "dt_graph_compute: the conv residual partly overlaps the output");
+        fold.res = r;
+        fold.res_mode = p->res_scaled ? 2 : 1;
+        fold.res_scale = p->res_scale;
+    }
+    return conv2d_fold(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, fold, root->data, wsp, ws, root->type, st);
 }
 
 int run_upscale(hipStream_t st, const dt_tensor* t) {
@@ -1186,8 +1235,7 @@ int run_plan(dt_backend* be, const dt_tensor* root, Plan& p) {
                                          p.eps, root->type, st);
         }
         case K_CONV:
-            return run_conv(be, root, p.in[0], p.in[1], p.in[2], p.in[3], p.up2, p.in[4], p.res_scaled,
-                            p.res_scale);
+            return run_conv(be, root, p.in[0], p.in[1], p.in[2], p.in[3], p.up2, &p);
         case K_ATTN_QK:
             ++g_kernels;
             return run_attn_qk(be, root, p);

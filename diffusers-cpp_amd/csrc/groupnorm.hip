@@ -99,13 +99,6 @@ __global__ __launch_bounds__(kBlock) void gn_stats_kernel(const T* __restrict__ 
     }
 }
 
-// x / (1 + 2^(-x log2 e)) with the hardware exp2 and reciprocal.  Large
-// negative x: the exponential overflows to inf and the result is -0.
-__device__ __forceinline__ float silu_fast(float t) {
-    const float e = __builtin_amdgcn_exp2f(t * -1.4426950408889634f);
-    return t * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
 // y = silu((x - mean) * (rstd * w_c) + b_c) over this workgroup's chunk of
 // group (n, g).
 template <typename T, bool VEC>
@@ -147,14 +140,10 @@ __device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int
     }
 }
 
-template <typename T, bool VEC>
-__global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
-                                                          const double* __restrict__ ws,
-                                                          const float* __restrict__ w,
-                                                          const float* __restrict__ b, T* y,
-                                                          FastDiv hw_vecs) {
-    __shared__ double red[kBlock / kWave];
-    const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
+// Group ng's (mean, rstd) from its stats partials, summed in a fixed order
+// by the whole workgroup (every caller gets bit-identical values).
+__device__ __forceinline__ void gn_group_stats(const double* __restrict__ ws, const GnShape& s, int ng,
+                                               double* red, float* mean, float* rstd) {
     const double* slot = ws + (int64_t)ng * (2 * s.nchunks + 1);
     double s1 = 0.0, s2 = 0.0;
     for (int i = threadIdx.x; i < s.nchunks; i += kBlock) {
@@ -167,9 +156,31 @@ __global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
     const double dm = s1 * inv_len;
     double var = s2 * inv_len - dm * dm;
     if (var < 0.0) var = 0.0;
-    const float mean = (float)(slot[0] + dm);
-    const float rstd = 1.0f / sqrtf((float)var + s.eps);
+    *mean = (float)(slot[0] + dm);
+    *rstd = 1.0f / sqrtf((float)var + s.eps);
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
+                                                          const double* __restrict__ ws,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ b, T* y,
+                                                          FastDiv hw_vecs) {
+    __shared__ double red[kBlock / kWave];
+    const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
+    float mean, rstd;
+    gn_group_stats(ws, s, ng, red, &mean, &rstd);
     gn_apply_chunk<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs);
+}
+
+// (mean, rstd) of every group, for a consumer that applies the
+// normalisation itself (the 3x3 conv's channel-last copy).
+__global__ __launch_bounds__(kBlock) void gn_mean_rstd_kernel(const double* __restrict__ ws, GnShape s,
+                                                              float2* __restrict__ mr) {
+    __shared__ double red[kBlock / kWave];
+    float mean, rstd;
+    gn_group_stats(ws, s, blockIdx.x, red, &mean, &rstd);
+    if (threadIdx.x == 0) mr[blockIdx.x] = make_float2(mean, rstd);
 }
 
 // Statistics from per-tile (mean, M2, count) records, as dt_conv2d_gn writes
@@ -378,6 +389,43 @@ static int gn_run(const void* x, int64_t N, int64_t C, int64_t HW, int64_t group
 }
 
 namespace dit {
+
+int gn_mean_rstd(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups, float eps, void* workspace,
+                 float2* mr, int32_t io_type, hipStream_t st) {
+    int rc = gn_check_shape("GroupNorm statistics", x, mr, N, C, HW, groups, io_type);
+    if (rc) return rc;
+    DT_REQUIRE(N > 0 && HW > 0 && workspace && ((uintptr_t)workspace & 7) == 0,
+               "GroupNorm statistics: empty input or bad workspace");
+    // The vector path exactly when the unfused GroupNorm takes it: its
+    // statistics' partial sums depend on it.  That output is 16-byte aligned
+    // wherever an allocator places it, so x alone decides.
+    const bool vec = gn_vec_ok(HW, io_type) && aligned16(x);
+    const int epv = vec ? (io_type == DT_TYPE_BF16 ? 8 : 4) : 1;
+    GnShape s;
+    s.C = C;
+    s.HW = HW;
+    s.cg = C / groups;
+    s.group_len = s.cg * HW;
+    s.group_vecs = s.group_len / epv;
+    s.G = (int)groups;
+    s.nchunks = (int)chunks_for(s.group_vecs);
+    s.eps = eps;
+    s.apply_silu = 0;
+    DT_REQUIRE(s.group_vecs < (1ll << 31), "GroupNorm statistics: group too large");
+    const dim3 grid((unsigned)s.nchunks, (unsigned)(N * s.G));
+    double* ws = (double*)workspace;
+    if (io_type == DT_TYPE_F32) {
+        if (vec) hipLaunchKernelGGL((gn_stats_kernel<float, true>), grid, dim3(kBlock), 0, st, (const float*)x, s, ws);
+        else hipLaunchKernelGGL((gn_stats_kernel<float, false>), grid, dim3(kBlock), 0, st, (const float*)x, s, ws);
+    } else {
+        if (vec) hipLaunchKernelGGL((gn_stats_kernel<bf16, true>), grid, dim3(kBlock), 0, st, (const bf16*)x, s, ws);
+        else hipLaunchKernelGGL((gn_stats_kernel<bf16, false>), grid, dim3(kBlock), 0, st, (const bf16*)x, s, ws);
+    }
+    rc = check_launch("GroupNorm statistics");
+    if (rc) return rc;
+    hipLaunchKernelGGL(gn_mean_rstd_kernel, dim3((unsigned)(N * groups)), dim3(kBlock), 0, st, ws, s, mr);
+    return check_launch("GroupNorm statistics (mean, rstd)");
+}
 
 int gn_tile_stats_finalize(const void* stats, int64_t N, int64_t groups, int64_t n_tiles, hipStream_t st) {
     hipLaunchKernelGGL(gn_tile_stats_finalize_kernel, dim3((unsigned)(N * groups)), dim3(kBlock), 0, st,

@@ -93,16 +93,40 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out);
 constexpr int kBackendRopePositions = 4096;
 int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out);
 
-// dt_conv2d (+ bias) followed by ResnetBlock2D's residual (conv2d.hip):
-// y = res + conv, or (res + conv) * scale when `scaled`, with the conv
-// output, the sum and the product each rounded to io_type as the unfused
-// nodes store them.  res has the output's shape and type; it may be y itself
-// (each element is read by the thread that then writes it) but must not
-// overlap y otherwise, and y must not overlap the conv's input x (read
-// around each output pixel).
-int conv2d_residual(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
-                    int64_t K, int32_t upscale2, const float* bias, const void* res, int scaled, float scale, void* y,
-                    void* workspace, size_t workspace_bytes, int32_t io_type, hipStream_t st);
+// Work the graph executor folds into a dt_conv2d (+ bias) launch
+// (conv2d.hip: conv2d_fold).
+struct ConvFold {
+    // GroupNorm (+ affine) (+ SiLU) of the conv's input, applied as the 3x3
+    // conv's channel-last copy reads it: (mean, rstd) per (n, group) from
+    // gn_mean_rstd, the per-channel weight and bias (or null), the SiLU flag.
+    // The copy stores the values the unfused GroupNorm would (then rounded
+    // to bf16 as the copy rounds any input).
+    const float2* gn_mr = nullptr;
+    const float* gn_w = nullptr;
+    const float* gn_b = nullptr;
+    int gn_groups = 0;
+    int gn_silu = 0;
+    // ResnetBlock2D's residual: y = res + conv (res_mode 1) or (res + conv) *
+    // res_scale (2), the conv output, the sum and the product each rounded
+    // to the I/O type as the unfused nodes store them.  res has the output's
+    // shape and type; it may be y itself (each element is read by the thread
+    // that then writes it) but must not overlap y otherwise.
+    const void* res = nullptr;
+    int res_mode = 0;
+    float res_scale = 1.0f;
+};
+// dt_conv2d with `fold`; y must not overlap the conv's input x (read around
+// each output pixel).  The GroupNorm fold needs a 3x3 conv and a workspace.
+int conv2d_fold(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, const void* packed_w, int64_t Co,
+                int64_t K, int32_t upscale2, const float* bias, const ConvFold& fold, void* y, void* workspace,
+                size_t workspace_bytes, int32_t io_type, hipStream_t st);
+
+// GroupNorm statistics of x (NCHW, groups of C / groups channels) as
+// (mean, rstd) per (n, group) in mr[N * groups], with exactly the values
+// the two-pass dt_groupnorm_silu applies (groupnorm.hip); workspace as
+// dt_groupnorm_silu's (dt_groupnorm_workspace_bytes).
+int gn_mean_rstd(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups, float eps, void* workspace,
+                 float2* mr, int32_t io_type, hipStream_t st);
 
 // The bf16 values of a DT_TYPE_Q8_0_SPLIT weight [N][K] (codes, then scales
 // [K/32][ld_scales]) into out [N][K] (dequant.hip).

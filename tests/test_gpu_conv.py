@@ -276,3 +276,76 @@ def test_conv_residual_epilogue_equals_the_nodes(orc, dev, io, shape, co, k, sca
     conv = orc.conv2d(orc.round_bf16(as_input(x, io)), orc.round_bf16(w), b)
     want = (as_input(res, io) + conv) * np.float32(scale)
     check(host(fused_out), want, io, "conv + residual", one_rounding=False)
+
+
+# ----------------------------------------- GroupNorm in the channel-last copy --
+# norm -> SiLU -> conv (ResnetBlock2D.inl:114-127, 163-176): the executor
+# applies the GroupNorm (+ affine) (+ SiLU) as the 3x3 conv's channel-last
+# copy reads its input, so the normalised tensor is never stored.
+
+def _gn_conv_graph(x, gw, gb, G, w, b, io, affine, silu, up, res=None):
+    from graphkit import Graph
+    g = Graph()
+    N, C, H, W = x.shape
+    Co, K = w.shape[0], w.shape[-1]
+    X = g.leaf(dev_tensor(x, io))
+    v = g.reshape(X, [C // G * H * W, G, N])
+    cur = g.reshape(g.norm(v, 1e-6), [W, H, C, N])
+    if affine:
+        cur = g.mul(cur, g.leaf(dev_tensor(gw.reshape(1, C, 1, 1), torch.float32)))
+        cur = g.add(cur, g.leaf(dev_tensor(gb.reshape(1, C, 1, 1), torch.float32)))
+    if silu:
+        cur = g.mul(cur, g.sigmoid(cur))
+    gn = cur
+    u = g.upscale(gn, 2) if up else gn
+    c = g.conv_2d_direct(g.leaf(dev_tensor(w, torch.float32)), u, p0=K // 2, p1=K // 2)
+    y = g.add(c, g.reshape(g.leaf(dev_tensor(b, torch.float32)), [1, 1, Co, 1]))
+    if res is not None:
+        y = g.scale(g.add(g.leaf(dev_tensor(res, io)), y), 0.5)
+    return g, gn, y
+
+
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,G,co,affine,silu,up,residual", [
+    ((1, 64, 16, 24), 32, 64, True, True, False, False),
+    ((2, 32, 9, 13), 8, 48, True, True, False, True),      # plane not a multiple of 8: scalar statistics
+    ((1, 128, 32, 32), 32, 128, False, True, False, True),
+    ((1, 48, 12, 20), 4, 40, True, False, True, False),    # no SiLU, 2x upscale between norm and conv
+    ((1, 256, 20, 20), 32, 64, True, True, False, False)])
+def test_groupnorm_folded_into_conv_equals_the_nodes(orc, dev, io, shape, G, co, affine, silu, up, residual):
+    """Fused (GroupNorm statistics, (mean, rstd), the normalising
+    channel-last copy, the conv) against the same nodes with the GroupNorm
+    output kept as a graph output (two-pass GroupNorm, then the conv): the
+    same bits; and against the oracle."""
+    from graphkit import Backend
+    print(f"gn+conv x={shape} G={G} co={co} affine={affine} silu={silu} up={up} res={residual} {io}", flush=True)
+    x = orc.randn(SEED + 70, shape)
+    gw = orc.randn(SEED + 71, (shape[1],), mean=1.0, std=0.1)
+    gb = orc.randn(SEED + 72, (shape[1],), std=0.1)
+    w = orc.randn(SEED + 73, (co, shape[1], 3, 3), std=0.05)
+    b = orc.randn(SEED + 74, (co,), std=0.1)
+    f = 2 if up else 1
+    res = orc.randn(SEED + 75, (shape[0], co, shape[2] * f, shape[3] * f)) if residual else None
+    be = Backend()
+    try:
+        g, gn, y = _gn_conv_graph(x, gw, gb, G, w, b, io, affine, silu, up, res)
+        kernels, fused = g.compute(be.h, outputs=[y])
+        torch.cuda.synchronize()
+        fused_out = y.data.clone()
+        g2, gn2, y2 = _gn_conv_graph(x, gw, gb, G, w, b, io, affine, silu, up, res)
+        kernels2, fused2 = g2.compute(be.h, outputs=[y2, gn2])
+        torch.cuda.synchronize()
+        gn_out = gn2.data.clone()
+    finally:
+        be.close()
+    # statistics + (mean, rstd) replace statistics + apply (then pack, copy, conv): the same
+    # five launches, and the GroupNorm's root joins the conv's plan
+    assert kernels == kernels2 == 5 and fused == fused2 + 1, (kernels, kernels2, fused, fused2)
+    bits = torch.int16 if io == torch.bfloat16 else torch.int32
+    assert torch.equal(fused_out.view(bits), y2.data.view(bits))
+    ref_gn = orc.groupnorm_silu(as_input(x, io), G, gw if affine else None, gb if affine else None, 1e-6, silu=silu)
+    check(host(gn_out), ref_gn, io, "GroupNorm (unfused)", one_rounding=False)
+    want = orc.conv2d(orc.round_bf16(host(gn_out)), orc.round_bf16(w), b, up2=up)
+    if residual:
+        want = (as_input(res, io) + want) * np.float32(0.5)
+    check(host(fused_out), want, io, "GroupNorm + conv", one_rounding=False)

@@ -8,7 +8,9 @@ conv's input when the conv is its only consumer.  ResnetBlock2D's tail,
 ResnetBlock2D.inl:194: ADD(res, conv2) then SCALE), folds into conv2's
 epilogue when conv2's output and the ADD are used nowhere else; the memory
 replay lets the output sit exactly on the residual but not on the conv's
-input."""
+input.  A GroupNorm (+ affine) (+ SiLU) chain read only by a 3x3 conv
+(ResnetBlock2D.inl:114-127, 163-176) is applied in the conv's channel-last
+copy."""
 import os
 import re
 
@@ -135,3 +137,47 @@ def test_residual_fold_may_write_over_the_residual_only():
         y.d.data = (r if target == "res" else x).d.data + off
         roots, runs, held = g.plan_checked(outputs=[y])
         assert roots[_index(g, s)] != _index(g, y) and held >= 1, (off, roots)
+
+
+def _gn_conv(K=3, affine=True, silu=True, up=False, C=16, G=4, Co=8, H=6, W=10):
+    """GroupNorm::forward (reshape, NORM, reshape, MUL w, ADD b) + SiLU, then a conv + bias."""
+    g = Graph(device="cpu")
+    x = g.leaf(torch.zeros((1, C, H, W)))
+    v = g.reshape(x, [C // G * H * W, G, 1])
+    n = g.norm(v, 1e-6)
+    cur = g.reshape(n, [W, H, C, 1])
+    if affine:
+        cur = g.mul(cur, g.reshape(g.leaf(torch.zeros((C,))), [1, 1, C, 1]))
+        cur = g.add(cur, g.reshape(g.leaf(torch.zeros((C,))), [1, 1, C, 1]))
+    if silu:
+        cur = g.mul(cur, g.sigmoid(cur))
+    gn = cur
+    u = g.upscale(gn, 2) if up else gn
+    w = g.leaf(torch.zeros((Co, C, K, K)))
+    b = g.leaf(torch.zeros((Co,)))
+    c = g.conv_2d_direct(w, u, p0=(K - 1) // 2, p1=(K - 1) // 2)
+    y = g.add(c, g.reshape(b, [1, 1, Co, 1]))
+    return g, n, gn, c, y
+
+
+def test_groupnorm_folds_into_the_3x3_conv_copy():
+    for kw in (dict(), dict(affine=False), dict(silu=False), dict(up=True)):
+        g, n, gn, c, y = _gn_conv(**kw)
+        roots = g.plan(outputs=[y])
+        iy = _index(g, y)
+        assert roots[_index(g, n)] == iy and roots[_index(g, gn)] == iy and roots[_index(g, c)] == iy, kw
+        assert roots[iy] == -1, kw
+
+
+def test_groupnorm_not_folded_into_1x1_convs_or_when_wanted():
+    g, n, gn, c, y = _gn_conv(K=1)
+    roots = g.plan(outputs=[y])
+    assert roots[_index(g, n)] == _index(g, gn) and roots[_index(g, gn)] == -1
+    g, n, gn, c, y = _gn_conv()
+    roots = g.plan(outputs=[y, gn])
+    assert roots[_index(g, n)] == _index(g, gn) and roots[_index(g, gn)] == -1
+    assert roots[_index(g, c)] == _index(g, y)
+    # a bare NORM (no affine, no SiLU) is not a GroupNorm chain
+    g, n, gn, c, y = _gn_conv(affine=False, silu=False)
+    roots = g.plan(outputs=[y])
+    assert roots[_index(g, n)] == -1
