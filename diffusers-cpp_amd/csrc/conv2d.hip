@@ -726,30 +726,10 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
         if (ch + 2 < nch) issue((ch + 2) * kCi2, ch & 1);
     }
 
-    if constexpr (!STATS) {
-        conv_store_lds<T, RES>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g, e.lt, n);
-        return;
-    }
-    T* y = reinterpret_cast<T*>(a.y) + (int64_t)n * a.Co * a.Hs * a.Ws;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int p = wpx + 32 * i + lrow;
-        const int oh = oh0 + (p >> e.lt), ow = ow0 + (p & (a.TC - 1));
-        if (oh >= a.Hs || ow >= a.Ws) continue;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int co = co0 + wco + 32 * j + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (co >= a.Co) continue;
-                float v = acc[j][i][r];
-                if (a.bias) v = add_rn(v, a.bias[co]);
-                Io<T>::put(y + ((int64_t)co * a.Hs + oh) * a.Ws + ow, v);
-            }
-        }
-    }
+    // The stores go through LDS (ending in a barrier, so the statistics
+    // below may reuse it).
+    conv_store_lds<T, RES>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g, e.lt, n);
     if constexpr (STATS) {
-        __syncthreads();
         float* red = reinterpret_cast<float*>(smem);
         switch (a.cg) {
             case 4: conv_group_stats_reg<T, 4, 4>(a, acc, red, co0, oh0, ow0, wco, wpx, lrow, g, wave); break;
