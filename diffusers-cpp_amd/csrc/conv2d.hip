@@ -432,7 +432,12 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
 // index (pixels) or of co (weights) is set, so 8 consecutive records read
 // distinct banks.
 constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
-constexpr int kXLanesMax3 = 7 * 256;  // DMA lanes per X stage: 2 per record, up to 3 x 258 records
+// DMA lanes per X stage: 2 per record, up to the 10 x 34 records of an
+// 8 x 32 tile (the 16 x 16 tile needs 18 x 18).  Lanes past the patch read
+// the zero tail, so the count is kept to the largest patch.
+constexpr int kXLanesMax3 = 3 * 256;
+static_assert(2 * (8 + 2) * (32 + 2) <= kXLanesMax3 && 2 * (16 + 2) * (16 + 2) <= kXLanesMax3,
+              "X DMA lanes must cover the 3x3 patch of every tile shape conv_geometry2 picks");
 
 // GroupNorm applied by the channel-last copy: (mean, rstd) per (n, group),
 // the per-channel affine (or null), cg channels per group, the SiLU flag.
@@ -567,14 +572,37 @@ __device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int q = 8 * (r >> 2) + 4 * g + (r & 3), co = co0 + wco + 32 * j + q;
-                float v = acc[j][i][r];
-                if (a.bias && co < a.Co) v = add_rn(v, a.bias[co]);
-                Io<T>::put(lds + ((wco >> 6) * 32 + q) * S + wpx + 32 * i + lrow, v);
+                v[r] = acc[j][i][r];
+                if (a.bias && co < a.Co) v[r] = add_rn(v[r], a.bias[co]);
             }
+            if constexpr (sizeof(T) == 2) {
+                // Lanes 2k and 2k + 1 hold pixels p and p + 1.  For each
+                // pair of adjacent channels (r, r + 1) they swap one value
+                // (DPP lane ^ 1), so the even lane writes channel r's and
+                // the odd lane channel r + 1's two pixels as one dword.
+                const bool odd = lrow & 1;
+                const int p = wpx + 32 * i + (lrow & ~1);
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    const float mine = odd ? v[r + 1] : v[r];
+                    const float other = dpp_f32<0xB1>(odd ? v[r] : v[r + 1]);
+                    const int q = 8 * (r >> 2) + 4 * g + (r & 3) + (odd ? 1 : 0);
+                    *reinterpret_cast<uint32_t*>(lds + ((wco >> 6) * 32 + q) * S + p) =
+                        odd ? pack_bf16x2(other, mine) : pack_bf16x2(mine, other);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int q = 8 * (r >> 2) + 4 * g + (r & 3);
+                    Io<T>::put(lds + ((wco >> 6) * 32 + q) * S + wpx + 32 * i + lrow, v[r]);
+                }
+            }
+        }
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < PIECES; ++k) {
