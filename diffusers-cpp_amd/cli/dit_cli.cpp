@@ -890,6 +890,28 @@ void run(const Args& a) {
         Tensor y = m.forward(x, temb ? &*temb : nullptr);
         if (a.has("out")) s.output(y, "out");
         else s.keep(y);
+    } else if (c == "UpDecoderBlock2D") {
+        // UpDecoderBlock2D.py (the reference CLI's main.cpp:461-497 arguments): --in_channels,
+        // --out_channels, --num_layers, --resnet_groups, --output_scale_factor, --add_upsample,
+        // --temb_channels; --hidden_states, or --random-inputs SEED with --batch --height --width;
+        // parameters from --weights DIR or --random-weights SEED; --dtype f32|bf16;
+        // --packed-weights true packs the conv weights once at load
+        const int32_t act = a.str("dtype", "f32") == "bf16" ? DT_TYPE_BF16 : DT_TYPE_F32;
+        LinearWeightType wt(act);
+        ConvWeightType cw(a.flag("packed-weights", false) ? DT_TYPE_CONV2D_PACKED : DT_TYPE_F32);
+        UpDecoderBlock2D m(a.i64("in_channels"), a.i64("out_channels"), std::nullopt, 0.0f, a.i64("num_layers", 1),
+                           1e-6f, a.i64("resnet_groups", 32), true, a.f32("output_scale_factor", 1.0f),
+                           a.flag("add_upsample", true),
+                           a.has("temb_channels") ? std::optional<int64_t>(a.i64("temb_channels")) : std::nullopt);
+        Tensor x = a.has("random-inputs")
+                       ? s.random_input({a.i64("batch", 1), a.i64("in_channels"), a.i64("height"), a.i64("width")},
+                                        act, (uint64_t)a.i64("random-inputs"))
+                       : s.input_as("hidden_states", act);
+        if (a.has("random-weights")) s.random_weights(m, (uint64_t)a.i64("random-weights"), 0.02f);
+        else s.load_weights(m, a.str("weights"));
+        Tensor y = m.forward(x);
+        if (a.has("out")) s.output(y, "out");
+        else s.keep(y);
     } else if (c == "SiLU") {
         s.output(SiLU().forward(s.input("x")), "out");
     } else if (c == "Flux2PosEmbed") {

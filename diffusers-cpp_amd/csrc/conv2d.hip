@@ -536,12 +536,18 @@ __device__ __forceinline__ void conv_wait_vm() {
 // residual (loaded before the LDS stage, so its latency overlaps it), the
 // ADD rounded to T, the SCALE (res_mode 2), one store.  A piece is read and
 // written by one thread only, so the output may sit on the residual.
+// The epilogue's LDS: 64 output-channel rows of 256 pixels, padded to 264
+// elements; the DMA kernel's shared array is at least this large.
+constexpr int kEpiStride = 264;
+template <typename T>
+constexpr int epi_lds_bytes() { return 64 * kEpiStride * (int)sizeof(T); }
+
 template <typename T, bool RES>
 __device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t (&acc)[2][4], uint8_t* smem,
                                                int co0, int oh0, int ow0, int wco, int wpx, int lrow, int g, int lt,
                                                int n) {
     constexpr int E = Io<T>::EPV;             // elements per 16-byte piece
-    constexpr int S = 264;                    // LDS row stride in elements (bank-spread rows)
+    constexpr int S = kEpiStride;             // LDS row stride in elements (bank-spread rows)
     constexpr int RP = 256 / E;               // pieces per 256-pixel row
     constexpr int PIECES = 64 * RP / 256;     // pieces per thread and pass
     T* lds = reinterpret_cast<T*>(smem);
@@ -646,13 +652,15 @@ __device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t
 
 template <typename T, int K, bool STATS, bool RES>
 __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const Conv2Extra e) {
-    static_assert(K == 3, "the DMA kernel is sized for 3x3 patches");
+    static_assert(K == 3 || K == 1, "the DMA kernel takes 3x3 and 1x1 patches");
     constexpr int KK = K * K, PAD = (K - 1) / 2;
     constexpr int XL = kXLanesMax3;  // X DMA lanes per stage
     constexpr int NX = XL / 256, NW = 2 * kTileCo * KK / 256;  // DMA instructions per wave per stage
     constexpr int XB = XL * 16, WB = kTileCo * KK * kRec2, STAGE = XB + WB;
     constexpr int QD = NX + NW;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * STAGE];
+    // the two DMA stages, then the epilogue's rows (larger for 1x1 patches)
+    constexpr int SMEM = 2 * STAGE > epi_lds_bytes<T>() ? 2 * STAGE : epi_lds_bytes<T>();
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = blockIdx.z, co0 = blockIdx.y * kTileCo;
@@ -882,11 +890,12 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
     const bool gn = fold->gn_mr != nullptr;
     DT_REQUIRE(!gn || (fold->gn_groups > 0 && Ci % fold->gn_groups == 0 && !stats),
                "%s: the GroupNorm fold needs groups dividing the input channels", what);
-    // 1x1 convs keep the staged path: the channel-last copy costs more than
-    // their single tap (gfx950, [1, 256, 512, 512] -> 128: 260-312 us with
-    // the copy against 135-225 us staged).
-    const bool dma = K == 3 && ws && ws_bytes >= (size_t)(nhwc_elems(N, Ci, H, W) * 2 + 256) && aligned16(ws) &&
-                     (!stats || (a.cg >= 4 && a.cg <= 64));
+    // With a workspace 3x3 convs, and 1x1 convs on bf16, take the DMA path
+    // (gfx950, 1x1 [1, 256, 512, 512] -> 128: bf16 158 us against 217 us
+    // staged; fp32 163 us against 136 us, its channel-last copy reading
+    // twice the bytes).
+    const bool dma = conv_uses_dma(K, io_type) && ws && ws_bytes >= (size_t)(nhwc_elems(N, Ci, H, W) * 2 + 256) &&
+                     aligned16(ws) && (!stats || (a.cg >= 4 && a.cg <= 64));
     int64_t tiles_w, tiles_h;
     DT_REQUIRE(!gn || dma, "%s: the GroupNorm fold needs a 3x3 conv with a workspace", what);
     if (dma) conv_geometry2(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
@@ -930,13 +939,25 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
 #define DT_CONV2_LAUNCH(TT, KS, ST, RS) \
     hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST, RS>), grid, dim3(256), 0, st, a, e)
         if (io_type == DT_TYPE_F32) {
-            if (stats) DT_CONV2_LAUNCH(float, 3, true, false);
-            else if (res_mode) DT_CONV2_LAUNCH(float, 3, false, true);
-            else DT_CONV2_LAUNCH(float, 3, false, false);
+            if (K == 1) {
+                if (stats) DT_CONV2_LAUNCH(float, 1, true, false);
+                else if (res_mode) DT_CONV2_LAUNCH(float, 1, false, true);
+                else DT_CONV2_LAUNCH(float, 1, false, false);
+            } else {
+                if (stats) DT_CONV2_LAUNCH(float, 3, true, false);
+                else if (res_mode) DT_CONV2_LAUNCH(float, 3, false, true);
+                else DT_CONV2_LAUNCH(float, 3, false, false);
+            }
         } else {
-            if (stats) DT_CONV2_LAUNCH(bf16, 3, true, false);
-            else if (res_mode) DT_CONV2_LAUNCH(bf16, 3, false, true);
-            else DT_CONV2_LAUNCH(bf16, 3, false, false);
+            if (K == 1) {
+                if (stats) DT_CONV2_LAUNCH(bf16, 1, true, false);
+                else if (res_mode) DT_CONV2_LAUNCH(bf16, 1, false, true);
+                else DT_CONV2_LAUNCH(bf16, 1, false, false);
+            } else {
+                if (stats) DT_CONV2_LAUNCH(bf16, 3, true, false);
+                else if (res_mode) DT_CONV2_LAUNCH(bf16, 3, false, true);
+                else DT_CONV2_LAUNCH(bf16, 3, false, false);
+            }
         }
 #undef DT_CONV2_LAUNCH
         return check_launch(what);

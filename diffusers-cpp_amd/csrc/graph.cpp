@@ -554,7 +554,10 @@ bool match_conv(Graph& g, const dt_tensor* t, Plan& p) {
 // the residual and scales, with the ADD's value rounded to the node type
 // as the graph stores it, so neither full-tensor pass runs.  Without the
 // SCALE (a factor of 1 still records it; a graph may also end at the ADD)
-// the ADD alone is folded.
+// the ADD alone is folded.  When both operands are convs (a block with a
+// 1x1 conv_shortcut), the 3x3 one takes the residual: its epilogue stages
+// the output through LDS, where the 1x1 kernel's would load the residual
+// element by element.  Among equals, hidden_states (the ADD's src1) does.
 bool match_conv_residual(Graph& g, const dt_tensor* t, Plan& p) {
     const dt_tensor* add = t;
     if (t->op == DT_OP_SCALE) {
@@ -564,16 +567,31 @@ bool match_conv_residual(Graph& g, const dt_tensor* t, Plan& p) {
             return false;
     }
     if (add->op != DT_OP_ADD || !dense(t)) return false;
-    for (int k = 0; k < 2; ++k) {
+    // the conv node under h (CONV_2D_DIRECT itself, or under its bias ADD)
+    auto conv_of = [](const dt_tensor* h) -> const dt_tensor* {
+        if (!h) return nullptr;
+        if (h->op == DT_OP_CONV_2D_DIRECT) return h;
+        if (h->op != DT_OP_ADD) return nullptr;
+        for (int k = 0; k < 2; ++k)
+            if (h->src[k] && h->src[k]->op == DT_OP_CONV_2D_DIRECT) return h->src[k];
+        return nullptr;
+    };
+    auto is3x3 = [&](const dt_tensor* h) {
+        const dt_tensor* c = conv_of(h);
+        return c && c->src[0] && c->src[0]->ne[0] == 3;
+    };
+    int order[2] = {1, 0};
+    if (!is3x3(add->src[1]) && is3x3(add->src[0])) {
+        order[0] = 0;
+        order[1] = 1;
+    }
+    for (int k : order) {
         const dt_tensor* h = add->src[k];
         const dt_tensor* res = add->src[1 - k];
         if (!h || !res || h == res || !g.internal(h) || !same_shape(h, add) || h->type != add->type ||
             !same_shape(res, add) || res->type != add->type || !dense(res))
             continue;
-        const bool conv = h->op == DT_OP_CONV_2D_DIRECT ||
-                          (h->op == DT_OP_ADD && ((h->src[0] && h->src[0]->op == DT_OP_CONV_2D_DIRECT) ||
-                                                  (h->src[1] && h->src[1]->op == DT_OP_CONV_2D_DIRECT)));
-        if (!conv) continue;
+        if (!conv_of(h)) continue;
         Plan cp;
         if (!match_conv(g, h, cp)) continue;
         g.claim(h);
@@ -1027,7 +1045,7 @@ int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt
     DT_REQUIRE(!G || (K == 3 && Ci % G == 0), "dt_graph_compute: GroupNorm folded into a conv needs a 3x3 kernel");
     // Scratch: [packed weights][channel-last copy][GroupNorm partials][(mean, rstd)]
     const size_t packed = prepacked ? 0 : (dt_conv2d_packed_bytes(Co, Ci, K) + 255) / 256 * 256;
-    const size_t ws = K == 3 ? (dt_conv2d_workspace_bytes(N, Ci, H, W) + 255) / 256 * 256 : 0;
+    const size_t ws = (dt_conv2d_workspace_bytes(N, Ci, H, W) + 255) / 256 * 256;
     const size_t gws = G ? (dt_groupnorm_workspace_bytes(N, Ci, H * W, G) + 255) / 256 * 256 : 0;
     const size_t mrb = G ? (size_t)(N * G) * sizeof(float2) : 0;
     void* scratch = nullptr;
@@ -1040,7 +1058,7 @@ int run_conv(dt_backend* be, const dt_tensor* root, const dt_tensor* x, const dt
         const int rc = dt_conv2d_pack_weights(data_of(w), w->type, Co, Ci, K, scratch, st);
         if (rc) return rc;
     }
-    g_kernels += (prepacked ? 0 : 1) + (K == 3 ? 1 : 0) + 1;  // pack, channel-last copy (3x3), conv
+    g_kernels += (prepacked ? 0 : 1) + (conv_uses_dma(K, root->type) ? 1 : 0) + 1;  // pack, channel-last copy, conv
     const float* b = bias ? (const float*)data_of(bias) : nullptr;
     void* wsp = ws ? (char*)scratch + packed : nullptr;
     if (!res && !G) return dt_conv2d(data_of(x), N, Ci, H, W, wp, Co, K, up2, b, root->data, wsp, ws, root->type, st);

@@ -93,6 +93,10 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out);
 constexpr int kBackendRopePositions = 4096;
 int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const float** out);
 
+// Whether dt_conv2d with a workspace runs a K x K conv on io_type through
+// the channel-last copy and the DMA kernel (else the register-staged kernel).
+inline bool conv_uses_dma(int64_t K, int32_t io_type) { return K == 3 || (K == 1 && io_type == DT_TYPE_BF16); }
+
 // Work the graph executor folds into a dt_conv2d (+ bias) launch
 // (conv2d.hip: conv2d_fold).
 struct ConvFold {

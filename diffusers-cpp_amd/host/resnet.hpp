@@ -1,7 +1,9 @@
 // resnet.hpp -- ResnetBlock2D (src/diffusers/models/resnet/ResnetBlock2D.hpp,
 // ResnetBlock2D.inl:7-195), the residual block of the VAE decoder's mid and
-// up blocks (UNetMidBlock2D.cpp:52, UpDecoderBlock2D.cpp:28), on the host
-// Tensor layer.  It records the reference's node sequence:
+// up blocks (UNetMidBlock2D.cpp:52, UpDecoderBlock2D.cpp:28), and
+// UpDecoderBlock2D (src/diffusers/models/unets/unet2d/UpDecoderBlock2D.cpp:6-74),
+// on the host Tensor layer.  ResnetBlock2D records the reference's node
+// sequence:
 //   norm1 -> SiLU -> conv1 [-> + time_emb_proj(SiLU(temb))[:, :, None, None]]
 //   -> norm2 -> SiLU -> conv2, then (shortcut(x) + h) / output_scale_factor
 // and the executor runs each GroupNorm + SiLU as one kernel and conv2 with
@@ -11,6 +13,8 @@
 #include <memory>
 #include <optional>
 #include <stdexcept>
+#include <string>
+#include <vector>
 
 #include "flux2.hpp"
 
@@ -90,6 +94,42 @@ public:
 private:
     std::unique_ptr<Linear> time_emb_proj_;
     std::unique_ptr<Conv2d> conv_shortcut_;
+};
+
+// UpDecoderBlock2D (UpDecoderBlock2D.cpp:6-74): num_layers ResnetBlock2D
+// (the first in_channels -> out_channels, the rest out -> out; groups
+// resnet_groups, eps resnet_eps, no temb projection unless temb_channels),
+// then with add_upsample an Upsample2D with its 3x3 conv.  As in the
+// reference, forward does not pass temb to the resnets.  Parameters are
+// named resnets.<i>.* and upsamplers.0.conv.*.
+class UpDecoderBlock2D : public Module {
+public:
+    UpDecoderBlock2D(int64_t in_channels, int64_t out_channels, std::optional<int64_t> resolution_idx = std::nullopt,
+                     float dropout = 0.0f, int64_t num_layers = 1, float resnet_eps = 1e-6f, int64_t resnet_groups = 32,
+                     bool resnet_pre_norm = true, float output_scale_factor = 1.0f, bool add_upsample = true,
+                     std::optional<int64_t> temb_channels = std::nullopt) {
+        (void)resolution_idx;
+        for (int64_t i = 0; i < num_layers; ++i) {
+            resnets_.emplace_back(new ResnetBlock2D<SiLU>(i == 0 ? in_channels : out_channels, out_channels,
+                                                          std::nullopt, dropout, temb_channels, resnet_groups,
+                                                          std::nullopt, resnet_pre_norm, resnet_eps, false, 3,
+                                                          output_scale_factor));
+            register_module("resnets." + std::to_string(i), *resnets_.back());
+        }
+        if (add_upsample) {
+            up_.reset(new Upsample2D(out_channels, true, out_channels));
+            register_module("upsamplers.0", *up_);
+        }
+    }
+
+    Tensor forward(Tensor hidden_states) const {
+        for (const auto& r : resnets_) hidden_states = r->forward(hidden_states);
+        return up_ ? up_->forward(hidden_states) : hidden_states;
+    }
+
+private:
+    std::vector<std::unique_ptr<ResnetBlock2D<SiLU>>> resnets_;
+    std::unique_ptr<Upsample2D> up_;
 };
 
 }  // namespace host

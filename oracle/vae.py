@@ -4,8 +4,10 @@ Test infrastructure only (the tests use it as the checker); the product
 never imports it.  Each function follows the reference module it names, op
 for op, in fp32 with NCHW tensors:
 
-  resnet_block2d  ResnetBlock2D::forward
-                  (src/diffusers/models/resnet/ResnetBlock2D.inl:7-195)
+  resnet_block2d      ResnetBlock2D::forward
+                      (src/diffusers/models/resnet/ResnetBlock2D.inl:7-195)
+  up_decoder_block2d  UpDecoderBlock2D::forward
+                      (src/diffusers/models/unets/unet2d/UpDecoderBlock2D.cpp:6-74)
 
 Parameters are a dict keyed by the reference's dotted parameter paths
 (norm1.weight, conv1.bias, ...); resnet_block2d_param_shapes lists them.
@@ -86,3 +88,36 @@ def resnet_block2d(x, P, groups=32, groups_out=None, eps=1e-6, output_scale_fact
         x = conv(x, g("conv_shortcut.weight"), P.get(prefix + "conv_shortcut.bias"), padding=0, threads=threads)
     s = (x + h).astype(np.float32)
     return (s * (np.float32(1.0) / np.float32(output_scale_factor))).astype(np.float32)
+
+
+def up_decoder_block2d_param_shapes(in_channels: int, out_channels: int, num_layers: int = 1,
+                                    add_upsample: bool = True, temb_channels: int | None = None,
+                                    prefix: str = ""):
+    """UpDecoderBlock2D's parameters (UpDecoderBlock2D.cpp:20-57): resnets.<i>.*
+    (the first in -> out, the rest out -> out) and upsamplers.0.conv.*."""
+    s = {}
+    for i in range(num_layers):
+        s.update(resnet_block2d_param_shapes(in_channels if i == 0 else out_channels, out_channels, temb_channels,
+                                             prefix=f"{prefix}resnets.{i}."))
+    if add_upsample:
+        s[f"{prefix}upsamplers.0.conv.weight"] = (out_channels, out_channels, 3, 3)
+        s[f"{prefix}upsamplers.0.conv.bias"] = (out_channels,)
+    return s
+
+
+def up_decoder_block2d(x, P, num_layers=1, resnet_groups=32, eps=1e-6, output_scale_factor=1.0,
+                       add_upsample=True, prefix="", threads=0, conv_bf16=False):
+    """UpDecoderBlock2D::forward (UpDecoderBlock2D.cpp:60-74): the resnets in
+    order (temb is not passed to them), then with add_upsample the
+    Upsample2D: nearest 2x and its 3x3 conv + bias (Upsample2D.cpp:36-63)."""
+    h = np.asarray(x, np.float32)
+    for i in range(num_layers):
+        h = resnet_block2d(h, P, resnet_groups, None, eps, output_scale_factor, None, prefix=f"{prefix}resnets.{i}.",
+                           threads=threads, conv_bf16=conv_bf16)
+    if add_upsample:
+        w = P[prefix + "upsamplers.0.conv.weight"]
+        b = P[prefix + "upsamplers.0.conv.bias"]
+        if conv_bf16:
+            h, w = round_bf16(h), round_bf16(w)
+        h = conv2d(h, w, b, up2=True, threads=threads)
+    return h

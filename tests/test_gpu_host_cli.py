@@ -302,7 +302,7 @@ def test_conv2d(orc, cli, x_shape, ci, co, k, pad, bias):
     want = orc.conv2d(orc.round_bf16(xv), orc.round_bf16(w), b if bias else None)
     check(got, want, cli.bf16, "Conv2d")
     assert st["fused_nodes"] == (1 if bias else 0), st      # the bias ADD folds into the conv
-    assert st["kernels"] == (3 if k == 3 else 2), st         # pack, channel-last copy (3x3), conv
+    assert st["kernels"] == (3 if k == 3 or cli.bf16 else 2), st  # pack, channel-last copy (3x3; 1x1 bf16), conv
     # the weight packed once at load (DT_TYPE_CONV2D_PACKED): no pack per call, same bits
     sp = cli.run("Conv2d", *args, "--packed-weights", "true")
     assert np.array_equal(read_dtb(cli.out()).view(np.uint32), got.view(np.uint32))
@@ -392,10 +392,48 @@ def test_resnet_block2d(orc, cli, c):
     if not c["temb"]:
         # GroupNorm+SiLU 2 each; conv1 and conv2: pack, channel-last copy, conv (conv2 with
         # the bias, residual ADD and SCALE in its epilogue); the 1x1 shortcut: pack, conv
-        assert st["kernels"] == 10 + (2 if shortcut else 0), st
+        # (and the channel-last copy on bf16)
+        assert st["kernels"] == 10 + ((3 if cli.bf16 else 2) if shortcut else 0), st
     sp = cli.run("ResnetBlock2D", *args, "--packed-weights", "true")
     assert np.array_equal(read_dtb(cli.out()).view(np.uint32), got.view(np.uint32))
     assert sp["kernels"] == st["kernels"] - (3 if shortcut else 2), sp
+
+
+@pytest.mark.parametrize("c", [dict(cin=8, cout=4, layers=2, groups=4, H=8, W=8, up=False),
+                               dict(cin=8, cout=4, layers=2, groups=4, H=8, W=8, up=True),
+                               dict(cin=128, cout=64, layers=3, groups=32, H=24, W=20, up=True)],
+                         ids=lambda c: f"{c['cin']}-{c['cout']}-l{c['layers']}-up{int(c['up'])}")
+def test_up_decoder_block2d(orc, cli, c):
+    """UpDecoderBlock2D.py's two cases (8 -> 4, two layers, groups 4 on
+    1x8x8x8, with and without the upsampler) and a decoder-sized block."""
+    import oracle.vae as vae
+    shapes = vae.up_decoder_block2d_param_shapes(c["cin"], c["cout"], c["layers"], c["up"])
+    wdir = os.path.join(cli.tmp, "w")
+    os.makedirs(wdir, exist_ok=True)
+    P = {}
+    for i, (name, shape) in enumerate(sorted(shapes.items())):
+        mean = 1.0 if name.endswith(("norm1.weight", "norm2.weight")) else 0.0
+        std = 0.05 if name.endswith(".weight") and "norm" not in name else 0.1
+        P[name] = orc.randn(SEED + 80 + i, shape, mean=mean, std=std)
+        write_dtb(os.path.join(wdir, name + ".dtb"), P[name], 0)
+    xp, xv = cli.act(orc.randn(SEED + 79, (1, c["cin"], c["H"], c["W"])))
+    args = ["--in_channels", c["cin"], "--out_channels", c["cout"], "--num_layers", c["layers"],
+            "--resnet_groups", c["groups"], "--add_upsample", str(c["up"]).lower(),
+            "--dtype", "bf16" if cli.bf16 else "f32", "--hidden_states", xp, "--weights", wdir, "--out", cli.out()]
+    st = cli.run("UpDecoderBlock2D", *args)
+    got = read_dtb(cli.out())
+    want = vae.up_decoder_block2d(xv, P, c["layers"], c["groups"], 1e-6, 1.0, c["up"])
+    assert got.shape == want.shape
+    assert_bf16(got, want, "UpDecoderBlock2D")
+    # per resnet: two GroupNorm folds (statistics, (mean, rstd)), conv1 and conv2 (pack,
+    # channel-last copy, conv); the first block's 1x1 shortcut (pack, conv, and the copy on
+    # bf16) and the upsampler (pack, copy, conv)
+    shortcut = c["cin"] != c["cout"]
+    assert st["kernels"] == 10 * c["layers"] + ((3 if cli.bf16 else 2) if shortcut else 0) + (3 if c["up"] else 0), st
+    sp = cli.run("UpDecoderBlock2D", *args, "--packed-weights", "true")
+    assert np.array_equal(read_dtb(cli.out()).view(np.uint32), got.view(np.uint32))
+    n_convs = 2 * c["layers"] + (1 if shortcut else 0) + (1 if c["up"] else 0)
+    assert sp["kernels"] == st["kernels"] - n_convs, sp
 
 
 def test_cli_rejects_bad_input(dev):

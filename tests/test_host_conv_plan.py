@@ -181,3 +181,24 @@ def test_groupnorm_not_folded_into_1x1_convs_or_when_wanted():
     g, n, gn, c, y = _gn_conv(affine=False, silu=False)
     roots = g.plan(outputs=[y])
     assert roots[_index(g, n)] == -1
+
+
+def test_residual_goes_to_the_3x3_conv_when_both_operands_are_convs():
+    """A block with a 1x1 conv_shortcut adds two conv outputs: the 3x3 conv2
+    takes the residual (its epilogue stages through LDS), whichever ADD
+    operand it is; the shortcut stays a conv of its own."""
+    for swap in (False, True):
+        g = Graph(device="cpu")
+        x = g.leaf(torch.zeros((1, 8, 6, 10)))
+        hin = g.leaf(torch.zeros((1, 16, 6, 10)))
+        ws, bs = g.leaf(torch.zeros((16, 8, 1, 1))), g.leaf(torch.zeros((16,)))
+        w3, b3 = g.leaf(torch.zeros((16, 16, 3, 3))), g.leaf(torch.zeros((16,)))
+        sc = g.add(g.conv_2d_direct(ws, x, p0=0, p1=0), g.reshape(bs, [1, 1, 16, 1]))
+        c3 = g.conv_2d_direct(w3, hin, p0=1, p1=1)
+        h = g.add(c3, g.reshape(b3, [1, 1, 16, 1]))
+        s = g.add(h, sc) if swap else g.add(sc, h)
+        y = g.scale(s, 1.0)
+        roots = g.plan(outputs=[y])
+        iy = _index(g, y)
+        assert [roots[_index(g, t)] for t in (c3, h, s)] == [iy] * 3, swap
+        assert roots[_index(g, sc)] == -1, swap

@@ -9,8 +9,15 @@ conv2 leaves exactly the (projected) shortcut times 1 / output_scale_factor,
 and temb acts as a per-channel offset of conv1's output -- the same as
 folding its projection into conv1's bias.
 
-Reference module restated by the function pinned here:
-  resnet_block2d  src/diffusers/models/resnet/ResnetBlock2D.inl:110-195
+UpDecoderBlock2D is checked the same way on the reference test's two cases
+(test/src/diffusers/models/unets/unet2d/UpDecoderBlock2D.py: 8 -> 4, two
+layers, groups 4 on 1x8x8x8, with and without the upsampler), and an
+upsampler conv that passes its centre tap through returns exactly the
+nearest 2x repeat of the resnets' output.
+
+Reference modules restated by the functions pinned here:
+  resnet_block2d      src/diffusers/models/resnet/ResnetBlock2D.inl:110-195
+  up_decoder_block2d  src/diffusers/models/unets/unet2d/UpDecoderBlock2D.cpp:60-74
 """
 import numpy as np
 import pytest
@@ -130,3 +137,36 @@ def test_resnet_block2d_temb_vanishes_under_per_channel_groups(orc, vae):
     c = vae.resnet_block2d(x, P, 4, 2, 1e-6, 1.0, temb)
     d = vae.resnet_block2d(x, P, 4, 2, 1e-6, 1.0, None)
     assert not np.allclose(c, d, atol=1e-3)
+
+
+@pytest.mark.parametrize("add_upsample", [False, True])
+def test_up_decoder_block2d_matches_torch(orc, vae, add_upsample):
+    shapes = vae.up_decoder_block2d_param_shapes(8, 4, 2, add_upsample)
+    P = _params(orc, shapes, 500)
+    x = orc.randn(14, (1, 8, 8, 8))
+    y = vae.up_decoder_block2d(x, P, 2, 4, 1e-6, 1.0, add_upsample)
+    h = x
+    for i in range(2):
+        sub = {k[len(f"resnets.{i}."):]: v for k, v in P.items() if k.startswith(f"resnets.{i}.")}
+        h = _torch_block(h, sub, 4, 4, 1e-6, 1.0, None)
+    if add_upsample:
+        t = torch.from_numpy(np.asarray(h, np.float64))
+        t = F.interpolate(t, scale_factor=2, mode="nearest")
+        w = torch.from_numpy(P["upsamplers.0.conv.weight"].astype(np.float64))
+        b = torch.from_numpy(P["upsamplers.0.conv.bias"].astype(np.float64))
+        h = F.conv2d(t, w, b, padding=1).numpy()
+    assert y.shape == ((1, 4, 16, 16) if add_upsample else (1, 4, 8, 8))
+    assert_fp32(y, h, tol=2e-5, what="up_decoder_block2d")
+
+
+def test_up_decoder_block2d_centre_tap_upsampler_repeats_pixels(orc, vae):
+    P = _params(orc, vae.up_decoder_block2d_param_shapes(8, 4, 1, True), 600)
+    w = np.zeros((4, 4, 3, 3), np.float32)
+    for c in range(4):
+        w[c, c, 1, 1] = 1.0
+    P["upsamplers.0.conv.weight"] = w
+    P["upsamplers.0.conv.bias"] = np.zeros(4, np.float32)
+    x = orc.randn(15, (1, 8, 5, 7))
+    y = vae.up_decoder_block2d(x, P, 1, 4, 1e-6, 1.0, True)
+    h = vae.up_decoder_block2d(x, P, 1, 4, 1e-6, 1.0, False)
+    assert np.array_equal(y, np.repeat(np.repeat(h, 2, axis=2), 2, axis=3))
