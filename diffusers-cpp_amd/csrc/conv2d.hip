@@ -427,11 +427,17 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
 // applies the nearest 2x upscale and sends out-of-image taps to a zeroed
 // 256-byte tail of the workspace) and the [128 co][K*K] weight records.  Two
 // LDS stages of 16 channels, filled one chunk ahead; four waves of
-// 64 co x 128 px (2 x 4 MFMA 32x32x16 per tap).  Each 32-byte record's two
-// 16-byte units are swapped by the DMA source for records whose bit 2 of the
-// index (pixels) or of co (weights) is set, so 8 consecutive records read
-// distinct banks.
+// 64 co x 128 px (2 x 4 MFMA 32x32x16 per tap).  The DMA source swaps each
+// 32-byte record's two 16-byte units by the rule below (kSwzBit), so
+// consecutive records read distinct banks.
 constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
+// A record's two 16-byte units are swapped when bit 3 of its pixel (or
+// output-channel) index is set.  Record r's unit u then starts at bank
+// 8 (r mod 8) + 4 (u ^ bit3(r)) of 64, so any 16 consecutive records -- the
+// 16 lanes one ds_read_b128 cycle serves -- cover all 64 banks.  (Swapping
+// on bit 2 repeated banks every 8 records: SQ_LDS_BANK_CONFLICT was half of
+// SQ_LDS_IDX_ACTIVE.)
+constexpr int kSwzBit = 3;
 // DMA lanes per X stage: 2 per record, up to the 10 x 34 records of an
 // 8 x 32 tile (the 16 x 16 tile needs 18 x 18).  Lanes past the patch read
 // the zero tail, so the count is kept to the largest patch.
@@ -683,7 +689,7 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
             const int ih = oh0 + pr - PAD, iw = ow0 + pc - PAD;
             if (ih >= 0 && ih < a.Hs && iw >= 0 && iw < a.Ws) {
                 const int sh = a.up2 ? ih >> 1 : ih, sw = a.up2 ? iw >> 1 : iw;
-                const int su = u ^ ((rec >> 2) & 1);
+                const int su = u ^ ((rec >> kSwzBit) & 1);
                 src = e.xh + (((int64_t)n * a.H + sh) * a.W + sw) * e.C16 + su * 8;
                 xstep[m] = 1;
             }
@@ -695,7 +701,7 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
     for (int m = 0; m < NW; ++m) {
         const int L = (m * 4 + wave) * 64 + lane, rec = L >> 1, u = L & 1;
         const int co = rec / KK, tap = rec - co * KK;
-        const int su = u ^ ((co >> 2) & 1);
+        const int su = u ^ ((co >> kSwzBit) & 1);
         wsrc[m] = a.w + ((int64_t)(co0 + co) * KK + tap) * e.Cp32 + su * 8;
     }
     auto issue = [&](int c0, int s) {
@@ -726,7 +732,7 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
     for (int j = 0; j < 2; ++j) {
         const int co = wco + 32 * j + lrow;
         wrec[j] = co * KK;
-        wsw[j] = (g ^ ((co >> 2) & 1)) << 4;
+        wsw[j] = (g ^ ((co >> kSwzBit) & 1)) << 4;
     }
 
     const int nch = e.C16 / kCi2;
@@ -748,7 +754,7 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int rec = pbase[i] + kh * PC + kw;
-                xf[i] = *reinterpret_cast<const bf16x8_t*>(Xs + rec * kRec2 + ((g ^ ((rec >> 2) & 1)) << 4));
+                xf[i] = *reinterpret_cast<const bf16x8_t*>(Xs + rec * kRec2 + ((g ^ ((rec >> kSwzBit) & 1)) << 4));
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j)
