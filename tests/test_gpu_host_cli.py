@@ -436,6 +436,28 @@ def test_up_decoder_block2d(orc, cli, c):
     assert sp["kernels"] == st["kernels"] - n_convs, sp
 
 
+@pytest.mark.parametrize("block", ["ResnetBlock2D", "UpDecoderBlock2D"])
+def test_decoder_blocks_under_node_order_allocation(dev, block):
+    """With node memory placed as ggml's allocator would place it (node order,
+    in place where the op allows: the residual ADD may land on its input),
+    the GroupNorm-in-copy and residual-in-epilogue folds give the same bits
+    as with the executor's own placement; the memory replay keeps apart
+    whatever the placement would break."""
+    common = ["--random-inputs", "3", "--random-weights", "4", "--height", "40", "--width", "48",
+              "--dtype", "bf16", "--packed-weights", "true"]
+    if block == "ResnetBlock2D":
+        args = ["--in_channels", "64", "--out_channels", "32", "--groups", "32"] + common
+    else:
+        args = ["--in_channels", "64", "--out_channels", "32", "--num_layers", "2", "--resnet_groups", "32"] + common
+    runs = []
+    for alloc in ("fused", "node-order"):
+        r = subprocess.run([CLI, block, *args, "--alloc", alloc], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 0, r.stderr
+        runs.append(json.loads(r.stdout.strip().splitlines()[-1]))
+    assert runs[0]["output"]["fnv64"] == runs[1]["output"]["fnv64"], runs
+    assert runs[0]["output"]["nonfinite"] == 0
+
+
 def test_cli_rejects_bad_input(dev):
     with tempfile.TemporaryDirectory() as d:
         r = subprocess.run([CLI, "NoSuchCommand"], capture_output=True, text=True, timeout=60)
