@@ -357,8 +357,11 @@ public:
         m.named_parameters(ps);
         std::mt19937_64 gen(seed);
         for (auto& p : ps) {
-            const bool norm_w = p.first.rfind("norm", 0) == 0 && p.first.size() > 7 &&
-                                p.first.compare(p.first.size() - 7, 7, ".weight") == 0;
+            // a GroupNorm weight: <prefix.>norm*.weight
+            const size_t dot = p.first.rfind('.', p.first.size() - 8);
+            const size_t leaf = dot == std::string::npos ? 0 : dot + 1;
+            const bool norm_w = p.first.size() > 7 && p.first.compare(p.first.size() - 7, 7, ".weight") == 0 &&
+                                p.first.compare(leaf, 4, "norm") == 0;
             std::normal_distribution<float> nd(norm_w ? 1.0f : 0.0f, std);
             Blob b;
             b.shape = p.second.shape();
