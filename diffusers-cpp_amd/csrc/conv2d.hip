@@ -444,6 +444,10 @@ constexpr int kSwzBit = 3;
 constexpr int kXLanesMax3 = 3 * 256;
 static_assert(2 * (8 + 2) * (32 + 2) <= kXLanesMax3 && 2 * (16 + 2) * (16 + 2) <= kXLanesMax3,
               "X DMA lanes must cover the 3x3 patch of every tile shape conv_geometry2 picks");
+// The same for the 512-pixel tiles (16 x 32, or 32 x 16 on narrow images).
+constexpr int kXLanesMax3x2 = 5 * 256;
+static_assert(2 * (16 + 2) * (32 + 2) <= kXLanesMax3x2 && 2 * (32 + 2) * (16 + 2) <= kXLanesMax3x2,
+              "X DMA lanes must cover the 3x3 patch of every 512-pixel tile");
 
 // GroupNorm applied by the channel-last copy: (mean, rstd) per (n, group),
 // the per-channel affine (or null), cg channels per group, the SiLU flag.
@@ -542,19 +546,20 @@ __device__ __forceinline__ void conv_wait_vm() {
 // residual (loaded before the LDS stage, so its latency overlaps it), the
 // ADD rounded to T, the SCALE (res_mode 2), one store.  A piece is read and
 // written by one thread only, so the output may sit on the residual.
-// The epilogue's LDS: 64 output-channel rows of 256 pixels, padded to 264
-// elements; the DMA kernel's shared array is at least this large.
-constexpr int kEpiStride = 264;
-template <typename T>
-constexpr int epi_lds_bytes() { return 64 * kEpiStride * (int)sizeof(T); }
+// The epilogue's LDS: 64 output-channel rows of the tile's 64 FN pixels,
+// padded by 8 elements; the DMA kernel's shared array is at least this large.
+template <int FN>
+constexpr int epi_stride() { return 64 * FN + 8; }
+template <typename T, int FN>
+constexpr int epi_lds_bytes() { return 64 * epi_stride<FN>() * (int)sizeof(T); }
 
-template <typename T, bool RES>
-__device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t (&acc)[2][4], uint8_t* smem,
+template <typename T, bool RES, int FN>
+__device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t (&acc)[2][FN], uint8_t* smem,
                                                int co0, int oh0, int ow0, int wco, int wpx, int lrow, int g, int lt,
                                                int n) {
     constexpr int E = Io<T>::EPV;             // elements per 16-byte piece
-    constexpr int S = kEpiStride;             // LDS row stride in elements (bank-spread rows)
-    constexpr int RP = 256 / E;               // pieces per 256-pixel row
+    constexpr int S = epi_stride<FN>();       // LDS row stride in elements (bank-spread rows)
+    constexpr int RP = 64 * FN / E;           // pieces per pixel row
     constexpr int PIECES = 64 * RP / 256;     // pieces per thread and pass
     T* lds = reinterpret_cast<T*>(smem);
     const int tid = threadIdx.x, tcm = (1 << lt) - 1;
@@ -584,7 +589,7 @@ __device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t
             }
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < FN; ++i) {
             float v[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -656,16 +661,20 @@ __device__ __forceinline__ void conv_store_lds(const ConvArgs& a, const f32x16_t
     }
 }
 
-template <typename T, int K, bool STATS, bool RES>
+// FN: 32-pixel MFMA columns per wave, 4 (a 256-pixel tile of 8 x 32) or 8
+// (512 pixels, 16 x 32, halving the weight DMA per output pixel, for convs
+// with enough tiles to fill the chip).
+template <typename T, int K, bool STATS, bool RES, int FN>
 __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const Conv2Extra e) {
     static_assert(K == 3 || K == 1, "the DMA kernel takes 3x3 and 1x1 patches");
+    static_assert(FN == 4 || (FN == 8 && !STATS && !RES), "512-pixel tiles carry no statistics or residual epilogue");
     constexpr int KK = K * K, PAD = (K - 1) / 2;
-    constexpr int XL = kXLanesMax3;  // X DMA lanes per stage
+    constexpr int XL = FN == 4 ? kXLanesMax3 : kXLanesMax3x2;  // X DMA lanes per stage
     constexpr int NX = XL / 256, NW = 2 * kTileCo * KK / 256;  // DMA instructions per wave per stage
     constexpr int XB = XL * 16, WB = kTileCo * KK * kRec2, STAGE = XB + WB;
     constexpr int QD = NX + NW;
     // the two DMA stages, then the epilogue's rows (larger for 1x1 patches)
-    constexpr int SMEM = 2 * STAGE > epi_lds_bytes<T>() ? 2 * STAGE : epi_lds_bytes<T>();
+    constexpr int SMEM = 2 * STAGE > epi_lds_bytes<T, FN>() ? 2 * STAGE : epi_lds_bytes<T, FN>();
     __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -673,7 +682,7 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
     const int th = blockIdx.x / a.tiles_w, tw = blockIdx.x - th * a.tiles_w;
     const int oh0 = th * a.TR, ow0 = tw * a.TC;
     const int PC = a.TC + K - 1, npatch = (a.TR + K - 1) * PC;
-    const int wco = (wave >> 1) * 64, wpx = (wave & 1) * 128;
+    const int wco = (wave >> 1) * 64, wpx = (wave & 1) * 32 * FN;
     const int lrow = lane & 31, g = lane >> 5;
 
     // DMA sources, fixed for the whole K loop up to the channel offset.
@@ -713,17 +722,17 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
         for (int m = 0; m < NW; ++m) dma16(wsrc[m] + c0, st + XB + (m * 4 + wave) * 64 * 16);
     };
 
-    f32x16_t acc[2][4];
+    f32x16_t acc[2][FN];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[j][i][q] = 0.f;
 
-    int pbase[4];
+    int pbase[FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < FN; ++i) {
         const int p = wpx + 32 * i + lrow;
         pbase[i] = (p >> e.lt) * PC + (p & (a.TC - 1));
     }
@@ -747,19 +756,19 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
 #pragma unroll
         for (int tap = 0; tap < KK; ++tap) {
             const int kh = tap / K, kw = tap - kh * K;
-            bf16x8_t wf[2], xf[4];
+            bf16x8_t wf[2], xf[FN];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 wf[j] = *reinterpret_cast<const bf16x8_t*>(Ws_ + (wrec[j] + tap) * kRec2 + wsw[j]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < FN; ++i) {
                 const int rec = pbase[i] + kh * PC + kw;
                 xf[i] = *reinterpret_cast<const bf16x8_t*>(Xs + rec * kRec2 + ((g ^ ((rec >> kSwzBit) & 1)) << 4));
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < FN; ++i)
                     acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
         }
         // every wave's reads of this stage are done before it is refilled
@@ -770,7 +779,7 @@ __global__ __launch_bounds__(256) void conv2d_dma_kernel(const ConvArgs a, const
 
     // The stores go through LDS (ending in a barrier, so the statistics
     // below may reuse it).
-    conv_store_lds<T, RES>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g, e.lt, n);
+    conv_store_lds<T, RES, FN>(a, acc, smem, co0, oh0, ow0, wco, wpx, lrow, g, e.lt, n);
     if constexpr (STATS) {
         float* red = reinterpret_cast<float*>(smem);
         switch (a.cg) {
@@ -849,9 +858,10 @@ int64_t nhwc_elems(int64_t N, int64_t Ci, int64_t H, int64_t W) { return N * H *
 // and 4 x 64 tiles at every decoder shape ([1,128,1024,1024] -> 128 bf16:
 // 784 / 760 / 765 us against 701 us, channel-last copy included), with the
 // same output bits.
-void conv_geometry2(int64_t Hs, int64_t Ws, int* TR, int* TC, int64_t* tiles_w, int64_t* tiles_h) {
+// px: the tile's pixels, 256 or 512 (16 x 32).
+void conv_geometry2(int64_t Hs, int64_t Ws, int px, int* TR, int* TC, int64_t* tiles_w, int64_t* tiles_h) {
     *TC = Ws >= 32 ? 32 : 16;
-    *TR = kTilePx2 / *TC;
+    *TR = px / *TC;
     *tiles_w = (Ws + *TC - 1) / *TC;
     *tiles_h = (Hs + *TR - 1) / *TR;
 }
@@ -904,7 +914,17 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
                      aligned16(ws) && (!stats || (a.cg >= 4 && a.cg <= 64));
     int64_t tiles_w, tiles_h;
     DT_REQUIRE(!gn || dma, "%s: the GroupNorm fold needs a 3x3 conv with a workspace", what);
-    if (dma) conv_geometry2(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
+    // 512-pixel tiles (half the weight DMA per output pixel) when they still
+    // give two workgroups per CU; statistics and the residual epilogue keep
+    // 256-pixel tiles (their registers would spill with 256 accumulators).
+    int fn = 4;
+    if (dma && !stats && !res_mode) {
+        int tr, tc;
+        int64_t tw, th;
+        conv_geometry2(Hs, Ws, 512, &tr, &tc, &tw, &th);
+        if (tw * th * ((Co + kTileCo - 1) / kTileCo) * N >= 512) fn = 8;
+    }
+    if (dma) conv_geometry2(Hs, Ws, 64 * fn, &a.TR, &a.TC, &tiles_w, &tiles_h);
     else conv_geometry(Hs, Ws, &a.TR, &a.TC, &tiles_w, &tiles_h);
     a.tiles_w = (int)tiles_w;
     DT_REQUIRE(tiles_h * tiles_w < (1ll << 31), "%s: too many tiles", what);
@@ -942,8 +962,13 @@ int conv_launch(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
 #undef DT_NHWC
         int rc = check_launch(what);
         if (rc) return rc;
-#define DT_CONV2_LAUNCH(TT, KS, ST, RS) \
-    hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST, RS>), grid, dim3(256), 0, st, a, e)
+#define DT_CONV2_LAUNCH(TT, KS, ST, RS)                                                                     \
+    do {                                                                                                    \
+        if (fn == 8)                                                                                        \
+            hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST, RS, ((ST || RS) ? 4 : 8)>), grid, dim3(256), 0, st, a, e); \
+        else                                                                                                \
+            hipLaunchKernelGGL((conv2d_dma_kernel<TT, KS, ST, RS, 4>), grid, dim3(256), 0, st, a, e);       \
+    } while (0)
         if (io_type == DT_TYPE_F32) {
             if (K == 1) {
                 if (stats) DT_CONV2_LAUNCH(float, 1, true, false);

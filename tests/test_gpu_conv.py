@@ -351,3 +351,22 @@ def test_groupnorm_folded_into_conv_equals_the_nodes(orc, dev, io, shape, G, co,
     if residual:
         want = (as_input(res, io) + want) * np.float32(0.5)
     check(host(fused_out), want, io, "GroupNorm + conv", one_rounding=False)
+
+
+# 512-pixel tiles (16 x 32) are taken when they still give two workgroups
+# per CU (N x tiles x output-channel tiles >= 512); these shapes reach them,
+# with a batch, a partial output-channel tile, a partial column tile and the
+# 2x upscale.
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,co,up2", [((4, 16, 256, 256), 24, False), ((1, 8, 512, 520), 16, False),
+                                          ((1, 16, 256, 256), 8, True)])
+def test_conv2d_512_pixel_tiles(orc, dev, shape, co, up2, io):
+    print(f"conv2d 512px x={shape} co={co} up2={up2} {io}", flush=True)
+    x = orc.randn(SEED + 90, shape)
+    w = orc.randn(SEED + 91, (co, shape[1], 3, 3), std=0.2)
+    b = orc.randn(SEED + 92, (co,), std=0.1)
+    wp = dit_hip.conv2d_pack(dev_tensor(w, torch.float32))
+    y = dit_hip.conv2d(dev_tensor(x, io), wp, bias=dev_tensor(b, torch.float32), upscale2=up2, workspace=True)
+    torch.cuda.synchronize()
+    ref = orc.conv2d(orc.round_bf16(as_input(x, io)), orc.round_bf16(w), b, up2=up2)
+    check(host(y), ref, io, f"conv2d 512px {shape} -> {co}")
