@@ -247,7 +247,8 @@ def _residual_graph(x, w, b, res, scale, io, alias):
 @pytest.mark.parametrize("shape,co,k,scale,alias", [((1, 24, 9, 13), 40, 3, 0.5, False),
                                                     ((1, 64, 16, 20), 64, 3, 1.0, True),
                                                     ((2, 32, 7, 70), 48, 1, 1.0 / 3.0, False),
-                                                    ((1, 128, 32, 32), 128, 3, 0.7, True)])
+                                                    ((1, 128, 32, 32), 128, 3, 0.7, True),
+                                                    ((4, 16, 256, 256), 24, 3, 0.5, True)])  # a batch, in place
 def test_conv_residual_epilogue_equals_the_nodes(orc, dev, io, shape, co, k, scale, alias):
     """The fused conv + bias + ADD + SCALE launch stores the bits the nodes
     store when run one by one (conv + bias, ADD, SCALE: conv2's output kept
