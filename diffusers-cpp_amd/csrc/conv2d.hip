@@ -415,21 +415,23 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
     }
 }
 
-// ---- with a workspace (3x3): channel-last input, direct global -> LDS DMA ---
-// Measured on gfx950 (bf16, 3x3, Co = Ci): [1,512,128,128] 463, [1,512,256,256]
-// 474, [1,256,512,512] 385, [1,128,1024,1024] 288 TFLOP/s, and 610 on the
-// 2x upscale of [1,512,128,128]; the register-staged kernel 99-125.
+// ---- with a workspace (3x3; 1x1 on bf16): channel-last input, direct
+// global -> LDS DMA.  Measured on gfx950 (bf16, 3x3, Co = Ci, channel-last
+// copy included): [1,512,128,128] 693, [1,512,256,256] 846, [1,256,512,512]
+// 674, [1,128,1024,1024] 497 TFLOP/s; the register-staged kernel 99-125.
 // The input is first transposed to bf16 NHWC with channels zero-padded to a
-// multiple of 16 (to_nhwc16_kernel, one bandwidth-bound pass), so a 16-channel
-// slice of one pixel is a contiguous 32-byte record and both operands stream
-// into LDS by global_load_lds with no per-element work: the input patch of a
-// 256-pixel tile (every lane computes its own source pixel, which also
+// multiple of 16 (to_nhwc16_kernel, one bandwidth-bound pass, which can also
+// apply a GroupNorm + SiLU), so a 16-channel slice of one pixel is a
+// contiguous 32-byte record and both operands stream into LDS by
+// global_load_lds with no per-element work: the input patch of a 256- or
+// 512-pixel tile (every lane computes its own source pixel, which also
 // applies the nearest 2x upscale and sends out-of-image taps to a zeroed
 // 256-byte tail of the workspace) and the [128 co][K*K] weight records.  Two
-// LDS stages of 16 channels, filled one chunk ahead; four waves of
-// 64 co x 128 px (2 x 4 MFMA 32x32x16 per tap).  The DMA source swaps each
+// LDS stages of 16 channels, filled one chunk ahead; four waves of 64 co x
+// 32 FN px (2 x FN MFMA 32x32x16 per tap).  The DMA source swaps each
 // 32-byte record's two 16-byte units by the rule below (kSwzBit), so
-// consecutive records read distinct banks.
+// consecutive records read distinct banks.  The output leaves through LDS
+// (conv_store_lds).
 constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
 // A record's two 16-byte units are swapped when bit 3 of its pixel (or
 // output-channel) index is set.  Record r's unit u then starts at bank
