@@ -233,7 +233,11 @@ def probe_kernels(t):
     }
 
 
-def copy_ceiling(torch, dev, flush):
+def cold_torch_copy(torch, dev, flush):
+    """One 256 MiB torch device copy, timed as single cold launches after a
+    cache flush (dispatch latency included): a calibration figure for the
+    cold-launch columns, not a streaming ceiling (the ceilings at the path's
+    byte shapes come from the back-to-back ceiling sweep)."""
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     src.fill_(1)
@@ -595,11 +599,9 @@ def denoise_step(steps, warmup, weight_format="bf16", hip_graph=True):
                     "Q8_0 (N(0,0.02) quantised on device) kept as Q8_0 (codes + fp32 scales, 1.125 B/weight)")
                    + "; RMSNorm weights N(1,0.02)",
         "linear_weight_bytes": res["linear_weight_bytes"],
-        "gemm": {"hipblaslt": "hipBLASLt" + (" on each Q8_0 weight expanded to bf16 just before its GEMM"
-                                             if weight_format == "q8_0" else ""),
-                 "mfma": "the library's MFMA GEMM" + (" with the Q8_0 dequantisation in its load path"
-                                                      if weight_format == "q8_0" else "")}.get(res.get("gemm"),
-                                                                                               res.get("gemm")),
+        "gemm": ("hand-written bf16 MFMA GEMM (diffusers-cpp_amd/csrc/gemm.hip"
+                 + (", gemm_q8_kernel: Q8_0 dequantised in its load path)" if weight_format == "q8_0" else ")")
+                 if res.get("gemm") == "mfma" else res.get("gemm")),
         "launch": "one HIP graph replay per step" if hip_graph else "eager launches after the fusion pass",
         "s_per_step": round(t, 5),
         "ms_per_step_min": res["ms_per_step_min"],
@@ -655,7 +657,7 @@ def main():
             print(json.dumps({"vae": vae_measurements(torch, dev, flush)}), flush=True)
         else:
             print(json.dumps({"secondary": secondary(torch, dev, flush),
-                              "copy_ceiling_GBs": round(copy_ceiling(torch, dev, flush), 1)}), flush=True)
+                              "cold_torch_copy_GBs": round(cold_torch_copy(torch, dev, flush), 1)}), flush=True)
         return
 
     # The CPU baselines of the other workloads run before this process
@@ -669,8 +671,8 @@ def main():
     denoise_q8 = (denoise_step(args.denoise_steps, args.denoise_warmup, "q8_0")
                   if args.denoise_steps > 0 and args.secondary else None)
     # The three runs compute the same step on the same weights and inputs:
-    # graph replay, eager launches and Q8_0 weights (expanded to the same
-    # bf16 values per GEMM) must agree bit for bit.
+    # graph replay, eager launches and Q8_0 weights (dequantised in the
+    # GEMM's load path to the same bf16 values) must agree bit for bit.
     ref_hash = denoise["output"]["fnv64"] if denoise else None
     for name, other in (("eager launches", denoise_eager), ("Q8_0 weights", denoise_q8)):
         if other and other["output"]["fnv64"] != ref_hash:
@@ -811,7 +813,7 @@ def main():
         ts = time_stream(torch, [c[name] for c in singles], 40 * NSETS)
         kernels_standalone[name]["us_stream_mean"] = round(ts * 1e6, 2)
         kernels_standalone[name]["frac_hbm_stream"] = round(single_ab[name] / ts / 1e9 / HBM_PEAK_GBS, 4)
-    ceiling = copy_ceiling(torch, dev, flush)
+    cold_copy = cold_torch_copy(torch, dev, flush)
     extra = secondary(torch, dev, flush) if args.secondary else None
     if extra is not None:
         extra["vae"] = vae_measurements(torch, dev, flush)
@@ -871,7 +873,7 @@ def main():
         "denoise_step": denoise,
         "denoise_step_q8_0_weights": denoise_q8,
         "denoise_step_eager_launches": denoise_eager,
-        "copy_ceiling_GBs": round(ceiling, 1),
+        "cold_torch_copy_GBs": round(cold_copy, 1),
         "stream_probe_ms_per_step": round(probe_s * 1e3, 4),
         "stream_probe_GBs": round(total / probe_s / 1e9, 1),
         "frac_of_stream_probe": round(probe_s / step_s, 4),

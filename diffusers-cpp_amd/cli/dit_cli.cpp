@@ -273,12 +273,6 @@ public:
         const std::string alloc = a.str("alloc", "fused");
         if (alloc == "node-order") rt.set_allocation(HipRuntime::Allocation::NodeOrder);
         else if (alloc != "fused") throw std::runtime_error("--alloc must be fused or node-order");
-        // --gemm hipblaslt|mfma: who runs MUL_MATs with bf16 weights (dt_backend_set_gemm)
-        const std::string gemm = a.str("gemm", "hipblaslt");
-        if (gemm != "hipblaslt" && gemm != "mfma") throw std::runtime_error("--gemm must be hipblaslt or mfma");
-        if (!plan_only)
-            check(dt_backend_set_gemm(rt.backend(), gemm == "mfma" ? DT_GEMM_MFMA : DT_GEMM_HIPBLASLT),
-                  "dt_backend_set_gemm");
     }
 
     Tensor input(const std::string& key) {
@@ -759,7 +753,7 @@ void run_model(Session& s, const Args& a) {
                 steps, warmup, sorted.empty() ? 0.0 : sorted[sorted.size() / 2], mean,
                 sorted.empty() ? 0.0 : sorted.front(), st.nodes, st.kernels, st.fused_nodes, st.arena_bytes,
                 n_params, format.c_str(), resident_bytes, q8_bytes, replay ? "true" : "false",
-                a.str("alloc", "fused").c_str(), a.str("gemm", "hipblaslt").c_str(), st.launches_held,
+                a.str("alloc", "fused").c_str(), "mfma", st.launches_held,
                 output_json(oc).c_str(), gguf_note.c_str());
     std::fflush(stdout);
     if (oc.nonfinite)

@@ -15,7 +15,6 @@
 
 #include "capi_util.hpp"
 #include "dit_hip.h"
-#include "gemm_lib.hpp"
 #include "kernels.hpp"
 
 namespace dit {
@@ -66,9 +65,7 @@ struct dt_backend {
     int rope_axis_dim;
     float rope_base;
     bool own_stream;    // created by dt_graph_capture
-    uint64_t generation;  // bumped whenever scratch, rope_table or the hipBLASLt state move
-    int32_t gemm_provider;  // DT_GEMM_HIPBLASLT or DT_GEMM_MFMA
-    dit::LtState* lt;       // hipBLASLt handle, workspace and per-shape plans (first use)
+    uint64_t generation;  // bumped whenever scratch or rope_table move
 };
 
 struct dt_graph_exec {
@@ -96,8 +93,7 @@ extern "C" int dt_backend_init(int32_t device_ordinal, dt_backend** out) {
     void* noalloc = nullptr;  // dt_groupnorm_silu_noalloc's device scratch, resolved for this device now
     const int rc = dit::noalloc_scratch(&noalloc);
     if (rc) return rc;
-    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f, false, 0, DT_GEMM_HIPBLASLT,
-                              nullptr};
+    auto* be = new dt_backend{device_ordinal, nullptr, nullptr, 0, nullptr, 0, 0.f, false, 0};
     *out = be;
     return DT_OK;
 }
@@ -109,11 +105,6 @@ extern "C" int dt_backend_free(dt_backend* be) {
         (void)hipStreamSynchronize(be->stream);
         if (be->scratch) (void)hipFree(be->scratch);
         if (be->rope_table) (void)hipFree(be->rope_table);
-    }
-    if (be->lt) {
-        (void)hipSetDevice(be->device);
-        (void)hipStreamSynchronize(be->stream);
-        dit::lt_destroy(be->lt);
     }
     if (be->own_stream) {
         (void)hipStreamSynchronize(be->stream);
@@ -266,21 +257,6 @@ int backend_rope_table(dt_backend* be, int axis_dim, float freq_base, const floa
     return DT_OK;
 }
 
-int backend_gemm_provider(dt_backend* be) { return be ? be->gemm_provider : DT_GEMM_MFMA; }
-
-int backend_lib_gemm(dt_backend* be, const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
-                     int64_t M, int64_t N, int64_t K, const void* addend, int64_t ldd, int32_t out_type) {
-    DT_REQUIRE(be != nullptr, "backend_lib_gemm: null backend");
-    if (!be->lt) {
-        int rc = lt_refuse_under_capture(be->stream, "hipBLASLt: the backend's first GEMM");
-        if (rc) return rc;
-        rc = lt_create(&be->lt);
-        if (rc) return rc;
-        ++be->generation;  // a capture that made the state must not be kept
-    }
-    return lt_gemm(be->lt, be->stream, A, lda, B, ldb, C, ldc, M, N, K, addend, ldd, out_type);
-}
-
 int backend_scratch(dt_backend* be, size_t bytes, void** out) {
     DT_REQUIRE(be != nullptr && out != nullptr, "backend_scratch: null argument");
     if (bytes > be->scratch_bytes) {
@@ -301,14 +277,6 @@ int backend_scratch(dt_backend* be, size_t bytes, void** out) {
 }
 
 }  // namespace dit
-
-extern "C" int dt_backend_set_gemm(dt_backend* be, int32_t provider) {
-    DT_REQUIRE(be != nullptr, "dt_backend_set_gemm: null backend");
-    DT_REQUIRE(provider == DT_GEMM_HIPBLASLT || provider == DT_GEMM_MFMA, "dt_backend_set_gemm: provider %d",
-               provider);
-    be->gemm_provider = provider;
-    return DT_OK;
-}
 
 extern "C" int dt_graph_capture(dt_backend* be, dt_tensor** nodes, int32_t n_nodes, dt_graph_exec** out) {
     return dt_graph_capture_ex(be, nodes, n_nodes, 0, out);

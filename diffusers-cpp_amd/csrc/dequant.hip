@@ -436,105 +436,7 @@ __global__ __launch_bounds__(256) void q8_0_split_kernel(const uint8_t* __restri
     scales[(int64_t)blk * ld_scales + r] = f16_bits_to_f32(h[0]);
 }
 
-// The bf16 values of a DT_TYPE_Q8_0_SPLIT weight (codes q + 128 [N][ld_codes
-// = K], scales [K/32][ld_scales]): w[n][k] = d * q rounded to bf16 -- d * q
-// is exact in fp32 (11-bit x 8-bit significands), so these are dt_dequant's
-// and the Q8_0 GEMM's operand values.  One thread per 16 outputs of a row
-// (one 16-byte load of codes, streamed: they are read once); default-policy
-// stores, since the GEMM that follows reads them at once.
-__global__ __launch_bounds__(256) void q8_split_to_bf16_kernel(const uint8_t* __restrict__ codes,
-                                                               const float* __restrict__ scales,
-                                                               int64_t ld_scales, uint32_t total, FastDiv chunks,
-                                                               int64_t K, bf16* __restrict__ out) {
-    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total) return;
-    const uint32_t n = fdiv(idx, chunks);
-    const uint32_t k0 = (idx - n * chunks.d) * 16;
-    const uint4 c = ld_stream(codes + (int64_t)n * K + k0);
-    const float d = scales[(int64_t)(k0 >> 5) * ld_scales + n];
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    uint32_t pk[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = mul_rn(d, (float)((int)((w[j] >> (8 * i)) & 0xFF) - 128));
-        pk[2 * j] = pack_bf16x2(v[0], v[1]);
-        pk[2 * j + 1] = pack_bf16x2(v[2], v[3]);
-    }
-    uint4* o = reinterpret_cast<uint4*>(out + (int64_t)n * K + k0);
-    o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-}
-
-// The same values over tiles of 16 rows x 256 codes.  The scales are stored
-// [K/32][ld_scales], so one row's scales are ld_scales floats apart: a wave of
-// the kernel above reads its 32 scales from 32 cache lines.  Here the tile's
-// 8 x 16 scales arrive as 8 runs of 16 consecutive floats through LDS.  Each
-// thread expands two 8-code pieces of one row, 128 codes apart, so each store
-// instruction writes 16 lanes of 16 contiguous bytes per row (256-byte runs).
-// Measured on 3072 x 3072 .. 3072 x 12288, back to back: 0.49-0.68 of
-// 8 TB/s against 0.36-0.49 for the kernel above.  The same tiles with 16
-// codes per thread (two 16-byte stores 32 bytes apart per lane) reached
-// 0.42-0.58, as did tiles of 8 x 512 .. 2 x 2048 codes or 2-4 runs per thread.
-constexpr int kQ8TileRows = 16, kQ8TileRun = 256;
-
-__global__ __launch_bounds__(256) void q8_split_to_bf16_tiled_kernel(const uint8_t* __restrict__ codes,
-                                                                     const float* __restrict__ scales,
-                                                                     int64_t ld_scales, int64_t K,
-                                                                     bf16* __restrict__ out) {
-    static_assert(kQ8TileRows == 16 && kQ8TileRun == 16 * 16, "the index arithmetic assumes 16 x 256 tiles");
-    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-    __shared__ float sd[kQ8TileRun / 32][kQ8TileRows];
-    const int t = threadIdx.x;
-    const int64_t n0 = (int64_t)blockIdx.y * kQ8TileRows, k0 = (int64_t)blockIdx.x * kQ8TileRun;
-    if (t < (kQ8TileRun / 32) * kQ8TileRows)
-        sd[t >> 4][t & 15] = scales[(k0 / 32 + (t >> 4)) * ld_scales + n0 + (t & 15)];
-    const int row = t >> 4, c = t & 15;
-    const int64_t base = (n0 + row) * K + k0;
-    // pieces h = 0, 1: codes [128 h + 8 c, + 8), k-block 4 h + c / 4
-    u32x2 pc[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-        pc[h] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(codes + base + 128 * h + 8 * c));
-    __syncthreads();
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const float d = sd[4 * h + (c >> 2)][row];
-        uint32_t pk[4];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = mul_rn(d, (float)((int)((pc[h][j] >> (8 * i)) & 0xFF) - 128));
-            pk[2 * j] = pack_bf16x2(v[0], v[1]);
-            pk[2 * j + 1] = pack_bf16x2(v[2], v[3]);
-        }
-        *reinterpret_cast<uint4*>(out + base + 128 * h + 8 * c) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    }
-}
-
 }  // namespace
-
-int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, int64_t N, int64_t K, void* out,
-                     hipStream_t st) {
-    DT_REQUIRE(N >= 0 && K > 0 && K % 32 == 0 && ld_scales >= N, "q8_split_to_bf16: bad shape");
-    if (N == 0) return DT_OK;
-    DT_REQUIRE(codes && scales && out && aligned16(out) && aligned16(codes),
-               "q8_split_to_bf16: null or misaligned pointer");
-    if (N % kQ8TileRows == 0 && K % kQ8TileRun == 0 && N / kQ8TileRows < 65536 && K / kQ8TileRun < (1ll << 31)) {
-        const dim3 grid((unsigned)(K / kQ8TileRun), (unsigned)(N / kQ8TileRows));
-        hipLaunchKernelGGL(q8_split_to_bf16_tiled_kernel, grid, dim3(256), 0, st, (const uint8_t*)codes, scales,
-                           ld_scales, K, (bf16*)out);
-        return check_launch("q8_split_to_bf16");
-    }
-    const int64_t total = N * (K / 16);
-    DT_REQUIRE(total < (1ll << 31), "q8_split_to_bf16: %lld chunks exceed 2^31", (long long)total);
-    hipLaunchKernelGGL(q8_split_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
-                       (const uint8_t*)codes, scales, ld_scales, (uint32_t)total, make_fastdiv((uint32_t)(K / 16)),
-                       K, (bf16*)out);
-    return check_launch("q8_split_to_bf16");
-}
 
 }  // namespace dit
 

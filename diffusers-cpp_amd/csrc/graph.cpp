@@ -791,31 +791,6 @@ bool match_gemm_add(Graph& g, const dt_tensor* a, Plan& p) {
 constexpr const char* kMulMatOperands =
     "dt_graph_compute: MUL_MAT needs BF16 or whole Q8_0_SPLIT weight rows and BF16 activation rows";
 
-// MUL_MATs go to the backend's provider: hipBLASLt (the vendor library for
-// plain GEMMs) or the library's MFMA GEMMs.
-bool lib_gemm(dt_backend* be) { return backend_gemm_provider(be) == DT_GEMM_HIPBLASLT; }
-
-// One MUL_MAT through hipBLASLt.  A Q8_0_SPLIT weight is first expanded to
-// its bf16 values (those of dt_dequant and the Q8_0 GEMM) in the backend's
-// scratch, so the product equals the bf16-copy path's bit for bit while only
-// the 1.125-byte weights stay resident.
-int lib_mul_mat(dt_backend* be, const GemmArgs& g, void* C, int64_t ldc, const void* addend, int64_t ldd,
-                int32_t type) {
-    const void* w = g.b;
-    int64_t ldw = g.ldb;
-    if (g.bs) {
-        void* buf = nullptr;
-        int rc = backend_scratch(be, (size_t)g.N * g.K * 2, &buf);
-        if (rc) return rc;
-        rc = q8_split_to_bf16(g.b, g.bs, g.ldbs, g.N, g.K, buf, backend_stream(be));
-        if (rc) return rc;
-        ++g_kernels;
-        w = buf;
-        ldw = g.K;
-    }
-    return backend_lib_gemm(be, g.a, g.lda, w, ldw, C, ldc, g.M, g.N, g.K, addend, ldd, type);
-}
-
 int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
     hipStream_t st = backend_stream(be);
     GemmArgs g;
@@ -823,7 +798,6 @@ int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const
     DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
     DT_REQUIRE(out_rows(out, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
     if (addend) DT_REQUIRE(out_rows(addend, g.N, &ldd), "dt_graph_compute: bad GEMM addend");
-    if (lib_gemm(be)) return lib_mul_mat(be, g, out->data, ldc, addend ? addend->data : nullptr, ldd, out->type);
     if (g.bs)
         return dt_gemm_q8_0(g.a, g.lda, g.b, g.ldb, g.bs, g.ldbs, out->data, ldc, g.M, g.N, g.K, nullptr,
                             addend ? addend->data : nullptr, ldd, out->type, st);
@@ -842,9 +816,8 @@ const void* data_of(const dt_tensor* t) {
     return t && t->data ? (const char*)t->data + off : nullptr;
 }
 
-// Independent MUL_MATs at one position: one grouped MFMA launch, or one
-// hipBLASLt call each (its single calls beat the grouped MFMA launch: the
-// single-stream block's five projections 0.62 against 0.82 ms).
+// Independent MUL_MATs at one position: one grouped MFMA launch, whose
+// tiles share the grid.
 int run_gemm_group(dt_backend* be, const std::vector<const dt_tensor*>& members) {
     hipStream_t st = backend_stream(be);
     dt_gemm_problem ps[8];
@@ -863,13 +836,7 @@ int run_gemm_group(dt_backend* be, const std::vector<const dt_tensor*>& members)
         ps[i] = dt_gemm_problem{g.a, g.lda, g.b, g.ldb, mm->data, ldc, nullptr, 0, nullptr, g.M, g.N, g.K, g.bs,
                                 g.ldbs};
     }
-    if (!lib_gemm(be)) return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
-    for (int i = 0; i < n; ++i) {
-        const int rc = lib_mul_mat(be, gs[i], ps[i].C, ps[i].ldc, nullptr, 0, members[0]->type);
-        if (rc) return rc;
-    }
-    g_kernels += n - 1;
-    return DT_OK;
+    return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
 }
 
 // Forward pass over unfused MUL_MATs: node i starts a group of the MUL_MATs

@@ -132,16 +132,4 @@ int conv2d_fold(const void* x, int64_t N, int64_t Ci, int64_t H, int64_t W, cons
 int gn_mean_rstd(const void* x, int64_t N, int64_t C, int64_t HW, int64_t groups, float eps, void* workspace,
                  float2* mr, int32_t io_type, hipStream_t st);
 
-// The bf16 values of a DT_TYPE_Q8_0_SPLIT weight [N][K] (codes, then scales
-// [K/32][ld_scales]) into out [N][K] (dequant.hip).
-int q8_split_to_bf16(const void* codes, const float* scales, int64_t ld_scales, int64_t N, int64_t K, void* out,
-                     hipStream_t st);
-
-// The backend's GEMM provider (DT_GEMM_HIPBLASLT or DT_GEMM_MFMA), and a
-// plain bf16 GEMM through its hipBLASLt state (made on first use; that
-// counts as a scratch move for captured graphs).
-int backend_gemm_provider(dt_backend* be);
-int backend_lib_gemm(dt_backend* be, const void* A, int64_t lda, const void* B, int64_t ldb, void* C, int64_t ldc,
-                     int64_t M, int64_t N, int64_t K, const void* addend, int64_t ldd, int32_t out_type);
-
 }  // namespace dit

@@ -18,7 +18,6 @@ LIB_PATH = os.path.join(_HERE, "lib", "libdit_hip.so")
 
 # ggml type ids
 F32, F16, Q8_0, Q4_K, I32, BF16 = 0, 1, 8, 12, 26, 30
-GEMM_HIPBLASLT, GEMM_MFMA = 0, 1
 
 # dt_tensor.op ids
 (OP_NONE, OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_SCALE, OP_SIGMOID, OP_NORM, OP_RMS_NORM,
@@ -115,7 +114,6 @@ _SIGS = {
                                         c_void_p, c_int64, c_int32, c_int32, c_float, c_void_p, c_int32,
                                         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                         c_int64, _I64P, _I64P, _I64P, c_float, c_int32, _S]),
-    "dt_backend_set_gemm": (c_int32, [c_void_p, c_int32]),
     "dt_graph_capture": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32, POINTER(c_void_p)]),
     "dt_graph_capture_ex": (c_int32, [c_void_p, POINTER(POINTER(DtTensor)), c_int32, c_uint32, POINTER(c_void_p)]),
     "dt_graph_exec_launch": (c_int32, [c_void_p, c_void_p]),

@@ -21,7 +21,7 @@
  *  - Every pointer named x/y/src/dst/... is DEVICE memory owned by the
  *    caller; the library allocates device memory only in dt_buffer_alloc
  *    and for a dt_backend's own state, made by its first dt_graph_compute
- *    that needs it (scratch, RoPE table, hipBLASLt handle and workspace)
+ *    that needs it (scratch and RoPE table)
  *    and freed by dt_backend_free.
  *  - `stream` is a hipStream_t (NULL = the default stream).  All kernels are
  *    stream-ordered and asynchronous; none synchronises the device.
@@ -29,8 +29,8 @@
  *  - Every function returns 0 (DT_OK) or a DT_ERR_* code and never aborts;
  *    dt_last_error() returns a thread-local message for the last failure.
  *  - Threads: the kernel entry points ((ii), (iii)) keep no state and may be
- *    called from any thread.  A dt_backend (its scratch, RoPE table and
- *    hipBLASLt plans) and the nodes given to its dt_graph_* calls are used
+ *    called from any thread.  A dt_backend (its scratch and RoPE table)
+ *    and the nodes given to its dt_graph_* calls are used
  *    by one host thread at a time, as the reference builds and computes a
  *    graph on the thread whose Scope holds it (thread_local,
  *    src/ggml/Scope.hpp:74-75); separate backends may run on separate
@@ -476,21 +476,6 @@ int dt_backend_free(dt_backend *be);
  * caller's stream is never destroyed by the library. */
 int dt_backend_set_stream(dt_backend *be, dt_stream_t stream);
 int dt_backend_synchronize(dt_backend *be);
-/* Which GEMM runs dt_graph_compute's MUL_MATs (no counterpart in the
- * reference, whose ggml backend picks its own kernels): DT_GEMM_HIPBLASLT
- * (the default) calls hipBLASLt, with one handle, a 32 MiB workspace and
- * per-shape algorithms kept by the backend from the first compute on (so
- * run dt_graph_compute once before dt_graph_capture; a capture that reaches
- * a GEMM shape no eager compute has run fails);
- * a Q8_0_SPLIT weight is expanded to its bf16 values (dt_dequant's) in the
- * backend's scratch just before its call, so it gives the bf16-copy path's
- * result bit for bit.  DT_GEMM_MFMA runs the library's own MFMA GEMMs
- * (dt_gemm_bf16 / dt_gemm_bf16_grouped; dt_gemm_q8_0 for Q8_0_SPLIT
- * weights, which equals dt_dequant + dt_gemm_bf16 bit for bit).  The two
- * providers accumulate in different orders: results agree to fp32 rounding
- * before the output's own rounding. */
-enum { DT_GEMM_HIPBLASLT = 0, DT_GEMM_MFMA = 1 };
-int dt_backend_set_gemm(dt_backend *be, int32_t provider);
 int dt_buffer_alloc(dt_backend *be, size_t bytes, void **out);
 int dt_buffer_free(dt_backend *be, void *ptr);
 /* ggml_backend_tensor_set / get: n bytes at byte offset of a contiguous
@@ -585,10 +570,9 @@ int dt_graph_last_stats_ex(int32_t *kernels_launched, int32_t *nodes_fused, int3
  * instead of the fusion pass plus a launch per kernel (the role of the
  * reference's repeated ggml_backend_graph_compute, ExecutionRuntime.cpp:227,
  * 254).  Call dt_graph_compute on the same nodes once first, so the
- * backend's scratch and RoPE table, and with DT_GEMM_HIPBLASLT its
- * hipBLASLt handle and each GEMM shape's plan, exist (capture allocates
- * nothing; a capture that would make hipBLASLt state fails with
- * DT_ERR_INVALID_ARG and records nothing).  The
+ * backend's scratch and RoPE table exist (capture allocates nothing; a
+ * capture that would (re)allocate them fails with DT_ERR_INVALID_ARG and
+ * keeps nothing).  The
  * replay reads and writes the node data pointers given at capture: inputs
  * are updated in place between replays.  A backend on the NULL stream gets
  * a stream of its own (default priority), used from then on.  The graph

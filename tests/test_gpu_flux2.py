@@ -211,12 +211,11 @@ def test_model_small_hip_graph(orc, tmp):
 
 def test_model_small_q8_0_weights(orc, tmp):
     """The same model with --weight-format q8_0: every Linear weight is
-    quantised to Q8_0 on the device and repacked (DT_TYPE_Q8_0_SPLIT); the
-    hipBLASLt provider expands each to its bf16 values per GEMM, the MFMA
-    provider dequantises inside its GEMM.  With either provider the output
-    equals, bit for bit, the bf16 path with the same provider run on the
-    oracle's bf16 rounding of dequantize(quantize(W)), and is held to the
-    bf16 bar against the oracle's fp32 model on those weights."""
+    quantised to Q8_0 on the device and repacked (DT_TYPE_Q8_0_SPLIT), and
+    the MFMA GEMM dequantises inside its load path.  The output equals, bit
+    for bit, the bf16 path run on the oracle's bf16 rounding of
+    dequantize(quantize(W)), and is held to the bf16 bar against the
+    oracle's fp32 model on those weights."""
     import oracle.flux2 as of
     cfg = SMALL_MODEL
     P = make_params(orc, of.model_param_shapes(cfg), 5000)
@@ -232,16 +231,15 @@ def test_model_small_q8_0_weights(orc, tmp):
     qdir = os.path.join(tmp, "dequantized")
     os.makedirs(qdir)
     wq, wb = write_params(tmp, P), write_params(qdir, Pq)
-    for gemm in ("hipblaslt", "mfma"):
-        oq, ob = os.path.join(tmp, f"oq_{gemm}.dtb"), os.path.join(tmp, f"ob_{gemm}.dtb")
-        sq = _run_small_model(f, wq, oq, n_img, n_txt, "--weight-format", "q8_0", "--gemm", gemm)
-        print(f"  {sq}", flush=True)
-        assert sq["weight_format"] == "q8_0"
-        sb = _run_small_model(f, wb, ob, n_img, n_txt, "--gemm", gemm)
-        assert sb["weight_format"] == "bf16"
-        got_q, got_b = read_dtb(oq), read_dtb(ob)
-        assert np.array_equal(got_q.view(np.uint32), got_b.view(np.uint32)), \
-            f"Q8_0 path ({gemm}) differs from bf16 on dequantised weights: max |d| {np.abs(got_q - got_b).max()}"
+    oq, ob = os.path.join(tmp, "oq.dtb"), os.path.join(tmp, "ob.dtb")
+    sq = _run_small_model(f, wq, oq, n_img, n_txt, "--weight-format", "q8_0")
+    print(f"  {sq}", flush=True)
+    assert sq["weight_format"] == "q8_0"
+    sb = _run_small_model(f, wb, ob, n_img, n_txt)
+    assert sb["weight_format"] == "bf16"
+    got_q, got_b = read_dtb(oq), read_dtb(ob)
+    assert np.array_equal(got_q.view(np.uint32), got_b.view(np.uint32)), \
+        f"Q8_0 path differs from bf16 on dequantised weights: max |d| {np.abs(got_q - got_b).max()}"
     want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], Pq, cfg)
     check(got_q.reshape(n_img, 128), want, "model 1+2 blocks, Q8_0 weights")
 

@@ -10,11 +10,8 @@ that do not depend on size:
   - the output is finite, and its spread is what the random weights give:
     proj_out has 3072 inputs of unit-variance rows times N(0, 0.02) weights,
     std ~ 0.02 * sqrt(3072) = 1.11 (band 0.7 .. 1.6);
-  - keeping the weights as Q8_0 gives the bf16 copy path's output bit for
-    bit with either GEMM provider: hipBLASLt (the default) on the weights
-    expanded to bf16 per GEMM, or the library's MFMA GEMM with the
-    dequantisation in its load path (--gemm mfma); the two providers
-    accumulate in different orders, and their steps agree to rounding;
+  - keeping the weights as Q8_0 (the MFMA GEMM dequantises them in its load
+    path) gives the bf16 copy path's output bit for bit;
   - replaying the step as a HIP graph gives the eager output bit for bit;
   - node memory placed as ggml_gallocr places it (node order), with the
     executor holding back the launches that would read reused memory, stays
@@ -58,7 +55,8 @@ def step(tag, *extra):
 
 
 def test_full_step_output_is_finite_with_the_expected_spread():
-    st, o = step("bf16", "--gemm", "hipblaslt")
+    st, o = step("bf16")
+    assert st["gemm"] == "mfma"
     assert o.shape == (1, 4096, 128)
     out = st["output"]
     assert out["elements"] == 4096 * 128 and out["nonfinite"] == 0
@@ -67,31 +65,16 @@ def test_full_step_output_is_finite_with_the_expected_spread():
     assert abs(float(np.std(o.astype(np.float64))) - out["std"]) < 1e-3 * out["std"]
 
 
-@pytest.mark.parametrize("gemm", ["hipblaslt", "mfma"])
-def test_full_step_q8_0_weights_equal_bf16_copies_bit_for_bit(gemm):
-    sb, ob = step("bf16" if gemm == "hipblaslt" else "mfma", "--gemm", gemm)
-    sq, oq = step("q8_0 " + gemm, "--weight-format", "q8_0", "--gemm", gemm)
-    assert sq["weight_format"] == "q8_0" and sb["gemm"] == sq["gemm"] == gemm
+def test_full_step_q8_0_weights_equal_bf16_copies_bit_for_bit():
+    sb, ob = step("bf16")
+    sq, oq = step("q8_0", "--weight-format", "q8_0")
+    assert sq["weight_format"] == "q8_0" and sb["gemm"] == sq["gemm"] == "mfma"
     assert sq["output"]["fnv64"] == sb["output"]["fnv64"]
     assert np.array_equal(oq.view(np.uint32), ob.view(np.uint32))
 
 
-def test_full_step_hipblaslt_and_mfma_gemms_agree():
-    """The default GEMM provider (hipBLASLt) against the library's MFMA GEMM
-    on the same weights: the products differ only in accumulation order
-    (fp32 rounding), which 25 blocks of bf16 activations carry to the output
-    as rounding noise (the same order as the node-order placement's, whose
-    parity with the oracle is held at full depth below)."""
-    sb, ob = step("bf16", "--gemm", "hipblaslt")
-    sm, om = step("mfma", "--gemm", "mfma")
-    assert sb["gemm"] == "hipblaslt" and sb["output"]["nonfinite"] == 0
-    rel, cos = bf16_metrics(ob, om)
-    print(f"  hipBLASLt vs MFMA GEMMs: rel_l2={rel:.3e} cos={cos:.7f}", flush=True)
-    assert cos >= 0.999
-
-
 def test_full_step_hip_graph_replay_equals_eager_bit_for_bit():
-    sb, ob = step("bf16", "--gemm", "hipblaslt")
+    sb, ob = step("bf16")
     sg, og = step("graph", "--hip-graph", "true", "--warmup", "1", "--steps", "3")
     assert sg["hip_graph"] is True
     assert sg["output"]["fnv64"] == sb["output"]["fnv64"]
@@ -106,7 +89,7 @@ def test_full_step_node_order_allocation():
     unrelated values and a cosine far below that; the placement's parity with
     the oracle is held at the bf16 bar on the same 5 + 20 block depth at
     width 256 (test_deep_model_both_placements_match_the_oracle)."""
-    sb, ob = step("bf16", "--gemm", "hipblaslt")
+    sb, ob = step("bf16")
     sn, on = step("node-order", "--alloc", "node-order")
     assert sn["alloc"] == "node-order" and sn["launches_held"] > 0
     assert sn["output"]["nonfinite"] == 0
@@ -117,11 +100,11 @@ def test_full_step_node_order_allocation():
     assert cos >= 0.999
 
 
-@pytest.mark.parametrize("alloc,gemm", [("fused", "hipblaslt"), ("node-order", "hipblaslt"), ("fused", "mfma")])
-def test_deep_model_both_placements_match_the_oracle(orc, alloc, gemm):
+@pytest.mark.parametrize("alloc", ["fused", "node-order"])
+def test_deep_model_both_placements_match_the_oracle(orc, alloc):
     """5 double + 20 single blocks (the full step's depth) at width 256
-    (2 x 128 heads), 64 image + 16 text tokens: both memory placements and
-    both GEMM providers against the oracle's fp32 model at the bf16 bar."""
+    (2 x 128 heads), 64 image + 16 text tokens: both memory placements
+    against the oracle's fp32 model at the bf16 bar."""
     import oracle.flux2 as of
     from test_gpu_flux2 import _run_small_model, _small_model_inputs
     cfg = dict(num_layers=5, num_single_layers=20, num_attention_heads=2, attention_head_dim=128,
@@ -132,11 +115,11 @@ def test_deep_model_both_placements_match_the_oracle(orc, alloc, gemm):
         hid, txt, pos, f = _small_model_inputs(orc, tmp)
         n_txt, n_img = txt.shape[0], hid.shape[0]
         out = os.path.join(tmp, "o.dtb")
-        st = _run_small_model(f, write_params(tmp, P), out, n_img, n_txt, "--alloc", alloc, "--gemm", gemm,
+        st = _run_small_model(f, write_params(tmp, P), out, n_img, n_txt, "--alloc", alloc,
                               layers=(5, 20))
-        print(f"  {alloc}, {gemm}: {st['kernels']} kernels, {st['launches_held']} launches held", flush=True)
+        print(f"  {alloc}: {st['kernels']} kernels, {st['launches_held']} launches held", flush=True)
         want = of.model(hid, txt, 0.5, pos[n_txt:], pos[:n_txt], P, cfg)
-        check(read_dtb(out).reshape(n_img, 128), want, f"model 5+20 blocks, {alloc} placement, {gemm} GEMMs")
+        check(read_dtb(out).reshape(n_img, 128), want, f"model 5+20 blocks, {alloc} placement")
 
 
 def test_double_block_at_the_step_shape(orc):
