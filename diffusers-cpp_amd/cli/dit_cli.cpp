@@ -13,6 +13,9 @@
 // GGUFLoaderVisitor does; `GgufInfo --gguf PATH` prints a file's header,
 // metadata and tensor table, and `Flux2Transformer2DModel --plan-only true
 // --gguf PATH` the file tensor and range each parameter would be read from.
+// `HashWeights --seed S --path P --rows R [--cols C] --out FILE` writes the
+// Q8_0 blocks (or, without --cols, the RMSNorm weights) that --hash-weights S
+// gives parameter P, as raw bytes (no device).
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -26,6 +29,7 @@
 #include <random>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "flux2.hpp"
@@ -223,7 +227,7 @@ float bf16_bits_to_f32(uint16_t h) {
 struct OutputCheck {
     int64_t n = 0, nonfinite = 0;
     double mean = 0, std = 0;
-    uint64_t fnv = 1469598103934665603ull;
+    uint64_t fnv = 0xCBF29CE484222325ull;
 };
 
 OutputCheck check_output(const std::vector<uint8_t>& bytes, int32_t type) {
@@ -513,14 +517,69 @@ void resident_input(HipRuntime& rt, DeviceBuffers& bufs, const Tensor& leaf, con
     check(dt_tensor_set(*leaf, host, 0, bytes, nullptr), "dt_tensor_set");
 }
 
-void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffers& bufs, size_t* resident_bytes,
-                    size_t* q8_bytes, size_t* n_params) {
+// --hash-weights SEED: weights whose exact values follow from integer
+// arithmetic alone, so a host-side check can regenerate them bit for bit
+// (the device's libm plays no part).  For a parameter path P:
+//   key = splitmix64(SEED * G ^ fnv1a64(P)), z(i) = splitmix64(key + i * G),
+//   G = 0x9E3779B97F4A7C15.
+// Linear weight [rows, cols]: Q8_0 block b (row-major) has the fp16 scale
+// 0x0E00 | (z(9b) & 0x1FF) and codes 4(k-1)+m = (y[2m] + y[2m+1] - 255) / 2
+// (truncated) from the bytes y of z(9b+k), k = 1..8, m = 0..3.
+// RMSNorm weight i: 1 + ((z(i) >> 40) - 2^23) * 2^-28 in fp32.
+constexpr uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+
+uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+uint64_t hash_key(uint64_t seed, const std::string& path) {
+    uint64_t h = 0xCBF29CE484222325ull;
+    for (unsigned char c : path) h = (h ^ c) * 1099511628211ull;
+    return mix64(seed * kGolden ^ h);
+}
+
+float hash_norm_weight(uint64_t key, int64_t i) {
+    return 1.0f + (float)((int32_t)(mix64(key + (uint64_t)i * kGolden) >> 40) - 8388608) * 0x1.0p-28f;
+}
+
+void hash_q8_0_blocks(uint64_t key, int64_t n_blocks, uint8_t* out) {
+    const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    for (unsigned t = 0; t < nt; ++t)
+        pool.emplace_back([=] {
+            for (int64_t b = (int64_t)t; b < n_blocks; b += nt) {
+                uint8_t* blk = out + b * 34;
+                const uint32_t d = 0x0E00u | (uint32_t)(mix64(key + (uint64_t)(9 * b) * kGolden) & 0x1FF);
+                blk[0] = (uint8_t)d;
+                blk[1] = (uint8_t)(d >> 8);
+                for (int k = 1; k <= 8; ++k) {
+                    const uint64_t z = mix64(key + (uint64_t)(9 * b + k) * kGolden);
+                    for (int m = 0; m < 4; ++m) {
+                        const int sum = (int)((z >> (16 * m)) & 0xFF) + (int)((z >> (16 * m + 8)) & 0xFF);
+                        blk[2 + 4 * (k - 1) + m] = (uint8_t)(int8_t)((sum - 255) / 2);
+                    }
+                }
+            }
+        });
+    for (auto& th : pool) th.join();
+}
+
+// Every Linear weight of m drawn (device N(0, 0.02), quantised to Q8_0 there)
+// or hash-drawn as Q8_0 blocks on the host, then kept as a BF16 copy or in
+// the DT_TYPE_Q8_0_SPLIT layout; RMSNorm weights N(1, 0.02) or hash-drawn.
+void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, bool hashed, DeviceBuffers& bufs,
+                    size_t* resident_bytes, size_t* q8_bytes, size_t* n_params) {
     std::vector<std::pair<std::string, Tensor>> ps;
     m.named_parameters(ps);
-    auto linear = [](const Tensor& t) { return t.dtype() == DT_TYPE_BF16 || t.dtype() == DT_TYPE_Q8_0_SPLIT; };
+    auto linear = [](const Tensor& t) {
+        return t.dtype() == DT_TYPE_BF16 || t.dtype() == DT_TYPE_Q8_0_SPLIT || (t.dtype() == DT_TYPE_F32 && t.ndim() == 2);
+    };
     auto resident = [](const Tensor& t) {
-        return t.dtype() == DT_TYPE_BF16 ? (size_t)t.numel() * 2
-                                         : (size_t)dt_q8_0_split_bytes(t.shape()[0], t.shape()[1]);
+        return t.dtype() == DT_TYPE_BF16  ? (size_t)t.numel() * 2
+               : t.dtype() == DT_TYPE_F32 ? (size_t)t.numel() * 4
+                                          : (size_t)dt_q8_0_split_bytes(t.shape()[0], t.shape()[1]);
     };
     size_t total = 0, max_n = 0;
     for (auto& p : ps)
@@ -531,8 +590,9 @@ void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffer
             max_n = std::max(max_n, (size_t)p.second.numel());
         }
     char* big = (char*)bufs.alloc(total);
-    float* f32 = (float*)bufs.alloc(max_n * 4);
+    float* f32 = hashed ? nullptr : (float*)bufs.alloc(max_n * 4);
     void* q8 = bufs.alloc(max_n / 32 * 34 + 256);
+    std::vector<uint8_t> host_q8(hashed ? max_n / 32 * 34 : 0);
     std::mt19937_64 gen(seed);
     std::normal_distribution<float> nd(1.0f, 0.02f);
     size_t off = 0, idx = 0;
@@ -543,21 +603,44 @@ void random_weights(HipRuntime& rt, const Module& m, uint64_t seed, DeviceBuffer
         ++idx;
         if (linear(t)) {
             const int64_t rows = t.shape()[0], cols = t.shape()[1], rb = cols / 32 * 34;
-            check(dt_fill_randn(f32, rows * cols, seed * 1000003ull + idx, 0.0f, 0.02f, nullptr), "dt_fill_randn");
-            if (t.dtype() == DT_TYPE_BF16) {
+            if (hashed) {
+                hash_q8_0_blocks(hash_key(seed, p.first), rows * (cols / 32), host_q8.data());
+                dt_tensor blocks{};  // the Q8_0 bytes as a [rows, cols] Q8_0 tensor
+                blocks.type = DT_TYPE_Q8_0;
+                blocks.ne[0] = cols;
+                blocks.ne[1] = rows;
+                blocks.ne[2] = blocks.ne[3] = 1;
+                blocks.nb[0] = 34;
+                blocks.nb[1] = rb;
+                blocks.nb[2] = blocks.nb[3] = rb * rows;
+                blocks.data = q8;
+                check(dt_tensor_set(&blocks, host_q8.data(), 0, (size_t)(rows * rb), nullptr), "dt_tensor_set");
+            } else {
+                check(dt_fill_randn(f32, rows * cols, seed * 1000003ull + idx, 0.0f, 0.02f, nullptr),
+                      "dt_fill_randn");
                 check(dt_quantize_q8_0(f32, rows, cols, cols, q8, rb, nullptr), "dt_quantize_q8_0");
-                check(dt_dequant(q8, DT_TYPE_Q8_0, rows, cols, rb, big + off, cols, DT_TYPE_BF16, nullptr),
+            }
+            if (t.dtype() == DT_TYPE_BF16 || t.dtype() == DT_TYPE_F32) {
+                check(dt_dequant(q8, DT_TYPE_Q8_0, rows, cols, rb, big + off, cols, t.dtype(), nullptr),
                       "dt_dequant");
             } else {
-                q8_split_from_f32(f32, rows, cols, q8, big + off);
+                check(dt_q8_0_split(q8, rows, cols, rb, big + off, cols,
+                                    reinterpret_cast<float*>(big + off + dt_q8_0_split_scale_offset(rows, cols)),
+                                    rows, nullptr),
+                      "dt_q8_0_split");
             }
             rt.bind_device(*t, big + off);
             off += align256(resident(t));
             *resident_bytes += resident(t);
             *q8_bytes += (size_t)(rows * rb);
-        } else if (t.dtype() == DT_TYPE_F32) {
+        } else if (t.dtype() == DT_TYPE_F32 && t.ndim() == 1) {
             std::vector<float> h((size_t)t.numel());
-            for (float& v : h) v = nd(gen);  // RMSNorm weights
+            if (hashed) {
+                const uint64_t key = hash_key(seed, p.first);
+                for (size_t i = 0; i < h.size(); ++i) h[i] = hash_norm_weight(key, (int64_t)i);
+            } else {
+                for (float& v : h) v = nd(gen);  // RMSNorm weights
+            }
             resident_input(rt, bufs, t, h.data(), h.size() * 4);
         } else {
             throw std::runtime_error("random weights: unexpected parameter type for " + p.first);
@@ -605,12 +688,17 @@ void run_model(Session& s, const Args& a) {
     HipRuntime& rt = s.rt;
     DeviceBuffers& bufs = s.dev;
     const std::string format = a.str("weight-format", "bf16");
-    if (format != "bf16" && format != "q8_0") throw std::runtime_error("--weight-format must be bf16 or q8_0");
-    LinearWeightType wt(format == "q8_0" ? DT_TYPE_Q8_0_SPLIT : DT_TYPE_BF16);
+    if (format != "bf16" && format != "q8_0" && format != "f32")
+        throw std::runtime_error("--weight-format must be bf16, q8_0 or f32");
+    LinearWeightType wt(format == "q8_0" ? DT_TYPE_Q8_0_SPLIT : format == "f32" ? DT_TYPE_F32 : DT_TYPE_BF16);
+    // --dtype: the activations' type (bf16, or f32 as the reference keeps them)
+    const std::string dtype = a.str("dtype", "bf16");
+    if (dtype != "bf16" && dtype != "f32") throw std::runtime_error("--dtype must be bf16 or f32");
+    const int32_t act = dtype == "f32" ? DT_TYPE_F32 : DT_TYPE_BF16;
     Flux2Transformer2DModel model(cfg);
 
-    Tensor hidden = Tensor::empty({1, n_img, cfg.in_channels}, DT_TYPE_BF16);
-    Tensor text = Tensor::empty({1, n_txt, cfg.joint_attention_dim}, DT_TYPE_BF16);
+    Tensor hidden = Tensor::empty({1, n_img, cfg.in_channels}, act);
+    Tensor text = Tensor::empty({1, n_txt, cfg.joint_attention_dim}, act);
     Tensor timestep = Tensor::empty({1}, DT_TYPE_F32);
     Tensor img_ids = Tensor::empty({n_img, 4}, DT_TYPE_I32);
     Tensor txt_ids = Tensor::empty({n_txt, 4}, DT_TYPE_I32);
@@ -663,8 +751,10 @@ void run_model(Session& s, const Args& a) {
         return;
     }
     std::string gguf_note;
-    if (a.has("random-weights")) {
-        random_weights(rt, model, (uint64_t)a.i64("random-weights"), bufs, &resident_bytes, &q8_bytes, &n_params);
+    if (a.has("random-weights") || a.has("hash-weights")) {
+        const bool hashed = a.has("hash-weights");
+        random_weights(rt, model, (uint64_t)a.i64(hashed ? "hash-weights" : "random-weights"), hashed, bufs,
+                       &resident_bytes, &q8_bytes, &n_params);
     } else if (a.has("gguf")) {
         // A GGUF checkpoint, placed as the reference's GGUFLoaderVisitor
         // reads it (fused q/k/v/mlp, to_out and linear_in tensors split).
@@ -689,8 +779,17 @@ void run_model(Session& s, const Args& a) {
             return v;
         };
         auto h = bf16_normals(hidden.numel()), e = bf16_normals(text.numel());
-        resident_input(rt, bufs, hidden, h.data(), h.size() * 2);
-        resident_input(rt, bufs, text, e.data(), e.size() * 2);
+        auto upload = [&](const Tensor& t, const std::vector<uint16_t>& v) {  // the same values in either type
+            if (act == DT_TYPE_BF16) return resident_input(rt, bufs, t, v.data(), v.size() * 2);
+            std::vector<float> f(v.size());
+            for (size_t i = 0; i < v.size(); ++i) {
+                const uint32_t u = (uint32_t)v[i] << 16;
+                std::memcpy(&f[i], &u, 4);
+            }
+            resident_input(rt, bufs, t, f.data(), f.size() * 4);
+        };
+        upload(hidden, h);
+        upload(text, e);
         const float ts = a.f32("timestep", 0.5f);
         resident_input(rt, bufs, timestep, &ts, 4);
         const int64_t side = (int64_t)std::llround(std::sqrt((double)n_img));
@@ -804,9 +903,36 @@ void gguf_info(const Args& a) {
     std::printf("%s\n", out.c_str());
 }
 
+// HashWeights: the host-side values of --hash-weights for one parameter.
+void hash_weights(const Args& a) {
+    const uint64_t seed = (uint64_t)a.i64("seed");
+    const std::string path = a.str("path");
+    const int64_t rows = a.i64("rows"), cols = a.i64("cols", 0);
+    std::vector<uint8_t> bytes;
+    if (cols) {
+        if (rows <= 0 || cols % 32) throw std::runtime_error("HashWeights: rows > 0 and cols % 32 == 0");
+        bytes.resize((size_t)(rows * (cols / 32) * 34));
+        hash_q8_0_blocks(hash_key(seed, path), rows * (cols / 32), bytes.data());
+    } else {
+        const uint64_t key = hash_key(seed, path);
+        std::vector<float> w((size_t)rows);
+        for (int64_t i = 0; i < rows; ++i) w[i] = hash_norm_weight(key, i);
+        bytes.resize(w.size() * 4);
+        std::memcpy(bytes.data(), w.data(), bytes.size());
+    }
+    std::ofstream f(a.str("out"), std::ios::binary);
+    f.write(reinterpret_cast<const char*>(bytes.data()), (std::streamsize)bytes.size());
+    if (!f) throw std::runtime_error("HashWeights: cannot write " + a.str("out"));
+    std::printf("{\"command\": \"HashWeights\", \"bytes\": %zu}\n", bytes.size());
+}
+
 void run(const Args& a) {
     if (a.command == "GgufInfo") {
         gguf_info(a);
+        return;
+    }
+    if (a.command == "HashWeights") {
+        hash_weights(a);
         return;
     }
     Session s(a);

@@ -647,6 +647,85 @@ __global__ __launch_bounds__(256) void gemm_128_kernel(const Group grp) {
     epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
 }
 
+// ---- any shape: 128 x 128, K in steps of 16 under a bounds mask ---------------
+// For the GEMMs the kernels above do not take: K not a multiple of 64 (ggml's
+// mul_mat takes any K, e.g. a ResnetBlock2D's time-embedding projection with
+// 16 inputs), leading dimensions or bases without 16-byte alignment, and Q8_0
+// weights with K % 64 == 32.  Each thread loads 8 consecutive k of one A row
+// and one B row element by element, with zeros past K, through one LDS stage;
+// a Q8_0 weight element is d * (u - 128) (exact in fp32) rounded to bf16, the
+// value dt_dequant writes.  Four waves of 64 x 64 on the same MFMA as the
+// kernels above.  These shapes are small (they occur outside the step's
+// projections), so the kernel is written for coverage, not rate.
+template <typename TC, bool Q8>
+__global__ __launch_bounds__(256) void gemm_any_kernel(const Group grp) {
+    constexpr int FM = 2, FN = 2, LDW = 24;  // LDS row: 16 bf16 + 8 of padding (48 bytes)
+    __shared__ __attribute__((aligned(16))) uint16_t sa[128 * LDW];
+    __shared__ __attribute__((aligned(16))) uint16_t sb[128 * LDW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int tm, tn;
+    const Problem& p = locate<128, 128>(grp, &tm, &tn);
+    const int m0 = tm * 128, n0 = tn * 128;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int row = tid >> 1, kh = (tid & 1) * 8;
+    const int64_t am = min(m0 + row, p.M - 1), bn = min(n0 + row, p.N - 1);
+    const uint16_t* arow = p.A + am * p.lda;
+    const uint16_t* brow = p.B + bn * p.ldb;
+    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.B) + bn * p.ldb;
+
+    f32x16_t acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][i][e] = 0.f;
+
+    const int lrow = lane & 31, lk = (lane >> 5) * 8;
+    for (int k0 = 0; k0 < p.K; k0 += 16) {
+        uint32_t av[4], bv[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            uint32_t a2 = 0, b2 = 0;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k = k0 + kh + e + h;
+                if (k < p.K) {
+                    a2 |= (uint32_t)arow[k] << (16 * h);
+                    uint32_t bb;
+                    if constexpr (Q8) {
+                        const float d = p.Bs[(int64_t)(k >> 5) * p.ldbs + bn];
+                        bb = f32_to_bf16_bits(mul_rn(d, (float)((int)qrow[k] - 128)));
+                    } else {
+                        bb = brow[k];
+                    }
+                    b2 |= bb << (16 * h);
+                }
+            }
+            av[e / 2] = a2;
+            bv[e / 2] = b2;
+        }
+        __syncthreads();  // every wave's reads of the previous k-step are done
+        *reinterpret_cast<uint4*>(&sa[row * LDW + kh]) = make_uint4(av[0], av[1], av[2], av[3]);
+        *reinterpret_cast<uint4*>(&sb[row * LDW + kh]) = make_uint4(bv[0], bv[1], bv[2], bv[3]);
+        __syncthreads();
+        bf16x8_t wf[FN], xf[FM];
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            wf[j] = *reinterpret_cast<const bf16x8_t*>(&sb[(wn + 32 * j + lrow) * LDW + lk]);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            xf[i] = *reinterpret_cast<const bf16x8_t*>(&sa[(wm + 32 * i + lrow) * LDW + lk]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
+    }
+    epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
+}
+
 // ---- launch ---------------------------------------------------------------------
 
 struct Config {
@@ -655,9 +734,10 @@ struct Config {
 };
 // 0: 256 x 256, 8 waves, K = 32 stages (one workgroup per CU); 1: 128 x 128
 // (two per CU); 2: 256 x 256, 4 waves, K = 64 stages; 3: Q8_0 weights,
-// 256 x 256, 8 waves, K = 64, three stages (the only one for Q8_0 B).
-constexpr Config kConfigs[4] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
-                                {256, 256, 512, 1, 1.0}};
+// 256 x 256, 8 waves, K = 64, three stages; 4: any shape (masked, 128 x 128).
+constexpr int kAnyConfig = 4;
+constexpr Config kConfigs[5] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
+                                {256, 256, 512, 1, 1.0}, {128, 128, 256, 2, 0.1}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -713,30 +793,40 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
         hipLaunchKernelGGL((gemm_k64_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == 3)
         hipLaunchKernelGGL((gemm_q8_kernel<TC>), grid, block, 0, st, g);
+    else if (cfg == kAnyConfig && ps[0].Bs)
+        hipLaunchKernelGGL((gemm_any_kernel<TC, true>), grid, block, 0, st, g);
+    else if (cfg == kAnyConfig)
+        hipLaunchKernelGGL((gemm_any_kernel<TC, false>), grid, block, 0, st, g);
     else
         hipLaunchKernelGGL((gemm_128_kernel<TC>), grid, block, 0, st, g);
     return check_launch("dt_gemm_bf16");
 }
 
-int validate(const dt_gemm_problem& q, int32_t c_type, Problem* out) {
+// Checks a problem and says whether the tiled kernels take it (K % 64 == 0,
+// 16-byte aligned operand rows); any other valid shape runs gemm_any_kernel.
+int validate(const dt_gemm_problem& q, int32_t c_type, Problem* out, bool* tiled) {
     DT_REQUIRE(q.M >= 0 && q.N >= 0 && q.K > 0, "dt_gemm_bf16: bad shape");
-    DT_REQUIRE(q.K % 64 == 0, "dt_gemm_bf16: K (%lld) must be a multiple of 64", (long long)q.K);
     DT_REQUIRE(q.M < (1ll << 31) && q.N < (1ll << 31) && q.K < (1ll << 31), "dt_gemm_bf16: shape too large");
+    *tiled = true;
     if (q.M > 0 && q.N > 0) {  // an empty problem's leading dimensions are never used
-        // bf16 B: ldb in elements, % 8; Q8_0 codes: ldb in bytes, % 16.
-        const int64_t ldb_align = q.b_scale ? 16 : 8;
-        DT_REQUIRE(q.lda >= q.K && q.ldb >= q.K && q.ldc >= q.N && q.lda % 8 == 0 && q.ldb % ldb_align == 0,
-                   "dt_gemm_bf16: leading dimensions must cover the rows and keep 16-byte alignment");
+        DT_REQUIRE(q.lda >= q.K && q.ldb >= q.K && q.ldc >= q.N,
+                   "dt_gemm_bf16: leading dimensions must cover the rows");
         if (q.b_scale) {
+            DT_REQUIRE(q.K % 32 == 0, "dt_gemm_q8_0: K (%lld) must be a multiple of 32 (Q8_0 blocks)",
+                       (long long)q.K);
             DT_REQUIRE(q.ld_scale >= q.N && (reinterpret_cast<uintptr_t>(q.b_scale) & 3) == 0,
                        "dt_gemm_bf16: Q8_0 scales must be 4-byte aligned with ld_scale >= N");
         }
         DT_REQUIRE(!q.addend || q.ldd >= q.N, "dt_gemm_bf16: ldd < N");
         DT_REQUIRE(q.A && q.B && q.C, "dt_gemm_bf16: null pointer");
-        DT_REQUIRE(aligned16(q.A) && aligned16(q.B), "dt_gemm_bf16: A and B must be 16-byte aligned");
+        DT_REQUIRE((reinterpret_cast<uintptr_t>(q.A) & 1) == 0 && (q.b_scale || (reinterpret_cast<uintptr_t>(q.B) & 1) == 0),
+                   "dt_gemm_bf16: bf16 operands must be 2-byte aligned");
         const int es = c_type == DT_TYPE_F32 ? 4 : 2;
         DT_REQUIRE(q.N % 4 != 0 || ((reinterpret_cast<uintptr_t>(q.C) % (4 * es)) == 0 && q.ldc % 4 == 0),
                    "dt_gemm_bf16: C must be %d-byte aligned with ldc %% 4 == 0", 4 * es);
+        // bf16 B: ldb in elements, % 8; Q8_0 codes: ldb in bytes, % 16.
+        const int64_t ldb_align = q.b_scale ? 16 : 8;
+        *tiled = q.K % 64 == 0 && q.lda % 8 == 0 && q.ldb % ldb_align == 0 && aligned16(q.A) && aligned16(q.B);
     }
     *out = Problem{(const uint16_t*)q.A, (const uint16_t*)q.B, q.C, q.addend, q.bias, q.lda, q.ldb,
                    q.ldc, q.ldd, (int)q.M, (int)q.N, (int)q.K, q.b_scale, q.ld_scale};
@@ -750,24 +840,31 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
                                     int32_t config, dt_stream_t stream) {
     using namespace dit;
     DT_REQUIRE(c_type == DT_TYPE_BF16 || c_type == DT_TYPE_F32, "dt_gemm_bf16: c_type %d unsupported", c_type);
-    DT_REQUIRE(config >= -1 && config <= 3, "dt_gemm_bf16: config %d out of range", config);
+    DT_REQUIRE(config >= -1 && config <= kAnyConfig, "dt_gemm_bf16: config %d out of range", config);
     DT_REQUIRE(count >= 0 && count <= kMaxGroup, "dt_gemm_bf16_grouped: count %d outside 0..%d", count,
                kMaxGroup);
     DT_REQUIRE(problems || count == 0, "dt_gemm_bf16_grouped: null problem list");
     Problem ps[kMaxGroup];
     int n = 0, n_q8 = 0;
+    bool all_tiled = true;
     for (int i = 0; i < count; ++i) {
         Problem p;
-        int rc = validate(problems[i], c_type, &p);
+        bool tiled = true;
+        int rc = validate(problems[i], c_type, &p, &tiled);
         if (rc) return rc;
         n_q8 += p.Bs != nullptr;
-        if (p.M > 0 && p.N > 0) ps[n++] = p;
+        if (p.M > 0 && p.N > 0) {
+            ps[n++] = p;
+            all_tiled &= tiled;
+        }
     }
     DT_REQUIRE(n_q8 == 0 || n_q8 == count, "dt_gemm_bf16_grouped: a group mixes Q8_0 and bf16 weights");
-    DT_REQUIRE((n_q8 > 0) == (config == 3) || config == -1,
+    DT_REQUIRE(config == -1 || config == kAnyConfig || (n_q8 > 0) == (config == 3),
                "dt_gemm_bf16: config %d does not take %s weights", config, n_q8 ? "Q8_0" : "bf16");
+    DT_REQUIRE(config == -1 || config == kAnyConfig || all_tiled,
+               "dt_gemm_bf16: config %d needs K %% 64 == 0 and 16-byte aligned rows", config);
     if (n == 0) return DT_OK;
-    const int cfg = config >= 0 ? config : n_q8 ? 3 : pick_config(ps, n, cu_count());
+    const int cfg = config >= 0 ? config : !all_tiled ? kAnyConfig : n_q8 ? 3 : pick_config(ps, n, cu_count());
     hipStream_t st = (hipStream_t)stream;
     return c_type == DT_TYPE_F32 ? launch<float>(ps, n, cfg, st) : launch<bf16>(ps, n, cfg, st);
 }

@@ -723,14 +723,31 @@ struct GemmArgs {
     int64_t lda, ldb, M, N, K;
     const float* bs;
     int64_t ldbs;
+    bool f32;  // F32 weight and activation: the fp32 GEMM
 };
 
 bool q8_weight(const dt_tensor* t) { return t->src[0] && t->src[0]->type == DT_TYPE_Q8_0_SPLIT; }
 
+bool f32_gemm(const dt_tensor* t) {
+    return t->src[0] && t->src[1] && t->src[0]->type == DT_TYPE_F32 && t->src[1]->type == DT_TYPE_F32;
+}
+
 bool gemm_args(const dt_tensor* t, GemmArgs* g) {
     const dt_tensor* w = t->src[0];
     const dt_tensor* x = t->src[1];
-    if (!w || !x || x->type != DT_TYPE_BF16) return false;
+    if (!w || !x) return false;
+    g->f32 = f32_gemm(t);
+    if (g->f32) {
+        if (t->type != DT_TYPE_F32 || w->ne[2] != 1 || w->ne[3] != 1 || x->ne[0] != w->ne[0] || w->nb[0] != 4 ||
+            (w->ne[1] > 1 && w->nb[1] % 4))
+            return false;
+        int64_t rows, xs;
+        if (!row_layout(x, &rows, &xs)) return false;
+        *g = GemmArgs{x->data, w->data, xs, w->ne[1] > 1 ? w->nb[1] / 4 : w->ne[0], rows, w->ne[1], w->ne[0],
+                      nullptr, 0, true};
+        return true;
+    }
+    if (x->type != DT_TYPE_BF16) return false;
     const bool q8 = w->type == DT_TYPE_Q8_0_SPLIT;
     if (!q8 && w->type != DT_TYPE_BF16) return false;
     if (w->ne[2] != 1 || w->ne[3] != 1 || x->ne[0] != w->ne[0]) return false;
@@ -789,7 +806,8 @@ bool match_gemm_add(Graph& g, const dt_tensor* a, Plan& p) {
 }
 
 constexpr const char* kMulMatOperands =
-    "dt_graph_compute: MUL_MAT needs BF16 or whole Q8_0_SPLIT weight rows and BF16 activation rows";
+    "dt_graph_compute: MUL_MAT needs BF16 or whole Q8_0_SPLIT weight rows and BF16 activation rows, or F32 "
+    "weight and activation rows";
 
 int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const dt_tensor* addend) {
     hipStream_t st = backend_stream(be);
@@ -798,6 +816,12 @@ int run_mul_mat(dt_backend* be, const dt_tensor* mm, const dt_tensor* out, const
     DT_REQUIRE(gemm_args(mm, &g), "%s", kMulMatOperands);
     DT_REQUIRE(out_rows(out, g.N, &ldc), "dt_graph_compute: MUL_MAT output must be BF16/F32 rows of N");
     if (addend) DT_REQUIRE(out_rows(addend, g.N, &ldd), "dt_graph_compute: bad GEMM addend");
+    if (g.f32) {
+        DT_REQUIRE(out->type == DT_TYPE_F32 && (!addend || addend->type == DT_TYPE_F32),
+                   "dt_graph_compute: an F32 MUL_MAT writes F32");
+        return dt_gemm_f32((const float*)g.a, g.lda, (const float*)g.b, g.ldb, (float*)out->data, ldc, g.M, g.N, g.K,
+                           nullptr, addend ? (const float*)addend->data : nullptr, ldd, st);
+    }
     if (g.bs)
         return dt_gemm_q8_0(g.a, g.lda, g.b, g.ldb, g.bs, g.ldbs, out->data, ldc, g.M, g.N, g.K, nullptr,
                             addend ? addend->data : nullptr, ldd, out->type, st);
@@ -824,6 +848,7 @@ int run_gemm_group(dt_backend* be, const std::vector<const dt_tensor*>& members)
     const int n = (int)members.size();
     DT_REQUIRE(n >= 1 && n <= 8, "dt_graph_compute: GEMM group of %d", n);
     GemmArgs gs[8];
+    bool f32 = false;
     for (int i = 0; i < n; ++i) {
         const dt_tensor* mm = members[i];
         GemmArgs& g = gs[i];
@@ -835,7 +860,10 @@ int run_gemm_group(dt_backend* be, const std::vector<const dt_tensor*>& members)
         if (g.bs) g.bs = reinterpret_cast<const float*>((const char*)g.b + dt_q8_0_split_scale_offset(g.N, g.K));
         ps[i] = dt_gemm_problem{g.a, g.lda, g.b, g.ldb, mm->data, ldc, nullptr, 0, nullptr, g.M, g.N, g.K, g.bs,
                                 g.ldbs};
+        DT_REQUIRE(i == 0 || g.f32 == f32, "dt_graph_compute: a GEMM group mixes F32 and BF16 products");
+        f32 = g.f32;
     }
+    if (f32) return dt_gemm_f32_grouped(ps, n, st);
     return dt_gemm_bf16_grouped(ps, n, members[0]->type, -1, st);
 }
 
@@ -863,6 +891,7 @@ void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
             const dt_tensor* t = nodes[j];
             if (t->op == DT_OP_VIEW) continue;
             if (!groupable(j) || t->type != nodes[i]->type || q8_weight(t) != q8_weight(nodes[i]) ||
+                f32_gemm(t) != f32_gemm(nodes[i]) ||
                 !ready_before(t->src[0], i) || !ready_before(t->src[1], i))
                 break;
             members.push_back(j);
@@ -957,6 +986,32 @@ void merge_qk_swiglu(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plan
         move_to(qb, qa);
         move_to(sidx, qa);
     }
+}
+
+// FLASH_ATTN_EXT with F32 q, k, v (and output): the fp32 attention, its
+// scores in the backend's scratch.
+int run_flash_attn_f32(dt_backend* be, const dt_tensor* t) {
+    const dt_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2];
+    DT_REQUIRE(t->type == DT_TYPE_F32 && k->type == DT_TYPE_F32 && v->type == DT_TYPE_F32,
+               "dt_graph_compute: FLASH_ATTN_EXT mixes F32 and other operand types");
+    DT_REQUIRE(q->nb[0] == 4 && k->nb[0] == 4 && v->nb[0] == 4 && t->nb[0] == 4,
+               "dt_graph_compute: FLASH_ATTN_EXT rows must be contiguous");
+    DT_REQUIRE(t->ne[0] == q->ne[0] && t->ne[1] == q->ne[2] && t->ne[2] == q->ne[1] &&
+                   t->ne[3] == q->ne[3] && k->ne[1] == v->ne[1] && k->ne[2] == q->ne[2] &&
+                   v->ne[2] == q->ne[2] && k->ne[3] == q->ne[3] && v->ne[3] == q->ne[3] &&
+                   k->ne[0] == q->ne[0] && v->ne[0] == q->ne[0],
+               "dt_graph_compute: FLASH_ATTN_EXT shapes disagree");
+    const int64_t qs[3] = {q->nb[3] / 4, q->nb[1] / 4, q->nb[2] / 4};
+    const int64_t ks[3] = {k->nb[3] / 4, k->nb[1] / 4, k->nb[2] / 4};
+    const int64_t vs[3] = {v->nb[3] / 4, v->nb[1] / 4, v->nb[2] / 4};
+    const int64_t os[3] = {t->nb[3] / 4, t->nb[2] / 4, t->nb[1] / 4};
+    const size_t ws_bytes = dt_flash_attn_f32_workspace_bytes(q->ne[3], q->ne[2], q->ne[1], k->ne[1], q->ne[0]);
+    void* ws = nullptr;
+    const int rc = backend_scratch(be, ws_bytes, &ws);
+    if (rc) return rc;
+    return dt_flash_attn_f32((const float*)q->data, (const float*)k->data, (const float*)v->data, (float*)t->data,
+                             q->ne[3], q->ne[2], q->ne[1], k->ne[1], q->ne[0], qs, ks, vs, os, fparam(t, 0), ws,
+                             ws_bytes, backend_stream(be));
 }
 
 int run_flash_attn(hipStream_t st, const dt_tensor* t) {
@@ -1284,6 +1339,8 @@ int run_unfused(dt_backend* be, dt_tensor* t) {
             return run_mul_mat(be, t, t, nullptr);
         case DT_OP_FLASH_ATTN_EXT:
             ++g_kernels;
+            if (t->src[0] && t->src[0]->type == DT_TYPE_F32 && t->src[1] && t->src[2] && !t->src[3])
+                return run_flash_attn_f32(be, t);
             return run_flash_attn(st, t);
         case DT_OP_CONV_2D_DIRECT:
             DT_REQUIRE(t->src[0] && t->src[1], "dt_graph_compute: CONV_2D_DIRECT needs a weight and an input");

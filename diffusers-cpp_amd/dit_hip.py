@@ -120,6 +120,13 @@ _SIGS = {
     "dt_graph_exec_free": (c_int32, [c_void_p]),
     "dt_q8_0_split_scale_offset": (c_int64, [c_int64, c_int64]),
     "dt_q8_0_split_bytes": (c_int64, [c_int64, c_int64]),
+    "dt_gemm_f32": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                              c_void_p, c_void_p, c_int64, _S]),
+    "dt_gemm_f32_grouped": (c_int32, [c_void_p, c_int32, _S]),
+    "dt_flash_attn_f32_workspace_bytes": (ctypes.c_size_t, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "dt_flash_attn_f32": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                    c_int64, POINTER(c_int64), POINTER(c_int64), POINTER(c_int64),
+                                    POINTER(c_int64), c_float, c_void_p, ctypes.c_size_t, _S]),
     "dt_flash_attn_bf16": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                                      c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64),
                                      POINTER(c_int64), POINTER(c_int64), c_float, c_int32, _S]),
@@ -634,6 +641,38 @@ def flash_attn(q, k, v, scale=None, out=None, out_dtype=None):
     check(load().dt_flash_attn_bf16(_p(q), _p(k), _p(v), _p(out), B, H, Sq, Skv, D, st(q), st(k),
                                     st(v), st(out), scale, io_type(out), stream()),
           "dt_flash_attn_bf16")
+    return out
+
+
+def gemm_f32(a, b, bias=None, addend=None, out=None):
+    """a: fp32 [M, K], b: fp32 [N, K] (rows K-contiguous) -> a @ b.T (+ bias) (+ addend), fp32 MFMA."""
+    torch = _torch()
+    M, K = a.shape
+    N = b.shape[0]
+    assert b.shape[1] == K and a.stride(1) == 1 and b.stride(1) == 1
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    ldd = addend.stride(0) if addend is not None else 0
+    check(load().dt_gemm_f32(_p(a), a.stride(0), _p(b), b.stride(0), _p(out), out.stride(0), M, N, K, _p(bias),
+                             _p(addend), ldd, stream()), "dt_gemm_f32")
+    return out
+
+
+def flash_attn_f32(q, k, v, scale=None, out=None):
+    """q: fp32 [B, Sq, H, 128], k, v: [B, Skv, H, 128] (d contiguous) ->
+    softmax(scale q k^T) v as fp32 [B, Sq, H, 128], in fp32 throughout."""
+    torch = _torch()
+    B, Sq, H, D = q.shape
+    Skv = k.shape[1]
+    if out is None:
+        out = torch.empty((B, Sq, H, D), dtype=torch.float32, device=q.device)
+    st = lambda t: (c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
+    scale = 1.0 / D ** 0.5 if scale is None else scale
+    lib = load()
+    nbytes = lib.dt_flash_attn_f32_workspace_bytes(B, H, Sq, Skv, D)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    check(lib.dt_flash_attn_f32(_p(q), _p(k), _p(v), _p(out), B, H, Sq, Skv, D, st(q), st(k), st(v), st(out),
+                                scale, _p(ws), ws.numel(), stream()), "dt_flash_attn_f32")
     return out
 
 

@@ -303,11 +303,13 @@ Node* HipRuntime::scale(Node* t, float value) {
 Node* HipRuntime::clamp(Node* t, float mn, float mx) { return unary(t, DT_UN_CLAMP, mn, mx); }
 
 // ggml_mul_mat(w, x) (Runtime.hpp:136-139; Linear.cpp:24): y = x W^T over
-// ne0.  The MFMA GEMM takes BF16 activations and BF16 or Q8_0_SPLIT weights
-// (Q8_0 dequantised to bf16 inside the GEMM): an F32 operand is cast to BF16
-// by a CPY node first (ggml's CPU backend likewise converts the activation to
-// the weight's vec_dot type), and the result is F32 when the activation was
-// F32 (ggml's result type) or BF16 for BF16 activations.
+// ne0.  F32 weights with F32 activations (the reference's precision) stay
+// F32: the fp32 GEMM.  Otherwise the bf16 MFMA GEMM takes BF16 activations
+// and BF16 or Q8_0_SPLIT weights (Q8_0 dequantised to bf16 inside the GEMM):
+// an F32 activation is cast to BF16 by a CPY node first (ggml's CPU backend
+// likewise converts the activation to the weight's vec_dot type), and the
+// result is F32 when the activation was F32 (ggml's result type) or BF16 for
+// BF16 activations.
 Node* HipRuntime::mul_mat(Node* w, Node* x) {
     if (w->ne[0] != x->ne[0]) throw std::invalid_argument("mul_mat: ne0 (K) of weight and input differ");
     if (w->ne[2] != 1 || w->ne[3] != 1) throw Unsupported("mul_mat: batched weights are not supported");
@@ -315,9 +317,14 @@ Node* HipRuntime::mul_mat(Node* w, Node* x) {
         throw Unsupported("mul_mat: repack Q8_0 weights once at load (dt_q8_0_split -> DT_TYPE_Q8_0_SPLIT) or "
                           "dequantise them to BF16 (dt_dequant)");
     const int32_t out_type = x->type == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32;
-    if (w->type != DT_TYPE_BF16 && w->type != DT_TYPE_Q8_0_SPLIT) w = cast(w, DT_TYPE_BF16);
-    if (x->type != DT_TYPE_BF16) x = cast(x, DT_TYPE_BF16);
-    else if (x->nb[0] != 2) x = cont(x);
+    if (w->type == DT_TYPE_F32 && x->type == DT_TYPE_F32) {
+        if (w->nb[0] != 4) w = cont(w);
+        if (x->nb[0] != 4) x = cont(x);
+    } else {
+        if (w->type != DT_TYPE_BF16 && w->type != DT_TYPE_Q8_0_SPLIT) w = cast(w, DT_TYPE_BF16);
+        if (x->type != DT_TYPE_BF16) x = cast(x, DT_TYPE_BF16);
+        else if (x->nb[0] != 2) x = cont(x);
+    }
     const int64_t ne[4] = {w->ne[1], x->ne[1], x->ne[2], x->ne[3]};
     Node* r = make(out_type, ne, DT_OP_MUL_MAT);
     r->src[0] = w;
@@ -403,7 +410,8 @@ Node* HipRuntime::concat(Node* a, Node* b, int dim) {
 Node* HipRuntime::sum_rows(Node*) { throw Unsupported("sum_rows: not part of the DiT elementwise chain"); }
 // ggml_flash_attn_ext (Runtime.hpp:250-257; FlashAttentionOp.cpp:84-94):
 // q ne {D, Sq, H, B}, k / v ne {D, Skv, H, B} -> ne {D, H, Sq, B}.  No mask,
-// ALiBi or softcap (Flux2 uses none); F32 operands are cast to BF16 and give
+// ALiBi or softcap (Flux2 uses none).  F32 q, k and v stay F32 (the fp32
+// attention, F32 result); otherwise F32 operands are cast to BF16 and give
 // an F32 result, BF16 operands a BF16 result.
 Node* HipRuntime::flash_attn_ext(Node* q, Node* k, Node* v, Node* mask, float scale, float max_bias,
                                  float logit_softcap) {
@@ -413,7 +421,11 @@ Node* HipRuntime::flash_attn_ext(Node* q, Node* k, Node* v, Node* mask, float sc
     if (q->ne[0] != 128 || k->ne[0] != 128 || v->ne[0] != 128)
         throw Unsupported("flash_attn_ext: head_dim 128 only");
     const int32_t out_type = q->type == DT_TYPE_BF16 ? DT_TYPE_BF16 : DT_TYPE_F32;
-    auto prep = [&](Node* t) { return t->type != DT_TYPE_BF16 ? cast(t, DT_TYPE_BF16) : t->nb[0] != 2 ? cont(t) : t; };
+    const bool f32 = q->type == DT_TYPE_F32 && k->type == DT_TYPE_F32 && v->type == DT_TYPE_F32;
+    auto prep = [&](Node* t) {
+        if (f32) return t->nb[0] != 4 ? cont(t) : t;
+        return t->type != DT_TYPE_BF16 ? cast(t, DT_TYPE_BF16) : t->nb[0] != 2 ? cont(t) : t;
+    };
     q = prep(q);
     k = prep(k);
     v = prep(v);

@@ -313,7 +313,9 @@ int dt_fill_randn(float *y, int64_t n, uint64_t seed, float mean, float std,
  * Linear::forward (src/nn/Linear.cpp:17-36), and with `addend` the
  * `attn(x) + mlp(y)` sum of Flux2FusedAttentionOutput::forward
  * (src/diffusers/models/transformers/flux2/Flux2FusedAttentionOutput.hpp:31-36).
- * K % 64 == 0; lda, ldb % 8 == 0; A, B 16-byte aligned.  C may alias addend. */
+ * Any K >= 1 and leading dimensions (A, B 2-byte aligned); K % 64 == 0 with
+ * lda, ldb % 8 == 0 and A, B 16-byte aligned runs the tiled kernels, any
+ * other shape a masked 128 x 128 kernel.  C may alias addend. */
 int dt_gemm_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C, int64_t ldc,
                  int64_t M, int64_t N, int64_t K, const float *bias, const void *addend,
                  int64_t ldd, int32_t c_type, dt_stream_t stream);
@@ -324,7 +326,9 @@ int dt_gemm_bf16(const void *A, int64_t lda, const void *B, int64_t ldb, void *C
  * element in HBM.  Replaces the same Runtime::mul_mat call as dt_gemm_bf16
  * for the reference's Q8_0 Linear weights (src/nn/Linear.cpp:17-36;
  * flux2-klein-9b-q8.json), whose CPU path dequantises inside ggml's matmul.
- * ld_codes % 16 == 0, scales 4-byte aligned with ld_scales >= N, K % 64 == 0. */
+ * K % 32 == 0 (whole Q8_0 blocks); scales 4-byte aligned with ld_scales >= N;
+ * K % 64 == 0 with ld_codes % 16 == 0 runs the tiled kernel, K % 64 == 32 the
+ * masked one. */
 int dt_gemm_q8_0(const void *A, int64_t lda, const void *codes, int64_t ld_codes, const float *scales,
                  int64_t ld_scales, void *C, int64_t ldc, int64_t M, int64_t N, int64_t K,
                  const float *bias, const void *addend, int64_t ldd, int32_t c_type,
@@ -333,7 +337,8 @@ int dt_gemm_q8_0(const void *A, int64_t lda, const void *codes, int64_t ld_codes
 /* dt_gemm_bf16 with an explicit tile configuration: 0 = 256x256 per
  * workgroup with direct global->LDS loads in four K = 32 stages, 1 = 128x128
  * with two workgroups per CU, 2 = 256x256 with two K = 64 stages, 3 = Q8_0
- * weights (required for them); -1 picks by shape as dt_gemm_bf16 does.
+ * weights (the tiled kernel for them), 4 = the masked any-shape kernel (bf16
+ * or Q8_0 weights); -1 picks by shape as dt_gemm_bf16 does.
  * For tuning and tests; no counterpart in the reference. */
 int dt_gemm_bf16_config(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float *bias,
@@ -404,6 +409,28 @@ int dt_flash_attn_qk_bf16(const void *q0, const int64_t *q0_strides, const float
                           int64_t seq_q, int64_t seq_kv, int64_t head_dim, const int64_t *k_strides,
                           const int64_t *v_strides, const int64_t *o_strides, float scale,
                           int32_t o_type, dt_stream_t stream);
+
+/* fp32 counterparts for graphs whose weights and activations are both F32
+ * (the reference's own precision: Linear::forward with F32 weights,
+ * src/nn/Linear.cpp:17-36, and FlashAttentionOp::operator() on F32 q/k/v,
+ * src/nn/attention/FlashAttentionOp.cpp:84-94).  Products and sums in fp32
+ * on the fp32 matrix cores.
+ * dt_gemm_f32: C = A B^T (+ bias) (+ addend) as dt_gemm_bf16 with fp32 A
+ * [M, K], B [N, K], C and addend (any K; A, B 4-byte aligned; with N % 4 == 0
+ * C 16-byte aligned and ldc % 4 == 0).  dt_gemm_f32_grouped: up to 8 of them
+ * in one launch (b_scale must be NULL).
+ * dt_flash_attn_f32: softmax(scale Q K^T) V per (batch, head), strides as
+ * dt_flash_attn_bf16, fp32 o; the scores of up to 8 heads at a time go
+ * through `workspace` (dt_flash_attn_f32_workspace_bytes, 16-byte aligned). */
+int dt_gemm_f32(const float *A, int64_t lda, const float *B, int64_t ldb, float *C, int64_t ldc, int64_t M,
+                int64_t N, int64_t K, const float *bias, const float *addend, int64_t ldd, dt_stream_t stream);
+int dt_gemm_f32_grouped(const dt_gemm_problem *problems, int32_t count, dt_stream_t stream);
+size_t dt_flash_attn_f32_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_q, int64_t seq_kv,
+                                         int64_t head_dim);
+int dt_flash_attn_f32(const float *q, const float *k, const float *v, float *o, int64_t batch, int64_t heads,
+                      int64_t seq_q, int64_t seq_kv, int64_t head_dim, const int64_t *q_strides,
+                      const int64_t *k_strides, const int64_t *v_strides, const int64_t *o_strides, float scale,
+                      void *workspace, size_t workspace_bytes, dt_stream_t stream);
 
 /* ======================================================================== */
 /* (iii) unfused ggml-op kernels on ggml-shaped descriptors                 */

@@ -36,6 +36,11 @@ def load():
         "or_mt64_nth": (c_uint64, [c_uint64, c_uint64]),
         "or_randn_f32": (None, [c_uint64, c_int64, c_float, c_float, P]),
         "or_rand_int32": (None, [c_uint64, c_int64, c_int32, c_int32, P]),
+        "or_splitmix64": (c_uint64, [c_uint64]),
+        "or_fnv1a64": (c_uint64, [ctypes.c_char_p]),
+        "or_hash_key": (c_uint64, [c_uint64, ctypes.c_char_p]),
+        "or_hash_q8_0": (None, [c_uint64, ctypes.c_char_p, c_int64, c_int64, P, c_int]),
+        "or_hash_norm_weight": (None, [c_uint64, ctypes.c_char_p, c_int64, P]),
         "or_f16_to_f32": (c_float, [c_uint16]),
         "or_f32_to_f16": (c_uint16, [c_float]),
         "or_bf16_to_f32": (c_float, [c_uint16]),
@@ -68,6 +73,7 @@ def load():
                                  c_int, P, c_int]),
         "or_linear_f32": (None, [P, c_int64, c_int64, c_int64, P, c_int64, c_int64, P, P, c_int64,
                                  c_int]),
+        "or_linear_q8_0_ggml": (None, [P, c_int64, c_int64, c_int64, P, c_int64, P, P, c_int64, c_int]),
         "or_attention_f32": (None, [P, P, P, P, c_int64, c_int64, c_int64, c_int64, P, P, P, P,
                                     c_float, c_int]),
         "or_max_threads": (c_int, []),
@@ -105,6 +111,25 @@ def randint(seed: int, shape, lo: int, hi: int) -> np.ndarray:
     out = np.empty(int(np.prod(shape)), dtype=np.int32)
     load().or_rand_int32(seed, out.size, lo, hi, _p(out))
     return out.reshape(shape)
+
+
+def hash_key(seed: int, path: str) -> int:
+    return int(load().or_hash_key(seed, path.encode()))
+
+
+def hash_q8_0(seed: int, path: str, rows: int, cols: int, threads=0) -> np.ndarray:
+    """Q8_0 block bytes of a hash-drawn [rows, cols] Linear weight (the rule
+    dit_cli --hash-weights applies; stated in oracle.c)."""
+    assert cols % 32 == 0
+    out = np.empty(rows * cols // 32 * 34, dtype=np.uint8)
+    load().or_hash_q8_0(seed, path.encode(), rows, cols, _p(out), threads)
+    return out
+
+
+def hash_norm_weight(seed: int, path: str, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    load().or_hash_norm_weight(seed, path.encode(), n, _p(out))
+    return out
 
 
 def tensor_seed(index: int) -> int:
@@ -289,8 +314,35 @@ def conv2d(x, w, b=None, padding=None, up2=False, threads=0):
     return y
 
 
+class Q8_0Weight:
+    """A [rows, cols] Linear weight held as ggml Q8_0 blocks (rows of cols/32
+    blocks of 34 bytes).  linear() multiplies by it with ggml's CPU Q8_0
+    arithmetic (activations quantised to Q8_0, or_linear_q8_0_ggml), as the
+    reference's mul_mat does for a Q8_0 weight."""
+
+    def __init__(self, blocks, rows: int, cols: int):
+        assert cols % 32 == 0
+        self.blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        assert self.blocks.size == rows * cols // 32 * 34
+        self.shape = (rows, cols)
+
+    def dequantize(self, threads=0) -> np.ndarray:
+        return dequantize(self.blocks, self.shape[0] * self.shape[1], 8, threads).reshape(self.shape)
+
+
 def linear(x, w, b=None, threads=0):
-    """x: [..., K]; w: [N, K] (PyTorch Linear weight); b: [N] or None -> [..., N]."""
+    """x: [..., K]; w: [N, K] (PyTorch Linear weight) or a Q8_0Weight; b: [N]
+    or None -> [..., N].  An fp32 weight: fp32 products, exact-order sum
+    rounded once; a Q8_0Weight: ggml's Q8_0 x Q8_0 arithmetic."""
+    if isinstance(w, Q8_0Weight):
+        x = _f32(x)
+        N, K = w.shape
+        assert x.shape[-1] == K
+        M = x.size // K
+        y = np.empty(x.shape[:-1] + (N,), dtype=np.float32)
+        bp = _p(_f32(b)) if b is not None else None
+        load().or_linear_q8_0_ggml(_p(x), M, K, K, _p(w.blocks), N, bp, _p(y), N, threads)
+        return y
     x, w = _f32(x), _f32(w)
     K = x.shape[-1]
     N = w.shape[0]

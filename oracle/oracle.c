@@ -97,6 +97,71 @@ void or_rand_int32(uint64_t seed, int64_t n, int32_t lo, int32_t hi, int32_t *ou
 }
 
 /* ======================================================================== */
+/* hash-drawn test weights                                                   */
+/* ======================================================================== */
+
+/* Synthetic Linear and RMSNorm weights whose exact values depend only on
+ * integer arithmetic, so a device-side run (dit_cli --hash-weights) and this
+ * restatement produce the same bytes with no libm involved.  For a seed and
+ * a parameter path (e.g. "transformer_blocks.0.attn.to_q.weight"):
+ *   key  = splitmix64(seed * G ^ fnv1a64(path)),  G = 0x9E3779B97F4A7C15
+ *   z(i) = splitmix64(key + i * G)
+ * Q8_0 block b of a [rows, cols] weight (row-major over rows x cols/32):
+ *   d = fp16 bits 0x0E00 | (z(9b) & 0x1FF)  (d in [3.66e-4, 4.88e-4))
+ *   code 4(k-1)+m, k = 1..8, m = 0..3: bytes y = z(9b+k) little-endian,
+ *   q = (y[2m] + y[2m+1] - 255) / 2, truncated toward zero, in [-127, 127]
+ *   (triangular, std 52.2, so d*q has std ~0.022).
+ * RMSNorm weight i: 1.0f + (float)((int32)(z(i) >> 40) - 2^23) * 2^-28,
+ * one fp32 rounding. */
+static const uint64_t or_golden = 0x9E3779B97F4A7C15ULL;
+
+/* splitmix64's output function (Steele, Lea, Flood 2014; Vigna's public
+ * splitmix64.c): the n-th output of the generator seeded s is
+ * or_splitmix64(s + n * G), n = 1, 2, ... */
+uint64_t or_splitmix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+/* 64-bit FNV-1a (offset basis 0xCBF29CE484222325, prime 0x100000001B3). */
+uint64_t or_fnv1a64(const char *s) {
+    uint64_t h = 0xCBF29CE484222325ULL;
+    for (const unsigned char *c = (const unsigned char *)s; *c; ++c) h = (h ^ *c) * 0x100000001B3ULL;
+    return h;
+}
+
+uint64_t or_hash_key(uint64_t seed, const char *path) { return or_splitmix64(seed * or_golden ^ or_fnv1a64(path)); }
+
+void or_hash_q8_0(uint64_t seed, const char *path, int64_t rows, int64_t cols, uint8_t *dst, int nthreads) {
+    const uint64_t key = or_hash_key(seed, path);
+    const int64_t nb = rows * (cols / 32);
+#pragma omp parallel for schedule(static) OR_OMP_THREADS(nthreads)
+    for (int64_t b = 0; b < nb; ++b) {
+        uint8_t *blk = dst + b * 34;
+        const uint64_t z0 = or_splitmix64(key + (uint64_t)(9 * b) * or_golden);
+        const uint16_t d = (uint16_t)(0x0E00u | (uint32_t)(z0 & 0x1FF));
+        blk[0] = (uint8_t)(d & 0xFF);
+        blk[1] = (uint8_t)(d >> 8);
+        for (int k = 1; k <= 8; ++k) {
+            const uint64_t z = or_splitmix64(key + (uint64_t)(9 * b + k) * or_golden);
+            for (int m = 0; m < 4; ++m) {
+                const int y0 = (int)((z >> (16 * m)) & 0xFF), y1 = (int)((z >> (16 * m + 8)) & 0xFF);
+                blk[2 + 4 * (k - 1) + m] = (uint8_t)(int8_t)((y0 + y1 - 255) / 2);
+            }
+        }
+    }
+}
+
+void or_hash_norm_weight(uint64_t seed, const char *path, int64_t n, float *out) {
+    const uint64_t key = or_hash_key(seed, path);
+    for (int64_t i = 0; i < n; ++i) {
+        const int32_t v = (int32_t)(or_splitmix64(key + (uint64_t)i * or_golden) >> 40) - 8388608;
+        out[i] = 1.0f + (float)v * 0x1.0p-28f;
+    }
+}
+
+/* ======================================================================== */
 /* number formats                                                            */
 /* ======================================================================== */
 
@@ -713,6 +778,70 @@ void or_linear_f32(const float *x, int64_t M, int64_t K, int64_t x_stride,
             for (int64_t i = 0; i < M; ++i)
                 for (int64_t j = j0; j < j1; ++j) y[i * y_stride + j] = y[i * y_stride + j] + b[j];
     }
+}
+
+/* ggml's CPU mul_mat for a Q8_0 weight (Linear::forward -> Runtime::mul_mat,
+ * src/nn/Linear.cpp:17-36, on the reference's Q8_0 checkpoints), restated
+ * from public ggml (the submodule is not vendored, so its pinned commit is
+ * unknown): Q8_0's vec_dot type is Q8_0, so every activation row is first
+ * quantised to Q8_0 blocks by the rule of or_quantize_q8_0, then
+ *   y[i][j] = sum over blocks b, in order, of
+ *             (float)(sum_t qx[t] * qw[t]) * (fp16(d_x) * fp16(d_w))
+ * with the 32-term integer dot exact and each block term and the running sum
+ * rounded to fp32 (ggml_vec_dot_q8_0_q8_0's scalar form; its SIMD forms
+ * regroup the same fp32 sum).  w: N rows of K/32 blocks of 34 bytes. */
+void or_linear_q8_0_ggml(const float *x, int64_t M, int64_t K, int64_t x_stride, const uint8_t *w, int64_t N,
+                         const float *b, float *y, int64_t y_stride, int nthreads) {
+    const int64_t nb = K / 32, rb = nb * 34;
+    int8_t *qx = (int8_t *)malloc((size_t)(M * K));
+    float *dx = (float *)malloc((size_t)(M * nb) * sizeof(float));
+    int8_t *qw = (int8_t *)malloc((size_t)(N * K));
+    float *dw = (float *)malloc((size_t)(N * nb) * sizeof(float));
+#pragma omp parallel for schedule(static) OR_OMP_THREADS(nthreads)
+    for (int64_t i = 0; i < M; ++i) {
+        uint8_t blk[34];
+        for (int64_t c = 0; c < nb; ++c) {
+            or_quantize_q8_0(x + i * x_stride + c * 32, 32, blk);
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            dx[i * nb + c] = or_f16_to_f32(dh);
+            memcpy(qx + i * K + c * 32, blk + 2, 32);
+        }
+    }
+#pragma omp parallel for schedule(static) OR_OMP_THREADS(nthreads)
+    for (int64_t j = 0; j < N; ++j)
+        for (int64_t c = 0; c < nb; ++c) {
+            const uint8_t *blk = w + j * rb + c * 34;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            dw[j * nb + c] = or_f16_to_f32(dh);
+            memcpy(qw + j * K + c * 32, blk + 2, 32);
+        }
+    enum { JB = 16 };
+#pragma omp parallel for schedule(dynamic, 1) OR_OMP_THREADS(nthreads)
+    for (int64_t j0 = 0; j0 < N; j0 += JB) {
+        const int64_t j1 = j0 + JB < N ? j0 + JB : N;
+        for (int64_t i = 0; i < M; ++i) {
+            const int8_t *xr = qx + i * K;
+            const float *dxr = dx + i * nb;
+            for (int64_t j = j0; j < j1; ++j) {
+                const int8_t *wr = qw + j * K;
+                const float *dwr = dw + j * nb;
+                float sum = 0.0f;
+                for (int64_t c = 0; c < nb; ++c) {
+                    int32_t si = 0;
+                    for (int t = 0; t < 32; ++t) si += (int32_t)xr[c * 32 + t] * (int32_t)wr[c * 32 + t];
+                    const float term = (float)si * (dxr[c] * dwr[c]);
+                    sum = sum + term;
+                }
+                y[i * y_stride + j] = b ? sum + b[j] : sum;
+            }
+        }
+    }
+    free(qx);
+    free(dx);
+    free(qw);
+    free(dw);
 }
 
 /* ggml_flash_attn_ext without mask: src/nn/attention/FlashAttentionOp.cpp:84-94. */

@@ -30,6 +30,14 @@ extern "C" {
 uint64_t or_mt64_nth(uint64_t seed, uint64_t n);           /* n-th output, 1-based */
 void or_randn_f32(uint64_t seed, int64_t n, float mean, float std, float *out);
 void or_rand_int32(uint64_t seed, int64_t n, int32_t lo, int32_t hi, int32_t *out);
+/* Hash-drawn test weights (integer arithmetic only): Q8_0 blocks of a
+ * [rows, cols] Linear weight and RMSNorm weights, keyed by seed and the
+ * parameter path (the rule is stated in oracle.c). */
+uint64_t or_splitmix64(uint64_t z);
+uint64_t or_fnv1a64(const char *s);
+uint64_t or_hash_key(uint64_t seed, const char *path);
+void or_hash_q8_0(uint64_t seed, const char *path, int64_t rows, int64_t cols, uint8_t *dst, int nthreads);
+void or_hash_norm_weight(uint64_t seed, const char *path, int64_t n, float *out);
 
 /* ---- number formats ----------------------------------------------------- */
 float    or_f16_to_f32(uint16_t h);
@@ -130,6 +138,11 @@ void or_conv2d_f32(const float *x, int64_t N, int64_t Ci, int64_t H, int64_t W,
 void or_linear_f32(const float *x, int64_t M, int64_t K, int64_t x_stride,
                    const float *w, int64_t N, int64_t w_stride, const float *b,
                    float *y, int64_t y_stride, int nthreads);
+/* ggml's CPU mul_mat for a Q8_0 weight: activation rows quantised to Q8_0,
+ * integer block dots, fp32 block sum (see oracle.c).  w: N rows of K/32
+ * blocks of 34 bytes; K % 32 == 0. */
+void or_linear_q8_0_ggml(const float *x, int64_t M, int64_t K, int64_t x_stride, const uint8_t *w, int64_t N,
+                         const float *b, float *y, int64_t y_stride, int nthreads);
 
 /* Unmasked softmax attention, ggml_flash_attn_ext as FlashAttentionOp::operator()
  * calls it (src/nn/attention/FlashAttentionOp.cpp:84-94): for each head h and

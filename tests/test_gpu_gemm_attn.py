@@ -137,10 +137,39 @@ def test_gemm_grouped(orc, dev, config):
         assert_fp32(host(o), r, what=f"grouped gemm {M}x{N}x{K}")
 
 
-def test_gemm_rejects_bad_shapes(dev):
-    a = torch.zeros((64, 48), dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(RuntimeError, match="multiple of 64"):
-        dit_hip.gemm(a, a)
+@pytest.mark.parametrize("M,N,K,lda_pad", [(64, 48, 16, 0), (300, 136, 40, 0), (33, 20, 3, 0), (129, 257, 200, 0),
+                                           (70, 96, 64, 3), (1, 1, 1, 0)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_any_shape(orc, dev, M, N, K, lda_pad, out_dtype):
+    """Shapes the tiled kernels do not take (ggml's mul_mat takes any K): K
+    not a multiple of 64, a leading dimension that breaks 16-byte rows
+    (lda = K + 3), single elements.  They run the masked kernel, against the
+    oracle; an explicit tiled configuration refuses them."""
+    print(f"gemm any M={M} N={N} K={K} lda=K+{lda_pad} {out_dtype}", flush=True)
+    a = orc.randn(SEED + 230, (M, K + lda_pad))
+    b = orc.randn(SEED + 231, (N, K), std=0.02)
+    y = dit_hip.gemm(dev_tensor(a, torch.bfloat16)[:, :K], dev_tensor(b, torch.bfloat16), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    check(host(y), orc.linear(orc.round_bf16(a[:, :K]), orc.round_bf16(b)), out_dtype, f"gemm any {M}x{N}x{K}")
+    y4 = dit_hip.gemm(dev_tensor(a, torch.bfloat16)[:, :K], dev_tensor(b, torch.bfloat16), out_dtype=out_dtype,
+                      config=4)
+    torch.cuda.synchronize()
+    assert torch.equal(y4.view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32),
+                       y.view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32))
+    with pytest.raises(RuntimeError, match="K % 64 == 0"):
+        dit_hip.gemm(dev_tensor(a, torch.bfloat16)[:, :K], dev_tensor(b, torch.bfloat16), config=0)
+
+
+def test_gemm_any_shape_equals_tiled_on_tiled_shapes(orc, dev):
+    """On a shape every kernel takes, the masked kernel accumulates k in the
+    same order as the tiled ones (k-steps of 16, ascending): bit-identical C."""
+    M, N, K = 200, 192, 256
+    a = dev_tensor(orc.randn(SEED + 232, (M, K)), torch.bfloat16)
+    b = dev_tensor(orc.randn(SEED + 233, (N, K), std=0.02), torch.bfloat16)
+    outs = [dit_hip.gemm(a, b, out_dtype=torch.float32, config=c) for c in (0, 1, 2, 4)]
+    torch.cuda.synchronize()
+    for c, o in zip((1, 2, 4), outs[1:]):
+        assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32)), f"config {c}"
     z = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
     w = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
     assert dit_hip.gemm(z, w).shape == (0, 8)
@@ -168,7 +197,8 @@ def test_q8_0_split_layout(orc, dev):
     assert np.array_equal(q8.scales.cpu().numpy(), d.T)
 
 
-Q8_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192), (300, 522, 256)]
+Q8_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192), (300, 522, 256),
+             (77, 130, 96), (40, 64, 32)]  # the last two: K % 64 == 32, the masked kernel
 
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
@@ -183,7 +213,7 @@ def test_gemm_q8_0_equals_dequant_then_gemm(orc, dev, M, N, K, out_dtype):
     _, q8, wd = _q8_weight(orc, SEED + 262, N, K)
     ad = dev_tensor(a, torch.bfloat16)
     y = dit_hip.gemm_q8_0(ad, q8, out_dtype=out_dtype)
-    y_ref = dit_hip.gemm(ad, wd, out_dtype=out_dtype, config=2)
+    y_ref = dit_hip.gemm(ad, wd, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(y, y_ref), "Q8_0 GEMM differs from dequant + bf16 GEMM"
     check(host(y), orc.linear(orc.round_bf16(a), host(wd)), out_dtype, f"gemm_q8_0 {M}x{N}x{K}")
@@ -243,6 +273,56 @@ def _attn_ref(orc, q, k, v, scale=None):
 
 
 ATTN_SHAPES = [(1, 300, 300, 3), (2, 128, 64, 2), (1, 77, 500, 1), (1, 64, 1, 2), (1, 1, 129, 4)]
+
+
+# ------------------------------------------------------------- fp32 path --
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (77, 33, 40), (300, 136, 3),
+                                   (129, 260, 12288)])
+def test_gemm_f32(orc, dev, M, N, K):
+    """F32 weights with F32 activations (the reference's own Linear precision)
+    on the fp32 matrix cores, against the oracle's linear at the fp32 bar
+    (|d| <= 1e-5 max(|ref|, 1)); with a bias and an addend; K of any size
+    (3 and 40 take the masked loads)."""
+    print(f"gemm_f32 M={M} N={N} K={K}", flush=True)
+    a = orc.randn(SEED + 280, (M, K))
+    b = orc.randn(SEED + 281, (N, K), std=0.02)
+    bias = orc.randn(SEED + 282, (N,), std=0.1)
+    add = orc.randn(SEED + 283, (M, N))
+    y = dit_hip.gemm_f32(dev_tensor(a, torch.float32), dev_tensor(b, torch.float32),
+                         bias=dev_tensor(bias, torch.float32), addend=dev_tensor(add, torch.float32))
+    torch.cuda.synchronize()
+    assert_fp32(host(y), orc.linear(a, b, bias) + add, what=f"gemm_f32 {M}x{N}x{K}")
+
+
+def test_gemm_f32_strided_in_place(orc, dev):
+    """lda = K + 4, C written into a wider buffer, and C aliasing the addend."""
+    M, N, K = 200, 96, 256
+    big_a = orc.randn(SEED + 284, (M, K + 4))
+    b = orc.randn(SEED + 285, (N, K), std=0.02)
+    c0 = orc.randn(SEED + 286, (M, N + 4))
+    cd = dev_tensor(c0, torch.float32)
+    dit_hip.gemm_f32(dev_tensor(big_a, torch.float32)[:, :K], dev_tensor(b, torch.float32), addend=cd[:, :N],
+                     out=cd[:, :N])
+    torch.cuda.synchronize()
+    got = host(cd)
+    assert_fp32(got[:, :N], orc.linear(big_a[:, :K], b) + c0[:, :N], what="gemm_f32 strided in place")
+    assert np.array_equal(got[:, N:], c0[:, N:]), "wrote past N"
+
+
+@pytest.mark.parametrize("B,Sq,Skv,H", ATTN_SHAPES + [(1, 1536, 1536, 24)])
+def test_flash_attn_f32(orc, dev, B, Sq, Skv, H):
+    """fp32 q, k, v (the reference's F32 attention): fp32 scores, softmax and
+    products, against the oracle's attention at the fp32 bar; the last shape
+    is the 1536-token single-stream block's."""
+    print(f"attn_f32 B={B} Sq={Sq} Skv={Skv} H={H}", flush=True)
+    q = orc.randn(SEED + 290, (B, Sq, H, 128))
+    k = orc.randn(SEED + 291, (B, Skv, H, 128))
+    v = orc.randn(SEED + 292, (B, Skv, H, 128))
+    o = dit_hip.flash_attn_f32(dev_tensor(q, torch.float32), dev_tensor(k, torch.float32),
+                               dev_tensor(v, torch.float32))
+    torch.cuda.synchronize()
+    ref = np.stack([orc.attention(q[i], k[i], v[i]) for i in range(B)])
+    assert_fp32(host(o), ref, what=f"attn_f32 {B}x{Sq}x{Skv}x{H}")
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])

@@ -84,3 +84,25 @@ def test_node_order_allocation_keeps_most_fusion():
     assert f["launches_held"] == 0 and p["fused_nodes"] == f["fused_nodes"]
     assert 0 < p["launches_held"] < 100, p
     assert p["fused_nodes_checked"] > 0.7 * p["fused_nodes"], p
+
+
+@pytest.mark.parametrize("path,rows,cols", [("transformer_blocks.0.attn.to_q.weight", 96, 256),
+                                            ("single_transformer_blocks.19.attn.to_out.mlp.weight", 3, 9216),
+                                            ("single_transformer_blocks.0.attn.norm_q.weight", 128, 0)])
+def test_hash_weights_match_the_oracle(orc, tmp_path, path, rows, cols):
+    """dit_cli --hash-weights draws its weights on the host by the rule the
+    oracle restates (or_hash_q8_0 / or_hash_norm_weight): the Q8_0 blocks of
+    a Linear weight and an RMSNorm weight's fp32 values are byte-identical,
+    so a full-width model run on the GPU can be checked against the oracle
+    on the same weights without shipping them."""
+    if not os.path.exists(CLI):
+        pytest.skip("dit_cli not built")
+    out = tmp_path / "w.bin"
+    args = [CLI, "HashWeights", "--seed", "11", "--path", path, "--rows", str(rows), "--out", str(out)]
+    if cols:
+        args += ["--cols", str(cols)]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    got = out.read_bytes()
+    want = orc.hash_q8_0(11, path, rows, cols) if cols else orc.hash_norm_weight(11, path, rows)
+    assert got == want.tobytes()

@@ -35,6 +35,62 @@ def test_mt19937_64_known_answer(orc):
     assert orc.mt64_nth(5489, 10000) == 9981545732273789042
 
 
+def test_hash_primitives_known_answers(orc):
+    """splitmix64's published first outputs for seed 0 (Vigna's splitmix64.c:
+    output n = mix(n * 0x9E3779B97F4A7C15)) and FNV-1a 64 test vectors."""
+    lib, G = orc.load(), 0x9E3779B97F4A7C15
+    assert lib.or_splitmix64(G) == 0xE220A8397B1DCDAF
+    assert lib.or_splitmix64((2 * G) % 2**64) == 0x6E789E6AA1B965F4
+    assert lib.or_splitmix64((3 * G) % 2**64) == 0x06C45D188009454F
+    assert lib.or_fnv1a64(b"") == 0xCBF29CE484222325
+    assert lib.or_fnv1a64(b"a") == 0xAF63DC4C8601EC8C
+    assert lib.or_fnv1a64(b"foobar") == 0x85944171F73967E8
+    assert orc.hash_key(7, "w") == lib.or_splitmix64((7 * G % 2**64) ^ lib.or_fnv1a64(b"w"))
+
+
+def test_hash_q8_0_weights(orc):
+    """The hash-drawn Q8_0 rule (dit_cli --hash-weights): block b takes
+    z(9b) for its fp16 scale and z(9b+1..8) for its codes, composed here from
+    the pinned primitives for a few blocks; codes stay in [-127, 127] with the
+    triangular law's spread (std 255/(2 sqrt 6) ~ 52.1), the scale in
+    [0x0E00, 0x0FFF]; another path or seed changes every block."""
+    lib, G = orc.load(), 0x9E3779B97F4A7C15
+    rows, cols = 96, 256
+    b = orc.hash_q8_0(3, "blocks.0.w", rows, cols).reshape(-1, 34)
+    key = orc.hash_key(3, "blocks.0.w")
+    z = lambda i: lib.or_splitmix64((key + i * G) % 2**64)
+    for blk in (0, 1, 5, rows * cols // 32 - 1):
+        d = z(9 * blk) & 0x1FF | 0x0E00
+        assert int(b[blk, 0]) | int(b[blk, 1]) << 8 == d
+        for k in range(1, 9):
+            y = [(z(9 * blk + k) >> (8 * j)) & 0xFF for j in range(8)]
+            for m in range(4):
+                q = int((y[2 * m] + y[2 * m + 1] - 255) / 2)  # truncation toward zero
+                assert np.int8(b[blk, 2 + 4 * (k - 1) + m].view(np.int8)) == q
+    codes = b[:, 2:].view(np.int8).astype(np.float64)
+    assert codes.min() >= -127 and codes.max() <= 127
+    assert abs(codes.std() - 255 / (2 * np.sqrt(6))) < 1.0 and abs(codes.mean()) < 1.0
+    dbits = b[:, 0].astype(np.int64) | b[:, 1].astype(np.int64) << 8
+    assert dbits.min() >= 0x0E00 and dbits.max() <= 0x0FFF
+    other = orc.hash_q8_0(3, "blocks.1.w", rows, cols).reshape(-1, 34)
+    assert (other != b).any(axis=1).all()
+    assert (orc.hash_q8_0(4, "blocks.0.w", rows, cols).reshape(-1, 34) != b).any(axis=1).all()
+    w = orc.dequantize(b.ravel(), rows * cols, 8)
+    assert 0.018 < w.std() < 0.026
+
+
+def test_hash_norm_weights(orc):
+    """RMSNorm weights of the rule: 1 + (top 24 bits of z(i) - 2^23) * 2^-28,
+    within 2^-5 of 1, element i from z(i)."""
+    lib, G = orc.load(), 0x9E3779B97F4A7C15
+    w = orc.hash_norm_weight(9, "attn.norm_q.weight", 128)
+    key = orc.hash_key(9, "attn.norm_q.weight")
+    for i in (0, 1, 127):
+        v = (lib.or_splitmix64((key + i * G) % 2**64) >> 40) - (1 << 23)
+        assert w[i] == np.float32(1.0) + np.float32(v * 2.0**-28)
+    assert np.all(np.abs(w - 1) <= 2.0**-5) and w.std() > 0.005
+
+
 def test_randn_is_standard_normal(orc):
     from scipy import stats
     x = orc.randn(orc.tensor_seed(0), (200_000,)).astype(np.float64)
@@ -263,6 +319,53 @@ def test_linear_vs_torch_float64(orc, M, N, K):
     assert_fp32(orc.linear(x, w), ref.numpy(), tol=1e-6, what="linear")
     assert_fp32(orc.linear(x, w, b), (ref + torch.from_numpy(b).double()).numpy(), tol=1e-6,
                 what="linear+bias")
+
+
+def test_linear_q8_0_ggml_brute_force(orc):
+    """ggml's Q8_0 mul_mat arithmetic: activation rows quantised to Q8_0,
+    exact integer block dots, each block term (float)dot * (d_x * d_w) and the
+    running sum in fp32 -- here spelled out per element in numpy from the
+    quantiser's bytes, with a bias; bit-identical."""
+    M, N, K = 7, 5, 96
+    x = orc.randn(orc.tensor_seed(56), (M, K))
+    w = orc.randn(orc.tensor_seed(57), (N, K), std=0.02)
+    b = orc.randn(orc.tensor_seed(58), (N,))
+    W = orc.Q8_0Weight(orc.quantize(w, 8), N, K)
+    qx = orc.quantize(x, 8).reshape(M, K // 32, 34)
+    qw = W.blocks.reshape(N, K // 32, 34)
+    f32 = np.float32
+    want = np.empty((M, N), np.float32)
+    for i in range(M):
+        for j in range(N):
+            s = f32(0)
+            for c in range(K // 32):
+                dot = int((qx[i, c, 2:].view(np.int8).astype(np.int64) * qw[j, c, 2:].view(np.int8)).sum())
+                d = f32(qx[i, c, :2].view(np.float16)[0]) * f32(qw[j, c, :2].view(np.float16)[0])
+                s = f32(s + f32(f32(dot) * d))
+            want[i, j] = f32(s + b[j])
+    assert np.array_equal(orc.linear(x, W, b), want)
+
+
+def test_linear_q8_0_ggml_invariants(orc):
+    """Activations that Q8_0 represents exactly (each block's amax 127 d, d an
+    fp16 value, every element d q) requantise losslessly, so the product is
+    the exact one (fp32 summation order aside); a Gaussian activation's
+    quantisation error sits at the Q8_0 level (relative L2 ~ 1/(127 sqrt 12)
+    of the block amax per element, 0.3-1% of the output here)."""
+    M, N, K = 9, 40, 256
+    rng = np.random.default_rng(5)
+    d = rng.integers(0x2000, 0x3C00, (M, K // 32)).astype(np.uint16).view(np.float16).astype(np.float32)
+    q = rng.integers(-127, 128, (M, K // 32, 32))
+    q[:, :, 0] = 127
+    x = (d[:, :, None] * q).reshape(M, K).astype(np.float32)
+    w = orc.randn(orc.tensor_seed(59), (N, K), std=0.02)
+    W = orc.Q8_0Weight(orc.quantize(w, 8), N, K)
+    wd = W.dequantize()
+    exact = x.astype(np.float64) @ wd.astype(np.float64).T
+    assert_fp32(orc.linear(x, W), exact, tol=2e-6, what="q8_0 ggml on representable activations")
+    g = orc.randn(orc.tensor_seed(60), (M, K))
+    rel = np.linalg.norm(orc.linear(g, W) - orc.linear(g, wd)) / np.linalg.norm(orc.linear(g, wd))
+    assert 2e-3 < rel < 1.5e-2, rel
 
 
 def test_linear_operand_roles(orc):
