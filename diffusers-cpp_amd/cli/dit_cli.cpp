@@ -822,9 +822,13 @@ void run_model(Session& s, const Args& a) {
     rt.set_output(*out);
 
     // --hip-graph true: the step is recorded once and replayed as a HIP graph.
-    const bool replay = a.flag("hip-graph", false);
+    // --replan true: the device-less plan (HipRuntime::plan) runs between
+    // steps, as a caller inspecting the placement would; the steps' output
+    // must not change.
+    const bool replay = a.flag("hip-graph", false), replan = a.flag("replan", false);
     std::vector<double> ms;
     for (int i = 0; i < warmup + steps; ++i) {
+        if (replan && i > 0) rt.plan();
         const auto t0 = std::chrono::steady_clock::now();
         if (replay)
             rt.compute_graph();

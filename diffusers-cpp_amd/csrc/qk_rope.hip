@@ -2,7 +2,7 @@
 // mode, adjacent pairs), the node chain RMSNorm::forward (RMS_NORM + MUL)
 // and Flux2PosEmbed::forward (4x ROPE on 32-wide views + 3x CONCAT) emit per
 // q and per k (Flux2Attention.hpp:93-122, Flux2ParallelSelfAttention.hpp:
-// 181-194, Flux2PosEmbed.hpp:29-108).
+// 52-101, Flux2PosEmbed.hpp:29-108).
 //
 // Fast path (head_dim 128, axis_dim % 8 == 0): a head is one 16-lane DPP row,
 // each lane owns 8 consecutive dims (one 16-byte bf16 load, two for fp32) =

@@ -698,7 +698,14 @@ void HipRuntime::prepare(bool allocate) {
     if (!allocate) {
         if (node_order && n) {
             // The executor's plan for this placement, on stand-in addresses
-            // (leaves apart from the arena), without a device.
+            // (leaves apart from the arena), without a device.  Every node's
+            // and leaf's data pointer is restored afterwards, so a plan()
+            // between two computes leaves the prepared placement in force.
+            std::vector<void*> saved_leaves, saved_nodes;
+            saved_leaves.reserve(leaves_.size());
+            saved_nodes.reserve(order_.size());
+            for (Node* l : leaves_) saved_leaves.push_back(l->data);
+            for (Node* t : order_) saved_nodes.push_back(t->data);
             const uintptr_t kLeafBase = (uintptr_t)1 << 44, kArenaBase = (uintptr_t)1 << 40;
             size_t off = 0;
             for (Node* l : leaves_) {
@@ -716,8 +723,8 @@ void HipRuntime::prepare(bool allocate) {
             stats_.launches_held = held;
             stats_.fused_nodes_checked = 0;
             for (int i = 0; i < n; ++i) stats_.fused_nodes_checked += cf[i] >= 0;
-            for (Node* l : leaves_) l->data = nullptr;
-            for (Node* t : order_) t->data = nullptr;
+            for (size_t i = 0; i < leaves_.size(); ++i) leaves_[i]->data = saved_leaves[i];
+            for (size_t i = 0; i < order_.size(); ++i) order_[i]->data = saved_nodes[i];
         }
         return;
     }

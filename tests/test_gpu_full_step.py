@@ -116,6 +116,18 @@ def test_full_step_node_order_allocation():
     assert cos >= 0.999
 
 
+def test_plan_between_steps_keeps_the_node_order_placement():
+    """HipRuntime::plan() (the device-less planner, which replays the
+    executor's plan on stand-in addresses) called between steps in node-order
+    placement, eager and replayed as a HIP graph: every step still runs on
+    the prepared device memory, output bit-identical to the plain run."""
+    _, on = step("node-order", "--alloc", "node-order")
+    for tag, extra in (("node-order-replan", ()), ("node-order-replan-graph", ("--hip-graph", "true"))):
+        st, o = step(tag, "--alloc", "node-order", "--replan", "true", "--steps", 2, "--warmup", 1, *extra)
+        assert st["alloc"] == "node-order"
+        assert np.array_equal(o.view(np.uint16), on.view(np.uint16)), tag
+
+
 @pytest.mark.parametrize("alloc", ["fused", "node-order"])
 def test_deep_model_both_placements_match_the_oracle(orc, alloc):
     """5 double + 20 single blocks (the full step's depth) at width 256
