@@ -9,9 +9,11 @@
 //      (sum d, sum d^2) with d = x - K (K = the group's first element, a
 //      shift that removes cancellation), fp32 over 16-byte vectors and fp64
 //      across vectors/lanes, written to its own workspace slot;
-//   2. apply: each workgroup first sums its group's partials in a fixed
-//      order (every workgroup of a group gets bit-identical statistics),
-//      then streams its chunk: y = silu(((x - mean) * rstd) * w_c + b_c).
+//   2. apply: each workgroup issues its chunk's loads, then sums its
+//      group's partials in a fixed order (every workgroup of a group gets
+//      bit-identical statistics) while those loads are in flight, then
+//      streams out y = silu(((x - mean) * rstd) * w_c + b_c).  The partials
+//      and the chunk arrive in one memory latency, not two in a row.
 // x is read twice (1.5x the algorithmic bytes).  Measured on gfx950: stats
 // loads that allocate in the caches, and running the two passes group batch
 // by group batch so the re-read could come from the 256 MB last-level cache,
@@ -99,12 +101,28 @@ __global__ __launch_bounds__(kBlock) void gn_stats_kernel(const T* __restrict__ 
     }
 }
 
-// y = silu((x - mean) * (rstd * w_c) + b_c) over this workgroup's chunk of
-// group (n, g).
+// This workgroup's chunk of group (n, g): the thread's vectors are loaded
+// (packed; see gn_stats_kernel) by gn_chunk_load, then gn_chunk_finish
+// computes y = silu((x - mean) * (rstd * w_c) + b_c) and stores it.
 template <typename T, bool VEC>
-__device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int n, int g, float mean, float rstd,
-                                               const float* __restrict__ w, const float* __restrict__ b, T* y,
-                                               FastDiv hw_vecs) {
+__device__ __forceinline__ void gn_chunk_load(const T* x, const GnShape& s, int n, int g, uint4 (&raw)[kVecsPerThread]) {
+    constexpr int EPV = VEC ? Io<T>::EPV : 1;
+    if constexpr (VEC) {
+        const T* xg = x + (int64_t)n * s.C * s.HW + (int64_t)g * s.group_len;
+        const int64_t v0 = (int64_t)blockIdx.x * kChunkVecs;
+        const int64_t v1 = v0 + kChunkVecs < s.group_vecs ? v0 + kChunkVecs : s.group_vecs;
+#pragma unroll
+        for (int i = 0; i < kVecsPerThread; ++i) {
+            const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
+            if (v < v1) raw[i] = ld_stream(xg + v * EPV);
+        }
+    }
+}
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void gn_chunk_finish(const T* x, const GnShape& s, int n, int g, float mean, float rstd,
+                                                const float* __restrict__ w, const float* __restrict__ b, T* y,
+                                                FastDiv hw_vecs, const uint4 (&raw)[kVecsPerThread]) {
     constexpr int EPV = VEC ? Io<T>::EPV : 1;
     const int64_t off = (int64_t)n * s.C * s.HW + (int64_t)g * s.group_len;
     const T* xg = x + off;
@@ -113,14 +131,6 @@ __device__ __forceinline__ void gn_apply_chunk(const T* x, const GnShape& s, int
     const int64_t v0 = (int64_t)blockIdx.x * kChunkVecs;
     int64_t v1 = v0 + kChunkVecs;
     if (v1 > s.group_vecs) v1 = s.group_vecs;
-    uint4 raw[kVecsPerThread];  // every load first, packed (see gn_stats_kernel)
-    if constexpr (VEC) {
-#pragma unroll
-        for (int i = 0; i < kVecsPerThread; ++i) {
-            const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
-            if (v < v1) raw[i] = ld_stream(xg + v * EPV);
-        }
-    }
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i) {
         const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
@@ -168,9 +178,11 @@ __global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
                                                           FastDiv hw_vecs) {
     __shared__ double red[kBlock / kWave];
     const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
+    uint4 raw[kVecsPerThread];
+    gn_chunk_load<T, VEC>(x, s, n, g, raw);
     float mean, rstd;
     gn_group_stats(ws, s, ng, red, &mean, &rstd);
-    gn_apply_chunk<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs);
+    gn_chunk_finish<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs, raw);
 }
 
 // (mean, rstd) of every group, for a consumer that applies the
@@ -229,10 +241,12 @@ __global__ __launch_bounds__(kBlock) void gn_apply_stats_kernel(const T* x, GnSh
                                                                 const float* __restrict__ b, T* y,
                                                                 FastDiv hw_vecs) {
     const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
+    uint4 raw[kVecsPerThread];
+    gn_chunk_load<T, VEC>(x, s, n, g, raw);
     const double2 r = mv[ng];
     const float mean = (float)r.x;
     const float rstd = 1.0f / sqrtf((float)r.y + s.eps);
-    gn_apply_chunk<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs);
+    gn_chunk_finish<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs, raw);
 }
 
 int64_t chunks_for(int64_t group_vecs) { return (group_vecs + kChunkVecs - 1) / kChunkVecs; }
