@@ -254,12 +254,20 @@ constexpr int EBK = 64, EROWB = EBK * 2, EOPB = 256 * EROWB, ESTAGEB = 2 * EOPB;
 
 __device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
 
-template <typename TC>
+// SCHED: the k-step's operand reads for the next step are interleaved one by
+// one between pairs of the current step's MFMAs (sched_group_barrier), so
+// the compiler keeps both operand sets live instead of reading each fragment
+// just before its MFMAs with an LDS round trip exposed.
+template <typename TC, bool SCHED>
 __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     constexpr int FM = 4, FN = 4, NS = 2;
     __shared__ __attribute__((aligned(16))) uint8_t smem[NS * ESTAGEB];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // The wave index is uniform: read it into a scalar so every LDS
+    // destination below is a scalar (M0 without a per-instruction
+    // readfirstlane).
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int tm, tn;
     const Problem& p = locate<256, 256>(grp, &tm, &tn);
     const int m0 = tm * 256, n0 = tn * 256;
@@ -267,25 +275,32 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
 
     // DMA sources: wave w fills rows [64 w, 64 w + 64) of both operands, eight
     // instructions of 8 rows each; lane i covers row + i / 8, stored chunk i % 8.
-    const uint16_t* ga[8];
-    const uint16_t* gb[8];
+    // Buffer loads to LDS: the tile's first row is the (scalar) buffer base,
+    // each lane's row and chunk a 32-bit byte offset (< 256 rows x ld x 2
+    // bytes), the k-tile a scalar offset.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.A + (int64_t)m0 * p.lda), 0, 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.B + (int64_t)n0 * p.ldb), 0, 0x7FFFFFFF, 0x00020000);
+    uint32_t oa[8], ob[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int row = 64 * wave + 8 * j + (lane >> 3);
         const int c = (lane & 7) ^ swz8(row);
-        ga[j] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + c * 8;
-        gb[j] = p.B + (int64_t)min(n0 + row, p.N - 1) * p.ldb + c * 8;
+        oa[j] = (uint32_t)(((int64_t)(min(m0 + row, p.M - 1) - m0) * p.lda + c * 8) * 2);
+        ob[j] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + c * 8) * 2);
     }
+    typedef __attribute__((address_space(3))) void* lds_ptr_t;
     auto issue = [&](int kt, int s) {
         uint8_t* base = smem + s * ESTAGEB + 64 * wave * EROWB;
-        const int k0 = kt * EBK;
+        const int koff = kt * EBK * 2;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            __builtin_amdgcn_global_load_lds(ga[j] + k0, base + 8 * j * EROWB, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(gb[j] + k0, base + EOPB + 8 * j * EROWB, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(base + 8 * j * EROWB), 16, oa[j], koff, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(base + EOPB + 8 * j * EROWB), 16, ob[j], koff,
+                                                     0, 0);
         }
     };
-
     f32x16_t acc[FN][FM];
 #pragma unroll
     for (int j = 0; j < FN; ++j)
@@ -322,6 +337,18 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
             for (int i = 0; i < FM; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
     };
+    // After read_ops(next) + mfma(current): 8 x {1 LDS read, 1 MFMA}, then
+    // the other 8 MFMAs, so the last read has 8 MFMAs to land in.
+    auto pipe = [&]() {
+        if constexpr (SCHED) {
+#pragma unroll
+            for (int r = 0; r < FN + FM; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, FN * FM - (FN + FM), 0);
+        }
+    };
 
     const int nk = p.K / EBK;
     issue(0, 0);
@@ -330,33 +357,53 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     else wait_vm<0>();
     __builtin_amdgcn_s_barrier();
     read_ops(0, 0, wa, xa);
-    // The last k-tile is peeled off so the loop body has no join between the
-    // next tile's operand reads and the MFMAs that run meanwhile.
-    for (int kt = 0; kt < nk - 1; ++kt) {
+    // One k-tile: its four k-steps, each step's MFMAs running while the next
+    // step's operands are read.  ISSUE: stage s is refilled with k-tile kt + 2
+    // after the barrier (the last two k-tiles issue nothing); the peeled last
+    // k-tile has no barrier.  Kept branch-free inside, so the DMA
+    // instructions interleave with the step-3 MFMAs.
+    auto body = [&](int kt, auto issue_next) {
         const int s = kt & 1;
         read_ops(s, 1, wb, xb);
         mfma(wa, xa);
+        pipe();
         read_ops(s, 2, wa, xa);
         mfma(wb, xb);
+        pipe();
         read_ops(s, 3, wb, xb);
         mfma(wa, xa);
+        pipe();
         // Stage s is refilled with k-tile kt + 2 once every wave's reads of
         // it have returned; k-tile kt + 1 (the other stage) must have landed.
         wait_vm<0>();
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
-        if (kt + 2 < nk) issue(kt + 2, s);
+        if constexpr (decltype(issue_next)::value) issue(kt + 2, s);
         read_ops(s ^ 1, 0, wa, xa);
         mfma(wb, xb);
-    }
+        if constexpr (SCHED) {
+            // the DMA instructions one per MFMA, then the next step's reads
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if constexpr (decltype(issue_next)::value)
+                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (DMA)
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
+            }
+        }
+    };
+    for (int kt = 0; kt < nk - 2; ++kt) body(kt, std::true_type{});
+    if (nk >= 2) body(nk - 2, std::false_type{});
     {
         const int s = (nk - 1) & 1;
         read_ops(s, 1, wb, xb);
         mfma(wa, xa);
+        pipe();
         read_ops(s, 2, wa, xa);
         mfma(wb, xb);
+        pipe();
         read_ops(s, 3, wb, xb);
         mfma(wa, xa);
+        pipe();
         mfma(wb, xb);
     }
     epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
@@ -734,10 +781,11 @@ struct Config {
 };
 // 0: 256 x 256, 8 waves, K = 32 stages (one workgroup per CU); 1: 128 x 128
 // (two per CU); 2: 256 x 256, 4 waves, K = 64 stages; 3: Q8_0 weights,
-// 256 x 256, 8 waves, K = 64, three stages; 4: any shape (masked, 128 x 128).
-constexpr int kAnyConfig = 4;
-constexpr Config kConfigs[5] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
-                                {256, 256, 512, 1, 1.0}, {128, 128, 256, 2, 0.1}};
+// 256 x 256, 8 waves, K = 64, three stages; 4: any shape (masked, 128 x 128);
+// 5: config 2 with the operand reads interleaved into the MFMA stream.
+constexpr int kAnyConfig = 4, kLastConfig = 5;
+constexpr Config kConfigs[6] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
+                                {256, 256, 512, 1, 1.0},  {128, 128, 256, 2, 0.1}, {256, 256, 256, 1, 1.3}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -745,15 +793,15 @@ int64_t tiles_of(const Problem& p, int cfg) {
 }
 
 // Estimated time: ceil(tiles / concurrent workgroups) waves, each lasting the
-// tile area x workgroups per CU / the per-CU rate, between the 256 x 256 and
-// 128 x 128 tiles.  Among the 256 x 256 kernels the K = 64 one streams whole
-// L2 lines and wins on long K (gfx950, M = 4608: +4-6% at K >= 6144); at
-// K = 3072 the 8-wave kernel is as fast or faster, also for the grouped
-// q/k/v/gate/up projections of a single-stream block (814 vs 855 us).
+// tile area x workgroups per CU / the per-CU rate, between the 256 x 256
+// tiles (the scheduled K = 64 kernel, config 5: on gfx950 at M = 4608 it runs
+// 1.01-1.14 PFLOP/s against 0.80-0.94 for the 8-wave kernel and 0.86-0.97
+// for the unscheduled K = 64 kernel, bit-identical to the latter) and the
+// 128 x 128 tiles.
 int pick_config(const Problem* ps, int n, int cus) {
     int best = 1;
     double best_t = 1e300;
-    for (int cfg = 0; cfg < 2; ++cfg) {
+    for (int cfg : {5, 1}) {
         const Config c = kConfigs[cfg];
         int64_t tiles = 0;
         for (int i = 0; i < n; ++i) tiles += tiles_of(ps[i], cfg);
@@ -764,11 +812,6 @@ int pick_config(const Problem* ps, int n, int cus) {
             best_t = t;
             best = cfg;
         }
-    }
-    if (best == 0) {
-        int max_k = 0;
-        for (int i = 0; i < n; ++i) max_k = max(max_k, ps[i].K);
-        if (max_k >= 6144) best = 2;
     }
     return best;
 }
@@ -790,7 +833,9 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
     if (cfg == 0)
         hipLaunchKernelGGL((gemm_dma256_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == 2)
-        hipLaunchKernelGGL((gemm_k64_kernel<TC>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, false>), grid, block, 0, st, g);
+    else if (cfg == 5)
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, true>), grid, block, 0, st, g);
     else if (cfg == 3)
         hipLaunchKernelGGL((gemm_q8_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == kAnyConfig && ps[0].Bs)
@@ -840,7 +885,7 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
                                     int32_t config, dt_stream_t stream) {
     using namespace dit;
     DT_REQUIRE(c_type == DT_TYPE_BF16 || c_type == DT_TYPE_F32, "dt_gemm_bf16: c_type %d unsupported", c_type);
-    DT_REQUIRE(config >= -1 && config <= kAnyConfig, "dt_gemm_bf16: config %d out of range", config);
+    DT_REQUIRE(config >= -1 && config <= kLastConfig, "dt_gemm_bf16: config %d out of range", config);
     DT_REQUIRE(count >= 0 && count <= kMaxGroup, "dt_gemm_bf16_grouped: count %d outside 0..%d", count,
                kMaxGroup);
     DT_REQUIRE(problems || count == 0, "dt_gemm_bf16_grouped: null problem list");
