@@ -238,30 +238,40 @@ __global__ __launch_bounds__(512) void gemm_dma256_kernel(const Group grp) {
     epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
 }
 
-// ---- 256 x 256, 4 waves of 128 x 128, K = 64 per stage, 2 stages -------------
-// Each wave owns a 128 x 128 quarter of the tile (4 x 4 blocks of 32 x 32,
-// 256 fp32 accumulators, one wave per SIMD): per k-step it reads 8 operands
-// for 16 MFMAs, against 6 for 8 in the 8-wave kernel, which keeps the LDS
-// port that the DMA writes share below the MFMA time.
+// ---- BM x 256, 4 waves, K = 64 per stage, 2 stages ----------------------------
+// BM = 256: each wave owns a 128 x 128 quarter of the tile (4 x 4 blocks of
+// 32 x 32, 256 fp32 accumulators, one wave per SIMD): per k-step it reads 8
+// operands for 16 MFMAs, against 6 for 8 in the 8-wave kernel, which keeps
+// the LDS port that the DMA writes share below the MFMA time.
+// BM = 224 (7 blocks of 32): the four waves side by side along n, each
+// 224 x 64 (7 x 2 blocks, 224 accumulators, 9 operand reads for 14 MFMAs).
+// M = 4608 then makes 21 tile rows, so a 4608 x 3072 product is 252 tiles on
+// the 256 CUs instead of 216 256 x 256 tiles (16% of the CUs idle).
 // Rows of 64 bf16 = 128 bytes per stage, so each DMA row segment is one whole
 // L2 line (the 64-byte segments of K = 32 stages issue twice the requests and
 // feed LDS at ~14 TB/s against ~22 TB/s with full lines, measured on gfx950
-// for this tile shape).  Two stages of 64 KB; chunk c of row r is stored at
-// chunk c ^ swz8(r), swz8(r) = (r ^ (r >> 3)) & 7, so the 16-byte reads of 8
-// (32-bank) or 16 (64-bank) consecutive rows at one logical chunk hit
-// distinct banks.  Operand reads are software-pipelined one k-step ahead.
-constexpr int EBK = 64, EROWB = EBK * 2, EOPB = 256 * EROWB, ESTAGEB = 2 * EOPB;
+// for this tile shape).  Two stages of (BM + 256) x 128 bytes; chunk c of row
+// r is stored at chunk c ^ swz8(r), swz8(r) = (r ^ (r >> 3)) & 7, so the
+// 16-byte reads of 8 (32-bank) or 16 (64-bank) consecutive rows at one
+// logical chunk hit distinct banks.  Operand reads are software-pipelined one
+// k-step ahead.
+constexpr int EBK = 64, EROWB = EBK * 2;
 
 __device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
 
-// SCHED: the k-step's operand reads for the next step are interleaved one by
-// one between pairs of the current step's MFMAs (sched_group_barrier), so
-// the compiler keeps both operand sets live instead of reading each fragment
-// just before its MFMAs with an LDS round trip exposed.
-template <typename TC, bool SCHED>
+// SCHED: the next k-step's operand reads are interleaved one by one into the
+// current step's MFMAs, and the stage DMA one instruction per MFMA after the
+// barrier (sched_group_barrier), so the compiler keeps both operand sets
+// live instead of reading each fragment just before its MFMAs with an LDS
+// round trip exposed.
+template <typename TC, bool SCHED, int BM>
 __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
-    constexpr int FM = 4, FN = 4, NS = 2;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * ESTAGEB];
+    static_assert(BM == 256 || BM == 224, "tile height");
+    constexpr int WAVES_M = BM == 256 ? 2 : 1, WAVES_N = 4 / WAVES_M;
+    constexpr int FM = BM / WAVES_M / 32, FN = 256 / WAVES_N / 32;
+    constexpr int AOPB = BM * EROWB, STAGEB = AOPB + 256 * EROWB, NS = 2;
+    constexpr int A_DMA = BM / 4 / 8;  // A rows per wave / 8 rows per DMA instruction
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGEB];
 
     const int tid = threadIdx.x, lane = tid & 63;
     // The wave index is uniform: read it into a scalar so every LDS
@@ -269,36 +279,43 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     // readfirstlane).
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int tm, tn;
-    const Problem& p = locate<256, 256>(grp, &tm, &tn);
-    const int m0 = tm * 256, n0 = tn * 256;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const Problem& p = locate<BM, 256>(grp, &tm, &tn);
+    const int m0 = tm * BM, n0 = tn * 256;
+    const int wm = (wave / WAVES_N) * (BM / WAVES_M), wn = (wave % WAVES_N) * (256 / WAVES_N);
 
-    // DMA sources: wave w fills rows [64 w, 64 w + 64) of both operands, eight
-    // instructions of 8 rows each; lane i covers row + i / 8, stored chunk i % 8.
-    // Buffer loads to LDS: the tile's first row is the (scalar) buffer base,
-    // each lane's row and chunk a 32-bit byte offset (< 256 rows x ld x 2
-    // bytes), the k-tile a scalar offset.
+    // DMA sources: wave w fills A rows [BM/4 w, +BM/4) and B rows [64 w,
+    // +64), instructions of 8 rows each; lane i covers row + i / 8, stored
+    // chunk i % 8.  Buffer loads to LDS: the tile's first row is the
+    // (scalar) buffer base, each lane's row and chunk a 32-bit byte offset
+    // (< 256 rows x ld x 2 bytes), the k-tile a scalar offset.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.A + (int64_t)m0 * p.lda), 0, 0x7FFFFFFF, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.B + (int64_t)n0 * p.ldb), 0, 0x7FFFFFFF, 0x00020000);
-    uint32_t oa[8], ob[8];
+    uint32_t oa[8], ob[8];  // oa: the first A_DMA used (a fixed size: captured by the lambdas below)
+#pragma unroll
+    for (int j = 0; j < A_DMA; ++j) {
+        const int row = (BM / 4) * wave + 8 * j + (lane >> 3);
+        const int c = (lane & 7) ^ swz8(row);
+        oa[j] = (uint32_t)(((int64_t)(min(m0 + row, p.M - 1) - m0) * p.lda + c * 8) * 2);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int row = 64 * wave + 8 * j + (lane >> 3);
         const int c = (lane & 7) ^ swz8(row);
-        oa[j] = (uint32_t)(((int64_t)(min(m0 + row, p.M - 1) - m0) * p.lda + c * 8) * 2);
         ob[j] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + c * 8) * 2);
     }
     typedef __attribute__((address_space(3))) void* lds_ptr_t;
     auto issue = [&](int kt, int s) {
-        uint8_t* base = smem + s * ESTAGEB + 64 * wave * EROWB;
+        uint8_t* abase = smem + s * STAGEB + (BM / 4) * wave * EROWB;
+        uint8_t* bbase = smem + s * STAGEB + AOPB + 64 * wave * EROWB;
         const int koff = kt * EBK * 2;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(base + 8 * j * EROWB), 16, oa[j], koff, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(base + EOPB + 8 * j * EROWB), 16, ob[j], koff,
-                                                     0, 0);
+        for (int j = 0; j < 8; ++j) {  // A and B rows alternately
+            if (j < A_DMA)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(abase + 8 * j * EROWB), 16, oa[j], koff, 0,
+                                                         0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(bbase + 8 * j * EROWB), 16, ob[j], koff, 0, 0);
         }
     };
     f32x16_t acc[FN][FM];
@@ -311,8 +328,7 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
 
     const int lrow = lane & 31, g = lane >> 5;
     // Per-fragment swizzle of the rows this lane reads (rows wn + 32 j + lrow
-    // and wm + 32 i + lrow; 32 j only changes bit 5, which swz8 ignores except
-    // through r >> 3).
+    // and wm + 32 i + lrow).
     int sb[FN], sa[FM];
 #pragma unroll
     for (int j = 0; j < FN; ++j) sb[j] = swz8(wn + 32 * j + lrow);
@@ -320,8 +336,8 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     for (int i = 0; i < FM; ++i) sa[i] = swz8(wm + 32 * i + lrow);
     bf16x8_t wa[FN], xa[FM], wb[FN], xb[FM];
     auto read_ops = [&](int s, int kk, bf16x8_t (&wf)[FN], bf16x8_t (&xf)[FM]) {
-        const uint8_t* As = smem + s * ESTAGEB;
-        const uint8_t* Bs = As + EOPB;
+        const uint8_t* As = smem + s * STAGEB;
+        const uint8_t* Bs = As + AOPB;
         const int c = 2 * kk + g;
 #pragma unroll
         for (int j = 0; j < FN; ++j)
@@ -337,8 +353,8 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
             for (int i = 0; i < FM; ++i)
                 acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j], xf[i], acc[j][i], 0, 0, 0);
     };
-    // After read_ops(next) + mfma(current): 8 x {1 LDS read, 1 MFMA}, then
-    // the other 8 MFMAs, so the last read has 8 MFMAs to land in.
+    // After read_ops(next) + mfma(current): {1 LDS read, 1 MFMA} per operand,
+    // then the remaining MFMAs, so the last read has several MFMAs to land in.
     auto pipe = [&]() {
         if constexpr (SCHED) {
 #pragma unroll
@@ -353,7 +369,7 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     const int nk = p.K / EBK;
     issue(0, 0);
     if (nk > 1) issue(1, 1);
-    if (nk > 1) wait_vm<16>();
+    if (nk > 1) wait_vm<A_DMA + 8>();
     else wait_vm<0>();
     __builtin_amdgcn_s_barrier();
     read_ops(0, 0, wa, xa);
@@ -383,11 +399,11 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
         mfma(wb, xb);
         if constexpr (SCHED) {
             // the DMA instructions one per MFMA, then the next step's reads
+            constexpr int NDMA = decltype(issue_next)::value ? A_DMA + 8 : 0;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if constexpr (decltype(issue_next)::value)
-                    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read (DMA)
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
+            for (int r = 0; r < (NDMA > FN * FM ? NDMA : FN * FM); ++r) {
+                if (r < NDMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read (DMA)
+                if (r < FN * FM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             }
         }
     };
@@ -782,10 +798,12 @@ struct Config {
 // 0: 256 x 256, 8 waves, K = 32 stages (one workgroup per CU); 1: 128 x 128
 // (two per CU); 2: 256 x 256, 4 waves, K = 64 stages; 3: Q8_0 weights,
 // 256 x 256, 8 waves, K = 64, three stages; 4: any shape (masked, 128 x 128);
-// 5: config 2 with the operand reads interleaved into the MFMA stream.
-constexpr int kAnyConfig = 4, kLastConfig = 5;
-constexpr Config kConfigs[6] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
-                                {256, 256, 512, 1, 1.0},  {128, 128, 256, 2, 0.1}, {256, 256, 256, 1, 1.3}};
+// 5: config 2 with the operand reads interleaved into the MFMA stream; 6: the
+// same at 224 x 256.
+constexpr int kAnyConfig = 4, kLastConfig = 6;
+constexpr Config kConfigs[7] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
+                                {256, 256, 512, 1, 1.0},  {128, 128, 256, 2, 0.1}, {256, 256, 256, 1, 1.3},
+                                {224, 256, 256, 1, 1.2}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -799,6 +817,16 @@ int64_t tiles_of(const Problem& p, int cfg) {
 // for the unscheduled K = 64 kernel, bit-identical to the latter) and the
 // 128 x 128 tiles.
 int pick_config(const Problem* ps, int n, int cus) {
+    // 224 x 256 tiles when the 256 x 256 ones fill half to all but a few of
+    // the CUs in their only wave and the 224-row tiles still fit in one (e.g.
+    // M = 4608 or 4096, N = 3072: 216 or 192 tiles -> 252 or 228; measured
+    // 3-6% faster).
+    int64_t t5 = 0, t6 = 0;
+    for (int i = 0; i < n; ++i) {
+        t5 += tiles_of(ps[i], 5);
+        t6 += tiles_of(ps[i], 6);
+    }
+    if (2 * t5 >= cus && t5 < cus && t6 > t5 && t6 <= cus) return 6;
     int best = 1;
     double best_t = 1e300;
     for (int cfg : {5, 1}) {
@@ -833,9 +861,11 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
     if (cfg == 0)
         hipLaunchKernelGGL((gemm_dma256_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == 2)
-        hipLaunchKernelGGL((gemm_k64_kernel<TC, false>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, false, 256>), grid, block, 0, st, g);
     else if (cfg == 5)
-        hipLaunchKernelGGL((gemm_k64_kernel<TC, true>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 256>), grid, block, 0, st, g);
+    else if (cfg == 6)
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 224>), grid, block, 0, st, g);
     else if (cfg == 3)
         hipLaunchKernelGGL((gemm_q8_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == kAnyConfig && ps[0].Bs)

@@ -57,7 +57,7 @@ def test_quantize_q8_0_strided_rows(orc, dev):
 GEMM_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192)]
 
 
-@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5])
+@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5, 6])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 def test_gemm(orc, dev, M, N, K, out_dtype, config):
@@ -71,7 +71,7 @@ def test_gemm(orc, dev, M, N, K, out_dtype, config):
     check(host(y), ref, out_dtype, f"gemm {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 5])
+@pytest.mark.parametrize("config", [0, 1, 2, 5, 6])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_gemm_strided_bias_addend(orc, dev, out_dtype, config):
     M, N, K = 300, 384, 512
@@ -104,7 +104,7 @@ def test_gemm_in_place_addend(orc, dev):
     assert_fp32(host(c), orc.linear(orc.round_bf16(a), orc.round_bf16(b)) + c0, what="gemm in-place")
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 5])
+@pytest.mark.parametrize("config", [0, 1, 2, 5, 6])
 def test_gemm_large_sampled_rows(orc, dev, config):
     """4608 x 3072 x 3072 (a Flux2 block's attention projection); 88 rows
     spread over every row tile are checked against the oracle."""
@@ -119,7 +119,7 @@ def test_gemm_large_sampled_rows(orc, dev, config):
     assert_fp32(host(y)[rows], ref, what="gemm 4608x3072x3072")
 
 
-@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5])
+@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5, 6])
 def test_gemm_grouped(orc, dev, config):
     """Five GEMMs of different N and K (and an empty one) in one launch, each
     against the oracle: the q/k/v/gate/up pattern plus ragged edges."""
@@ -166,9 +166,9 @@ def test_gemm_any_shape_equals_tiled_on_tiled_shapes(orc, dev):
     M, N, K = 200, 192, 256
     a = dev_tensor(orc.randn(SEED + 232, (M, K)), torch.bfloat16)
     b = dev_tensor(orc.randn(SEED + 233, (N, K), std=0.02), torch.bfloat16)
-    outs = [dit_hip.gemm(a, b, out_dtype=torch.float32, config=c) for c in (0, 1, 2, 4, 5)]
+    outs = [dit_hip.gemm(a, b, out_dtype=torch.float32, config=c) for c in (0, 1, 2, 4, 5, 6)]
     torch.cuda.synchronize()
-    for c, o in zip((1, 2, 4, 5), outs[1:]):
+    for c, o in zip((1, 2, 4, 5, 6), outs[1:]):
         assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32)), f"config {c}"
     z = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
     w = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
