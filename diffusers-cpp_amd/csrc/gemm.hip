@@ -457,45 +457,57 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(const Group grp) {
     constexpr int FM = 4, FN = 2;  // wave sub-tile 128 (m) x 64 (n)
     __shared__ __attribute__((aligned(16))) uint8_t smem[QSTAGES * QSTAGEB];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar LDS destinations
     int tm, tn;
     const Problem& p = locate<256, 256>(grp, &tm, &tn);
     const int m0 = tm * 256, n0 = tn * 256;
     const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
-    const uint8_t* Bq = reinterpret_cast<const uint8_t*>(p.B);
 
     // DMA sources.  A: wave w fills rows [32 w, +32), 4 instructions of 8 rows
     // (lane i: row + i / 8, chunk i % 8).  B: the same rows, 2 instructions of
     // 16 rows (lane i: row + i / 4, chunk i % 4).  Scales: the 64 scales of
     // k-block w / 4 for rows 64 (w % 4) + i, 4 bytes a lane, so every wave
-    // issues the same QDMA instructions with every lane active.
-    const uint16_t* ga[4];
-    const uint8_t* gb[2];
+    // issues the same QDMA instructions with every lane active.  Buffer loads
+    // to LDS: the tile's first row (first scale) is the scalar buffer base,
+    // each lane's part a 32-bit byte offset, the k-tile a scalar offset.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(p.A + (int64_t)m0 * p.lda), 0, 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(p.B) + (int64_t)n0 * p.ldb), 0, 0x7FFFFFFF,
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.Bs), 0, 0x7FFFFFFF, 0x00020000);
+    uint32_t oa[4], ob[2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int row = 32 * wave + 8 * j + (lane >> 3);
         const int c = (lane & 7) ^ swz8(row);
-        ga[j] = p.A + (int64_t)min(m0 + row, p.M - 1) * p.lda + c * 8;
+        oa[j] = (uint32_t)(((int64_t)(min(m0 + row, p.M - 1) - m0) * p.lda + c * 8) * 2);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int row = 32 * wave + 16 * j + (lane >> 2);
         const int c = (lane & 3) ^ qswz(row);
-        gb[j] = Bq + (int64_t)min(n0 + row, p.N - 1) * p.ldb + c * 16;
+        ob[j] = (uint32_t)((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + c * 16);
     }
     const int sblk = wave >> 2;
-    const float* gs = p.Bs + (int64_t)sblk * p.ldbs + min(n0 + 64 * (wave & 3) + lane, p.N - 1);
+    const uint32_t os = (uint32_t)(((int64_t)sblk * p.ldbs + min(n0 + 64 * (wave & 3) + lane, p.N - 1)) * 4);
     const int s_lds = QA_OPB + QB_OPB + sblk * 1024 + 256 * (wave & 3);
+    typedef __attribute__((address_space(3))) void* lds_ptr_t;
     auto issue = [&](int kt, int s) {
         uint8_t* st = smem + s * QSTAGEB;
         const int k0 = kt * QBK;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            __builtin_amdgcn_global_load_lds(ga[j] + k0, st + (32 * wave + 8 * j) * QA_ROWB, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (32 * wave + 8 * j) * QA_ROWB), 16, oa[j],
+                                                     k0 * 2, 0, 0);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            __builtin_amdgcn_global_load_lds(gb[j] + k0, st + QA_OPB + (32 * wave + 16 * j) * QB_ROWB, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(gs + (int64_t)(2 * kt) * p.ldbs, st + s_lds, 4, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(st + QA_OPB + (32 * wave + 16 * j) * QB_ROWB),
+                                                     16, ob[j], k0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(st + s_lds), 4, os,
+                                                 (int)((int64_t)(2 * kt) * p.ldbs * 4), 0, 0);
     };
 
     f32x16_t acc[FN][FM];
