@@ -151,17 +151,30 @@ __device__ __forceinline__ void gn_chunk_finish(const T* x, const GnShape& s, in
 }
 
 // Group ng's (mean, rstd) from its stats partials, summed in a fixed order
-// by the whole workgroup (every caller gets bit-identical values).
+// (every caller gets bit-identical values).  Up to one partial per lane:
+// each wave sums them itself (an xor butterfly, whose every lane ends with
+// the same value), so the small maps' apply pass has no LDS round trip or
+// barrier before its math; more partials: the whole workgroup, through LDS.
 __device__ __forceinline__ void gn_group_stats(const double* __restrict__ ws, const GnShape& s, int ng,
                                                double* red, float* mean, float* rstd) {
     const double* slot = ws + (int64_t)ng * (2 * s.nchunks + 1);
     double s1 = 0.0, s2 = 0.0;
-    for (int i = threadIdx.x; i < s.nchunks; i += kBlock) {
-        s1 += slot[1 + 2 * i];
-        s2 += slot[2 + 2 * i];
+    if (s.nchunks <= kWave) {
+        const int lane = threadIdx.x & (kWave - 1);
+        if (lane < s.nchunks) {
+            s1 = slot[1 + 2 * lane];
+            s2 = slot[2 + 2 * lane];
+        }
+        s1 = wave_sum_f64(s1);
+        s2 = wave_sum_f64(s2);
+    } else {
+        for (int i = threadIdx.x; i < s.nchunks; i += kBlock) {
+            s1 += slot[1 + 2 * i];
+            s2 += slot[2 + 2 * i];
+        }
+        s1 = block_sum_f64(s1, red);
+        s2 = block_sum_f64(s2, red);
     }
-    s1 = block_sum_f64(s1, red);
-    s2 = block_sum_f64(s2, red);
     const double inv_len = 1.0 / (double)s.group_len;
     const double dm = s1 * inv_len;
     double var = s2 * inv_len - dm * dm;
