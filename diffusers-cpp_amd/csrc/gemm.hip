@@ -36,6 +36,7 @@
 // groups of GROUP_M tile rows so concurrently running tiles share A rows and
 // B columns.  Rows past M or N load a clamped valid row: their products only
 // reach C entries that are never stored.
+#include <initializer_list>
 #include <type_traits>
 
 #include "capi_util.hpp"
@@ -626,10 +627,16 @@ __global__ __launch_bounds__(512) void gemm_q8_kernel(const Group grp) {
 }
 
 // ---- 128 x 128, register-staged, 2 stages --------------------------------------
+// Q8: the weight operand in the split layout (uint8 codes u = q + 128 and fp32
+// block scales), dequantised as it is staged: each thread converts 16 codes of
+// one row, w = fma(u, d, -128 d) = d * q (exact) rounded to bf16 -- the value
+// dt_dequant writes -- so LDS holds the bf16 operand and the MFMA sequence is
+// the bf16 kernel's.  Products with few 256 x 256 tiles (the 512 text tokens)
+// keep four times as many workgroups as gemm_q8_kernel.
 constexpr int SBK = 64;
 constexpr int SLDSW = SBK + 8;  // padded LDS row, in bf16 elements
 
-template <typename TC>
+template <typename TC, bool Q8 = false>
 __global__ __launch_bounds__(256) void gemm_128_kernel(const Group grp) {
     constexpr int FM = 2, FN = 2, T = 256;
     constexpr int CH = 128 * (SBK / 8) / T;  // 16-byte chunks per thread per operand
@@ -658,15 +665,47 @@ __global__ __launch_bounds__(256) void gemm_128_kernel(const Group grp) {
     }
     uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
     static_assert(CH == 4, "four chunks per thread per operand");
+    // Q8: thread t stages codes [16 (t % 4), +16) of weight rows t / 4 and
+    // t / 4 + 64, with their block scales.
+    const int qr = tid >> 2, qc = tid & 3;
+    const uint8_t* gq = reinterpret_cast<const uint8_t*>(Bp) + (int64_t)min(n0 + qr, Nx) * ldb + 16 * qc;
+    const int64_t oq = ((int64_t)min(n0 + qr + 64, Nx) - min(n0 + qr, Nx)) * ldb;
+    const float* gs = Q8 ? p.Bs + min(n0 + qr, Nx) : nullptr;
+    const int64_t os = (int64_t)min(n0 + qr + 64, Nx) - min(n0 + qr, Nx);
+    float sq0 = 0.f, sq1 = 0.f;
     auto fetch = [&](int k0) {
         ra0 = *reinterpret_cast<const uint4*>(ga + oa[0] + k0);
         ra1 = *reinterpret_cast<const uint4*>(ga + oa[1] + k0);
         ra2 = *reinterpret_cast<const uint4*>(ga + oa[2] + k0);
         ra3 = *reinterpret_cast<const uint4*>(ga + oa[3] + k0);
-        rb0 = *reinterpret_cast<const uint4*>(gb + ob[0] + k0);
-        rb1 = *reinterpret_cast<const uint4*>(gb + ob[1] + k0);
-        rb2 = *reinterpret_cast<const uint4*>(gb + ob[2] + k0);
-        rb3 = *reinterpret_cast<const uint4*>(gb + ob[3] + k0);
+        if constexpr (Q8) {
+            rb0 = *reinterpret_cast<const uint4*>(gq + k0);
+            rb1 = *reinterpret_cast<const uint4*>(gq + oq + k0);
+            const int64_t blk = (k0 + 16 * qc) >> 5;
+            sq0 = gs[blk * p.ldbs];
+            sq1 = gs[blk * p.ldbs + os];
+        } else {
+            rb0 = *reinterpret_cast<const uint4*>(gb + ob[0] + k0);
+            rb1 = *reinterpret_cast<const uint4*>(gb + ob[1] + k0);
+            rb2 = *reinterpret_cast<const uint4*>(gb + ob[2] + k0);
+            rb3 = *reinterpret_cast<const uint4*>(gb + ob[3] + k0);
+        }
+    };
+    // 16 codes -> 16 bf16 weights (two 16-byte chunks)
+    auto dq16 = [&](const uint4& u, float d, uint16_t* dst) {
+        const float m = -128.0f * d;
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+        uint32_t pk[8];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            float w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = __builtin_fmaf((float)((w4[h] >> (8 * e)) & 0xFFu), d, m);
+            pk[2 * h] = pack_bf16x2(w[0], w[1]);
+            pk[2 * h + 1] = pack_bf16x2(w[2], w[3]);
+        }
+        *reinterpret_cast<uint4*>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        *reinterpret_cast<uint4*>(dst + 8) = make_uint4(pk[4], pk[5], pk[6], pk[7]);
     };
     auto stash = [&](int s) {
         uint16_t* As = smem + s * STAGE + row0 * SLDSW + kc * 8;
@@ -676,10 +715,16 @@ __global__ __launch_bounds__(256) void gemm_128_kernel(const Group grp) {
         *reinterpret_cast<uint4*>(As + RS) = ra1;
         *reinterpret_cast<uint4*>(As + 2 * RS) = ra2;
         *reinterpret_cast<uint4*>(As + 3 * RS) = ra3;
-        *reinterpret_cast<uint4*>(Bs) = rb0;
-        *reinterpret_cast<uint4*>(Bs + RS) = rb1;
-        *reinterpret_cast<uint4*>(Bs + 2 * RS) = rb2;
-        *reinterpret_cast<uint4*>(Bs + 3 * RS) = rb3;
+        if constexpr (Q8) {
+            uint16_t* Bq = smem + s * STAGE + 128 * SLDSW + qr * SLDSW + 16 * qc;
+            dq16(rb0, sq0, Bq);
+            dq16(rb1, sq1, Bq + 64 * SLDSW);
+        } else {
+            *reinterpret_cast<uint4*>(Bs) = rb0;
+            *reinterpret_cast<uint4*>(Bs + RS) = rb1;
+            *reinterpret_cast<uint4*>(Bs + 2 * RS) = rb2;
+            *reinterpret_cast<uint4*>(Bs + 3 * RS) = rb3;
+        }
     };
 
     f32x16_t acc[FN][FM];
@@ -828,20 +873,11 @@ int64_t tiles_of(const Problem& p, int cfg) {
 // 1.01-1.14 PFLOP/s against 0.80-0.94 for the 8-wave kernel and 0.86-0.97
 // for the unscheduled K = 64 kernel, bit-identical to the latter) and the
 // 128 x 128 tiles.
-int pick_config(const Problem* ps, int n, int cus) {
-    // 224 x 256 tiles when the 256 x 256 ones fill half to all but a few of
-    // the CUs in their only wave and the 224-row tiles still fit in one (e.g.
-    // M = 4608 or 4096, N = 3072: 216 or 192 tiles -> 252 or 228; measured
-    // 3-6% faster).
-    int64_t t5 = 0, t6 = 0;
-    for (int i = 0; i < n; ++i) {
-        t5 += tiles_of(ps[i], 5);
-        t6 += tiles_of(ps[i], 6);
-    }
-    if (2 * t5 >= cus && t5 < cus && t6 > t5 && t6 <= cus) return 6;
-    int best = 1;
+// Whole-wave cost model: waves of tiles x tile area x workgroups per CU / rate.
+int pick_by_waves(const Problem* ps, int n, int cus, std::initializer_list<int> cands) {
+    int best = *cands.begin();
     double best_t = 1e300;
-    for (int cfg : {5, 1}) {
+    for (int cfg : cands) {
         const Config c = kConfigs[cfg];
         int64_t tiles = 0;
         for (int i = 0; i < n; ++i) tiles += tiles_of(ps[i], cfg);
@@ -854,6 +890,26 @@ int pick_config(const Problem* ps, int n, int cus) {
         }
     }
     return best;
+}
+
+// Q8_0 weights: 256 x 256 tiles (gemm_q8_kernel) or, when those leave most
+// CUs idle (the 512 text tokens' products, a 128-column output), 128 x 128
+// tiles dequantised as they are staged (measured 1.9x faster at 512 x 3072 x
+// 9216, 10% slower at 512 x 18432 x 3072, where 256 x 256 gives 144 tiles).
+int pick_config_q8(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {3, 1}); }
+
+int pick_config(const Problem* ps, int n, int cus) {
+    // 224 x 256 tiles when the 256 x 256 ones fill half to all but a few of
+    // the CUs in their only wave and the 224-row tiles still fit in one (e.g.
+    // M = 4608 or 4096, N = 3072: 216 or 192 tiles -> 252 or 228; measured
+    // 3-6% faster).
+    int64_t t5 = 0, t6 = 0;
+    for (int i = 0; i < n; ++i) {
+        t5 += tiles_of(ps[i], 5);
+        t6 += tiles_of(ps[i], 6);
+    }
+    if (2 * t5 >= cus && t5 < cus && t6 > t5 && t6 <= cus) return 6;
+    return pick_by_waves(ps, n, cus, {5, 1});
 }
 
 template <typename TC>
@@ -884,6 +940,8 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
         hipLaunchKernelGGL((gemm_any_kernel<TC, true>), grid, block, 0, st, g);
     else if (cfg == kAnyConfig)
         hipLaunchKernelGGL((gemm_any_kernel<TC, false>), grid, block, 0, st, g);
+    else if (ps[0].Bs)
+        hipLaunchKernelGGL((gemm_128_kernel<TC, true>), grid, block, 0, st, g);
     else
         hipLaunchKernelGGL((gemm_128_kernel<TC>), grid, block, 0, st, g);
     return check_launch("dt_gemm_bf16");
@@ -946,12 +1004,15 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
         }
     }
     DT_REQUIRE(n_q8 == 0 || n_q8 == count, "dt_gemm_bf16_grouped: a group mixes Q8_0 and bf16 weights");
-    DT_REQUIRE(config == -1 || config == kAnyConfig || (n_q8 > 0) == (config == 3),
+    DT_REQUIRE(config == -1 || config == kAnyConfig || config == 1 || (n_q8 > 0) == (config == 3),
                "dt_gemm_bf16: config %d does not take %s weights", config, n_q8 ? "Q8_0" : "bf16");
     DT_REQUIRE(config == -1 || config == kAnyConfig || all_tiled,
                "dt_gemm_bf16: config %d needs K %% 64 == 0 and 16-byte aligned rows", config);
     if (n == 0) return DT_OK;
-    const int cfg = config >= 0 ? config : !all_tiled ? kAnyConfig : n_q8 ? 3 : pick_config(ps, n, cu_count());
+    const int cfg = config >= 0      ? config
+                    : !all_tiled     ? kAnyConfig
+                    : n_q8           ? pick_config_q8(ps, n, cu_count())
+                                     : pick_config(ps, n, cu_count());
     hipStream_t st = (hipStream_t)stream;
     return c_type == DT_TYPE_F32 ? launch<float>(ps, n, cfg, st) : launch<bf16>(ps, n, cfg, st);
 }

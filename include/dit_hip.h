@@ -336,12 +336,14 @@ int dt_gemm_q8_0(const void *A, int64_t lda, const void *codes, int64_t ld_codes
 
 /* dt_gemm_bf16 with an explicit tile configuration: 0 = 256x256 per
  * workgroup with direct global->LDS loads in four K = 32 stages, 1 = 128x128
- * with two workgroups per CU, 2 = 256x256 with two K = 64 stages, 3 = Q8_0
- * weights (the tiled kernel for them), 4 = the masked any-shape kernel (bf16
- * or Q8_0 weights), 5 = config 2 with buffer loads to LDS and its LDS reads
- * and loads interleaved into the MFMA stream (same results bit for bit; the
- * 256x256 kernel dt_gemm_bf16 picks); -1 picks by shape as dt_gemm_bf16 does.
- * For tuning and tests; no counterpart in the reference. */
+ * with two workgroups per CU (bf16 or Q8_0 weights; Q8_0 dequantised as it
+ * is staged), 2 = 256x256 with two K = 64 stages, 3 = Q8_0 weights at
+ * 256x256, 4 = the masked any-shape kernel (bf16 or Q8_0 weights), 5 =
+ * config 2 with buffer loads to LDS and its LDS reads and loads interleaved
+ * into the MFMA stream (same results bit for bit; the 256x256 kernel
+ * dt_gemm_bf16 picks), 6 = config 5 with 224-row tiles; -1 picks by shape
+ * as dt_gemm_bf16 does (Q8_0: 3 or 1).  Every configuration gives the same
+ * bits.  For tuning and tests; no counterpart in the reference. */
 int dt_gemm_bf16_config(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float *bias,
                         const void *addend, int64_t ldd, int32_t c_type, int32_t config,

@@ -201,18 +201,27 @@ Q8_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (
              (77, 130, 96), (40, 64, 32)]  # the last two: K % 64 == 32, the masked kernel
 
 
+@pytest.mark.parametrize("config", [-1, 1, 3])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", Q8_SHAPES)
-def test_gemm_q8_0_equals_dequant_then_gemm(orc, dev, M, N, K, out_dtype):
-    """Dequantising in the GEMM's load path gives the bf16 weights dt_dequant
+def test_gemm_q8_0_equals_dequant_then_gemm(orc, dev, M, N, K, out_dtype, config):
+    """Dequantising in the GEMM's load path (config 3: 256 x 256 tiles,
+    converted after the LDS read; config 1: 128 x 128 tiles, converted as
+    they are staged; -1: picked by shape) gives the bf16 weights dt_dequant
     writes and the same fp32 accumulation order, so C is bit-identical to
     dt_dequant followed by the bf16 GEMM; and within the bar of the oracle on
     the dequantised weights."""
-    print(f"gemm_q8_0 M={M} N={N} K={K} {out_dtype}", flush=True)
+    if config != -1 and K % 64:
+        pytest.skip("K % 64 == 32 runs the masked kernel only")
+    print(f"gemm_q8_0 M={M} N={N} K={K} {out_dtype} config={config}", flush=True)
     a = orc.randn(SEED + 261, (M, K))
     _, q8, wd = _q8_weight(orc, SEED + 262, N, K)
     ad = dev_tensor(a, torch.bfloat16)
-    y = dit_hip.gemm_q8_0(ad, q8, out_dtype=out_dtype)
+    if config == -1:
+        y = dit_hip.gemm_q8_0(ad, q8, out_dtype=out_dtype)
+    else:
+        y = torch.empty((M, N), dtype=out_dtype, device="cuda")
+        dit_hip.gemm_grouped([(ad, q8, y)], config=config)
     y_ref = dit_hip.gemm(ad, wd, out_dtype=out_dtype)
     torch.cuda.synchronize()
     assert torch.equal(y, y_ref), "Q8_0 GEMM differs from dequant + bf16 GEMM"
