@@ -898,19 +898,11 @@ int pick_by_waves(const Problem* ps, int n, int cus, std::initializer_list<int> 
 // 9216, 10% slower at 512 x 18432 x 3072, where 256 x 256 gives 144 tiles).
 int pick_config_q8(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {3, 1}); }
 
-int pick_config(const Problem* ps, int n, int cus) {
-    // 224 x 256 tiles when the 256 x 256 ones fill half to all but a few of
-    // the CUs in their only wave and the 224-row tiles still fit in one (e.g.
-    // M = 4608 or 4096, N = 3072: 216 or 192 tiles -> 252 or 228; measured
-    // 3-6% faster).
-    int64_t t5 = 0, t6 = 0;
-    for (int i = 0; i < n; ++i) {
-        t5 += tiles_of(ps[i], 5);
-        t6 += tiles_of(ps[i], 6);
-    }
-    if (2 * t5 >= cus && t5 < cus && t6 > t5 && t6 <= cus) return 6;
-    return pick_by_waves(ps, n, cus, {5, 1});
-}
+// bf16 weights: 256 x 256 tiles, 224 x 256 tiles when they need fewer rows of
+// work in all (e.g. M = 4608 or 4096 with N = 3072: 216 or 192 tiles -> one
+// wave of 252 or 228; 4608 x 9216: three waves of 756 instead of 648 tiles,
+// 8% faster), or 128 x 128 tiles for the products with few tiles.
+int pick_config(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {5, 6, 1}); }
 
 template <typename TC>
 int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
