@@ -265,7 +265,17 @@ __device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
 // barrier (sched_group_barrier), so the compiler keeps both operand sets
 // live instead of reading each fragment just before its MFMAs with an LDS
 // round trip exposed.
-template <typename TC, bool SCHED, int BM>
+// Q8: the weight operand is Q8_0 in the split layout (uint8 codes u = q + 128
+// [N][K] and fp32 block scales [K/32][N]).  Its codes and scales for k-tile
+// kt + 2 are loaded into registers where the bf16 kernel issues their DMA
+// (16 codes of 4 rows per thread), converted one k-tile later, w = fma(u, d,
+// -128 d) = d * q (exact) rounded to bf16 -- the value dt_dequant writes --
+// and written to the stage in the bf16 layout before the barrier that
+// publishes it.  The MFMA sequence is then the bf16 kernel's: C equals
+// dt_dequant followed by the bf16 GEMM bit for bit.  Each code is converted
+// once per workgroup (the eight-wave gemm_q8_kernel converts each twice, after
+// the LDS read); measured 4-16% faster than it on the step's products.
+template <typename TC, bool SCHED, int BM, bool Q8 = false>
 __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     static_assert(BM == 256 || BM == 224, "tile height");
     constexpr int WAVES_M = BM == 256 ? 2 : 1, WAVES_N = 4 / WAVES_M;
@@ -292,8 +302,24 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(p.A + (int64_t)m0 * p.lda), 0, 0x7FFFFFFF, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(p.B + (int64_t)n0 * p.ldb), 0, 0x7FFFFFFF, 0x00020000);
+        Q8 ? static_cast<void*>(const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(p.B) + (int64_t)n0 * p.ldb))
+           : static_cast<void*>(const_cast<uint16_t*>(p.B + (int64_t)n0 * p.ldb)),
+        0, 0x7FFFFFFF, 0x00020000);
     uint32_t oa[8], ob[8];  // oa: the first A_DMA used (a fixed size: captured by the lambdas below)
+    // Q8: thread t stages codes [16 (t % 4), +16) of B rows t / 4 + 64 j
+    // (j < 4) and their block scales; they are converted to bf16 and written
+    // to the stage one k-tile later (qwrite).
+    const int qr = tid >> 2, qc = tid & 3;
+    uint32_t oq[4];
+    const float* qs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = min(n0 + qr + 64 * j, p.N - 1);
+        oq[j] = Q8 ? (uint32_t)((int64_t)(n - n0) * p.ldb + 16 * qc) : 0u;
+        qs[j] = Q8 ? p.Bs + n + (int64_t)(qc >> 1) * p.ldbs : nullptr;
+    }
+    uint4 qcode[4];
+    float qscale[4];
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
         const int row = (BM / 4) * wave + 8 * j + (lane >> 3);
@@ -307,16 +333,51 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
         ob[j] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + c * 8) * 2);
     }
     typedef __attribute__((address_space(3))) void* lds_ptr_t;
+    auto qload = [&](int kt) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rb, oq[j], kt * EBK, 0);
+            qcode[j] = make_uint4(v[0], v[1], v[2], v[3]);
+            qscale[j] = qs[j][(int64_t)(2 * kt) * p.ldbs];
+        }
+    };
+    // B rows of k-tile (codes in qcode) as bf16 into stage s: chunk c of row
+    // r at c ^ swz8(r), w = fma(u, d, -128 d) rounded to bf16 (dt_dequant's).
+    auto qwrite = [&](int s) {
+        uint8_t* bbase = smem + s * STAGEB + AOPB;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = qr + 64 * j;
+            const float d = qscale[j], m = -128.0f * d;
+            const uint32_t w4[4] = {qcode[j].x, qcode[j].y, qcode[j].z, qcode[j].w};
+            uint32_t pk[8];
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                float w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = __builtin_fmaf((float)((w4[h] >> (8 * e)) & 0xFFu), d, m);
+                pk[2 * h] = pack_bf16x2(w[0], w[1]);
+                pk[2 * h + 1] = pack_bf16x2(w[2], w[3]);
+            }
+            const int sw = swz8(r);
+            *reinterpret_cast<uint4*>(bbase + r * EROWB + (((2 * qc) ^ sw) << 4)) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            *reinterpret_cast<uint4*>(bbase + r * EROWB + (((2 * qc + 1) ^ sw) << 4)) =
+                make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        }
+    };
     auto issue = [&](int kt, int s) {
         uint8_t* abase = smem + s * STAGEB + (BM / 4) * wave * EROWB;
         uint8_t* bbase = smem + s * STAGEB + AOPB + 64 * wave * EROWB;
         const int koff = kt * EBK * 2;
+        if constexpr (Q8) qload(kt);  // before the A DMA: waiting for the codes leaves the DMA in flight
 #pragma unroll
         for (int j = 0; j < 8; ++j) {  // A and B rows alternately
             if (j < A_DMA)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(abase + 8 * j * EROWB), 16, oa[j], koff, 0,
                                                          0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(bbase + 8 * j * EROWB), 16, ob[j], koff, 0, 0);
+            if constexpr (!Q8)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(bbase + 8 * j * EROWB), 16, ob[j], koff, 0,
+                                                         0);
         }
     };
     f32x16_t acc[FN][FM];
@@ -369,9 +430,11 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
 
     const int nk = p.K / EBK;
     issue(0, 0);
+    if constexpr (Q8) qwrite(0);
     if (nk > 1) issue(1, 1);
-    if (nk > 1) wait_vm<A_DMA + 8>();
+    if (nk > 1) wait_vm<A_DMA + 8>();  // Q8: 4 code and 4 scale loads stand in for the 8 B DMAs
     else wait_vm<0>();
+    if constexpr (Q8) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the B rows written
     __builtin_amdgcn_s_barrier();
     read_ops(0, 0, wa, xa);
     // One k-tile: its four k-steps, each step's MFMAs running while the next
@@ -388,6 +451,7 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
         mfma(wb, xb);
         pipe();
         read_ops(s, 3, wb, xb);
+        if constexpr (Q8) qwrite(s ^ 1);  // k-tile kt + 1's weights
         mfma(wa, xa);
         pipe();
         // Stage s is refilled with k-tile kt + 2 once every wave's reads of
@@ -857,10 +921,10 @@ struct Config {
 // 256 x 256, 8 waves, K = 64, three stages; 4: any shape (masked, 128 x 128);
 // 5: config 2 with the operand reads interleaved into the MFMA stream; 6: the
 // same at 224 x 256.
-constexpr int kAnyConfig = 4, kLastConfig = 6;
-constexpr Config kConfigs[7] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
+constexpr int kAnyConfig = 4, kLastConfig = 7;
+constexpr Config kConfigs[8] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
                                 {256, 256, 512, 1, 1.0},  {128, 128, 256, 2, 0.1}, {256, 256, 256, 1, 1.3},
-                                {224, 256, 256, 1, 1.2}};
+                                {224, 256, 256, 1, 1.2},  {256, 256, 256, 1, 1.25}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -892,11 +956,11 @@ int pick_by_waves(const Problem* ps, int n, int cus, std::initializer_list<int> 
     return best;
 }
 
-// Q8_0 weights: 256 x 256 tiles (gemm_q8_kernel) or, when those leave most
-// CUs idle (the 512 text tokens' products, a 128-column output), 128 x 128
-// tiles dequantised as they are staged (measured 1.9x faster at 512 x 3072 x
-// 9216, 10% slower at 512 x 18432 x 3072, where 256 x 256 gives 144 tiles).
-int pick_config_q8(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {3, 1}); }
+// Q8_0 weights: the K = 64 kernel's 256 x 256 tiles with the weights
+// dequantised as they are staged (config 7) or, when those leave most CUs
+// idle (the 512 text tokens' products, a 128-column output), 128 x 128 tiles
+// dequantised the same way (1.9x faster than 256 x 256 at 512 x 3072 x 9216).
+int pick_config_q8(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {7, 1}); }
 
 // bf16 weights: 256 x 256 tiles, 224 x 256 tiles when they need fewer rows of
 // work in all (e.g. M = 4608 or 4096 with N = 3072: 216 or 192 tiles -> one
@@ -926,6 +990,8 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
         hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 256>), grid, block, 0, st, g);
     else if (cfg == 6)
         hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 224>), grid, block, 0, st, g);
+    else if (cfg == 7)
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 256, true>), grid, block, 0, st, g);
     else if (cfg == 3)
         hipLaunchKernelGGL((gemm_q8_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == kAnyConfig && ps[0].Bs)
@@ -996,7 +1062,8 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
         }
     }
     DT_REQUIRE(n_q8 == 0 || n_q8 == count, "dt_gemm_bf16_grouped: a group mixes Q8_0 and bf16 weights");
-    DT_REQUIRE(config == -1 || config == kAnyConfig || config == 1 || (n_q8 > 0) == (config == 3),
+    const bool q8_config = config == 3 || config == 7;  // configurations for Q8_0 weights only
+    DT_REQUIRE(config == -1 || config == kAnyConfig || config == 1 || (n_q8 > 0) == q8_config,
                "dt_gemm_bf16: config %d does not take %s weights", config, n_q8 ? "Q8_0" : "bf16");
     DT_REQUIRE(config == -1 || config == kAnyConfig || all_tiled,
                "dt_gemm_bf16: config %d needs K %% 64 == 0 and 16-byte aligned rows", config);

@@ -201,13 +201,14 @@ Q8_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (
              (77, 130, 96), (40, 64, 32)]  # the last two: K % 64 == 32, the masked kernel
 
 
-@pytest.mark.parametrize("config", [-1, 1, 3])
+@pytest.mark.parametrize("config", [-1, 1, 3, 7])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", Q8_SHAPES)
 def test_gemm_q8_0_equals_dequant_then_gemm(orc, dev, M, N, K, out_dtype, config):
-    """Dequantising in the GEMM's load path (config 3: 256 x 256 tiles,
-    converted after the LDS read; config 1: 128 x 128 tiles, converted as
-    they are staged; -1: picked by shape) gives the bf16 weights dt_dequant
+    """Dequantising in the GEMM's load path (config 3: 256 x 256 tiles in
+    eight waves, converted after the LDS read; config 7: the K = 64 kernel's
+    256 x 256 tiles and config 1: 128 x 128 tiles, converted as they are
+    staged; -1: picked by shape) gives the bf16 weights dt_dequant
     writes and the same fp32 accumulation order, so C is bit-identical to
     dt_dequant followed by the bf16 GEMM; and within the bar of the oracle on
     the dequantised weights."""
@@ -246,8 +247,9 @@ def test_gemm_q8_0_bias_addend_strided(orc, dev, out_dtype):
 
 def test_gemm_q8_0_grouped_and_large(orc, dev):
     """The five projections of a single-stream block as one grouped Q8_0
-    launch (4608 rows, N = 3072 x 3 + 9216 x 2, K = 3072), bit-identical to
-    the bf16 grouped GEMM on the dequantised weights."""
+    launch (4608 rows, N = 3072 x 3 + 9216 x 2, K = 3072), by the picked
+    configuration and by the eight-wave kernel, bit-identical to the bf16
+    grouped GEMM on the dequantised weights."""
     M, K = 4608, 3072
     a = dev_tensor(orc.randn(SEED + 267, (M, K)), torch.bfloat16)
     items_q, items_b = [], []
@@ -255,11 +257,13 @@ def test_gemm_q8_0_grouped_and_large(orc, dev):
         _, q8, wd = _q8_weight(orc, SEED + 270 + i, N, K)
         items_q.append((a, q8, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
         items_b.append((a, wd, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
-    outs_q = dit_hip.gemm_grouped(items_q)
+    outs_q = [o.clone() for o in dit_hip.gemm_grouped(items_q)]
+    outs_q3 = dit_hip.gemm_grouped(items_q, config=3)
     outs_b = dit_hip.gemm_grouped(items_b, config=2)
     torch.cuda.synchronize()
-    for oq, ob in zip(outs_q, outs_b):
-        assert torch.equal(oq, ob)
+    for oq, oq3, ob in zip(outs_q, outs_q3, outs_b):
+        assert torch.equal(oq, ob), "picked Q8_0 configuration"
+        assert torch.equal(oq3, ob), "eight-wave Q8_0 kernel"
 
 
 def test_gemm_q8_0_rejects(orc, dev):
@@ -270,8 +274,10 @@ def test_gemm_q8_0_rejects(orc, dev):
                               (a, wd, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))])
     with pytest.raises(RuntimeError, match="does not take Q8_0"):
         dit_hip.gemm_grouped([(a, q8, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))], config=2)
-    with pytest.raises(RuntimeError, match="does not take bf16"):
-        dit_hip.gemm_grouped([(a, wd, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))], config=3)
+    for config in (3, 7):
+        with pytest.raises(RuntimeError, match="does not take bf16"):
+            dit_hip.gemm_grouped([(a, wd, torch.empty((64, 64), dtype=torch.bfloat16, device="cuda"))],
+                                 config=config)
 
 
 # ---------------------------------------------------------------- attention --
