@@ -600,7 +600,7 @@ def denoise_step(steps, warmup, weight_format="bf16", hip_graph=True):
                    + "; RMSNorm weights N(1,0.02)",
         "linear_weight_bytes": res["linear_weight_bytes"],
         "gemm": ("hand-written bf16 MFMA GEMM (diffusers-cpp_amd/csrc/gemm.hip"
-                 + (", gemm_q8_kernel: Q8_0 dequantised in its load path)" if weight_format == "q8_0" else ")")
+                 + (", Q8_0 codes dequantised to bf16 as they are staged into LDS)" if weight_format == "q8_0" else ")")
                  if res.get("gemm") == "mfma" else res.get("gemm")),
         "launch": "one HIP graph replay per step" if hip_graph else "eager launches after the fusion pass",
         "s_per_step": round(t, 5),
