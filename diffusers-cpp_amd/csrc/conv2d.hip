@@ -432,7 +432,7 @@ __global__ __launch_bounds__(256) void conv2d_kernel(const ConvArgs a) {
 // 32-byte record's two 16-byte units by the rule below (kSwzBit), so
 // consecutive records read distinct banks.  The output leaves through LDS
 // (conv_store_lds).
-constexpr int kCi2 = 16, kRec2 = 32, kTilePx2 = 256;
+constexpr int kCi2 = 16, kRec2 = 32;
 // A record's two 16-byte units are swapped when bit 3 of its pixel (or
 // output-channel) index is set.  Record r's unit u then starts at bank
 // 8 (r mod 8) + 4 (u ^ bit3(r)) of 64, so any 16 consecutive records -- the
