@@ -201,6 +201,27 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
     return s;
 }
 
+// Two block_sum_f64 at once, with the same sums in the same order (so the
+// same bits), through one LDS exchange: red2 holds 2 doubles per wave.
+__device__ __forceinline__ void block_sum2_f64(double& a, double& b, double* red2) {
+    a = wave_sum_f64(a);
+    b = wave_sum_f64(b);
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+    const int nw = (blockDim.x + kWave - 1) / kWave;
+    __syncthreads();
+    if (lane == 0) {
+        red2[2 * wid] = a;
+        red2[2 * wid + 1] = b;
+    }
+    __syncthreads();
+    a = 0.0;
+    b = 0.0;
+    for (int i = 0; i < nw; ++i) {
+        a += red2[2 * i];
+        b += red2[2 * i + 1];
+    }
+}
+
 __device__ __forceinline__ float block_sum_f32(float v, float* red) {
     v = wave_sum(v);
     const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
