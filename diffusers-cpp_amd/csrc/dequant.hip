@@ -32,18 +32,10 @@ __device__ __forceinline__ void store_out8<float>(float* p, const float* v) {
     Io<float>::store(p + 4, v + 4);
 }
 
+// Lane `part` (0..3) of Q8_0 block h (fp16 d, then 32 int8 codes as 16
+// halfwords): outputs [8 part, 8 part + 8) of the block, stored at out.
 template <typename T>
-__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t* __restrict__ src,
-                                                           int64_t row_bytes, T* __restrict__ dst,
-                                                           int64_t dst_stride, uint32_t total,
-                                                           FastDiv chunks_per_row) {
-    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total) return;
-    const uint32_t r = fdiv(idx, chunks_per_row);
-    const uint32_t k = idx - r * chunks_per_row.d;
-    const uint32_t blk = k >> 2, part = k & 3;
-    const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 34;
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+__device__ __forceinline__ void q8_0_decode8(const uint16_t* h, uint32_t part, T* out) {
     const float d = f16_bits_to_f32(h[0]);
     float v[8];
 #pragma unroll
@@ -52,24 +44,17 @@ __global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t* __rest
         v[2 * i] = mul_rn(d, (float)(int8_t)(two & 0xFF));
         v[2 * i + 1] = mul_rn(d, (float)(int8_t)(two >> 8));
     }
-    store_out8<T>(dst + (int64_t)r * dst_stride + (int64_t)k * 8, v);
+    store_out8<T>(out + part * 8, v);
 }
 
+// Lane k (0..31) of the Q4_K super-block at b: outputs [8k, 8k + 8), stored
+// at out.  Sub-block j = 2*c64 + hi; header bytes 4..15 are scales[0..11].
 template <typename T>
-__global__ __launch_bounds__(256) void dequant_q4_K_kernel(const uint8_t* __restrict__ src,
-                                                           int64_t row_bytes, T* __restrict__ dst,
-                                                           int64_t dst_stride, uint32_t total,
-                                                           FastDiv chunks_per_row) {
-    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= total) return;
-    const uint32_t r = fdiv(idx, chunks_per_row);
-    const uint32_t k = idx - r * chunks_per_row.d;
-    const uint32_t blk = k >> 5, e0 = (k & 31) * 8;     // element offset in the super-block
+__device__ __forceinline__ void q4_K_decode8(const uint8_t* b, uint32_t k, T* out) {
+    const uint32_t e0 = k * 8;                            // element offset in the super-block
     const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
-    const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 144;
-    const uint4 hdr = *reinterpret_cast<const uint4*>(b);   // shared by 32 lanes: cached
+    const uint4 hdr = *reinterpret_cast<const uint4*>(b);
     const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
-    // Sub-block j = 2*c64 + hi; header bytes 4..15 are scales[0..11].
     const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);
     const uint32_t by = (hdr.y >> sh) & 0xFF;   // scales[j & 3]
     const uint32_t bz = (hdr.z >> sh) & 0xFF;   // scales[(j & 3) + 4]
@@ -91,7 +76,35 @@ __global__ __launch_bounds__(256) void dequant_q4_K_kernel(const uint8_t* __rest
         v[i] = sub_rn(mul_rn(d1, (float)((q8.x >> (8 * i + shift)) & 0xF)), m1);
         v[4 + i] = sub_rn(mul_rn(d1, (float)((q8.y >> (8 * i + shift)) & 0xF)), m1);
     }
-    store_out8<T>(dst + (int64_t)r * dst_stride + (int64_t)k * 8, v);
+    store_out8<T>(out + e0, v);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t* __restrict__ src,
+                                                           int64_t row_bytes, T* __restrict__ dst,
+                                                           int64_t dst_stride, uint32_t total,
+                                                           FastDiv chunks_per_row) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t r = fdiv(idx, chunks_per_row);
+    const uint32_t k = idx - r * chunks_per_row.d;
+    const uint32_t blk = k >> 2, part = k & 3;
+    const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 34;
+    q8_0_decode8<T>(reinterpret_cast<const uint16_t*>(b), part, dst + (int64_t)r * dst_stride + (int64_t)blk * 32);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void dequant_q4_K_kernel(const uint8_t* __restrict__ src,
+                                                           int64_t row_bytes, T* __restrict__ dst,
+                                                           int64_t dst_stride, uint32_t total,
+                                                           FastDiv chunks_per_row) {
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const uint32_t r = fdiv(idx, chunks_per_row);
+    const uint32_t k = idx - r * chunks_per_row.d;
+    const uint32_t blk = k >> 5;
+    const uint8_t* b = src + (int64_t)r * row_bytes + (int64_t)blk * 144;   // header shared by 32 lanes: cached
+    q4_K_decode8<T>(b, k & 31, dst + (int64_t)r * dst_stride + (int64_t)blk * 256);
 }
 
 constexpr int kStageThreads = 256;
@@ -115,16 +128,8 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q8_0_staged_kernel(cons
     __syncthreads();
     const int blk = t >> 2, part = t & 3;
     if (blk >= nblk) return;
-    const uint16_t* h = reinterpret_cast<const uint16_t*>(stage) + blk * 17;
-    const float d = f16_bits_to_f32(h[0]);
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t two = h[1 + part * 4 + i];
-        v[2 * i] = mul_rn(d, (float)(int8_t)(two & 0xFF));
-        v[2 * i + 1] = mul_rn(d, (float)(int8_t)(two >> 8));
-    }
-    store_out8<T>(dst + (int64_t)row * dst_stride + (int64_t)(b0 + blk) * 32 + part * 8, v);
+    q8_0_decode8<T>(reinterpret_cast<const uint16_t*>(stage) + blk * 17, part,
+                    dst + (int64_t)row * dst_stride + (int64_t)(b0 + blk) * 32);
 }
 
 // Q4_K, staged: workgroup (seg, row) decodes super-blocks [8 seg, 8 seg + 8)
@@ -142,31 +147,8 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_staged_kernel(cons
     __syncthreads();
     const int sb = t >> 5, k = t & 31;
     if (sb >= nblk) return;
-    const uint32_t e0 = k * 8;                            // element offset in the super-block
-    const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
-    const uint8_t* b = reinterpret_cast<const uint8_t*>(stage) + sb * 144;
-    const uint4 hdr = *reinterpret_cast<const uint4*>(b);
-    const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
-    const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);
-    const uint32_t by = (hdr.y >> sh) & 0xFF, bz = (hdr.z >> sh) & 0xFF, bw = (hdr.w >> sh) & 0xFF;
-    uint32_t sc, m;
-    if (j < 4) {
-        sc = by & 63;
-        m = bz & 63;
-    } else {
-        sc = (bw & 0xF) | ((by >> 6) << 4);
-        m = (bw >> 4) | ((bz >> 6) << 4);
-    }
-    const float d1 = mul_rn(f16_bits_to_f32(hdr.x & 0xFFFF), (float)sc);
-    const float m1 = mul_rn(f16_bits_to_f32(hdr.x >> 16), (float)m);
-    const uint32_t shift = hi * 4;
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[i] = sub_rn(mul_rn(d1, (float)((q8.x >> (8 * i + shift)) & 0xF)), m1);
-        v[4 + i] = sub_rn(mul_rn(d1, (float)((q8.y >> (8 * i + shift)) & 0xF)), m1);
-    }
-    store_out8<T>(dst + (int64_t)row * dst_stride + (int64_t)(b0 + sb) * 256 + e0, v);
+    q4_K_decode8<T>(reinterpret_cast<const uint8_t*>(stage) + sb * 144, k,
+                    dst + (int64_t)row * dst_stride + (int64_t)(b0 + sb) * 256);
 }
 
 // Dense tensors (rows packed back to back in the source and the output) are
@@ -195,19 +177,8 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q8_0_flat_kernel(const 
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int blk = u * kQ8SegBlocks + (t >> 2), part = t & 3;
-        if (blk < nblk) {
-            const uint16_t* h = reinterpret_cast<const uint16_t*>(stage) + blk * 17;
-            const float d = f16_bits_to_f32(h[0]);
-            float v[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t two = h[1 + part * 4 + i];
-                v[2 * i] = mul_rn(d, (float)(int8_t)(two & 0xFF));
-                v[2 * i + 1] = mul_rn(d, (float)(int8_t)(two >> 8));
-            }
-            store_out8<T>(dst + (b0 + blk) * 32 + part * 8, v);
-        }
+        const int blk = u * kQ8SegBlocks + (t >> 2);
+        if (blk < nblk) q8_0_decode8<T>(reinterpret_cast<const uint16_t*>(stage) + blk * 17, t & 3, dst + (b0 + blk) * 32);
     }
 }
 
@@ -227,34 +198,121 @@ __global__ __launch_bounds__(kStageThreads) void dequant_q4_K_flat_kernel(const 
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int sb = u * kQ4SegBlocks + (t >> 5), k = t & 31;
-        if (sb < nblk) {
-            const uint32_t e0 = k * 8;
-            const uint32_t c64 = e0 >> 6, o = e0 & 63, hi = o >> 5, l0 = o & 31;
-            const uint8_t* b = reinterpret_cast<const uint8_t*>(stage) + sb * 144;
-            const uint4 hdr = *reinterpret_cast<const uint4*>(b);
-            const uint2 q8 = *reinterpret_cast<const uint2*>(b + 16 + 32 * c64 + l0);
-            const uint32_t j = 2 * c64 + hi, sh = 8 * (j & 3);
-            const uint32_t by = (hdr.y >> sh) & 0xFF, bz = (hdr.z >> sh) & 0xFF, bw = (hdr.w >> sh) & 0xFF;
-            uint32_t sc, m;
-            if (j < 4) {
-                sc = by & 63;
-                m = bz & 63;
-            } else {
-                sc = (bw & 0xF) | ((by >> 6) << 4);
-                m = (bw >> 4) | ((bz >> 6) << 4);
-            }
-            const float d1 = mul_rn(f16_bits_to_f32(hdr.x & 0xFFFF), (float)sc);
-            const float m1 = mul_rn(f16_bits_to_f32(hdr.x >> 16), (float)m);
-            const uint32_t shift = hi * 4;
-            float v[8];
+        const int sb = u * kQ4SegBlocks + (t >> 5);
+        if (sb < nblk) q4_K_decode8<T>(reinterpret_cast<const uint8_t*>(stage) + sb * 144, t & 31, dst + (b0 + sb) * 256);
+    }
+}
+
+// The same runs in two halves, for U = 2 and 4 (tensors that fill the chip
+// in one round with shorter runs): every load of the run is issued at once,
+// the first half is decoded and stored while the second half's loads are in
+// flight, then the second half.  At 3072 x 3072 (U = 4) this took Q4_K from
+// 5.36 to 4.83 us and Q8_0 from 6.20 to 5.83 us back to back, the same bits.
+// At U = 8 it was slower (Q4_K 12.6 -> 14.3 us at 3072 x 9216; issuing the
+// whole run's loads at once without the halves, 13.7 us): there the flat
+// kernels' load loop, whose trips wait for each load before its LDS write,
+// keeps fewer reads in flight and is the fastest form measured.
+// A partial last run (nblocks not a multiple of the run) takes the flat
+// kernels' path, uniformly for its workgroup.
+template <typename T, int U>
+__global__ __launch_bounds__(kStageThreads) void dequant_q8_0_halves_kernel(const uint8_t* __restrict__ src,
+                                                                            int64_t nblocks, T* __restrict__ dst) {
+    constexpr int SEG = kQ8SegBlocks * U, NVEC = SEG * 34 / 16, HV = NVEC / 2;
+    constexpr int LH = (HV + kStageThreads - 1) / kStageThreads;      // loads per thread per half
+    static_assert(SEG * 34 % 32 == 0, "each half is whole 16-byte vectors");
+    __shared__ __attribute__((aligned(16))) uint4 stage[NVEC];
+    const int t = threadIdx.x;
+    const int64_t b0 = (int64_t)blockIdx.x * SEG;
+    const int nblk = (int)min<int64_t>(SEG, nblocks - b0);
+    const uint8_t* base = src + b0 * 34;
+    const uint16_t* h = reinterpret_cast<const uint16_t*>(stage);
+    if (nblk < SEG) {
+        const int bytes = nblk * 34, nvec = bytes >> 4;
+        for (int i = t; i < nvec; i += kStageThreads) stage[i] = ld_stream(base + 16 * i);
+        if (t < (bytes & 15) / 2)
+            reinterpret_cast<uint16_t*>(stage)[nvec * 8 + t] = reinterpret_cast<const uint16_t*>(base + 16 * nvec)[t];
+        __syncthreads();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = sub_rn(mul_rn(d1, (float)((q8.x >> (8 * i + shift)) & 0xF)), m1);
-                v[4 + i] = sub_rn(mul_rn(d1, (float)((q8.y >> (8 * i + shift)) & 0xF)), m1);
-            }
-            store_out8<T>(dst + (b0 + sb) * 256 + e0, v);
+        for (int u = 0; u < U; ++u) {
+            const int blk = u * kQ8SegBlocks + (t >> 2);
+            if (blk < nblk) q8_0_decode8<T>(h + blk * 17, t & 3, dst + (b0 + blk) * 32);
         }
+        return;
+    }
+    // Vector i of each half; threads past the half reload its last vector
+    // (same address, same LDS word), so every load is unconditional.
+    int iv[LH];
+    uint4 ra[LH], rb[LH];
+#pragma unroll
+    for (int l = 0; l < LH; ++l) {
+        iv[l] = min(l * kStageThreads + t, HV - 1);
+        ra[l] = ld_stream(base + 16 * iv[l]);
+    }
+#pragma unroll
+    for (int l = 0; l < LH; ++l) rb[l] = ld_stream(base + 16 * (HV + iv[l]));
+#pragma unroll
+    for (int l = 0; l < LH; ++l) stage[iv[l]] = ra[l];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U / 2; ++u) {                 // blocks [0, SEG/2): bytes [0, 16 HV)
+        const int blk = u * kQ8SegBlocks + (t >> 2);
+        q8_0_decode8<T>(h + blk * 17, t & 3, dst + (b0 + blk) * 32);
+    }
+#pragma unroll
+    for (int l = 0; l < LH; ++l) stage[HV + iv[l]] = rb[l];
+    __syncthreads();
+#pragma unroll
+    for (int u = U / 2; u < U; ++u) {
+        const int blk = u * kQ8SegBlocks + (t >> 2);
+        q8_0_decode8<T>(h + blk * 17, t & 3, dst + (b0 + blk) * 32);
+    }
+}
+
+template <typename T, int U>
+__global__ __launch_bounds__(kStageThreads) void dequant_q4_K_halves_kernel(const uint8_t* __restrict__ src,
+                                                                            int64_t nblocks, T* __restrict__ dst) {
+    constexpr int SEG = kQ4SegBlocks * U, HV = SEG * 9 / 2;
+    constexpr int LH = (HV + kStageThreads - 1) / kStageThreads;
+    __shared__ __attribute__((aligned(16))) uint4 stage[SEG * 9];
+    const int t = threadIdx.x;
+    const int64_t b0 = (int64_t)blockIdx.x * SEG;
+    const int nblk = (int)min<int64_t>(SEG, nblocks - b0);
+    const uint8_t* base = src + b0 * 144;
+    const uint8_t* sbs = reinterpret_cast<const uint8_t*>(stage);
+    if (nblk < SEG) {
+        for (int i = t; i < nblk * 9; i += kStageThreads) stage[i] = ld_stream(base + 16 * i);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int sb = u * kQ4SegBlocks + (t >> 5);
+            if (sb < nblk) q4_K_decode8<T>(sbs + sb * 144, t & 31, dst + (b0 + sb) * 256);
+        }
+        return;
+    }
+    int iv[LH];
+    uint4 ra[LH], rb[LH];
+#pragma unroll
+    for (int l = 0; l < LH; ++l) {
+        iv[l] = min(l * kStageThreads + t, HV - 1);
+        ra[l] = ld_stream(base + 16 * iv[l]);
+    }
+#pragma unroll
+    for (int l = 0; l < LH; ++l) rb[l] = ld_stream(base + 16 * (HV + iv[l]));
+#pragma unroll
+    for (int l = 0; l < LH; ++l) stage[iv[l]] = ra[l];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U / 2; ++u) {                 // super-blocks [0, SEG/2): vectors [0, HV)
+        const int sb = u * kQ4SegBlocks + (t >> 5);
+        q4_K_decode8<T>(sbs + sb * 144, t & 31, dst + (b0 + sb) * 256);
+    }
+#pragma unroll
+    for (int l = 0; l < LH; ++l) stage[HV + iv[l]] = rb[l];
+    __syncthreads();
+#pragma unroll
+    for (int u = U / 2; u < U; ++u) {
+        const int sb = u * kQ4SegBlocks + (t >> 5);
+        q4_K_decode8<T>(sbs + sb * 144, t & 31, dst + (b0 + sb) * 256);
     }
 }
 
@@ -278,9 +336,16 @@ template <typename T, int U>
 void launch_flat(bool q8, const void* src, int64_t nblocks, void* dst, hipStream_t st) {
     const int64_t seg = (q8 ? kQ8SegBlocks : kQ4SegBlocks) * U;
     const dim3 grid((unsigned)((nblocks + seg - 1) / seg));
-    if (q8)
+    constexpr bool halves = U == 2 || U == 4;
+    if (q8 && halves)
+        hipLaunchKernelGGL((dequant_q8_0_halves_kernel<T, U>), grid, dim3(kStageThreads), 0, st,
+                           (const uint8_t*)src, nblocks, (T*)dst);
+    else if (q8)
         hipLaunchKernelGGL((dequant_q8_0_flat_kernel<T, U>), grid, dim3(kStageThreads), 0, st, (const uint8_t*)src,
                            nblocks, (T*)dst);
+    else if (halves)
+        hipLaunchKernelGGL((dequant_q4_K_halves_kernel<T, U>), grid, dim3(kStageThreads), 0, st,
+                           (const uint8_t*)src, nblocks, (T*)dst);
     else
         hipLaunchKernelGGL((dequant_q4_K_flat_kernel<T, U>), grid, dim3(kStageThreads), 0, st, (const uint8_t*)src,
                            nblocks, (T*)dst);

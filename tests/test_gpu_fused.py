@@ -354,12 +354,13 @@ def test_groupnorm_no_affine_inplace_and_offset_mean(orc, dev, dtype):
 # ----------------------------------------------------------- dequantisation ---
 @pytest.mark.parametrize("qtype", [dit_hip.Q8_0, dit_hip.Q4_K])
 @pytest.mark.parametrize("rows,cols", [(3072, 9216), (9216, 3072), (3072, 3072), (2048, 3072), (96, 9216),
-                                       (9216, 256)])
+                                       (9216, 256), (3001, 3072), (2001, 3072)])
 def test_dequant_bit_exact(orc, dev, qtype, rows, cols):
-    """The dense tensors run the flat kernels with a run length chosen by
-    size: on 256 CUs the two full-size shapes take 8 blocks per run, 3072^2
-    takes 4, 2048 x 3072 takes 2 and the two narrow shapes 1; every run
-    length gives ggml's bits."""
+    """The dense tensors run with a run length chosen by size: on 256 CUs
+    the two full-size shapes take 8 blocks per run (the flat kernels), 3072^2
+    and 3001 x 3072 take 4 and 2048 x 3072 and 2001 x 3072 take 2 (the
+    two-half kernels; 3001 and 2001 rows end in a partial run), the two
+    narrow shapes 1; every run length gives ggml's bits."""
     print(f"dequant q{qtype} {rows}x{cols}", flush=True)
     w = orc.randn(SEED + 31, (rows, cols), std=0.02)
     blocks = orc.quantize(w, qtype)
