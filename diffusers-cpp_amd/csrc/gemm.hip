@@ -250,11 +250,18 @@ __global__ __launch_bounds__(512) void gemm_dma256_kernel(const Group grp) {
     epilogue<FM, FN, TC>(p, acc, m0 + wm, n0 + wn, lane);
 }
 
-// ---- BM x 256, 4 waves, K = 64 per stage, 2 stages ----------------------------
-// BM = 256: each wave owns a 128 x 128 quarter of the tile (4 x 4 blocks of
-// 32 x 32, 256 fp32 accumulators, one wave per SIMD): per k-step it reads 8
-// operands for 16 MFMAs, against 6 for 8 in the 8-wave kernel, which keeps
-// the LDS port that the DMA writes share below the MFMA time.
+// ---- BM x 256, 4 or 8 waves, K = 64 per stage, 2 stages --------------------
+// BM = 256, NW = 4: each wave owns a 128 x 128 quarter of the tile (4 x 4
+// blocks of 32 x 32, 256 fp32 accumulators, one wave per SIMD): per k-step it
+// reads 8 operands for 16 MFMAs.
+// BM = 256, NW = 8 (the default for the step's products): each wave owns
+// 128 x 64 (4 x 2 blocks, 128 accumulators, 208 VGPRs, two waves per SIMD),
+// reading 6 operands for 8 MFMAs -- 1.5x the LDS reads per MFMA, but while
+// one wave of a SIMD waits on its LDS reads, the stage DMA or the barrier,
+// the other issues MFMAs.  Measured on gfx950 with the same stages and bits:
+// 12-21% faster on every product of the step (4608 x 27648 x 3072: 865 ->
+// 713 us, 1.10 PFLOP/s; 4096 x 4096 x 24576: 1.11 -> 1.24 PFLOP/s), and
+// 14-18% with Q8_0 weights staged.
 // BM = 224 (7 blocks of 32): the four waves side by side along n, each
 // 224 x 64 (7 x 2 blocks, 224 accumulators, 9 operand reads for 14 MFMAs).
 // M = 4608 then makes 21 tile rows, so a 4608 x 3072 product is 252 tiles on
@@ -286,13 +293,15 @@ __device__ __forceinline__ int swz8(int r) { return (r ^ (r >> 3)) & 7; }
 // dt_dequant followed by the bf16 GEMM bit for bit.  Each code is converted
 // once per workgroup (the eight-wave gemm_q8_kernel converts each twice, after
 // the LDS read); measured 4-16% faster than it on the step's products.
-template <typename TC, bool SCHED, int BM, bool Q8 = false>
-__global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
+template <typename TC, bool SCHED, int BM, bool Q8 = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void gemm_k64_kernel(const Group grp) {
     static_assert(BM == 256 || BM == 224, "tile height");
-    constexpr int WAVES_M = BM == 256 ? 2 : 1, WAVES_N = 4 / WAVES_M;
+    static_assert(NW == 4 || (NW == 8 && BM == 256), "eight waves: 256-row tiles");
+    constexpr int WAVES_M = BM == 256 ? 2 : 1, WAVES_N = NW / WAVES_M;
     constexpr int FM = BM / WAVES_M / 32, FN = 256 / WAVES_N / 32;
     constexpr int AOPB = BM * EROWB, STAGEB = AOPB + 256 * EROWB, NS = 2;
-    constexpr int A_DMA = BM / 4 / 8;  // A rows per wave / 8 rows per DMA instruction
+    constexpr int A_DMA = BM / NW / 8;  // A rows per wave / 8 rows per DMA instruction
+    constexpr int B_DMA = 256 / NW / 8;
     __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGEB];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -316,37 +325,38 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
         Q8 ? static_cast<void*>(const_cast<uint8_t*>(reinterpret_cast<const uint8_t*>(p.B) + (int64_t)n0 * p.ldb))
            : static_cast<void*>(const_cast<uint16_t*>(p.B + (int64_t)n0 * p.ldb)),
         0, 0x7FFFFFFF, 0x00020000);
-    uint32_t oa[8], ob[8];  // oa: the first A_DMA used (a fixed size: captured by the lambdas below)
-    // Q8: thread t stages codes [16 (t % 4), +16) of B rows t / 4 + 64 j
-    // (j < 4) and their block scales; they are converted to bf16 and written
-    // to the stage one k-tile later (qwrite).
+    uint32_t oa[8], ob[8];  // the first A_DMA / B_DMA used (a fixed size: captured by the lambdas below)
+    // Q8: thread t stages codes [16 (t % 4), +16) of B rows t / 4 + 16 NW j
+    // (j < 16 / NW) and their block scales; they are converted to bf16 and
+    // written to the stage one k-tile later (qwrite).
+    constexpr int QJ = 16 / NW, QROWS = 16 * NW;  // weight rows per thread; rows per pass
     const int qr = tid >> 2, qc = tid & 3;
-    uint32_t oq[4];
-    const float* qs[4];
+    uint32_t oq[QJ];
+    const float* qs[QJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = min(n0 + qr + 64 * j, p.N - 1);
+    for (int j = 0; j < QJ; ++j) {
+        const int n = min(n0 + qr + QROWS * j, p.N - 1);
         oq[j] = Q8 ? (uint32_t)((int64_t)(n - n0) * p.ldb + 16 * qc) : 0u;
         qs[j] = Q8 ? p.Bs + n + (int64_t)(qc >> 1) * p.ldbs : nullptr;
     }
-    uint4 qcode[4];
-    float qscale[4];
+    uint4 qcode[QJ];
+    float qscale[QJ];
 #pragma unroll
     for (int j = 0; j < A_DMA; ++j) {
-        const int row = (BM / 4) * wave + 8 * j + (lane >> 3);
+        const int row = (BM / NW) * wave + 8 * j + (lane >> 3);
         const int c = (lane & 7) ^ swz8(row);
         oa[j] = (uint32_t)(((int64_t)(min(m0 + row, p.M - 1) - m0) * p.lda + c * 8) * 2);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int row = 64 * wave + 8 * j + (lane >> 3);
+    for (int j = 0; j < B_DMA; ++j) {
+        const int row = (256 / NW) * wave + 8 * j + (lane >> 3);
         const int c = (lane & 7) ^ swz8(row);
         ob[j] = (uint32_t)(((int64_t)(min(n0 + row, p.N - 1) - n0) * p.ldb + c * 8) * 2);
     }
     typedef __attribute__((address_space(3))) void* lds_ptr_t;
     auto qload = [&](int kt) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < QJ; ++j) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(rb, oq[j], kt * EBK, 0);
             qcode[j] = make_uint4(v[0], v[1], v[2], v[3]);
             qscale[j] = qs[j][(int64_t)(2 * kt) * p.ldbs];
@@ -357,8 +367,8 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     auto qwrite = [&](int s) {
         uint8_t* bbase = smem + s * STAGEB + AOPB;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r = qr + 64 * j;
+        for (int j = 0; j < QJ; ++j) {
+            const int r = qr + QROWS * j;
             const float d = qscale[j], m = -128.0f * d;
             const uint32_t w4[4] = {qcode[j].x, qcode[j].y, qcode[j].z, qcode[j].w};
             uint32_t pk[8];
@@ -377,8 +387,8 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
         }
     };
     auto issue = [&](int kt, int s) {
-        uint8_t* abase = smem + s * STAGEB + (BM / 4) * wave * EROWB;
-        uint8_t* bbase = smem + s * STAGEB + AOPB + 64 * wave * EROWB;
+        uint8_t* abase = smem + s * STAGEB + (BM / NW) * wave * EROWB;
+        uint8_t* bbase = smem + s * STAGEB + AOPB + (256 / NW) * wave * EROWB;
         const int koff = kt * EBK * 2;
         if constexpr (Q8) qload(kt);  // before the A DMA: waiting for the codes leaves the DMA in flight
 #pragma unroll
@@ -386,7 +396,7 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
             if (j < A_DMA)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(abase + 8 * j * EROWB), 16, oa[j], koff, 0,
                                                          0);
-            if constexpr (!Q8)
+            if (!Q8 && j < B_DMA)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(bbase + 8 * j * EROWB), 16, ob[j], koff, 0,
                                                          0);
         }
@@ -443,7 +453,7 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
     issue(0, 0);
     if constexpr (Q8) qwrite(0);
     if (nk > 1) issue(1, 1);
-    if (nk > 1) wait_vm<A_DMA + 8>();  // Q8: 4 code and 4 scale loads stand in for the 8 B DMAs
+    if (nk > 1) wait_vm<A_DMA + B_DMA>();  // Q8: QJ code and QJ scale loads stand in for the B_DMA B DMAs
     else wait_vm<0>();
     if constexpr (Q8) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the B rows written
     __builtin_amdgcn_s_barrier();
@@ -475,7 +485,7 @@ __global__ __launch_bounds__(256) void gemm_k64_kernel(const Group grp) {
         mfma(wb, xb);
         if constexpr (SCHED) {
             // the DMA instructions one per MFMA, then the next step's reads
-            constexpr int NDMA = decltype(issue_next)::value ? A_DMA + 8 : 0;
+            constexpr int NDMA = decltype(issue_next)::value ? A_DMA + B_DMA : 0;
 #pragma unroll
             for (int r = 0; r < (NDMA > FN * FM ? NDMA : FN * FM); ++r) {
                 if (r < NDMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read (DMA)
@@ -931,11 +941,13 @@ struct Config {
 // (two per CU); 2: 256 x 256, 4 waves, K = 64 stages; 3: Q8_0 weights,
 // 256 x 256, 8 waves, K = 64, three stages; 4: any shape (masked, 128 x 128);
 // 5: config 2 with the operand reads interleaved into the MFMA stream; 6: the
-// same at 224 x 256.
-constexpr int kAnyConfig = 4, kLastConfig = 7;
-constexpr Config kConfigs[8] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
+// same at 224 x 256; 7: config 5 with Q8_0 weights dequantised as they are
+// staged; 8, 9: configs 5 and 7 in eight waves of 128 x 64 (two per SIMD).
+constexpr int kAnyConfig = 4, kLastConfig = 9;
+constexpr Config kConfigs[10] = {{256, 256, 512, 1, 1.15}, {128, 128, 256, 2, 0.9}, {256, 256, 256, 1, 1.15},
                                 {256, 256, 512, 1, 1.0},  {128, 128, 256, 2, 0.1}, {256, 256, 256, 1, 1.3},
-                                {224, 256, 256, 1, 1.2},  {256, 256, 256, 1, 1.25}};
+                                {224, 256, 256, 1, 1.2},  {256, 256, 256, 1, 1.25}, {256, 256, 512, 1, 1.3},
+                                {256, 256, 512, 1, 1.3}};
 
 int64_t tiles_of(const Problem& p, int cfg) {
     const Config c = kConfigs[cfg];
@@ -967,17 +979,19 @@ int pick_by_waves(const Problem* ps, int n, int cus, std::initializer_list<int> 
     return best;
 }
 
-// Q8_0 weights: the K = 64 kernel's 256 x 256 tiles with the weights
-// dequantised as they are staged (config 7) or, when those leave most CUs
-// idle (the 512 text tokens' products, a 128-column output), 128 x 128 tiles
-// dequantised the same way (1.9x faster than 256 x 256 at 512 x 3072 x 9216).
-int pick_config_q8(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {7, 1}); }
+// Q8_0 weights: the eight-wave K = 64 kernel's 256 x 256 tiles with the
+// weights dequantised as they are staged (config 9) or, when those leave most
+// CUs idle (the 512 text tokens' 3072-column products, a 128-column output),
+// 128 x 128 tiles dequantised the same way (512 x 3072 x 9216: 135 against
+// 203 us).
+int pick_config_q8(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {9, 1}); }
 
-// bf16 weights: 256 x 256 tiles, 224 x 256 tiles when they need fewer rows of
-// work in all (e.g. M = 4608 or 4096 with N = 3072: 216 or 192 tiles -> one
-// wave of 252 or 228; 4608 x 9216: three waves of 756 instead of 648 tiles,
-// 8% faster), or 128 x 128 tiles for the products with few tiles.
-int pick_config(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {5, 6, 1}); }
+// bf16 weights: the eight-wave K = 64 kernel's 256 x 256 tiles (config 8), or
+// 128 x 128 tiles for the products with few tiles.  Config 8 measured faster
+// than the four-wave 224 x 256 tiles on every product of the step that those
+// took (4608 x 3072 x 9216: 210 against 225 us; 4608 x 3072 x 3072: 81.5
+// against 91.6 us), so they are no longer a candidate.
+int pick_config(const Problem* ps, int n, int cus) { return pick_by_waves(ps, n, cus, {8, 1}); }
 
 template <typename TC>
 int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
@@ -1003,6 +1017,10 @@ int launch(const Problem* ps, int n, int cfg, hipStream_t st) {
         hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 224>), grid, block, 0, st, g);
     else if (cfg == 7)
         hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 256, true>), grid, block, 0, st, g);
+    else if (cfg == 8)
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 256, false, 8>), grid, block, 0, st, g);
+    else if (cfg == 9)
+        hipLaunchKernelGGL((gemm_k64_kernel<TC, true, 256, true, 8>), grid, block, 0, st, g);
     else if (cfg == 3)
         hipLaunchKernelGGL((gemm_q8_kernel<TC>), grid, block, 0, st, g);
     else if (cfg == kAnyConfig && ps[0].Bs)
@@ -1073,7 +1091,7 @@ extern "C" int dt_gemm_bf16_grouped(const dt_gemm_problem* problems, int32_t cou
         }
     }
     DT_REQUIRE(n_q8 == 0 || n_q8 == count, "dt_gemm_bf16_grouped: a group mixes Q8_0 and bf16 weights");
-    const bool q8_config = config == 3 || config == 7;  // configurations for Q8_0 weights only
+    const bool q8_config = config == 3 || config == 7 || config == 9;  // configurations for Q8_0 weights only
     DT_REQUIRE(config == -1 || config == kAnyConfig || config == 1 || (n_q8 > 0) == q8_config,
                "dt_gemm_bf16: config %d does not take %s weights", config, n_q8 ? "Q8_0" : "bf16");
     DT_REQUIRE(config == -1 || config == kAnyConfig || all_tiled,

@@ -483,7 +483,8 @@ def quantize_q8_0(x, out=None):
 def gemm(a, b, bias=None, addend=None, out=None, out_dtype=None, config=-1):
     """a: bf16 [M, K], b: bf16 [N, K] (rows K-contiguous) -> a @ b.T (+ bias) (+ addend).
     config: tile configuration (0: 256x256, 8 waves, K = 32 stages; 1: 128x128;
-    2: 256x256, 4 waves, K = 64 stages; -1: by shape).  Q8_0 weights: gemm_q8_0."""
+    2: 256x256, 4 waves, K = 64 stages; 5: config 2 scheduled; 6: config 5 at
+    224x256; 8: config 5 in 8 waves; -1: by shape).  Q8_0 weights: gemm_q8_0."""
     torch = _torch()
     M, K = a.shape
     N = b.shape[0]

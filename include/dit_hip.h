@@ -341,10 +341,11 @@ int dt_gemm_q8_0(const void *A, int64_t lda, const void *codes, int64_t ld_codes
  * 256x256 in eight waves (dequantised after the LDS read), 4 = the masked
  * any-shape kernel (bf16 or Q8_0 weights), 5 =
  * config 2 with buffer loads to LDS and its LDS reads and loads interleaved
- * into the MFMA stream (same results bit for bit; the 256x256 kernel
- * dt_gemm_bf16 picks), 6 = config 5 with 224-row tiles, 7 = config 5 with
- * Q8_0 weights dequantised as they are staged; -1 picks by shape as
- * dt_gemm_bf16 does (Q8_0: 7 or 1).  Every configuration gives the same
+ * into the MFMA stream, 6 = config 5 with 224-row tiles, 7 = config 5 with
+ * Q8_0 weights dequantised as they are staged, 8 = config 5 in eight waves
+ * of 128x64 (two per SIMD; the 256x256 kernel dt_gemm_bf16 picks), 9 =
+ * config 7 in eight waves (the Q8_0 one); -1 picks by shape as dt_gemm_bf16
+ * does (bf16: 8 or 1; Q8_0: 9 or 1).  Every configuration gives the same
  * bits.  For tuning and tests; no counterpart in the reference. */
 int dt_gemm_bf16_config(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float *bias,

@@ -57,7 +57,7 @@ def test_quantize_q8_0_strided_rows(orc, dev):
 GEMM_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (64, 33, 192)]
 
 
-@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5, 6])
+@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5, 6, 8])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 def test_gemm(orc, dev, M, N, K, out_dtype, config):
@@ -71,7 +71,7 @@ def test_gemm(orc, dev, M, N, K, out_dtype, config):
     check(host(y), ref, out_dtype, f"gemm {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 5, 6])
+@pytest.mark.parametrize("config", [0, 1, 2, 5, 6, 8])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_gemm_strided_bias_addend(orc, dev, out_dtype, config):
     M, N, K = 300, 384, 512
@@ -104,7 +104,7 @@ def test_gemm_in_place_addend(orc, dev):
     assert_fp32(host(c), orc.linear(orc.round_bf16(a), orc.round_bf16(b)) + c0, what="gemm in-place")
 
 
-@pytest.mark.parametrize("config", [0, 1, 2, 5, 6])
+@pytest.mark.parametrize("config", [0, 1, 2, 5, 6, 8])
 def test_gemm_large_sampled_rows(orc, dev, config):
     """4608 x 3072 x 3072 (a Flux2 block's attention projection); 88 rows
     spread over every row tile are checked against the oracle."""
@@ -119,7 +119,7 @@ def test_gemm_large_sampled_rows(orc, dev, config):
     assert_fp32(host(y)[rows], ref, what="gemm 4608x3072x3072")
 
 
-@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5, 6])
+@pytest.mark.parametrize("config", [-1, 0, 1, 2, 5, 6, 8])
 def test_gemm_grouped(orc, dev, config):
     """Five GEMMs of different N and K (and an empty one) in one launch, each
     against the oracle: the q/k/v/gate/up pattern plus ragged edges."""
@@ -166,9 +166,9 @@ def test_gemm_any_shape_equals_tiled_on_tiled_shapes(orc, dev):
     M, N, K = 200, 192, 256
     a = dev_tensor(orc.randn(SEED + 232, (M, K)), torch.bfloat16)
     b = dev_tensor(orc.randn(SEED + 233, (N, K), std=0.02), torch.bfloat16)
-    outs = [dit_hip.gemm(a, b, out_dtype=torch.float32, config=c) for c in (0, 1, 2, 4, 5, 6)]
+    outs = [dit_hip.gemm(a, b, out_dtype=torch.float32, config=c) for c in (0, 1, 2, 4, 5, 6, 8)]
     torch.cuda.synchronize()
-    for c, o in zip((1, 2, 4, 5, 6), outs[1:]):
+    for c, o in zip((1, 2, 4, 5, 6, 8), outs[1:]):
         assert torch.equal(o.view(torch.int32), outs[0].view(torch.int32)), f"config {c}"
     z = torch.zeros((0, 64), dtype=torch.bfloat16, device="cuda")
     w = torch.zeros((8, 64), dtype=torch.bfloat16, device="cuda")
@@ -201,14 +201,14 @@ Q8_SHAPES = [(1, 64, 64), (130, 200, 320), (256, 256, 3072), (513, 1000, 128), (
              (77, 130, 96), (40, 64, 32)]  # the last two: K % 64 == 32, the masked kernel
 
 
-@pytest.mark.parametrize("config", [-1, 1, 3, 7])
+@pytest.mark.parametrize("config", [-1, 1, 3, 7, 9])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M,N,K", Q8_SHAPES)
 def test_gemm_q8_0_equals_dequant_then_gemm(orc, dev, M, N, K, out_dtype, config):
     """Dequantising in the GEMM's load path (config 3: 256 x 256 tiles in
-    eight waves, converted after the LDS read; config 7: the K = 64 kernel's
-    256 x 256 tiles and config 1: 128 x 128 tiles, converted as they are
-    staged; -1: picked by shape) gives the bf16 weights dt_dequant
+    eight waves, converted after the LDS read; configs 7 and 9: the K = 64
+    kernel's 256 x 256 tiles in four or eight waves and config 1: 128 x 128
+    tiles, converted as they are staged; -1: picked by shape) gives the bf16 weights dt_dequant
     writes and the same fp32 accumulation order, so C is bit-identical to
     dt_dequant followed by the bf16 GEMM; and within the bar of the oracle on
     the dequantised weights."""
@@ -258,11 +258,13 @@ def test_gemm_q8_0_grouped_and_large(orc, dev):
         items_q.append((a, q8, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
         items_b.append((a, wd, torch.empty((M, N), dtype=torch.bfloat16, device="cuda")))
     outs_q = [o.clone() for o in dit_hip.gemm_grouped(items_q)]
+    outs_q7 = [o.clone() for o in dit_hip.gemm_grouped(items_q, config=7)]
     outs_q3 = dit_hip.gemm_grouped(items_q, config=3)
     outs_b = dit_hip.gemm_grouped(items_b, config=2)
     torch.cuda.synchronize()
-    for oq, oq3, ob in zip(outs_q, outs_q3, outs_b):
+    for oq, oq7, oq3, ob in zip(outs_q, outs_q7, outs_q3, outs_b):
         assert torch.equal(oq, ob), "picked Q8_0 configuration"
+        assert torch.equal(oq7, ob), "four-wave K = 64 Q8_0 kernel"
         assert torch.equal(oq3, ob), "eight-wave Q8_0 kernel"
 
 
