@@ -44,6 +44,7 @@
 #include <algorithm>
 #include <cstring>
 #include <iterator>
+#include <functional>
 #include <map>
 #include <unordered_map>
 #include <vector>
@@ -911,6 +912,80 @@ void group_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
     }
 }
 
+// 256 x 256 tiles of a MUL_MAT (the GEMM's large tiles) and the waves of them
+// one launch needs on MI355X's 256 CUs.  A planning estimate only (the plan
+// is made without a device); the GEMM picks its tiles at launch.
+int64_t big_tiles(const dt_tensor* t) {
+    GemmArgs ga;
+    if (!gemm_args(t, &ga)) return 0;
+    return ((ga.M + 255) / 256) * ((ga.N + 255) / 256);
+}
+constexpr int64_t kPlanCus = 256;
+int64_t tile_waves(int64_t tiles) { return (tiles + kPlanCus - 1) / kPlanCus; }
+
+// Forward pass over the MUL_MATs still launched on their own: one whose
+// output is first read after a later MUL_MAT launch of the same K, output
+// type and weight kind runs in that launch when the two together take fewer
+// waves of tiles than apart.  In a double-stream block the image
+// feed-forward's output projection (4096 x 3072 x 9216, 192 tiles) is read
+// only by its gated residual, which runs in the next block's adaLN, so it
+// joins the text stream's (512 x 3072 x 9216, 24 tiles): one wave of 216
+// instead of two launches.  The later launch keeps its position; the moved
+// node's inputs stay alive until then (runs_at).
+void defer_gemms(Graph& g, dt_tensor** nodes, int n, std::vector<Plan>& plans) {
+    auto movable = [&](int j) {
+        const dt_tensor* t = nodes[j];
+        GemmArgs ga;
+        return t->op == DT_OP_MUL_MAT && !g.claimed[j] && !g.nomove[j] && !g.banned[j] && plans[j].kind == K_NONE &&
+               !(t->flags & DT_FLAG_OUTPUT) && gemm_args(t, &ga);
+    };
+    // The earliest launch position that reads t's value (through VIEWs).
+    std::function<int(const dt_tensor*)> first_read = [&](const dt_tensor* t) {
+        int first = n;
+        auto it = g.consumers.find(t);
+        if (it == g.consumers.end()) return first;
+        for (int c : it->second) {
+            if (nodes[c]->op == DT_OP_VIEW) {
+                if (nodes[c]->flags & DT_FLAG_OUTPUT) return -1;
+                first = std::min(first, first_read(nodes[c]));
+            } else {
+                first = std::min(first, g.runs_at[c]);
+            }
+        }
+        return first;
+    };
+    for (int i = 0; i < n; ++i) {
+        if (!movable(i)) continue;
+        const dt_tensor* t = nodes[i];
+        const int64_t K = t->src[0]->ne[0], ti = big_tiles(t);
+        const int until = first_read(t);
+        for (int j = i + 1; j < until; ++j) {
+            const bool single = movable(j);
+            const bool group = plans[j].kind == K_GEMM_GROUP && !g.nomove[j] && plans[j].members.size() < 8;
+            if (!single && !group) continue;
+            std::vector<const dt_tensor*> ms = group ? plans[j].members : std::vector<const dt_tensor*>{nodes[j]};
+            bool fits = true;
+            int64_t tj = 0, wj = 0;
+            for (const dt_tensor* m : ms) {
+                fits = fits && m->type == t->type && q8_weight(m) == q8_weight(t) && f32_gemm(m) == f32_gemm(t) &&
+                       m->src[0]->ne[0] == K;
+                tj += big_tiles(m);
+            }
+            wj = tile_waves(tj);
+            if (!fits || tile_waves(ti + tj) >= tile_waves(ti) + wj) continue;
+            Plan& p = plans[j];
+            if (single) {
+                p.kind = K_GEMM_GROUP;
+                p.members = {nodes[j]};
+            }
+            p.members.push_back(t);
+            plans[i].kind = K_DEFERRED;
+            g.runs_at[i] = j;
+            break;
+        }
+    }
+}
+
 // Forward pass over SwiGLU roots: with the two single-segment QK roots that
 // precede it (q and k of the same block) and inputs computed before the
 // first of them, the three run as one launch at the first QK's position
@@ -1615,6 +1690,7 @@ int plan_graph(dt_tensor** nodes, int32_t n_nodes, Graph& g, std::vector<Plan>& 
     }
     group_gemms(g, nodes, n_nodes, plans);
     merge_qk_swiglu(g, nodes, n_nodes, plans);
+    defer_gemms(g, nodes, n_nodes, plans);
     return DT_OK;
 }
 

@@ -52,7 +52,7 @@ def test_q8_0_weights_plan_like_bf16():
 
 @pytest.mark.parametrize("kind,layers,nodes,fused,mm,grouped,deferred", [
     ("single", dict(num_layers=0), 58, 34, 7, 5, 1),
-    ("double", dict(num_single_layers=0), 110, 56, 14, 8, 4),
+    ("double", dict(num_single_layers=0), 110, 56, 14, 8, 5),
 ])
 def test_per_block_fusion(kind, layers, nodes, fused, mm, grouped, deferred):
     """A second block adds its nodes, fusions and GEMMs; `grouped` roots run
@@ -60,9 +60,12 @@ def test_per_block_fusion(kind, layers, nodes, fused, mm, grouped, deferred):
     and the SwiGLU with k's QK-RMSNorm+RoPE, q's being the attention's
     prologue; double:
     k, v and the three txt projections with q, up with gate on each stream,
-    to_out with to_add_out), and `deferred` residuals are written by the next
-    adaLN's fused kernel (one per block boundary: single 1; double 2 inside
-    the block and 2 at the boundary)."""
+    to_out with to_add_out), and `deferred` nodes run in a later launch:
+    residuals written by the next adaLN's fused kernel (one per block
+    boundary: single 1; double 2 inside the block and 2 at the boundary),
+    and in a double block the image feed-forward's output projection, which
+    joins the text stream's (192 + 24 tiles: one wave instead of two
+    launches)."""
     key = "num_single_layers" if kind == "single" else "num_layers"
     a = plan(**layers, **{key: 1})
     b = plan(**layers, **{key: 2})
