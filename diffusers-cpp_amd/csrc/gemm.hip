@@ -314,9 +314,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_k64_kernel(const Group grp) {
     const int m0 = tm * BM, n0 = tn * 256;
     const int wm = (wave / WAVES_N) * (BM / WAVES_M), wn = (wave % WAVES_N) * (256 / WAVES_N);
 
-    // DMA sources: wave w fills A rows [BM/4 w, +BM/4) and B rows [64 w,
-    // +64), instructions of 8 rows each; lane i covers row + i / 8, stored
-    // chunk i % 8.  Buffer loads to LDS: the tile's first row is the
+    // DMA sources: wave w fills A rows [BM/NW w, +BM/NW) and B rows
+    // [256/NW w, +256/NW), instructions of 8 rows each; lane i covers row +
+    // i / 8, stored chunk i % 8.  Buffer loads to LDS: the tile's first row is the
     // (scalar) buffer base, each lane's row and chunk a 32-bit byte offset
     // (< 256 rows x ld x 2 bytes), the k-tile a scalar offset.
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
