@@ -103,35 +103,35 @@ __global__ __launch_bounds__(kBlock) void gn_stats_kernel(const T* __restrict__ 
 // This workgroup's chunk of group (n, g): the thread's vectors are loaded
 // (packed; see gn_stats_kernel) by gn_chunk_load, then gn_chunk_finish
 // computes y = silu((x - mean) * (rstd * w_c) + b_c) and stores it.
-template <typename T, bool VEC>
-__device__ __forceinline__ void gn_chunk_load(const T* x, const GnShape& s, int n, int g, uint4 (&raw)[kVecsPerThread]) {
+template <typename T, bool VEC, int AV = kVecsPerThread>
+__device__ __forceinline__ void gn_chunk_load(const T* x, const GnShape& s, int n, int g, uint4 (&raw)[AV]) {
     constexpr int EPV = VEC ? Io<T>::EPV : 1;
     if constexpr (VEC) {
         const T* xg = x + (int64_t)n * s.C * s.HW + (int64_t)g * s.group_len;
-        const int64_t v0 = (int64_t)blockIdx.x * kChunkVecs;
-        const int64_t v1 = v0 + kChunkVecs < s.group_vecs ? v0 + kChunkVecs : s.group_vecs;
+        const int64_t v0 = (int64_t)blockIdx.x * (kBlock * AV);
+        const int64_t v1 = v0 + kBlock * AV < s.group_vecs ? v0 + kBlock * AV : s.group_vecs;
 #pragma unroll
-        for (int i = 0; i < kVecsPerThread; ++i) {
+        for (int i = 0; i < AV; ++i) {
             const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
             if (v < v1) raw[i] = ld_stream(xg + v * EPV);
         }
     }
 }
 
-template <typename T, bool VEC>
+template <typename T, bool VEC, int AV = kVecsPerThread>
 __device__ __forceinline__ void gn_chunk_finish(const T* x, const GnShape& s, int n, int g, float mean, float rstd,
                                                 const float* __restrict__ w, const float* __restrict__ b, T* y,
-                                                FastDiv hw_vecs, const uint4 (&raw)[kVecsPerThread]) {
+                                                FastDiv hw_vecs, const uint4 (&raw)[AV]) {
     constexpr int EPV = VEC ? Io<T>::EPV : 1;
     const int64_t off = (int64_t)n * s.C * s.HW + (int64_t)g * s.group_len;
     const T* xg = x + off;
     T* yg = y + off;
     const int64_t c0 = (int64_t)g * s.cg;
-    const int64_t v0 = (int64_t)blockIdx.x * kChunkVecs;
-    int64_t v1 = v0 + kChunkVecs;
+    const int64_t v0 = (int64_t)blockIdx.x * (kBlock * AV);
+    int64_t v1 = v0 + kBlock * AV;
     if (v1 > s.group_vecs) v1 = s.group_vecs;
 #pragma unroll
-    for (int i = 0; i < kVecsPerThread; ++i) {
+    for (int i = 0; i < AV; ++i) {
         const int64_t v = v0 + threadIdx.x + (int64_t)i * kBlock;
         if (v >= v1) break;
         float a[EPV];
@@ -182,7 +182,10 @@ __device__ __forceinline__ void gn_group_stats(const double* __restrict__ ws, co
     *rstd = 1.0f / sqrtf((float)var + s.eps);
 }
 
-template <typename T, bool VEC>
+// AV vectors per thread: the apply pass's own chunking (kBlock * AV
+// vectors per workgroup), independent of the statistics pass's chunks,
+// whose partials it sums; the output is the same for any AV.
+template <typename T, bool VEC, int AV = kVecsPerThread>
 __global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
                                                           const double* __restrict__ ws,
                                                           const float* __restrict__ w,
@@ -190,11 +193,11 @@ __global__ __launch_bounds__(kBlock) void gn_apply_kernel(const T* x, GnShape s,
                                                           FastDiv hw_vecs) {
     __shared__ double red[kBlock / kWave];
     const int ng = blockIdx.y, n = ng / s.G, g = ng - n * s.G;
-    uint4 raw[kVecsPerThread];
-    gn_chunk_load<T, VEC>(x, s, n, g, raw);
+    uint4 raw[AV];
+    gn_chunk_load<T, VEC, AV>(x, s, n, g, raw);
     float mean, rstd;
     gn_group_stats(ws, s, ng, red, &mean, &rstd);
-    gn_chunk_finish<T, VEC>(x, s, n, g, mean, rstd, w, b, y, hw_vecs, raw);
+    gn_chunk_finish<T, VEC, AV>(x, s, n, g, mean, rstd, w, b, y, hw_vecs, raw);
 }
 
 // (mean, rstd) of every group, for a consumer that applies the
@@ -271,8 +274,18 @@ int launch(const void* x, const GnShape& s, int64_t N, const float* w, const flo
     hipLaunchKernelGGL((gn_stats_kernel<T, VEC>), grid, dim3(kBlock), 0, st, (const T*)x, s, ws);
     int rc = check_launch("dt_groupnorm_silu(stats)");
     if (rc) return rc;
-    hipLaunchKernelGGL((gn_apply_kernel<T, VEC>), grid, dim3(kBlock), 0, st, (const T*)x, s, ws, w,
-                       b, (T*)y, make_fastdiv((uint32_t)(s.HW / EPV)));
+    const FastDiv hv = make_fastdiv((uint32_t)(s.HW / EPV));
+    // Two vectors per thread when four would leave fewer than 2048 apply
+    // workgroups (8 per CU on 256 CUs): the bf16 [1, 512, 128, 128] map,
+    // 1024 -> 2048 workgroups, the shape of the fastest plain copy of its
+    // bytes.  Four above that (every other decoder map measured faster so).
+    const int64_t half_chunks = (s.group_vecs + 2 * kBlock - 1) / (2 * kBlock);
+    if (VEC && (int64_t)s.nchunks * N * s.G < 2048) {
+        const dim3 g2((unsigned)half_chunks, (unsigned)(N * s.G));
+        hipLaunchKernelGGL((gn_apply_kernel<T, VEC, 2>), g2, dim3(kBlock), 0, st, (const T*)x, s, ws, w, b, (T*)y, hv);
+    } else {
+        hipLaunchKernelGGL((gn_apply_kernel<T, VEC>), grid, dim3(kBlock), 0, st, (const T*)x, s, ws, w, b, (T*)y, hv);
+    }
     return check_launch("dt_groupnorm_silu(apply)");
 }
 
